@@ -1,0 +1,278 @@
+"""Benchmark of the MI355X logits->token step (one GPU).
+
+Default: configuration C2 of BASELINE.json (the headline): one sampled step
+over B=64 rows of V=151,936 fp32 logits with presence/frequency penalties over
+2,048-token histories, T 0.7, top-k 50, top-p 0.9, one uniform per row. A
+"step" is one jf_sample call over one batch; inputs are resident in HBM and
+rotated over >= 512 MB of distinct copies so the 256 MB Infinity Cache cannot
+serve a repeated step. Prints one JSON line.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1..5]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "justfit-llm_amd"))
+
+PEAK_HBM_GBS = 8000.0
+ROTATE_BYTES = 512 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--mode", default="auto",
+                    help="C3/C4: greedy or sampled (auto: sampled)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="bound of the CPU-baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def build_workload(cfg, mode):
+    """Host inputs, per-row policies and the algorithmic bytes of one step."""
+    import jf_sampler as J
+    from jf_sampler import workloads as WL
+    w = {}
+    if cfg == 1:
+        c = WL.config1()
+        w.update(V=c["V"], logits=c["logits"], policies=[J.policy(**c["policy"])],
+                 histories=c["histories"], generated=c["generated"], mark_prompt=True,
+                 name="C1 greedy B=1 V=151936 fp32 repetition 1.1 over 256 prompt ids",
+                 dtype="f32")
+        hist_bytes = 256 * 4
+    elif cfg == 2:
+        c = WL.config2()
+        B = c["logits"].shape[0]
+        w.update(V=c["V"], logits=c["logits"], policies=[J.policy(**c["policy"])] * B,
+                 histories=c["histories"], generated=c["generated"], mark_prompt=False,
+                 uniforms=c["uniforms"],
+                 name="C2 sampled B=64 V=151936 fp32 T0.7 top-k 50 top-p 0.9 "
+                      "presence 0.5 frequency 0.3 over 2048 ids",
+                 dtype="f32")
+        hist_bytes = B * 2048 * 4
+    elif cfg == 3:
+        c = WL.config3()
+        B = c["logits_bf16"].shape[0]
+        sampled = mode != "greedy"
+        p = J.policy(temperature=1.0, constrained=True) if sampled else J.policy(constrained=True)
+        w.update(V=c["V"], logits_bf16=c["logits_bf16"], masks=c["masks"], policies=[p] * B,
+                 uniforms=c["uniforms"],
+                 name=f"C3 grammar B=32 V=151936 bf16 mask u32[32][4748] "
+                      f"{'T1.0 sampled' if sampled else 'greedy'}",
+                 dtype="bf16->f32")
+        hist_bytes = c["masks"].nbytes
+    elif cfg == 4:
+        c = WL.config4()
+        rows = c["logits"].shape[0]
+        sampled = mode != "greedy"
+        pol = J.policy(temperature=1.0) if sampled else J.policy()
+        w.update(V=c["V"], logits=c["logits"], policies=[pol] * rows,
+                 name=f"C4 tree verify 16x16 nodes V=151936 fp32 "
+                      f"{'rejection sampling (dense q)' if sampled else 'greedy'}",
+                 dtype="f32", tree=c, sampled=sampled)
+        hist_bytes = c["q"].nbytes if sampled else 0
+        if sampled:
+            w["uniforms"] = c["uniforms"]
+    else:
+        c = WL.config5()
+        B = c["logits_bf16"].shape[0]
+        w.update(V=c["V"], logits_bf16=c["logits_bf16"], policies=[J.policy(**c["policy"])] * B,
+                 histories=c["histories"], generated=c["generated"], mark_prompt=True,
+                 uniforms=c["uniforms"],
+                 name="C5 large B=256 V=248320 bf16 min-p 0.05 top-k 1000 top-p 0.95 "
+                      "T0.8 penalties over 8192 ids",
+                 dtype="bf16->f32")
+        hist_bytes = B * 8192 * 4
+    lg = w.get("logits", w.get("logits_bf16"))
+    rows = lg.shape[0]
+    w["rows"] = rows
+    w["alg_bytes"] = lg.nbytes + hist_bytes + rows * 4 * 2  # + uniforms + outputs
+    return w
+
+
+class GpuStep:
+    """Device-resident inputs (rotated copies) and one jf_sample per step."""
+
+    def __init__(self, w):
+        import torch
+        import jf_sampler as J
+        self.w = w
+        dev = torch.device("cuda", 0)
+        V, rows = w["V"], w["rows"]
+        host = w.get("logits")
+        if host is not None:
+            base = torch.from_numpy(host)
+        else:
+            base = torch.from_numpy(w["logits_bf16"].view(np.int16)).view(torch.bfloat16)
+        per = base.numel() * base.element_size()
+        copies = max(2, -(-ROTATE_BYTES // per))
+        self.copies = [base.to(dev) for _ in range(copies)]
+        self.sampler = J.Sampler(V, rows)
+        self.kw = []
+        self.tables = []
+        extra = {}
+        if "masks" in w:
+            extra["masks"] = torch.from_numpy(w["masks"].view(np.int32)).to(dev)
+        if "uniforms" in w:
+            u = w["uniforms"]
+            if u.ndim == 2:  # C4: per-row uniform slot 24 + r of each request
+                rq = u.shape[0]
+                idx = np.array([k * 40 + 24 + r for k in range(rq) for r in range(rows // rq)],
+                               np.uint32)
+                extra["uniform_index"] = torch.from_numpy(idx.view(np.int32)).to(dev)
+                u = u.reshape(-1)
+            extra["uniforms"] = torch.from_numpy(np.ascontiguousarray(u)).to(dev)
+        if w.get("tree") is not None and w.get("sampled"):
+            c = w["tree"]
+            from jf_sampler import workloads as WL
+            draft = np.full(rows, 0xFFFFFFFF, np.uint32)
+            for k, parent in enumerate(c["trees"]):
+                n = WL.chain_length(parent)
+                for r in range(n - 1):
+                    draft[k * 16 + r] = c["tokens"][k][r + 1]
+            extra["draft_tokens"] = torch.from_numpy(draft.view(np.int32)).to(dev)
+            self.q = [torch.from_numpy(c["q"]).to(dev) for _ in range(len(self.copies))]
+            extra["out_draft_probs"] = torch.zeros(rows, dtype=torch.float32, device=dev)
+        self.out = torch.zeros(rows, dtype=torch.int32, device=dev)
+        for i in range(len(self.copies)):
+            kw = dict(extra)
+            if "histories" in w:
+                H = max(len(h) for h in w["histories"])
+                t = J.PenaltyTable(V, rows, H + 8)
+                for r, h in enumerate(w["histories"]):
+                    t.rebuild(r, h, w["generated"][r], None, w["mark_prompt"])
+                self.tables.append(t)
+                kw["penalties"] = t
+                kw["penalty_rows"] = list(range(rows))
+            if w.get("tree") is not None and w.get("sampled"):
+                kw["dense_q"] = self.q[i]
+            a, keep = self.sampler.sample_args(self.copies[i], w["policies"], self.out, **kw)
+            self.kw.append((a, keep))
+        torch.cuda.synchronize()
+
+    def step(self, i):
+        a, _ = self.kw[i % len(self.kw)]
+        self.sampler.launch(a)
+
+
+def cpu_baseline(w, seconds):
+    """The oracle (a C restatement, -O2, pthreads over rows) on a bounded
+    sample of the same workload: whole steps until `seconds` elapse."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    V, rows = w["V"], w["rows"]
+    threads = min(16, os.cpu_count() or 1)
+    pols = [O.policy_from(p) for p in w["policies"]]
+    words, pen_rows = None, None
+    if "histories" in w:
+        words = np.zeros((rows, V), np.uint32)
+        for r, h in enumerate(w["histories"]):
+            rc, words[r] = O.rebuild_penalty_words(V, h, w["generated"][r], None, w["mark_prompt"])
+        pen_rows = np.arange(rows, dtype=np.uint32)
+    is_bf16 = "logits_bf16" in w
+    lg = w["logits_bf16"] if is_bf16 else w["logits"]
+    u = w.get("uniforms")
+    if u is not None and u.ndim == 2:
+        u = None
+    if w.get("tree") is not None and w.get("sampled"):
+        return None  # the dense-residual draw is not in the batch driver
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        O.select_batch(V, pols, lg, is_bf16=is_bf16, masks=w.get("masks"), words=words,
+                       pen_rows=pen_rows, uniforms=u, threads=threads)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return dict(value=steps / el, unit="steps/s", cores=threads, kind="port",
+                sample=f"{steps} full steps ({rows} rows each) of the same seeded "
+                       f"workload in {el:.1f} s, oracle/jf_oracle.c -O2, "
+                       f"{threads} threads over rows")
+
+
+def read_traffic(cfg):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(REPO, "profiles", f"select_c{cfg}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":")[1])
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: every box has one "
+                          "MI355X; rows shard across GPUs with no exchange (see "
+                          "DESIGN.md), so run --gpus 1"}))
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    w = build_workload(args.config, args.mode)
+    print(f"# {w['name']}: building inputs", file=sys.stderr, flush=True)
+    g = GpuStep(w)
+    for i in range(args.warmup):
+        g.step(i)
+    torch.cuda.synchronize()
+    K = args.steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    ev[0].record()
+    for i in range(K):
+        g.step(args.warmup + i)
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    per = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(K)]) * 1000.0  # us
+    total_ms = ev[0].elapsed_time(ev[K])
+    ms_per_step = total_ms / K
+    p50, p90 = float(np.percentile(per, 50)), float(np.percentile(per, 90))
+    mean_us = float(per.mean())
+    achieved = w["alg_bytes"] / (mean_us * 1e-6) / 1e9
+    cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
+    traffic = read_traffic(args.config)
+    line = {
+        "metric": "sampling steps/sec at B=64,V=151936; achieved HBM GB/s vs peak; p50 us/step",
+        "value": 1000.0 / ms_per_step,
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "p50_us": p50,
+        "p90_us": p90,
+        "wall_s": wall,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w["dtype"],
+        "data": f"synthetic (seeded generators in justfit-llm_amd/jf_sampler/workloads.py), "
+                f"{len(g.copies)} rotated input copies >= 512 MB",
+        "config": {"workload": w["name"], "rows": w["rows"], "vocabulary": w["V"],
+                   "algorithmic_bytes_per_step": w["alg_bytes"]},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
+                     "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

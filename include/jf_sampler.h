@@ -1,0 +1,266 @@
+/*
+ * jf_sampler.h — C ABI of the MI355X (gfx950) logits->token path.
+ *
+ * The entry points replace the reference's target token policy operator
+ * justfit::ops::Sampling (source/runtime/ops/Sampling.hpp:114-199) and the
+ * tree acceptance dispatch Runtime::encodeTreeAcceptance
+ * (source/runtime/model/Runtime.cpp:1284-1306, kernel
+ * source/runtime/metal/kernels/decode/tree.metal:20-84). Every device pointer
+ * is a plain HIP device address; `stream` is a hipStream_t (NULL = the null
+ * stream). Calls are asynchronous on that stream unless stated otherwise.
+ *
+ * Errors: every function returns JF_OK (0) or a JF_ERR_* code and leaves a
+ * thread-local message for jf_last_error(). Bad arguments are rejected before
+ * anything is enqueued, as the reference throws std::invalid_argument before
+ * it encodes (Sampling.cpp:139-142, 283-295; BufferExtent.hpp:24-28). A row
+ * whose logits leave nothing to select yields JF_NO_TOKEN in-band, the
+ * reference's non-finite-row sentinel (Runtime.cpp:1410-1421).
+ */
+#ifndef JF_SAMPLER_H
+#define JF_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JF_OK 0
+#define JF_ERR_INVALID_ARGUMENT 1 /* std::invalid_argument in the reference */
+#define JF_ERR_LOGIC 2            /* std::logic_error in the reference */
+#define JF_ERR_DEVICE 3           /* a HIP runtime call failed */
+#define JF_ERR_NO_MEMORY 4
+
+#define JF_NO_TOKEN 0xffffffffu
+
+/* Uniform slots of one lane's cycle (metal/abi/Sampling.h:19-29). */
+#define JF_UNIFORM_INITIAL 0u
+#define JF_UNIFORM_PROPOSALS 1u
+#define JF_UNIFORM_ACCEPTANCE 8u
+#define JF_UNIFORM_CORRECTION 15u
+#define JF_UNIFORM_TREE_DRAWS 24u
+#define JF_SAMPLING_UNIFORMS 40u
+/* Draft candidates per proposal position (ExecutionGeometry.h:288). */
+#define JF_DRAFT_CANDIDATES 16u
+/* Penalty word layout (metal/abi/Sampling.h:111-112). */
+#define JF_PENALTY_PROMPT_BIT 0x80000000u
+#define JF_PENALTY_COUNT_MASK 0x7fffffffu
+/* Tree geometry (metal/abi/TreeVerify.h:175-176). */
+#define JF_TREE_MAXIMUM_ROWS 16u
+#define JF_TREE_MAXIMUM_DEPTH 8u
+
+#define JF_DTYPE_F32 0u
+#define JF_DTYPE_BF16 1u
+
+/* jf_policy.flags */
+#define JF_POLICY_CONSTRAINED 1u  /* SamplingPolicy::constrained */
+#define JF_POLICY_EXCLUDE_STOP 2u /* SamplingPolicy::excludesStopTokens */
+
+/* One row's target policy: ops::SamplingPolicy + SamplingPenalties
+ * (Sampling.hpp:19-50). temperature 0 selects greedily; top_k 0 or past the
+ * vocabulary disables top-k (Sampling.cpp:23-26). */
+typedef struct jf_policy {
+  uint32_t top_k;
+  float temperature;
+  float top_p;
+  float min_p;
+  float repetition;
+  float presence;
+  float frequency;
+  uint32_t flags;
+} jf_policy;
+
+typedef struct jf_sampler jf_sampler;
+typedef struct jf_penalty_table jf_penalty_table;
+
+/* The message of the calling thread's last failed call. */
+const char *jf_last_error(void);
+
+/* SamplingParameters::validationError (model/Model.hpp:77-95): JF_OK or
+ * JF_ERR_INVALID_ARGUMENT with the reference's message. */
+int jf_policy_validate(const jf_policy *policy);
+
+/* ops::Sampling::Sampling(vocabulary) (Sampling.cpp:82-86), plus the device
+ * scratch the reference sizes with Sampling::workspace(rows)
+ * (Sampling.cpp:37-48), owned here for up to max_rows rows per call. Creates
+ * on the current HIP device; synchronous. */
+int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
+                      jf_sampler **out);
+int jf_sampler_destroy(jf_sampler *sampler);
+/* Bytes of device scratch the sampler holds (Sampling::workspace role). */
+uint64_t jf_sampler_workspace_bytes(const jf_sampler *sampler);
+
+/* ---- penalties -------------------------------------------------------- */
+
+/* Host helpers with the reference's exact semantics and errors:
+ * Sampling::rebuildPenaltyWords (Sampling.cpp:50-71) and
+ * Sampling::countPenaltyTokens (Sampling.cpp:75-80) over dense host words. */
+int jf_penalty_words_rebuild(uint32_t *words, uint32_t vocabulary,
+                             const uint32_t *history, uint64_t history_len,
+                             uint64_t generated_tokens, int has_pending,
+                             uint32_t pending_token, int mark_prompt);
+int jf_penalty_words_count(uint32_t *words, uint32_t vocabulary,
+                           const uint32_t *selected, uint64_t count);
+
+/* The device penalty table: the reference's PenaltyTable (Sampling.hpp:55-58,
+ * one dense uint32 word per vocabulary token per state lane) stored sparsely,
+ * as each row's nonzero words sorted by token. Rows hold at most max_entries
+ * distinct tokens. */
+int jf_penalty_table_create(uint32_t vocabulary, uint32_t rows,
+                            uint32_t max_entries, jf_penalty_table **out);
+int jf_penalty_table_destroy(jf_penalty_table *table);
+/* rebuildPenaltyWords into table row `row` from a host history (same
+ * arguments, same errors); uploads on `stream`. */
+int jf_penalty_table_rebuild(jf_penalty_table *table, uint32_t row,
+                             const uint32_t *history, uint64_t history_len,
+                             uint64_t generated_tokens, int has_pending,
+                             uint32_t pending_token, int mark_prompt,
+                             void *stream);
+/* countPenaltyTokens into table row `row` (host tokens); uploads on
+ * `stream`. */
+int jf_penalty_table_count(jf_penalty_table *table, uint32_t row,
+                           const uint32_t *selected, uint64_t count,
+                           void *stream);
+
+/* ---- uniforms --------------------------------------------------------- */
+
+/* Runtime::nextUniform (Runtime.cpp:1098-1105): SplitMix64 of
+ * seed + (++counter) * 0x9e3779b97f4a7c15, top 24 bits scaled by 2^-24. */
+float jf_next_uniform(uint64_t seed, uint64_t *counter);
+/* Runtime::stageSamplingCycle (Runtime.cpp:1107-1114) into 40 host floats. */
+void jf_stage_sampling_cycle(uint64_t seed, uint64_t *counter,
+                             uint32_t verify_rows, int tree_cycle,
+                             float *uniforms40);
+
+/* ---- selection -------------------------------------------------------- */
+
+/* One selection over `rows` rows: what Sampling::addInitial and
+ * Sampling::addVerify encode (Sampling.cpp:134-172, 244-276) — penalties,
+ * then each greedy row's argmax or each sampled row's min-p/top-k/top-p draw
+ * — generalized from <= 4 lanes x 8/16 rows to `rows` independent rows with
+ * explicit strides. Row r reads:
+ *   logits  + r * logits_stride   (elements of dtype; 16-byte aligned rows)
+ *   masks   + r * mask_stride     (uint32 words; constrained rows only)
+ *   uniforms[uniform_index ? uniform_index[r]
+ *            : uniform_offset + r * uniform_stride]   (sampled rows; a
+ *   stride of 0 gives every row the same uniform, the reference's
+ *   correction slot; stride 1 with offset 24 its per-row tree draws)
+ *   penalty table row penalty_rows[r] and extra_tokens + r * extra_stride
+ *   (extra_counts[r] tokens each counted once more: the draft tokens a
+ *   verify row's context adds, Sampling.cpp:118-131, sampling.metal:978-993)
+ *   draft_tokens[r] for r < drafted_rows: JF_NO_TOKEN, or the draft token
+ *   the row's draw corrects (TargetSamplingParams::drafted_rows: a drafted
+ *   verify row); rows from drafted_rows on are not drafted; the draft
+ *   distribution is dense
+ *   (draft_q + r * draft_q_stride) when draft_q is set, else the sparse
+ *   candidates draft_cand_ids/probs + r * JF_DRAFT_CANDIDATES.
+ * Writes out_tokens[r] and, when set, out_draft_probs[r] (the target's
+ * probability of the row's draft token, TargetVocabularyRow::draft_probability)
+ * and the kept distribution (out_kept_counts[r]; ids ascending and their
+ * probabilities in out_kept_ids/out_kept_probs + r * kept_capacity).
+ * The logits are read-only: the reference rewrites penalized logits in place,
+ * this build applies penalties on the fly. */
+typedef struct jf_sample_args {
+  uint32_t rows;
+  uint32_t dtype;
+  const void *logits;
+  uint64_t logits_stride;
+  const uint32_t *masks;
+  uint64_t mask_stride;
+  const jf_policy *policies;       /* host, rows entries */
+  uint32_t stop_token_0;
+  uint32_t stop_token_1;
+  const jf_penalty_table *penalties;
+  const uint32_t *penalty_rows;    /* host, rows entries, or NULL */
+  const uint32_t *extra_tokens;    /* device */
+  const uint32_t *extra_counts;    /* host, rows entries (<= 16), or NULL */
+  uint64_t extra_stride;
+  const float *uniforms;           /* device */
+  const uint32_t *uniform_index;   /* device, or NULL */
+  uint64_t uniform_offset;
+  uint64_t uniform_stride;
+  const uint32_t *draft_tokens;    /* device, or NULL */
+  uint32_t drafted_rows;
+  const uint32_t *draft_cand_ids;  /* device */
+  const float *draft_cand_probs;   /* device */
+  const float *draft_q;            /* device, or NULL */
+  uint64_t draft_q_stride;
+  uint32_t *out_tokens;            /* device */
+  float *out_draft_probs;          /* device, or NULL */
+  uint32_t *out_kept_counts;       /* device, or NULL */
+  uint32_t *out_kept_ids;          /* device */
+  float *out_kept_probs;           /* device */
+  uint32_t kept_capacity;
+} jf_sample_args;
+
+int jf_sample(jf_sampler *sampler, const jf_sample_args *args, void *stream);
+
+/* ---- acceptance ------------------------------------------------------- */
+
+/* Sampling::addAcceptance (Sampling.cpp:278-328) -> decode_accept_dflash
+ * (sampling.metal:1528-1558) over `lanes` lanes of verify_rows (8 or 16)
+ * rows. Per lane l: proposed_tokens + l*(verify_rows-1), candidates and
+ * proposal_probs + l*(verify_rows-1)*16, target_draft_probs +
+ * l*verify_rows (the selection's out_draft_probs), uniforms + l*40,
+ * target_tokens + l*verify_rows (in: the selection's tokens; out: the
+ * accepted chain). maximum_retained and policies are host arrays. */
+typedef struct jf_accept_chain_args {
+  uint32_t lanes;
+  uint32_t verify_rows;
+  const uint32_t *proposed_tokens;
+  const uint32_t *candidates;
+  const float *proposal_probs;
+  const float *target_draft_probs;
+  const float *uniforms;
+  uint32_t *target_tokens;
+  uint32_t *retained_counts;
+  uint32_t *accepted_counts;
+  const uint32_t *maximum_retained; /* host */
+  const jf_policy *policies;        /* host */
+  uint32_t stop_token_0;
+  uint32_t stop_token_1;
+} jf_accept_chain_args;
+
+int jf_accept_chain(jf_sampler *sampler, const jf_accept_chain_args *args,
+                    void *stream);
+
+/* One lane's draft tree: the fields of JustFitTreeLane that acceptance reads
+ * (TreeVerify.h:178-187) and the sampled chain of JustFitTreeAcceptParams
+ * (TreeVerify.h:196-208). Rows in DFS preorder, parent[r] < r, row 0 the
+ * anchor; rows 0 .. chain_rows-1 are the draft's sampled chain and chain_q[r]
+ * is the draft probability of row r+1's token. */
+typedef struct jf_tree_lane {
+  uint32_t rows;
+  uint32_t chain_rows;
+  uint32_t parent[JF_TREE_MAXIMUM_ROWS];
+  uint32_t token[JF_TREE_MAXIMUM_ROWS];
+  float chain_q[JF_TREE_MAXIMUM_DEPTH];
+} jf_tree_lane;
+
+/* verify_tree_accept (tree.metal:20-84) over `lanes` lanes. Per lane l:
+ * trees[l] (host), target_tokens + l*rows_per_lane (in: each row's selected
+ * token; out: the accepted path's tokens then the bonus token),
+ * target_draft_probs + l*rows_per_lane, uniforms + l*40, path_rows + l*8. */
+typedef struct jf_accept_tree_args {
+  uint32_t lanes;
+  uint32_t rows_per_lane;
+  const jf_tree_lane *trees;        /* host */
+  const float *target_draft_probs;
+  const float *uniforms;
+  uint32_t *target_tokens;
+  uint32_t *retained_counts;
+  uint32_t *accepted_counts;
+  uint32_t *path_rows;
+  const uint32_t *maximum_retained; /* host */
+  const jf_policy *policies;        /* host */
+  uint32_t stop_token_0;
+  uint32_t stop_token_1;
+} jf_accept_tree_args;
+
+int jf_accept_tree(jf_sampler *sampler, const jf_accept_tree_args *args,
+                   void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

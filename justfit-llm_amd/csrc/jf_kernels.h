@@ -1,0 +1,205 @@
+// Shared declarations of the gfx950 sampler: the device parameter records
+// the host builds, the scratch records the kernels exchange, and the launch
+// entry points of jf_kernels.hip.
+#pragma once
+
+#include <stdint.h>
+
+namespace jf {
+
+// Per-row target policy as the kernels read it (the reference's
+// TargetSamplingParams + SamplingPenaltyParams fields of one lane,
+// metal/abi/Sampling.h:40-61, 118-129), derived on the host.
+struct RowParams {
+  uint32_t flags;
+  uint32_t top_k;             // effective: the vocabulary when disabled
+  float inv_t;                // 1 / temperature
+  float top_p;
+  float minp_offset;          // temperature * log(min_p)
+  float repetition;
+  float repetition_inverse;   // min(1 / repetition, FLT_MAX)
+  float presence;
+  float frequency;
+  uint32_t penalty_row;
+  uint32_t extra_count;
+  uint32_t reserved[5];
+};
+static_assert(sizeof(RowParams) == 64, "row params are 64 bytes");
+
+enum RowFlags : uint32_t {
+  kRowSampled = 1u,
+  kRowConstrained = 2u,
+  kRowExcludeStop = 4u,
+  kRowPenalized = 8u,
+  kRowMinP = 16u,
+  kRowTopP = 32u,
+  kRowTopK = 64u,
+};
+
+// One block's summary of its chunk of a row.
+struct BlockHeader {
+  float maximum;       // sampled: largest admitted logit (-FLT_MAX if none)
+  uint32_t count;      // sampled: candidates written
+  uint32_t admitted;   // sampled: admitted non-NaN tokens
+  uint32_t overflow;   // sampled: candidates did not fit
+  float best_value;    // greedy
+  uint32_t best_id;    // greedy
+  uint32_t reserved[2];
+};
+static_assert(sizeof(BlockHeader) == 32, "block headers are 32 bytes");
+
+// A row the single pass could not finish: the multi-pass stages carry it.
+struct RowState {
+  uint32_t stage;
+  float maximum;
+  uint32_t thr_key;      // min-p floor key, 0 without min-p
+  uint32_t bkey;         // kept set boundary in (key desc, id asc) order
+  uint32_t bid;
+  uint32_t prefix;       // radix descent
+  uint32_t pmask;
+  uint32_t chunk;        // the chunk a locate or walk stage works in
+  uint64_t remaining;    // radix descent: count or mass still to place
+  uint64_t n1;           // tokens at or above the min-p floor
+  uint64_t mass2;
+  uint64_t nucleus;
+  uint64_t mass3;
+  uint64_t target;
+  uint64_t within;       // target or rank inside `chunk`
+  uint32_t tie_key;
+  uint32_t residual;
+  float draft_w;
+  uint32_t drafted;
+  uint64_t reserved[3];
+};
+static_assert(sizeof(RowState) == 128, "row states are 128 bytes");
+
+struct StagePartial {
+  uint64_t v[256];
+};
+
+// Geometry of one selection launch.
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kPenaltyBucket = 2048;
+constexpr int kBlockCandidates = 1024;
+constexpr int kMergeCapacity = 2048;
+constexpr int kPenaltyWordsLds = 2048;
+constexpr int kMaxExtra = 16;
+constexpr uint32_t kChunkF32 = 8192;
+constexpr uint32_t kChunkBF16 = 16384;
+
+struct SampleLaunch {
+  const void *logits;
+  uint64_t stride;
+  const uint32_t *masks;
+  uint64_t mask_stride;
+  const RowParams *params;
+  uint32_t vocabulary;
+  uint32_t chunks;
+  uint32_t rows;
+  uint32_t stop0;
+  uint32_t stop1;
+  uint32_t stage;
+  uint32_t aligned;       // rows start on 16-byte boundaries: vector loads
+  const uint2 *pen_entries;
+  const uint32_t *pen_offsets;
+  uint32_t pen_max_entries;
+  uint32_t pen_buckets;
+  const uint32_t *extra;
+  uint64_t extra_stride;
+  const float *uniforms;
+  const uint32_t *uniform_index;
+  uint64_t uniform_offset;
+  uint64_t uniform_stride;
+  const uint32_t *draft_tokens;
+  uint32_t drafted_rows;
+  const uint32_t *cand_ids;
+  const float *cand_probs;
+  const float *dense_q;
+  uint64_t q_stride;
+  BlockHeader *headers;
+  uint2 *cands;
+  uint32_t *counters;
+  RowState *states;
+  StagePartial *partials;
+  uint32_t *out_tokens;
+  float *out_draft;
+  uint32_t *out_kept_counts;
+  uint32_t *out_kept_ids;
+  float *out_kept_probs;
+  uint32_t kept_cap;
+};
+
+// Multi-pass stages, in launch order.
+enum Stage : uint32_t {
+  kStageDone = 0,
+  kStageCount1 = 1,
+  kStageTopK3 = 2,
+  kStageTopK0 = 5,
+  kStageTopKTie = 6,
+  kStageTopKLocate = 7,
+  kStageMass2 = 8,
+  kStageTopP3 = 9,
+  kStageTopP0 = 12,
+  kStageTopPTie = 13,
+  kStageTopPLocate = 14,
+  kStageMass3 = 15,
+  kStageDraw = 16,
+  kStageWalk = 17,
+  kStageKeptCount = 18,
+  kStageKeptWrite = 19,
+  kStageLast = 19,
+};
+
+struct AcceptChainLane {
+  uint32_t remaining;
+  uint32_t sampled;
+};
+
+struct AcceptChainLaunch {
+  uint32_t lanes;
+  uint32_t verify_rows;
+  const uint32_t *proposed;
+  const uint32_t *candidates;
+  const float *proposal_probs;
+  const float *target_draft_probs;
+  const float *uniforms;
+  uint32_t *target_tokens;
+  uint32_t *retained;
+  uint32_t *accepted;
+  const AcceptChainLane *lane_params;
+  uint32_t stop0;
+  uint32_t stop1;
+};
+
+struct TreeLaneParams {
+  uint32_t rows;
+  uint32_t chain_rows;
+  uint32_t remaining;
+  uint32_t sampled;
+  uint32_t parent[16];
+  uint32_t token[16];
+  float chain_q[8];
+};
+
+struct AcceptTreeLaunch {
+  uint32_t lanes;
+  uint32_t rows_per_lane;
+  const TreeLaneParams *trees;
+  const float *target_draft_probs;
+  const float *uniforms;
+  uint32_t *target_tokens;
+  uint32_t *retained;
+  uint32_t *accepted;
+  uint32_t *path_rows;
+  uint32_t stop0;
+  uint32_t stop1;
+};
+
+// Launchers (jf_kernels.hip); they return the hipError_t of the launch.
+int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream);
+int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);
+int launch_accept_chain(const AcceptChainLaunch &a, void *stream);
+int launch_accept_tree(const AcceptTreeLaunch &a, void *stream);
+
+}  // namespace jf

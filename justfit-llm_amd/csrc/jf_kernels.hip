@@ -1,0 +1,1565 @@
+// gfx950 kernels of JustFit's logits->token path.
+//
+// One selection is one launch of select_kernel over rows x chunks blocks
+// (plus, for rows whose candidates do not fit, the multi-pass stage_kernel
+// launches). Each block holds its chunk of a row in registers: one pass over
+// HBM with 16-byte loads, the penalties, the constraint mask and the stop
+// exclusion applied on the fly (the reference's decode_sample_penalize,
+// TargetRow::admits; sampling.metal:33-37, 928-993). A greedy row reduces its
+// argmax (sampling.metal:1427-1512); a sampled row writes its chunk's
+// maximum and the tokens that can still belong to its min-p/top-k/top-p
+// distribution. The last block of a row to finish (the reference's
+// split_arrive_last, split_reduce.h:14-28) merges: the global maximum, the
+// min-p floor, the exact top-k in (logit desc, id asc) order, the top-p
+// nucleus, and the inverse-CDF draw in id order with the residual of a
+// drafted row (sampling.metal:585-829). Every sum that decides a token is an
+// exact 64-bit sum of floor(w * 2^44), so the parallel order never changes
+// a result.
+#include "jf_device.h"
+#include "jf_kernels.h"
+
+namespace jf {
+
+template <int DT>
+struct Geo;
+template <>
+struct Geo<0> {  // fp32: 4 tokens per 16-byte load
+  static constexpr int VEC = 4, LOADS = 8, TPL = 32, SEG = 2048;
+  static constexpr uint32_t CHUNK = kChunkF32;
+};
+template <>
+struct Geo<1> {  // bf16: 8 tokens per 16-byte load
+  static constexpr int VEC = 8, LOADS = 8, TPL = 64, SEG = 4096;
+  static constexpr uint32_t CHUNK = kChunkBF16;
+};
+
+constexpr uint32_t kMaxChunkWords = kChunkBF16 / 32;
+constexpr uint32_t kMaxChunks = 64;
+
+struct PrepLds {
+  uint32_t pbits[kMaxChunkWords];
+  uint32_t xbits[kMaxChunkWords];
+  uint32_t rankb[kMaxChunkWords];
+  uint32_t pwords[kPenaltyWordsLds];
+  uint32_t extras[kMaxExtra];
+};
+struct MergeLds {
+  uint32_t key[kMergeCapacity];
+  uint32_t id[kMergeCapacity];
+  uint8_t fl[kMergeCapacity];
+};
+
+struct __align__(16) Lds {
+  union {
+    PrepLds prep;
+    MergeLds merge;
+  };
+  uint64_t hist[256];
+  uint64_t wl[kWaves];
+  float wf[kWaves];
+  uint32_t wu[kWaves];
+  uint32_t wu2[kWaves];
+  float hmax[kMaxChunks];
+  uint32_t hcnt[kMaxChunks];
+  uint32_t hoff[kMaxChunks + 1];
+  uint32_t last;
+  uint32_t sel_bin;
+  uint64_t sel_excl;
+  uint32_t hit;
+  uint32_t found_id;
+  float found_w;
+  uint32_t u32a;
+  uint64_t u64a;
+};
+
+// ---- block helpers (every thread of the block calls them) ---------------
+
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, Lds &s) {
+  v = wave_sum_u32(v);
+  __syncthreads();
+  if (lane_id() == 0) s.wu[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return s.wu[0] + s.wu[1] + s.wu[2] + s.wu[3];
+}
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, Lds &s) {
+  v = wave_sum_u64(v);
+  __syncthreads();
+  if (lane_id() == 0) s.wl[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3];
+}
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, Lds &s) {
+  v = wave_max_u32(v);
+  __syncthreads();
+  if (lane_id() == 0) s.wu[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return max(max(s.wu[0], s.wu[1]), max(s.wu[2], s.wu[3]));
+}
+__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, Lds &s) {
+  v = wave_min_u32(v);
+  __syncthreads();
+  if (lane_id() == 0) s.wu[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return min(min(s.wu[0], s.wu[1]), min(s.wu[2], s.wu[3]));
+}
+__device__ __forceinline__ float block_max_f32(float v, Lds &s) {
+  v = wave_max_f32(v);
+  __syncthreads();
+  if (lane_id() == 0) s.wf[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return __builtin_fmaxf(__builtin_fmaxf(s.wf[0], s.wf[1]),
+                         __builtin_fmaxf(s.wf[2], s.wf[3]));
+}
+// Exclusive prefix over threads in thread order; *total gets the block sum.
+__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, Lds &s,
+                                                        uint64_t *total) {
+  const uint64_t incl = wave_incl_scan_u64(v);
+  const uint32_t w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane_id() == 63) s.wl[w] = incl;
+  __syncthreads();
+  uint64_t off = 0, tot = 0;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) {
+    off += (k < (int)w) ? s.wl[k] : 0;
+    tot += s.wl[k];
+  }
+  if (total) *total = tot;
+  return off + incl - v;
+}
+
+// Wave 0 finds the highest bin b of s.hist whose suffix sum (bins >= b)
+// reaches T; s.sel_bin = b, s.sel_excl = sum of the bins above b. The
+// caller guarantees the total reaches T.
+__device__ __forceinline__ void crossing_bin(Lds &s, uint64_t T) {
+  if (threadIdx.x < 64) {
+    const uint32_t l = threadIdx.x;
+    const uint64_t h0 = s.hist[4 * l], h1 = s.hist[4 * l + 1],
+                   h2 = s.hist[4 * l + 2], h3 = s.hist[4 * l + 3];
+    const uint64_t own = h0 + h1 + h2 + h3;
+    uint64_t suf = own;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint64_t o = shfl_down_u64(suf, d);
+      if (l + d < 64) suf += o;
+    }
+    const uint64_t m = ballot(suf >= T);
+    const int L = m ? (int)__popcll(m) - 1 : 0;
+    const uint64_t above = shfl_u64(suf - own, L);
+    if ((int)l == L) {
+      // Walk this lane's four bins from the top.
+      uint64_t acc = above;
+      uint32_t bin = 4 * l;
+      uint64_t excl = acc;
+      if (acc + h3 >= T) {
+        bin = 4 * l + 3;
+        excl = acc;
+      } else if (acc + h3 + h2 >= T) {
+        bin = 4 * l + 2;
+        excl = acc + h3;
+      } else if (acc + h3 + h2 + h1 >= T) {
+        bin = 4 * l + 1;
+        excl = acc + h3 + h2;
+      } else {
+        bin = 4 * l;
+        excl = acc + h3 + h2 + h1;
+      }
+      s.sel_bin = bin;
+      s.sel_excl = excl;
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ bool at_or_before(uint32_t key, uint32_t token,
+                                             uint32_t bkey, uint32_t bid) {
+  return key > bkey || (key == bkey && token <= bid);
+}
+
+// ---- one chunk of one row into registers ---------------------------------
+
+// Loads chunk `chunk` of `row`: xs[j*VEC+e] is token
+// chunk*CHUNK + w*SEG + j*64*VEC + lane*VEC + e (w = wave, lane = lane id),
+// penalized; bit j*VEC+e of the result is set when the row admits the token
+// (in the vocabulary, in the mask of a constrained row, not an excluded stop
+// token). Block-uniform control flow: every thread calls it.
+template <int DT>
+__device__ __forceinline__ uint64_t load_chunk(const SampleLaunch &a,
+                                               const RowParams &rp,
+                                               uint32_t row, uint32_t chunk,
+                                               Lds &s,
+                                               float (&xs)[Geo<DT>::TPL]) {
+  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
+                SEG = Geo<DT>::SEG;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  constexpr uint32_t VMASK = (1u << VEC) - 1u;
+  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const uint32_t V = a.vocabulary;
+  const uint32_t base = chunk * CHUNK;
+  const uint32_t lane_base = base + w * SEG + lane * VEC;
+
+  if constexpr (DT == 0) {
+    const float *rowp = (const float *)a.logits + (uint64_t)row * a.stride;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const uint32_t t0 = lane_base + j * 64 * VEC;
+      if (t0 + VEC <= V && a.aligned) {
+        const float4 v = *(const float4 *)(rowp + t0);
+        xs[j * 4 + 0] = v.x;
+        xs[j * 4 + 1] = v.y;
+        xs[j * 4 + 2] = v.z;
+        xs[j * 4 + 3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          xs[j * VEC + e] = (t0 + e < V) ? rowp[t0 + e] : 0.0f;
+      }
+    }
+  } else {
+    const uint16_t *rowp =
+        (const uint16_t *)a.logits + (uint64_t)row * a.stride;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const uint32_t t0 = lane_base + j * 64 * VEC;
+      if (t0 + VEC <= V && a.aligned) {
+        const uint4 v = *(const uint4 *)(rowp + t0);
+        const uint32_t p[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          xs[j * 8 + 2 * q] = u2f(p[q] << 16);
+          xs[j * 8 + 2 * q + 1] = u2f(p[q] & 0xffff0000u);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          xs[j * VEC + e] =
+              (t0 + e < V) ? bf16_to_float(rowp[t0 + e]) : 0.0f;
+      }
+    }
+  }
+
+  uint64_t adm = 0;
+  const bool constrained = (rp.flags & kRowConstrained) != 0;
+  const uint32_t *mrow = a.masks + (uint64_t)row * a.mask_stride;
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    const uint32_t t0 = lane_base + j * 64 * VEC;
+    uint32_t vm = 0;
+    if (t0 + VEC <= V)
+      vm = VMASK;
+    else if (t0 < V)
+      vm = (1u << (V - t0)) - 1u;
+    if (constrained && vm) vm &= (mrow[t0 >> 5] >> (t0 & 31)) & VMASK;
+    adm |= (uint64_t)vm << (j * VEC);
+  }
+  if (rp.flags & kRowExcludeStop) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t st = k ? a.stop1 : a.stop0;
+      if (st >= base && st < base + CHUNK) {
+        const uint32_t o = st - base;
+        const uint32_t sw = o / SEG, sj = (o % SEG) / (64 * VEC),
+                       sl = (o % (64 * VEC)) / VEC, se = o % VEC;
+        if (sw == w && sl == lane) adm &= ~(1ull << (sj * VEC + se));
+      }
+    }
+  }
+
+  if (rp.flags & kRowPenalized) {
+    constexpr uint32_t NWORDS = CHUNK / 32;
+    PrepLds &p = s.prep;
+    for (uint32_t i = tid; i < NWORDS; i += kThreads) {
+      p.pbits[i] = 0;
+      p.xbits[i] = 0;
+    }
+    __syncthreads();
+    const uint32_t prow = rp.penalty_row;
+    uint32_t lo = 0, hi = 0;
+    const uint2 *ent = nullptr;
+    if (prow != kNoToken) {
+      const uint32_t *offs =
+          a.pen_offsets + (uint64_t)prow * (a.pen_buckets + 1);
+      const uint32_t b0 = base / kPenaltyBucket;
+      const uint32_t b1 = min((base + CHUNK) / kPenaltyBucket, a.pen_buckets);
+      lo = offs[b0];
+      hi = offs[b1];
+      ent = a.pen_entries + (uint64_t)prow * a.pen_max_entries;
+      for (uint32_t i = lo + tid; i < hi; i += kThreads) {
+        const uint2 e = ent[i];
+        const uint32_t o = e.x - base;
+        atomicOr(&p.pbits[o >> 5], 1u << (o & 31));
+        if (i - lo < (uint32_t)kPenaltyWordsLds) p.pwords[i - lo] = e.y;
+      }
+    }
+    const uint32_t nx = rp.extra_count;
+    if (tid < nx) {
+      const uint32_t t = a.extra[(uint64_t)row * a.extra_stride + tid];
+      p.extras[tid] = t;
+      if (t >= base && t < base + CHUNK && t < V) {
+        const uint32_t o = t - base;
+        atomicOr(&p.xbits[o >> 5], 1u << (o & 31));
+      }
+    }
+    __syncthreads();
+    // Rank of each word's first entry: exclusive prefix of popcounts.
+    {
+      constexpr uint32_t PER = NWORDS / kThreads;
+      uint32_t c[PER];
+      uint32_t local = 0;
+#pragma unroll
+      for (uint32_t k = 0; k < PER; ++k) {
+        c[k] = __popc(p.pbits[tid * PER + k]);
+        local += c[k];
+      }
+      uint64_t total;
+      uint32_t off = (uint32_t)block_excl_scan_u64(local, s, &total);
+#pragma unroll
+      for (uint32_t k = 0; k < PER; ++k) {
+        p.rankb[tid * PER + k] = off;
+        off += c[k];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const uint32_t o0 = w * SEG + j * 64 * VEC + lane * VEC;
+      const uint32_t wi = o0 >> 5, sh = o0 & 31;
+      const uint32_t pw = p.pbits[wi], xw = p.xbits[wi];
+      const uint32_t pb = (pw >> sh) & VMASK, xb = (xw >> sh) & VMASK;
+      if (pb | xb) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          if (!(((pb | xb) >> e) & 1u)) continue;
+          uint32_t word = 0;
+          if ((pb >> e) & 1u) {
+            const uint32_t r =
+                p.rankb[wi] + __popc(pw & ((1u << (sh + e)) - 1u));
+            word = r < (uint32_t)kPenaltyWordsLds ? p.pwords[r] : ent[lo + r].y;
+          }
+          uint32_t count = word & kCountMask;
+          if ((xb >> e) & 1u) {
+            const uint32_t t = base + o0 + e;
+            for (uint32_t k = 0; k < nx; ++k) count += p.extras[k] == t;
+          }
+          if (count || (word & kPromptBit))
+            xs[j * VEC + e] =
+                penalize(xs[j * VEC + e], count, rp.repetition,
+                         rp.repetition_inverse, rp.presence, rp.frequency);
+        }
+      }
+    }
+    __syncthreads();  // the prep area is reused by the caller
+  }
+  return adm;
+}
+
+// Writes the (key, id) of every token whose bit is set in `pb`, in id order
+// across the block, at dst[start + rank] for ranks below `limit - start`.
+// Returns the number of set bits in the block.
+template <int DT>
+__device__ __forceinline__ uint32_t emit_ordered(uint64_t pb,
+                                                 const float (&xs)[Geo<DT>::TPL],
+                                                 uint32_t lane_base, uint2 *dst,
+                                                 uint32_t start, uint32_t limit,
+                                                 Lds &s) {
+  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS;
+  constexpr uint32_t VMASK = (1u << VEC) - 1u;
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t wtot = wave_sum_u32(__popcll(pb));
+  __syncthreads();
+  if (lane_id() == 0) s.wu2[w] = wtot;
+  __syncthreads();
+  uint32_t woff = 0, btot = 0;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) {
+    woff += (k < (int)w) ? s.wu2[k] : 0;
+    btot += s.wu2[k];
+  }
+  uint32_t running = start + woff;
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    const uint32_t bits = (uint32_t)(pb >> (j * VEC)) & VMASK;
+    if (ballot(bits != 0) == 0) continue;
+    const uint32_t nb = __popc(bits);
+    uint32_t excl = 0, tot = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint64_t bm = ballot((nb >> k) & 1u);
+      excl += mbcnt(bm) << k;
+      tot += (uint32_t)__popcll(bm) << k;
+    }
+    uint32_t idx = running + excl;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      if ((bits >> e) & 1u) {
+        if (idx < limit)
+          dst[idx] = make_uint2(logit_key(xs[j * VEC + e]),
+                                lane_base + j * 64 * VEC + e);
+        ++idx;
+      }
+    }
+    running += tot;
+  }
+  return btot;
+}
+
+// The first `limit` set bits of `pb` in block id order (w, j, lane, e).
+template <int DT>
+__device__ __forceinline__ uint64_t first_in_order(uint64_t pb, uint32_t limit,
+                                                   Lds &s) {
+  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS;
+  constexpr uint32_t VMASK = (1u << VEC) - 1u;
+  const uint32_t w = threadIdx.x >> 6;
+  const uint32_t wtot = wave_sum_u32(__popcll(pb));
+  __syncthreads();
+  if (lane_id() == 0) s.wu2[w] = wtot;
+  __syncthreads();
+  uint32_t running = 0;
+  for (int k = 0; k < (int)w; ++k) running += s.wu2[k];
+  uint64_t kept = 0;
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    const uint32_t bits = (uint32_t)(pb >> (j * VEC)) & VMASK;
+    const uint32_t nb = __popc(bits);
+    uint32_t excl = 0, tot = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint64_t bm = ballot((nb >> k) & 1u);
+      excl += mbcnt(bm) << k;
+      tot += (uint32_t)__popcll(bm) << k;
+    }
+    uint32_t idx = running + excl;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e)
+      if ((bits >> e) & 1u) {
+        if (idx < limit) kept |= 1ull << (j * VEC + e);
+        ++idx;
+      }
+    running += tot;
+  }
+  return kept;
+}
+
+// ---- outputs --------------------------------------------------------------
+
+__device__ __forceinline__ void write_result(const SampleLaunch &a,
+                                             uint32_t row, uint32_t token,
+                                             float draft_p, uint32_t kept) {
+  a.out_tokens[row] = token;
+  if (a.out_draft) a.out_draft[row] = draft_p;
+  if (a.out_kept_counts) a.out_kept_counts[row] = kept;
+}
+
+__device__ __forceinline__ float row_uniform(const SampleLaunch &a,
+                                             uint32_t row) {
+  return a.uniforms[a.uniform_index ? (uint64_t)a.uniform_index[row]
+                                     : a.uniform_offset + row * a.uniform_stride];
+}
+
+// The draft token a row's draw corrects, or kNoToken.
+__device__ __forceinline__ uint32_t row_draft(const SampleLaunch &a,
+                                              uint32_t row) {
+  return (a.draft_tokens && row < a.drafted_rows) ? a.draft_tokens[row]
+                                                   : kNoToken;
+}
+
+// The draft's probability of `token` for a drafted row: its dense q, or
+// the first sparse candidate that lists it (sampling.metal:703-708).
+__device__ __forceinline__ float draft_q(const SampleLaunch &a, uint32_t row,
+                                         uint32_t token) {
+  if (a.dense_q) return a.dense_q[(uint64_t)row * a.q_stride + token];
+  const uint32_t *ids = a.cand_ids + (uint64_t)row * 16;
+  const float *pr = a.cand_probs + (uint64_t)row * 16;
+  for (int j = 0; j < 16; ++j)
+    if (ids[j] == token) return pr[j];
+  return 0.0f;
+}
+
+__device__ __forceinline__ uint64_t residual_of(uint64_t wq, uint64_t mass,
+                                                float q) {
+  const uint64_t qm = floor_mul(mass, q);
+  return wq > qm ? wq - qm : 0;
+}
+
+// ---- the merge of a sampled row ------------------------------------------
+
+// Items of the merge live in s.merge (key, id, flag) in id order. Per-thread
+// contiguous ranges give ordered scans.
+struct ItemRange {
+  uint32_t begin, end;
+};
+__device__ __forceinline__ ItemRange my_items(uint32_t n) {
+  const uint32_t per = (n + kThreads - 1) / kThreads;
+  const uint32_t b = min(threadIdx.x * per, n);
+  return {b, min(b + per, n)};
+}
+
+// Keeps, among flagged items, the first `keep` in (key desc, id asc) order:
+// radix descent over the key bytes, then the lowest ids among the ties.
+__device__ __forceinline__ void lds_topk(Lds &s, uint32_t n, uint32_t keep) {
+  MergeLds &m = s.merge;
+  uint32_t prefix = 0, pmask = 0;
+  uint64_t need = keep;
+  for (int d = 3; d >= 0; --d) {
+    s.hist[threadIdx.x] = 0;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+      const uint32_t k = m.key[i];
+      if (m.fl[i] && (k & pmask) == prefix)
+        atomicAdd((unsigned long long *)&s.hist[(k >> (8 * d)) & 255u], 1ull);
+    }
+    __syncthreads();
+    crossing_bin(s, need);
+    need -= s.sel_excl;
+    prefix |= s.sel_bin << (8 * d);
+    pmask |= 255u << (8 * d);
+    __syncthreads();
+  }
+  // need = how many tokens tied at `prefix` stay, lowest ids first.
+  const ItemRange r = my_items(n);
+  uint32_t ties = 0;
+  for (uint32_t i = r.begin; i < r.end; ++i) ties += m.fl[i] && m.key[i] == prefix;
+  uint32_t rank = (uint32_t)block_excl_scan_u64(ties, s, nullptr);
+  for (uint32_t i = r.begin; i < r.end; ++i) {
+    if (!m.fl[i]) continue;
+    const uint32_t k = m.key[i];
+    if (k > prefix) continue;
+    if (k < prefix) {
+      m.fl[i] = 0;
+    } else {
+      m.fl[i] = rank < need ? 1 : 0;
+      ++rank;
+    }
+  }
+  __syncthreads();
+}
+
+// Top-p over the flagged items (sampling.metal:615-641): keep them in order
+// until the running mass exceeds floor(top_p * mass); that token stays.
+__device__ __forceinline__ void lds_topp(Lds &s, uint32_t n, float maximum, float inv_t,
+                         float top_p) {
+  MergeLds &m = s.merge;
+  uint64_t local = 0;
+  for (uint32_t i = threadIdx.x; i < n; i += kThreads)
+    if (m.fl[i]) local += quantize(weight_of(key_logit(m.key[i]), maximum, inv_t));
+  const uint64_t mass = block_sum_u64(local, s);
+  if (mass == 0) return;  // nothing weighs: the nucleus never closes
+  const uint64_t nucleus = floor_mul(mass, top_p);
+  uint64_t need = nucleus + 1;  // the kept prefix's mass must reach this
+  uint32_t prefix = 0, pmask = 0;
+  for (int d = 3; d >= 0; --d) {
+    s.hist[threadIdx.x] = 0;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+      const uint32_t k = m.key[i];
+      if (m.fl[i] && (k & pmask) == prefix) {
+        const uint64_t wq = quantize(weight_of(key_logit(k), maximum, inv_t));
+        if (wq) atomicAdd((unsigned long long *)&s.hist[(k >> (8 * d)) & 255u],
+                          (unsigned long long)wq);
+      }
+    }
+    __syncthreads();
+    crossing_bin(s, need);
+    need -= s.sel_excl;
+    prefix |= s.sel_bin << (8 * d);
+    pmask |= 255u << (8 * d);
+    __syncthreads();
+  }
+  const uint64_t wk = quantize(weight_of(key_logit(prefix), maximum, inv_t));
+  const uint64_t ties_kept = (need + wk - 1) / wk;
+  const ItemRange r = my_items(n);
+  uint32_t ties = 0;
+  for (uint32_t i = r.begin; i < r.end; ++i) ties += m.fl[i] && m.key[i] == prefix;
+  uint32_t rank = (uint32_t)block_excl_scan_u64(ties, s, nullptr);
+  for (uint32_t i = r.begin; i < r.end; ++i) {
+    if (!m.fl[i]) continue;
+    const uint32_t k = m.key[i];
+    if (k > prefix) continue;
+    if (k < prefix) {
+      m.fl[i] = 0;
+    } else {
+      m.fl[i] = rank < ties_kept ? 1 : 0;
+      ++rank;
+    }
+  }
+  __syncthreads();
+}
+
+// The draw over the flagged items in id order (sampling.metal:694-829) and
+// the row's outputs.
+__device__ __forceinline__ void lds_draw(const SampleLaunch &a, uint32_t row, Lds &s,
+                         uint32_t n, float maximum, float inv_t) {
+  MergeLds &m = s.merge;
+  const ItemRange r = my_items(n);
+  uint64_t mloc = 0;
+  uint32_t kloc = 0;
+  for (uint32_t i = r.begin; i < r.end; ++i)
+    if (m.fl[i]) {
+      mloc += quantize(weight_of(key_logit(m.key[i]), maximum, inv_t));
+      ++kloc;
+    }
+  uint64_t mass3;
+  (void)block_excl_scan_u64(mloc, s, &mass3);
+  uint64_t kept_total;
+  const uint32_t kept_rank = (uint32_t)block_excl_scan_u64(kloc, s, &kept_total);
+  const double scale = (double)mass3 * 0x1p-44;
+  if (a.out_kept_ids) {
+    uint32_t k = kept_rank;
+    for (uint32_t i = r.begin; i < r.end; ++i) {
+      if (!m.fl[i]) continue;
+      if (k < a.kept_cap) {
+        const float w = weight_of(key_logit(m.key[i]), maximum, inv_t);
+        a.out_kept_ids[(uint64_t)row * a.kept_cap + k] = m.id[i];
+        a.out_kept_probs[(uint64_t)row * a.kept_cap + k] =
+            mass3 ? (float)((double)w / scale) : 0.0f;
+      }
+      ++k;
+    }
+  }
+  if (mass3 == 0) {
+    if (threadIdx.x == 0) write_result(a, row, kNoToken, 0.0f, (uint32_t)kept_total);
+    return;
+  }
+  const uint32_t draft = row_draft(a, row);
+  const bool drafted = draft != kNoToken;
+  uint64_t dloc = 0;
+  uint32_t any = 0;
+  if (drafted) {
+    for (uint32_t i = r.begin; i < r.end; ++i)
+      if (m.fl[i]) {
+        const uint64_t wq =
+            quantize(weight_of(key_logit(m.key[i]), maximum, inv_t));
+        const uint64_t d = residual_of(wq, mass3, draft_q(a, row, m.id[i]));
+        dloc += d;
+        any |= d > 0;
+      }
+  }
+  const bool residual = drafted && block_max_u32(any, s) != 0;
+  if (!residual) dloc = mloc;
+  uint64_t total;
+  const uint64_t excl = block_excl_scan_u64(dloc, s, &total);
+  uint64_t target = floor_mul(total, row_uniform(a, row));
+  if (target >= total) target = total - 1;
+  if (threadIdx.x == 0) {
+    s.hit = kNoToken;
+    s.found_w = 0.0f;
+  }
+  __syncthreads();
+  if (excl <= target && excl + dloc > target) {
+    uint64_t run = excl;
+    for (uint32_t i = r.begin; i < r.end; ++i) {
+      if (!m.fl[i]) continue;
+      const uint64_t wq =
+          quantize(weight_of(key_logit(m.key[i]), maximum, inv_t));
+      run += residual ? residual_of(wq, mass3, draft_q(a, row, m.id[i])) : wq;
+      if (run > target) {
+        s.hit = m.id[i];
+        break;
+      }
+    }
+  }
+  if (drafted)
+    for (uint32_t i = r.begin; i < r.end; ++i)
+      if (m.fl[i] && m.id[i] == draft)
+        s.found_w = weight_of(key_logit(m.key[i]), maximum, inv_t);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    write_result(a, row, s.hit,
+                 drafted ? (float)((double)s.found_w / scale) : 0.0f,
+                 (uint32_t)kept_total);
+}
+
+// Starts the multi-pass stages of a row the merge cannot finish.
+__device__ __forceinline__ void begin_stages(const SampleLaunch &a, const RowParams &rp,
+                             uint32_t row, float maximum, uint32_t admitted) {
+  RowState st = {};
+  st.maximum = maximum;
+  st.bkey = 0;
+  st.bid = 0;
+  if (rp.flags & kRowMinP) {
+    st.thr_key = logit_key(__builtin_fminf(maximum + rp.minp_offset, maximum));
+    st.stage = kStageCount1;
+  } else {
+    st.thr_key = 0;
+    st.n1 = admitted;
+    if (rp.top_k < admitted) {
+      st.stage = kStageTopK3;
+      st.remaining = rp.top_k;
+    } else {
+      st.stage = (rp.flags & kRowTopP) ? kStageMass2 : kStageMass3;
+    }
+  }
+  st.drafted = row_draft(a, row) != kNoToken ? 1u : 0u;
+  a.states[row] = st;
+}
+
+template <int DT>
+__device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowParams &rp,
+                              uint32_t row, Lds &s) {
+  const uint32_t S = a.chunks, tid = threadIdx.x;
+  const BlockHeader *hb = a.headers + (uint64_t)row * S;
+  float hm = -3.402823466e38f;
+  uint32_t hc = 0, ha = 0, ho = 0;
+  if (tid < S) {
+    const BlockHeader h = hb[tid];
+    hm = h.maximum;
+    hc = h.count;
+    ha = h.admitted;
+    ho = h.overflow;
+    s.hcnt[tid] = hc;
+  }
+  const float maximum = block_max_f32(hm, s);
+  const uint32_t admitted = block_sum_u32(ha, s);
+  const uint32_t overflow = block_max_u32(ho, s);
+  if (tid == 0) {
+    uint32_t n = 0;
+    for (uint32_t c = 0; c < S; ++c) {
+      s.hoff[c] = n;
+      n += s.hcnt[c];
+    }
+    s.hoff[S] = n;
+  }
+  __syncthreads();
+  const uint32_t n_all = s.hoff[S];
+  if (admitted == 0 || maximum == __builtin_inff()) {
+    if (tid == 0) {
+      write_result(a, row, kNoToken, 0.0f, 0);
+      a.states[row].stage = kStageDone;
+    }
+    return;
+  }
+  const uint32_t K = rp.top_k;
+  const bool fits = n_all <= (uint32_t)kMergeCapacity;
+  if (overflow || (!fits && K > (uint32_t)kMergeCapacity)) {
+    if (tid == 0) begin_stages(a, rp, row, maximum, admitted);
+    return;
+  }
+  if (tid == 0) a.states[row].stage = kStageDone;
+  const uint32_t thr = (rp.flags & kRowMinP)
+                           ? logit_key(__builtin_fminf(maximum + rp.minp_offset,
+                                                       maximum))
+                           : 0u;
+  MergeLds &m = s.merge;
+  uint32_t n;
+  if (fits) {
+    // Every candidate into LDS, in id order.
+    for (uint32_t c = 0; c < S; ++c) {
+      const uint2 *src = a.cands + ((uint64_t)row * S + c) * kBlockCandidates;
+      const uint32_t off = s.hoff[c], cnt = s.hoff[c + 1] - off;
+      for (uint32_t i = tid; i < cnt; i += kThreads) {
+        const uint2 v = src[i];
+        m.key[off + i] = v.x;
+        m.id[off + i] = v.y;
+        m.fl[off + i] = v.x >= thr ? 1 : 0;
+      }
+    }
+    n = n_all;
+    __syncthreads();
+    uint32_t c1 = 0;
+    for (uint32_t i = tid; i < n; i += kThreads) c1 += m.fl[i];
+    const uint32_t n1 = block_sum_u32(c1, s);
+    if (K < n1) lds_topk(s, n, K);
+  } else {
+    // More candidates than LDS holds and K fits: select the first K at or
+    // above the min-p floor straight from the global lists, then keep them.
+    // Items are addressed by their global rank in the concatenated lists.
+    auto item = [&](uint32_t i) -> uint2 {
+      uint32_t c = 0;
+      while (s.hoff[c + 1] <= i) ++c;
+      return a.cands[((uint64_t)row * S + c) * kBlockCandidates + (i - s.hoff[c])];
+    };
+    uint32_t c1 = 0;
+    for (uint32_t i = tid; i < n_all; i += kThreads) c1 += item(i).x >= thr;
+    const uint32_t n1 = block_sum_u32(c1, s);
+    uint32_t prefix = 0, pmask = 0;
+    uint64_t need = 0;
+    const bool cut = K < n1;
+    if (cut) {
+      need = K;
+      for (int d = 3; d >= 0; --d) {
+        s.hist[tid] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < n_all; i += kThreads) {
+          const uint32_t k = item(i).x;
+          if (k >= thr && (k & pmask) == prefix)
+            atomicAdd((unsigned long long *)&s.hist[(k >> (8 * d)) & 255u], 1ull);
+        }
+        __syncthreads();
+        crossing_bin(s, need);
+        need -= s.sel_excl;
+        prefix |= s.sel_bin << (8 * d);
+        pmask |= 255u << (8 * d);
+        __syncthreads();
+      }
+    }
+    // Ordered compaction: ties at `prefix` by id, up to `need` of them.
+    const ItemRange r = my_items(n_all);
+    uint32_t ties = 0;
+    if (cut)
+      for (uint32_t i = r.begin; i < r.end; ++i) {
+        const uint32_t k = item(i).x;
+        ties += k >= thr && k == prefix;
+      }
+    const uint32_t tie0 = (uint32_t)block_excl_scan_u64(ties, s, nullptr);
+    uint32_t keep = 0;
+    {
+      uint32_t tr = tie0;
+      for (uint32_t i = r.begin; i < r.end; ++i) {
+        const uint32_t k = item(i).x;
+        if (k < thr) continue;
+        if (!cut || k > prefix) {
+          ++keep;
+        } else if (k == prefix) {
+          keep += tr < need;
+          ++tr;
+        }
+      }
+    }
+    uint64_t kept_total;
+    uint32_t out = (uint32_t)block_excl_scan_u64(keep, s, &kept_total);
+    {
+      uint32_t tr = tie0;
+      for (uint32_t i = r.begin; i < r.end; ++i) {
+        const uint2 v = item(i);
+        const uint32_t k = v.x;
+        if (k < thr) continue;
+        bool take = !cut || k > prefix;
+        if (cut && k == prefix) {
+          take = tr < need;
+          ++tr;
+        }
+        if (take) {
+          m.key[out] = k;
+          m.id[out] = v.y;
+          m.fl[out] = 1;
+          ++out;
+        }
+      }
+    }
+    n = (uint32_t)kept_total;
+    __syncthreads();
+  }
+  if (rp.flags & kRowTopP) lds_topp(s, n, maximum, rp.inv_t, rp.top_p);
+  lds_draw(a, row, s, n, maximum, rp.inv_t);
+}
+
+// ---- the single-pass selection kernel -------------------------------------
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
+  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SEG = Geo<DT>::SEG;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  __shared__ Lds s;
+  const uint32_t S = a.chunks;
+  const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
+  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const RowParams rp = a.params[row];
+  float xs[TPL];
+  uint64_t adm = load_chunk<DT>(a, rp, row, chunk, s, xs);
+  const uint32_t lane_base = chunk * CHUNK + w * SEG + lane * VEC;
+  BlockHeader *hdr = a.headers + (uint64_t)row * S + chunk;
+
+  if (!(rp.flags & kRowSampled)) {
+    float best = -__builtin_inff();
+    uint32_t bid = kNoToken;
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+      if (!((adm >> i) & 1)) continue;
+      const float v = xs[i];
+      const uint32_t t = lane_base + (i / VEC) * 64 * VEC + (i % VEC);
+      if (v > best || (v == best && t < bid)) {
+        best = v;
+        bid = t;
+      }
+    }
+    wave_argmax(best, bid);
+    if (lane == 0) {
+      s.wf[w] = best;
+      s.wu[w] = bid;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float bv = s.wf[0];
+      uint32_t bi = s.wu[0];
+      for (int k = 1; k < kWaves; ++k)
+        if (s.wf[k] > bv || (s.wf[k] == bv && s.wu[k] < bi)) {
+          bv = s.wf[k];
+          bi = s.wu[k];
+        }
+      hdr->best_value = bv;
+      hdr->best_id = bi;
+    }
+  } else {
+    // Admitted non-NaN tokens: their maximum, count and largest key per lane.
+    float mx = -3.402823466e38f;
+    uint32_t cnt = 0, kmax = 0;
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+      if (!((adm >> i) & 1)) continue;
+      const float v = xs[i];
+      if (v != v) {
+        adm &= ~(1ull << i);
+        continue;
+      }
+      mx = __builtin_fmaxf(mx, v);
+      kmax = max(kmax, logit_key(v));
+      ++cnt;
+    }
+    // A bound for the block's top-k: each wave's ceil(k/4)-th largest lane
+    // maximum has at least that many tokens at or above it in the wave.
+    const uint32_t K = rp.top_k;
+    const uint32_t kw = (K + kWaves - 1) / kWaves;
+    uint32_t wth = 0;
+    if ((rp.flags & kRowTopK) && kw <= 64) wth = wave_kth_largest(kmax, kw);
+    const float bmax = block_max_f32(mx, s);
+    const uint32_t badm = block_sum_u32(cnt, s);
+    const uint32_t tk = (rp.flags & kRowTopK) && kw <= 64 ? block_min_u32(wth, s) : 0u;
+    uint32_t thr = tk;
+    if (rp.flags & kRowMinP)
+      thr = max(thr, logit_key(__builtin_fminf(bmax + rp.minp_offset, bmax)));
+    uint64_t cb = 0;
+#pragma unroll
+    for (int i = 0; i < TPL; ++i)
+      if (((adm >> i) & 1) && logit_key(xs[i]) >= thr) cb |= 1ull << i;
+    const uint32_t c = block_sum_u32(__popcll(cb), s);
+    uint2 *dst = a.cands + ((uint64_t)row * S + chunk) * kBlockCandidates;
+    uint32_t emitted = 0, overflow = 0;
+    if (c <= (uint32_t)kBlockCandidates) {
+      emit_ordered<DT>(cb, xs, lane_base, dst, 0, kBlockCandidates, s);
+      emitted = c;
+    } else if (K <= (uint32_t)kBlockCandidates) {
+      // Exactly the block's first K candidates in order.
+      uint32_t prefix = 0, pmask = 0;
+      uint64_t need = K;
+      for (int d = 3; d >= 0; --d) {
+        s.hist[tid] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TPL; ++i) {
+          if (!((cb >> i) & 1)) continue;
+          const uint32_t k = logit_key(xs[i]);
+          if ((k & pmask) == prefix)
+            atomicAdd((unsigned long long *)&s.hist[(k >> (8 * d)) & 255u], 1ull);
+        }
+        __syncthreads();
+        crossing_bin(s, need);
+        need -= s.sel_excl;
+        prefix |= s.sel_bin << (8 * d);
+        pmask |= 255u << (8 * d);
+        __syncthreads();
+      }
+      uint64_t gt = 0, eq = 0;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        if (!((cb >> i) & 1)) continue;
+        const uint32_t k = logit_key(xs[i]);
+        if (k > prefix) gt |= 1ull << i;
+        if (k == prefix) eq |= 1ull << i;
+      }
+      // Ties at the K-th key stay by lowest id; the list stays in id order.
+      const uint64_t keep = gt | first_in_order<DT>(eq, (uint32_t)need, s);
+      emit_ordered<DT>(keep, xs, lane_base, dst, 0, kBlockCandidates, s);
+      emitted = K;
+    } else {
+      overflow = 1;
+    }
+    if (tid == 0) {
+      hdr->maximum = bmax;
+      hdr->count = emitted;
+      hdr->admitted = badm;
+      hdr->overflow = overflow;
+    }
+  }
+
+  // The last block of the row to arrive merges (split_reduce.h:14-45).
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    const uint32_t prev = atomicAdd(&a.counters[row], 1u);
+    s.last = prev == S - 1;
+  }
+  __syncthreads();
+  if (!s.last) return;
+  __threadfence();
+  if (tid == 0) a.counters[row] = 0;
+  if (!(rp.flags & kRowSampled)) {
+    if (tid < 64) {
+      float bv = -__builtin_inff();
+      uint32_t bi = kNoToken;
+      for (uint32_t c = tid; c < S; c += 64) {
+        const BlockHeader h = a.headers[(uint64_t)row * S + c];
+        if (h.best_value > bv || (h.best_value == bv && h.best_id < bi)) {
+          bv = h.best_value;
+          bi = h.best_id;
+        }
+      }
+      wave_argmax(bv, bi);
+      if (tid == 0) {
+        write_result(a, row, bi, 0.0f, 0);
+        a.states[row].stage = kStageDone;
+      }
+    }
+    return;
+  }
+  merge_sampled<DT>(a, rp, row, s);
+}
+
+// ---- multi-pass stages ---------------------------------------------------
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
+  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SEG = Geo<DT>::SEG,
+                LOADS = Geo<DT>::LOADS;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  constexpr uint32_t VMASK = (1u << VEC) - 1u;
+  __shared__ Lds s;
+  const uint32_t S = a.chunks;
+  const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
+  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const uint32_t stage = a.stage;
+  RowState st = a.states[row];
+  if (st.stage != stage) return;
+  const bool single = stage == kStageTopKLocate || stage == kStageTopPLocate ||
+                      stage == kStageWalk;
+  if (single && chunk != st.chunk) return;
+  const RowParams rp = a.params[row];
+  float xs[TPL];
+  uint64_t adm = load_chunk<DT>(a, rp, row, chunk, s, xs);
+  const uint32_t lane_base = chunk * CHUNK + w * SEG + lane * VEC;
+  const float M = st.maximum, inv_t = rp.inv_t;
+  // Members: admitted non-NaN, at or above the min-p floor, at or before
+  // the kept boundary.
+  uint64_t mem = 0;
+#pragma unroll
+  for (int i = 0; i < TPL; ++i) {
+    if (!((adm >> i) & 1)) continue;
+    const float v = xs[i];
+    if (v != v) continue;
+    const uint32_t k = logit_key(v);
+    const uint32_t t = lane_base + (i / VEC) * 64 * VEC + (i % VEC);
+    if (k >= st.thr_key && at_or_before(k, t, st.bkey, st.bid)) mem |= 1ull << i;
+  }
+  StagePartial *part = a.partials + (uint64_t)row * S + chunk;
+  const uint32_t draft = row_draft(a, row);
+
+  auto wq_of = [&](int i) -> uint64_t {
+    return quantize(weight_of(xs[i], M, inv_t));
+  };
+  auto tok_of = [&](int i) -> uint32_t {
+    return lane_base + (i / VEC) * 64 * VEC + (i % VEC);
+  };
+  // The `within`-th (0-based) token with a set bit, in id order; returns
+  // its token in every thread.
+  auto locate = [&](uint64_t bits, uint64_t within) -> uint32_t {
+    if (tid == 0) s.hit = kNoToken;
+    const uint32_t wtot = wave_sum_u32(__popcll(bits));
+    __syncthreads();
+    if (lane == 0) s.wu2[w] = wtot;
+    __syncthreads();
+    uint32_t running = 0;
+    for (int k = 0; k < (int)w; ++k) running += s.wu2[k];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const uint32_t b = (uint32_t)(bits >> (j * VEC)) & VMASK;
+      const uint32_t nb = __popc(b);
+      uint32_t excl = 0, tot = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint64_t bm = ballot((nb >> k) & 1u);
+        excl += mbcnt(bm) << k;
+        tot += (uint32_t)__popcll(bm) << k;
+      }
+      uint32_t idx = running + excl;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        if ((b >> e) & 1u) {
+          if (idx == within) s.hit = tok_of(j * VEC + e);
+          ++idx;
+        }
+      running += tot;
+    }
+    __syncthreads();
+    return s.hit;
+  };
+
+  switch (stage) {
+    case kStageCount1: {
+      const uint32_t c = block_sum_u32(__popcll(mem), s);
+      if (tid == 0) part->v[0] = c;
+      break;
+    }
+    case kStageTopK3: case kStageTopK3 + 1: case kStageTopK3 + 2: case kStageTopK0:
+    case kStageTopP3: case kStageTopP3 + 1: case kStageTopP3 + 2: case kStageTopP0: {
+      const bool by_mass = stage >= kStageTopP3;
+      const int d = by_mass ? (int)(kStageTopP0 - stage) : (int)(kStageTopK0 - stage);
+      s.hist[tid] = 0;
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        if (!((mem >> i) & 1)) continue;
+        const uint32_t k = logit_key(xs[i]);
+        if ((k & st.pmask) != st.prefix) continue;
+        const uint64_t v = by_mass ? wq_of(i) : 1ull;
+        if (v) atomicAdd((unsigned long long *)&s.hist[(k >> (8 * d)) & 255u],
+                         (unsigned long long)v);
+      }
+      __syncthreads();
+      part->v[tid] = s.hist[tid];
+      break;
+    }
+    case kStageTopKTie:
+    case kStageTopPTie: {
+      uint32_t c = 0;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i)
+        c += ((mem >> i) & 1) && logit_key(xs[i]) == st.tie_key;
+      c = block_sum_u32(c, s);
+      if (tid == 0) part->v[0] = c;
+      break;
+    }
+    case kStageTopKLocate:
+    case kStageTopPLocate:
+      break;
+    case kStageMass2:
+    case kStageMass3:
+    case kStageKeptCount: {
+      uint64_t sum = 0;
+      uint32_t c = 0;
+      if (tid == 0) {
+        s.found_w = 0.0f;
+        s.u32a = 0;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < TPL; ++i)
+        if ((mem >> i) & 1) {
+          sum += wq_of(i);
+          ++c;
+        }
+      if (stage == kStageMass3 && draft != kNoToken) {
+#pragma unroll
+        for (int i = 0; i < TPL; ++i)
+          if (((mem >> i) & 1) && tok_of(i) == draft) {
+            s.found_w = weight_of(xs[i], M, inv_t);
+            s.u32a = 1;
+          }
+      }
+      sum = block_sum_u64(sum, s);
+      c = block_sum_u32(c, s);
+      if (tid == 0) {
+        part->v[0] = stage == kStageKeptCount ? c : sum;
+        part->v[1] = s.u32a;
+        part->v[2] = __float_as_uint(s.found_w);
+      }
+      break;
+    }
+    case kStageDraw: {
+      uint64_t dsum = 0, wsum = 0;
+      uint32_t any = 0;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i)
+        if ((mem >> i) & 1) {
+          const uint64_t wq = wq_of(i);
+          wsum += wq;
+          if (st.drafted) {
+            const uint64_t d = residual_of(wq, st.mass3, draft_q(a, row, tok_of(i)));
+            dsum += d;
+            any |= d > 0;
+          }
+        }
+      dsum = block_sum_u64(dsum, s);
+      wsum = block_sum_u64(wsum, s);
+      any = block_max_u32(any, s);
+      if (tid == 0) {
+        part->v[0] = dsum;
+        part->v[1] = wsum;
+        part->v[2] = any;
+      }
+      break;
+    }
+    case kStageKeptWrite: {
+      // Offset of this chunk: the kept counts of the chunks before it.
+      uint64_t off = 0;
+      for (uint32_t c = 0; c < chunk; ++c) off += a.partials[(uint64_t)row * S + c].v[0];
+      const double scale = (double)st.mass3 * 0x1p-44;
+      const uint32_t wtot = wave_sum_u32(__popcll(mem));
+      __syncthreads();
+      if (lane == 0) s.wu2[w] = wtot;
+      __syncthreads();
+      uint64_t running = off;
+      for (int k = 0; k < (int)w; ++k) running += s.wu2[k];
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) {
+        const uint32_t b = (uint32_t)(mem >> (j * VEC)) & VMASK;
+        const uint32_t nb = __popc(b);
+        uint32_t excl = 0, tot = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint64_t bm = ballot((nb >> k) & 1u);
+          excl += mbcnt(bm) << k;
+          tot += (uint32_t)__popcll(bm) << k;
+        }
+        uint64_t idx = running + excl;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          if ((b >> e) & 1u) {
+            if (idx < a.kept_cap) {
+              const int i = j * VEC + e;
+              a.out_kept_ids[(uint64_t)row * a.kept_cap + idx] = tok_of(i);
+              a.out_kept_probs[(uint64_t)row * a.kept_cap + idx] =
+                  st.mass3 ? (float)((double)weight_of(xs[i], M, inv_t) / scale)
+                           : 0.0f;
+            }
+            ++idx;
+          }
+        running += tot;
+      }
+      break;
+    }
+    default:
+      break;
+  }
+
+  if (stage == kStageTopKLocate || stage == kStageTopPLocate) {
+    // The within-th tie of this chunk closes the kept set.
+    uint64_t ties = 0;
+#pragma unroll
+    for (int i = 0; i < TPL; ++i)
+      if (((mem >> i) & 1) && logit_key(xs[i]) == st.tie_key) ties |= 1ull << i;
+    const uint32_t id = locate(ties, st.within);
+    if (tid == 0) {
+      RowState ns = st;
+      ns.bkey = st.tie_key;
+      ns.bid = id;
+      ns.prefix = 0;
+      ns.pmask = 0;
+      if (stage == kStageTopKLocate && (rp.flags & kRowTopP))
+        ns.stage = kStageMass2;
+      else
+        ns.stage = kStageMass3;
+      a.states[row] = ns;
+    }
+    return;
+  }
+  if (stage == kStageWalk) {
+    // The draw inside the chosen chunk: the first member whose running
+    // weight exceeds the remaining target.
+    uint64_t dl[TPL];
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+      dl[i] = 0;
+      if ((mem >> i) & 1) {
+        const uint64_t wq = wq_of(i);
+        dl[i] = st.residual ? residual_of(wq, st.mass3, draft_q(a, row, tok_of(i))) : wq;
+      }
+    }
+    if (tid == 0) s.hit = kNoToken;
+    // Layout order: token = base + w*SEG + j*64*VEC + lane*VEC + e, so id
+    // order is (w, j, lane, e). Recompute with that order.
+    __syncthreads();
+    uint64_t wsum = 0;
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) wsum += dl[i];
+    const uint64_t wave_total = wave_sum_u64(wsum);
+    __syncthreads();
+    if (lane == 0) s.wl[w] = wave_total;
+    __syncthreads();
+    uint64_t run = 0;
+    for (int k = 0; k < (int)w; ++k) run += s.wl[k];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      uint64_t lsum = 0;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) lsum += dl[j * VEC + e];
+      const uint64_t incl = wave_incl_scan_u64(lsum);
+      const uint64_t jt = shfl_u64(incl, 63);
+      uint64_t acc = run + incl - lsum;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const uint64_t d = dl[j * VEC + e];
+        if (d && acc <= st.within && acc + d > st.within) s.hit = tok_of(j * VEC + e);
+        acc += d;
+      }
+      run += jt;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const double scale = (double)st.mass3 * 0x1p-44;
+      write_result(a, row, s.hit,
+                   st.drafted ? (float)((double)st.draft_w / scale) : 0.0f, 0);
+      RowState ns = st;
+      ns.stage = a.out_kept_ids ? kStageKeptCount : kStageDone;
+      a.states[row] = ns;
+    }
+    return;
+  }
+
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    const uint32_t prev = atomicAdd(&a.counters[row], 1u);
+    s.last = prev == S - 1;
+  }
+  __syncthreads();
+  if (!s.last) return;
+  __threadfence();
+  if (tid == 0) a.counters[row] = 0;
+
+  // Finalize the stage for this row.
+  const StagePartial *parts = a.partials + (uint64_t)row * S;
+  if ((stage >= kStageTopK3 && stage <= kStageTopK0) ||
+      (stage >= kStageTopP3 && stage <= kStageTopP0)) {
+    uint64_t h = 0;
+    for (uint32_t c = 0; c < S; ++c) h += parts[c].v[tid];
+    s.hist[tid] = h;
+    __syncthreads();
+    crossing_bin(s, st.remaining);
+    if (tid == 0) {
+      const bool by_mass = stage >= kStageTopP3;
+      const int d = by_mass ? (int)(kStageTopP0 - stage) : (int)(kStageTopK0 - stage);
+      RowState ns = st;
+      ns.remaining = st.remaining - s.sel_excl;
+      ns.prefix = st.prefix | (s.sel_bin << (8 * d));
+      ns.pmask = st.pmask | (255u << (8 * d));
+      if (d > 0) {
+        ns.stage = stage + 1;
+      } else {
+        ns.tie_key = ns.prefix;
+        if (by_mass) {
+          // Tied tokens weigh the same; keep as many as reach the mass.
+          const uint64_t wk = quantize(weight_of(key_logit(ns.prefix), M, inv_t));
+          ns.remaining = (ns.remaining + wk - 1) / wk;
+          ns.stage = kStageTopPTie;
+        } else {
+          ns.stage = kStageTopKTie;
+        }
+      }
+      a.states[row] = ns;
+    }
+    return;
+  }
+  if (tid != 0) return;
+  RowState ns = st;
+  switch (stage) {
+    case kStageCount1: {
+      uint64_t n1 = 0;
+      for (uint32_t c = 0; c < S; ++c) n1 += parts[c].v[0];
+      ns.n1 = n1;
+      if (rp.top_k < n1) {
+        ns.stage = kStageTopK3;
+        ns.remaining = rp.top_k;
+      } else {
+        ns.stage = (rp.flags & kRowTopP) ? kStageMass2 : kStageMass3;
+      }
+      break;
+    }
+    case kStageTopKTie:
+    case kStageTopPTie: {
+      uint64_t cum = 0;
+      uint32_t c = 0;
+      for (; c < S; ++c) {
+        const uint64_t t = parts[c].v[0];
+        if (cum + t >= st.remaining) break;
+        cum += t;
+      }
+      ns.chunk = c < S ? c : S - 1;
+      ns.within = st.remaining - cum - 1;
+      ns.stage = stage == kStageTopKTie ? kStageTopKLocate : kStageTopPLocate;
+      break;
+    }
+    case kStageMass2: {
+      uint64_t mass = 0;
+      for (uint32_t c = 0; c < S; ++c) mass += parts[c].v[0];
+      ns.mass2 = mass;
+      if (mass == 0) {
+        ns.stage = kStageMass3;
+      } else {
+        ns.nucleus = floor_mul(mass, rp.top_p);
+        ns.remaining = ns.nucleus + 1;
+        ns.prefix = 0;
+        ns.pmask = 0;
+        ns.stage = kStageTopP3;
+      }
+      break;
+    }
+    case kStageMass3: {
+      uint64_t mass = 0;
+      for (uint32_t c = 0; c < S; ++c) {
+        mass += parts[c].v[0];
+        if (parts[c].v[1]) ns.draft_w = __uint_as_float((uint32_t)parts[c].v[2]);
+      }
+      ns.mass3 = mass;
+      if (mass == 0) {
+        write_result(a, row, kNoToken, 0.0f, 0);
+        ns.stage = a.out_kept_ids ? kStageKeptCount : kStageDone;
+      } else {
+        ns.stage = kStageDraw;
+      }
+      break;
+    }
+    case kStageDraw: {
+      uint32_t any = 0;
+      for (uint32_t c = 0; c < S; ++c) any |= (uint32_t)parts[c].v[2];
+      const bool residual = st.drafted && any;
+      uint64_t total = 0;
+      for (uint32_t c = 0; c < S; ++c) total += residual ? parts[c].v[0] : parts[c].v[1];
+      uint64_t target = floor_mul(total, row_uniform(a, row));
+      if (target >= total) target = total - 1;
+      uint64_t cum = 0;
+      uint32_t c = 0;
+      for (; c < S; ++c) {
+        const uint64_t t = residual ? parts[c].v[0] : parts[c].v[1];
+        if (cum + t > target) break;
+        cum += t;
+      }
+      ns.residual = residual ? 1u : 0u;
+      ns.chunk = c < S ? c : S - 1;
+      ns.within = target - cum;
+      ns.target = target;
+      ns.stage = kStageWalk;
+      break;
+    }
+    case kStageKeptCount: {
+      uint64_t kept = 0;
+      for (uint32_t c = 0; c < S; ++c) kept += parts[c].v[0];
+      if (a.out_kept_counts) a.out_kept_counts[row] = (uint32_t)kept;
+      ns.stage = kStageKeptWrite;
+      break;
+    }
+    case kStageKeptWrite:
+      ns.stage = kStageDone;
+      break;
+    default:
+      break;
+  }
+  a.states[row] = ns;
+}
+
+// ---- acceptance --------------------------------------------------------
+
+// finish_acceptance (sampling.metal:1381-1392).
+__device__ __forceinline__ void finish(const uint32_t *tokens, uint32_t accepted,
+                                       uint32_t remaining, uint32_t stop0,
+                                       uint32_t stop1, uint32_t *retained,
+                                       uint32_t *accepted_out) {
+  *accepted_out = accepted;
+  uint32_t kept = min(accepted + 1, remaining);
+  for (uint32_t i = 0; i < kept; ++i)
+    if (tokens[i] == stop0 || tokens[i] == stop1) {
+      kept = i + 1;
+      break;
+    }
+  *retained = kept;
+}
+
+// decode_accept_dflash (sampling.metal:1399-1423, 1514-1558), one thread per
+// lane.
+__global__ void accept_chain_kernel(AcceptChainLaunch a) {
+  const uint32_t lane = blockIdx.x * blockDim.x + threadIdx.x;
+  if (lane >= a.lanes) return;
+  const uint32_t P = a.verify_rows - 1;
+  const AcceptChainLane lp = a.lane_params[lane];
+  const uint32_t *draft = a.proposed + (uint64_t)lane * P;
+  uint32_t *tokens = a.target_tokens + (uint64_t)lane * a.verify_rows;
+  uint32_t accepted = 0;
+  if (lp.sampled) {
+    const uint32_t *ids = a.candidates + (uint64_t)lane * P * 16;
+    const float *probs = a.proposal_probs + (uint64_t)lane * P * 16;
+    const float *p = a.target_draft_probs + (uint64_t)lane * a.verify_rows;
+    const float *u = a.uniforms + (uint64_t)lane * 40;
+    while (accepted < P) {
+      const uint32_t token = draft[accepted];
+      if (token == kNoToken) break;
+      float q = 0.0f;
+      for (int j = 0; j < 16; ++j)
+        if (ids[accepted * 16 + j] == token) {
+          q = probs[accepted * 16 + j];
+          break;
+        }
+      const float uu = u[accepted < 7 ? 8 + accepted : 16 + accepted - 7];
+      if (!(uu * q < p[accepted])) break;
+      tokens[accepted] = token;
+      ++accepted;
+    }
+  } else {
+    while (accepted < P && draft[accepted] == tokens[accepted]) ++accepted;
+  }
+  finish(tokens, accepted, lp.remaining, a.stop0, a.stop1, a.retained + lane,
+         a.accepted + lane);
+}
+
+// verify_tree_accept (tree.metal:20-84), one thread per lane.
+__global__ void accept_tree_kernel(AcceptTreeLaunch a) {
+  const uint32_t lane = blockIdx.x * blockDim.x + threadIdx.x;
+  if (lane >= a.lanes) return;
+  const TreeLaneParams &tr = a.trees[lane];
+  uint32_t *tokens = a.target_tokens + (uint64_t)lane * a.rows_per_lane;
+  const float *p = a.target_draft_probs + (uint64_t)lane * a.rows_per_lane;
+  const float *u = a.uniforms + (uint64_t)lane * 40;
+  const bool sampled = tr.sampled != 0;
+  uint32_t path[8];
+  uint32_t length = 1, current = 0;
+  path[0] = 0;
+  while (length < 8) {
+    if (sampled && current + 1 < tr.chain_rows) {
+      if (u[8 + current] * tr.chain_q[current] < p[current]) {
+        path[length++] = current + 1;
+        current = current + 1;
+        continue;
+      }
+    }
+    const uint32_t wanted = tokens[current];
+    uint32_t found = 0;
+    for (uint32_t r = current + 1; r < tr.rows; ++r)
+      if (tr.parent[r] == current && tr.token[r] == wanted &&
+          !(sampled && r == current + 1 && current + 1 < tr.chain_rows)) {
+        found = r;
+        break;
+      }
+    if (!found) break;
+    path[length++] = found;
+    current = found;
+  }
+  uint32_t output[8];
+  for (uint32_t i = 0; i < length; ++i)
+    output[i] = i + 1 < length ? tr.token[path[i + 1]] : tokens[path[i]];
+  for (uint32_t i = 0; i < length; ++i) tokens[i] = output[i];
+  finish(tokens, length - 1, tr.remaining, a.stop0, a.stop1, a.retained + lane,
+         a.accepted + lane);
+  for (uint32_t i = 0; i < 8; ++i)
+    a.path_rows[(uint64_t)lane * 8 + i] = i < length ? path[i] : path[length - 1];
+}
+
+// ---- launchers -------------------------------------------------------
+
+int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream) {
+  const dim3 grid(a.rows * a.chunks), block(kThreads);
+  if (dtype == 0)
+    hipLaunchKernelGGL(select_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(select_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream) {
+  const dim3 grid(a.rows * a.chunks), block(kThreads);
+  if (dtype == 0)
+    hipLaunchKernelGGL(stage_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(stage_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_accept_chain(const AcceptChainLaunch &a, void *stream) {
+  const dim3 grid((a.lanes + 63) / 64), block(64);
+  hipLaunchKernelGGL(accept_chain_kernel, grid, block, 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_accept_tree(const AcceptTreeLaunch &a, void *stream) {
+  const dim3 grid((a.lanes + 63) / 64), block(64);
+  hipLaunchKernelGGL(accept_tree_kernel, grid, block, 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+}  // namespace jf

@@ -1,0 +1,677 @@
+// Host side of the C ABI (include/jf_sampler.h): argument checks with the
+// reference's messages, per-row kernel parameters, the device penalty table,
+// staged uploads and the launches of jf_kernels.hip.
+#include "jf_sampler.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "jf_kernels.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, std::string message) {
+  g_error = std::move(message);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(JF_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define JF_HIP(call, what)                       \
+  do {                                           \
+    const hipError_t e_ = (call);                \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+// Pinned host slots for asynchronous parameter uploads. A slot is reused
+// only after the copy that last read it has completed.
+class StagingRing {
+ public:
+  ~StagingRing() { release(); }
+
+  int upload(void *device_dst, const void *src, size_t bytes,
+             hipStream_t stream) {
+    if (!bytes) return JF_OK;
+    Slot &slot = slots_[next_];
+    next_ = (next_ + 1) % kSlots;
+    if (slot.pending) {
+      JF_HIP(hipEventSynchronize(slot.event), "staging wait");
+      slot.pending = false;
+    }
+    if (slot.capacity < bytes) {
+      if (slot.host) JF_HIP(hipHostFree(slot.host), "staging free");
+      slot.host = nullptr;
+      slot.capacity = 0;
+      size_t cap = 4096;
+      while (cap < bytes) cap <<= 1;
+      JF_HIP(hipHostMalloc(&slot.host, cap, hipHostMallocDefault),
+             "staging alloc");
+      slot.capacity = cap;
+    }
+    if (!slot.event)
+      JF_HIP(hipEventCreateWithFlags(&slot.event, hipEventDisableTiming),
+             "staging event");
+    std::memcpy(slot.host, src, bytes);
+    JF_HIP(hipMemcpyAsync(device_dst, slot.host, bytes, hipMemcpyHostToDevice,
+                          stream),
+           "parameter upload");
+    JF_HIP(hipEventRecord(slot.event, stream), "staging record");
+    slot.pending = true;
+    return JF_OK;
+  }
+
+  void release() {
+    for (Slot &slot : slots_) {
+      if (slot.pending && slot.event) (void)hipEventSynchronize(slot.event);
+      if (slot.event) (void)hipEventDestroy(slot.event);
+      if (slot.host) (void)hipHostFree(slot.host);
+      slot = Slot{};
+    }
+  }
+
+ private:
+  static constexpr int kSlots = 8;
+  struct Slot {
+    void *host = nullptr;
+    size_t capacity = 0;
+    hipEvent_t event = nullptr;
+    bool pending = false;
+  };
+  Slot slots_[kSlots];
+  int next_ = 0;
+};
+
+template <class T>
+int device_alloc(T **p, size_t count, const char *what) {
+  *p = nullptr;
+  if (!count) return JF_OK;
+  JF_HIP(hipMalloc((void **)p, count * sizeof(T)), what);
+  return JF_OK;
+}
+
+bool penalties_active(const jf_policy &p) {
+  return p.repetition != 1.0f || p.presence != 0.0f || p.frequency != 0.0f;
+}
+
+uint32_t effective_top_k(const jf_policy &p, uint32_t vocabulary) {
+  return p.top_k && p.top_k < vocabulary ? p.top_k : vocabulary;
+}
+
+}  // namespace
+
+struct jf_penalty_table {
+  uint32_t vocabulary = 0;
+  uint32_t rows = 0;
+  uint32_t max_entries = 0;
+  uint32_t buckets = 0;
+  int device = 0;
+  uint2 *entries = nullptr;    // [rows][max_entries] {token, word}
+  uint32_t *offsets = nullptr; // [rows][buckets + 1]
+  std::vector<std::vector<std::pair<uint32_t, uint32_t>>> host;
+  StagingRing staging;
+};
+
+struct jf_sampler {
+  uint32_t vocabulary = 0;
+  uint32_t max_rows = 0;
+  uint32_t max_chunks = 0;
+  int device = 0;
+  jf::RowParams *params = nullptr;
+  jf::BlockHeader *headers = nullptr;
+  uint2 *cands = nullptr;
+  uint32_t *counters = nullptr;
+  jf::RowState *states = nullptr;
+  jf::StagePartial *partials = nullptr;
+  jf::AcceptChainLane *chain_lanes = nullptr;
+  jf::TreeLaneParams *tree_lanes = nullptr;
+  uint64_t workspace_bytes = 0;
+  std::vector<jf::RowParams> last_params;
+  bool params_valid = false;
+  StagingRing staging;
+};
+
+extern "C" {
+
+const char *jf_last_error(void) { return g_error.c_str(); }
+
+int jf_policy_validate(const jf_policy *p) {
+  if (!p) return fail(JF_ERR_INVALID_ARGUMENT, "policy is null");
+  const bool temperature_valid =
+      p->temperature == 0.0f ||
+      (std::isfinite(p->temperature) && p->temperature >= FLT_MIN);
+  if (!temperature_valid || !(p->top_p > 0.0f && p->top_p <= 1.0f) ||
+      !(p->min_p >= 0.0f) || p->min_p > 1.0f)
+    return fail(JF_ERR_INVALID_ARGUMENT,
+                "sampling requires temperature 0 or at least FLT_MIN, top_p "
+                "in (0,1] and min_p in [0,1]");
+  if (!(std::fabs(p->presence) <= 2.0f) || !(std::fabs(p->frequency) <= 2.0f) ||
+      !std::isfinite(p->repetition) || p->repetition <= 0.0f)
+    return fail(JF_ERR_INVALID_ARGUMENT,
+                "sampling requires presence and frequency penalties in [-2,2] "
+                "and a positive repetition penalty");
+  return JF_OK;
+}
+
+// ---- sampler -------------------------------------------------------------
+
+int jf_sampler_destroy(jf_sampler *s) {
+  if (!s) return JF_OK;
+  s->staging.release();
+  (void)hipFree(s->params);
+  (void)hipFree(s->headers);
+  (void)hipFree(s->cands);
+  (void)hipFree(s->counters);
+  (void)hipFree(s->states);
+  (void)hipFree(s->partials);
+  (void)hipFree(s->chain_lanes);
+  (void)hipFree(s->tree_lanes);
+  delete s;
+  return JF_OK;
+}
+
+int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
+                      jf_sampler **out) {
+  if (!out) return fail(JF_ERR_INVALID_ARGUMENT, "output pointer is null");
+  *out = nullptr;
+  if (!vocabulary) return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling geometry");
+  if (!max_rows) return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling workspace row count");
+  const uint32_t max_chunks = (vocabulary + jf::kChunkF32 - 1) / jf::kChunkF32;
+  if (max_chunks > 64)
+    return fail(JF_ERR_INVALID_ARGUMENT, "vocabulary exceeds 524288 tokens");
+  jf_sampler *s = new (std::nothrow) jf_sampler;
+  if (!s) return fail(JF_ERR_NO_MEMORY, "sampler allocation failed");
+  s->vocabulary = vocabulary;
+  s->max_rows = max_rows;
+  s->max_chunks = max_chunks;
+  int rc = JF_OK;
+  const hipError_t ge = hipGetDevice(&s->device);
+  if (ge != hipSuccess) rc = hip_fail(ge, "hipGetDevice");
+  const uint64_t blocks = (uint64_t)max_rows * max_chunks;
+  if (rc == JF_OK) rc = device_alloc(&s->params, max_rows, "row parameters");
+  if (rc == JF_OK) rc = device_alloc(&s->headers, blocks, "block headers");
+  if (rc == JF_OK) rc = device_alloc(&s->cands, blocks * jf::kBlockCandidates, "candidates");
+  if (rc == JF_OK) rc = device_alloc(&s->counters, max_rows, "arrival counters");
+  if (rc == JF_OK) rc = device_alloc(&s->states, max_rows, "row states");
+  if (rc == JF_OK) rc = device_alloc(&s->partials, blocks, "stage partials");
+  if (rc == JF_OK) rc = device_alloc(&s->chain_lanes, max_rows, "chain lanes");
+  if (rc == JF_OK) rc = device_alloc(&s->tree_lanes, max_rows, "tree lanes");
+  if (rc == JF_OK) {
+    const hipError_t e1 = hipMemset(s->counters, 0, max_rows * sizeof(uint32_t));
+    const hipError_t e2 = hipMemset(s->states, 0, max_rows * sizeof(jf::RowState));
+    const hipError_t e3 = hipDeviceSynchronize();
+    if (e1 != hipSuccess) rc = hip_fail(e1, "counter init");
+    else if (e2 != hipSuccess) rc = hip_fail(e2, "state init");
+    else if (e3 != hipSuccess) rc = hip_fail(e3, "init sync");
+  }
+  if (rc != JF_OK) {
+    jf_sampler_destroy(s);
+    return rc;
+  }
+  s->workspace_bytes =
+      max_rows * (sizeof(jf::RowParams) + sizeof(uint32_t) + sizeof(jf::RowState) +
+                  sizeof(jf::AcceptChainLane) + sizeof(jf::TreeLaneParams)) +
+      blocks * (sizeof(jf::BlockHeader) + jf::kBlockCandidates * sizeof(uint2) +
+                sizeof(jf::StagePartial));
+  *out = s;
+  return JF_OK;
+}
+
+uint64_t jf_sampler_workspace_bytes(const jf_sampler *s) {
+  return s ? s->workspace_bytes : 0;
+}
+
+static int check_device(int device) {
+  int current = -1;
+  JF_HIP(hipGetDevice(&current), "hipGetDevice");
+  if (current != device)
+    return fail(JF_ERR_INVALID_ARGUMENT,
+                "call made on a different device than the object was created on");
+  return JF_OK;
+}
+
+// ---- penalties -------------------------------------------------------------
+
+int jf_penalty_words_rebuild(uint32_t *words, uint32_t vocabulary,
+                             const uint32_t *history, uint64_t history_len,
+                             uint64_t generated, int has_pending,
+                             uint32_t pending, int mark_prompt) {
+  if (history_len <= generated)
+    return fail(JF_ERR_LOGIC, "request history holds no prompt");
+  if ((!words && vocabulary) || (!history && history_len))
+    return fail(JF_ERR_INVALID_ARGUMENT, "null buffer");
+  for (uint64_t i = 0; i < history_len; ++i)
+    if (history[i] >= vocabulary)
+      return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
+  if (has_pending && pending >= vocabulary)
+    return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
+  const uint64_t prompt = history_len - generated;
+  std::fill(words, words + vocabulary, 0u);
+  if (mark_prompt)
+    for (uint64_t i = 0; i < prompt; ++i) words[history[i]] |= JF_PENALTY_PROMPT_BIT;
+  for (uint64_t i = prompt; i < history_len; ++i) ++words[history[i]];
+  if (has_pending) ++words[pending];
+  return JF_OK;
+}
+
+int jf_penalty_words_count(uint32_t *words, uint32_t vocabulary,
+                           const uint32_t *selected, uint64_t count) {
+  if ((!selected && count) || (!words && vocabulary))
+    return fail(JF_ERR_INVALID_ARGUMENT, "null buffer");
+  for (uint64_t i = 0; i < count; ++i)
+    if (selected[i] >= vocabulary)
+      return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
+  for (uint64_t i = 0; i < count; ++i) ++words[selected[i]];
+  return JF_OK;
+}
+
+int jf_penalty_table_destroy(jf_penalty_table *t) {
+  if (!t) return JF_OK;
+  t->staging.release();
+  (void)hipFree(t->entries);
+  (void)hipFree(t->offsets);
+  delete t;
+  return JF_OK;
+}
+
+int jf_penalty_table_create(uint32_t vocabulary, uint32_t rows,
+                            uint32_t max_entries, jf_penalty_table **out) {
+  if (!out) return fail(JF_ERR_INVALID_ARGUMENT, "output pointer is null");
+  *out = nullptr;
+  if (!vocabulary || !rows || !max_entries)
+    return fail(JF_ERR_INVALID_ARGUMENT, "invalid penalty table geometry");
+  jf_penalty_table *t = new (std::nothrow) jf_penalty_table;
+  if (!t) return fail(JF_ERR_NO_MEMORY, "penalty table allocation failed");
+  t->vocabulary = vocabulary;
+  t->rows = rows;
+  t->max_entries = max_entries;
+  t->buckets = (vocabulary + jf::kPenaltyBucket - 1) / jf::kPenaltyBucket;
+  t->host.resize(rows);
+  int rc = JF_OK;
+  hipError_t ge = hipGetDevice(&t->device);
+  if (ge != hipSuccess) rc = hip_fail(ge, "hipGetDevice");
+  if (rc == JF_OK) rc = device_alloc(&t->entries, (size_t)rows * max_entries, "penalty entries");
+  if (rc == JF_OK) rc = device_alloc(&t->offsets, (size_t)rows * (t->buckets + 1), "penalty offsets");
+  if (rc == JF_OK) {
+    ge = hipMemset(t->offsets, 0, (size_t)rows * (t->buckets + 1) * sizeof(uint32_t));
+    if (ge == hipSuccess) ge = hipDeviceSynchronize();
+    if (ge != hipSuccess) rc = hip_fail(ge, "penalty table init");
+  }
+  if (rc != JF_OK) {
+    jf_penalty_table_destroy(t);
+    return rc;
+  }
+  *out = t;
+  return JF_OK;
+}
+
+static int upload_penalty_row(jf_penalty_table *t, uint32_t row, void *stream) {
+  const auto &h = t->host[row];
+  std::vector<uint8_t> blob(h.size() * sizeof(uint2) +
+                            (t->buckets + 1) * sizeof(uint32_t));
+  uint2 *ent = (uint2 *)blob.data();
+  uint32_t *off = (uint32_t *)(blob.data() + h.size() * sizeof(uint2));
+  uint32_t bucket = 0;
+  for (size_t i = 0; i < h.size(); ++i) {
+    ent[i] = make_uint2(h[i].first, h[i].second);
+    while (bucket <= h[i].first / jf::kPenaltyBucket) off[bucket++] = (uint32_t)i;
+  }
+  while (bucket <= t->buckets) off[bucket++] = (uint32_t)h.size();
+  const hipStream_t st = (hipStream_t)stream;
+  int rc = t->staging.upload(t->entries + (size_t)row * t->max_entries, ent,
+                             h.size() * sizeof(uint2), st);
+  if (rc != JF_OK) return rc;
+  return t->staging.upload(t->offsets + (size_t)row * (t->buckets + 1), off,
+                           (t->buckets + 1) * sizeof(uint32_t), st);
+}
+
+int jf_penalty_table_rebuild(jf_penalty_table *t, uint32_t row,
+                             const uint32_t *history, uint64_t history_len,
+                             uint64_t generated, int has_pending,
+                             uint32_t pending, int mark_prompt, void *stream) {
+  if (!t) return fail(JF_ERR_INVALID_ARGUMENT, "penalty table is null");
+  if (row >= t->rows)
+    return fail(JF_ERR_INVALID_ARGUMENT, "penalized lane has no penalty table row");
+  int rc = check_device(t->device);
+  if (rc != JF_OK) return rc;
+  std::vector<uint32_t> words(t->vocabulary);
+  rc = jf_penalty_words_rebuild(words.data(), t->vocabulary, history, history_len,
+                                generated, has_pending, pending, mark_prompt);
+  if (rc != JF_OK) return rc;
+  std::vector<std::pair<uint32_t, uint32_t>> entries;
+  for (uint32_t v = 0; v < t->vocabulary; ++v)
+    if (words[v]) entries.emplace_back(v, words[v]);
+  if (entries.size() > t->max_entries)
+    return fail(JF_ERR_INVALID_ARGUMENT, "penalty history exceeds the table row");
+  t->host[row] = std::move(entries);
+  return upload_penalty_row(t, row, stream);
+}
+
+int jf_penalty_table_count(jf_penalty_table *t, uint32_t row,
+                           const uint32_t *selected, uint64_t count,
+                           void *stream) {
+  if (!t) return fail(JF_ERR_INVALID_ARGUMENT, "penalty table is null");
+  if (row >= t->rows)
+    return fail(JF_ERR_INVALID_ARGUMENT, "penalized lane has no penalty table row");
+  if (!selected && count) return fail(JF_ERR_INVALID_ARGUMENT, "null buffer");
+  int rc = check_device(t->device);
+  if (rc != JF_OK) return rc;
+  for (uint64_t i = 0; i < count; ++i)
+    if (selected[i] >= t->vocabulary)
+      return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
+  auto h = t->host[row];
+  for (uint64_t i = 0; i < count; ++i) {
+    auto it = std::lower_bound(h.begin(), h.end(),
+                               std::make_pair(selected[i], 0u));
+    if (it != h.end() && it->first == selected[i])
+      ++it->second;
+    else
+      h.insert(it, std::make_pair(selected[i], 1u));
+  }
+  if (h.size() > t->max_entries)
+    return fail(JF_ERR_INVALID_ARGUMENT, "penalty history exceeds the table row");
+  t->host[row] = std::move(h);
+  return upload_penalty_row(t, row, stream);
+}
+
+// ---- uniforms ---------------------------------------------------------
+
+float jf_next_uniform(uint64_t seed, uint64_t *counter) {
+  uint64_t v = seed + (++*counter) * 0x9e3779b97f4a7c15ULL;
+  v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ULL;
+  v = (v ^ (v >> 27)) * 0x94d049bb133111ebULL;
+  v ^= v >> 31;
+  return float(v >> 40) * 0x1p-24F;
+}
+
+void jf_stage_sampling_cycle(uint64_t seed, uint64_t *counter,
+                             uint32_t verify_rows, int tree_cycle,
+                             float *u) {
+  std::fill(u, u + JF_SAMPLING_UNIFORMS, 0.0f);
+  const uint32_t end = (tree_cycle && verify_rows == 16) ? JF_SAMPLING_UNIFORMS
+                       : verify_rows == 16                ? 24u
+                                                          : 16u;
+  for (uint32_t i = JF_UNIFORM_PROPOSALS; i < end; ++i)
+    u[i] = jf_next_uniform(seed, counter);
+}
+
+// ---- selection ---------------------------------------------------------
+
+int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
+  if (!s || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler or arguments");
+  int rc = check_device(s->device);
+  if (rc != JF_OK) return rc;
+  const uint32_t V = s->vocabulary, rows = a->rows;
+  if (!rows || rows > s->max_rows)
+    return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling batch width");
+  if (a->dtype != JF_DTYPE_F32 && a->dtype != JF_DTYPE_BF16)
+    return fail(JF_ERR_INVALID_ARGUMENT, "unsupported logits dtype");
+  if (!a->logits || !a->policies || !a->out_tokens)
+    return fail(JF_ERR_INVALID_ARGUMENT, "null logits, policies or output tokens");
+  const uint64_t esize = a->dtype == JF_DTYPE_F32 ? 4 : 2;
+  if (rows > 1 && a->logits_stride < V)
+    return fail(JF_ERR_INVALID_ARGUMENT, "logits row stride is below the vocabulary");
+  if ((uintptr_t)a->logits % esize)
+    return fail(JF_ERR_INVALID_ARGUMENT, "logits are not aligned to their element size");
+  const bool aligned =
+      (uintptr_t)a->logits % 16 == 0 && (rows == 1 || (a->logits_stride * esize) % 16 == 0);
+  const bool kept = a->out_kept_ids || a->out_kept_probs || a->out_kept_counts;
+  if (kept && (!a->out_kept_ids || !a->out_kept_probs || !a->out_kept_counts ||
+               !a->kept_capacity))
+    return fail(JF_ERR_INVALID_ARGUMENT,
+                "kept outputs need ids, probabilities, counts and a capacity");
+  const uint32_t W = (V + 31) / 32;
+  std::vector<jf::RowParams> params(rows);
+  bool any_constrained = false, any_sampled = false, staged = false;
+  bool need_count1 = false, need_topk = false, need_topp = false;
+  for (uint32_t r = 0; r < rows; ++r) {
+    const jf_policy &p = a->policies[r];
+    rc = jf_policy_validate(&p);
+    if (rc != JF_OK) return rc;
+    jf::RowParams rp{};
+    const bool sampled = p.temperature > 0.0f;
+    if (sampled) {
+      rp.flags |= jf::kRowSampled;
+      rp.top_k = effective_top_k(p, V);
+      rp.inv_t = 1.0f / p.temperature;
+      rp.top_p = p.top_p;
+      if (rp.top_k < V) rp.flags |= jf::kRowTopK;
+      if (p.top_p < 1.0f) rp.flags |= jf::kRowTopP;
+      if (p.min_p > 0.0f) {
+        rp.flags |= jf::kRowMinP;
+        rp.minp_offset = p.temperature * std::log(p.min_p);
+      }
+      any_sampled = true;
+      if (rp.top_k > (uint32_t)jf::kBlockCandidates) {
+        staged = true;
+        need_count1 |= (rp.flags & jf::kRowMinP) != 0;
+        need_topk |= (rp.flags & jf::kRowTopK) != 0;
+        need_topp |= (rp.flags & jf::kRowTopP) != 0;
+      }
+    }
+    if (p.flags & JF_POLICY_CONSTRAINED) {
+      rp.flags |= jf::kRowConstrained;
+      any_constrained = true;
+    }
+    if (p.flags & JF_POLICY_EXCLUDE_STOP) rp.flags |= jf::kRowExcludeStop;
+    rp.penalty_row = JF_NO_TOKEN;
+    const uint32_t extra = a->extra_counts ? a->extra_counts[r] : 0u;
+    if (extra > (uint32_t)jf::kMaxExtra)
+      return fail(JF_ERR_INVALID_ARGUMENT, "more than 16 extra penalty tokens in a row");
+    if (extra && !a->extra_tokens)
+      return fail(JF_ERR_INVALID_ARGUMENT, "extra penalty tokens are null");
+    if (penalties_active(p)) {
+      if (!a->penalties || !a->penalty_rows || a->penalty_rows[r] >= a->penalties->rows)
+        return fail(JF_ERR_INVALID_ARGUMENT, "penalized lane has no penalty table row");
+      if (a->penalties->vocabulary != V)
+        return fail(JF_ERR_INVALID_ARGUMENT, "penalty table vocabulary differs");
+      rp.flags |= jf::kRowPenalized;
+      rp.penalty_row = a->penalty_rows[r];
+      rp.extra_count = extra;
+      rp.repetition = p.repetition;
+      rp.repetition_inverse = std::min(1.0f / p.repetition, FLT_MAX);
+      rp.presence = p.presence;
+      rp.frequency = p.frequency;
+    }
+    params[r] = rp;
+  }
+  if (any_constrained && (!a->masks || (rows > 1 && a->mask_stride < W)))
+    return fail(JF_ERR_INVALID_ARGUMENT, "constraint mask buffer is missing or short");
+  if (any_sampled && !a->uniforms)
+    return fail(JF_ERR_INVALID_ARGUMENT, "sampling uniforms are null");
+  if (a->draft_tokens && a->drafted_rows && !a->draft_q &&
+      (!a->draft_cand_ids || !a->draft_cand_probs))
+    return fail(JF_ERR_INVALID_ARGUMENT, "drafted rows need draft probabilities");
+
+  const hipStream_t st = (hipStream_t)stream;
+  const bool same = s->params_valid && s->last_params.size() == params.size() &&
+                    std::memcmp(s->last_params.data(), params.data(),
+                                params.size() * sizeof(jf::RowParams)) == 0;
+  if (!same) {
+    rc = s->staging.upload(s->params, params.data(),
+                           params.size() * sizeof(jf::RowParams), st);
+    if (rc != JF_OK) return rc;
+    s->last_params = params;
+    s->params_valid = true;
+  }
+
+  jf::SampleLaunch L{};
+  L.logits = a->logits;
+  L.stride = rows > 1 ? a->logits_stride : V;
+  L.masks = a->masks;
+  L.mask_stride = a->mask_stride;
+  L.params = s->params;
+  L.vocabulary = V;
+  L.chunks = (V + (a->dtype == JF_DTYPE_F32 ? jf::kChunkF32 : jf::kChunkBF16) - 1) /
+             (a->dtype == JF_DTYPE_F32 ? jf::kChunkF32 : jf::kChunkBF16);
+  L.rows = rows;
+  L.stop0 = a->stop_token_0;
+  L.stop1 = a->stop_token_1;
+  L.aligned = aligned ? 1u : 0u;
+  if (a->penalties) {
+    L.pen_entries = a->penalties->entries;
+    L.pen_offsets = a->penalties->offsets;
+    L.pen_max_entries = a->penalties->max_entries;
+    L.pen_buckets = a->penalties->buckets;
+  }
+  L.extra = a->extra_tokens;
+  L.extra_stride = a->extra_stride;
+  L.uniforms = a->uniforms;
+  L.uniform_index = a->uniform_index;
+  L.uniform_offset = a->uniform_offset;
+  L.uniform_stride = a->uniform_stride;
+  L.draft_tokens = a->draft_tokens;
+  L.drafted_rows = a->draft_tokens ? a->drafted_rows : 0u;
+  L.cand_ids = a->draft_cand_ids;
+  L.cand_probs = a->draft_cand_probs;
+  L.dense_q = a->draft_q;
+  L.q_stride = a->draft_q_stride;
+  L.headers = s->headers;
+  L.cands = s->cands;
+  L.counters = s->counters;
+  L.states = s->states;
+  L.partials = s->partials;
+  L.out_tokens = a->out_tokens;
+  L.out_draft = a->out_draft_probs;
+  L.out_kept_counts = a->out_kept_counts;
+  L.out_kept_ids = a->out_kept_ids;
+  L.out_kept_probs = a->out_kept_probs;
+  L.kept_cap = a->kept_capacity;
+
+  int e = jf::launch_select(L, a->dtype, stream);
+  if (e != hipSuccess) return hip_fail((hipError_t)e, "select launch");
+  if (staged) {
+    for (uint32_t stage = jf::kStageCount1; stage <= jf::kStageLast; ++stage) {
+      if (stage == jf::kStageCount1 && !need_count1) continue;
+      if (stage >= jf::kStageTopK3 && stage <= jf::kStageTopKLocate && !need_topk) continue;
+      if (stage >= jf::kStageMass2 && stage <= jf::kStageTopPLocate && !need_topp) continue;
+      if (stage >= jf::kStageKeptCount && !kept) continue;
+      L.stage = stage;
+      e = jf::launch_stage(L, a->dtype, stream);
+      if (e != hipSuccess) return hip_fail((hipError_t)e, "stage launch");
+    }
+  }
+  return JF_OK;
+}
+
+// ---- acceptance -----------------------------------------------------------
+
+int jf_accept_chain(jf_sampler *s, const jf_accept_chain_args *a,
+                    void *stream) {
+  if (!s || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler or arguments");
+  int rc = check_device(s->device);
+  if (rc != JF_OK) return rc;
+  if (!a->lanes || a->lanes > s->max_rows || !a->maximum_retained || !a->policies)
+    return fail(JF_ERR_INVALID_ARGUMENT, "invalid DFlash acceptance batch");
+  if (a->verify_rows != 8 && a->verify_rows != 16)
+    return fail(JF_ERR_INVALID_ARGUMENT, "verify shape must be 8 or 16");
+  if (!a->proposed_tokens || !a->target_tokens || !a->retained_counts ||
+      !a->accepted_counts)
+    return fail(JF_ERR_INVALID_ARGUMENT, "null acceptance buffer");
+  std::vector<jf::AcceptChainLane> lanes(a->lanes);
+  bool any_sampled = false;
+  for (uint32_t l = 0; l < a->lanes; ++l) {
+    const uint32_t m = a->maximum_retained[l];
+    if (!m || m > a->verify_rows)
+      return fail(JF_ERR_INVALID_ARGUMENT, "invalid DFlash retention limit");
+    lanes[l].remaining = m;
+    lanes[l].sampled = a->policies[l].temperature > 0.0f ? 1u : 0u;
+    any_sampled |= lanes[l].sampled != 0;
+  }
+  if (any_sampled && (!a->candidates || !a->proposal_probs ||
+                      !a->target_draft_probs || !a->uniforms))
+    return fail(JF_ERR_INVALID_ARGUMENT, "sampled acceptance needs candidates, "
+                                         "probabilities and uniforms");
+  rc = s->staging.upload(s->chain_lanes, lanes.data(),
+                         lanes.size() * sizeof(jf::AcceptChainLane),
+                         (hipStream_t)stream);
+  if (rc != JF_OK) return rc;
+  jf::AcceptChainLaunch L{};
+  L.lanes = a->lanes;
+  L.verify_rows = a->verify_rows;
+  L.proposed = a->proposed_tokens;
+  L.candidates = a->candidates;
+  L.proposal_probs = a->proposal_probs;
+  L.target_draft_probs = a->target_draft_probs;
+  L.uniforms = a->uniforms;
+  L.target_tokens = a->target_tokens;
+  L.retained = a->retained_counts;
+  L.accepted = a->accepted_counts;
+  L.lane_params = s->chain_lanes;
+  L.stop0 = a->stop_token_0;
+  L.stop1 = a->stop_token_1;
+  const int e = jf::launch_accept_chain(L, stream);
+  if (e != hipSuccess) return hip_fail((hipError_t)e, "acceptance launch");
+  return JF_OK;
+}
+
+int jf_accept_tree(jf_sampler *s, const jf_accept_tree_args *a, void *stream) {
+  if (!s || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler or arguments");
+  int rc = check_device(s->device);
+  if (rc != JF_OK) return rc;
+  if (!a->lanes || a->lanes > s->max_rows || !a->trees || !a->maximum_retained ||
+      !a->policies)
+    return fail(JF_ERR_INVALID_ARGUMENT, "invalid tree acceptance batch");
+  if (!a->rows_per_lane || a->rows_per_lane > JF_TREE_MAXIMUM_ROWS)
+    return fail(JF_ERR_INVALID_ARGUMENT, "tree rows per lane must be 1..16");
+  if (!a->target_tokens || !a->retained_counts || !a->accepted_counts ||
+      !a->path_rows)
+    return fail(JF_ERR_INVALID_ARGUMENT, "null acceptance buffer");
+  std::vector<jf::TreeLaneParams> lanes(a->lanes);
+  bool any_sampled = false;
+  for (uint32_t l = 0; l < a->lanes; ++l) {
+    const jf_tree_lane &t = a->trees[l];
+    if (!t.rows || t.rows > a->rows_per_lane || t.chain_rows > t.rows)
+      return fail(JF_ERR_INVALID_ARGUMENT, "invalid draft tree rows");
+    for (uint32_t r = 1; r < t.rows; ++r)
+      if (t.parent[r] >= r)
+        return fail(JF_ERR_INVALID_ARGUMENT, "draft tree rows are not in DFS preorder");
+    const uint32_t m = a->maximum_retained[l];
+    if (!m || m > JF_TREE_MAXIMUM_DEPTH)
+      return fail(JF_ERR_INVALID_ARGUMENT, "invalid tree retention limit");
+    jf::TreeLaneParams &p = lanes[l];
+    p.rows = t.rows;
+    p.chain_rows = t.chain_rows;
+    p.remaining = m;
+    p.sampled = a->policies[l].temperature > 0.0f ? 1u : 0u;
+    any_sampled |= p.sampled != 0;
+    std::memcpy(p.parent, t.parent, sizeof(p.parent));
+    std::memcpy(p.token, t.token, sizeof(p.token));
+    std::memcpy(p.chain_q, t.chain_q, sizeof(p.chain_q));
+  }
+  if (any_sampled && (!a->target_draft_probs || !a->uniforms))
+    return fail(JF_ERR_INVALID_ARGUMENT,
+                "sampled tree acceptance needs probabilities and uniforms");
+  rc = s->staging.upload(s->tree_lanes, lanes.data(),
+                         lanes.size() * sizeof(jf::TreeLaneParams),
+                         (hipStream_t)stream);
+  if (rc != JF_OK) return rc;
+  jf::AcceptTreeLaunch L{};
+  L.lanes = a->lanes;
+  L.rows_per_lane = a->rows_per_lane;
+  L.trees = s->tree_lanes;
+  L.target_draft_probs = a->target_draft_probs;
+  L.uniforms = a->uniforms;
+  L.target_tokens = a->target_tokens;
+  L.retained = a->retained_counts;
+  L.accepted = a->accepted_counts;
+  L.path_rows = a->path_rows;
+  L.stop0 = a->stop_token_0;
+  L.stop1 = a->stop_token_1;
+  const int e = jf::launch_accept_tree(L, stream);
+  if (e != hipSuccess) return hip_fail((hipError_t)e, "tree acceptance launch");
+  return JF_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,609 @@
+/*
+ * jf_oracle.c — CPU restatement of JustFit's logits->token path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see jf_oracle.h): the checker for the HIP build
+ * and the timed CPU baseline. Built with -O2 -ffp-contract=off so every fp32
+ * expression rounds exactly as written.
+ *
+ * Pins (tests/test_oracle.py):
+ *   jfo_logit_key / jfo_key_logit  order and +-0 against float compares,
+ *                                  round trip over sampled bit patterns.
+ *   jfo_expf                       <= 2 ulp against double exp over a sweep.
+ *   jfo_floor_mul                  against Python's exact integers.
+ *   jfo_splitmix64                 published SplitMix64 known answers
+ *                                  (Steele, Lea & Flood 2014; seed 0 ->
+ *                                  0xe220a8397b1dcdaf).
+ *   penalty words                  against a dict-based restatement and the
+ *                                  closed-form penalty formula.
+ *   jfo_select_row greedy          np.argmax with lowest-id ties.
+ *   jfo_select_row sampled         brute force over tiny vocabularies
+ *                                  (itertools/fractions), kept sets against
+ *                                  sort-by-(logit desc, id asc), probabilities
+ *                                  against float64 softmax (1e-5), chi-square
+ *                                  of the draw over many uniforms, and the
+ *                                  speculative-sampling identity for the
+ *                                  residual draw.
+ *   chain/tree acceptance          hand-built cases, chain-shaped trees equal
+ *                                  to chain acceptance.
+ */
+#include "jf_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- scalar helpers --------------------------------------------------- */
+
+static uint32_t f2u(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+static float u2f(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* sampling.metal:167-171: a larger logit has a larger key; -0 and +0 share. */
+uint32_t jfo_logit_key(float value) {
+  uint32_t bits = f2u(value);
+  bits = (bits << 1) ? bits : 0u;
+  return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+}
+
+/* sampling.metal:172-174 */
+float jfo_key_logit(uint32_t key) {
+  return u2f((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+/* Cephes expf (S. L. Moshier, Cephes Math Library): x = n ln2 + r with the
+ * two-constant Cody-Waite split of ln2, e^r = 1 + r + r^2 P(r) with Cephes'
+ * degree-5 P, then scaling by 2^n. Below -86 the result is 0, so every
+ * nonzero result is a normal float. */
+float jfo_expf(float x) {
+  if (!(x >= -86.0f))
+    return 0.0f;
+  if (x > 88.0f)
+    return INFINITY;
+  const float n = rintf(x * 1.44269504088896341f);
+  float r = fmaf(n, -0.693359375f, x);
+  r = fmaf(n, 2.12194440e-4f, r);
+  float p = 1.9875691500e-4f;
+  p = fmaf(p, r, 1.3981999507e-3f);
+  p = fmaf(p, r, 8.3334519073e-3f);
+  p = fmaf(p, r, 4.1665795894e-2f);
+  p = fmaf(p, r, 1.6666665459e-1f);
+  p = fmaf(p, r, 5.0000001201e-1f);
+  const float r2 = r * r;
+  const float y = fmaf(p, r2, r) + 1.0f;
+  const int ni = (int)n;
+  return y * u2f((uint32_t)(ni + 127) << 23);
+}
+
+/* floor(a * f) exactly, for f in [0, 1] (NaN and f <= 0 give 0, f >= 1 gives
+ * a). f = M * 2^-sh with a 24-bit M, so the product fits 128 bits. */
+uint64_t jfo_floor_mul(uint64_t a, float f) {
+  if (!(f > 0.0f))
+    return 0;
+  if (f >= 1.0f)
+    return a;
+  const uint32_t b = f2u(f);
+  const uint32_t e = b >> 23;
+  const uint64_t m = e ? ((b & 0x7fffffu) | 0x800000u) : (b & 0x7fffffu);
+  const int sh = e ? 150 - (int)e : 149;
+  const unsigned __int128 p = (unsigned __int128)a * m;
+  return sh >= 128 ? 0 : (uint64_t)(p >> sh);
+}
+
+/* Runtime.cpp:1098-1105 (SplitMix64 finalizer over seed + counter * golden). */
+uint64_t jfo_splitmix64(uint64_t seed, uint64_t counter) {
+  uint64_t v = seed + counter * 0x9e3779b97f4a7c15ULL;
+  v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ULL;
+  v = (v ^ (v >> 27)) * 0x94d049bb133111ebULL;
+  return v ^ (v >> 31);
+}
+
+float jfo_next_uniform(uint64_t seed, uint64_t *counter) {
+  const uint64_t v = jfo_splitmix64(seed, ++*counter);
+  return (float)(v >> 40) * 0x1p-24f;
+}
+
+/* Runtime.cpp:1107-1114: slots 1.. of a cycle; 16 for 8 verify rows, 24 for
+ * 16, all 40 for a 16-row tree cycle. */
+void jfo_stage_cycle(uint64_t seed, uint64_t *counter, uint32_t verify_rows,
+                     int tree_cycle, float *u) {
+  for (int i = 0; i < 40; ++i)
+    u[i] = 0.0f;
+  const uint32_t end =
+      (tree_cycle && verify_rows == 16) ? 40u : verify_rows == 16 ? 24u : 16u;
+  for (uint32_t i = 1; i < end; ++i)
+    u[i] = jfo_next_uniform(seed, counter);
+}
+
+/* ---- penalties -------------------------------------------------------- */
+
+/* Sampling.cpp:50-71 (rebuildPenaltyWords). Returns -1 for a history without
+ * a prompt, -2 for a token outside the vocabulary. */
+int jfo_rebuild_penalty_words(uint32_t *words, uint32_t vocabulary,
+                              const uint32_t *history, uint64_t history_len,
+                              uint64_t generated, int has_pending,
+                              uint32_t pending, int mark_prompt) {
+  if (history_len <= generated)
+    return -1;
+  for (uint64_t i = 0; i < history_len; ++i)
+    if (history[i] >= vocabulary)
+      return -2;
+  if (has_pending && pending >= vocabulary)
+    return -2;
+  const uint64_t prompt = history_len - generated;
+  memset(words, 0, (size_t)vocabulary * 4);
+  if (mark_prompt)
+    for (uint64_t i = 0; i < prompt; ++i)
+      words[history[i]] |= JFO_PENALTY_PROMPT_BIT;
+  for (uint64_t i = prompt; i < history_len; ++i)
+    ++words[history[i]];
+  if (has_pending)
+    ++words[pending];
+  return 0;
+}
+
+/* Sampling.cpp:75-80 (countPenaltyTokens). */
+int jfo_count_penalty_tokens(uint32_t *words, uint32_t vocabulary,
+                             const uint32_t *selected, uint64_t count) {
+  for (uint64_t i = 0; i < count; ++i)
+    if (selected[i] >= vocabulary)
+      return -2;
+  for (uint64_t i = 0; i < count; ++i)
+    ++words[selected[i]];
+  return 0;
+}
+
+/* Sampling.cpp:110-112: 1 / repetition, saturated to the largest float. */
+float jfo_repetition_inverse(float repetition) {
+  const float inv = 1.0f / repetition;
+  return inv < FLT_MAX ? inv : FLT_MAX;
+}
+
+/* sampling.metal:928-935 (penalize_logit); clamp = fmin(fmax(.)), so a NaN
+ * becomes -FLT_MAX. */
+float jfo_penalize_logit(float value, uint32_t count, float repetition,
+                         float repetition_inverse, float presence,
+                         float frequency) {
+  value *= value > 0.0f ? repetition_inverse : repetition;
+  if (count) {
+    const float scaled = frequency * (float)count;
+    const float lowered = scaled + presence;
+    value = value - lowered;
+  }
+  return fminf(fmaxf(value, -FLT_MAX), FLT_MAX);
+}
+
+/* ---- policy ----------------------------------------------------------- */
+
+/* Model.hpp:77-95 (validationError). */
+int jfo_policy_valid(const jfo_policy *p) {
+  const int t_ok = p->temperature == 0.0f ||
+                   (isfinite(p->temperature) && p->temperature >= FLT_MIN);
+  if (!t_ok || !(p->top_p > 0.0f && p->top_p <= 1.0f) || !(p->min_p >= 0.0f) ||
+      p->min_p > 1.0f)
+    return -1;
+  if (!(fabsf(p->presence) <= 2.0f) || !(fabsf(p->frequency) <= 2.0f) ||
+      !isfinite(p->repetition) || p->repetition <= 0.0f)
+    return -2;
+  return 0;
+}
+
+static int penalties_active(const jfo_policy *p) {
+  return p->repetition != 1.0f || p->presence != 0.0f || p->frequency != 0.0f;
+}
+
+/* ---- one row ---------------------------------------------------------- */
+
+typedef struct {
+  uint32_t key;
+  uint32_t id;
+} keyed;
+
+/* Order of the logits: key descending, id ascending (sampling.metal:176-207). */
+static int by_order(const void *a, const void *b) {
+  const keyed *x = (const keyed *)a, *y = (const keyed *)b;
+  if (x->key != y->key)
+    return x->key > y->key ? -1 : 1;
+  return x->id < y->id ? -1 : (x->id > y->id);
+}
+static int by_id(const void *a, const void *b) {
+  const keyed *x = (const keyed *)a, *y = (const keyed *)b;
+  return x->id < y->id ? -1 : (x->id > y->id);
+}
+
+static float row_value(const jfo_row_input *in, uint32_t t) {
+  if (in->logits)
+    return in->logits[t];
+  return u2f((uint32_t)in->logits_bf16[t] << 16);
+}
+
+/* TargetRow::admits (sampling.metal:33-37). */
+static int admits(const jfo_policy *p, const jfo_row_input *in, uint32_t t,
+                  uint32_t stop0, uint32_t stop1) {
+  if ((p->flags & JFO_ROW_CONSTRAINED) &&
+      !(in->mask[t / 32] & (1u << (t % 32))))
+    return 0;
+  return !(p->flags & JFO_ROW_EXCLUDE_STOP) || (t != stop0 && t != stop1);
+}
+
+/* The row's logit of token t after its penalties (sampling.metal:941-963;
+ * Sampling.cpp:88-132): only rows whose policy has active penalties. */
+static float penalized(const jfo_policy *p, float inv_rep,
+                       const jfo_row_input *in, uint32_t t) {
+  float v = row_value(in, t);
+  if (!penalties_active(p))
+    return v;
+  const uint32_t word = in->words ? in->words[t] : 0u;
+  uint32_t count = word & JFO_PENALTY_COUNT_MASK;
+  for (uint32_t i = 0; i < in->extra_count; ++i)
+    count += in->extra[i] == t;
+  if (!count && !(word & JFO_PENALTY_PROMPT_BIT))
+    return v;
+  return jfo_penalize_logit(v, count, p->repetition, inv_rep, p->presence,
+                            p->frequency);
+}
+
+/* The draft's probability of token t: dense q, or the first of the sparse
+ * candidates that lists t (sampling.metal:703-708, 1361-1369). */
+static float draft_q(const jfo_row_input *in, uint32_t t) {
+  if (in->dense_q)
+    return in->dense_q[t];
+  if (!in->cand_ids)
+    return 0.0f;
+  for (uint32_t j = 0; j < JFO_DRAFT_CANDIDATES; ++j)
+    if (in->cand_ids[j] == t)
+      return in->cand_probs[j];
+  return 0.0f;
+}
+
+static uint64_t quantize(float w) {
+  return (uint64_t)(w * 0x1p44f);
+}
+
+int jfo_select_row(uint32_t V, uint32_t stop0, uint32_t stop1,
+                   const jfo_policy *p, const jfo_row_input *in,
+                   jfo_row_output *out, uint32_t *kept_ids, float *kept_probs,
+                   uint32_t kept_capacity) {
+  const float inv_rep = jfo_repetition_inverse(p->repetition);
+  out->token = JFO_NO_TOKEN;
+  out->draft_probability = 0.0f;
+  out->kept_count = 0;
+  out->maximum = -FLT_MAX;
+
+  /* Greedy (sampling.metal:1427-1512): admitted argmax, largest value then
+   * lowest id; NaN never wins; a -inf row gives its lowest admitted id. */
+  if (!(p->temperature > 0.0f)) {
+    float best = -INFINITY;
+    uint32_t best_id = JFO_NO_TOKEN;
+    for (uint32_t t = 0; t < V; ++t) {
+      if (!admits(p, in, t, stop0, stop1))
+        continue;
+      const float v = penalized(p, inv_rep, in, t);
+      if (v > best || (v == best && t < best_id)) {
+        best = v;
+        best_id = t;
+      }
+    }
+    out->token = best_id;
+    out->maximum = best;
+    return 0;
+  }
+
+  /* Sampled. The admitted non-NaN tokens, their maximum M
+   * (sampling.metal:95-127 keeps -inf out of M). */
+  keyed *list = (keyed *)malloc(sizeof(keyed) * (V ? V : 1));
+  if (!list)
+    return -3;
+  uint32_t n = 0;
+  float M = -FLT_MAX;
+  for (uint32_t t = 0; t < V; ++t) {
+    if (!admits(p, in, t, stop0, stop1))
+      continue;
+    const float v = penalized(p, inv_rep, in, t);
+    if (isnan(v))
+      continue;
+    if (v > M)
+      M = v;
+    list[n].key = jfo_logit_key(v);
+    list[n].id = t;
+    ++n;
+  }
+  out->maximum = M;
+  if (n == 0 || M == INFINITY) {
+    free(list);
+    return 0;
+  }
+  qsort(list, n, sizeof(keyed), by_order);
+  const float inv_t = 1.0f / p->temperature;
+
+  /* min-p (sampling.metal:593-607): keys at or above that of
+   * min(M + T log(min_p), M). */
+  uint32_t n1 = n;
+  if (p->min_p > 0.0f) {
+    const float offset = p->temperature * logf(p->min_p);
+    const float floor_value = fminf(M + offset, M);
+    const uint32_t floor_key = jfo_logit_key(floor_value);
+    n1 = 0;
+    while (n1 < n && list[n1].key >= floor_key)
+      ++n1;
+  }
+  /* top-k of those, exactly k in order (sampling.metal:608-637). */
+  const uint32_t k_eff = (p->top_k && p->top_k < V) ? p->top_k : V;
+  const uint32_t n2 = k_eff < n1 ? k_eff : n1;
+
+  uint64_t *wq = (uint64_t *)malloc(sizeof(uint64_t) * (n2 ? n2 : 1));
+  float *w = (float *)malloc(sizeof(float) * (n2 ? n2 : 1));
+  if (!wq || !w) {
+    free(list);
+    free(wq);
+    free(w);
+    return -3;
+  }
+  uint64_t mass2 = 0;
+  for (uint32_t i = 0; i < n2; ++i) {
+    const float x = jfo_key_logit(list[i].key);
+    const float d = x - M;
+    w[i] = jfo_expf(d * inv_t);
+    wq[i] = quantize(w[i]);
+    mass2 += wq[i];
+  }
+  /* top-p over the mass of what min-p and top-k keep: walk in order until
+   * the running mass exceeds top_p of it; keep all if it never does
+   * (sampling.metal:615-641). */
+  uint32_t n3 = n2;
+  if (p->top_p < 1.0f) {
+    const uint64_t nucleus = jfo_floor_mul(mass2, p->top_p);
+    uint64_t walked = 0;
+    for (uint32_t i = 0; i < n2; ++i) {
+      walked += wq[i];
+      if (walked > nucleus) {
+        n3 = i + 1;
+        break;
+      }
+    }
+  }
+  /* The kept set in id order (sampling.metal:645-651). */
+  keyed *kept = (keyed *)malloc(sizeof(keyed) * (n3 ? n3 : 1));
+  float *kw = (float *)malloc(sizeof(float) * (n3 ? n3 : 1));
+  uint64_t *kq = (uint64_t *)malloc(sizeof(uint64_t) * (n3 ? n3 : 1));
+  uint64_t *dq = (uint64_t *)malloc(sizeof(uint64_t) * (n3 ? n3 : 1));
+  if (!kept || !kw || !kq || !dq) {
+    free(list); free(wq); free(w); free(kept); free(kw); free(kq); free(dq);
+    return -3;
+  }
+  for (uint32_t i = 0; i < n3; ++i)
+    kept[i] = list[i];
+  qsort(kept, n3, sizeof(keyed), by_id);
+  uint64_t mass3 = 0;
+  for (uint32_t i = 0; i < n3; ++i) {
+    const float x = jfo_key_logit(kept[i].key);
+    kw[i] = jfo_expf((x - M) * inv_t);
+    kq[i] = quantize(kw[i]);
+    mass3 += kq[i];
+  }
+  out->kept_count = n3;
+  const double scale = (double)mass3 * 0x1p-44;
+  if (kept_ids)
+    for (uint32_t i = 0; i < n3 && i < kept_capacity; ++i) {
+      kept_ids[i] = kept[i].id;
+      kept_probs[i] = mass3 ? (float)((double)kw[i] / scale) : 0.0f;
+    }
+  if (mass3 == 0) {
+    free(list); free(wq); free(w); free(kept); free(kw); free(kq); free(dq);
+    return 0;
+  }
+  /* Draw weights: a drafted row's residual max(w - q * mass, 0), or w when
+   * nothing remains of it (sampling.metal:739-765). */
+  const int drafted = in->draft_token != JFO_NO_TOKEN;
+  int residual = 0;
+  for (uint32_t i = 0; i < n3; ++i) {
+    if (drafted) {
+      const uint64_t qm = jfo_floor_mul(mass3, draft_q(in, kept[i].id));
+      dq[i] = kq[i] > qm ? kq[i] - qm : 0;
+      residual |= dq[i] > 0;
+    } else {
+      dq[i] = kq[i];
+    }
+  }
+  if (drafted && !residual)
+    for (uint32_t i = 0; i < n3; ++i)
+      dq[i] = kq[i];
+  uint64_t total = 0;
+  for (uint32_t i = 0; i < n3; ++i)
+    total += dq[i];
+  /* Inverse CDF in id order: the first token whose running weight exceeds
+   * u * total (sampling.metal:766-829). */
+  uint64_t target = jfo_floor_mul(total, in->uniform);
+  if (target >= total)
+    target = total - 1;
+  uint64_t run = 0;
+  for (uint32_t i = 0; i < n3; ++i) {
+    run += dq[i];
+    if (run > target) {
+      out->token = kept[i].id;
+      break;
+    }
+  }
+  /* p(draft) = kept weight / kept mass (sampling.metal:828-829). */
+  if (drafted)
+    for (uint32_t i = 0; i < n3; ++i)
+      if (kept[i].id == in->draft_token)
+        out->draft_probability = (float)((double)kw[i] / scale);
+  free(list); free(wq); free(w); free(kept); free(kw); free(kq); free(dq);
+  return 0;
+}
+
+/* ---- batch over host threads ------------------------------------------ */
+
+typedef struct {
+  uint32_t rows, V, stop0, stop1;
+  const jfo_policy *policies;
+  const void *logits;
+  int is_bf16;
+  uint64_t stride;
+  const uint32_t *mask;
+  uint64_t mask_stride;
+  const uint32_t *words;
+  const uint32_t *pen_row;
+  const float *uniforms;
+  uint32_t *out_tokens;
+  float *out_maximum;
+  uint32_t next;
+  pthread_mutex_t lock;
+  int status;
+} batch_job;
+
+static void *batch_worker(void *arg) {
+  batch_job *job = (batch_job *)arg;
+  for (;;) {
+    pthread_mutex_lock(&job->lock);
+    const uint32_t r = job->next++;
+    pthread_mutex_unlock(&job->lock);
+    if (r >= job->rows)
+      return NULL;
+    jfo_row_input in;
+    memset(&in, 0, sizeof(in));
+    if (job->is_bf16)
+      in.logits_bf16 = (const uint16_t *)job->logits + r * job->stride;
+    else
+      in.logits = (const float *)job->logits + r * job->stride;
+    in.mask = job->mask ? job->mask + r * job->mask_stride : NULL;
+    if (job->words && job->pen_row && job->pen_row[r] != JFO_NO_TOKEN)
+      in.words = job->words + (uint64_t)job->pen_row[r] * job->V;
+    in.uniform = job->uniforms ? job->uniforms[r] : 0.0f;
+    in.draft_token = JFO_NO_TOKEN;
+    jfo_row_output out;
+    const int rc = jfo_select_row(job->V, job->stop0, job->stop1,
+                                  &job->policies[r], &in, &out, NULL, NULL, 0);
+    if (rc)
+      job->status = rc;
+    job->out_tokens[r] = out.token;
+    if (job->out_maximum)
+      job->out_maximum[r] = out.maximum;
+  }
+}
+
+int jfo_select_batch(uint32_t rows, uint32_t V, uint32_t stop0, uint32_t stop1,
+                     const jfo_policy *policies, const void *logits,
+                     int is_bf16, uint64_t stride, const uint32_t *mask,
+                     uint64_t mask_stride, const uint32_t *words,
+                     const uint32_t *pen_row, const float *uniforms,
+                     uint32_t *out_tokens, float *out_maximum,
+                     uint32_t threads) {
+  batch_job job = {rows, V, stop0, stop1, policies, logits, is_bf16, stride,
+                   mask, mask_stride, words, pen_row, uniforms, out_tokens,
+                   out_maximum, 0, PTHREAD_MUTEX_INITIALIZER, 0};
+  if (threads < 1)
+    threads = 1;
+  if (threads > 256)
+    threads = 256;
+  pthread_t tid[256];
+  uint32_t started = 0;
+  for (uint32_t i = 1; i < threads; ++i)
+    if (pthread_create(&tid[started], NULL, batch_worker, &job) == 0)
+      ++started;
+  batch_worker(&job);
+  for (uint32_t i = 0; i < started; ++i)
+    pthread_join(tid[i], NULL);
+  return job.status;
+}
+
+/* ---- acceptance ------------------------------------------------------- */
+
+/* finish_acceptance (sampling.metal:1381-1392). */
+static void finish(const uint32_t *tokens, uint32_t accepted, uint32_t remaining,
+                   uint32_t stop0, uint32_t stop1, uint32_t *retained,
+                   uint32_t *accepted_out) {
+  *accepted_out = accepted;
+  uint32_t kept = accepted + 1 < remaining ? accepted + 1 : remaining;
+  for (uint32_t i = 0; i < kept; ++i)
+    if (tokens[i] == stop0 || tokens[i] == stop1) {
+      kept = i + 1;
+      break;
+    }
+  *retained = kept;
+}
+
+/* decode_accept_dflash (sampling.metal:1399-1423, 1514-1558). Acceptance
+ * uniform of proposal i: slot 8 + i below 7, slot 16 + i - 7 after. */
+void jfo_accept_chain(const jfo_chain_params *p, const uint32_t *draft_tokens,
+                      const uint32_t *cand_ids, const float *cand_probs,
+                      const float *target_draft_prob, const float *u,
+                      uint32_t *target_tokens, uint32_t *retained,
+                      uint32_t *accepted_out) {
+  uint32_t accepted = 0;
+  if (p->sampled) {
+    while (accepted < p->proposals) {
+      const uint32_t token = draft_tokens[accepted];
+      if (token == JFO_NO_TOKEN)
+        break;
+      float q = 0.0f;
+      for (uint32_t j = 0; j < JFO_DRAFT_CANDIDATES; ++j)
+        if (cand_ids[accepted * JFO_DRAFT_CANDIDATES + j] == token) {
+          q = cand_probs[accepted * JFO_DRAFT_CANDIDATES + j];
+          break;
+        }
+      const float pr = target_draft_prob[accepted];
+      const float uu = u[accepted < 7 ? 8 + accepted : 16 + accepted - 7];
+      if (!(uu * q < pr))
+        break;
+      target_tokens[accepted] = token;
+      ++accepted;
+    }
+  } else {
+    while (accepted < p->proposals &&
+           draft_tokens[accepted] == target_tokens[accepted])
+      ++accepted;
+  }
+  finish(target_tokens, accepted, p->remaining, p->stop0, p->stop1, retained,
+         accepted_out);
+}
+
+/* verify_tree_accept (tree.metal:20-84). */
+void jfo_accept_tree(const jfo_tree_params *p, const float *target_draft_prob,
+                     const float *u, uint32_t *tokens, uint32_t *retained,
+                     uint32_t *accepted_out, uint32_t *path_rows) {
+  uint32_t path[JFO_TREE_MAX_DEPTH];
+  uint32_t length = 1, current = 0;
+  path[0] = 0;
+  while (length < JFO_TREE_MAX_DEPTH) {
+    if (p->sampled && current + 1 < p->chain_rows) {
+      const float q = p->chain_q[current];
+      const float pr = target_draft_prob[current];
+      if (u[8 + current] * q < pr) {
+        path[length++] = current + 1;
+        current = current + 1;
+        continue;
+      }
+    }
+    const uint32_t wanted = tokens[current];
+    uint32_t found = 0;
+    for (uint32_t row = current + 1; row < p->rows; ++row)
+      if (p->parent[row] == current && p->token[row] == wanted &&
+          !(p->sampled && row == current + 1 && current + 1 < p->chain_rows)) {
+        found = row;
+        break;
+      }
+    if (!found)
+      break;
+    path[length++] = found;
+    current = found;
+  }
+  uint32_t output[JFO_TREE_MAX_DEPTH];
+  for (uint32_t i = 0; i < length; ++i)
+    output[i] = i + 1 < length ? p->token[path[i + 1]] : tokens[path[i]];
+  for (uint32_t i = 0; i < length; ++i)
+    tokens[i] = output[i];
+  finish(tokens, length - 1, p->remaining, p->stop0, p->stop1, retained,
+         accepted_out);
+  for (uint32_t i = 0; i < JFO_TREE_MAX_DEPTH; ++i)
+    path_rows[i] = i < length ? path[i] : path[length - 1];
+}

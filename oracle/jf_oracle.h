@@ -1,0 +1,149 @@
+/*
+ * jf_oracle — CPU restatement of JustFit's logits->token path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * or the timed CPU baseline. The product (libjf_sampler.so) never links,
+ * loads or calls it.
+ *
+ * Every function restates the reference's semantics with sequential, plainly
+ * ordered code; the file:line citations point into the reference tree
+ * (source/runtime/...). Where the reference's arithmetic is Metal fast-math
+ * whose rounding cannot be reproduced off an Apple GPU, this restatement pins
+ * one definition that the HIP build must meet bit for bit:
+ *   - weights w = jfo_expf((x - M) * inv_t), jfo_expf = Cephes expf (Moshier),
+ *     zero below x = -86;
+ *   - every sum that decides a token (top-p mass, nucleus walk, the draw, the
+ *     residual) runs on w_q = floor(w * 2^44) in exact 64-bit integers, so the
+ *     order of summation cannot change a result;
+ *   - sampled rows never keep a NaN logit.
+ * How each function is pinned (brute force, closed form, known answers,
+ * statistics) is recorded next to it in jf_oracle.c; nothing here is "parity
+ * unpinned".
+ */
+#ifndef JF_ORACLE_H
+#define JF_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JFO_NO_TOKEN 0xffffffffu
+#define JFO_PENALTY_PROMPT_BIT 0x80000000u
+#define JFO_PENALTY_COUNT_MASK 0x7fffffffu
+#define JFO_WEIGHT_BITS 44
+#define JFO_DRAFT_CANDIDATES 16u
+
+#define JFO_ROW_CONSTRAINED 1u
+#define JFO_ROW_EXCLUDE_STOP 2u
+
+uint32_t jfo_logit_key(float value);
+float jfo_key_logit(uint32_t key);
+float jfo_expf(float x);
+uint64_t jfo_floor_mul(uint64_t a, float f);
+uint64_t jfo_splitmix64(uint64_t seed, uint64_t counter);
+float jfo_next_uniform(uint64_t seed, uint64_t *counter);
+void jfo_stage_cycle(uint64_t seed, uint64_t *counter, uint32_t verify_rows,
+                     int tree_cycle, float *uniforms40);
+
+int jfo_rebuild_penalty_words(uint32_t *words, uint32_t vocabulary,
+                              const uint32_t *history, uint64_t history_len,
+                              uint64_t generated, int has_pending,
+                              uint32_t pending, int mark_prompt);
+int jfo_count_penalty_tokens(uint32_t *words, uint32_t vocabulary,
+                             const uint32_t *selected, uint64_t count);
+float jfo_penalize_logit(float value, uint32_t count, float repetition,
+                         float repetition_inverse, float presence,
+                         float frequency);
+float jfo_repetition_inverse(float repetition);
+
+typedef struct {
+  uint32_t top_k;      /* 0 or >= vocabulary: disabled */
+  float temperature;   /* 0: greedy */
+  float top_p;         /* (0, 1] */
+  float min_p;         /* [0, 1] */
+  float repetition;    /* > 0 */
+  float presence;
+  float frequency;
+  uint32_t flags;      /* JFO_ROW_CONSTRAINED | JFO_ROW_EXCLUDE_STOP */
+} jfo_policy;
+
+typedef struct {
+  const float *logits;          /* fp32 row, or NULL when logits_bf16 is set */
+  const uint16_t *logits_bf16;  /* bf16 row (widened exactly) */
+  const uint32_t *mask;         /* ceil(V/32) words when constrained */
+  const uint32_t *words;        /* dense penalty words [V], or NULL */
+  const uint32_t *extra;        /* tokens counted once each on top of words */
+  uint32_t extra_count;
+  float uniform;
+  uint32_t draft_token;         /* JFO_NO_TOKEN: not drafted */
+  const uint32_t *cand_ids;     /* sparse q: JFO_DRAFT_CANDIDATES ids */
+  const float *cand_probs;      /*           and their probabilities */
+  const float *dense_q;         /* dense q [V] (takes precedence) */
+} jfo_row_input;
+
+typedef struct {
+  uint32_t token;
+  float draft_probability;
+  uint32_t kept_count;
+  float maximum;
+} jfo_row_output;
+
+/* Validation of a request's sampling fields (Model.hpp:77-95): 0 if valid. */
+int jfo_policy_valid(const jfo_policy *policy);
+
+/* One selected row: greedy argmax or the sampled draw. kept_ids/kept_probs
+ * (optional, capacity kept_capacity) receive the kept set in id order. */
+int jfo_select_row(uint32_t vocabulary, uint32_t stop0, uint32_t stop1,
+                   const jfo_policy *policy, const jfo_row_input *in,
+                   jfo_row_output *out, uint32_t *kept_ids, float *kept_probs,
+                   uint32_t kept_capacity);
+
+/* Rows of one batch over `threads` host threads (the CPU baseline). Row r
+ * reads logits + r * stride (fp32 or bf16 by is_bf16), mask + r * mask_stride,
+ * words + pen_row[r] * V when pen_row[r] != JFO_NO_TOKEN, uniforms[r]. */
+int jfo_select_batch(uint32_t rows, uint32_t vocabulary, uint32_t stop0,
+                     uint32_t stop1, const jfo_policy *policies,
+                     const void *logits, int is_bf16, uint64_t stride,
+                     const uint32_t *mask, uint64_t mask_stride,
+                     const uint32_t *words, const uint32_t *pen_row,
+                     const float *uniforms, uint32_t *out_tokens,
+                     float *out_maximum, uint32_t threads);
+
+/* Chain acceptance of one lane (sampling.metal:1381-1423, 1514-1558). */
+typedef struct {
+  uint32_t proposals;        /* verify rows - 1 */
+  uint32_t remaining;        /* maximum retained, 1..verify rows */
+  uint32_t stop0, stop1;
+  int sampled;
+} jfo_chain_params;
+void jfo_accept_chain(const jfo_chain_params *p, const uint32_t *draft_tokens,
+                      const uint32_t *cand_ids, const float *cand_probs,
+                      const float *target_draft_prob, const float *uniforms40,
+                      uint32_t *target_tokens, uint32_t *retained,
+                      uint32_t *accepted);
+
+/* Tree acceptance of one lane (tree.metal:20-84). */
+#define JFO_TREE_MAX_ROWS 16u
+#define JFO_TREE_MAX_DEPTH 8u
+typedef struct {
+  uint32_t rows;
+  uint32_t chain_rows;
+  uint32_t remaining;
+  uint32_t stop0, stop1;
+  int sampled;
+  uint32_t parent[JFO_TREE_MAX_ROWS];
+  uint32_t token[JFO_TREE_MAX_ROWS];
+  float chain_q[JFO_TREE_MAX_DEPTH];
+} jfo_tree_params;
+void jfo_accept_tree(const jfo_tree_params *p, const float *target_draft_prob,
+                     const float *uniforms40, uint32_t *target_tokens,
+                     uint32_t *retained, uint32_t *accepted,
+                     uint32_t *path_rows);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,243 @@
+"""GPU parity of jf_sample (through the C ABI) against the CPU oracle.
+
+Bar: bit-exact tokens, kept sets, kept probabilities and draft probabilities
+(the oracle restates the same fp32 weight and exact integer sums); greedy ids
+bit-exact. Full-size configs C1-C3 and C5 are compared row by row; edge cases
+cover ties, empty/NaN/inf rows, masks, stop exclusion, vocabularies that do
+not fill a chunk, and the multi-pass stages (top-k disabled with top-p or
+min-p, large k)."""
+import numpy as np
+import pytest
+
+import jf_sampler as J
+from jf_sampler import workloads as WL
+from harness import NO, assert_same, run_gpu, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def both(V, policies, **kw):
+    print(f"case V={V} rows={len(policies)} keys={sorted(kw)}", flush=True)
+    g = run_gpu(V, policies, **kw)
+    r = run_oracle(V, policies, **kw)
+    return g, r
+
+
+def test_c1_greedy_repetition():
+    c = WL.config1()
+    pol = [J.policy(**c["policy"])]
+    g, r = both(c["V"], pol, logits=c["logits"], histories=c["histories"],
+                generated=c["generated"], mark_prompt=[True])
+    assert_same(g, r, check_draft=False)
+
+
+def test_c2_sampled_full():
+    c = WL.config2()
+    B = c["logits"].shape[0]
+    pol = [J.policy(**c["policy"])] * B
+    g, r = both(c["V"], pol, logits=c["logits"], histories=c["histories"],
+                generated=c["generated"], uniforms=c["uniforms"], kept_capacity=64)
+    assert_same(g, r)
+    assert np.all(g["kept_counts"] <= 50) and np.all(g["kept_counts"] >= 1)
+
+
+@pytest.mark.parametrize("sampled", [False, True])
+def test_c3_grammar(sampled):
+    c = WL.config3()
+    B = c["logits_bf16"].shape[0]
+    p = J.policy(temperature=1.0, constrained=True) if sampled else J.policy(constrained=True)
+    g, r = both(c["V"], [p] * B, logits_bf16=c["logits_bf16"], masks=c["masks"],
+                uniforms=c["uniforms"], kept_capacity=4096 if sampled else 0)
+    assert_same(g, r)
+    for row in range(B):  # every selected token is admitted by the mask
+        assert c["allowed"][row, g["tokens"][row]]
+
+
+def test_c5_large_full():
+    c = WL.config5()
+    B = c["logits_bf16"].shape[0]
+    pol = [J.policy(**c["policy"])] * B
+    g, r = both(c["V"], pol, logits_bf16=c["logits_bf16"], histories=c["histories"],
+                generated=c["generated"], mark_prompt=[True] * B,
+                uniforms=c["uniforms"], kept_capacity=1024)
+    assert_same(g, r)
+
+
+def rand_logits(rng, rows, V, scale=2.0, decimals=None):
+    x = rng.normal(0, scale, (rows, V)).astype(np.float32)
+    if decimals is not None:
+        x = np.round(x, decimals).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("V", [100, 4097, 8192, 70001, 151936])
+def test_mixed_batch_shapes(V):
+    rng = np.random.default_rng(V)
+    rows = 12
+    x = rand_logits(rng, rows, V, decimals=1)
+    pols = [J.policy(), J.policy(temperature=0.7, top_k=50, top_p=0.9),
+            J.policy(temperature=1.3, top_k=5), J.policy(temperature=0.5, min_p=0.1),
+            J.policy(temperature=1.0, top_k=20, min_p=0.2, top_p=0.5),
+            J.policy(repetition=1.3), J.policy(temperature=0.9, top_k=1),
+            J.policy(temperature=2.0, top_k=300, top_p=0.99),
+            J.policy(temperature=0.7, top_k=V + 5, min_p=0.5),
+            J.policy(temperature=1.0, top_k=1000), J.policy(temperature=0.3, top_k=64, min_p=1.0),
+            J.policy(temperature=0.7, top_k=50, presence=1.5, frequency=-0.5, repetition=0.8)]
+    hist = [rng.integers(0, V, 300).astype(np.uint32) for _ in range(rows)]
+    u = rng.random(rows).astype(np.float32)
+    g, r = both(V, pols, logits=x, histories=hist, generated=[150] * rows,
+                mark_prompt=[True] * rows, uniforms=u, kept_capacity=1100)
+    assert_same(g, r)
+
+
+def test_ties_and_constant_rows():
+    rng = np.random.default_rng(11)
+    V = 20000
+    x = np.zeros((6, V), np.float32)
+    x[1] = 1.0
+    x[2, ::7] = 3.0
+    x[3] = np.round(rng.normal(0, 0.5, V), 0)
+    x[4] = -0.0
+    x[4, ::2] = 0.0
+    x[5] = rand_logits(rng, 1, V, decimals=0)[0]
+    pols = [J.policy(temperature=1.0, top_k=50), J.policy(temperature=0.5, top_k=300, top_p=0.3),
+            J.policy(temperature=1.0, top_k=1000), J.policy(temperature=0.8, top_k=7, top_p=0.9),
+            J.policy(temperature=1.0, top_k=33), J.policy()]
+    u = np.array([0.1, 0.5, 0.99, 0.0, 0.7, 0.3], np.float32)
+    g, r = both(V, pols, logits=x, uniforms=u, kept_capacity=1024)
+    assert_same(g, r)
+
+
+def test_masks_stops_and_sentinels():
+    rng = np.random.default_rng(12)
+    V = 50000
+    rows = 8
+    x = rand_logits(rng, rows, V)
+    allowed = rng.random((rows, V)) < 0.05
+    allowed[0] = False                       # nothing admitted
+    x[1] = np.nan                            # NaN row
+    x[2] = -np.inf                           # -inf row
+    x[3, 123] = np.inf                       # +inf in a sampled row
+    x[4, ::3] = np.nan                       # partial NaN
+    allowed[5] = False
+    allowed[5, [7, 8]] = True                # only the stop tokens
+    masks = WL.mask_words(allowed)
+    stop = (7, 8)
+    pols = [J.policy(constrained=True), J.policy(temperature=1.0), J.policy(temperature=1.0),
+            J.policy(temperature=1.0), J.policy(temperature=0.9, top_k=40, constrained=True),
+            J.policy(temperature=1.0, constrained=True, exclude_stop=True),
+            J.policy(constrained=True, exclude_stop=True), J.policy()]
+    x[7] = -np.inf
+    x[7, 999] = 5.0
+    u = rng.random(rows).astype(np.float32)
+    g, r = both(V, pols, logits=x, masks=masks, uniforms=u, stop=stop, kept_capacity=2500)
+    assert_same(g, r)
+    assert g["tokens"][0] == NO and g["tokens"][1] == NO and g["tokens"][2] == NO
+    assert g["tokens"][3] == NO and g["tokens"][5] == NO
+    assert g["tokens"][7] == 999
+
+
+def test_extra_verify_tokens_and_sparse_draft():
+    """Verify rows: each row r counts the draft tokens 1..r (penalize_verify)
+    and drafted rows draw the residual against 16 sparse candidates."""
+    rng = np.random.default_rng(13)
+    V = 30000
+    rows = 8
+    x = rand_logits(rng, rows, V)
+    inputs = rng.integers(0, V, rows + 1).astype(np.uint32)
+    inputs[3] = inputs[5]  # a repeated draft token
+    hist = [rng.integers(0, V, 200).astype(np.uint32)] * rows
+    extra = [inputs[1:r + 1] for r in range(rows)]
+    cand = rng.integers(0, V, (rows, 16)).astype(np.uint32)
+    cand[:, 0] = inputs[1:rows + 1]
+    cand[2, 5] = cand[2, 0]  # duplicate candidate: first entry counts
+    cp = rng.dirichlet(np.ones(16), rows).astype(np.float32)
+    p = J.policy(temperature=0.9, top_k=40, top_p=0.95, repetition=1.2, presence=0.4, frequency=0.2)
+    u = rng.random(rows).astype(np.float32)
+    # make drafts likely kept: boost them
+    for r in range(rows):
+        x[r, inputs[r + 1]] += 6.0
+    g, r = both(V, [p] * rows, logits=x, histories=hist, generated=[100] * rows,
+                mark_prompt=[True] * rows, extra=extra, uniforms=u,
+                draft_tokens=inputs[1:], drafted_rows=rows - 1,
+                cand_ids=cand, cand_probs=cp, kept_capacity=64)
+    assert_same(g, r)
+    assert np.any(g["draft_probs"][:rows - 1] > 0)
+
+
+@pytest.mark.parametrize("kind", ["unfiltered", "topp", "minp", "bigk", "all"])
+def test_multipass_stages(kind):
+    rng = np.random.default_rng(14)
+    V = 151936 if kind in ("unfiltered", "topp") else 60000
+    rows = 4
+    x = rand_logits(rng, rows, V, scale=1.0)
+    pol = {"unfiltered": J.policy(temperature=1.0),
+           "topp": J.policy(temperature=0.8, top_p=0.9),
+           "minp": J.policy(temperature=1.0, min_p=0.02),
+           "bigk": J.policy(temperature=1.5, top_k=5000),
+           "all": J.policy(temperature=0.9, top_k=3000, top_p=0.7, min_p=0.01)}[kind]
+    u = rng.random(rows).astype(np.float32)
+    g, r = both(V, [pol] * rows, logits=x, uniforms=u, kept_capacity=V)
+    assert_same(g, r)
+
+
+def test_dense_residual_multipass():
+    rng = np.random.default_rng(15)
+    V = 40000
+    rows = 4
+    x = rand_logits(rng, rows, V)
+    q = rng.dirichlet(np.ones(V) * 0.3, rows).astype(np.float32)
+    d = np.array([int(np.argmax(x[r])) for r in range(rows)], np.uint32)
+    d[3] = 17
+    u = rng.random(rows).astype(np.float32)
+    g, r = both(V, [J.policy(temperature=1.0)] * rows, logits=x, uniforms=u,
+                draft_tokens=d, dense_q=q, kept_capacity=0)
+    assert_same(g, r)
+
+
+def test_determinism_repeat():
+    c = WL.config2(B=16)
+    pol = [J.policy(**c["policy"])] * 16
+    kw = dict(logits=c["logits"], histories=c["histories"], generated=c["generated"],
+              uniforms=c["uniforms"][:16], kept_capacity=64)
+    a = run_gpu(c["V"], pol, **kw)
+    b = run_gpu(c["V"], pol, repeat=3, **kw)
+    for k in a:
+        np.testing.assert_array_equal(a[k], b[k])
+
+
+def test_chi_square_of_one_million_draws():
+    """1e6 draws of one row (rows share the logits, uniforms differ) against
+    the kept distribution."""
+    import torch
+    from scipy import stats
+    V = 256
+    rows = 1 << 17
+    calls = 8
+    rng = np.random.default_rng(16)
+    base = rng.normal(0, 1.5, V).astype(np.float32)
+    pol = J.policy(temperature=0.8, top_k=40, top_p=0.9)
+    dev = torch.device("cuda", 0)
+    lg = torch.from_numpy(np.tile(base, (rows, 1))).to(dev)
+    out = torch.zeros(rows, dtype=torch.int32, device=dev)
+    s = J.Sampler(V, rows)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(16)
+    toks = []
+    for _ in range(calls):
+        u = torch.rand(rows, device=dev, generator=gen)
+        s.sample(lg, [pol] * rows, out, uniforms=u)
+        toks.append(out.cpu().numpy().copy())
+    toks = np.concatenate(toks)
+    rows = rows * calls
+    ref = run_oracle(V, [pol], logits=base[None], uniforms=np.zeros(1, np.float32),
+                     kept_capacity=V)
+    ids = ref["kept_ids"][0, :ref["kept_counts"][0]]
+    probs = ref["kept_probs"][0, :ref["kept_counts"][0]].astype(np.float64)
+    assert set(np.unique(toks)) <= set(ids.tolist())
+    counts = np.array([(toks == t).sum() for t in ids])
+    expected = probs / probs.sum() * rows
+    keep = expected >= 5
+    chi2 = ((counts[keep] - expected[keep]) ** 2 / expected[keep]).sum()
+    pval = stats.chi2.sf(chi2, keep.sum() - 1)
+    assert pval > 1e-4, (chi2, pval)
