@@ -95,6 +95,33 @@ __device__ __forceinline__ float bf16_to_float(uint32_t bits16) {
   return u2f(bits16 << 16);
 }
 
+// ---- cross-block scratch -------------------------------------------------
+// Blocks of one row exchange partial results through device memory. The
+// writers store with device-coherent (L2 write-through) stores and wait for
+// them to complete before they count their arrival; the reader loads with
+// device-coherent (L2-bypassing) loads. No cache writeback or invalidate of
+// the whole L2 is needed, which a device-scope fence would issue per block.
+__device__ __forceinline__ void st_dev(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(uint64_t *p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(float *p, float v) {
+  st_dev((uint32_t *)p, __float_as_uint(v));
+}
+__device__ __forceinline__ uint32_t ld_dev(const uint32_t *p) {
+  return __hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev(const uint64_t *p) {
+  return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p) {
+  return __uint_as_float(ld_dev((const uint32_t *)p));
+}
+// Waits until every memory access this thread issued has completed.
+__device__ __forceinline__ void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
 // ---- wave64 primitives ------------------------------------------------
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }

@@ -44,7 +44,8 @@ struct BlockHeader {
   uint32_t overflow;   // sampled: candidates did not fit
   float best_value;    // greedy
   uint32_t best_id;    // greedy
-  uint32_t reserved[2];
+  uint32_t floor_key;  // sampled: the row's K-th key is at least this
+  uint32_t reserved;
 };
 static_assert(sizeof(BlockHeader) == 32, "block headers are 32 bytes");
 
@@ -86,7 +87,7 @@ constexpr int kMergeCapacity = 2048;
 constexpr int kPenaltyWordsLds = 2048;
 constexpr int kMaxExtra = 16;
 constexpr uint32_t kChunkF32 = 8192;
-constexpr uint32_t kChunkBF16 = 16384;
+constexpr uint32_t kChunkBF16 = 8192;
 
 struct SampleLaunch {
   const void *logits;
@@ -118,7 +119,7 @@ struct SampleLaunch {
   const float *dense_q;
   uint64_t q_stride;
   BlockHeader *headers;
-  uint2 *cands;
+  uint64_t *cands;       // key | id << 32
   uint32_t *counters;
   RowState *states;
   StagePartial *partials;

@@ -29,11 +29,12 @@ struct Geo<0> {  // fp32: 4 tokens per 16-byte load
 };
 template <>
 struct Geo<1> {  // bf16: 8 tokens per 16-byte load
-  static constexpr int VEC = 8, LOADS = 8, TPL = 64, SEG = 4096;
+  static constexpr int VEC = 8, LOADS = 4, TPL = 32, SEG = 2048;
   static constexpr uint32_t CHUNK = kChunkBF16;
 };
 
-constexpr uint32_t kMaxChunkWords = kChunkBF16 / 32;
+constexpr uint32_t kMaxChunkWords = kChunkF32 / 32;
+constexpr uint32_t kLowestKey = 0x007fffffu;  // the key of -infinity
 constexpr uint32_t kMaxChunks = 64;
 
 struct PrepLds {
@@ -47,6 +48,7 @@ struct MergeLds {
   uint32_t key[kMergeCapacity];
   uint32_t id[kMergeCapacity];
   uint8_t fl[kMergeCapacity];
+  uint32_t bins[1024];
 };
 
 struct __align__(16) Lds {
@@ -62,6 +64,8 @@ struct __align__(16) Lds {
   float hmax[kMaxChunks];
   uint32_t hcnt[kMaxChunks];
   uint32_t hoff[kMaxChunks + 1];
+  uint32_t cids[16];
+  float cprobs[16];
   uint32_t last;
   uint32_t sel_bin;
   uint64_t sel_excl;
@@ -72,37 +76,51 @@ struct __align__(16) Lds {
   uint64_t u64a;
 };
 
+// The select kernel's LDS: the chunk's penalty lookup and the reductions.
+struct __align__(16) SelectLds {
+  PrepLds prep;
+  uint64_t wl[kWaves];
+  float wf[kWaves];
+  uint32_t wu[kWaves];
+  uint32_t wu2[kWaves];
+};
+
 // ---- block helpers (every thread of the block calls them) ---------------
 
-__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, Lds &s) {
+template <class L>
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, L &s) {
   v = wave_sum_u32(v);
   __syncthreads();
   if (lane_id() == 0) s.wu[threadIdx.x >> 6] = v;
   __syncthreads();
   return s.wu[0] + s.wu[1] + s.wu[2] + s.wu[3];
 }
-__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, Lds &s) {
+template <class L>
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, L &s) {
   v = wave_sum_u64(v);
   __syncthreads();
   if (lane_id() == 0) s.wl[threadIdx.x >> 6] = v;
   __syncthreads();
   return s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3];
 }
-__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, Lds &s) {
+template <class L>
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, L &s) {
   v = wave_max_u32(v);
   __syncthreads();
   if (lane_id() == 0) s.wu[threadIdx.x >> 6] = v;
   __syncthreads();
   return max(max(s.wu[0], s.wu[1]), max(s.wu[2], s.wu[3]));
 }
-__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, Lds &s) {
+template <class L>
+__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, L &s) {
   v = wave_min_u32(v);
   __syncthreads();
   if (lane_id() == 0) s.wu[threadIdx.x >> 6] = v;
   __syncthreads();
   return min(min(s.wu[0], s.wu[1]), min(s.wu[2], s.wu[3]));
 }
-__device__ __forceinline__ float block_max_f32(float v, Lds &s) {
+template <class L>
+__device__ __forceinline__ float block_max_f32(float v, L &s) {
   v = wave_max_f32(v);
   __syncthreads();
   if (lane_id() == 0) s.wf[threadIdx.x >> 6] = v;
@@ -111,7 +129,8 @@ __device__ __forceinline__ float block_max_f32(float v, Lds &s) {
                          __builtin_fmaxf(s.wf[2], s.wf[3]));
 }
 // Exclusive prefix over threads in thread order; *total gets the block sum.
-__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, Lds &s,
+template <class L>
+__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, L &s,
                                                         uint64_t *total) {
   const uint64_t incl = wave_incl_scan_u64(v);
   const uint32_t w = threadIdx.x >> 6;
@@ -178,17 +197,31 @@ __device__ __forceinline__ bool at_or_before(uint32_t key, uint32_t token,
 
 // ---- one chunk of one row into registers ---------------------------------
 
+constexpr float kNotAdmitted = __builtin_nanf("");
+
+// Makes the compiler treat the chunk's registers as rewritten here, so it
+// does not hoist per-token work out of the loop that follows (which would
+// hold a second copy of the chunk in registers).
+template <int N>
+__device__ __forceinline__ void opaque(float (&xs)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(xs[i]));
+}
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 // Loads chunk `chunk` of `row`: xs[j*VEC+e] is token
-// chunk*CHUNK + w*SEG + j*64*VEC + lane*VEC + e (w = wave, lane = lane id),
-// penalized; bit j*VEC+e of the result is set when the row admits the token
-// (in the vocabulary, in the mask of a constrained row, not an excluded stop
-// token). Block-uniform control flow: every thread calls it.
-template <int DT>
-__device__ __forceinline__ uint64_t load_chunk(const SampleLaunch &a,
-                                               const RowParams &rp,
-                                               uint32_t row, uint32_t chunk,
-                                               Lds &s,
-                                               float (&xs)[Geo<DT>::TPL]) {
+// chunk*CHUNK + w*SEG + j*64*VEC + lane*VEC + e (w = wave, lane = lane id)
+// after its penalties, or NaN when the row does not admit it (outside the
+// vocabulary, outside a constrained row's mask, an excluded stop token). A
+// NaN logit is never selected either (greedy comparisons skip it, sampled
+// rows keep no NaN), so one NaN test covers both. Block-uniform control
+// flow: every thread calls it.
+template <int DT, class L>
+__device__ __forceinline__ void load_chunk(const SampleLaunch &a,
+                                           const RowParams &rp, uint32_t row,
+                                           uint32_t chunk, L &s,
+                                           float (&xs)[Geo<DT>::TPL]) {
   constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
                 SEG = Geo<DT>::SEG;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
@@ -198,13 +231,42 @@ __device__ __forceinline__ uint64_t load_chunk(const SampleLaunch &a,
   const uint32_t base = chunk * CHUNK;
   const uint32_t lane_base = base + w * SEG + lane * VEC;
 
+  // Penalty entries of this chunk are loaded before the logits: vector
+  // loads complete in issue order, so the bitmap below can be built while
+  // the logits are still in flight.
+  const bool penalized = (rp.flags & kRowPenalized) != 0;
+  constexpr uint32_t NWORDS = CHUNK / 32;
+  constexpr int EPT = 4;  // entries per thread held in registers
+  uint32_t lo = 0, hi = 0;
+  const uint2 *ent = nullptr;
+  uint2 pe[EPT];
+  if (penalized) {
+    PrepLds &p = s.prep;
+    for (uint32_t i = tid; i < NWORDS; i += kThreads) {
+      p.pbits[i] = 0;
+      p.xbits[i] = 0;
+    }
+    const uint32_t prow = rp.penalty_row;
+    const uint32_t *offs = a.pen_offsets + (uint64_t)prow * (a.pen_buckets + 1);
+    const uint32_t b0 = base / kPenaltyBucket;
+    const uint32_t b1 = min((base + CHUNK) / kPenaltyBucket, a.pen_buckets);
+    lo = __builtin_amdgcn_readfirstlane(offs[b0]);
+    hi = __builtin_amdgcn_readfirstlane(offs[b1]);
+    ent = a.pen_entries + (uint64_t)prow * a.pen_max_entries;
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const uint32_t i = lo + tid + k * kThreads;
+      pe[k] = i < hi ? ent[i] : make_uint2(kNoToken, 0u);
+    }
+  }
+
   if constexpr (DT == 0) {
     const float *rowp = (const float *)a.logits + (uint64_t)row * a.stride;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const uint32_t t0 = lane_base + j * 64 * VEC;
       if (t0 + VEC <= V && a.aligned) {
-        const float4 v = *(const float4 *)(rowp + t0);
+        const f32x4 v = __builtin_nontemporal_load((const f32x4 *)(rowp + t0));
         xs[j * 4 + 0] = v.x;
         xs[j * 4 + 1] = v.y;
         xs[j * 4 + 2] = v.z;
@@ -212,7 +274,7 @@ __device__ __forceinline__ uint64_t load_chunk(const SampleLaunch &a,
       } else {
 #pragma unroll
         for (int e = 0; e < VEC; ++e)
-          xs[j * VEC + e] = (t0 + e < V) ? rowp[t0 + e] : 0.0f;
+          xs[j * VEC + e] = (t0 + e < V) ? rowp[t0 + e] : kNotAdmitted;
       }
     }
   } else {
@@ -222,74 +284,41 @@ __device__ __forceinline__ uint64_t load_chunk(const SampleLaunch &a,
     for (int j = 0; j < LOADS; ++j) {
       const uint32_t t0 = lane_base + j * 64 * VEC;
       if (t0 + VEC <= V && a.aligned) {
-        const uint4 v = *(const uint4 *)(rowp + t0);
-        const uint32_t p[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          xs[j * 8 + 2 * q] = u2f(p[q] << 16);
-          xs[j * 8 + 2 * q + 1] = u2f(p[q] & 0xffff0000u);
-        }
+        const u32x4 v = __builtin_nontemporal_load((const u32x4 *)(rowp + t0));
+        xs[j * 8 + 0] = u2f(v.x << 16);
+        xs[j * 8 + 1] = u2f(v.x & 0xffff0000u);
+        xs[j * 8 + 2] = u2f(v.y << 16);
+        xs[j * 8 + 3] = u2f(v.y & 0xffff0000u);
+        xs[j * 8 + 4] = u2f(v.z << 16);
+        xs[j * 8 + 5] = u2f(v.z & 0xffff0000u);
+        xs[j * 8 + 6] = u2f(v.w << 16);
+        xs[j * 8 + 7] = u2f(v.w & 0xffff0000u);
       } else {
 #pragma unroll
         for (int e = 0; e < VEC; ++e)
           xs[j * VEC + e] =
-              (t0 + e < V) ? bf16_to_float(rowp[t0 + e]) : 0.0f;
+              (t0 + e < V) ? bf16_to_float(rowp[t0 + e]) : kNotAdmitted;
       }
     }
   }
 
-  uint64_t adm = 0;
-  const bool constrained = (rp.flags & kRowConstrained) != 0;
-  const uint32_t *mrow = a.masks + (uint64_t)row * a.mask_stride;
-#pragma unroll
-  for (int j = 0; j < LOADS; ++j) {
-    const uint32_t t0 = lane_base + j * 64 * VEC;
-    uint32_t vm = 0;
-    if (t0 + VEC <= V)
-      vm = VMASK;
-    else if (t0 < V)
-      vm = (1u << (V - t0)) - 1u;
-    if (constrained && vm) vm &= (mrow[t0 >> 5] >> (t0 & 31)) & VMASK;
-    adm |= (uint64_t)vm << (j * VEC);
-  }
-  if (rp.flags & kRowExcludeStop) {
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const uint32_t st = k ? a.stop1 : a.stop0;
-      if (st >= base && st < base + CHUNK) {
-        const uint32_t o = st - base;
-        const uint32_t sw = o / SEG, sj = (o % SEG) / (64 * VEC),
-                       sl = (o % (64 * VEC)) / VEC, se = o % VEC;
-        if (sw == w && sl == lane) adm &= ~(1ull << (sj * VEC + se));
-      }
-    }
-  }
-
-  if (rp.flags & kRowPenalized) {
-    constexpr uint32_t NWORDS = CHUNK / 32;
+  if (penalized) {
     PrepLds &p = s.prep;
-    for (uint32_t i = tid; i < NWORDS; i += kThreads) {
-      p.pbits[i] = 0;
-      p.xbits[i] = 0;
-    }
-    __syncthreads();
-    const uint32_t prow = rp.penalty_row;
-    uint32_t lo = 0, hi = 0;
-    const uint2 *ent = nullptr;
-    if (prow != kNoToken) {
-      const uint32_t *offs =
-          a.pen_offsets + (uint64_t)prow * (a.pen_buckets + 1);
-      const uint32_t b0 = base / kPenaltyBucket;
-      const uint32_t b1 = min((base + CHUNK) / kPenaltyBucket, a.pen_buckets);
-      lo = offs[b0];
-      hi = offs[b1];
-      ent = a.pen_entries + (uint64_t)prow * a.pen_max_entries;
-      for (uint32_t i = lo + tid; i < hi; i += kThreads) {
-        const uint2 e = ent[i];
-        const uint32_t o = e.x - base;
+    __syncthreads();  // bitmaps cleared
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const uint32_t i = lo + tid + k * kThreads;
+      if (i < hi) {
+        const uint32_t o = pe[k].x - base;
         atomicOr(&p.pbits[o >> 5], 1u << (o & 31));
-        if (i - lo < (uint32_t)kPenaltyWordsLds) p.pwords[i - lo] = e.y;
+        if (i - lo < (uint32_t)kPenaltyWordsLds) p.pwords[i - lo] = pe[k].y;
       }
+    }
+    for (uint32_t i = lo + tid + EPT * kThreads; i < hi; i += kThreads) {
+      const uint2 e = ent[i];
+      const uint32_t o = e.x - base;
+      atomicOr(&p.pbits[o >> 5], 1u << (o & 31));
+      if (i - lo < (uint32_t)kPenaltyWordsLds) p.pwords[i - lo] = e.y;
     }
     const uint32_t nx = rp.extra_count;
     if (tid < nx) {
@@ -350,18 +379,50 @@ __device__ __forceinline__ uint64_t load_chunk(const SampleLaunch &a,
     }
     __syncthreads();  // the prep area is reused by the caller
   }
-  return adm;
+
+  // Admission: the constraint mask and the stop tokens.
+  const bool constrained = (rp.flags & kRowConstrained) != 0;
+  uint32_t stop_j[2] = {0xffu, 0xffu}, stop_e[2] = {0, 0};
+  if (rp.flags & kRowExcludeStop) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t st = k ? a.stop1 : a.stop0;
+      if (st >= base && st < base + CHUNK) {
+        const uint32_t o = st - base;
+        if (o / SEG == w && (o % (64 * VEC)) / VEC == lane) {
+          stop_j[k] = (o % SEG) / (64 * VEC);
+          stop_e[k] = o % VEC;
+        }
+      }
+    }
+  }
+  if (constrained || (rp.flags & kRowExcludeStop)) {
+    const uint32_t *mrow = a.masks + (uint64_t)row * a.mask_stride;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const uint32_t t0 = lane_base + j * 64 * VEC;
+      uint32_t vm = VMASK;
+      if (constrained && t0 < V) vm = (mrow[t0 >> 5] >> (t0 & 31)) & VMASK;
+      if (stop_j[0] == (uint32_t)j) vm &= ~(1u << stop_e[0]);
+      if (stop_j[1] == (uint32_t)j) vm &= ~(1u << stop_e[1]);
+      if (vm != VMASK) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          xs[j * VEC + e] = ((vm >> e) & 1u) ? xs[j * VEC + e] : kNotAdmitted;
+      }
+    }
+  }
 }
 
 // Writes the (key, id) of every token whose bit is set in `pb`, in id order
 // across the block, at dst[start + rank] for ranks below `limit - start`.
 // Returns the number of set bits in the block.
-template <int DT>
+template <int DT, class L>
 __device__ __forceinline__ uint32_t emit_ordered(uint64_t pb,
                                                  const float (&xs)[Geo<DT>::TPL],
-                                                 uint32_t lane_base, uint2 *dst,
+                                                 uint32_t lane_base, uint64_t *dst,
                                                  uint32_t start, uint32_t limit,
-                                                 Lds &s) {
+                                                 L &s) {
   constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS;
   constexpr uint32_t VMASK = (1u << VEC) - 1u;
   const uint32_t w = threadIdx.x >> 6;
@@ -393,8 +454,8 @@ __device__ __forceinline__ uint32_t emit_ordered(uint64_t pb,
     for (int e = 0; e < VEC; ++e) {
       if ((bits >> e) & 1u) {
         if (idx < limit)
-          dst[idx] = make_uint2(logit_key(xs[j * VEC + e]),
-                                lane_base + j * 64 * VEC + e);
+          dst[idx] = (uint64_t)logit_key(xs[j * VEC + e]) |
+                     ((uint64_t)(lane_base + j * 64 * VEC + e) << 32);
         ++idx;
       }
     }
@@ -404,9 +465,9 @@ __device__ __forceinline__ uint32_t emit_ordered(uint64_t pb,
 }
 
 // The first `limit` set bits of `pb` in block id order (w, j, lane, e).
-template <int DT>
+template <int DT, class L>
 __device__ __forceinline__ uint64_t first_in_order(uint64_t pb, uint32_t limit,
-                                                   Lds &s) {
+                                                   L &s) {
   constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS;
   constexpr uint32_t VMASK = (1u << VEC) - 1u;
   const uint32_t w = threadIdx.x >> 6;
@@ -464,15 +525,23 @@ __device__ __forceinline__ uint32_t row_draft(const SampleLaunch &a,
 }
 
 // The draft's probability of `token` for a drafted row: its dense q, or
-// the first sparse candidate that lists it (sampling.metal:703-708).
+// the first sparse candidate that lists it (sampling.metal:703-708); the
+// merge stages the row's 16 candidates in s.cids/s.cprobs.
 __device__ __forceinline__ float draft_q(const SampleLaunch &a, uint32_t row,
-                                         uint32_t token) {
+                                         uint32_t token, const Lds &s) {
   if (a.dense_q) return a.dense_q[(uint64_t)row * a.q_stride + token];
-  const uint32_t *ids = a.cand_ids + (uint64_t)row * 16;
-  const float *pr = a.cand_probs + (uint64_t)row * 16;
   for (int j = 0; j < 16; ++j)
-    if (ids[j] == token) return pr[j];
+    if (s.cids[j] == token) return s.cprobs[j];
   return 0.0f;
+}
+__device__ __forceinline__ void stage_candidates(const SampleLaunch &a,
+                                                 uint32_t row, Lds &s) {
+  if (threadIdx.x < 16) {
+    const bool sparse = !a.dense_q && row_draft(a, row) != kNoToken;
+    s.cids[threadIdx.x] = sparse ? a.cand_ids[(uint64_t)row * 16 + threadIdx.x] : kNoToken;
+    s.cprobs[threadIdx.x] = sparse ? a.cand_probs[(uint64_t)row * 16 + threadIdx.x] : 0.0f;
+  }
+  __syncthreads();
 }
 
 __device__ __forceinline__ uint64_t residual_of(uint64_t wq, uint64_t mass,
@@ -629,7 +698,7 @@ __device__ __forceinline__ void lds_draw(const SampleLaunch &a, uint32_t row, Ld
       if (m.fl[i]) {
         const uint64_t wq =
             quantize(weight_of(key_logit(m.key[i]), maximum, inv_t));
-        const uint64_t d = residual_of(wq, mass3, draft_q(a, row, m.id[i]));
+        const uint64_t d = residual_of(wq, mass3, draft_q(a, row, m.id[i], s));
         dloc += d;
         any |= d > 0;
       }
@@ -651,7 +720,7 @@ __device__ __forceinline__ void lds_draw(const SampleLaunch &a, uint32_t row, Ld
       if (!m.fl[i]) continue;
       const uint64_t wq =
           quantize(weight_of(key_logit(m.key[i]), maximum, inv_t));
-      run += residual ? residual_of(wq, mass3, draft_q(a, row, m.id[i])) : wq;
+      run += residual ? residual_of(wq, mass3, draft_q(a, row, m.id[i], s)) : wq;
       if (run > target) {
         s.hit = m.id[i];
         break;
@@ -667,6 +736,184 @@ __device__ __forceinline__ void lds_draw(const SampleLaunch &a, uint32_t row, Ld
     write_result(a, row, s.hit,
                  drafted ? (float)((double)s.found_w / scale) : 0.0f,
                  (uint32_t)kept_total);
+}
+
+// The merge of at most kThreads compacted items (id order in s.merge):
+// thread t holds item t and its rank in (key desc, id asc) order by counting,
+// which gives top-k, the rank-order walk of top-p and, in thread order, the
+// id-order draw.
+__device__ __forceinline__ void small_merge(const SampleLaunch &a,
+                                            const RowParams &rp, uint32_t row,
+                                            Lds &s, uint32_t n, float maximum) {
+  MergeLds &m = s.merge;
+  const uint32_t t = threadIdx.x;
+  const bool have = t < n;
+  const uint32_t key = have ? m.key[t] : 0u;
+  const uint32_t id = have ? m.id[t] : kNoToken;
+  uint32_t rank = 0;
+  if (have)
+    for (uint32_t j = 0; j < n; ++j) {
+      const uint32_t kj = m.key[j];
+      rank += (kj > key) || (kj == key && j < t);
+    }
+  const uint32_t n2 = min(rp.top_k, n);
+  const float inv_t = rp.inv_t;
+  const float w = have ? weight_of(key_logit(key), maximum, inv_t) : 0.0f;
+  const uint64_t wq = quantize(w);
+  uint32_t n3 = n2;
+  if (rp.flags & kRowTopP) {
+    // Weights in rank order, their running sum, the first rank past the
+    // nucleus.
+    __syncthreads();
+    if (have && rank < n2) s.hist[rank] = wq;
+    __syncthreads();
+    const uint64_t mine = t < n2 ? s.hist[t] : 0;
+    uint64_t mass2;
+    const uint64_t excl = block_excl_scan_u64(mine, s, &mass2);
+    if (t == 0) s.hit = n2;
+    __syncthreads();
+    if (mass2) {
+      const uint64_t nucleus = floor_mul(mass2, rp.top_p);
+      if (t < n2 && excl <= nucleus && excl + mine > nucleus) s.hit = t + 1;
+    }
+    __syncthreads();
+    n3 = s.hit;
+  }
+  const bool kept = have && rank < n3;
+  uint64_t mass3;
+  const uint32_t kept_rank =
+      (uint32_t)block_excl_scan_u64(kept ? 1u : 0u, s, nullptr);
+  (void)block_excl_scan_u64(kept ? wq : 0, s, &mass3);
+  const double scale = (double)mass3 * 0x1p-44;
+  if (a.out_kept_ids && kept && kept_rank < a.kept_cap) {
+    a.out_kept_ids[(uint64_t)row * a.kept_cap + kept_rank] = id;
+    a.out_kept_probs[(uint64_t)row * a.kept_cap + kept_rank] =
+        mass3 ? (float)((double)w / scale) : 0.0f;
+  }
+  if (mass3 == 0) {
+    if (t == 0) write_result(a, row, kNoToken, 0.0f, n3);
+    return;
+  }
+  const uint32_t draft = row_draft(a, row);
+  const bool drafted = draft != kNoToken;
+  uint64_t d = kept ? wq : 0;
+  if (drafted) {
+    const uint64_t r = kept ? residual_of(wq, mass3, draft_q(a, row, id, s)) : 0;
+    if (block_max_u32(r > 0 ? 1u : 0u, s)) d = r;
+  }
+  uint64_t total;
+  const uint64_t excl = block_excl_scan_u64(d, s, &total);
+  uint64_t target = floor_mul(total, row_uniform(a, row));
+  if (target >= total) target = total - 1;
+  if (t == 0) {
+    s.found_w = 0.0f;
+    s.hit = kNoToken;
+  }
+  __syncthreads();
+  if (kept && excl <= target && excl + d > target) s.hit = id;
+  if (drafted && kept && id == draft) s.found_w = w;
+  __syncthreads();
+  if (t == 0)
+    write_result(a, row, s.hit, drafted ? (float)((double)s.found_w / scale) : 0.0f,
+                 n3);
+}
+
+// Keeps the first K of the n compacted items (id order in s.merge) in
+// (key desc, id asc) order, compacted in id order, when K <= kThreads: a
+// 1024-bin histogram of the values between the items' least value and the
+// row maximum finds the bin of the K-th item, whose few items are ranked
+// exactly. Returns false, changing nothing, when the values do not spread
+// over the bins (the caller then takes the radix path).
+__device__ __forceinline__ bool hist_select(Lds &s, uint32_t &n, uint32_t K,
+                                            float maximum) {
+  MergeLds &m = s.merge;
+  constexpr int PER = kMergeCapacity / kThreads;
+  const uint32_t tid = threadIdx.x;
+  uint32_t kmin = 0xffffffffu;
+  for (uint32_t i = tid; i < n; i += kThreads) kmin = min(kmin, m.key[i]);
+  kmin = block_min_u32(kmin, s);
+  const float lo = key_logit(kmin);
+  const float scale = 1023.0f / (maximum - lo);
+  if (!(scale > 0.0f && scale < 3.0e38f) || kmin <= kLowestKey) return false;
+  for (uint32_t b = tid; b < 1024; b += kThreads) m.bins[b] = 0;
+  if (tid == 0) s.u32a = 0;
+  __syncthreads();
+  auto bin_of = [&](uint32_t key) -> uint32_t {
+    const float v = (key_logit(key) - lo) * scale;
+    return min(1023u, (uint32_t)v);
+  };
+  for (uint32_t i = tid; i < n; i += kThreads) atomicAdd(&m.bins[bin_of(m.key[i])], 1u);
+  __syncthreads();
+  // The highest bin whose suffix count reaches K.
+  uint32_t own = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) own += m.bins[4 * tid + k];
+  uint64_t total;
+  const uint32_t before = (uint32_t)block_excl_scan_u64(own, s, &total);
+  const uint32_t suffix = (uint32_t)total - before;  // bins >= 4 tid
+  if (suffix >= K && suffix - own < K) {
+    uint32_t acc = suffix - own;
+    uint32_t b = 4 * tid + 3;
+    for (int k = 3; k >= 0; --k) {
+      b = 4 * tid + k;
+      if (acc + m.bins[b] >= K) break;
+      acc += m.bins[b];
+    }
+    s.sel_bin = b;
+    s.sel_excl = acc;
+  }
+  __syncthreads();
+  const uint32_t bstar = s.sel_bin;
+  const uint32_t need = K - (uint32_t)s.sel_excl;
+  if (m.bins[bstar] > (uint32_t)kThreads) return false;
+  // The items of the boundary bin, ranked exactly.
+  for (uint32_t i = tid; i < n; i += kThreads) {
+    const uint32_t b = bin_of(m.key[i]);
+    m.fl[i] = b > bstar ? 1 : 0;
+    if (b == bstar) {
+      const uint32_t slot = atomicAdd(&s.u32a, 1u);
+      s.hist[slot] = ((uint64_t)m.key[i] << 32) | i;
+    }
+  }
+  __syncthreads();
+  const uint32_t nb = s.u32a;
+  if (tid < nb) {
+    const uint64_t me = s.hist[tid];
+    const uint32_t key = (uint32_t)(me >> 32), pos = (uint32_t)me;
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < nb; ++j) {
+      const uint64_t o = s.hist[j];
+      const uint32_t ok = (uint32_t)(o >> 32), op = (uint32_t)o;
+      rank += ok > key || (ok == key && m.id[op] < m.id[pos]);
+    }
+    if (rank < need) m.fl[pos] = 1;
+  }
+  __syncthreads();
+  // Ordered compaction of the kept items.
+  uint32_t kk[PER], ki[PER];
+  uint32_t cnt = 0;
+  const uint32_t first = tid * PER;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint32_t i = first + k;
+    const bool keep = i < n && m.fl[i];
+    kk[k] = keep ? m.key[i] : 0u;
+    ki[k] = keep ? m.id[i] : kNoToken;
+    cnt += keep;
+  }
+  uint64_t kept;
+  uint32_t out = (uint32_t)block_excl_scan_u64(cnt, s, &kept);
+#pragma unroll
+  for (int k = 0; k < PER; ++k)
+    if (ki[k] != kNoToken) {
+      m.key[out] = kk[k];
+      m.id[out] = ki[k];
+      m.fl[out] = 1;
+      ++out;
+    }
+  n = (uint32_t)kept;
+  __syncthreads();
+  return true;
 }
 
 // Starts the multi-pass stages of a row the merge cannot finish.
@@ -699,18 +946,22 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
   const uint32_t S = a.chunks, tid = threadIdx.x;
   const BlockHeader *hb = a.headers + (uint64_t)row * S;
   float hm = -3.402823466e38f;
-  uint32_t hc = 0, ha = 0, ho = 0;
+  uint32_t hc = 0, ha = 0, ho = 0, hf = 0;
   if (tid < S) {
-    const BlockHeader h = hb[tid];
-    hm = h.maximum;
-    hc = h.count;
-    ha = h.admitted;
-    ho = h.overflow;
+    const BlockHeader *h = hb + tid;
+    hm = ld_dev(&h->maximum);
+    hc = ld_dev(&h->count);
+    ha = ld_dev(&h->admitted);
+    ho = ld_dev(&h->overflow);
+    hf = ld_dev(&h->floor_key);
     s.hcnt[tid] = hc;
   }
+  stage_candidates(a, row, s);
   const float maximum = block_max_f32(hm, s);
   const uint32_t admitted = block_sum_u32(ha, s);
   const uint32_t overflow = block_max_u32(ho, s);
+  // The K-th key of the row is at least every block's floor.
+  const uint32_t floor_key = block_max_u32(hf, s);
   if (tid == 0) {
     uint32_t n = 0;
     for (uint32_t c = 0; c < S; ++c) {
@@ -735,30 +986,56 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
     return;
   }
   if (tid == 0) a.states[row].stage = kStageDone;
-  const uint32_t thr = (rp.flags & kRowMinP)
-                           ? logit_key(__builtin_fminf(maximum + rp.minp_offset,
-                                                       maximum))
-                           : 0u;
+  uint32_t thr = (rp.flags & kRowMinP)
+                     ? logit_key(__builtin_fminf(maximum + rp.minp_offset, maximum))
+                     : 0u;
+  if (rp.flags & kRowTopK) thr = max(thr, floor_key);
   MergeLds &m = s.merge;
   uint32_t n;
   if (fits) {
-    // Every candidate into LDS, in id order.
-    for (uint32_t c = 0; c < S; ++c) {
-      const uint2 *src = a.cands + ((uint64_t)row * S + c) * kBlockCandidates;
-      const uint32_t off = s.hoff[c], cnt = s.hoff[c + 1] - off;
-      for (uint32_t i = tid; i < cnt; i += kThreads) {
-        const uint2 v = src[i];
-        m.key[off + i] = v.x;
-        m.id[off + i] = v.y;
-        m.fl[off + i] = v.x >= thr ? 1 : 0;
+    // Candidates at or above the floor into LDS in id order: every load
+    // issued first, contiguous items per thread, then an ordered compaction.
+    constexpr int PER = kMergeCapacity / kThreads;
+    uint64_t v[PER];
+    const uint32_t first = tid * PER;
+    uint32_t c = 0;
+    for (uint32_t step = kMaxChunks / 2; step; step >>= 1)
+      if (c + step < S && s.hoff[c + step] <= first) c += step;
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const uint32_t i = first + k;
+      v[k] = 0;
+      if (i < n_all) {
+        while (s.hoff[c + 1] <= i) ++c;
+        v[k] = ld_dev(a.cands + ((uint64_t)row * S + c) * kBlockCandidates +
+                      (i - s.hoff[c]));
       }
     }
-    n = n_all;
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      cnt += (first + k < n_all) && (uint32_t)v[k] >= thr;
+    uint64_t total;
+    uint32_t out = (uint32_t)block_excl_scan_u64(cnt, s, &total);
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      if (first + k < n_all && (uint32_t)v[k] >= thr) {
+        m.key[out] = (uint32_t)v[k];
+        m.id[out] = (uint32_t)(v[k] >> 32);
+        m.fl[out] = 1;
+        ++out;
+      }
+    n = (uint32_t)total;
     __syncthreads();
-    uint32_t c1 = 0;
-    for (uint32_t i = tid; i < n; i += kThreads) c1 += m.fl[i];
-    const uint32_t n1 = block_sum_u32(c1, s);
-    if (K < n1) lds_topk(s, n, K);
+    if (n <= (uint32_t)kThreads) {
+      small_merge(a, rp, row, s, n, maximum);
+      return;
+    }
+    if (K <= (uint32_t)kThreads && hist_select(s, n, K, maximum)) {
+      small_merge(a, rp, row, s, n, maximum);
+      return;
+    }
+    if (K < n) lds_topk(s, n, K);
   } else {
     // More candidates than LDS holds and K fits: select the first K at or
     // above the min-p floor straight from the global lists, then keep them.
@@ -766,7 +1043,9 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
     auto item = [&](uint32_t i) -> uint2 {
       uint32_t c = 0;
       while (s.hoff[c + 1] <= i) ++c;
-      return a.cands[((uint64_t)row * S + c) * kBlockCandidates + (i - s.hoff[c])];
+      const uint64_t v =
+          ld_dev(a.cands + ((uint64_t)row * S + c) * kBlockCandidates + (i - s.hoff[c]));
+      return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
     };
     uint32_t c1 = 0;
     for (uint32_t i = tid; i < n_all; i += kThreads) c1 += item(i).x >= thr;
@@ -843,34 +1122,82 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
   lds_draw(a, row, s, n, maximum, rp.inv_t);
 }
 
+// Every thread's device-coherent stores complete, then one arrival; true in
+// every thread of the block that arrives last, which returns the counter to
+// zero for the next launch.
+__device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t S,
+                                            Lds &s) {
+  wait_memory();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    s.last = prev == S - 1;
+    if (s.last) st_dev(counter, 0u);
+  }
+  __syncthreads();
+  return s.last != 0;
+}
+
+template <int DT>
+__device__ __forceinline__ void merge_row(const SampleLaunch &a,
+                                          const RowParams &rp, uint32_t row,
+                                          Lds &s) {
+  const uint32_t S = a.chunks, tid = threadIdx.x;
+  if (!(rp.flags & kRowSampled)) {
+    if (tid < 64) {
+      float bv = -__builtin_inff();
+      uint32_t bi = kNoToken;
+      for (uint32_t c = tid; c < S; c += 64) {
+        const BlockHeader *h = a.headers + (uint64_t)row * S + c;
+        const float hv = ld_dev(&h->best_value);
+        const uint32_t hi = ld_dev(&h->best_id);
+        if (hv > bv || (hv == bv && hi < bi)) {
+          bv = hv;
+          bi = hi;
+        }
+      }
+      wave_argmax(bv, bi);
+      if (tid == 0) {
+        write_result(a, row, bi, 0.0f, 0);
+        a.states[row].stage = kStageDone;
+      }
+    }
+    return;
+  }
+  merge_sampled<DT>(a, rp, row, s);
+}
+
 // ---- the single-pass selection kernel -------------------------------------
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
-  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SEG = Geo<DT>::SEG;
+  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SEG = Geo<DT>::SEG,
+                LOADS = Geo<DT>::LOADS;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
-  __shared__ Lds s;
+  __shared__ SelectLds s;
   const uint32_t S = a.chunks;
   const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
   const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const RowParams rp = a.params[row];
   float xs[TPL];
-  uint64_t adm = load_chunk<DT>(a, rp, row, chunk, s, xs);
+  load_chunk<DT>(a, rp, row, chunk, s, xs);
   const uint32_t lane_base = chunk * CHUNK + w * SEG + lane * VEC;
   BlockHeader *hdr = a.headers + (uint64_t)row * S + chunk;
 
   if (!(rp.flags & kRowSampled)) {
+    // Largest value, lowest id among equals; NaN never wins and a -inf
+    // token wins only over nothing (sampling.metal:1427-1464). A lane's
+    // tokens ascend, so the first of equal values stays.
     float best = -__builtin_inff();
     uint32_t bid = kNoToken;
 #pragma unroll
     for (int i = 0; i < TPL; ++i) {
-      if (!((adm >> i) & 1)) continue;
       const float v = xs[i];
-      const uint32_t t = lane_base + (i / VEC) * 64 * VEC + (i % VEC);
-      if (v > best || (v == best && t < bid)) {
-        best = v;
-        bid = t;
-      }
+      const bool take = v > best || (v == best && bid == kNoToken);
+      best = take ? v : best;
+      bid = take ? lane_base + (i / VEC) * 64 * VEC + (i % VEC) : bid;
     }
     wave_argmax(best, bid);
     if (lane == 0) {
@@ -890,76 +1217,100 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
       hdr->best_id = bi;
     }
   } else {
-    // Admitted non-NaN tokens: their maximum, count and largest key per lane.
-    float mx = -3.402823466e38f;
-    uint32_t cnt = 0, kmax = 0;
+    // Admitted (non-NaN) tokens: the lane's maximum and count.
+    float mx = -__builtin_inff();
+    uint32_t cnt = 0;
 #pragma unroll
     for (int i = 0; i < TPL; ++i) {
-      if (!((adm >> i) & 1)) continue;
-      const float v = xs[i];
-      if (v != v) {
-        adm &= ~(1ull << i);
-        continue;
-      }
-      mx = __builtin_fmaxf(mx, v);
-      kmax = max(kmax, logit_key(v));
-      ++cnt;
+      mx = __builtin_fmaxf(mx, xs[i]);
+      cnt += xs[i] == xs[i];
     }
     // A bound for the block's top-k: each wave's ceil(k/4)-th largest lane
-    // maximum has at least that many tokens at or above it in the wave.
+    // maximum has that many of the wave's tokens at or above it, so the
+    // block has at least k tokens at or above the least of the four.
     const uint32_t K = rp.top_k;
     const uint32_t kw = (K + kWaves - 1) / kWaves;
+    const bool bound = (rp.flags & kRowTopK) && kw <= 64;
     uint32_t wth = 0;
-    if ((rp.flags & kRowTopK) && kw <= 64) wth = wave_kth_largest(kmax, kw);
-    const float bmax = block_max_f32(mx, s);
-    const uint32_t badm = block_sum_u32(cnt, s);
-    const uint32_t tk = (rp.flags & kRowTopK) && kw <= 64 ? block_min_u32(wth, s) : 0u;
+    if (bound) wth = wave_kth_largest(cnt ? logit_key(mx) : 0u, kw);
+    const float wmax = wave_max_f32(mx);
+    const uint32_t wcnt = wave_sum_u32(cnt);
+    if (lane == 0) {
+      s.wf[w] = wmax;
+      s.wu[w] = wcnt;
+      s.wu2[w] = wth;
+    }
+    __syncthreads();
+    const float bmax = __builtin_fmaxf(
+        __builtin_fmaxf(__builtin_fmaxf(s.wf[0], s.wf[1]),
+                        __builtin_fmaxf(s.wf[2], s.wf[3])),
+        -3.402823466e38f);
+    const uint32_t badm = s.wu[0] + s.wu[1] + s.wu[2] + s.wu[3];
+    const uint32_t tk =
+        bound ? min(min(s.wu2[0], s.wu2[1]), min(s.wu2[2], s.wu2[3])) : 0u;
     uint32_t thr = tk;
     if (rp.flags & kRowMinP)
       thr = max(thr, logit_key(__builtin_fminf(bmax + rp.minp_offset, bmax)));
+    // Candidates: one compare per 16-byte vector, bits only where it hits.
+    const float tv = thr <= kLowestKey ? -__builtin_inff() : key_logit(thr);
     uint64_t cb = 0;
 #pragma unroll
-    for (int i = 0; i < TPL; ++i)
-      if (((adm >> i) & 1) && logit_key(xs[i]) >= thr) cb |= 1ull << i;
+    for (int j = 0; j < LOADS; ++j) {
+      float vm = xs[j * VEC];
+#pragma unroll
+      for (int e = 1; e < VEC; ++e) vm = __builtin_fmaxf(vm, xs[j * VEC + e]);
+      if (vm >= tv) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          cb |= (uint64_t)(xs[j * VEC + e] >= tv) << (j * VEC + e);
+      }
+    }
     const uint32_t c = block_sum_u32(__popcll(cb), s);
-    uint2 *dst = a.cands + ((uint64_t)row * S + chunk) * kBlockCandidates;
+    uint64_t *dst = a.cands + ((uint64_t)row * S + chunk) * kBlockCandidates;
     uint32_t emitted = 0, overflow = 0;
     if (c <= (uint32_t)kBlockCandidates) {
       emit_ordered<DT>(cb, xs, lane_base, dst, 0, kBlockCandidates, s);
       emitted = c;
     } else if (K <= (uint32_t)kBlockCandidates) {
-      // Exactly the block's first K candidates in order.
-      uint32_t prefix = 0, pmask = 0;
-      uint64_t need = K;
-      for (int d = 3; d >= 0; --d) {
-        s.hist[tid] = 0;
-        __syncthreads();
+      // Too many candidates: raise the threshold by bisection over keys.
+      // Invariant: at least K tokens at or above lo, fewer than K at or
+      // above hi. It stops early at a key that leaves K..kBlockCandidates
+      // tokens; otherwise it ends on the K-th key itself, and the tokens
+      // tied there are kept by lowest id so that exactly K remain.
+      uint32_t lo_k = thr, hi_k = logit_key(bmax) + 1;
+      uint32_t found = 0;
+      while (hi_k - lo_k > 1) {
+        const uint32_t mid = lo_k + (hi_k - lo_k) / 2;
+        const float mv = mid <= kLowestKey ? -__builtin_inff() : key_logit(mid);
+        opaque(xs);
+        uint32_t cm = 0;
 #pragma unroll
-        for (int i = 0; i < TPL; ++i) {
-          if (!((cb >> i) & 1)) continue;
-          const uint32_t k = logit_key(xs[i]);
-          if ((k & pmask) == prefix)
-            atomicAdd((unsigned long long *)&s.hist[(k >> (8 * d)) & 255u], 1ull);
+        for (int i = 0; i < TPL; ++i) cm += xs[i] >= mv;
+        cm = block_sum_u32(cm, s);
+        if (cm < K) {
+          hi_k = mid;
+        } else if (cm <= (uint32_t)kBlockCandidates) {
+          found = mid;
+          break;
+        } else {
+          lo_k = mid;
         }
-        __syncthreads();
-        crossing_bin(s, need);
-        need -= s.sel_excl;
-        prefix |= s.sel_bin << (8 * d);
-        pmask |= 255u << (8 * d);
-        __syncthreads();
       }
-      uint64_t gt = 0, eq = 0;
+      const uint32_t cut = found ? found : lo_k;
+      const float cv = cut <= kLowestKey ? -__builtin_inff() : key_logit(cut);
+      opaque(xs);
+      uint64_t ge = 0, eq = 0;
 #pragma unroll
       for (int i = 0; i < TPL; ++i) {
-        if (!((cb >> i) & 1)) continue;
-        const uint32_t k = logit_key(xs[i]);
-        if (k > prefix) gt |= 1ull << i;
-        if (k == prefix) eq |= 1ull << i;
+        ge |= (uint64_t)(xs[i] >= cv) << i;
+        eq |= (uint64_t)(xs[i] == cv) << i;
       }
-      // Ties at the K-th key stay by lowest id; the list stays in id order.
-      const uint64_t keep = gt | first_in_order<DT>(eq, (uint32_t)need, s);
-      emit_ordered<DT>(keep, xs, lane_base, dst, 0, kBlockCandidates, s);
-      emitted = K;
+      uint64_t keep = ge;
+      if (!found) {
+        const uint32_t above = block_sum_u32(__popcll(ge & ~eq), s);
+        keep = (ge & ~eq) | first_in_order<DT>(eq, K - above, s);
+      }
+      emitted = emit_ordered<DT>(keep, xs, lane_base, dst, 0, kBlockCandidates, s);
     } else {
       overflow = 1;
     }
@@ -968,40 +1319,20 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
       hdr->count = emitted;
       hdr->admitted = badm;
       hdr->overflow = overflow;
+      hdr->floor_key = tk;
     }
   }
+}
 
-  // The last block of the row to arrive merges (split_reduce.h:14-45).
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    const uint32_t prev = atomicAdd(&a.counters[row], 1u);
-    s.last = prev == S - 1;
-  }
-  __syncthreads();
-  if (!s.last) return;
-  __threadfence();
-  if (tid == 0) a.counters[row] = 0;
-  if (!(rp.flags & kRowSampled)) {
-    if (tid < 64) {
-      float bv = -__builtin_inff();
-      uint32_t bi = kNoToken;
-      for (uint32_t c = tid; c < S; c += 64) {
-        const BlockHeader h = a.headers[(uint64_t)row * S + c];
-        if (h.best_value > bv || (h.best_value == bv && h.best_id < bi)) {
-          bv = h.best_value;
-          bi = h.best_id;
-        }
-      }
-      wave_argmax(bv, bi);
-      if (tid == 0) {
-        write_result(a, row, bi, 0.0f, 0);
-        a.states[row].stage = kStageDone;
-      }
-    }
-    return;
-  }
-  merge_sampled<DT>(a, rp, row, s);
+// One block per row merges the row's chunk summaries (the reduction the
+// reference's last-arriving group does, split_reduce.h:14-45; here the
+// kernel boundary orders the partials before their reader).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void merge_kernel(SampleLaunch a) {
+  __shared__ Lds s;
+  const uint32_t row = blockIdx.x;
+  const RowParams rp = a.params[row];
+  merge_row<DT>(a, rp, row, s);
 }
 
 // ---- multi-pass stages ---------------------------------------------------
@@ -1024,15 +1355,15 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
   if (single && chunk != st.chunk) return;
   const RowParams rp = a.params[row];
   float xs[TPL];
-  uint64_t adm = load_chunk<DT>(a, rp, row, chunk, s, xs);
+  load_chunk<DT>(a, rp, row, chunk, s, xs);
+  stage_candidates(a, row, s);
   const uint32_t lane_base = chunk * CHUNK + w * SEG + lane * VEC;
   const float M = st.maximum, inv_t = rp.inv_t;
-  // Members: admitted non-NaN, at or above the min-p floor, at or before
+  // Members: admitted (non-NaN), at or above the min-p floor, at or before
   // the kept boundary.
   uint64_t mem = 0;
 #pragma unroll
   for (int i = 0; i < TPL; ++i) {
-    if (!((adm >> i) & 1)) continue;
     const float v = xs[i];
     if (v != v) continue;
     const uint32_t k = logit_key(v);
@@ -1085,7 +1416,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
   switch (stage) {
     case kStageCount1: {
       const uint32_t c = block_sum_u32(__popcll(mem), s);
-      if (tid == 0) part->v[0] = c;
+      if (tid == 0) st_dev(&part->v[0], (uint64_t)c);
       break;
     }
     case kStageTopK3: case kStageTopK3 + 1: case kStageTopK3 + 2: case kStageTopK0:
@@ -1104,7 +1435,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
                          (unsigned long long)v);
       }
       __syncthreads();
-      part->v[tid] = s.hist[tid];
+      st_dev(&part->v[tid], s.hist[tid]);
       break;
     }
     case kStageTopKTie:
@@ -1114,7 +1445,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       for (int i = 0; i < TPL; ++i)
         c += ((mem >> i) & 1) && logit_key(xs[i]) == st.tie_key;
       c = block_sum_u32(c, s);
-      if (tid == 0) part->v[0] = c;
+      if (tid == 0) st_dev(&part->v[0], (uint64_t)c);
       break;
     }
     case kStageTopKLocate:
@@ -1147,9 +1478,9 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       sum = block_sum_u64(sum, s);
       c = block_sum_u32(c, s);
       if (tid == 0) {
-        part->v[0] = stage == kStageKeptCount ? c : sum;
-        part->v[1] = s.u32a;
-        part->v[2] = __float_as_uint(s.found_w);
+        st_dev(&part->v[0], stage == kStageKeptCount ? (uint64_t)c : sum);
+        st_dev(&part->v[1], (uint64_t)s.u32a);
+        st_dev(&part->v[2], (uint64_t)__float_as_uint(s.found_w));
       }
       break;
     }
@@ -1162,7 +1493,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
           const uint64_t wq = wq_of(i);
           wsum += wq;
           if (st.drafted) {
-            const uint64_t d = residual_of(wq, st.mass3, draft_q(a, row, tok_of(i)));
+            const uint64_t d = residual_of(wq, st.mass3, draft_q(a, row, tok_of(i), s));
             dsum += d;
             any |= d > 0;
           }
@@ -1171,9 +1502,9 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       wsum = block_sum_u64(wsum, s);
       any = block_max_u32(any, s);
       if (tid == 0) {
-        part->v[0] = dsum;
-        part->v[1] = wsum;
-        part->v[2] = any;
+        st_dev(&part->v[0], dsum);
+        st_dev(&part->v[1], wsum);
+        st_dev(&part->v[2], (uint64_t)any);
       }
       break;
     }
@@ -1250,7 +1581,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       dl[i] = 0;
       if ((mem >> i) & 1) {
         const uint64_t wq = wq_of(i);
-        dl[i] = st.residual ? residual_of(wq, st.mass3, draft_q(a, row, tok_of(i))) : wq;
+        dl[i] = st.residual ? residual_of(wq, st.mass3, draft_q(a, row, tok_of(i), s)) : wq;
       }
     }
     if (tid == 0) s.hit = kNoToken;
@@ -1294,23 +1625,14 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     return;
   }
 
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    const uint32_t prev = atomicAdd(&a.counters[row], 1u);
-    s.last = prev == S - 1;
-  }
-  __syncthreads();
-  if (!s.last) return;
-  __threadfence();
-  if (tid == 0) a.counters[row] = 0;
+  if (!arrive_last(a.counters + row, S, s)) return;
 
   // Finalize the stage for this row.
   const StagePartial *parts = a.partials + (uint64_t)row * S;
   if ((stage >= kStageTopK3 && stage <= kStageTopK0) ||
       (stage >= kStageTopP3 && stage <= kStageTopP0)) {
     uint64_t h = 0;
-    for (uint32_t c = 0; c < S; ++c) h += parts[c].v[tid];
+    for (uint32_t c = 0; c < S; ++c) h += ld_dev(&parts[c].v[tid]);
     s.hist[tid] = h;
     __syncthreads();
     crossing_bin(s, st.remaining);
@@ -1343,7 +1665,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
   switch (stage) {
     case kStageCount1: {
       uint64_t n1 = 0;
-      for (uint32_t c = 0; c < S; ++c) n1 += parts[c].v[0];
+      for (uint32_t c = 0; c < S; ++c) n1 += ld_dev(&parts[c].v[0]);
       ns.n1 = n1;
       if (rp.top_k < n1) {
         ns.stage = kStageTopK3;
@@ -1358,7 +1680,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       uint64_t cum = 0;
       uint32_t c = 0;
       for (; c < S; ++c) {
-        const uint64_t t = parts[c].v[0];
+        const uint64_t t = ld_dev(&parts[c].v[0]);
         if (cum + t >= st.remaining) break;
         cum += t;
       }
@@ -1369,7 +1691,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     }
     case kStageMass2: {
       uint64_t mass = 0;
-      for (uint32_t c = 0; c < S; ++c) mass += parts[c].v[0];
+      for (uint32_t c = 0; c < S; ++c) mass += ld_dev(&parts[c].v[0]);
       ns.mass2 = mass;
       if (mass == 0) {
         ns.stage = kStageMass3;
@@ -1385,8 +1707,8 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     case kStageMass3: {
       uint64_t mass = 0;
       for (uint32_t c = 0; c < S; ++c) {
-        mass += parts[c].v[0];
-        if (parts[c].v[1]) ns.draft_w = __uint_as_float((uint32_t)parts[c].v[2]);
+        mass += ld_dev(&parts[c].v[0]);
+        if (ld_dev(&parts[c].v[1])) ns.draft_w = __uint_as_float((uint32_t)ld_dev(&parts[c].v[2]));
       }
       ns.mass3 = mass;
       if (mass == 0) {
@@ -1399,16 +1721,16 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     }
     case kStageDraw: {
       uint32_t any = 0;
-      for (uint32_t c = 0; c < S; ++c) any |= (uint32_t)parts[c].v[2];
+      for (uint32_t c = 0; c < S; ++c) any |= (uint32_t)ld_dev(&parts[c].v[2]);
       const bool residual = st.drafted && any;
       uint64_t total = 0;
-      for (uint32_t c = 0; c < S; ++c) total += residual ? parts[c].v[0] : parts[c].v[1];
+      for (uint32_t c = 0; c < S; ++c) total += residual ? ld_dev(&parts[c].v[0]) : ld_dev(&parts[c].v[1]);
       uint64_t target = floor_mul(total, row_uniform(a, row));
       if (target >= total) target = total - 1;
       uint64_t cum = 0;
       uint32_t c = 0;
       for (; c < S; ++c) {
-        const uint64_t t = residual ? parts[c].v[0] : parts[c].v[1];
+        const uint64_t t = residual ? ld_dev(&parts[c].v[0]) : ld_dev(&parts[c].v[1]);
         if (cum + t > target) break;
         cum += t;
       }
@@ -1421,7 +1743,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     }
     case kStageKeptCount: {
       uint64_t kept = 0;
-      for (uint32_t c = 0; c < S; ++c) kept += parts[c].v[0];
+      for (uint32_t c = 0; c < S; ++c) kept += ld_dev(&parts[c].v[0]);
       if (a.out_kept_counts) a.out_kept_counts[row] = (uint32_t)kept;
       ns.stage = kStageKeptWrite;
       break;
@@ -1533,11 +1855,14 @@ __global__ void accept_tree_kernel(AcceptTreeLaunch a) {
 // ---- launchers -------------------------------------------------------
 
 int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream) {
-  const dim3 grid(a.rows * a.chunks), block(kThreads);
-  if (dtype == 0)
+  const dim3 grid(a.rows * a.chunks), block(kThreads), mgrid(a.rows);
+  if (dtype == 0) {
     hipLaunchKernelGGL(select_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
-  else
+    hipLaunchKernelGGL(merge_kernel<0>, mgrid, block, 0, (hipStream_t)stream, a);
+  } else {
     hipLaunchKernelGGL(select_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(merge_kernel<1>, mgrid, block, 0, (hipStream_t)stream, a);
+  }
   return (int)hipGetLastError();
 }
 

@@ -130,7 +130,7 @@ struct jf_sampler {
   int device = 0;
   jf::RowParams *params = nullptr;
   jf::BlockHeader *headers = nullptr;
-  uint2 *cands = nullptr;
+  uint64_t *cands = nullptr;
   uint32_t *counters = nullptr;
   jf::RowState *states = nullptr;
   jf::StagePartial *partials = nullptr;
@@ -222,7 +222,7 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
   s->workspace_bytes =
       max_rows * (sizeof(jf::RowParams) + sizeof(uint32_t) + sizeof(jf::RowState) +
                   sizeof(jf::AcceptChainLane) + sizeof(jf::TreeLaneParams)) +
-      blocks * (sizeof(jf::BlockHeader) + jf::kBlockCandidates * sizeof(uint2) +
+      blocks * (sizeof(jf::BlockHeader) + jf::kBlockCandidates * sizeof(uint64_t) +
                 sizeof(jf::StagePartial));
   *out = s;
   return JF_OK;
