@@ -24,12 +24,12 @@ template <int DT>
 struct Geo;
 template <>
 struct Geo<0> {  // fp32: 4 tokens per 16-byte load
-  static constexpr int VEC = 4, LOADS = 8, TPL = 32, SEG = 2048;
+  static constexpr int VEC = 4, LOADS = 8, TPL = 32, SLAB = kThreads * VEC;
   static constexpr uint32_t CHUNK = kChunkF32;
 };
 template <>
 struct Geo<1> {  // bf16: 8 tokens per 16-byte load
-  static constexpr int VEC = 8, LOADS = 4, TPL = 32, SEG = 2048;
+  static constexpr int VEC = 8, LOADS = 4, TPL = 32, SLAB = kThreads * VEC;
   static constexpr uint32_t CHUNK = kChunkBF16;
 };
 
@@ -38,10 +38,8 @@ constexpr uint32_t kLowestKey = 0x007fffffu;  // the key of -infinity
 constexpr uint32_t kMaxChunks = 64;
 
 struct PrepLds {
-  uint32_t pbits[kMaxChunkWords];
-  uint32_t xbits[kMaxChunkWords];
-  uint32_t rankb[kMaxChunkWords];
-  uint32_t pwords[kPenaltyWordsLds];
+  float pvals[kChunkF32];          // penalized logit by chunk offset
+  uint32_t pbits[kMaxChunkWords];  // tokens of the chunk with a value there
   uint32_t extras[kMaxExtra];
 };
 struct MergeLds {
@@ -57,6 +55,7 @@ struct __align__(16) Lds {
     MergeLds merge;
   };
   uint64_t hist[256];
+  uint64_t wj[kWaves][8];
   uint64_t wl[kWaves];
   float wf[kWaves];
   uint32_t wu[kWaves];
@@ -79,6 +78,8 @@ struct __align__(16) Lds {
 // The select kernel's LDS: the chunk's penalty lookup and the reductions.
 struct __align__(16) SelectLds {
   PrepLds prep;
+  uint32_t ccount;
+  uint64_t wj[kWaves][8];
   uint64_t wl[kWaves];
   float wf[kWaves];
   uint32_t wu[kWaves];
@@ -211,7 +212,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Loads chunk `chunk` of `row`: xs[j*VEC+e] is token
-// chunk*CHUNK + w*SEG + j*64*VEC + lane*VEC + e (w = wave, lane = lane id)
+// chunk*CHUNK + j*SLAB + tid*VEC + e (SLAB = kThreads*VEC: the block's j-th
+// 16-byte loads cover one contiguous slab, so a partial last chunk leaves
+// every thread some of its tokens)
 // after its penalties, or NaN when the row does not admit it (outside the
 // vocabulary, outside a constrained row's mask, an excluded stop token). A
 // NaN logit is never selected either (greedy comparisons skip it, sampled
@@ -223,13 +226,13 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
                                            uint32_t chunk, L &s,
                                            float (&xs)[Geo<DT>::TPL]) {
   constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
-                SEG = Geo<DT>::SEG;
+                SLAB = Geo<DT>::SLAB;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
   constexpr uint32_t VMASK = (1u << VEC) - 1u;
-  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const uint32_t tid = threadIdx.x;
   const uint32_t V = a.vocabulary;
   const uint32_t base = chunk * CHUNK;
-  const uint32_t lane_base = base + w * SEG + lane * VEC;
+  const uint32_t lane_base = base + tid * VEC;
 
   // Penalty entries of this chunk are loaded before the logits: vector
   // loads complete in issue order, so the bitmap below can be built while
@@ -242,10 +245,7 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
   uint2 pe[EPT];
   if (penalized) {
     PrepLds &p = s.prep;
-    for (uint32_t i = tid; i < NWORDS; i += kThreads) {
-      p.pbits[i] = 0;
-      p.xbits[i] = 0;
-    }
+    for (uint32_t i = tid; i < NWORDS; i += kThreads) p.pbits[i] = 0;
     const uint32_t prow = rp.penalty_row;
     const uint32_t *offs = a.pen_offsets + (uint64_t)prow * (a.pen_buckets + 1);
     const uint32_t b0 = base / kPenaltyBucket;
@@ -264,7 +264,7 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
     const float *rowp = (const float *)a.logits + (uint64_t)row * a.stride;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-      const uint32_t t0 = lane_base + j * 64 * VEC;
+      const uint32_t t0 = lane_base + j * SLAB;
       if (t0 + VEC <= V && a.aligned) {
         const f32x4 v = __builtin_nontemporal_load((const f32x4 *)(rowp + t0));
         xs[j * 4 + 0] = v.x;
@@ -282,7 +282,7 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
         (const uint16_t *)a.logits + (uint64_t)row * a.stride;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-      const uint32_t t0 = lane_base + j * 64 * VEC;
+      const uint32_t t0 = lane_base + j * SLAB;
       if (t0 + VEC <= V && a.aligned) {
         const u32x4 v = __builtin_nontemporal_load((const u32x4 *)(rowp + t0));
         xs[j * 8 + 0] = u2f(v.x << 16);
@@ -303,77 +303,56 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
   }
 
   if (penalized) {
+    // Each penalized token's thread reads its logit and writes the
+    // penalized value (sampling.metal:928-963) at its chunk offset; the
+    // lanes holding the token pick it up below. Verify rows also count the
+    // extra (draft) tokens of their context.
     PrepLds &p = s.prep;
-    __syncthreads();  // bitmaps cleared
+    const uint32_t nx = rp.extra_count;
+    if (tid < nx) p.extras[tid] = a.extra[(uint64_t)row * a.extra_stride + tid];
+    __syncthreads();  // bitmap cleared, extras staged
+    auto apply = [&](uint32_t t, uint32_t word) {
+      uint32_t count = word & kCountMask;
+      for (uint32_t k = 0; k < nx; ++k) count += p.extras[k] == t;
+      if (!count && !(word & kPromptBit)) return;
+      const float x = DT == 0 ? ((const float *)a.logits)[(uint64_t)row * a.stride + t]
+                              : bf16_to_float(((const uint16_t *)a.logits)[(uint64_t)row * a.stride + t]);
+      const uint32_t o = t - base;
+      p.pvals[o] = penalize(x, count, rp.repetition, rp.repetition_inverse,
+                            rp.presence, rp.frequency);
+      atomicOr(&p.pbits[o >> 5], 1u << (o & 31));
+    };
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
       const uint32_t i = lo + tid + k * kThreads;
-      if (i < hi) {
-        const uint32_t o = pe[k].x - base;
-        atomicOr(&p.pbits[o >> 5], 1u << (o & 31));
-        if (i - lo < (uint32_t)kPenaltyWordsLds) p.pwords[i - lo] = pe[k].y;
-      }
+      if (i < hi) apply(pe[k].x, pe[k].y);
     }
     for (uint32_t i = lo + tid + EPT * kThreads; i < hi; i += kThreads) {
       const uint2 e = ent[i];
-      const uint32_t o = e.x - base;
-      atomicOr(&p.pbits[o >> 5], 1u << (o & 31));
-      if (i - lo < (uint32_t)kPenaltyWordsLds) p.pwords[i - lo] = e.y;
-    }
-    const uint32_t nx = rp.extra_count;
-    if (tid < nx) {
-      const uint32_t t = a.extra[(uint64_t)row * a.extra_stride + tid];
-      p.extras[tid] = t;
-      if (t >= base && t < base + CHUNK && t < V) {
-        const uint32_t o = t - base;
-        atomicOr(&p.xbits[o >> 5], 1u << (o & 31));
-      }
+      apply(e.x, e.y);
     }
     __syncthreads();
-    // Rank of each word's first entry: exclusive prefix of popcounts.
-    {
-      constexpr uint32_t PER = NWORDS / kThreads;
-      uint32_t c[PER];
-      uint32_t local = 0;
-#pragma unroll
-      for (uint32_t k = 0; k < PER; ++k) {
-        c[k] = __popc(p.pbits[tid * PER + k]);
-        local += c[k];
-      }
-      uint64_t total;
-      uint32_t off = (uint32_t)block_excl_scan_u64(local, s, &total);
-#pragma unroll
-      for (uint32_t k = 0; k < PER; ++k) {
-        p.rankb[tid * PER + k] = off;
-        off += c[k];
-      }
+    // Extra tokens the table does not hold: the first of equal ones applies.
+    if (tid < nx) {
+      const uint32_t t = p.extras[tid];
+      bool first = t >= base && t < base + CHUNK && t < V;
+      for (uint32_t k = 0; k < tid; ++k) first = first && p.extras[k] != t;
+      if (first && !((p.pbits[(t - base) >> 5] >> ((t - base) & 31)) & 1u))
+        apply(t, 0u);
     }
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-      const uint32_t o0 = w * SEG + j * 64 * VEC + lane * VEC;
-      const uint32_t wi = o0 >> 5, sh = o0 & 31;
-      const uint32_t pw = p.pbits[wi], xw = p.xbits[wi];
-      const uint32_t pb = (pw >> sh) & VMASK, xb = (xw >> sh) & VMASK;
-      if (pb | xb) {
+      const uint32_t o0 = j * SLAB + tid * VEC;
+      const uint32_t pb = (p.pbits[o0 >> 5] >> (o0 & 31)) & VMASK;
+      if (pb) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          if (!(((pb | xb) >> e) & 1u)) continue;
-          uint32_t word = 0;
-          if ((pb >> e) & 1u) {
-            const uint32_t r =
-                p.rankb[wi] + __popc(pw & ((1u << (sh + e)) - 1u));
-            word = r < (uint32_t)kPenaltyWordsLds ? p.pwords[r] : ent[lo + r].y;
-          }
-          uint32_t count = word & kCountMask;
-          if ((xb >> e) & 1u) {
-            const uint32_t t = base + o0 + e;
-            for (uint32_t k = 0; k < nx; ++k) count += p.extras[k] == t;
-          }
-          if (count || (word & kPromptBit))
-            xs[j * VEC + e] =
-                penalize(xs[j * VEC + e], count, rp.repetition,
-                         rp.repetition_inverse, rp.presence, rp.frequency);
+        for (int q = 0; q < VEC / 4; ++q) {
+          const float4 pv = *(const float4 *)&p.pvals[o0 + 4 * q];
+          xs[j * VEC + 4 * q + 0] = (pb >> (4 * q + 0)) & 1u ? pv.x : xs[j * VEC + 4 * q + 0];
+          xs[j * VEC + 4 * q + 1] = (pb >> (4 * q + 1)) & 1u ? pv.y : xs[j * VEC + 4 * q + 1];
+          xs[j * VEC + 4 * q + 2] = (pb >> (4 * q + 2)) & 1u ? pv.z : xs[j * VEC + 4 * q + 2];
+          xs[j * VEC + 4 * q + 3] = (pb >> (4 * q + 3)) & 1u ? pv.w : xs[j * VEC + 4 * q + 3];
         }
       }
     }
@@ -389,8 +368,8 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
       const uint32_t st = k ? a.stop1 : a.stop0;
       if (st >= base && st < base + CHUNK) {
         const uint32_t o = st - base;
-        if (o / SEG == w && (o % (64 * VEC)) / VEC == lane) {
-          stop_j[k] = (o % SEG) / (64 * VEC);
+        if ((o % SLAB) / VEC == tid) {
+          stop_j[k] = o / SLAB;
           stop_e[k] = o % VEC;
         }
       }
@@ -400,7 +379,7 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
     const uint32_t *mrow = a.masks + (uint64_t)row * a.mask_stride;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-      const uint32_t t0 = lane_base + j * 64 * VEC;
+      const uint32_t t0 = lane_base + j * SLAB;
       uint32_t vm = VMASK;
       if (constrained && t0 < V) vm = (mrow[t0 >> 5] >> (t0 & 31)) & VMASK;
       if (stop_j[0] == (uint32_t)j) vm &= ~(1u << stop_e[0]);
@@ -414,89 +393,64 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
   }
 }
 
-// Writes the (key, id) of every token whose bit is set in `pb`, in id order
-// across the block, at dst[start + rank] for ranks below `limit - start`.
-// Returns the number of set bits in the block.
-template <int DT, class L>
-__device__ __forceinline__ uint32_t emit_ordered(uint64_t pb,
-                                                 const float (&xs)[Geo<DT>::TPL],
-                                                 uint32_t lane_base, uint64_t *dst,
-                                                 uint32_t start, uint32_t limit,
-                                                 L &s) {
-  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS;
-  constexpr uint32_t VMASK = (1u << VEC) - 1u;
+// Offsets in block id order. A chunk's tokens run in (j, tid, e) order:
+// load j of every thread, threads ascending, VEC tokens each. Given each
+// thread's per-load values v[j] (counts or weights), off[j] is the sum of
+// the values of every load that comes before this thread's load j; returns
+// the block total. Every thread calls it.
+template <int LOADS, class T, class L>
+__device__ __forceinline__ T order_offsets(const T (&v)[LOADS], T (&off)[LOADS],
+                                           L &s) {
   const uint32_t w = threadIdx.x >> 6;
-  const uint32_t wtot = wave_sum_u32(__popcll(pb));
-  __syncthreads();
-  if (lane_id() == 0) s.wu2[w] = wtot;
-  __syncthreads();
-  uint32_t woff = 0, btot = 0;
-#pragma unroll
-  for (int k = 0; k < kWaves; ++k) {
-    woff += (k < (int)w) ? s.wu2[k] : 0;
-    btot += s.wu2[k];
-  }
-  uint32_t running = start + woff;
+  T incl[LOADS];
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
-    const uint32_t bits = (uint32_t)(pb >> (j * VEC)) & VMASK;
-    if (ballot(bits != 0) == 0) continue;
-    const uint32_t nb = __popc(bits);
-    uint32_t excl = 0, tot = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint64_t bm = ballot((nb >> k) & 1u);
-      excl += mbcnt(bm) << k;
-      tot += (uint32_t)__popcll(bm) << k;
-    }
-    uint32_t idx = running + excl;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      if ((bits >> e) & 1u) {
-        if (idx < limit)
-          dst[idx] = (uint64_t)logit_key(xs[j * VEC + e]) |
-                     ((uint64_t)(lane_base + j * 64 * VEC + e) << 32);
-        ++idx;
-      }
-    }
-    running += tot;
+    if constexpr (sizeof(T) == 8)
+      incl[j] = wave_incl_scan_u64(v[j]);
+    else
+      incl[j] = wave_incl_scan_u32(v[j]);
   }
-  return btot;
+  __syncthreads();
+  if (lane_id() == 63)
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) s.wj[w][j] = (uint64_t)incl[j];
+  __syncthreads();
+  T run = 0;
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    T before = 0, tot = 0;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) {
+      const T t = (T)s.wj[k][j];
+      before += k < (int)w ? t : T(0);
+      tot += t;
+    }
+    off[j] = run + before + incl[j] - v[j];
+    run += tot;
+  }
+  return run;
 }
 
-// The first `limit` set bits of `pb` in block id order (w, j, lane, e).
+// The first `limit` set bits of `pb` in block id order.
 template <int DT, class L>
 __device__ __forceinline__ uint64_t first_in_order(uint64_t pb, uint32_t limit,
                                                    L &s) {
   constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS;
   constexpr uint32_t VMASK = (1u << VEC) - 1u;
-  const uint32_t w = threadIdx.x >> 6;
-  const uint32_t wtot = wave_sum_u32(__popcll(pb));
-  __syncthreads();
-  if (lane_id() == 0) s.wu2[w] = wtot;
-  __syncthreads();
-  uint32_t running = 0;
-  for (int k = 0; k < (int)w; ++k) running += s.wu2[k];
+  uint32_t nb[LOADS], off[LOADS];
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) nb[j] = __popc((uint32_t)(pb >> (j * VEC)) & VMASK);
+  order_offsets<LOADS>(nb, off, s);
   uint64_t kept = 0;
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
-    const uint32_t bits = (uint32_t)(pb >> (j * VEC)) & VMASK;
-    const uint32_t nb = __popc(bits);
-    uint32_t excl = 0, tot = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint64_t bm = ballot((nb >> k) & 1u);
-      excl += mbcnt(bm) << k;
-      tot += (uint32_t)__popcll(bm) << k;
-    }
-    uint32_t idx = running + excl;
+    uint32_t idx = off[j];
 #pragma unroll
     for (int e = 0; e < VEC; ++e)
-      if ((bits >> e) & 1u) {
+      if ((pb >> (j * VEC + e)) & 1u) {
         if (idx < limit) kept |= 1ull << (j * VEC + e);
         ++idx;
       }
-    running += tot;
   }
   return kept;
 }
@@ -738,10 +692,10 @@ __device__ __forceinline__ void lds_draw(const SampleLaunch &a, uint32_t row, Ld
                  (uint32_t)kept_total);
 }
 
-// The merge of at most kThreads compacted items (id order in s.merge):
-// thread t holds item t and its rank in (key desc, id asc) order by counting,
-// which gives top-k, the rank-order walk of top-p and, in thread order, the
-// id-order draw.
+// The merge of at most kThreads items in s.merge (any order): thread t
+// holds item t and counts its rank in (key desc, id asc) order, which gives
+// the top-k cut and the rank-order walk of top-p; the kept items' ranks by id
+// give the id-order draw.
 __device__ __forceinline__ void small_merge(const SampleLaunch &a,
                                             const RowParams &rp, uint32_t row,
                                             Lds &s, uint32_t n, float maximum) {
@@ -754,12 +708,12 @@ __device__ __forceinline__ void small_merge(const SampleLaunch &a,
   if (have)
     for (uint32_t j = 0; j < n; ++j) {
       const uint32_t kj = m.key[j];
-      rank += (kj > key) || (kj == key && j < t);
+      rank += (kj > key) || (kj == key && m.id[j] < id);
     }
   const uint32_t n2 = min(rp.top_k, n);
-  const float inv_t = rp.inv_t;
-  const float w = have ? weight_of(key_logit(key), maximum, inv_t) : 0.0f;
+  const float w = have ? weight_of(key_logit(key), maximum, rp.inv_t) : 0.0f;
   const uint64_t wq = quantize(w);
+  if (have) m.bins[t] = rank;
   uint32_t n3 = n2;
   if (rp.flags & kRowTopP) {
     // Weights in rank order, their running sum, the first rank past the
@@ -779,15 +733,17 @@ __device__ __forceinline__ void small_merge(const SampleLaunch &a,
     __syncthreads();
     n3 = s.hit;
   }
+  __syncthreads();
   const bool kept = have && rank < n3;
+  uint32_t irank = 0;  // rank by id among the kept items
+  if (kept)
+    for (uint32_t j = 0; j < n; ++j) irank += m.bins[j] < n3 && m.id[j] < id;
   uint64_t mass3;
-  const uint32_t kept_rank =
-      (uint32_t)block_excl_scan_u64(kept ? 1u : 0u, s, nullptr);
   (void)block_excl_scan_u64(kept ? wq : 0, s, &mass3);
   const double scale = (double)mass3 * 0x1p-44;
-  if (a.out_kept_ids && kept && kept_rank < a.kept_cap) {
-    a.out_kept_ids[(uint64_t)row * a.kept_cap + kept_rank] = id;
-    a.out_kept_probs[(uint64_t)row * a.kept_cap + kept_rank] =
+  if (a.out_kept_ids && kept && irank < a.kept_cap) {
+    a.out_kept_ids[(uint64_t)row * a.kept_cap + irank] = id;
+    a.out_kept_probs[(uint64_t)row * a.kept_cap + irank] =
         mass3 ? (float)((double)w / scale) : 0.0f;
   }
   if (mass3 == 0) {
@@ -801,21 +757,60 @@ __device__ __forceinline__ void small_merge(const SampleLaunch &a,
     const uint64_t r = kept ? residual_of(wq, mass3, draft_q(a, row, id, s)) : 0;
     if (block_max_u32(r > 0 ? 1u : 0u, s)) d = r;
   }
-  uint64_t total;
-  const uint64_t excl = block_excl_scan_u64(d, s, &total);
-  uint64_t target = floor_mul(total, row_uniform(a, row));
-  if (target >= total) target = total - 1;
+  // The draw weights in id order, their running sum, the first past u.
+  __syncthreads();
+  if (kept) {
+    s.hist[irank] = d;
+    m.bins[256 + irank] = id;
+  }
   if (t == 0) {
     s.found_w = 0.0f;
     s.hit = kNoToken;
   }
   __syncthreads();
-  if (kept && excl <= target && excl + d > target) s.hit = id;
+  const uint64_t dp = t < n3 ? s.hist[t] : 0;
+  uint64_t total;
+  const uint64_t excl = block_excl_scan_u64(dp, s, &total);
+  uint64_t target = floor_mul(total, row_uniform(a, row));
+  if (target >= total) target = total - 1;
+  if (t < n3 && excl <= target && excl + dp > target) s.hit = m.bins[256 + t];
   if (drafted && kept && id == draft) s.found_w = w;
   __syncthreads();
   if (t == 0)
     write_result(a, row, s.hit, drafted ? (float)((double)s.found_w / scale) : 0.0f,
                  n3);
+}
+
+// Sorts the n items of s.merge by id (bitonic, padded to a power of two
+// with id kNoToken), so that the radix path sees them in id order.
+__device__ __forceinline__ void lds_sort_by_id(Lds &s, uint32_t n) {
+  MergeLds &m = s.merge;
+  uint32_t P = 1;
+  while (P < n) P <<= 1;
+  for (uint32_t i = n + threadIdx.x; i < P; i += kThreads) {
+    m.key[i] = 0;
+    m.id[i] = kNoToken;
+  }
+  __syncthreads();
+  for (uint32_t size = 2; size <= P; size <<= 1)
+    for (uint32_t stride = size >> 1; stride; stride >>= 1) {
+      for (uint32_t i = threadIdx.x; i < P / 2; i += kThreads) {
+        const uint32_t lo = 2 * stride * (i / stride) + (i % stride);
+        const uint32_t hi = lo + stride;
+        const bool ascending = (lo & size) == 0;
+        const uint32_t a = m.id[lo], b = m.id[hi];
+        if ((a > b) == ascending) {
+          m.id[lo] = b;
+          m.id[hi] = a;
+          const uint32_t k = m.key[lo];
+          m.key[lo] = m.key[hi];
+          m.key[hi] = k;
+        }
+      }
+      __syncthreads();
+    }
+  for (uint32_t i = threadIdx.x; i < n; i += kThreads) m.fl[i] = 1;
+  __syncthreads();
 }
 
 // Keeps the first K of the n compacted items (id order in s.merge) in
@@ -993,8 +988,8 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
   MergeLds &m = s.merge;
   uint32_t n;
   if (fits) {
-    // Candidates at or above the floor into LDS in id order: every load
-    // issued first, contiguous items per thread, then an ordered compaction.
+    // Candidates at or above the floor into LDS: every load issued first,
+    // contiguous items per thread, then a compaction.
     constexpr int PER = kMergeCapacity / kThreads;
     uint64_t v[PER];
     const uint32_t first = tid * PER;
@@ -1008,8 +1003,7 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
       v[k] = 0;
       if (i < n_all) {
         while (s.hoff[c + 1] <= i) ++c;
-        v[k] = ld_dev(a.cands + ((uint64_t)row * S + c) * kBlockCandidates +
-                      (i - s.hoff[c]));
+        v[k] = a.cands[((uint64_t)row * S + c) * kBlockCandidates + (i - s.hoff[c])];
       }
     }
 #pragma unroll
@@ -1027,39 +1021,28 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
       }
     n = (uint32_t)total;
     __syncthreads();
-    if (n <= (uint32_t)kThreads) {
-      small_merge(a, rp, row, s, n, maximum);
-      return;
-    }
-    if (K <= (uint32_t)kThreads && hist_select(s, n, K, maximum)) {
-      small_merge(a, rp, row, s, n, maximum);
-      return;
-    }
-    if (K < n) lds_topk(s, n, K);
   } else {
-    // More candidates than LDS holds and K fits: select the first K at or
-    // above the min-p floor straight from the global lists, then keep them.
-    // Items are addressed by their global rank in the concatenated lists.
-    auto item = [&](uint32_t i) -> uint2 {
+    // More candidates than LDS holds (K fits): select the first K at or
+    // above the floor straight from the lists (keys by radix descent, then
+    // the lowest ids among the ties), then append them to LDS.
+    auto item = [&](uint32_t i) -> uint64_t {
       uint32_t c = 0;
-      while (s.hoff[c + 1] <= i) ++c;
-      const uint64_t v =
-          ld_dev(a.cands + ((uint64_t)row * S + c) * kBlockCandidates + (i - s.hoff[c]));
-      return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+      for (uint32_t step = kMaxChunks / 2; step; step >>= 1)
+        if (c + step < S && s.hoff[c + step] <= i) c += step;
+      return a.cands[((uint64_t)row * S + c) * kBlockCandidates + (i - s.hoff[c])];
     };
     uint32_t c1 = 0;
-    for (uint32_t i = tid; i < n_all; i += kThreads) c1 += item(i).x >= thr;
+    for (uint32_t i = tid; i < n_all; i += kThreads) c1 += (uint32_t)item(i) >= thr;
     const uint32_t n1 = block_sum_u32(c1, s);
-    uint32_t prefix = 0, pmask = 0;
-    uint64_t need = 0;
-    const bool cut = K < n1;
-    if (cut) {
-      need = K;
+    uint32_t kap = 0, iota = kNoToken;  // keep key > kap, or key == kap and id <= iota
+    if (K < n1) {
+      uint32_t prefix = 0, pmask = 0;
+      uint64_t need = K;
       for (int d = 3; d >= 0; --d) {
         s.hist[tid] = 0;
         __syncthreads();
         for (uint32_t i = tid; i < n_all; i += kThreads) {
-          const uint32_t k = item(i).x;
+          const uint32_t k = (uint32_t)item(i);
           if (k >= thr && (k & pmask) == prefix)
             atomicAdd((unsigned long long *)&s.hist[(k >> (8 * d)) & 255u], 1ull);
         }
@@ -1070,54 +1053,56 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
         pmask |= 255u << (8 * d);
         __syncthreads();
       }
-    }
-    // Ordered compaction: ties at `prefix` by id, up to `need` of them.
-    const ItemRange r = my_items(n_all);
-    uint32_t ties = 0;
-    if (cut)
-      for (uint32_t i = r.begin; i < r.end; ++i) {
-        const uint32_t k = item(i).x;
-        ties += k >= thr && k == prefix;
+      kap = prefix;
+      // The need-th smallest id among the ties: the need-th largest of
+      // 0xffffff - id, by descent over its three bytes.
+      uint32_t ip = 0, im = 0;
+      for (int d = 2; d >= 0; --d) {
+        s.hist[tid] = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < n_all; i += kThreads) {
+          const uint64_t v = item(i);
+          if ((uint32_t)v != kap) continue;
+          const uint32_t ri = 0xffffffu - (uint32_t)(v >> 32);
+          if ((ri & im) == ip)
+            atomicAdd((unsigned long long *)&s.hist[(ri >> (8 * d)) & 255u], 1ull);
+        }
+        __syncthreads();
+        crossing_bin(s, need);
+        need -= s.sel_excl;
+        ip |= s.sel_bin << (8 * d);
+        im |= 255u << (8 * d);
+        __syncthreads();
       }
-    const uint32_t tie0 = (uint32_t)block_excl_scan_u64(ties, s, nullptr);
-    uint32_t keep = 0;
-    {
-      uint32_t tr = tie0;
-      for (uint32_t i = r.begin; i < r.end; ++i) {
-        const uint32_t k = item(i).x;
-        if (k < thr) continue;
-        if (!cut || k > prefix) {
-          ++keep;
-        } else if (k == prefix) {
-          keep += tr < need;
-          ++tr;
-        }
-      }
+      iota = 0xffffffu - ip;
     }
-    uint64_t kept_total;
-    uint32_t out = (uint32_t)block_excl_scan_u64(keep, s, &kept_total);
-    {
-      uint32_t tr = tie0;
-      for (uint32_t i = r.begin; i < r.end; ++i) {
-        const uint2 v = item(i);
-        const uint32_t k = v.x;
-        if (k < thr) continue;
-        bool take = !cut || k > prefix;
-        if (cut && k == prefix) {
-          take = tr < need;
-          ++tr;
-        }
-        if (take) {
-          m.key[out] = k;
-          m.id[out] = v.y;
-          m.fl[out] = 1;
-          ++out;
-        }
+    if (tid == 0) s.u32a = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < n_all; i += kThreads) {
+      const uint64_t v = item(i);
+      const uint32_t k = (uint32_t)v, id = (uint32_t)(v >> 32);
+      if (k < thr) continue;
+      if (k > kap || (k == kap && id <= iota)) {
+        const uint32_t slot = atomicAdd(&s.u32a, 1u);
+        m.key[slot] = k;
+        m.id[slot] = id;
+        m.fl[slot] = 1;
       }
     }
-    n = (uint32_t)kept_total;
+    __syncthreads();
+    n = s.u32a;
     __syncthreads();
   }
+  if (n <= (uint32_t)kThreads) {
+    small_merge(a, rp, row, s, n, maximum);
+    return;
+  }
+  if (K <= (uint32_t)kThreads && hist_select(s, n, K, maximum)) {
+    small_merge(a, rp, row, s, n, maximum);
+    return;
+  }
+  lds_sort_by_id(s, n);
+  if (K < n) lds_topk(s, n, K);
   if (rp.flags & kRowTopP) lds_topp(s, n, maximum, rp.inv_t, rp.top_p);
   lds_draw(a, row, s, n, maximum, rp.inv_t);
 }
@@ -1173,7 +1158,7 @@ __device__ __forceinline__ void merge_row(const SampleLaunch &a,
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
-  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SEG = Geo<DT>::SEG,
+  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
                 LOADS = Geo<DT>::LOADS;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
   __shared__ SelectLds s;
@@ -1183,7 +1168,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
   const RowParams rp = a.params[row];
   float xs[TPL];
   load_chunk<DT>(a, rp, row, chunk, s, xs);
-  const uint32_t lane_base = chunk * CHUNK + w * SEG + lane * VEC;
+  const uint32_t lane_base = chunk * CHUNK + tid * VEC;
   BlockHeader *hdr = a.headers + (uint64_t)row * S + chunk;
 
   if (!(rp.flags & kRowSampled)) {
@@ -1197,7 +1182,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
       const float v = xs[i];
       const bool take = v > best || (v == best && bid == kNoToken);
       best = take ? v : best;
-      bid = take ? lane_base + (i / VEC) * 64 * VEC + (i % VEC) : bid;
+      bid = take ? lane_base + (i / VEC) * SLAB + (i % VEC) : bid;
     }
     wave_argmax(best, bid);
     if (lane == 0) {
@@ -1240,6 +1225,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
       s.wu[w] = wcnt;
       s.wu2[w] = wth;
     }
+    if (tid == 0) s.ccount = 0;
     __syncthreads();
     const float bmax = __builtin_fmaxf(
         __builtin_fmaxf(__builtin_fmaxf(s.wf[0], s.wf[1]),
@@ -1251,9 +1237,11 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
     uint32_t thr = tk;
     if (rp.flags & kRowMinP)
       thr = max(thr, logit_key(__builtin_fminf(bmax + rp.minp_offset, bmax)));
-    // Candidates: one compare per 16-byte vector, bits only where it hits.
+    // Candidates: one compare per 16-byte vector; each hit appends its
+    // (key, id) at a slot from the block's LDS counter. The merge is
+    // independent of the order of the list.
     const float tv = thr <= kLowestKey ? -__builtin_inff() : key_logit(thr);
-    uint64_t cb = 0;
+    uint64_t *dst = a.cands + ((uint64_t)row * S + chunk) * kBlockCandidates;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       float vm = xs[j * VEC];
@@ -1262,14 +1250,18 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
       if (vm >= tv) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e)
-          cb |= (uint64_t)(xs[j * VEC + e] >= tv) << (j * VEC + e);
+          if (xs[j * VEC + e] >= tv) {
+            const uint32_t slot = atomicAdd(&s.ccount, 1u);
+            if (slot < (uint32_t)kBlockCandidates)
+              dst[slot] = (uint64_t)logit_key(xs[j * VEC + e]) |
+                          ((uint64_t)(lane_base + j * SLAB + e) << 32);
+          }
       }
     }
-    const uint32_t c = block_sum_u32(__popcll(cb), s);
-    uint64_t *dst = a.cands + ((uint64_t)row * S + chunk) * kBlockCandidates;
+    __syncthreads();
+    const uint32_t c = s.ccount;
     uint32_t emitted = 0, overflow = 0;
     if (c <= (uint32_t)kBlockCandidates) {
-      emit_ordered<DT>(cb, xs, lane_base, dst, 0, kBlockCandidates, s);
       emitted = c;
     } else if (K <= (uint32_t)kBlockCandidates) {
       // Too many candidates: raise the threshold by bisection over keys.
@@ -1310,7 +1302,18 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
         const uint32_t above = block_sum_u32(__popcll(ge & ~eq), s);
         keep = (ge & ~eq) | first_in_order<DT>(eq, K - above, s);
       }
-      emitted = emit_ordered<DT>(keep, xs, lane_base, dst, 0, kBlockCandidates, s);
+      __syncthreads();
+      if (tid == 0) s.ccount = 0;
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < TPL; ++i)
+        if ((keep >> i) & 1) {
+          const uint32_t slot = atomicAdd(&s.ccount, 1u);
+          dst[slot] = (uint64_t)logit_key(xs[i]) |
+                      ((uint64_t)(lane_base + (i / VEC) * SLAB + (i % VEC)) << 32);
+        }
+      __syncthreads();
+      emitted = s.ccount;
     } else {
       overflow = 1;
     }
@@ -1339,14 +1342,14 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(SampleLaunch a) {
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
-  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SEG = Geo<DT>::SEG,
+  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
                 LOADS = Geo<DT>::LOADS;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
   constexpr uint32_t VMASK = (1u << VEC) - 1u;
   __shared__ Lds s;
   const uint32_t S = a.chunks;
   const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
-  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const uint32_t tid = threadIdx.x;
   const uint32_t stage = a.stage;
   RowState st = a.states[row];
   if (st.stage != stage) return;
@@ -1357,7 +1360,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
   float xs[TPL];
   load_chunk<DT>(a, rp, row, chunk, s, xs);
   stage_candidates(a, row, s);
-  const uint32_t lane_base = chunk * CHUNK + w * SEG + lane * VEC;
+  const uint32_t lane_base = chunk * CHUNK + tid * VEC;
   const float M = st.maximum, inv_t = rp.inv_t;
   // Members: admitted (non-NaN), at or above the min-p floor, at or before
   // the kept boundary.
@@ -1367,7 +1370,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     const float v = xs[i];
     if (v != v) continue;
     const uint32_t k = logit_key(v);
-    const uint32_t t = lane_base + (i / VEC) * 64 * VEC + (i % VEC);
+    const uint32_t t = lane_base + (i / VEC) * SLAB + (i % VEC);
     if (k >= st.thr_key && at_or_before(k, t, st.bkey, st.bid)) mem |= 1ull << i;
   }
   StagePartial *part = a.partials + (uint64_t)row * S + chunk;
@@ -1377,37 +1380,25 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     return quantize(weight_of(xs[i], M, inv_t));
   };
   auto tok_of = [&](int i) -> uint32_t {
-    return lane_base + (i / VEC) * 64 * VEC + (i % VEC);
+    return lane_base + (i / VEC) * SLAB + (i % VEC);
   };
   // The `within`-th (0-based) token with a set bit, in id order; returns
   // its token in every thread.
   auto locate = [&](uint64_t bits, uint64_t within) -> uint32_t {
     if (tid == 0) s.hit = kNoToken;
-    const uint32_t wtot = wave_sum_u32(__popcll(bits));
-    __syncthreads();
-    if (lane == 0) s.wu2[w] = wtot;
-    __syncthreads();
-    uint32_t running = 0;
-    for (int k = 0; k < (int)w; ++k) running += s.wu2[k];
+    uint32_t nb[LOADS], off[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) nb[j] = __popc((uint32_t)(bits >> (j * VEC)) & VMASK);
+    order_offsets<LOADS>(nb, off, s);
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-      const uint32_t b = (uint32_t)(bits >> (j * VEC)) & VMASK;
-      const uint32_t nb = __popc(b);
-      uint32_t excl = 0, tot = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint64_t bm = ballot((nb >> k) & 1u);
-        excl += mbcnt(bm) << k;
-        tot += (uint32_t)__popcll(bm) << k;
-      }
-      uint32_t idx = running + excl;
+      uint64_t idx = off[j];
 #pragma unroll
       for (int e = 0; e < VEC; ++e)
-        if ((b >> e) & 1u) {
+        if ((bits >> (j * VEC + e)) & 1u) {
           if (idx == within) s.hit = tok_of(j * VEC + e);
           ++idx;
         }
-      running += tot;
     }
     __syncthreads();
     return s.hit;
@@ -1513,27 +1504,16 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       uint64_t off = 0;
       for (uint32_t c = 0; c < chunk; ++c) off += a.partials[(uint64_t)row * S + c].v[0];
       const double scale = (double)st.mass3 * 0x1p-44;
-      const uint32_t wtot = wave_sum_u32(__popcll(mem));
-      __syncthreads();
-      if (lane == 0) s.wu2[w] = wtot;
-      __syncthreads();
-      uint64_t running = off;
-      for (int k = 0; k < (int)w; ++k) running += s.wu2[k];
+      uint32_t nb[LOADS], offs[LOADS];
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) nb[j] = __popc((uint32_t)(mem >> (j * VEC)) & VMASK);
+      order_offsets<LOADS>(nb, offs, s);
 #pragma unroll
       for (int j = 0; j < LOADS; ++j) {
-        const uint32_t b = (uint32_t)(mem >> (j * VEC)) & VMASK;
-        const uint32_t nb = __popc(b);
-        uint32_t excl = 0, tot = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint64_t bm = ballot((nb >> k) & 1u);
-          excl += mbcnt(bm) << k;
-          tot += (uint32_t)__popcll(bm) << k;
-        }
-        uint64_t idx = running + excl;
+        uint64_t idx = off + offs[j];
 #pragma unroll
         for (int e = 0; e < VEC; ++e)
-          if ((b >> e) & 1u) {
+          if ((mem >> (j * VEC + e)) & 1u) {
             if (idx < a.kept_cap) {
               const int i = j * VEC + e;
               a.out_kept_ids[(uint64_t)row * a.kept_cap + idx] = tok_of(i);
@@ -1543,7 +1523,6 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
             }
             ++idx;
           }
-        running += tot;
       }
       break;
     }
@@ -1585,33 +1564,23 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       }
     }
     if (tid == 0) s.hit = kNoToken;
-    // Layout order: token = base + w*SEG + j*64*VEC + lane*VEC + e, so id
-    // order is (w, j, lane, e). Recompute with that order.
-    __syncthreads();
-    uint64_t wsum = 0;
-#pragma unroll
-    for (int i = 0; i < TPL; ++i) wsum += dl[i];
-    const uint64_t wave_total = wave_sum_u64(wsum);
-    __syncthreads();
-    if (lane == 0) s.wl[w] = wave_total;
-    __syncthreads();
-    uint64_t run = 0;
-    for (int k = 0; k < (int)w; ++k) run += s.wl[k];
+    uint64_t lsum[LOADS], offs[LOADS];
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-      uint64_t lsum = 0;
+      lsum[j] = 0;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) lsum += dl[j * VEC + e];
-      const uint64_t incl = wave_incl_scan_u64(lsum);
-      const uint64_t jt = shfl_u64(incl, 63);
-      uint64_t acc = run + incl - lsum;
+      for (int e = 0; e < VEC; ++e) lsum[j] += dl[j * VEC + e];
+    }
+    order_offsets<LOADS>(lsum, offs, s);
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      uint64_t acc = offs[j];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const uint64_t d = dl[j * VEC + e];
         if (d && acc <= st.within && acc + d > st.within) s.hit = tok_of(j * VEC + e);
         acc += d;
       }
-      run += jt;
     }
     __syncthreads();
     if (tid == 0) {
