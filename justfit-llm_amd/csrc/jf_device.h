@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace jf {
 
 constexpr uint32_t kNoToken = 0xffffffffu;
@@ -135,6 +137,43 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t mask) {
       __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+// Lane exchanges without the LDS crossbar where the lane pattern allows:
+// DPP quad permutes for xor 1 and 2, DPP row shifts for xor 4 and 8 (both
+// partners lie in the same 16-lane row), a swizzle for xor 16 and a
+// permute for xor 32.
+template <int M>
+__device__ __forceinline__ uint32_t xor_u32(uint32_t v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32);
+  if constexpr (M == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (M == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (M == 4 || M == 8) {
+    // row_shl:M reads lane i + M, row_shr:M reads lane i - M.
+    const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 + M, 0xF, 0xF, false);
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x110 + M, 0xF, 0xF, false);
+    return (lane_id() & M) ? dn : up;
+  } else if constexpr (M == 16) {
+    // Bitmask swizzle within 32 lanes: and 0x1f, or 0, xor 0x10.
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F);
+  } else {
+    return (uint32_t)__shfl_xor((int)v, 32, kWave);
+  }
+}
+template <int M>
+__device__ __forceinline__ float xor_f32(float v) {
+  return __uint_as_float(xor_u32<M>(__float_as_uint(v)));
+}
+template <int M>
+__device__ __forceinline__ uint64_t xor_u64(uint64_t v) {
+  return ((uint64_t)xor_u32<M>((uint32_t)(v >> 32)) << 32) | xor_u32<M>((uint32_t)v);
+}
+// Lane i - D within its 16-lane row, or 0 for the first D lanes of a row.
+template <int D>
+__device__ __forceinline__ uint32_t row_shr_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x110 + D, 0xF, 0xF, true);
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   const uint32_t lo = __shfl_xor((uint32_t)v, m, kWave);
   const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, kWave);
@@ -145,73 +184,82 @@ __device__ __forceinline__ uint64_t shfl_down_u64(uint64_t v, int d) {
   const uint32_t hi = __shfl_down((uint32_t)(v >> 32), d, kWave);
   return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int d) {
-  const uint32_t lo = __shfl_up((uint32_t)v, d, kWave);
-  const uint32_t hi = __shfl_up((uint32_t)(v >> 32), d, kWave);
-  return ((uint64_t)hi << 32) | lo;
-}
 __device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
   const uint32_t lo = __shfl((uint32_t)v, src, kWave);
   const uint32_t hi = __shfl((uint32_t)(v >> 32), src, kWave);
   return ((uint64_t)hi << 32) | lo;
 }
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  return ((uint64_t)readlane_u32((uint32_t)(v >> 32), l) << 32) | readlane_u32((uint32_t)v, l);
+}
 
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, kWave);
+// Butterfly reductions: every lane ends with the wave's result.
+#define JF_BUTTERFLY(T, XOR, OP)                                   \
+  v = OP(v, XOR<1>(v));                                            \
+  v = OP(v, XOR<2>(v));                                            \
+  v = OP(v, XOR<4>(v));                                            \
+  v = OP(v, XOR<8>(v));                                            \
+  v = OP(v, XOR<16>(v));                                           \
+  v = OP(v, XOR<32>(v));                                           \
   return v;
-}
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v += shfl_xor_u64(v, m);
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v = max(v, (uint32_t)__shfl_xor(v, m, kWave));
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v = min(v, (uint32_t)__shfl_xor(v, m, kWave));
-  return v;
-}
-__device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
-}
-// Inclusive prefix sum over lanes.
-__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
-  const uint32_t lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint64_t o = shfl_up_u64(v, d);
-    if (lane >= (uint32_t)d) v += o;
-  }
-  return v;
-}
+
+__device__ __forceinline__ uint32_t add_u32(uint32_t a, uint32_t b) { return a + b; }
+__device__ __forceinline__ uint64_t add_u64(uint64_t a, uint64_t b) { return a + b; }
+__device__ __forceinline__ uint32_t max_u32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t min_u32(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ float max_f32(float a, float b) { return __builtin_fmaxf(a, b); }
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { JF_BUTTERFLY(uint32_t, xor_u32, add_u32) }
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) { JF_BUTTERFLY(uint64_t, xor_u64, add_u64) }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { JF_BUTTERFLY(uint32_t, xor_u32, max_u32) }
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { JF_BUTTERFLY(uint32_t, xor_u32, min_u32) }
+__device__ __forceinline__ float wave_max_f32(float v) { JF_BUTTERFLY(float, xor_f32, max_f32) }
+#undef JF_BUTTERFLY
+
+// Inclusive prefix sums over lanes: row-wise by DPP shifts, then the
+// totals of the rows before (lanes 15, 31, 47) added.
 __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
-  const uint32_t lane = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint32_t o = __shfl_up(v, d, kWave);
-    if (lane >= (uint32_t)d) v += o;
-  }
-  return v;
+  v += row_shr_u32<1>(v);
+  v += row_shr_u32<2>(v);
+  v += row_shr_u32<4>(v);
+  v += row_shr_u32<8>(v);
+  const uint32_t r0 = readlane_u32(v, 15), r1 = readlane_u32(v, 31),
+                 r2 = readlane_u32(v, 47);
+  const uint32_t row = lane_id() >> 4;
+  return v + (row >= 1 ? r0 : 0u) + (row >= 2 ? r1 : 0u) + (row >= 3 ? r2 : 0u);
+}
+__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
+  auto shr = [](uint64_t x, auto d) -> uint64_t {
+    constexpr int D = decltype(d)::value;
+    return ((uint64_t)row_shr_u32<D>((uint32_t)(x >> 32)) << 32) | row_shr_u32<D>((uint32_t)x);
+  };
+  v += shr(v, std::integral_constant<int, 1>{});
+  v += shr(v, std::integral_constant<int, 2>{});
+  v += shr(v, std::integral_constant<int, 4>{});
+  v += shr(v, std::integral_constant<int, 8>{});
+  const uint64_t r0 = readlane_u64(v, 15), r1 = readlane_u64(v, 31),
+                 r2 = readlane_u64(v, 47);
+  const uint32_t row = lane_id() >> 4;
+  return v + (row >= 1 ? r0 : 0ull) + (row >= 2 ? r1 : 0ull) + (row >= 3 ? r2 : 0ull);
 }
 
 // The largest greedy candidate of the wave: larger value, then lower id.
 __device__ __forceinline__ void wave_argmax(float &value, uint32_t &id) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) {
-    const float ov = __shfl_xor(value, m, kWave);
-    const uint32_t oi = __shfl_xor(id, m, kWave);
+  auto step = [&](float ov, uint32_t oi) {
     if (ov > value || (ov == value && oi < id)) {
       value = ov;
       id = oi;
     }
-  }
+  };
+  step(xor_f32<1>(value), xor_u32<1>(id));
+  step(xor_f32<2>(value), xor_u32<2>(id));
+  step(xor_f32<4>(value), xor_u32<4>(id));
+  step(xor_f32<8>(value), xor_u32<8>(id));
+  step(xor_f32<16>(value), xor_u32<16>(id));
+  step(xor_f32<32>(value), xor_u32<32>(id));
 }
 
 // The k-th largest (1-based) of the wave's 64 values, by bitwise descent:

@@ -72,6 +72,11 @@ struct __align__(16) Lds {
   uint32_t found_id;
   float found_w;
   uint32_t u32a;
+  uint32_t nbound;
+  float row_max;
+  uint32_t row_admitted;
+  uint32_t row_overflow;
+  uint32_t row_floor;
   uint64_t u64a;
 };
 
@@ -157,12 +162,9 @@ __device__ __forceinline__ void crossing_bin(Lds &s, uint64_t T) {
     const uint64_t h0 = s.hist[4 * l], h1 = s.hist[4 * l + 1],
                    h2 = s.hist[4 * l + 2], h3 = s.hist[4 * l + 3];
     const uint64_t own = h0 + h1 + h2 + h3;
-    uint64_t suf = own;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint64_t o = shfl_down_u64(suf, d);
-      if (l + d < 64) suf += o;
-    }
+    // Suffix sum over lanes: the total less the prefix before this lane.
+    const uint64_t incl = wave_incl_scan_u64(own);
+    const uint64_t suf = readlane_u64(incl, 63) - (incl - own);
     const uint64_t m = ballot(suf >= T);
     const int L = m ? (int)__popcll(m) - 1 : 0;
     const uint64_t above = shfl_u64(suf - own, L);
@@ -429,30 +431,6 @@ __device__ __forceinline__ T order_offsets(const T (&v)[LOADS], T (&off)[LOADS],
     run += tot;
   }
   return run;
-}
-
-// The first `limit` set bits of `pb` in block id order.
-template <int DT, class L>
-__device__ __forceinline__ uint64_t first_in_order(uint64_t pb, uint32_t limit,
-                                                   L &s) {
-  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS;
-  constexpr uint32_t VMASK = (1u << VEC) - 1u;
-  uint32_t nb[LOADS], off[LOADS];
-#pragma unroll
-  for (int j = 0; j < LOADS; ++j) nb[j] = __popc((uint32_t)(pb >> (j * VEC)) & VMASK);
-  order_offsets<LOADS>(nb, off, s);
-  uint64_t kept = 0;
-#pragma unroll
-  for (int j = 0; j < LOADS; ++j) {
-    uint32_t idx = off[j];
-#pragma unroll
-    for (int e = 0; e < VEC; ++e)
-      if ((pb >> (j * VEC + e)) & 1u) {
-        if (idx < limit) kept |= 1ull << (j * VEC + e);
-        ++idx;
-      }
-  }
-  return kept;
 }
 
 // ---- outputs --------------------------------------------------------------
@@ -781,6 +759,197 @@ __device__ __forceinline__ void small_merge(const SampleLaunch &a,
                  n3);
 }
 
+// Bitonic sort of one value per lane over the wave (ascending, or
+// descending): stage (K, J) orders lane pairs J apart within blocks of K.
+template <bool kDescending, int K, int J>
+__device__ __forceinline__ uint64_t sort_stage(uint64_t v, uint32_t lane) {
+  const uint64_t o = xor_u64<J>(v);
+  const bool up = ((lane & (uint32_t)K) == 0) != kDescending;
+  const bool keep_min = ((lane & (uint32_t)J) == 0) == up;
+  return keep_min ? (o < v ? o : v) : (o > v ? o : v);
+}
+template <bool kDescending>
+__device__ __forceinline__ uint64_t wave_sort_u64(uint64_t v) {
+  const uint32_t lane = lane_id();
+  v = sort_stage<kDescending, 2, 1>(v, lane);
+  v = sort_stage<kDescending, 4, 2>(v, lane);
+  v = sort_stage<kDescending, 4, 1>(v, lane);
+  v = sort_stage<kDescending, 8, 4>(v, lane);
+  v = sort_stage<kDescending, 8, 2>(v, lane);
+  v = sort_stage<kDescending, 8, 1>(v, lane);
+  v = sort_stage<kDescending, 16, 8>(v, lane);
+  v = sort_stage<kDescending, 16, 4>(v, lane);
+  v = sort_stage<kDescending, 16, 2>(v, lane);
+  v = sort_stage<kDescending, 16, 1>(v, lane);
+  v = sort_stage<kDescending, 32, 16>(v, lane);
+  v = sort_stage<kDescending, 32, 8>(v, lane);
+  v = sort_stage<kDescending, 32, 4>(v, lane);
+  v = sort_stage<kDescending, 32, 2>(v, lane);
+  v = sort_stage<kDescending, 32, 1>(v, lane);
+  v = sort_stage<kDescending, 64, 32>(v, lane);
+  v = sort_stage<kDescending, 64, 16>(v, lane);
+  v = sort_stage<kDescending, 64, 8>(v, lane);
+  v = sort_stage<kDescending, 64, 4>(v, lane);
+  v = sort_stage<kDescending, 64, 2>(v, lane);
+  v = sort_stage<kDescending, 64, 1>(v, lane);
+  return v;
+}
+
+// The last steps of a row with at most 64 items left (s.merge.key/id[0, n),
+// any order), run by one wave: a sort by (key desc, id asc) gives the
+// top-k cut and the walk of top-p (sampling.metal:585-650); a sort of the
+// kept items by id gives the draw's order and the kept outputs
+// (sampling.metal:700-829).
+__device__ __forceinline__ void wave_merge(const SampleLaunch &a,
+                                           const RowParams &rp, uint32_t row,
+                                           const Lds &s, uint32_t n,
+                                           float maximum, float u,
+                                           uint32_t draft) {
+  const MergeLds &m = s.merge;
+  const uint32_t lane = lane_id();
+  // (key desc, id asc) is the descending order of key:~id.
+  uint64_t c = lane < n ? ((uint64_t)m.key[lane] << 32) | (uint32_t)~m.id[lane] : 0ull;
+  c = wave_sort_u64<true>(c);
+  const uint32_t key = (uint32_t)(c >> 32), id = ~(uint32_t)c;
+  const uint32_t n2 = min(rp.top_k, n);
+  const bool in2 = lane < n2;
+  const float w = in2 ? weight_of(key_logit(key), maximum, rp.inv_t) : 0.0f;
+  const uint64_t wq = quantize(w);
+  uint32_t n3 = n2;
+  if (rp.flags & kRowTopP) {
+    const uint64_t incl = wave_incl_scan_u64(wq);
+    const uint64_t mass2 = shfl_u64(incl, 63);
+    if (mass2) {
+      const uint64_t nucleus = floor_mul(mass2, rp.top_p);
+      const uint64_t hm = ballot(in2 && incl - wq <= nucleus && incl > nucleus);
+      if (hm) n3 = (uint32_t)__builtin_ctzll(hm) + 1;
+    }
+  }
+  const bool kept_rank = lane < n3;
+  const uint64_t mass3 = wave_sum_u64(kept_rank ? wq : 0);
+  // The kept items in id order: lane i holds the i-th smallest id.
+  uint64_t e = kept_rank ? ((uint64_t)id << 32) | lane : ~0ull;
+  e = wave_sort_u64<false>(e);
+  const bool kept = lane < n3;
+  const uint32_t src = (uint32_t)e & 63u;
+  const uint32_t tok = (uint32_t)(e >> 32);
+  const float wk = __shfl(w, (int)src, kWave);
+  const uint64_t wqk = shfl_u64(wq, (int)src);
+  const double scale = (double)mass3 * 0x1p-44;
+  if (a.out_kept_ids && kept && lane < a.kept_cap) {
+    a.out_kept_ids[(uint64_t)row * a.kept_cap + lane] = tok;
+    a.out_kept_probs[(uint64_t)row * a.kept_cap + lane] =
+        mass3 ? (float)((double)wk / scale) : 0.0f;
+  }
+  if (mass3 == 0) {
+    if (lane == 0) write_result(a, row, kNoToken, 0.0f, n3);
+    return;
+  }
+  const bool drafted = draft != kNoToken;
+  uint64_t d = kept ? wqk : 0;
+  if (drafted) {
+    const uint64_t r = kept ? residual_of(wqk, mass3, draft_q(a, row, tok, s)) : 0;
+    if (ballot(r > 0)) d = r;
+  }
+  const uint64_t incl = wave_incl_scan_u64(d);
+  const uint64_t total = shfl_u64(incl, 63);
+  uint64_t target = floor_mul(total, u);
+  if (target >= total) target = total - 1;
+  const uint64_t hm = ballot(kept && incl - d <= target && incl > target);
+  const uint32_t token = __shfl(tok, hm ? (int)__builtin_ctzll(hm) : 0, kWave);
+  const uint64_t fm = ballot(drafted && kept && tok == draft);
+  const float fw = __shfl(wk, fm ? (int)__builtin_ctzll(fm) : 0, kWave);
+  if (lane == 0)
+    write_result(a, row, hm ? token : kNoToken,
+                 drafted && fm ? (float)((double)fw / scale) : 0.0f, n3);
+}
+
+// The exact top-K (K <= 64) of the candidates at or above `thr` that the
+// block holds in registers (v[k] = item first + k, key in the low word, id
+// in the high word): a 1024-bin value histogram over [value(thr), maximum]
+// finds the bin where the count from the top reaches K, and that bin's
+// items are ranked exactly. The kept items (all of them when there are at
+// most K) are appended to s.merge.key/id; returns their number, or -1 when
+// the boundary bin holds more than kThreads items or the values do not
+// spread over the bins. The caller zeroed s.merge.bins before a barrier.
+template <int PER>
+__device__ __forceinline__ int fast_select(const uint64_t (&v)[PER],
+                                           uint32_t first, uint32_t n_all,
+                                           uint32_t thr, uint32_t K,
+                                           float maximum, Lds &s) {
+  MergeLds &m = s.merge;
+  const uint32_t tid = threadIdx.x;
+  const float lo = key_logit(thr);
+  const float scale = 1023.0f / (maximum - lo);
+  if (!(scale > 0.0f && scale < 3.0e38f)) return -1;
+  auto bin_of = [&](uint32_t key) -> uint32_t {
+    return min(1023u, (uint32_t)((key_logit(key) - lo) * scale));
+  };
+  if (tid == 0) {
+    s.u32a = 0;
+    s.nbound = 0;
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k)
+    if (first + k < n_all && (uint32_t)v[k] >= thr)
+      atomicAdd(&m.bins[bin_of((uint32_t)v[k])], 1u);
+  __syncthreads();
+  uint32_t own = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) own += m.bins[4 * tid + k];
+  uint64_t total;
+  const uint32_t before = (uint32_t)block_excl_scan_u64(own, s, &total);
+  const uint32_t suffix = (uint32_t)total - before;  // bins >= 4 tid
+  const bool all = total <= K;
+  if (!all && suffix >= K && suffix - own < K) {
+    uint32_t acc = suffix - own;
+    uint32_t b = 4 * tid + 3;
+    for (int k = 3; k >= 0; --k) {
+      b = 4 * tid + k;
+      if (acc + m.bins[b] >= K) break;
+      acc += m.bins[b];
+    }
+    s.sel_bin = b;
+    s.sel_excl = acc;
+  }
+  __syncthreads();
+  const uint32_t bstar = all ? 0u : s.sel_bin;
+  const uint32_t need = all ? 0u : K - (uint32_t)s.sel_excl;
+  if (!all && m.bins[bstar] > (uint32_t)kThreads) return -1;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const uint32_t key = (uint32_t)v[k];
+    if (first + k >= n_all || key < thr) continue;
+    const uint32_t b = bin_of(key);
+    if (all || b > bstar) {
+      const uint32_t slot = atomicAdd(&s.u32a, 1u);
+      m.key[slot] = key;
+      m.id[slot] = (uint32_t)(v[k] >> 32);
+    } else if (b == bstar) {
+      s.hist[atomicAdd(&s.nbound, 1u)] = v[k];
+    }
+  }
+  __syncthreads();
+  const uint32_t nb = s.nbound;
+  if (tid < nb) {
+    const uint64_t me = s.hist[tid];
+    const uint32_t key = (uint32_t)me, id = (uint32_t)(me >> 32);
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < nb; ++j) {
+      const uint64_t o = s.hist[j];
+      const uint32_t ok = (uint32_t)o, oi = (uint32_t)(o >> 32);
+      rank += ok > key || (ok == key && oi < id);
+    }
+    if (rank < need) {
+      const uint32_t slot = atomicAdd(&s.u32a, 1u);
+      m.key[slot] = key;
+      m.id[slot] = id;
+    }
+  }
+  __syncthreads();
+  return (int)s.u32a;
+}
+
 // Sorts the n items of s.merge by id (bitonic, padded to a power of two
 // with id kNoToken), so that the radix path sees them in id order.
 __device__ __forceinline__ void lds_sort_by_id(Lds &s, uint32_t n) {
@@ -911,6 +1080,115 @@ __device__ __forceinline__ bool hist_select(Lds &s, uint32_t &n, uint32_t K,
   return true;
 }
 
+// A chunk whose candidates overflowed its list, selected again by the
+// merge with the row's threshold `thr`: its tokens at or above it or, when
+// more than the list holds, its first K (K <= kBlockCandidates) in (key
+// desc, id asc) order -- a bisection over keys to a cut that leaves
+// K..kBlockCandidates tokens, else the K-th key itself with the lowest ids
+// among its ties. The row's first K lie among the chunks' first K, so this
+// loses nothing. Rewrites the chunk's list and returns its length. Every
+// thread calls it; it clobbers s.prep (and so s.merge).
+template <int DT>
+__device__ __forceinline__ uint32_t reselect_chunk(const SampleLaunch &a,
+                                                   const RowParams &rp,
+                                                   uint32_t row, uint32_t chunk,
+                                                   uint32_t thr, uint32_t K,
+                                                   Lds &s) {
+  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  const uint32_t tid = threadIdx.x;
+  float xs[TPL];
+  load_chunk<DT>(a, rp, row, chunk, s, xs);
+  const uint32_t lane_base = chunk * CHUNK + tid * VEC;
+  uint64_t *dst = a.cands + ((uint64_t)row * a.chunks + chunk) * kBlockCandidates;
+  const float tv = thr <= kLowestKey ? -__builtin_inff() : key_logit(thr);
+  float bm = -__builtin_inff();
+  uint32_t cnt = 0;
+#pragma unroll
+  for (int i = 0; i < TPL; ++i) {
+    cnt += xs[i] >= tv;
+    bm = __builtin_fmaxf(bm, xs[i]);
+  }
+  cnt = block_sum_u32(cnt, s);
+  const float bmax = __builtin_fmaxf(block_max_f32(bm, s), -3.402823466e38f);
+  uint64_t keep = 0;
+  if (cnt <= (uint32_t)kBlockCandidates) {
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) keep |= (uint64_t)(xs[i] >= tv) << i;
+  } else {
+    // Invariant: at least K tokens at or above lo, fewer than K at or
+    // above hi.
+    uint32_t lo_k = thr, hi_k = logit_key(bmax) + 1;
+    uint32_t found = 0;
+    while (hi_k - lo_k > 1) {
+      const uint32_t mid = lo_k + (hi_k - lo_k) / 2;
+      const float mv = mid <= kLowestKey ? -__builtin_inff() : key_logit(mid);
+      opaque(xs);
+      uint32_t cm = 0;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) cm += xs[i] >= mv;
+      cm = block_sum_u32(cm, s);
+      if (cm < K) {
+        hi_k = mid;
+      } else if (cm <= (uint32_t)kBlockCandidates) {
+        found = mid;
+        break;
+      } else {
+        lo_k = mid;
+      }
+    }
+    const uint32_t cut = found ? found : lo_k;
+    const float cv = cut <= kLowestKey ? -__builtin_inff() : key_logit(cut);
+    opaque(xs);
+    uint64_t ge = 0, eq = 0;
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+      ge |= (uint64_t)(xs[i] >= cv) << i;
+      eq |= (uint64_t)(xs[i] == cv) << i;
+    }
+    keep = ge;
+    if (!found) {
+      // The K-th key itself: of the tokens tied there, the `need` lowest
+      // ids stay. L = the largest chunk offset with fewer than `need` ties
+      // below it (binary descent); offsets are distinct, so exactly `need`
+      // ties lie at offsets <= L. Offset of xs[i] = (i / VEC) * SLAB +
+      // (i % VEC) + tid * VEC.
+      const uint32_t need = K - block_sum_u32(__popcll(ge & ~eq), s);
+      const int toff = (int)(tid * VEC);
+      uint32_t L = 0;
+#pragma unroll 1
+      for (uint32_t bit = CHUNK / 2; bit; bit >>= 1) {
+        const int t = (int)(L + bit) - toff;
+        uint32_t c = 0;
+#pragma unroll
+        for (int i = 0; i < TPL; ++i)
+          c += ((eq >> i) & 1) && (i / VEC) * SLAB + (i % VEC) < t;
+        if (block_sum_u32(c, s) < need) L += bit;
+      }
+      const int lim = (int)L - toff;
+      uint64_t tie_keep = 0;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i)
+        tie_keep |= (uint64_t)(((eq >> i) & 1) && (i / VEC) * SLAB + (i % VEC) <= lim) << i;
+      keep = (ge & ~eq) | tie_keep;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) s.u32a = 0;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TPL; ++i)
+    if ((keep >> i) & 1) {
+      const uint32_t slot = atomicAdd(&s.u32a, 1u);
+      dst[slot] = (uint64_t)logit_key(xs[i]) |
+                  ((uint64_t)(lane_base + (i / VEC) * SLAB + (i % VEC)) << 32);
+    }
+  __syncthreads();
+  const uint32_t n = s.u32a;
+  __syncthreads();
+  return n;
+}
+
 // Starts the multi-pass stages of a row the merge cannot finish.
 __device__ __forceinline__ void begin_stages(const SampleLaunch &a, const RowParams &rp,
                              uint32_t row, float maximum, uint32_t admitted) {
@@ -940,33 +1218,52 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
                               uint32_t row, Lds &s) {
   const uint32_t S = a.chunks, tid = threadIdx.x;
   const BlockHeader *hb = a.headers + (uint64_t)row * S;
-  float hm = -3.402823466e38f;
-  uint32_t hc = 0, ha = 0, ho = 0, hf = 0;
-  if (tid < S) {
-    const BlockHeader *h = hb + tid;
-    hm = ld_dev(&h->maximum);
-    hc = ld_dev(&h->count);
-    ha = ld_dev(&h->admitted);
-    ho = ld_dev(&h->overflow);
-    hf = ld_dev(&h->floor_key);
-    s.hcnt[tid] = hc;
+  // Everything the row needs from memory is requested up front: the chunk
+  // summaries (one lane each, S <= 64), the uniform, the draft token and its
+  // sparse candidates. The select kernel's writes are visible here because
+  // it ended before this launch began.
+  const float u = row_uniform(a, row);
+  const uint32_t draft = row_draft(a, row);
+  for (uint32_t b = tid; b < 1024; b += kThreads) s.merge.bins[b] = 0;
+  if (tid < 16) {
+    const bool sparse = !a.dense_q && draft != kNoToken;
+    s.cids[tid] = sparse ? a.cand_ids[(uint64_t)row * 16 + tid] : kNoToken;
+    s.cprobs[tid] = sparse ? a.cand_probs[(uint64_t)row * 16 + tid] : 0.0f;
   }
-  stage_candidates(a, row, s);
-  const float maximum = block_max_f32(hm, s);
-  const uint32_t admitted = block_sum_u32(ha, s);
-  const uint32_t overflow = block_max_u32(ho, s);
-  // The K-th key of the row is at least every block's floor.
-  const uint32_t floor_key = block_max_u32(hf, s);
-  if (tid == 0) {
-    uint32_t n = 0;
-    for (uint32_t c = 0; c < S; ++c) {
-      s.hoff[c] = n;
-      n += s.hcnt[c];
+  if (tid < 64) {
+    float hm = -3.402823466e38f;
+    uint32_t hc = 0, ha = 0, ho = 0, hf = 0;
+    if (tid < S) {
+      const BlockHeader h = hb[tid];
+      hm = h.maximum;
+      hc = h.count;
+      ha = h.admitted;
+      ho = h.overflow;
+      hf = h.floor_key;
     }
-    s.hoff[S] = n;
+    const float mx = wave_max_f32(hm);
+    const uint32_t adm = wave_sum_u32(ha), ovf = wave_max_u32(ho),
+                   flr = wave_max_u32(hf);
+    const uint32_t incl = wave_incl_scan_u32(hc);
+    const uint64_t omask = ballot(ho != 0);
+    if (tid < S) {
+      s.hoff[tid + 1] = incl;
+      s.hcnt[tid] = hc;
+    }
+    if (tid == 0) {
+      s.u64a = omask;
+      s.hoff[0] = 0;
+      s.row_max = mx;
+      s.row_admitted = adm;
+      s.row_overflow = ovf;
+      s.row_floor = flr;
+    }
   }
   __syncthreads();
-  const uint32_t n_all = s.hoff[S];
+  const float maximum = s.row_max;
+  const uint32_t admitted = s.row_admitted, overflow = s.row_overflow;
+  // The K-th key of the row is at least every block's floor.
+  const uint32_t floor_key = s.row_floor;
   if (admitted == 0 || maximum == __builtin_inff()) {
     if (tid == 0) {
       write_result(a, row, kNoToken, 0.0f, 0);
@@ -975,16 +1272,36 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
     return;
   }
   const uint32_t K = rp.top_k;
-  const bool fits = n_all <= (uint32_t)kMergeCapacity;
-  if (overflow || (!fits && K > (uint32_t)kMergeCapacity)) {
-    if (tid == 0) begin_stages(a, rp, row, maximum, admitted);
-    return;
-  }
-  if (tid == 0) a.states[row].stage = kStageDone;
   uint32_t thr = (rp.flags & kRowMinP)
                      ? logit_key(__builtin_fminf(maximum + rp.minp_offset, maximum))
                      : 0u;
   if (rp.flags & kRowTopK) thr = max(thr, floor_key);
+  if (overflow && K <= (uint32_t)kBlockCandidates) {
+    // Chunks with more candidates than their lists hold (rare: flat or
+    // tied values): select each again, then recount.
+    uint64_t om = s.u64a;
+    while (om) {
+      const uint32_t c = (uint32_t)__builtin_ctzll(om);
+      om &= om - 1;
+      const uint32_t n = reselect_chunk<DT>(a, rp, row, c, thr, K, s);
+      if (tid == 0) s.hcnt[c] = n;
+    }
+    __syncthreads();
+    if (tid < 64) {
+      const uint32_t incl = wave_incl_scan_u32(tid < S ? s.hcnt[tid] : 0u);
+      if (tid < S) s.hoff[tid + 1] = incl;
+    }
+    for (uint32_t b = tid; b < 1024; b += kThreads) s.merge.bins[b] = 0;
+    __syncthreads();
+  }
+  const uint32_t n_all = s.hoff[S];
+  const bool fits = n_all <= (uint32_t)kMergeCapacity;
+  if ((overflow && K > (uint32_t)kBlockCandidates) ||
+      (!fits && K > (uint32_t)kMergeCapacity)) {
+    if (tid == 0) begin_stages(a, rp, row, maximum, admitted);
+    return;
+  }
+  if (tid == 0) a.states[row].stage = kStageDone;
   MergeLds &m = s.merge;
   uint32_t n;
   if (fits) {
@@ -1004,6 +1321,13 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
       if (i < n_all) {
         while (s.hoff[c + 1] <= i) ++c;
         v[k] = a.cands[((uint64_t)row * S + c) * kBlockCandidates + (i - s.hoff[c])];
+      }
+    }
+    if (K <= 64u && thr > kLowestKey) {
+      const int kept = fast_select(v, first, n_all, thr, K, maximum, s);
+      if (kept >= 0) {
+        if (tid < 64) wave_merge(a, rp, row, s, (uint32_t)kept, maximum, u, draft);
+        return;
       }
     }
 #pragma unroll
@@ -1092,6 +1416,14 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
     __syncthreads();
     n = s.u32a;
     __syncthreads();
+  }
+  if (K <= 64u && K < n && hist_select(s, n, K, maximum)) {
+    if (tid < 64) wave_merge(a, rp, row, s, n, maximum, u, draft);
+    return;
+  }
+  if (n <= 64u) {
+    if (tid < 64) wave_merge(a, rp, row, s, n, maximum, u, draft);
+    return;
   }
   if (n <= (uint32_t)kThreads) {
     small_merge(a, rp, row, s, n, maximum);
@@ -1260,68 +1592,14 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
     }
     __syncthreads();
     const uint32_t c = s.ccount;
-    uint32_t emitted = 0, overflow = 0;
-    if (c <= (uint32_t)kBlockCandidates) {
-      emitted = c;
-    } else if (K <= (uint32_t)kBlockCandidates) {
-      // Too many candidates: raise the threshold by bisection over keys.
-      // Invariant: at least K tokens at or above lo, fewer than K at or
-      // above hi. It stops early at a key that leaves K..kBlockCandidates
-      // tokens; otherwise it ends on the K-th key itself, and the tokens
-      // tied there are kept by lowest id so that exactly K remain.
-      uint32_t lo_k = thr, hi_k = logit_key(bmax) + 1;
-      uint32_t found = 0;
-      while (hi_k - lo_k > 1) {
-        const uint32_t mid = lo_k + (hi_k - lo_k) / 2;
-        const float mv = mid <= kLowestKey ? -__builtin_inff() : key_logit(mid);
-        opaque(xs);
-        uint32_t cm = 0;
-#pragma unroll
-        for (int i = 0; i < TPL; ++i) cm += xs[i] >= mv;
-        cm = block_sum_u32(cm, s);
-        if (cm < K) {
-          hi_k = mid;
-        } else if (cm <= (uint32_t)kBlockCandidates) {
-          found = mid;
-          break;
-        } else {
-          lo_k = mid;
-        }
-      }
-      const uint32_t cut = found ? found : lo_k;
-      const float cv = cut <= kLowestKey ? -__builtin_inff() : key_logit(cut);
-      opaque(xs);
-      uint64_t ge = 0, eq = 0;
-#pragma unroll
-      for (int i = 0; i < TPL; ++i) {
-        ge |= (uint64_t)(xs[i] >= cv) << i;
-        eq |= (uint64_t)(xs[i] == cv) << i;
-      }
-      uint64_t keep = ge;
-      if (!found) {
-        const uint32_t above = block_sum_u32(__popcll(ge & ~eq), s);
-        keep = (ge & ~eq) | first_in_order<DT>(eq, K - above, s);
-      }
-      __syncthreads();
-      if (tid == 0) s.ccount = 0;
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < TPL; ++i)
-        if ((keep >> i) & 1) {
-          const uint32_t slot = atomicAdd(&s.ccount, 1u);
-          dst[slot] = (uint64_t)logit_key(xs[i]) |
-                      ((uint64_t)(lane_base + (i / VEC) * SLAB + (i % VEC)) << 32);
-        }
-      __syncthreads();
-      emitted = s.ccount;
-    } else {
-      overflow = 1;
-    }
     if (tid == 0) {
+      // More candidates than the list holds: the merge selects this chunk
+      // again (with the row's own thresholds) or hands the row to the
+      // multi-pass stages.
       hdr->maximum = bmax;
-      hdr->count = emitted;
+      hdr->count = min(c, (uint32_t)kBlockCandidates);
       hdr->admitted = badm;
-      hdr->overflow = overflow;
+      hdr->overflow = c > (uint32_t)kBlockCandidates ? 1u : 0u;
       hdr->floor_key = tk;
     }
   }

@@ -165,6 +165,38 @@ def test_extra_verify_tokens_and_sparse_draft():
     assert np.any(g["draft_probs"][:rows - 1] > 0)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_overflowing_chunks_reselected(bf16):
+    """Chunks with more than 1024 candidates (flat or tied values) are
+    selected again by the merge with the row's thresholds: penalties,
+    verify-row extras and ties at the K-th key all go through that path."""
+    rng = np.random.default_rng(21)
+    V = 3 * 8192 + 777
+    rows = 6
+    x = np.round(rng.normal(0, 0.05, (rows, V)), 1).astype(np.float32)
+    x[1] = 2.0
+    x[2, ::5] = 4.0
+    x[3, :9000] = 1.5
+    x[4] = np.round(rng.normal(0, 0.02, V), 2)
+    hist = [rng.integers(0, V, 3000).astype(np.uint32) for _ in range(rows)]
+    extra = [rng.integers(0, V, r).astype(np.uint32) for r in range(rows)]
+    pols = [J.policy(temperature=1.0, top_k=64, repetition=1.3, presence=0.2),
+            J.policy(temperature=0.7, top_k=500, top_p=0.8, frequency=0.1),
+            J.policy(temperature=1.0, top_k=1000, presence=0.5),
+            J.policy(temperature=0.9, top_k=200, min_p=0.5, repetition=0.8),
+            J.policy(temperature=1.2, top_k=1024, top_p=0.99),
+            J.policy(temperature=1.0, top_k=3, presence=-0.4)]
+    u = rng.random(rows).astype(np.float32)
+    kw = dict(histories=hist, generated=[1500] * rows, mark_prompt=[True] * rows,
+              extra=extra, uniforms=u, kept_capacity=1024)
+    if bf16:
+        kw["logits_bf16"] = WL.to_bf16_bits(x)
+    else:
+        kw["logits"] = x
+    g, r = both(V, pols, **kw)
+    assert_same(g, r)
+
+
 @pytest.mark.parametrize("kind", ["unfiltered", "topp", "minp", "bigk", "all"])
 def test_multipass_stages(kind):
     rng = np.random.default_rng(14)
