@@ -40,7 +40,7 @@ enum RowFlags : uint32_t {
 struct BlockHeader {
   float maximum;       // sampled: largest admitted logit (-FLT_MAX if none)
   uint32_t count;      // sampled: candidates written
-  uint32_t admitted;   // sampled: admitted non-NaN tokens
+  uint32_t admitted;   // sampled: 1 when the chunk admits a non-NaN token
   uint32_t overflow;   // sampled: candidates did not fit
   float best_value;    // greedy
   uint32_t best_id;    // greedy

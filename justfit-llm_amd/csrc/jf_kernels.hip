@@ -37,9 +37,20 @@ constexpr uint32_t kMaxChunkWords = kChunkF32 / 32;
 constexpr uint32_t kLowestKey = 0x007fffffu;  // the key of -infinity
 constexpr uint32_t kMaxChunks = 64;
 
+// A chunk's penalized values, compact: the table's entries of the chunk
+// (sorted by token) are processed in rounds of kPenaltySlots; an entry's
+// value sits at its rank within the round, and the lane holding a token
+// finds that rank from the bitmap: the rank of its word's first entry plus
+// the entries before it in the word. Extra (draft) tokens the table does
+// not hold have their own bitmap and values by extra index.
+constexpr uint32_t kPenaltySlots = 1024;
 struct PrepLds {
-  float pvals[kChunkF32];          // penalized logit by chunk offset
-  uint32_t pbits[kMaxChunkWords];  // tokens of the chunk with a value there
+  float pvals[kPenaltySlots + 8];  // + the reads past a vector's last entry
+  uint32_t pbits[kMaxChunkWords];  // this round's entries
+  uint32_t wrank[kMaxChunkWords];  // rank of each word's first entry
+  uint32_t tbits[kMaxChunkWords];  // every entry of the chunk (verify rows)
+  uint32_t xbits[kMaxChunkWords];  // extra tokens outside the table
+  float xvals[kMaxExtra];
   uint32_t extras[kMaxExtra];
 };
 struct MergeLds {
@@ -210,6 +221,20 @@ __device__ __forceinline__ void opaque(float (&xs)[N]) {
 #pragma unroll
   for (int i = 0; i < N; ++i) asm volatile("" : "+v"(xs[i]));
 }
+// A load through the scalar cache (uniform address). Its wait counts only
+// scalar loads, so it does not wait behind the vector loads in flight.
+__device__ __forceinline__ uint32_t scalar_load_u32(const uint32_t *p) {
+  const uint64_t addr = (uint64_t)p;
+  const uint64_t u =
+      ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32)) << 32) |
+      (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)addr);
+  uint32_t v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)"
+               : "=s"(v)
+               : "s"(u)
+               : "memory");
+  return v;
+}
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -235,32 +260,6 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
   const uint32_t V = a.vocabulary;
   const uint32_t base = chunk * CHUNK;
   const uint32_t lane_base = base + tid * VEC;
-
-  // Penalty entries of this chunk are loaded before the logits: vector
-  // loads complete in issue order, so the bitmap below can be built while
-  // the logits are still in flight.
-  const bool penalized = (rp.flags & kRowPenalized) != 0;
-  constexpr uint32_t NWORDS = CHUNK / 32;
-  constexpr int EPT = 4;  // entries per thread held in registers
-  uint32_t lo = 0, hi = 0;
-  const uint2 *ent = nullptr;
-  uint2 pe[EPT];
-  if (penalized) {
-    PrepLds &p = s.prep;
-    for (uint32_t i = tid; i < NWORDS; i += kThreads) p.pbits[i] = 0;
-    const uint32_t prow = rp.penalty_row;
-    const uint32_t *offs = a.pen_offsets + (uint64_t)prow * (a.pen_buckets + 1);
-    const uint32_t b0 = base / kPenaltyBucket;
-    const uint32_t b1 = min((base + CHUNK) / kPenaltyBucket, a.pen_buckets);
-    lo = __builtin_amdgcn_readfirstlane(offs[b0]);
-    hi = __builtin_amdgcn_readfirstlane(offs[b1]);
-    ent = a.pen_entries + (uint64_t)prow * a.pen_max_entries;
-#pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-      const uint32_t i = lo + tid + k * kThreads;
-      pe[k] = i < hi ? ent[i] : make_uint2(kNoToken, 0u);
-    }
-  }
 
   if constexpr (DT == 0) {
     const float *rowp = (const float *)a.logits + (uint64_t)row * a.stride;
@@ -304,57 +303,160 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
     }
   }
 
+  // The constraint mask words of those tokens (constrained rows), also
+  // requested before anything waits.
+  const bool constrained = (rp.flags & kRowConstrained) != 0;
+  uint32_t mwords[LOADS];
+  if (constrained) {
+    const uint32_t *mrow = a.masks + (uint64_t)row * a.mask_stride;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const uint32_t t0 = lane_base + j * SLAB;
+      mwords[j] = t0 < V ? mrow[t0 >> 5] : 0u;
+    }
+  }
+
+  // Penalty entries of this chunk: its range in the table by scalar loads
+  // (which do not wait behind the vector loads above), then the entries,
+  // which arrive after the logits (vector loads complete in issue order).
+  const bool penalized = (rp.flags & kRowPenalized) != 0;
+  constexpr uint32_t NWORDS = CHUNK / 32;
+  constexpr int EPT = kPenaltySlots / kThreads;  // entries per thread held in registers
+  const uint32_t nx = penalized ? rp.extra_count : 0u;
+  uint32_t lo = 0, hi = 0;
+  const uint2 *ent = nullptr;
+  uint2 pe[EPT];
   if (penalized) {
-    // Each penalized token's thread reads its logit and writes the
-    // penalized value (sampling.metal:928-963) at its chunk offset; the
-    // lanes holding the token pick it up below. Verify rows also count the
-    // extra (draft) tokens of their context.
     PrepLds &p = s.prep;
-    const uint32_t nx = rp.extra_count;
+    for (uint32_t i = tid; i < NWORDS; i += kThreads) {
+      p.pbits[i] = 0;
+      p.wrank[i] = kNoToken;
+      if (nx) {
+        p.tbits[i] = 0;
+        p.xbits[i] = 0;
+      }
+    }
     if (tid < nx) p.extras[tid] = a.extra[(uint64_t)row * a.extra_stride + tid];
-    __syncthreads();  // bitmap cleared, extras staged
-    auto apply = [&](uint32_t t, uint32_t word) {
-      uint32_t count = word & kCountMask;
-      for (uint32_t k = 0; k < nx; ++k) count += p.extras[k] == t;
-      if (!count && !(word & kPromptBit)) return;
-      const float x = DT == 0 ? ((const float *)a.logits)[(uint64_t)row * a.stride + t]
-                              : bf16_to_float(((const uint16_t *)a.logits)[(uint64_t)row * a.stride + t]);
-      const uint32_t o = t - base;
-      p.pvals[o] = penalize(x, count, rp.repetition, rp.repetition_inverse,
-                            rp.presence, rp.frequency);
-      atomicOr(&p.pbits[o >> 5], 1u << (o & 31));
-    };
+    const uint32_t prow = rp.penalty_row;
+    const uint32_t *offs = a.pen_offsets + (uint64_t)prow * (a.pen_buckets + 1);
+    const uint32_t b0 = base / kPenaltyBucket;
+    const uint32_t b1 = min((base + CHUNK) / kPenaltyBucket, a.pen_buckets);
+    lo = scalar_load_u32(offs + b0);
+    hi = scalar_load_u32(offs + b1);
+    ent = a.pen_entries + (uint64_t)prow * a.pen_max_entries;
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
       const uint32_t i = lo + tid + k * kThreads;
-      if (i < hi) apply(pe[k].x, pe[k].y);
+      pe[k] = i < hi ? ent[i] : make_uint2(kNoToken, 0u);
     }
-    for (uint32_t i = lo + tid + EPT * kThreads; i < hi; i += kThreads) {
-      const uint2 e = ent[i];
-      apply(e.x, e.y);
+  }
+
+  if (penalized) {
+    // Each entry's thread reads its token's logit again (an L2 hit: the
+    // block has just loaded it) and writes the penalized value
+    // (sampling.metal:928-963) at its rank; the lanes holding the tokens
+    // take the values. Verify rows also count the extra (draft) tokens of
+    // their context. An entry with nothing to apply keeps its logit.
+    PrepLds &p = s.prep;
+    auto value_of = [&](uint32_t t, uint32_t word) -> float {
+      uint32_t count = word & kCountMask;
+      for (uint32_t k = 0; k < nx; ++k) count += p.extras[k] == t;
+      const float x = DT == 0 ? ((const float *)a.logits)[(uint64_t)row * a.stride + t]
+                              : bf16_to_float(((const uint16_t *)a.logits)[(uint64_t)row * a.stride + t]);
+      if (!count && !(word & kPromptBit)) return x;
+      return penalize(x, count, rp.repetition, rp.repetition_inverse, rp.presence,
+                      rp.frequency);
+    };
+    auto place = [&](uint32_t t, uint32_t word, uint32_t rank) {
+      const uint32_t o = t - base;
+      p.pvals[rank] = value_of(t, word);
+      atomicOr(&p.pbits[o >> 5], 1u << (o & 31));
+      atomicMin(&p.wrank[o >> 5], rank);
+      if (nx) atomicOr(&p.tbits[o >> 5], 1u << (o & 31));
+    };
+    // The lanes take this round's values: the vector's first rank is its
+    // word's first rank plus the entries before it in the word; its k-th
+    // penalized token takes the value k places further.
+    auto take = [&]() {
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) {
+        const uint32_t o0 = j * SLAB + tid * VEC;
+        const uint32_t pw = p.pbits[o0 >> 5];
+        const uint32_t sh = o0 & 31;
+        const uint32_t nib = (pw >> sh) & VMASK;
+        if (nib) {
+          const uint32_t r = p.wrank[o0 >> 5] + __popc(pw & ((1u << sh) - 1u));
+          if constexpr (VEC == 4) {
+            const float v0 = p.pvals[r], v1 = p.pvals[r + 1], v2 = p.pvals[r + 2],
+                        v3 = p.pvals[r + 3];
+            const uint32_t c1 = nib & 1u, c2 = c1 + ((nib >> 1) & 1u),
+                           c3 = c2 + ((nib >> 2) & 1u);
+            float *x = &xs[j * 4];
+            x[0] = (nib & 1u) ? v0 : x[0];
+            x[1] = (nib & 2u) ? (c1 ? v1 : v0) : x[1];
+            x[2] = (nib & 4u) ? (c2 == 0 ? v0 : (c2 == 1 ? v1 : v2)) : x[2];
+            x[3] = (nib & 8u) ? (c3 == 0 ? v0 : (c3 == 1 ? v1 : (c3 == 2 ? v2 : v3))) : x[3];
+          } else {
+            uint32_t rr = r;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e)
+              if ((nib >> e) & 1u) xs[j * VEC + e] = p.pvals[rr++];
+          }
+        }
+      }
+    };
+    const uint32_t total = hi - lo;
+    __syncthreads();  // bitmaps cleared, extras staged
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const uint32_t e = tid + k * kThreads;
+      if (e < total) place(pe[k].x, pe[k].y, e);
     }
     __syncthreads();
-    // Extra tokens the table does not hold: the first of equal ones applies.
-    if (tid < nx) {
-      const uint32_t t = p.extras[tid];
-      bool first = t >= base && t < base + CHUNK && t < V;
-      for (uint32_t k = 0; k < tid; ++k) first = first && p.extras[k] != t;
-      if (first && !((p.pbits[(t - base) >> 5] >> ((t - base) & 31)) & 1u))
-        apply(t, 0u);
+    take();
+    // More entries than one round holds (a history crowded into this
+    // chunk): further rounds, entries read as they go.
+    for (uint32_t r0 = kPenaltySlots; r0 < total; r0 += kPenaltySlots) {
+      __syncthreads();
+      for (uint32_t i = tid; i < NWORDS; i += kThreads) {
+        p.pbits[i] = 0;
+        p.wrank[i] = kNoToken;
+      }
+      __syncthreads();
+      for (uint32_t e = r0 + tid; e < min(total, r0 + kPenaltySlots); e += kThreads) {
+        const uint2 en = ent[lo + e];
+        place(en.x, en.y, e - r0);
+      }
+      __syncthreads();
+      take();
     }
-    __syncthreads();
+    if (nx) {
+      // Extra tokens the table does not hold: the first of equal ones
+      // applies, with the count of all of them.
+      __syncthreads();
+      if (tid < nx) {
+        const uint32_t t = p.extras[tid];
+        bool first = t >= base && t < base + CHUNK && t < V;
+        for (uint32_t k = 0; k < tid; ++k) first = first && p.extras[k] != t;
+        if (first && !((p.tbits[(t - base) >> 5] >> ((t - base) & 31)) & 1u)) {
+          p.xvals[tid] = value_of(t, 0u);
+          atomicOr(&p.xbits[(t - base) >> 5], 1u << ((t - base) & 31));
+        }
+      }
+      __syncthreads();
 #pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-      const uint32_t o0 = j * SLAB + tid * VEC;
-      const uint32_t pb = (p.pbits[o0 >> 5] >> (o0 & 31)) & VMASK;
-      if (pb) {
+      for (int j = 0; j < LOADS; ++j) {
+        const uint32_t o0 = j * SLAB + tid * VEC;
+        const uint32_t nib = (p.xbits[o0 >> 5] >> (o0 & 31)) & VMASK;
+        if (nib) {
 #pragma unroll
-        for (int q = 0; q < VEC / 4; ++q) {
-          const float4 pv = *(const float4 *)&p.pvals[o0 + 4 * q];
-          xs[j * VEC + 4 * q + 0] = (pb >> (4 * q + 0)) & 1u ? pv.x : xs[j * VEC + 4 * q + 0];
-          xs[j * VEC + 4 * q + 1] = (pb >> (4 * q + 1)) & 1u ? pv.y : xs[j * VEC + 4 * q + 1];
-          xs[j * VEC + 4 * q + 2] = (pb >> (4 * q + 2)) & 1u ? pv.z : xs[j * VEC + 4 * q + 2];
-          xs[j * VEC + 4 * q + 3] = (pb >> (4 * q + 3)) & 1u ? pv.w : xs[j * VEC + 4 * q + 3];
+          for (int e = 0; e < VEC; ++e)
+            if ((nib >> e) & 1u) {
+              const uint32_t t = base + o0 + e;
+              uint32_t k = 0;
+              while (p.extras[k] != t) ++k;  // the first equal extra
+              xs[j * VEC + e] = p.xvals[k];
+            }
         }
       }
     }
@@ -362,7 +464,6 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
   }
 
   // Admission: the constraint mask and the stop tokens.
-  const bool constrained = (rp.flags & kRowConstrained) != 0;
   uint32_t stop_j[2] = {0xffu, 0xffu}, stop_e[2] = {0, 0};
   if (rp.flags & kRowExcludeStop) {
 #pragma unroll
@@ -378,12 +479,11 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
     }
   }
   if (constrained || (rp.flags & kRowExcludeStop)) {
-    const uint32_t *mrow = a.masks + (uint64_t)row * a.mask_stride;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const uint32_t t0 = lane_base + j * SLAB;
       uint32_t vm = VMASK;
-      if (constrained && t0 < V) vm = (mrow[t0 >> 5] >> (t0 & 31)) & VMASK;
+      if (constrained && t0 < V) vm = (mwords[j] >> (t0 & 31)) & VMASK;
       if (stop_j[0] == (uint32_t)j) vm &= ~(1u << stop_e[0]);
       if (stop_j[1] == (uint32_t)j) vm &= ~(1u << stop_e[1]);
       if (vm != VMASK) {
@@ -1191,23 +1291,21 @@ __device__ __forceinline__ uint32_t reselect_chunk(const SampleLaunch &a,
 
 // Starts the multi-pass stages of a row the merge cannot finish.
 __device__ __forceinline__ void begin_stages(const SampleLaunch &a, const RowParams &rp,
-                             uint32_t row, float maximum, uint32_t admitted) {
+                             uint32_t row, float maximum) {
   RowState st = {};
   st.maximum = maximum;
   st.bkey = 0;
   st.bid = 0;
-  if (rp.flags & kRowMinP) {
-    st.thr_key = logit_key(__builtin_fminf(maximum + rp.minp_offset, maximum));
+  // The members' count decides whether top-k cuts; a row with neither
+  // min-p nor top-k keeps every admitted token.
+  if (rp.flags & (kRowMinP | kRowTopK)) {
+    st.thr_key = (rp.flags & kRowMinP)
+                     ? logit_key(__builtin_fminf(maximum + rp.minp_offset, maximum))
+                     : 0u;
     st.stage = kStageCount1;
   } else {
     st.thr_key = 0;
-    st.n1 = admitted;
-    if (rp.top_k < admitted) {
-      st.stage = kStageTopK3;
-      st.remaining = rp.top_k;
-    } else {
-      st.stage = (rp.flags & kRowTopP) ? kStageMass2 : kStageMass3;
-    }
+    st.stage = (rp.flags & kRowTopP) ? kStageMass2 : kStageMass3;
   }
   st.drafted = row_draft(a, row) != kNoToken ? 1u : 0u;
   a.states[row] = st;
@@ -1298,7 +1396,7 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
   const bool fits = n_all <= (uint32_t)kMergeCapacity;
   if ((overflow && K > (uint32_t)kBlockCandidates) ||
       (!fits && K > (uint32_t)kMergeCapacity)) {
-    if (tid == 0) begin_stages(a, rp, row, maximum, admitted);
+    if (tid == 0) begin_stages(a, rp, row, maximum);
     return;
   }
   if (tid == 0) a.states[row].stage = kStageDone;
@@ -1534,14 +1632,12 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
       hdr->best_id = bi;
     }
   } else {
-    // Admitted (non-NaN) tokens: the lane's maximum and count.
-    float mx = -__builtin_inff();
-    uint32_t cnt = 0;
+    // The lane's largest admitted (non-NaN) value: fmax skips NaN operands,
+    // so the NaN it starts from survives only when the lane admits nothing.
+    float mx = __builtin_nanf("");
 #pragma unroll
-    for (int i = 0; i < TPL; ++i) {
-      mx = __builtin_fmaxf(mx, xs[i]);
-      cnt += xs[i] == xs[i];
-    }
+    for (int i = 0; i < TPL; ++i) mx = __builtin_fmaxf(mx, xs[i]);
+    const bool any = mx == mx;
     // A bound for the block's top-k: each wave's ceil(k/4)-th largest lane
     // maximum has that many of the wave's tokens at or above it, so the
     // block has at least k tokens at or above the least of the four.
@@ -1549,12 +1645,12 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
     const uint32_t kw = (K + kWaves - 1) / kWaves;
     const bool bound = (rp.flags & kRowTopK) && kw <= 64;
     uint32_t wth = 0;
-    if (bound) wth = wave_kth_largest(cnt ? logit_key(mx) : 0u, kw);
+    if (bound) wth = wave_kth_largest(any ? logit_key(mx) : 0u, kw);
     const float wmax = wave_max_f32(mx);
-    const uint32_t wcnt = wave_sum_u32(cnt);
+    const uint32_t wany = ballot(any) != 0 ? 1u : 0u;
     if (lane == 0) {
       s.wf[w] = wmax;
-      s.wu[w] = wcnt;
+      s.wu[w] = wany;
       s.wu2[w] = wth;
     }
     if (tid == 0) s.ccount = 0;
@@ -1563,7 +1659,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
         __builtin_fmaxf(__builtin_fmaxf(s.wf[0], s.wf[1]),
                         __builtin_fmaxf(s.wf[2], s.wf[3])),
         -3.402823466e38f);
-    const uint32_t badm = s.wu[0] + s.wu[1] + s.wu[2] + s.wu[3];
+    const uint32_t badm = s.wu[0] | s.wu[1] | s.wu[2] | s.wu[3];
     const uint32_t tk =
         bound ? min(min(s.wu2[0], s.wu2[1]), min(s.wu2[2], s.wu2[3])) : 0u;
     uint32_t thr = tk;

@@ -455,7 +455,7 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
       any_sampled = true;
       if (rp.top_k > (uint32_t)jf::kBlockCandidates) {
         staged = true;
-        need_count1 |= (rp.flags & jf::kRowMinP) != 0;
+        need_count1 |= (rp.flags & (jf::kRowMinP | jf::kRowTopK)) != 0;
         need_topk |= (rp.flags & jf::kRowTopK) != 0;
         need_topp |= (rp.flags & jf::kRowTopP) != 0;
       }
