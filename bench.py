@@ -35,6 +35,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound of the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 64 MiB device copy (20 times): the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE readings to bytes")
     return ap.parse_args()
 
 
@@ -97,6 +101,7 @@ def build_workload(cfg, mode):
     rows = lg.shape[0]
     w["rows"] = rows
     w["alg_bytes"] = lg.nbytes + hist_bytes + rows * 4 * 2  # + uniforms + outputs
+    w["select_bytes"] = lg.nbytes + hist_bytes
     return w
 
 
@@ -165,6 +170,53 @@ class GpuStep:
         self.sampler.launch(a)
 
 
+class HipEvents:
+    """Raw HIP events (libamdhip64 through ctypes) for the library to record
+    around its selection kernel."""
+
+    def __init__(self, n):
+        import ctypes
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.ev = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            rc = self.hip.hipEventCreate(ctypes.byref(e))
+            assert rc == 0, f"hipEventCreate: {rc}"
+            self.ev.append(e)
+
+    def ms(self, i, j):
+        out = self.ct.c_float()
+        rc = self.hip.hipEventElapsedTime(self.ct.byref(out), self.ev[i], self.ev[j])
+        assert rc == 0, f"hipEventElapsedTime: {rc}"
+        return out.value
+
+    def destroy(self):
+        for e in self.ev:
+            self.hip.hipEventDestroy(e)
+
+
+def time_select(g, first, steps):
+    """The selection kernel's own duration: a pair of HIP events that the
+    library's launch of that kernel records at its start and end
+    (hipExtLaunchKernelGGL) on the stream it runs on. Returns the mean and
+    p50 in microseconds."""
+    import torch
+    ev = HipEvents(2 * steps)
+    torch.cuda.synchronize()
+    for i in range(steps):
+        a, _ = g.kw[(first + i) % len(g.kw)]
+        a.select_start_event = ev.ev[2 * i].value
+        a.select_done_event = ev.ev[2 * i + 1].value
+        g.sampler.launch(a)
+        a.select_start_event = None
+        a.select_done_event = None
+    torch.cuda.synchronize()
+    us = np.array([ev.ms(2 * i, 2 * i + 1) for i in range(steps)]) * 1000.0
+    ev.destroy()
+    return float(us.mean()), float(np.percentile(us, 50))
+
+
 def cpu_baseline(w, seconds):
     """The oracle (a C restatement, -O2, pthreads over rows) on a bounded
     sample of the same workload: whole steps until `seconds` elapse."""
@@ -212,8 +264,22 @@ def read_traffic(cfg):
     return None
 
 
+def copy_calibration():
+    import torch
+    n = 64 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n, "bytes_written": n, "launches": 20}))
+
+
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: every box has one "
                           "MI355X; rows shard across GPUs with no exchange (see "
@@ -244,7 +310,12 @@ def main():
     ms_per_step = total_ms / K
     p50, p90 = float(np.percentile(per, 50)), float(np.percentile(per, 90))
     mean_us = float(per.mean())
-    achieved = w["alg_bytes"] / (mean_us * 1e-6) / 1e9
+    step_gbs = w["alg_bytes"] / (mean_us * 1e-6) / 1e9
+    # The dominant kernel (the single pass over the logits) timed alone; its
+    # algorithmic bytes are the logits and the history ids (the merge's
+    # uniforms and outputs are a few hundred bytes).
+    sel_mean, sel_p50 = time_select(g, args.warmup + K, K)
+    achieved = w["select_bytes"] / (sel_mean * 1e-6) / 1e9
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
     traffic = read_traffic(args.config)
     line = {
@@ -268,7 +339,12 @@ def main():
                    "algorithmic_bytes_per_step": w["alg_bytes"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
-                     "traffic": traffic},
+                     "traffic": traffic,
+                     "kernel": "jf::select_kernel<%d>" % (1 if "bf16" in w["dtype"] else 0),
+                     "kernel_mean_us": sel_mean, "kernel_p50_us": sel_p50,
+                     "algorithmic_bytes": w["select_bytes"],
+                     "step_achieved": step_gbs,
+                     "step_frac": step_gbs / PEAK_HBM_GBS},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -191,6 +191,12 @@ typedef struct jf_sample_args {
   uint32_t *out_kept_ids;          /* device */
   float *out_kept_probs;           /* device */
   uint32_t kept_capacity;
+  /* Optional, with no counterpart in the reference: two hipEvent_t that the
+   * single-pass selection kernel's launch records at its own start and end
+   * (hipExtLaunchKernelGGL), so that a caller can time that kernel alone.
+   * Both NULL records nothing. */
+  void *select_start_event;
+  void *select_done_event;
 } jf_sample_args;
 
 int jf_sample(jf_sampler *sampler, const jf_sample_args *args, void *stream);

@@ -198,7 +198,10 @@ struct AcceptTreeLaunch {
 };
 
 // Launchers (jf_kernels.hip); they return the hipError_t of the launch.
-int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream);
+// With both events set, they record the selection kernel's own start and end.
+int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
+                  void *start_event = nullptr, void *stop_event = nullptr);
+int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream);
 int launch_accept_tree(const AcceptTreeLaunch &a, void *stream);

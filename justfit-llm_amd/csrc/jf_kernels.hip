@@ -15,6 +15,8 @@
 // drafted row (sampling.metal:585-829). Every sum that decides a token is an
 // exact 64-bit sum of floor(w * 2^44), so the parallel order never changes
 // a result.
+#include <hip/hip_ext.h>
+
 #include "jf_device.h"
 #include "jf_kernels.h"
 
@@ -267,7 +269,7 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
     for (int j = 0; j < LOADS; ++j) {
       const uint32_t t0 = lane_base + j * SLAB;
       if (t0 + VEC <= V && a.aligned) {
-        const f32x4 v = __builtin_nontemporal_load((const f32x4 *)(rowp + t0));
+        const f32x4 v = *(const f32x4 *)(rowp + t0);
         xs[j * 4 + 0] = v.x;
         xs[j * 4 + 1] = v.y;
         xs[j * 4 + 2] = v.z;
@@ -285,7 +287,7 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
     for (int j = 0; j < LOADS; ++j) {
       const uint32_t t0 = lane_base + j * SLAB;
       if (t0 + VEC <= V && a.aligned) {
-        const u32x4 v = __builtin_nontemporal_load((const u32x4 *)(rowp + t0));
+        const u32x4 v = *(const u32x4 *)(rowp + t0);
         xs[j * 8 + 0] = u2f(v.x << 16);
         xs[j * 8 + 1] = u2f(v.x & 0xffff0000u);
         xs[j * 8 + 2] = u2f(v.y << 16);
@@ -2197,15 +2199,30 @@ __global__ void accept_tree_kernel(AcceptTreeLaunch a) {
 
 // ---- launchers -------------------------------------------------------
 
-int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream) {
-  const dim3 grid(a.rows * a.chunks), block(kThreads), mgrid(a.rows);
-  if (dtype == 0) {
-    hipLaunchKernelGGL(select_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
-    hipLaunchKernelGGL(merge_kernel<0>, mgrid, block, 0, (hipStream_t)stream, a);
+int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
+                  void *start_event, void *stop_event) {
+  const dim3 grid(a.rows * a.chunks), block(kThreads);
+  const hipStream_t st = (hipStream_t)stream;
+  if (start_event) {
+    const hipEvent_t e0 = (hipEvent_t)start_event, e1 = (hipEvent_t)stop_event;
+    if (dtype == 0)
+      hipExtLaunchKernelGGL(select_kernel<0>, grid, block, 0, st, e0, e1, 0, a);
+    else
+      hipExtLaunchKernelGGL(select_kernel<1>, grid, block, 0, st, e0, e1, 0, a);
+  } else if (dtype == 0) {
+    hipLaunchKernelGGL(select_kernel<0>, grid, block, 0, st, a);
   } else {
-    hipLaunchKernelGGL(select_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
-    hipLaunchKernelGGL(merge_kernel<1>, mgrid, block, 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(select_kernel<1>, grid, block, 0, st, a);
   }
+  return (int)hipGetLastError();
+}
+
+int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream) {
+  const dim3 grid(a.rows), block(kThreads);
+  if (dtype == 0)
+    hipLaunchKernelGGL(merge_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(merge_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

@@ -549,8 +549,13 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   L.out_kept_probs = a->out_kept_probs;
   L.kept_cap = a->kept_capacity;
 
-  int e = jf::launch_select(L, a->dtype, stream);
+  if ((a->select_start_event == nullptr) != (a->select_done_event == nullptr))
+    return fail(JF_ERR_INVALID_ARGUMENT, "select events come in pairs");
+  int e = jf::launch_select(L, a->dtype, stream, a->select_start_event,
+                            a->select_done_event);
   if (e != hipSuccess) return hip_fail((hipError_t)e, "select launch");
+  e = jf::launch_merge(L, a->dtype, stream);
+  if (e != hipSuccess) return hip_fail((hipError_t)e, "merge launch");
   if (staged) {
     for (uint32_t stage = jf::kStageCount1; stage <= jf::kStageLast; ++stage) {
       if (stage == jf::kStageCount1 && !need_count1) continue;

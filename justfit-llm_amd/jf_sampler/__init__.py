@@ -64,7 +64,8 @@ class JfSampleArgs(ctypes.Structure):
         ("draft_q_stride", c_u64), ("out_tokens", c_vp),
         ("out_draft_probs", c_vp), ("out_kept_counts", c_vp),
         ("out_kept_ids", c_vp), ("out_kept_probs", c_vp),
-        ("kept_capacity", c_u32),
+        ("kept_capacity", c_u32), ("select_start_event", c_vp),
+        ("select_done_event", c_vp),
     ]
 
 
