@@ -32,7 +32,7 @@ def run_gpu(V, policies, *, logits=None, logits_bf16=None, masks=None,
         kw["masks"] = torch.from_numpy(np.ascontiguousarray(masks, np.uint32).view(np.int32)).to(dev)
     table = None
     if histories is not None:
-        H = max(len(h) for h in histories) + 8
+        H = max((len(h) for h in histories if h is not None), default=0) + 8
         table = J.PenaltyTable(V, rows, H + 32)
         for r, h in enumerate(histories):
             if h is None:
