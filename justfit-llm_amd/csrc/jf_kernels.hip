@@ -90,6 +90,7 @@ struct __align__(16) Lds {
   uint32_t row_admitted;
   uint32_t row_overflow;
   uint32_t row_floor;
+  uint32_t row_maxcount;
   uint64_t u64a;
 };
 
@@ -1052,6 +1053,68 @@ __device__ __forceinline__ int fast_select(const uint64_t (&v)[PER],
   return (int)s.u32a;
 }
 
+// The exact top-K (K <= 64) candidates of a row held in registers (v[k] =
+// key | id << 32; bit k of `valid` set for a real item at or above the
+// floor): a 1024-bin
+// value histogram over [value(thr), maximum] locates the bin where the
+// count from the top reaches K (wave 0 finds it), and every item of that
+// bin and above goes to s.merge.key/id. Returns their number (then K plus
+// the boundary bin's other items, or all items when there are at most K),
+// or -1 when the values do not spread over the bins. The caller zeroed
+// s.merge.bins before a barrier.
+template <int PER>
+__device__ __forceinline__ int spec_select(const uint64_t (&v)[PER], uint32_t valid,
+                                           uint32_t thr, uint32_t K, float maximum,
+                                           Lds &s) {
+  MergeLds &m = s.merge;
+  const uint32_t tid = threadIdx.x;
+  const float lo = key_logit(thr);
+  const float scale = 1023.0f / (maximum - lo);
+  if (!(scale > 0.0f && scale < 3.0e38f)) return -1;
+  auto bin_of = [&](uint32_t key) -> uint32_t {
+    return min(1023u, (uint32_t)((key_logit(key) - lo) * scale));
+  };
+  if (tid == 0) s.u32a = 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k)
+    if ((valid >> k) & 1) atomicAdd(&m.bins[bin_of((uint32_t)v[k])], 1u);
+  __syncthreads();
+  if (tid < 64) {
+    // Lane l owns bins 16 l .. 16 l + 15; the suffix count from the top.
+    uint32_t own = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) own += m.bins[16 * tid + k];
+    const uint32_t incl = wave_incl_scan_u32(own);
+    const uint32_t total = readlane_u32(incl, 63);
+    const uint32_t suffix = total - (incl - own);  // bins >= 16 l
+    if (total <= K) {
+      if (tid == 0) s.sel_bin = 0;
+    } else if (suffix >= K && suffix - own < K) {
+      uint32_t acc = suffix - own, b = 16 * tid + 15;
+      for (int k = 15; k >= 0; --k) {
+        b = 16 * tid + k;
+        if (acc + m.bins[b] >= K) break;
+        acc += m.bins[b];
+      }
+      s.sel_bin = b;
+    }
+  }
+  __syncthreads();
+  const uint32_t bstar = s.sel_bin;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    if (!((valid >> k) & 1)) continue;
+    const uint32_t key = (uint32_t)v[k];
+    if (bin_of(key) >= bstar) {
+      const uint32_t slot = atomicAdd(&s.u32a, 1u);
+      m.key[slot] = key;
+      m.id[slot] = (uint32_t)(v[k] >> 32);
+    }
+  }
+  __syncthreads();
+  return (int)s.u32a;
+}
+
 // Sorts the n items of s.merge by id (bitonic, padded to a power of two
 // with id kNoToken), so that the radix path sees them in id order.
 __device__ __forceinline__ void lds_sort_by_id(Lds &s, uint32_t n) {
@@ -1324,6 +1387,21 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
   // it ended before this launch began.
   const float u = row_uniform(a, row);
   const uint32_t draft = row_draft(a, row);
+  // Rows with a small top-k also fetch the first P slots of every chunk's
+  // candidate list now, before the counts are known (S * P <= SPEC items).
+  constexpr int SPEC = 10;
+  const uint32_t K = rp.top_k;
+  const uint32_t P = S <= 20 ? 128u : (S <= 40 ? 64u : 32u);
+  const uint32_t pshift = S <= 20 ? 7u : (S <= 40 ? 6u : 5u);
+  const bool spec = (rp.flags & kRowTopK) && K <= 64u;
+  uint64_t sv[SPEC];
+#pragma unroll
+  for (int k = 0; k < SPEC; ++k) {
+    const uint32_t i = tid + k * kThreads, c = i >> pshift;
+    sv[k] = 0;
+    if (spec && c < S)
+      sv[k] = a.cands[((uint64_t)row * S + c) * kBlockCandidates + (i & (P - 1))];
+  }
   for (uint32_t b = tid; b < 1024; b += kThreads) s.merge.bins[b] = 0;
   if (tid < 16) {
     const bool sparse = !a.dense_q && draft != kNoToken;
@@ -1343,7 +1421,7 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
     }
     const float mx = wave_max_f32(hm);
     const uint32_t adm = wave_sum_u32(ha), ovf = wave_max_u32(ho),
-                   flr = wave_max_u32(hf);
+                   flr = wave_max_u32(hf), hcmax = wave_max_u32(hc);
     const uint32_t incl = wave_incl_scan_u32(hc);
     const uint64_t omask = ballot(ho != 0);
     if (tid < S) {
@@ -1357,6 +1435,7 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
       s.row_admitted = adm;
       s.row_overflow = ovf;
       s.row_floor = flr;
+      s.row_maxcount = hcmax;
     }
   }
   __syncthreads();
@@ -1371,7 +1450,6 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
     }
     return;
   }
-  const uint32_t K = rp.top_k;
   uint32_t thr = (rp.flags & kRowMinP)
                      ? logit_key(__builtin_fminf(maximum + rp.minp_offset, maximum))
                      : 0u;
@@ -1404,6 +1482,30 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
   if (tid == 0) a.states[row].stage = kStageDone;
   MergeLds &m = s.merge;
   uint32_t n;
+  if (spec && !overflow && s.row_maxcount <= P && thr > kLowestKey) {
+    // Every list fits in the slots fetched up front: the items at or above
+    // the floor, selected straight from registers.
+    uint32_t valid = 0;
+#pragma unroll
+    for (int k = 0; k < SPEC; ++k) {
+      const uint32_t i = tid + k * kThreads, c = i >> pshift;
+      if (c < S && (i & (P - 1)) < s.hcnt[c] && (uint32_t)sv[k] >= thr) valid |= 1u << k;
+    }
+    const int got = spec_select(sv, valid, thr, K, maximum, s);
+    if (got >= 0) {
+      // At most K items and the boundary bin's: usually 64 or fewer.
+      n = (uint32_t)got;
+      if (n > 64u && !hist_select(s, n, K, maximum)) {
+        lds_sort_by_id(s, n);
+        lds_topk(s, n, K);
+        if (rp.flags & kRowTopP) lds_topp(s, n, maximum, rp.inv_t, rp.top_p);
+        lds_draw(a, row, s, n, maximum, rp.inv_t);
+        return;
+      }
+      if (tid < 64) wave_merge(a, rp, row, s, n, maximum, u, draft);
+      return;
+    }
+  }
   if (fits) {
     // Candidates at or above the floor into LDS: every load issued first,
     // contiguous items per thread, then a compaction.
