@@ -862,58 +862,47 @@ __device__ __forceinline__ void small_merge(const SampleLaunch &a,
                  n3);
 }
 
-// Bitonic sort of one value per lane over the wave (ascending, or
-// descending): stage (K, J) orders lane pairs J apart within blocks of K.
-template <bool kDescending, int K, int J>
-__device__ __forceinline__ uint64_t sort_stage(uint64_t v, uint32_t lane) {
-  const uint64_t o = xor_u64<J>(v);
-  const bool up = ((lane & (uint32_t)K) == 0) != kDescending;
-  const bool keep_min = ((lane & (uint32_t)J) == 0) == up;
-  return keep_min ? (o < v ? o : v) : (o > v ? o : v);
-}
-template <bool kDescending>
-__device__ __forceinline__ uint64_t wave_sort_u64(uint64_t v) {
-  const uint32_t lane = lane_id();
-  v = sort_stage<kDescending, 2, 1>(v, lane);
-  v = sort_stage<kDescending, 4, 2>(v, lane);
-  v = sort_stage<kDescending, 4, 1>(v, lane);
-  v = sort_stage<kDescending, 8, 4>(v, lane);
-  v = sort_stage<kDescending, 8, 2>(v, lane);
-  v = sort_stage<kDescending, 8, 1>(v, lane);
-  v = sort_stage<kDescending, 16, 8>(v, lane);
-  v = sort_stage<kDescending, 16, 4>(v, lane);
-  v = sort_stage<kDescending, 16, 2>(v, lane);
-  v = sort_stage<kDescending, 16, 1>(v, lane);
-  v = sort_stage<kDescending, 32, 16>(v, lane);
-  v = sort_stage<kDescending, 32, 8>(v, lane);
-  v = sort_stage<kDescending, 32, 4>(v, lane);
-  v = sort_stage<kDescending, 32, 2>(v, lane);
-  v = sort_stage<kDescending, 32, 1>(v, lane);
-  v = sort_stage<kDescending, 64, 32>(v, lane);
-  v = sort_stage<kDescending, 64, 16>(v, lane);
-  v = sort_stage<kDescending, 64, 8>(v, lane);
-  v = sort_stage<kDescending, 64, 4>(v, lane);
-  v = sort_stage<kDescending, 64, 2>(v, lane);
-  v = sort_stage<kDescending, 64, 1>(v, lane);
-  return v;
+// Makes one wave's LDS writes visible to its own later LDS reads of other
+// lanes' entries: LDS runs one wave's instructions in order, so waiting for
+// them to finish and keeping the compiler from moving memory operations
+// across is enough.
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
 // The last steps of a row with at most 64 items left (s.merge.key/id[0, n),
-// any order), run by one wave: a sort by (key desc, id asc) gives the
-// top-k cut and the walk of top-p (sampling.metal:585-650); a sort of the
-// kept items by id gives the draw's order and the kept outputs
+// any order), run by one wave. Each item counts the items ahead of it in
+// (key desc, id asc) order, which gives the top-k cut and the walk of top-p
+// (sampling.metal:585-650); each kept item counts the kept items of lower
+// id, which gives the draw's order and the kept outputs
 // (sampling.metal:700-829).
 __device__ __forceinline__ void wave_merge(const SampleLaunch &a,
                                            const RowParams &rp, uint32_t row,
-                                           const Lds &s, uint32_t n,
-                                           float maximum, float u,
-                                           uint32_t draft) {
-  const MergeLds &m = s.merge;
+                                           Lds &s, uint32_t n, float maximum,
+                                           float u, uint32_t draft) {
+  MergeLds &m = s.merge;
+  uint64_t *A = s.hist;        // items as key:~id, arrival order
+  uint64_t *B = s.hist + 64;   // the same in rank order
+  uint64_t *D = s.hist + 128;  // draw weights in id order
+  uint32_t *E = m.bins;        // kept ids in rank order
+  uint32_t *F = m.bins + 128;  // kept ids in id order
   const uint32_t lane = lane_id();
+  const bool have = lane < n;
   // (key desc, id asc) is the descending order of key:~id.
-  uint64_t c = lane < n ? ((uint64_t)m.key[lane] << 32) | (uint32_t)~m.id[lane] : 0ull;
-  c = wave_sort_u64<true>(c);
-  const uint32_t key = (uint32_t)(c >> 32), id = ~(uint32_t)c;
+  const uint64_t c = have ? ((uint64_t)m.key[lane] << 32) | (uint32_t)~m.id[lane] : 0ull;
+  A[lane] = c;
+  wave_lds_sync();
+  // Lanes at or past n hold 0, which ranks after every item.
+  uint32_t rank = 0;
+#pragma unroll
+  for (int j = 0; j < 64; j += 2) {
+    const uint64_t c0 = A[j], c1 = A[j + 1];
+    rank += (c0 > c ? 1u : 0u) + (c1 > c ? 1u : 0u);
+  }
+  if (have) B[rank] = c;
+  wave_lds_sync();
+  const uint64_t cr = have ? B[lane] : 0ull;
+  const uint32_t key = (uint32_t)(cr >> 32), id = ~(uint32_t)cr;
   const uint32_t n2 = min(rp.top_k, n);
   const bool in2 = lane < n2;
   const float w = in2 ? weight_of(key_logit(key), maximum, rp.inv_t) : 0.0f;
@@ -921,50 +910,57 @@ __device__ __forceinline__ void wave_merge(const SampleLaunch &a,
   uint32_t n3 = n2;
   if (rp.flags & kRowTopP) {
     const uint64_t incl = wave_incl_scan_u64(wq);
-    const uint64_t mass2 = shfl_u64(incl, 63);
+    const uint64_t mass2 = readlane_u64(incl, 63);
     if (mass2) {
       const uint64_t nucleus = floor_mul(mass2, rp.top_p);
       const uint64_t hm = ballot(in2 && incl - wq <= nucleus && incl > nucleus);
       if (hm) n3 = (uint32_t)__builtin_ctzll(hm) + 1;
     }
   }
-  const bool kept_rank = lane < n3;
-  const uint64_t mass3 = wave_sum_u64(kept_rank ? wq : 0);
-  // The kept items in id order: lane i holds the i-th smallest id.
-  uint64_t e = kept_rank ? ((uint64_t)id << 32) | lane : ~0ull;
-  e = wave_sort_u64<false>(e);
   const bool kept = lane < n3;
-  const uint32_t src = (uint32_t)e & 63u;
-  const uint32_t tok = (uint32_t)(e >> 32);
-  const float wk = __shfl(w, (int)src, kWave);
-  const uint64_t wqk = shfl_u64(wq, (int)src);
+  const uint64_t mass3 = wave_sum_u64(kept ? wq : 0);
+  // Id order of the kept items: rank among the kept ids.
+  E[lane] = kept ? id : kNoToken;
+  wave_lds_sync();
+  uint32_t irank = 0;
+#pragma unroll
+  for (int q = 0; q < 64; q += 4) {
+    const uint4 e4 = *(const uint4 *)&E[q];
+    irank += (e4.x < id ? 1u : 0u) + (e4.y < id ? 1u : 0u) + (e4.z < id ? 1u : 0u) +
+             (e4.w < id ? 1u : 0u);
+  }
   const double scale = (double)mass3 * 0x1p-44;
-  if (a.out_kept_ids && kept && lane < a.kept_cap) {
-    a.out_kept_ids[(uint64_t)row * a.kept_cap + lane] = tok;
-    a.out_kept_probs[(uint64_t)row * a.kept_cap + lane] =
-        mass3 ? (float)((double)wk / scale) : 0.0f;
+  if (a.out_kept_ids && kept && irank < a.kept_cap) {
+    a.out_kept_ids[(uint64_t)row * a.kept_cap + irank] = id;
+    a.out_kept_probs[(uint64_t)row * a.kept_cap + irank] =
+        mass3 ? (float)((double)w / scale) : 0.0f;
   }
   if (mass3 == 0) {
     if (lane == 0) write_result(a, row, kNoToken, 0.0f, n3);
     return;
   }
   const bool drafted = draft != kNoToken;
-  uint64_t d = kept ? wqk : 0;
+  uint64_t d = kept ? wq : 0;
   if (drafted) {
-    const uint64_t r = kept ? residual_of(wqk, mass3, draft_q(a, row, tok, s)) : 0;
+    const uint64_t r = kept ? residual_of(wq, mass3, draft_q(a, row, id, s)) : 0;
     if (ballot(r > 0)) d = r;
   }
-  const uint64_t incl = wave_incl_scan_u64(d);
-  const uint64_t total = shfl_u64(incl, 63);
+  const uint64_t fm = ballot(drafted && kept && id == draft);
+  const float fw = __shfl(w, fm ? (int)__builtin_ctzll(fm) : 0, kWave);
+  if (kept) {
+    D[irank] = d;
+    F[irank] = id;
+  }
+  wave_lds_sync();
+  const uint64_t dd = kept ? D[lane] : 0ull;
+  const uint64_t incl = wave_incl_scan_u64(dd);
+  const uint64_t total = readlane_u64(incl, 63);
   uint64_t target = floor_mul(total, u);
   if (target >= total) target = total - 1;
-  const uint64_t hm = ballot(kept && incl - d <= target && incl > target);
-  const uint32_t token = __shfl(tok, hm ? (int)__builtin_ctzll(hm) : 0, kWave);
-  const uint64_t fm = ballot(drafted && kept && tok == draft);
-  const float fw = __shfl(wk, fm ? (int)__builtin_ctzll(fm) : 0, kWave);
+  const uint64_t hm = ballot(kept && incl - dd <= target && incl > target);
+  const uint32_t token = hm ? F[__builtin_ctzll(hm)] : kNoToken;
   if (lane == 0)
-    write_result(a, row, hm ? token : kNoToken,
-                 drafted && fm ? (float)((double)fw / scale) : 0.0f, n3);
+    write_result(a, row, token, drafted && fm ? (float)((double)fw / scale) : 0.0f, n3);
 }
 
 // The exact top-K (K <= 64) of the candidates at or above `thr` that the

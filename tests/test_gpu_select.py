@@ -165,6 +165,29 @@ def test_extra_verify_tokens_and_sparse_draft():
     assert np.any(g["draft_probs"][:rows - 1] > 0)
 
 
+def test_small_topk_with_many_ties_at_the_kth_key():
+    """Rows with top-k <= 64 whose boundary holds hundreds of tied tokens
+    spread over the chunks (the one-wave merge's exact top-k by radix and id
+    descent), plus rows that just fit and just miss its slot budget."""
+    rng = np.random.default_rng(31)
+    V = 70000
+    rows = 6
+    x = rng.normal(0, 1.0, (rows, V)).astype(np.float32)
+    tied = rng.choice(V, 500, replace=False)
+    top = rng.choice(V, 10, replace=False)
+    x[:, tied] = 3.0
+    x[:, top] = 5.0
+    x[3] = np.round(x[3], 1)
+    x[4, :] = np.where(np.arange(V) % 3 == 0, 2.0, -1.0).astype(np.float32)
+    x[5, top] = 7.0
+    pols = [J.policy(temperature=1.0, top_k=20), J.policy(temperature=0.8, top_k=64, top_p=0.7),
+            J.policy(temperature=1.2, top_k=11, min_p=0.01), J.policy(temperature=1.0, top_k=33),
+            J.policy(temperature=1.0, top_k=50), J.policy(temperature=0.5, top_k=12)]
+    u = rng.random(rows).astype(np.float32)
+    g, r = both(V, pols, logits=x, uniforms=u, kept_capacity=64)
+    assert_same(g, r)
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 def test_overflowing_chunks_reselected(bf16):
     """Chunks with more than 1024 candidates (flat or tied values) are
