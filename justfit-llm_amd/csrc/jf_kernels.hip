@@ -45,7 +45,7 @@ constexpr uint32_t kMaxChunks = 64;
 // finds that rank from the bitmap: the rank of its word's first entry plus
 // the entries before it in the word. Extra (draft) tokens the table does
 // not hold have their own bitmap and values by extra index.
-constexpr uint32_t kPenaltySlots = 1024;
+constexpr uint32_t kPenaltySlots = 512;
 struct PrepLds {
   float pvals[kPenaltySlots + 8];  // + the reads past a vector's last entry
   uint32_t pbits[kMaxChunkWords];  // this round's entries
@@ -95,9 +95,11 @@ struct __align__(16) Lds {
 };
 
 // The select kernel's LDS: the chunk's penalty lookup and the reductions.
+constexpr uint32_t kWaveCandidates = kBlockCandidates / kWaves;
 struct __align__(16) SelectLds {
   PrepLds prep;
-  uint32_t ccount;
+  uint64_t stage[kWaves][kWaveCandidates];  // each wave's candidates
+  uint32_t wcount[kWaves];
   uint64_t wj[kWaves][8];
   uint64_t wl[kWaves];
   float wf[kWaves];
@@ -241,6 +243,16 @@ __device__ __forceinline__ uint32_t scalar_load_u32(const uint32_t *p) {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// The select kernel's first round of a chunk's penalized tokens, held by
+// the threads of their table entries: token id and penalized value (NaN when
+// the row does not admit the token). The lanes that hold these tokens drop
+// them, so each token counts once.
+constexpr int kSideEntries = kPenaltySlots / kThreads;
+struct SideEntries {
+  uint32_t tok[kSideEntries];
+  float val[kSideEntries];
+};
+
 // Loads chunk `chunk` of `row`: xs[j*VEC+e] is token
 // chunk*CHUNK + j*SLAB + tid*VEC + e (SLAB = kThreads*VEC: the block's j-th
 // 16-byte loads cover one contiguous slab, so a partial last chunk leaves
@@ -250,11 +262,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // NaN logit is never selected either (greedy comparisons skip it, sampled
 // rows keep no NaN), so one NaN test covers both. Block-uniform control
 // flow: every thread calls it.
-template <int DT, class L>
+template <int DT, bool kSide = false, class L>
 __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
                                            const RowParams &rp, uint32_t row,
                                            uint32_t chunk, L &s,
-                                           float (&xs)[Geo<DT>::TPL]) {
+                                           float (&xs)[Geo<DT>::TPL],
+                                           SideEntries *side = nullptr) {
   constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
                 SLAB = Geo<DT>::SLAB;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
@@ -326,6 +339,13 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
   constexpr uint32_t NWORDS = CHUNK / 32;
   constexpr int EPT = kPenaltySlots / kThreads;  // entries per thread held in registers
   const uint32_t nx = penalized ? rp.extra_count : 0u;
+  if constexpr (kSide) {
+#pragma unroll
+    for (int k = 0; k < kSideEntries; ++k) {
+      side->tok[k] = kNoToken;
+      side->val[k] = kNotAdmitted;
+    }
+  }
   uint32_t lo = 0, hi = 0;
   const uint2 *ent = nullptr;
   uint2 pe[EPT];
@@ -410,13 +430,45 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
     };
     const uint32_t total = hi - lo;
     __syncthreads();  // bitmaps cleared, extras staged
+    if constexpr (kSide) {
+      // The first round's tokens stay with their entries' threads (value
+      // and admission computed there); the lanes holding them drop them.
+      static_assert(EPT == kSideEntries, "one side entry per prefetched entry");
+      const uint32_t *mrow = a.masks + (uint64_t)row * a.mask_stride;
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-      const uint32_t e = tid + k * kThreads;
-      if (e < total) place(pe[k].x, pe[k].y, e);
+      for (int k = 0; k < EPT; ++k) {
+        const uint32_t e = tid + k * kThreads;
+        if (e < total) {
+          const uint32_t t = pe[k].x, o = t - base;
+          atomicOr(&p.pbits[o >> 5], 1u << (o & 31));
+          if (nx) atomicOr(&p.tbits[o >> 5], 1u << (o & 31));
+          float v = value_of(t, pe[k].y);
+          if (constrained && !((mrow[t >> 5] >> (t & 31)) & 1u)) v = kNotAdmitted;
+          if ((rp.flags & kRowExcludeStop) && (t == a.stop0 || t == a.stop1)) v = kNotAdmitted;
+          side->tok[k] = t;
+          side->val[k] = v;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) {
+        const uint32_t o0 = j * SLAB + tid * VEC;
+        const uint32_t nib = (p.pbits[o0 >> 5] >> (o0 & 31)) & VMASK;
+        if (nib) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e)
+            xs[j * VEC + e] = ((nib >> e) & 1u) ? kNotAdmitted : xs[j * VEC + e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) {
+        const uint32_t e = tid + k * kThreads;
+        if (e < total) place(pe[k].x, pe[k].y, e);
+      }
+      __syncthreads();
+      take();
     }
-    __syncthreads();
-    take();
     // More entries than one round holds (a history crowded into this
     // chunk): further rounds, entries read as they go.
     for (uint32_t r0 = kPenaltySlots; r0 < total; r0 += kPenaltySlots) {
@@ -1697,7 +1749,8 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
   const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const RowParams rp = a.params[row];
   float xs[TPL];
-  load_chunk<DT>(a, rp, row, chunk, s, xs);
+  SideEntries side;
+  load_chunk<DT, true>(a, rp, row, chunk, s, xs, &side);
   const uint32_t lane_base = chunk * CHUNK + tid * VEC;
   BlockHeader *hdr = a.headers + (uint64_t)row * S + chunk;
 
@@ -1713,6 +1766,15 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
       const bool take = v > best || (v == best && bid == kNoToken);
       best = take ? v : best;
       bid = take ? lane_base + (i / VEC) * SLAB + (i % VEC) : bid;
+    }
+    // This thread's penalized tokens (held apart, any id order).
+#pragma unroll
+    for (int k = 0; k < kSideEntries; ++k) {
+      const float v = side.val[k];
+      const uint32_t t = side.tok[k];
+      const bool take = v > best || (v == best && (bid == kNoToken || t < bid));
+      best = take ? v : best;
+      bid = take ? t : bid;
     }
     wave_argmax(best, bid);
     if (lane == 0) {
@@ -1737,6 +1799,8 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
     float mx = __builtin_nanf("");
 #pragma unroll
     for (int i = 0; i < TPL; ++i) mx = __builtin_fmaxf(mx, xs[i]);
+#pragma unroll
+    for (int k = 0; k < kSideEntries; ++k) mx = __builtin_fmaxf(mx, side.val[k]);
     const bool any = mx == mx;
     // A bound for the block's top-k: each wave's ceil(k/4)-th largest lane
     // maximum has that many of the wave's tokens at or above it, so the
@@ -1753,7 +1817,6 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
       s.wu[w] = wany;
       s.wu2[w] = wth;
     }
-    if (tid == 0) s.ccount = 0;
     __syncthreads();
     const float bmax = __builtin_fmaxf(
         __builtin_fmaxf(__builtin_fmaxf(s.wf[0], s.wf[1]),
@@ -1765,29 +1828,47 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
     uint32_t thr = tk;
     if (rp.flags & kRowMinP)
       thr = max(thr, logit_key(__builtin_fminf(bmax + rp.minp_offset, bmax)));
-    // Candidates: one compare per 16-byte vector; each hit appends its
-    // (key, id) at a slot from the block's LDS counter. The merge is
-    // independent of the order of the list.
+    // Candidates: each wave appends its hits (raw value, id) to its own
+    // LDS list, at slots counted in scalar registers from the ballots;
+    // then the block writes the lists to the chunk's list in HBM with
+    // their keys. The merge is independent of the order of the list.
     const float tv = thr <= kLowestKey ? -__builtin_inff() : key_logit(thr);
-    uint64_t *dst = a.cands + ((uint64_t)row * S + chunk) * kBlockCandidates;
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-      float vm = xs[j * VEC];
-#pragma unroll
-      for (int e = 1; e < VEC; ++e) vm = __builtin_fmaxf(vm, xs[j * VEC + e]);
-      if (vm >= tv) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e)
-          if (xs[j * VEC + e] >= tv) {
-            const uint32_t slot = atomicAdd(&s.ccount, 1u);
-            if (slot < (uint32_t)kBlockCandidates)
-              dst[slot] = (uint64_t)logit_key(xs[j * VEC + e]) |
-                          ((uint64_t)(lane_base + j * SLAB + e) << 32);
-          }
+    uint64_t *stage = s.stage[w];
+    uint32_t run = 0;
+    auto emit = [&](float x, uint32_t token) {
+      const bool hit = x >= tv;
+      const uint64_t m = ballot(hit);
+      if (m) {
+        const uint32_t slot = run + mbcnt(m);
+        if (hit && slot < kWaveCandidates)
+          stage[slot] = (uint64_t)f2u(x) | ((uint64_t)token << 32);
+        run += (uint32_t)__popcll(m);
       }
-    }
+    };
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) emit(xs[j * VEC + e], lane_base + j * SLAB + e);
+#pragma unroll
+    for (int k = 0; k < kSideEntries; ++k) emit(side.val[k], side.tok[k]);
+    if (lane == 0) s.wcount[w] = run;
     __syncthreads();
-    const uint32_t c = s.ccount;
+    uint32_t off[kWaves + 1], over = 0;
+    off[0] = 0;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) {
+      const uint32_t n = s.wcount[k];
+      over |= n > kWaveCandidates;
+      off[k + 1] = off[k] + min(n, kWaveCandidates);
+    }
+    uint64_t *dst = a.cands + ((uint64_t)row * S + chunk) * kBlockCandidates;
+    if (!over)
+      for (uint32_t i = tid; i < off[kWaves]; i += kThreads) {
+        const uint32_t k = (i >= off[1]) + (i >= off[2]) + (i >= off[3]);
+        const uint64_t e = s.stage[k][i - off[k]];
+        dst[i] = (uint64_t)logit_key(u2f((uint32_t)e)) | (e & 0xffffffff00000000ull);
+      }
+    const uint32_t c = over ? kBlockCandidates + 1 : off[kWaves];
     if (tid == 0) {
       // More candidates than the list holds: the merge selects this chunk
       // again (with the row's own thresholds) or hands the row to the
