@@ -47,6 +47,14 @@ def build(verbose: bool = True) -> str:
     if err.strip() and verbose:
         sys.stderr.write(err + "\n")
     os.replace(tmp, OUT)
+    # The read-ceiling probe of bench.py (measurement support, its own library).
+    probe = os.path.join(HERE, "jf_sampler", "libjf_read_probe.so")
+    cmd = [HIPCC] + FLAGS + ["-o", probe + ".tmp", os.path.join(CSRC, "read_probe.hip")]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stderr + "\n")
+        raise RuntimeError("hipcc failed building libjf_read_probe.so")
+    os.replace(probe + ".tmp", probe)
     return OUT
 
 
