@@ -152,6 +152,33 @@ enum Stage : uint32_t {
   kStageLast = 19,
 };
 
+// Classes of stages that share code (one stage-kernel build each).
+enum StageClass : int {
+  kClsCount = 0,     // kStageCount1
+  kClsDigits = 1,    // radix digits of the k-th key and of the nucleus
+  kClsTie = 2,       // ties at the boundary key
+  kClsLocate = 3,    // the boundary token inside one chunk
+  kClsMass = 4,      // kStageMass2, kStageMass3, kStageKeptCount
+  kClsDraw = 5,
+  kClsWalk = 6,
+  kClsKeptWrite = 7,
+  kClsNone = 8,
+};
+__host__ __device__ constexpr int stage_class(uint32_t stage) {
+  return stage == kStageCount1 ? kClsCount
+         : (stage >= kStageTopK3 && stage <= kStageTopK0) ||
+                   (stage >= kStageTopP3 && stage <= kStageTopP0)
+             ? kClsDigits
+         : stage == kStageTopKTie || stage == kStageTopPTie       ? kClsTie
+         : stage == kStageTopKLocate || stage == kStageTopPLocate ? kClsLocate
+         : stage == kStageMass2 || stage == kStageMass3 || stage == kStageKeptCount
+             ? kClsMass
+         : stage == kStageDraw      ? kClsDraw
+         : stage == kStageWalk      ? kClsWalk
+         : stage == kStageKeptWrite ? kClsKeptWrite
+                                    : kClsNone;
+}
+
 struct AcceptChainLane {
   uint32_t remaining;
   uint32_t sampled;

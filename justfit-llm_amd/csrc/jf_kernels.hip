@@ -1895,7 +1895,9 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(SampleLaunch a) {
 
 // ---- multi-pass stages ---------------------------------------------------
 
-template <int DT>
+// The stage kernel is compiled once per class of stages, so each launch
+// carries only its stage's code and registers.
+template <int DT, int CLS>
 __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
   constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
                 LOADS = Geo<DT>::LOADS;
@@ -1906,6 +1908,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
   const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
   const uint32_t tid = threadIdx.x;
   const uint32_t stage = a.stage;
+  if (stage_class(stage) != CLS) return;
   RowState st = a.states[row];
   if (st.stage != stage) return;
   const bool single = stage == kStageTopKLocate || stage == kStageTopPLocate ||
@@ -1961,12 +1964,15 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
 
   switch (stage) {
     case kStageCount1: {
+      if constexpr (CLS == kClsCount) {
       const uint32_t c = block_sum_u32(__popcll(mem), s);
       if (tid == 0) st_dev(&part->v[0], (uint64_t)c);
+      }
       break;
     }
     case kStageTopK3: case kStageTopK3 + 1: case kStageTopK3 + 2: case kStageTopK0:
     case kStageTopP3: case kStageTopP3 + 1: case kStageTopP3 + 2: case kStageTopP0: {
+      if constexpr (CLS == kClsDigits) {
       const bool by_mass = stage >= kStageTopP3;
       const int d = by_mass ? (int)(kStageTopP0 - stage) : (int)(kStageTopK0 - stage);
       s.hist[tid] = 0;
@@ -1982,16 +1988,19 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       }
       __syncthreads();
       st_dev(&part->v[tid], s.hist[tid]);
+      }
       break;
     }
     case kStageTopKTie:
     case kStageTopPTie: {
+      if constexpr (CLS == kClsTie) {
       uint32_t c = 0;
 #pragma unroll
       for (int i = 0; i < TPL; ++i)
         c += ((mem >> i) & 1) && logit_key(xs[i]) == st.tie_key;
       c = block_sum_u32(c, s);
       if (tid == 0) st_dev(&part->v[0], (uint64_t)c);
+      }
       break;
     }
     case kStageTopKLocate:
@@ -2000,6 +2009,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     case kStageMass2:
     case kStageMass3:
     case kStageKeptCount: {
+      if constexpr (CLS == kClsMass) {
       uint64_t sum = 0;
       uint32_t c = 0;
       if (tid == 0) {
@@ -2028,9 +2038,11 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
         st_dev(&part->v[1], (uint64_t)s.u32a);
         st_dev(&part->v[2], (uint64_t)__float_as_uint(s.found_w));
       }
+      }
       break;
     }
     case kStageDraw: {
+      if constexpr (CLS == kClsDraw) {
       uint64_t dsum = 0, wsum = 0;
       uint32_t any = 0;
 #pragma unroll
@@ -2052,9 +2064,11 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
         st_dev(&part->v[1], wsum);
         st_dev(&part->v[2], (uint64_t)any);
       }
+      }
       break;
     }
     case kStageKeptWrite: {
+      if constexpr (CLS == kClsKeptWrite) {
       // Offset of this chunk: the kept counts of the chunks before it.
       uint64_t off = 0;
       for (uint32_t c = 0; c < chunk; ++c) off += a.partials[(uint64_t)row * S + c].v[0];
@@ -2079,12 +2093,14 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
             ++idx;
           }
       }
+      }
       break;
     }
     default:
       break;
   }
 
+  if constexpr (CLS == kClsLocate) {
   if (stage == kStageTopKLocate || stage == kStageTopPLocate) {
     // The within-th tie of this chunk closes the kept set.
     uint64_t ties = 0;
@@ -2093,7 +2109,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       if (((mem >> i) & 1) && logit_key(xs[i]) == st.tie_key) ties |= 1ull << i;
     const uint32_t id = locate(ties, st.within);
     if (tid == 0) {
-      RowState ns = st;
+      RowState &ns = a.states[row];
       ns.bkey = st.tie_key;
       ns.bid = id;
       ns.prefix = 0;
@@ -2102,10 +2118,11 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
         ns.stage = kStageMass2;
       else
         ns.stage = kStageMass3;
-      a.states[row] = ns;
     }
     return;
   }
+  }
+  if constexpr (CLS == kClsWalk) {
   if (stage == kStageWalk) {
     // The draw inside the chosen chunk: the first member whose running
     // weight exceeds the remaining target.
@@ -2142,17 +2159,18 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       const double scale = (double)st.mass3 * 0x1p-44;
       write_result(a, row, s.hit,
                    st.drafted ? (float)((double)st.draft_w / scale) : 0.0f, 0);
-      RowState ns = st;
+      RowState &ns = a.states[row];
       ns.stage = a.out_kept_ids ? kStageKeptCount : kStageDone;
-      a.states[row] = ns;
     }
     return;
+  }
   }
 
   if (!arrive_last(a.counters + row, S, s)) return;
 
   // Finalize the stage for this row.
   const StagePartial *parts = a.partials + (uint64_t)row * S;
+  if constexpr (CLS == kClsDigits) {
   if ((stage >= kStageTopK3 && stage <= kStageTopK0) ||
       (stage >= kStageTopP3 && stage <= kStageTopP0)) {
     uint64_t h = 0;
@@ -2163,7 +2181,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     if (tid == 0) {
       const bool by_mass = stage >= kStageTopP3;
       const int d = by_mass ? (int)(kStageTopP0 - stage) : (int)(kStageTopK0 - stage);
-      RowState ns = st;
+      RowState &ns = a.states[row];
       ns.remaining = st.remaining - s.sel_excl;
       ns.prefix = st.prefix | (s.sel_bin << (8 * d));
       ns.pmask = st.pmask | (255u << (8 * d));
@@ -2180,14 +2198,15 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
           ns.stage = kStageTopKTie;
         }
       }
-      a.states[row] = ns;
     }
     return;
   }
+  }
   if (tid != 0) return;
-  RowState ns = st;
+  RowState &ns = a.states[row];
   switch (stage) {
     case kStageCount1: {
+      if constexpr (CLS == kClsCount) {
       uint64_t n1 = 0;
       for (uint32_t c = 0; c < S; ++c) n1 += ld_dev(&parts[c].v[0]);
       ns.n1 = n1;
@@ -2197,10 +2216,12 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       } else {
         ns.stage = (rp.flags & kRowTopP) ? kStageMass2 : kStageMass3;
       }
+      }
       break;
     }
     case kStageTopKTie:
     case kStageTopPTie: {
+      if constexpr (CLS == kClsTie) {
       uint64_t cum = 0;
       uint32_t c = 0;
       for (; c < S; ++c) {
@@ -2211,9 +2232,11 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       ns.chunk = c < S ? c : S - 1;
       ns.within = st.remaining - cum - 1;
       ns.stage = stage == kStageTopKTie ? kStageTopKLocate : kStageTopPLocate;
+      }
       break;
     }
     case kStageMass2: {
+      if constexpr (CLS == kClsMass) {
       uint64_t mass = 0;
       for (uint32_t c = 0; c < S; ++c) mass += ld_dev(&parts[c].v[0]);
       ns.mass2 = mass;
@@ -2226,9 +2249,11 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
         ns.pmask = 0;
         ns.stage = kStageTopP3;
       }
+      }
       break;
     }
     case kStageMass3: {
+      if constexpr (CLS == kClsMass) {
       uint64_t mass = 0;
       for (uint32_t c = 0; c < S; ++c) {
         mass += ld_dev(&parts[c].v[0]);
@@ -2241,9 +2266,11 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       } else {
         ns.stage = kStageDraw;
       }
+      }
       break;
     }
     case kStageDraw: {
+      if constexpr (CLS == kClsDraw) {
       uint32_t any = 0;
       for (uint32_t c = 0; c < S; ++c) any |= (uint32_t)ld_dev(&parts[c].v[2]);
       const bool residual = st.drafted && any;
@@ -2263,13 +2290,16 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       ns.within = target - cum;
       ns.target = target;
       ns.stage = kStageWalk;
+      }
       break;
     }
     case kStageKeptCount: {
+      if constexpr (CLS == kClsMass) {
       uint64_t kept = 0;
       for (uint32_t c = 0; c < S; ++c) kept += ld_dev(&parts[c].v[0]);
       if (a.out_kept_counts) a.out_kept_counts[row] = (uint32_t)kept;
       ns.stage = kStageKeptWrite;
+      }
       break;
     }
     case kStageKeptWrite:
@@ -2278,7 +2308,6 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     default:
       break;
   }
-  a.states[row] = ns;
 }
 
 // ---- acceptance --------------------------------------------------------
@@ -2407,10 +2436,29 @@ int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream) {
 
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream) {
   const dim3 grid(a.rows * a.chunks), block(kThreads);
-  if (dtype == 0)
-    hipLaunchKernelGGL(stage_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
-  else
-    hipLaunchKernelGGL(stage_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+  const hipStream_t st = (hipStream_t)stream;
+  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, st, a); };
+  const int cls = stage_class(a.stage);
+#define JF_STAGE_CASE(C)                              \
+  case C:                                             \
+    if (dtype == 0)                                   \
+      go(stage_kernel<0, C>);                         \
+    else                                              \
+      go(stage_kernel<1, C>);                         \
+    break;
+  switch (cls) {
+    JF_STAGE_CASE(kClsCount)
+    JF_STAGE_CASE(kClsDigits)
+    JF_STAGE_CASE(kClsTie)
+    JF_STAGE_CASE(kClsLocate)
+    JF_STAGE_CASE(kClsMass)
+    JF_STAGE_CASE(kClsDraw)
+    JF_STAGE_CASE(kClsWalk)
+    JF_STAGE_CASE(kClsKeptWrite)
+    default:
+      return (int)hipErrorInvalidValue;
+  }
+#undef JF_STAGE_CASE
   return (int)hipGetLastError();
 }
 
