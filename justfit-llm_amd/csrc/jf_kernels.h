@@ -129,6 +129,7 @@ struct SampleLaunch {
   uint32_t *out_kept_ids;
   float *out_kept_probs;
   uint32_t kept_cap;
+  uint32_t q_aligned;     // dense q rows start on 16-byte boundaries
 };
 
 // Multi-pass stages, in launch order.
@@ -144,9 +145,9 @@ enum Stage : uint32_t {
   kStageTopP0 = 12,
   kStageTopPTie = 13,
   kStageTopPLocate = 14,
-  kStageMass3 = 15,
-  kStageDraw = 16,
-  kStageWalk = 17,
+  kStageMass3 = 15,     // picks the draw's chunk for a row without a draft
+  kStageDraw = 16,      // drafted rows: residual masses, the draw's chunk
+  kStageWalk = 17,      // one block per row: the draw inside its chunk
   kStageKeptCount = 18,
   kStageKeptWrite = 19,
   kStageLast = 19,
@@ -160,8 +161,8 @@ enum StageClass : int {
   kClsLocate = 3,    // the boundary token inside one chunk
   kClsMass = 4,      // kStageMass2, kStageMass3, kStageKeptCount
   kClsDraw = 5,
-  kClsWalk = 6,
-  kClsKeptWrite = 7,
+  kClsKeptWrite = 6,
+  kClsWalk = 7,      // walk_kernel, not a stage_kernel build
   kClsNone = 8,
 };
 __host__ __device__ constexpr int stage_class(uint32_t stage) {
@@ -174,8 +175,8 @@ __host__ __device__ constexpr int stage_class(uint32_t stage) {
          : stage == kStageMass2 || stage == kStageMass3 || stage == kStageKeptCount
              ? kClsMass
          : stage == kStageDraw      ? kClsDraw
-         : stage == kStageWalk      ? kClsWalk
          : stage == kStageKeptWrite ? kClsKeptWrite
+         : stage == kStageWalk      ? kClsWalk
                                     : kClsNone;
 }
 

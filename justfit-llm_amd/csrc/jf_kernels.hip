@@ -1895,6 +1895,119 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(SampleLaunch a) {
 
 // ---- multi-pass stages ---------------------------------------------------
 
+// A drafted row's dense q over this thread's tokens of a chunk, in the
+// order of the chunk's logits; 16-byte loads when the rows are aligned.
+template <int DT>
+__device__ __forceinline__ void load_dense_q(const SampleLaunch &a, uint32_t row,
+                                             uint32_t chunk,
+                                             float (&qv)[Geo<DT>::TPL]) {
+  constexpr int VEC = Geo<DT>::VEC, SLAB = Geo<DT>::SLAB, LOADS = Geo<DT>::LOADS;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  const uint32_t lane_base = chunk * CHUNK + threadIdx.x * VEC;
+  const float *q = a.dense_q + (uint64_t)row * a.q_stride;
+  if (a.q_aligned && chunk * CHUNK + CHUNK <= a.vocabulary) {
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j)
+#pragma unroll
+      for (int h = 0; h < VEC / 4; ++h) {
+        const float4 f = *reinterpret_cast<const float4 *>(q + lane_base + j * SLAB + 4 * h);
+        qv[j * VEC + 4 * h + 0] = f.x;
+        qv[j * VEC + 4 * h + 1] = f.y;
+        qv[j * VEC + 4 * h + 2] = f.z;
+        qv[j * VEC + 4 * h + 3] = f.w;
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const uint32_t t = lane_base + j * SLAB + e;
+        qv[j * VEC + e] = t < a.vocabulary ? q[t] : 0.0f;
+      }
+  }
+}
+
+// The draw inside chunk `c` of a row: the first member, in id order, whose
+// running weight (the residual weight when `residual`) passes `within`
+// (sampling.metal:790-829 walks the whole row the same way). Members are the
+// admitted tokens at or above `thr_key` and at or before the kept boundary
+// (bkey, bid). Every thread of the block calls it; every thread gets the
+// token.
+template <int DT>
+__device__ __forceinline__ uint32_t walk_chunk(const SampleLaunch &a, const RowParams &rp,
+                                               uint32_t row, uint32_t c, float M,
+                                               uint32_t thr_key, uint32_t bkey, uint32_t bid,
+                                               bool residual, uint64_t mass3,
+                                               uint64_t within, Lds &s) {
+  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
+                LOADS = Geo<DT>::LOADS;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  // A dense draft row is requested ahead of the chunk's logits.
+  const bool dq = residual && a.dense_q;
+  float qv[TPL];
+  if (dq) load_dense_q<DT>(a, row, c, qv);
+  float xs[TPL];
+  load_chunk<DT>(a, rp, row, c, s, xs);
+  const uint32_t lane_base = c * CHUNK + threadIdx.x * VEC;
+  const float inv_t = rp.inv_t;
+  auto tok = [&](int i) -> uint32_t {
+    return lane_base + (i / VEC) * SLAB + (i % VEC);
+  };
+  auto d_of = [&](float v, float q, uint32_t t) -> uint64_t {
+    if (v != v) return 0;
+    const uint32_t k = logit_key(v);
+    if (k < thr_key || !at_or_before(k, t, bkey, bid)) return 0;
+    const uint64_t wq = quantize(weight_of(v, M, inv_t));
+    return residual ? residual_of(wq, mass3, dq ? q : draft_q(a, row, t, s)) : wq;
+  };
+  uint64_t lsum[LOADS], offs[LOADS];
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    lsum[j] = 0;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e)
+      lsum[j] += d_of(xs[j * VEC + e], dq ? qv[j * VEC + e] : 0.0f, tok(j * VEC + e));
+  }
+  if (threadIdx.x == 0) s.hit = kNoToken;
+  order_offsets<LOADS>(lsum, offs, s);
+  // The load whose range holds `within` recomputes its weights: its VEC
+  // values are picked out first, so only VEC weights are live at once.
+  int jsel = -1;
+  uint64_t acc = 0;
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j)
+    if (offs[j] <= within && offs[j] + lsum[j] > within) {
+      jsel = j;
+      acc = offs[j];
+    }
+  if (jsel >= 0) {
+    float xv[VEC], qq[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) xv[e] = qq[e] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        if (j == jsel) {
+          xv[e] = xs[j * VEC + e];
+          if (dq) qq[e] = qv[j * VEC + e];
+        }
+    const uint32_t tbase = lane_base + (uint32_t)jsel * SLAB;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const uint32_t t = tbase + e;
+      const uint64_t d = d_of(xv[e], qq[e], t);
+      if (d && acc + d > within) {
+        s.hit = t;
+        break;
+      }
+      acc += d;
+    }
+  }
+  __syncthreads();
+  return s.hit;
+}
+
 // The stage kernel is compiled once per class of stages, so each launch
 // carries only its stage's code and registers.
 template <int DT, int CLS>
@@ -1909,12 +2022,16 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
   const uint32_t tid = threadIdx.x;
   const uint32_t stage = a.stage;
   if (stage_class(stage) != CLS) return;
+  // The row's parameters are requested with its state, in one round trip.
+  const RowParams rp = a.params[row];
   RowState st = a.states[row];
   if (st.stage != stage) return;
-  const bool single = stage == kStageTopKLocate || stage == kStageTopPLocate ||
-                      stage == kStageWalk;
+  const bool single = stage == kStageTopKLocate || stage == kStageTopPLocate;
   if (single && chunk != st.chunk) return;
-  const RowParams rp = a.params[row];
+  // The draw stage's dense q is requested ahead of the chunk's logits.
+  float qv[CLS == kClsDraw ? TPL : 1];
+  if constexpr (CLS == kClsDraw)
+    if (a.dense_q) load_dense_q<DT>(a, row, chunk, qv);
   float xs[TPL];
   load_chunk<DT>(a, rp, row, chunk, s, xs);
   stage_candidates(a, row, s);
@@ -2051,7 +2168,8 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
           const uint64_t wq = wq_of(i);
           wsum += wq;
           if (st.drafted) {
-            const uint64_t d = residual_of(wq, st.mass3, draft_q(a, row, tok_of(i), s));
+            const float q = a.dense_q ? qv[i] : draft_q(a, row, tok_of(i), s);
+            const uint64_t d = residual_of(wq, st.mass3, q);
             dsum += d;
             any |= d > 0;
           }
@@ -2122,50 +2240,6 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     return;
   }
   }
-  if constexpr (CLS == kClsWalk) {
-  if (stage == kStageWalk) {
-    // The draw inside the chosen chunk: the first member whose running
-    // weight exceeds the remaining target.
-    uint64_t dl[TPL];
-#pragma unroll
-    for (int i = 0; i < TPL; ++i) {
-      dl[i] = 0;
-      if ((mem >> i) & 1) {
-        const uint64_t wq = wq_of(i);
-        dl[i] = st.residual ? residual_of(wq, st.mass3, draft_q(a, row, tok_of(i), s)) : wq;
-      }
-    }
-    if (tid == 0) s.hit = kNoToken;
-    uint64_t lsum[LOADS], offs[LOADS];
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-      lsum[j] = 0;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) lsum[j] += dl[j * VEC + e];
-    }
-    order_offsets<LOADS>(lsum, offs, s);
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-      uint64_t acc = offs[j];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const uint64_t d = dl[j * VEC + e];
-        if (d && acc <= st.within && acc + d > st.within) s.hit = tok_of(j * VEC + e);
-        acc += d;
-      }
-    }
-    __syncthreads();
-    if (tid == 0) {
-      const double scale = (double)st.mass3 * 0x1p-44;
-      write_result(a, row, s.hit,
-                   st.drafted ? (float)((double)st.draft_w / scale) : 0.0f, 0);
-      RowState &ns = a.states[row];
-      ns.stage = a.out_kept_ids ? kStageKeptCount : kStageDone;
-    }
-    return;
-  }
-  }
-
   if (!arrive_last(a.counters + row, S, s)) return;
 
   // Finalize the stage for this row.
@@ -2263,8 +2337,24 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       if (mass == 0) {
         write_result(a, row, kNoToken, 0.0f, 0);
         ns.stage = a.out_kept_ids ? kStageKeptCount : kStageDone;
-      } else {
+      } else if (st.drafted) {
         ns.stage = kStageDraw;
+      } else {
+        // Without a draft the chunk masses already place the draw.
+        uint64_t target = floor_mul(mass, row_uniform(a, row));
+        if (target >= mass) target = mass - 1;
+        uint64_t cum = 0;
+        uint32_t c = 0;
+        for (; c < S; ++c) {
+          const uint64_t t = ld_dev(&parts[c].v[0]);
+          if (cum + t > target) break;
+          cum += t;
+        }
+        ns.residual = 0;
+        ns.chunk = c < S ? c : S - 1;
+        ns.within = target - cum;
+        ns.target = target;
+        ns.stage = kStageWalk;
       }
       }
       break;
@@ -2275,7 +2365,8 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       for (uint32_t c = 0; c < S; ++c) any |= (uint32_t)ld_dev(&parts[c].v[2]);
       const bool residual = st.drafted && any;
       uint64_t total = 0;
-      for (uint32_t c = 0; c < S; ++c) total += residual ? ld_dev(&parts[c].v[0]) : ld_dev(&parts[c].v[1]);
+      for (uint32_t c = 0; c < S; ++c)
+        total += residual ? ld_dev(&parts[c].v[0]) : ld_dev(&parts[c].v[1]);
       uint64_t target = floor_mul(total, row_uniform(a, row));
       if (target >= total) target = total - 1;
       uint64_t cum = 0;
@@ -2307,6 +2398,26 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       break;
     default:
       break;
+  }
+}
+
+// The draw inside the chunk the row's last stage chose: one block per row.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void walk_kernel(SampleLaunch a) {
+  __shared__ Lds s;
+  const uint32_t row = blockIdx.x;
+  const RowParams rp = a.params[row];
+  const RowState st = a.states[row];
+  if (st.stage != kStageWalk) return;
+  stage_candidates(a, row, s);
+  const uint32_t hit = walk_chunk<DT>(a, rp, row, st.chunk, st.maximum, st.thr_key,
+                                      st.bkey, st.bid, st.residual != 0, st.mass3,
+                                      st.within, s);
+  if (threadIdx.x == 0) {
+    const double scale = (double)st.mass3 * 0x1p-44;
+    write_result(a, row, hit,
+                 st.drafted ? (float)((double)st.draft_w / scale) : 0.0f, 0);
+    a.states[row].stage = a.out_kept_ids ? kStageKeptCount : kStageDone;
   }
 }
 
@@ -2439,6 +2550,13 @@ int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream) {
   const hipStream_t st = (hipStream_t)stream;
   auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, st, a); };
   const int cls = stage_class(a.stage);
+  if (cls == kClsWalk) {
+    if (dtype == 0)
+      hipLaunchKernelGGL(walk_kernel<0>, dim3(a.rows), block, 0, st, a);
+    else
+      hipLaunchKernelGGL(walk_kernel<1>, dim3(a.rows), block, 0, st, a);
+    return (int)hipGetLastError();
+  }
 #define JF_STAGE_CASE(C)                              \
   case C:                                             \
     if (dtype == 0)                                   \
@@ -2453,7 +2571,6 @@ int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream) {
     JF_STAGE_CASE(kClsLocate)
     JF_STAGE_CASE(kClsMass)
     JF_STAGE_CASE(kClsDraw)
-    JF_STAGE_CASE(kClsWalk)
     JF_STAGE_CASE(kClsKeptWrite)
     default:
       return (int)hipErrorInvalidValue;

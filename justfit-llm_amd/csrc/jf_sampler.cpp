@@ -548,6 +548,10 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   L.out_kept_ids = a->out_kept_ids;
   L.out_kept_probs = a->out_kept_probs;
   L.kept_cap = a->kept_capacity;
+  L.q_aligned = a->draft_q && (uintptr_t)a->draft_q % 16 == 0 &&
+                        (a->draft_q_stride * sizeof(float)) % 16 == 0
+                    ? 1u
+                    : 0u;
 
   if ((a->select_start_event == nullptr) != (a->select_done_event == nullptr))
     return fail(JF_ERR_INVALID_ARGUMENT, "select events come in pairs");
@@ -561,6 +565,7 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
       if (stage == jf::kStageCount1 && !need_count1) continue;
       if (stage >= jf::kStageTopK3 && stage <= jf::kStageTopKLocate && !need_topk) continue;
       if (stage >= jf::kStageMass2 && stage <= jf::kStageTopPLocate && !need_topp) continue;
+      if (stage == jf::kStageDraw && !L.drafted_rows) continue;
       if (stage >= jf::kStageKeptCount && !kept) continue;
       L.stage = stage;
       e = jf::launch_stage(L, a->dtype, stream);
