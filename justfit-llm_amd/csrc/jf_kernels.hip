@@ -2242,13 +2242,21 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
   }
   if (!arrive_last(a.counters + row, S, s)) return;
 
-  // Finalize the stage for this row.
+  // Finalize the stage for this row. The chunks' partials are read with
+  // every load in flight at once: a runtime loop of device-coherent loads
+  // would wait a round trip per chunk.
   const StagePartial *parts = a.partials + (uint64_t)row * S;
   if constexpr (CLS == kClsDigits) {
   if ((stage >= kStageTopK3 && stage <= kStageTopK0) ||
       (stage >= kStageTopP3 && stage <= kStageTopP0)) {
     uint64_t h = 0;
-    for (uint32_t c = 0; c < S; ++c) h += ld_dev(&parts[c].v[tid]);
+    for (uint32_t c0 = 0; c0 < S; c0 += 8) {
+      uint64_t t[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) t[k] = ld_dev(&parts[min(c0 + k, S - 1)].v[tid]);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) h += c0 + k < S ? t[k] : 0ull;
+    }
     s.hist[tid] = h;
     __syncthreads();
     crossing_bin(s, st.remaining);
@@ -2276,19 +2284,44 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     return;
   }
   }
-  if (tid != 0) return;
+  // The other stages: wave 0, one lane per chunk (S <= 64).
+  if (tid >= 64) return;
+  const bool in = tid < S;
+  const StagePartial *pl = parts + min(tid, S - 1);
+  auto lane_v = [&](int f) -> uint64_t {
+    const uint64_t v = ld_dev(&pl->v[f]);
+    return in ? v : 0ull;
+  };
+  // The first chunk whose running total passes `target` (strictly when
+  // `strict`), and the total before it; the last chunk and the whole total
+  // when none does.
+  auto pick = [&](uint64_t v, uint64_t target, bool strict, uint32_t &chunk_out,
+                  uint64_t &before) {
+    const uint64_t incl = wave_incl_scan_u64(v);
+    const uint64_t m = ballot(in && (strict ? incl > target : incl >= target));
+    if (m) {
+      const int c = (int)__builtin_ctzll(m);
+      chunk_out = (uint32_t)c;
+      before = readlane_u64(incl - v, c);
+    } else {
+      chunk_out = S - 1;
+      before = readlane_u64(incl, 63);
+    }
+  };
   RowState &ns = a.states[row];
+  const bool lead = tid == 0;
   switch (stage) {
     case kStageCount1: {
       if constexpr (CLS == kClsCount) {
-      uint64_t n1 = 0;
-      for (uint32_t c = 0; c < S; ++c) n1 += ld_dev(&parts[c].v[0]);
-      ns.n1 = n1;
-      if (rp.top_k < n1) {
-        ns.stage = kStageTopK3;
-        ns.remaining = rp.top_k;
-      } else {
-        ns.stage = (rp.flags & kRowTopP) ? kStageMass2 : kStageMass3;
+      const uint64_t n1 = wave_sum_u64(lane_v(0));
+      if (lead) {
+        ns.n1 = n1;
+        if (rp.top_k < n1) {
+          ns.stage = kStageTopK3;
+          ns.remaining = rp.top_k;
+        } else {
+          ns.stage = (rp.flags & kRowTopP) ? kStageMass2 : kStageMass3;
+        }
       }
       }
       break;
@@ -2296,62 +2329,84 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     case kStageTopKTie:
     case kStageTopPTie: {
       if constexpr (CLS == kClsTie) {
-      uint64_t cum = 0;
-      uint32_t c = 0;
-      for (; c < S; ++c) {
-        const uint64_t t = ld_dev(&parts[c].v[0]);
-        if (cum + t >= st.remaining) break;
-        cum += t;
+      uint32_t c;
+      uint64_t cum;
+      pick(lane_v(0), st.remaining, false, c, cum);
+      if (lead) {
+        ns.chunk = c;
+        ns.within = st.remaining - cum - 1;
+        ns.stage = stage == kStageTopKTie ? kStageTopKLocate : kStageTopPLocate;
       }
-      ns.chunk = c < S ? c : S - 1;
-      ns.within = st.remaining - cum - 1;
-      ns.stage = stage == kStageTopKTie ? kStageTopKLocate : kStageTopPLocate;
       }
       break;
     }
     case kStageMass2: {
       if constexpr (CLS == kClsMass) {
-      uint64_t mass = 0;
-      for (uint32_t c = 0; c < S; ++c) mass += ld_dev(&parts[c].v[0]);
-      ns.mass2 = mass;
-      if (mass == 0) {
-        ns.stage = kStageMass3;
-      } else {
-        ns.nucleus = floor_mul(mass, rp.top_p);
-        ns.remaining = ns.nucleus + 1;
-        ns.prefix = 0;
-        ns.pmask = 0;
-        ns.stage = kStageTopP3;
+      const uint64_t mass = wave_sum_u64(lane_v(0));
+      if (lead) {
+        ns.mass2 = mass;
+        if (mass == 0) {
+          ns.stage = kStageMass3;
+        } else {
+          ns.nucleus = floor_mul(mass, rp.top_p);
+          ns.remaining = ns.nucleus + 1;
+          ns.prefix = 0;
+          ns.pmask = 0;
+          ns.stage = kStageTopP3;
+        }
       }
       }
       break;
     }
     case kStageMass3: {
       if constexpr (CLS == kClsMass) {
-      uint64_t mass = 0;
-      for (uint32_t c = 0; c < S; ++c) {
-        mass += ld_dev(&parts[c].v[0]);
-        if (ld_dev(&parts[c].v[1])) ns.draft_w = __uint_as_float((uint32_t)ld_dev(&parts[c].v[2]));
-      }
-      ns.mass3 = mass;
-      if (mass == 0) {
-        write_result(a, row, kNoToken, 0.0f, 0);
-        ns.stage = a.out_kept_ids ? kStageKeptCount : kStageDone;
-      } else if (st.drafted) {
-        ns.stage = kStageDraw;
-      } else {
+      const uint64_t v0 = lane_v(0), v1 = lane_v(1), v2 = lane_v(2);
+      const uint64_t mass = wave_sum_u64(v0);
+      // The chunk holding the draft token reports its weight.
+      const uint64_t fm = ballot(v1 != 0);
+      const uint32_t fw = fm ? (uint32_t)readlane_u64(v2, 63 - __builtin_clzll(fm)) : 0u;
+      uint32_t c = 0;
+      uint64_t cum = 0, target = 0;
+      const bool walk = mass != 0 && !st.drafted;
+      if (walk) {
         // Without a draft the chunk masses already place the draw.
-        uint64_t target = floor_mul(mass, row_uniform(a, row));
+        target = floor_mul(mass, row_uniform(a, row));
         if (target >= mass) target = mass - 1;
-        uint64_t cum = 0;
-        uint32_t c = 0;
-        for (; c < S; ++c) {
-          const uint64_t t = ld_dev(&parts[c].v[0]);
-          if (cum + t > target) break;
-          cum += t;
+        pick(v0, target, true, c, cum);
+      }
+      if (lead) {
+        if (fm) ns.draft_w = __uint_as_float(fw);
+        ns.mass3 = mass;
+        if (mass == 0) {
+          write_result(a, row, kNoToken, 0.0f, 0);
+          ns.stage = a.out_kept_ids ? kStageKeptCount : kStageDone;
+        } else if (st.drafted) {
+          ns.stage = kStageDraw;
+        } else {
+          ns.residual = 0;
+          ns.chunk = c;
+          ns.within = target - cum;
+          ns.target = target;
+          ns.stage = kStageWalk;
         }
-        ns.residual = 0;
-        ns.chunk = c < S ? c : S - 1;
+      }
+      }
+      break;
+    }
+    case kStageDraw: {
+      if constexpr (CLS == kClsDraw) {
+      const uint64_t v0 = lane_v(0), v1 = lane_v(1), v2 = lane_v(2);
+      const bool residual = st.drafted && ballot(v2 != 0) != 0;
+      const uint64_t v = residual ? v0 : v1;
+      const uint64_t total = wave_sum_u64(v);
+      uint64_t target = floor_mul(total, row_uniform(a, row));
+      if (target >= total) target = total - 1;
+      uint32_t c;
+      uint64_t cum;
+      pick(v, target, true, c, cum);
+      if (lead) {
+        ns.residual = residual ? 1u : 0u;
+        ns.chunk = c;
         ns.within = target - cum;
         ns.target = target;
         ns.stage = kStageWalk;
@@ -2359,42 +2414,18 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       }
       break;
     }
-    case kStageDraw: {
-      if constexpr (CLS == kClsDraw) {
-      uint32_t any = 0;
-      for (uint32_t c = 0; c < S; ++c) any |= (uint32_t)ld_dev(&parts[c].v[2]);
-      const bool residual = st.drafted && any;
-      uint64_t total = 0;
-      for (uint32_t c = 0; c < S; ++c)
-        total += residual ? ld_dev(&parts[c].v[0]) : ld_dev(&parts[c].v[1]);
-      uint64_t target = floor_mul(total, row_uniform(a, row));
-      if (target >= total) target = total - 1;
-      uint64_t cum = 0;
-      uint32_t c = 0;
-      for (; c < S; ++c) {
-        const uint64_t t = residual ? ld_dev(&parts[c].v[0]) : ld_dev(&parts[c].v[1]);
-        if (cum + t > target) break;
-        cum += t;
-      }
-      ns.residual = residual ? 1u : 0u;
-      ns.chunk = c < S ? c : S - 1;
-      ns.within = target - cum;
-      ns.target = target;
-      ns.stage = kStageWalk;
-      }
-      break;
-    }
     case kStageKeptCount: {
       if constexpr (CLS == kClsMass) {
-      uint64_t kept = 0;
-      for (uint32_t c = 0; c < S; ++c) kept += ld_dev(&parts[c].v[0]);
-      if (a.out_kept_counts) a.out_kept_counts[row] = (uint32_t)kept;
-      ns.stage = kStageKeptWrite;
+      const uint64_t kept = wave_sum_u64(lane_v(0));
+      if (lead) {
+        if (a.out_kept_counts) a.out_kept_counts[row] = (uint32_t)kept;
+        ns.stage = kStageKeptWrite;
+      }
       }
       break;
     }
     case kStageKeptWrite:
-      ns.stage = kStageDone;
+      if (lead) ns.stage = kStageDone;
       break;
     default:
       break;
