@@ -132,6 +132,25 @@ struct SampleLaunch {
   uint32_t q_aligned;     // dense q rows start on 16-byte boundaries
 };
 
+// The fast selection launch: the per-row facts every block needs before its
+// first load (flags, penalty table row) travel in the kernel arguments, and
+// each (table row, chunk) holds its penalty entries in a fixed run of
+// `slot_count` 32-bit slots, so a block requests them together with its
+// logits and waits on nothing first. Slot = offset in the chunk << 19 |
+// prompt bit << 18 | count (< 2^18); an empty slot is 0 (every real entry
+// has a count or the prompt bit).
+constexpr int kKernargRows = 256;
+constexpr uint32_t kSlotCountMask = 0x3ffffu;
+constexpr uint32_t kSlotPromptBit = 0x40000u;
+constexpr int kSlotOffsetShift = 19;
+struct FastLaunch {
+  SampleLaunch a;
+  const uint32_t *pen_slots;  // [table rows][chunks][slot_count]
+  uint32_t slot_count;        // 256 or 512
+  uint32_t row_base;          // sampler row of blockIdx.y == 0
+  uint32_t row_info[kKernargRows];  // RowFlags | penalty row << 8
+};
+
 // Multi-pass stages, in launch order.
 enum Stage : uint32_t {
   kStageDone = 0,
@@ -229,6 +248,9 @@ struct AcceptTreeLaunch {
 // With both events set, they record the selection kernel's own start and end.
 int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
                   void *start_event = nullptr, void *stop_event = nullptr);
+int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
+                       void *stream, void *start_event = nullptr,
+                       void *stop_event = nullptr);
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream);

@@ -1882,6 +1882,420 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
   }
 }
 
+// ---- the fast selection kernel ---------------------------------------------
+//
+// select_kernel's results for the rows the host admits (16-byte aligned rows,
+// every penalty chunk within its fixed slots, no extra verify tokens), with a
+// load phase that requests everything before it waits on anything:
+//   1. the chunk's penalty slots (their address needs only the kernel
+//      arguments), then the logits with nontemporal 16-byte loads, then a
+//      constrained row's mask words;
+//   2. each slot's thread re-reads its token's logit (and mask word): the
+//      block's own request for that line is already in flight, so the read
+//      merges with it in L2 instead of waiting behind the whole stream. The
+//      thread holds the penalized token as a side entry; the lane that loaded
+//      the token drops it through a per-thread bitmap (bit i <-> register i);
+//   3. greedy rows take the block maximum first and then the lowest id that
+//      holds it; sampled rows write the chunk summary and candidates exactly
+//      as select_kernel does.
+
+struct __align__(16) FastLds {
+  uint32_t bm[kThreads];  // bit i of bm[t]: register i of thread t is dropped
+  uint64_t stage[kWaves][kWaveCandidates];
+  uint32_t wcount[kWaves];
+  float wf[kWaves];
+  uint32_t wu[kWaves];
+  uint32_t wu2[kWaves];
+};
+
+// The largest multiple of 2^16 with at least k (1..64) lanes holding a value
+// >= it: a lower bound of the k-th largest that needs 16 ballots, not 32.
+__device__ __forceinline__ uint32_t wave_kth_bound16(uint32_t v, uint32_t k) {
+  uint32_t answer = 0;
+#pragma unroll
+  for (int b = 31; b >= 16; --b) {
+    const uint32_t trial = answer | (1u << b);
+    if ((uint32_t)__popcll(ballot(v >= trial)) >= k) answer = trial;
+  }
+  return answer;
+}
+
+// A RowParams record read through the scalar cache: issue_row_policy starts
+// the load and returns at once; wait_row_policy waits for it (its operands
+// make every use of the record depend on the wait).
+typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+struct RowPolicyRegs {
+  u32x16 v;
+};
+__device__ __forceinline__ RowPolicyRegs issue_row_policy(const RowParams *p) {
+  const uint64_t addr = (uint64_t)p;
+  const uint64_t u =
+      ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32)) << 32) |
+      (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)addr);
+  RowPolicyRegs r;
+  asm volatile("s_load_dwordx16 %0, %1, 0x0" : "=s"(r.v) : "s"(u) : "memory");
+  return r;
+}
+__device__ __forceinline__ RowParams wait_row_policy(RowPolicyRegs r) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(r.v)::"memory");
+  RowParams rp;
+  static_assert(sizeof(RowParams) == sizeof(u32x16), "one record per load");
+  __builtin_memcpy(&rp, &r.v, sizeof(rp));
+  return rp;
+}
+
+// Register i of a thread and the thread that loads chunk offset o.
+template <int DT>
+__device__ __forceinline__ uint32_t owner_of(uint32_t o) {
+  return (o % Geo<DT>::SLAB) / Geo<DT>::VEC;
+}
+template <int DT>
+__device__ __forceinline__ uint32_t register_of(uint32_t o) {
+  return (o / Geo<DT>::SLAB) * Geo<DT>::VEC + o % Geo<DT>::VEC;
+}
+
+// The thread's 32 tokens of chunk `base`, requested without a wait. A full
+// chunk issues its loads unconditionally. The partial last chunk clamps each
+// vector load to the last whole vector of the row (always in bounds; the
+// host admits V >= 8 only) and reads the tokens past the last whole vector
+// into `tail` element by element, after every vector load is out. The
+// registers past the vocabulary are the caller's to drop (past_end_bits).
+template <int DT>
+__device__ __forceinline__ void fast_load(const void *logits, uint64_t stride,
+                                          uint32_t V, uint32_t row, uint32_t base,
+                                          bool full, float (&xs)[32],
+                                          std::conditional_t<DT == 0, float, uint32_t> (&tail)[Geo<DT>::VEC],
+                                          uint32_t &tail_j) {
+  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS, SLAB = Geo<DT>::SLAB;
+  const uint32_t lane_base = base + threadIdx.x * VEC;
+  using Raw = std::conditional_t<DT == 0, float, uint16_t>;
+  const Raw *rowp = (const Raw *)logits + (uint64_t)row * stride;
+  u32x4 v[LOADS];
+  const uint32_t vfull = V - V % VEC;  // tokens covered by whole vectors
+  // One load sequence for both (a branch here makes the compiler wait
+  // between the partial chunk's loads): the address is selected, not the code.
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    const uint32_t t0 = lane_base + j * SLAB;
+    const uint32_t tl = full || t0 + VEC <= vfull ? t0 : vfull - VEC;
+    v[j] = __builtin_nontemporal_load((const u32x4 *)(rowp + tl));
+  }
+  tail_j = 0xffu;
+  if (!full) {
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j)
+      if (lane_base + j * SLAB == vfull && vfull < V) tail_j = (uint32_t)j;
+    if (tail_j != 0xffu) {
+      // Unconditional loads at clamped indices, kept raw until the caller
+      // places them (no wait here); the registers past the vocabulary are
+      // dropped by the caller.
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) tail[e] = rowp[min(vfull + e, V - 1)];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    if constexpr (DT == 0) {
+      xs[j * 4 + 0] = u2f(v[j].x);
+      xs[j * 4 + 1] = u2f(v[j].y);
+      xs[j * 4 + 2] = u2f(v[j].z);
+      xs[j * 4 + 3] = u2f(v[j].w);
+    } else {
+      xs[j * 8 + 0] = u2f(v[j].x << 16);
+      xs[j * 8 + 1] = u2f(v[j].x & 0xffff0000u);
+      xs[j * 8 + 2] = u2f(v[j].y << 16);
+      xs[j * 8 + 3] = u2f(v[j].y & 0xffff0000u);
+      xs[j * 8 + 4] = u2f(v[j].z << 16);
+      xs[j * 8 + 5] = u2f(v[j].z & 0xffff0000u);
+      xs[j * 8 + 6] = u2f(v[j].w << 16);
+      xs[j * 8 + 7] = u2f(v[j].w & 0xffff0000u);
+    }
+  }
+}
+
+// Drop bits of the thread's registers that hold no token of the vocabulary.
+template <int DT>
+__device__ __forceinline__ uint32_t past_end_bits(uint32_t V, uint32_t base) {
+  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS, SLAB = Geo<DT>::SLAB;
+  constexpr uint32_t VMASK = (1u << VEC) - 1u;
+  const uint32_t lane_base = base + threadIdx.x * VEC;
+  uint32_t bits = 0;
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    const uint32_t t0 = lane_base + j * SLAB;
+    const uint32_t m = t0 + VEC <= V ? 0u
+                       : t0 >= V     ? VMASK
+                                     : VMASK & ~((1u << (V - t0)) - 1u);
+    bits |= m << (j * VEC);
+  }
+  return bits;
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
+  constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
+                LOADS = Geo<DT>::LOADS;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  constexpr uint32_t VMASK = (1u << VEC) - 1u;
+  static_assert(TPL == 32, "one drop bit per register");
+  const SampleLaunch &a = f.a;
+  __shared__ FastLds s;
+  // Every kernel argument the loads need, read in one round trip before the
+  // first branch (the compiler would otherwise fetch some inside branches,
+  // one dependent round trip each, before the first logit load).
+  const uint32_t chunk = blockIdx.x, lrow = blockIdx.y;
+  const uint32_t info = f.row_info[lrow];
+  const uint32_t S = a.chunks, V = a.vocabulary, row = f.row_base + lrow;
+  const uint32_t slot_count = f.slot_count;
+  const uint32_t *pen_slots = f.pen_slots;
+  const void *logits = a.logits;
+  const uint64_t stride = a.stride;
+  const uint32_t *masks = a.masks;
+  const uint64_t mask_stride = a.mask_stride;
+  const RowParams *params = a.params;
+  const uint32_t stop0 = a.stop0, stop1 = a.stop1;
+  BlockHeader *headers = a.headers;
+  uint64_t *cands = a.cands;
+  asm volatile("" ::"s"(info), "s"(S), "s"(V), "s"(row), "s"(slot_count),
+               "s"(pen_slots), "s"(logits), "s"(stride), "s"(masks),
+               "s"(mask_stride), "s"(params), "s"(stop0), "s"(stop1),
+               "s"(headers), "s"(cands));
+  const uint32_t flags = info & 0xffu, prow = info >> 8;
+  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const uint32_t base = chunk * CHUNK;
+  const uint32_t lane_base = base + tid * VEC;
+  const bool full = base + CHUNK <= V;
+  const bool penalized = (flags & kRowPenalized) != 0;
+  const bool constrained = (flags & kRowConstrained) != 0;
+
+  // 1. Every request of the chunk: penalty slots, logits, mask words.
+  constexpr int SPT = kSideEntries;  // slots per thread (slot_count <= 512)
+  uint32_t slot[SPT];
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) slot[k] = 0;
+  if (penalized) {
+    const uint32_t *sp = pen_slots + ((uint64_t)prow * S + chunk) * slot_count;
+#pragma unroll
+    for (int k = 0; k < SPT; ++k)
+      if (k * kThreads < (int)slot_count) slot[k] = sp[tid + k * kThreads];
+    s.bm[tid] = 0;
+  }
+  float xs[TPL];
+  std::conditional_t<DT == 0, float, uint32_t> tail[VEC];
+  uint32_t tail_j;
+  fast_load<DT>(logits, stride, V, row, base, full, xs, tail, tail_j);
+  const uint32_t *mrow = masks + (uint64_t)row * mask_stride;
+  uint32_t mw[LOADS];
+  if (constrained) {
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const uint32_t t0 = lane_base + j * SLAB;
+      mw[j] = t0 < V ? mrow[t0 >> 5] : 0u;
+    }
+  }
+  if (penalized) __syncthreads();  // drop bitmaps cleared
+  // The row's policy by one scalar load issued after that barrier (a barrier
+  // waits for every outstanding scalar load); its wait sits at the first use.
+  // The compiler itself would read it with vector loads, since it cannot
+  // rule out that this kernel writes the records.
+  RowPolicyRegs prr = issue_row_policy(params + row);
+
+  // 2. Penalized tokens: recorded in the drop bitmaps, re-read by their
+  // slot's thread, penalized there (sampling.metal:928-963) and admitted
+  // (sampling.metal:33-37).
+  uint32_t drop = 0;
+  SideEntries side;
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) {
+    side.tok[k] = kNoToken;
+    side.val[k] = kNotAdmitted;
+  }
+  RowParams rp;
+  if (penalized) {
+    uint32_t raw[SPT], mword[SPT];
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      raw[k] = 0;
+      mword[k] = 0;
+      if (slot[k]) {
+        const uint32_t o = slot[k] >> kSlotOffsetShift, t = base + o;
+        atomicOr(&s.bm[owner_of<DT>(o)], 1u << register_of<DT>(o));
+        if constexpr (DT == 0)
+          raw[k] = f2u(((const float *)logits)[(uint64_t)row * stride + t]);
+        else
+          raw[k] = (uint32_t)((const uint16_t *)logits)[(uint64_t)row * stride + t];
+        if (constrained) mword[k] = mrow[t >> 5];
+      }
+    }
+    __syncthreads();  // bitmaps complete
+    drop = s.bm[tid];
+    rp = wait_row_policy(prr);
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      if (slot[k]) {
+        const uint32_t o = slot[k] >> kSlotOffsetShift, t = base + o;
+        const uint32_t count = slot[k] & kSlotCountMask;
+        const float x = DT == 0 ? u2f(raw[k]) : bf16_to_float(raw[k]);
+        float v = penalize(x, count, rp.repetition, rp.repetition_inverse,
+                           rp.presence, rp.frequency);
+        if (constrained && !((mword[k] >> (t & 31)) & 1u)) v = kNotAdmitted;
+        if ((flags & kRowExcludeStop) && (t == stop0 || t == stop1)) v = kNotAdmitted;
+        side.tok[k] = t;
+        side.val[k] = v;
+      }
+    }
+  }
+  // The constraint mask and the stop tokens join the drop bits.
+  if (constrained) {
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const uint32_t t0 = lane_base + j * SLAB;
+      const uint32_t keep = (mw[j] >> (t0 & 31)) & VMASK;
+      drop |= (~keep & VMASK) << (j * VEC);
+    }
+  }
+  bool stop_here = false;
+  if (flags & kRowExcludeStop) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t st = k ? stop1 : stop0;
+      if (st >= base && st < base + CHUNK) {
+        stop_here = true;
+        const uint32_t o = st - base;
+        if (owner_of<DT>(o) == tid) drop |= 1u << register_of<DT>(o);
+      }
+    }
+  }
+  if (!full) {
+    drop |= past_end_bits<DT>(V, base);
+    if (tail_j != 0xffu)
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          xs[j * VEC + e] = (uint32_t)j == tail_j ? (DT == 0 ? (float)tail[e] : bf16_to_float((uint32_t)tail[e]))
+                                                  : xs[j * VEC + e];
+  }
+  if (penalized || constrained || stop_here || !full) {
+    // A dropped register becomes NaN: its exponent bits and quiet bit set.
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+      const uint32_t m = (uint32_t)((int32_t)(drop << (31 - i)) >> 31);
+      xs[i] = u2f(f2u(xs[i]) | (m & 0x7fc00000u));
+    }
+  }
+
+  if (!penalized) rp = wait_row_policy(prr);
+
+  // 3. The lane's largest admitted value (fmax skips NaN operands, so the NaN
+  // it starts from survives only when the lane admits nothing).
+  float mx = kNotAdmitted;
+#pragma unroll
+  for (int i = 0; i < TPL; ++i) mx = __builtin_fmaxf(mx, xs[i]);
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) mx = __builtin_fmaxf(mx, side.val[k]);
+  BlockHeader *hdr = headers + (uint64_t)row * S + chunk;
+
+  if (!(flags & kRowSampled)) {
+    // Greedy (sampling.metal:1427-1464): the block maximum, then the lowest
+    // id holding it. NaN never wins; a -inf token wins only over nothing.
+    const float wmax = wave_max_f32(mx);
+    if (lane == 0) s.wf[w] = wmax;
+    __syncthreads();
+    const float M = __builtin_fmaxf(__builtin_fmaxf(s.wf[0], s.wf[1]),
+                                    __builtin_fmaxf(s.wf[2], s.wf[3]));
+    uint32_t id = kNoToken;
+    if (mx == M) {
+#pragma unroll
+      for (int i = TPL - 1; i >= 0; --i)
+        id = xs[i] == M ? lane_base + (i / VEC) * SLAB + (i % VEC) : id;
+#pragma unroll
+      for (int k = 0; k < SPT; ++k)
+        id = side.val[k] == M ? min(id, side.tok[k]) : id;
+    }
+    const uint32_t wid = wave_min_u32(id);
+    if (lane == 0) s.wu[w] = wid;
+    __syncthreads();
+    if (tid == 0) {
+      hdr->best_value = M == M ? M : -__builtin_inff();
+      hdr->best_id = min(min(s.wu[0], s.wu[1]), min(s.wu[2], s.wu[3]));
+    }
+    return;
+  }
+
+  const bool any = mx == mx;
+  // The chunk's top-k bound, as select_kernel (each wave's ceil(k/4)-th
+  // largest lane maximum, rounded down to a multiple of 2^16 of its key).
+  const uint32_t K = rp.top_k;
+  const uint32_t kw = (K + kWaves - 1) / kWaves;
+  const bool bound = (flags & kRowTopK) && kw <= 64;
+  uint32_t wth = 0;
+  if (bound) wth = wave_kth_bound16(any ? logit_key(mx) : 0u, kw);
+  const float wmax = wave_max_f32(mx);
+  const uint32_t wany = ballot(any) != 0 ? 1u : 0u;
+  if (lane == 0) {
+    s.wf[w] = wmax;
+    s.wu[w] = wany;
+    s.wu2[w] = wth;
+  }
+  __syncthreads();
+  const float bmax = __builtin_fmaxf(
+      __builtin_fmaxf(__builtin_fmaxf(s.wf[0], s.wf[1]),
+                      __builtin_fmaxf(s.wf[2], s.wf[3])),
+      -3.402823466e38f);
+  const uint32_t badm = s.wu[0] | s.wu[1] | s.wu[2] | s.wu[3];
+  const uint32_t tk =
+      bound ? min(min(s.wu2[0], s.wu2[1]), min(s.wu2[2], s.wu2[3])) : 0u;
+  uint32_t thr = tk;
+  if (flags & kRowMinP)
+    thr = max(thr, logit_key(__builtin_fminf(bmax + rp.minp_offset, bmax)));
+  const float tv = thr <= kLowestKey ? -__builtin_inff() : key_logit(thr);
+  uint64_t *stage = s.stage[w];
+  uint32_t run = 0;
+  auto emit = [&](float x, uint32_t token) {
+    const bool hit = x >= tv;
+    const uint64_t m = ballot(hit);
+    if (m) {
+      const uint32_t slot_i = __builtin_amdgcn_mbcnt_hi(
+          (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, run));
+      if (hit && slot_i < kWaveCandidates)
+        stage[slot_i] = (uint64_t)f2u(x) | ((uint64_t)token << 32);
+      run += (uint32_t)__popcll(m);
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) emit(xs[j * VEC + e], lane_base + j * SLAB + e);
+#pragma unroll
+  for (int k = 0; k < SPT; ++k) emit(side.val[k], side.tok[k]);
+  if (lane == 0) s.wcount[w] = run;
+  __syncthreads();
+  uint32_t off[kWaves + 1], over = 0;
+  off[0] = 0;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) {
+    const uint32_t n = s.wcount[k];
+    over |= n > kWaveCandidates;
+    off[k + 1] = off[k] + min(n, kWaveCandidates);
+  }
+  uint64_t *dst = cands + ((uint64_t)row * S + chunk) * kBlockCandidates;
+  if (!over)
+    for (uint32_t i = tid; i < off[kWaves]; i += kThreads) {
+      const uint32_t k = (i >= off[1]) + (i >= off[2]) + (i >= off[3]);
+      const uint64_t e = s.stage[k][i - off[k]];
+      dst[i] = (uint64_t)logit_key(u2f((uint32_t)e)) | (e & 0xffffffff00000000ull);
+    }
+  const uint32_t c = over ? kBlockCandidates + 1 : off[kWaves];
+  if (tid == 0) {
+    hdr->maximum = bmax;
+    hdr->count = min(c, (uint32_t)kBlockCandidates);
+    hdr->admitted = badm;
+    hdr->overflow = c > (uint32_t)kBlockCandidates ? 1u : 0u;
+    hdr->floor_key = tk;
+  }
+}
+
 // One block per row merges the row's chunk summaries (the reduction the
 // reference's last-arriving group does, split_reduce.h:14-45; here the
 // kernel boundary orders the partials before their reader).
@@ -2564,6 +2978,18 @@ int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
   } else {
     hipLaunchKernelGGL(select_kernel<1>, grid, block, 0, st, a);
   }
+  return (int)hipGetLastError();
+}
+
+int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
+                       void *stream, void *start_event, void *stop_event) {
+  const dim3 grid(f.a.chunks, rows), block(kThreads);
+  const hipStream_t st = (hipStream_t)stream;
+  const hipEvent_t e0 = (hipEvent_t)start_event, e1 = (hipEvent_t)stop_event;
+  if (dtype == 0)
+    hipExtLaunchKernelGGL(select_fast_kernel<0>, grid, block, 0, st, e0, e1, 0, f);
+  else
+    hipExtLaunchKernelGGL(select_fast_kernel<1>, grid, block, 0, st, e0, e1, 0, f);
   return (int)hipGetLastError();
 }
 

@@ -119,6 +119,13 @@ struct jf_penalty_table {
   int device = 0;
   uint2 *entries = nullptr;    // [rows][max_entries] {token, word}
   uint32_t *offsets = nullptr; // [rows][buckets + 1]
+  // The fast kernel's fixed slots: [rows][chunks][slot_count], 8192-token
+  // chunks; fits[row] when every chunk of the row fits its slots and every
+  // count fits the slot's 18 bits (otherwise select_kernel takes the row).
+  uint32_t chunks = 0;
+  uint32_t slot_count = 0;
+  uint32_t *slots = nullptr;
+  std::vector<uint8_t> fits;
   std::vector<std::vector<std::pair<uint32_t, uint32_t>>> host;
   StagingRing staging;
 };
@@ -281,6 +288,7 @@ int jf_penalty_table_destroy(jf_penalty_table *t) {
   t->staging.release();
   (void)hipFree(t->entries);
   (void)hipFree(t->offsets);
+  (void)hipFree(t->slots);
   delete t;
   return JF_OK;
 }
@@ -297,14 +305,24 @@ int jf_penalty_table_create(uint32_t vocabulary, uint32_t rows,
   t->rows = rows;
   t->max_entries = max_entries;
   t->buckets = (vocabulary + jf::kPenaltyBucket - 1) / jf::kPenaltyBucket;
+  t->chunks = (vocabulary + jf::kChunkF32 - 1) / jf::kChunkF32;
+  // Half again the mean entries of a chunk, in whole slots per thread.
+  t->slot_count = (uint64_t)max_entries * 3 / 2 <= (uint64_t)t->chunks * jf::kThreads
+                      ? (uint32_t)jf::kThreads
+                      : 2u * jf::kThreads;
+  t->fits.assign(rows, 1);
   t->host.resize(rows);
   int rc = JF_OK;
   hipError_t ge = hipGetDevice(&t->device);
   if (ge != hipSuccess) rc = hip_fail(ge, "hipGetDevice");
   if (rc == JF_OK) rc = device_alloc(&t->entries, (size_t)rows * max_entries, "penalty entries");
   if (rc == JF_OK) rc = device_alloc(&t->offsets, (size_t)rows * (t->buckets + 1), "penalty offsets");
+  if (rc == JF_OK)
+    rc = device_alloc(&t->slots, (size_t)rows * t->chunks * t->slot_count, "penalty slots");
   if (rc == JF_OK) {
     ge = hipMemset(t->offsets, 0, (size_t)rows * (t->buckets + 1) * sizeof(uint32_t));
+    if (ge == hipSuccess)
+      ge = hipMemset(t->slots, 0, (size_t)rows * t->chunks * t->slot_count * sizeof(uint32_t));
     if (ge == hipSuccess) ge = hipDeviceSynchronize();
     if (ge != hipSuccess) rc = hip_fail(ge, "penalty table init");
   }
@@ -332,8 +350,29 @@ static int upload_penalty_row(jf_penalty_table *t, uint32_t row, void *stream) {
   int rc = t->staging.upload(t->entries + (size_t)row * t->max_entries, ent,
                              h.size() * sizeof(uint2), st);
   if (rc != JF_OK) return rc;
-  return t->staging.upload(t->offsets + (size_t)row * (t->buckets + 1), off,
-                           (t->buckets + 1) * sizeof(uint32_t), st);
+  rc = t->staging.upload(t->offsets + (size_t)row * (t->buckets + 1), off,
+                         (t->buckets + 1) * sizeof(uint32_t), st);
+  if (rc != JF_OK) return rc;
+  // The fixed slots of each chunk, entries in token order, empty slots 0.
+  const size_t per_row = (size_t)t->chunks * t->slot_count;
+  std::vector<uint32_t> sl(per_row, 0u);
+  std::vector<uint32_t> used(t->chunks, 0u);
+  bool fits = true;
+  for (const auto &e : h) {
+    const uint32_t c = e.first / jf::kChunkF32, o = e.first % jf::kChunkF32;
+    const uint32_t count = e.second & JF_PENALTY_COUNT_MASK;
+    if (used[c] >= t->slot_count || count > jf::kSlotCountMask) {
+      fits = false;
+      break;
+    }
+    sl[(size_t)c * t->slot_count + used[c]++] =
+        (o << jf::kSlotOffsetShift) |
+        ((e.second & JF_PENALTY_PROMPT_BIT) ? jf::kSlotPromptBit : 0u) | count;
+  }
+  t->fits[row] = fits ? 1 : 0;
+  if (!fits) return JF_OK;
+  return t->staging.upload(t->slots + (size_t)row * per_row, sl.data(),
+                           per_row * sizeof(uint32_t), st);
 }
 
 int jf_penalty_table_rebuild(jf_penalty_table *t, uint32_t row,
@@ -555,8 +594,42 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
 
   if ((a->select_start_event == nullptr) != (a->select_done_event == nullptr))
     return fail(JF_ERR_INVALID_ARGUMENT, "select events come in pairs");
-  int e = jf::launch_select(L, a->dtype, stream, a->select_start_event,
-                            a->select_done_event);
+  // The fast selection kernel takes the launch when every row qualifies:
+  // aligned rows, no extra verify tokens, and penalty rows whose chunks fit
+  // their fixed slots (and vocabularies of at least one 16-byte vector).
+  bool fast = aligned && V >= 8;
+  for (uint32_t r = 0; fast && r < rows; ++r) {
+    const jf::RowParams &rp = params[r];
+    if (rp.extra_count) fast = false;
+    if ((rp.flags & jf::kRowPenalized) &&
+        (!a->penalties->fits[rp.penalty_row] || rp.penalty_row > 0xffffffu))
+      fast = false;
+  }
+  int e = hipSuccess;
+  if (fast) {
+    jf::FastLaunch F{};
+    F.a = L;
+    if (a->penalties) {
+      F.pen_slots = a->penalties->slots;
+      F.slot_count = a->penalties->slot_count;
+    }
+    for (uint32_t r0 = 0; r0 < rows && e == hipSuccess; r0 += jf::kKernargRows) {
+      const uint32_t n = std::min<uint32_t>(rows - r0, jf::kKernargRows);
+      F.row_base = r0;
+      for (uint32_t r = 0; r < n; ++r) {
+        const jf::RowParams &rp = params[r0 + r];
+        const uint32_t prow = (rp.flags & jf::kRowPenalized) ? rp.penalty_row : 0u;
+        F.row_info[r] = (rp.flags & 0xffu) | (prow << 8);
+      }
+      const bool first = r0 == 0, last = r0 + n == rows;
+      e = jf::launch_select_fast(F, n, a->dtype, stream,
+                                 first ? a->select_start_event : nullptr,
+                                 last ? a->select_done_event : nullptr);
+    }
+  } else {
+    e = jf::launch_select(L, a->dtype, stream, a->select_start_event,
+                          a->select_done_event);
+  }
   if (e != hipSuccess) return hip_fail((hipError_t)e, "select launch");
   e = jf::launch_merge(L, a->dtype, stream);
   if (e != hipSuccess) return hip_fail((hipError_t)e, "merge launch");
