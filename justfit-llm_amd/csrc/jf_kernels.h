@@ -252,6 +252,7 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
                        void *stream, void *start_event = nullptr,
                        void *stop_event = nullptr);
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
+int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream);
 int launch_accept_tree(const AcceptTreeLaunch &a, void *stream);

@@ -2307,6 +2307,269 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(SampleLaunch a) {
   merge_row<DT>(a, rp, row, s);
 }
 
+// ---- the small-K merge -----------------------------------------------------
+//
+// One block per row, for launches whose sampled rows all keep at most 64
+// tokens (top-k <= 64) and take their draft probabilities, if any, from the
+// sparse candidates. It computes what merge_kernel computes, built for
+// latency: every kernel argument in one round trip, then every load the row
+// needs in one batch (its policy, the chunk summaries, the first slots of
+// every chunk's candidate list, the uniform, the draft and its candidates);
+// the 1024-bin histogram that leaves the top K and the boundary bin; and a
+// finish by one wave in registers. Rows the speculative fetch does not cover
+// (an overflowed chunk, a list longer than the slots fetched, values that do
+// not spread over the bins) take merge_kernel's general path.
+
+// Lane exchange at a distance fixed at compile time (after unrolling).
+__device__ __forceinline__ uint64_t xor_lanes_u64(uint64_t v, int j) {
+  switch (j) {
+    case 1: return xor_u64<1>(v);
+    case 2: return xor_u64<2>(v);
+    case 4: return xor_u64<4>(v);
+    case 8: return xor_u64<8>(v);
+    case 16: return xor_u64<16>(v);
+    default: return xor_u64<32>(v);
+  }
+}
+// Bitonic sort of one 64-bit value per lane over the wave: lane 0 ends with
+// the largest (DESC) or the smallest.
+template <bool DESC>
+__device__ __forceinline__ uint64_t wave_sort_u64(uint64_t v) {
+  const uint32_t lane = lane_id();
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const uint64_t o = xor_lanes_u64(v, j);
+      // The lower lane of a pair takes the larger value in the blocks that
+      // end descending (for DESC, every block of the last merge).
+      const bool lower = (lane & j) == 0;
+      const bool block_desc = ((lane & k) == 0) == DESC;
+      const bool take_larger = lower == block_desc;
+      const uint64_t hi = o > v ? o : v, lo = o > v ? v : o;
+      v = take_larger ? hi : lo;
+    }
+  }
+  return v;
+}
+
+// The last steps of a row with at most 64 items left (s.merge.key/id[0, n),
+// any order), by one wave in registers. Sorting the items by (key desc, id
+// asc) gives the top-k cut and the walk of top-p (sampling.metal:585-650);
+// sorting the kept items by id gives the draw's order and the kept outputs
+// (sampling.metal:700-829). The results equal wave_merge's.
+__device__ __forceinline__ void wave_finish(const SampleLaunch &a, const RowParams &rp,
+                                            uint32_t row, const Lds &s, uint32_t n,
+                                            float maximum, float u, uint32_t draft) {
+  const MergeLds &m = s.merge;
+  const uint32_t lane = lane_id();
+  uint64_t c = lane < n ? ((uint64_t)m.key[lane] << 32) | (uint32_t)~m.id[lane] : 0ull;
+  c = wave_sort_u64<true>(c);  // lane r holds the item of rank r
+  const uint32_t key = (uint32_t)(c >> 32), id = ~(uint32_t)c;
+  const uint32_t n2 = min(rp.top_k, n);
+  const bool in2 = lane < n2;
+  const float w = in2 ? weight_of(key_logit(key), maximum, rp.inv_t) : 0.0f;
+  const uint64_t wq = quantize(w);
+  uint32_t n3 = n2;
+  if (rp.flags & kRowTopP) {
+    const uint64_t incl = wave_incl_scan_u64(wq);
+    const uint64_t mass2 = readlane_u64(incl, 63);
+    if (mass2) {
+      const uint64_t nucleus = floor_mul(mass2, rp.top_p);
+      const uint64_t hm = ballot(in2 && incl - wq <= nucleus && incl > nucleus);
+      if (hm) n3 = (uint32_t)__builtin_ctzll(hm) + 1;
+    }
+  }
+  const bool kept = lane < n3;
+  const uint64_t mass3 = wave_sum_u64(kept ? wq : 0);
+  const double scale = (double)mass3 * 0x1p-44;
+  const bool drafted = draft != kNoToken;
+  uint64_t d = kept ? wq : 0;
+  if (drafted) {
+    float q = 0.0f;
+    for (int j = 15; j >= 0; --j) q = s.cids[j] == id ? s.cprobs[j] : q;
+    const uint64_t r = kept ? residual_of(wq, mass3, q) : 0;
+    if (ballot(r > 0)) d = r;
+  }
+  const uint64_t fm = ballot(drafted && kept && id == draft);
+  const float fw = __shfl(w, fm ? (int)__builtin_ctzll(fm) : 0, kWave);
+  // Id order of the kept items, each carrying the lane of its rank.
+  uint64_t e = kept ? ((uint64_t)id << 32) | lane : ~0ull;
+  e = wave_sort_u64<false>(e);
+  const uint32_t src = (uint32_t)e & 63u, iid = (uint32_t)(e >> 32);
+  const uint64_t dq = shfl_u64(d, (int)src);
+  const float wi = __shfl(w, (int)src, kWave);
+  if (a.out_kept_ids && kept && lane < a.kept_cap) {
+    a.out_kept_ids[(uint64_t)row * a.kept_cap + lane] = iid;
+    a.out_kept_probs[(uint64_t)row * a.kept_cap + lane] =
+        mass3 ? (float)((double)wi / scale) : 0.0f;
+  }
+  if (mass3 == 0) {
+    if (lane == 0) write_result(a, row, kNoToken, 0.0f, n3);
+    return;
+  }
+  const uint64_t dd = kept ? dq : 0ull;
+  const uint64_t incl = wave_incl_scan_u64(dd);
+  const uint64_t total = readlane_u64(incl, 63);
+  uint64_t target = floor_mul(total, u);
+  if (target >= total) target = total - 1;
+  const uint64_t hm = ballot(kept && incl - dd <= target && incl > target);
+  const uint32_t token = hm ? readlane_u32(iid, (int)__builtin_ctzll(hm)) : kNoToken;
+  if (lane == 0)
+    write_result(a, row, token, drafted && fm ? (float)((double)fw / scale) : 0.0f, n3);
+}
+
+// The general merge of a row for merge_small_kernel, out of line so that
+// its register pressure stays out of the fast path's schedule. A called
+// function cannot reach the kernel's arguments (its kernel-argument segment
+// pointer is null), so the kernel copies the launch record into LDS first;
+// the function works in the kernel's LDS record.
+__shared__ Lds g_small_lds;
+__shared__ SampleLaunch g_small_launch;
+template <int DT>
+__device__ __noinline__ void merge_small_general(uint32_t row) {
+  const SampleLaunch &a = g_small_launch;
+  const RowParams rp = a.params[row];
+  merge_sampled<DT>(a, rp, row, g_small_lds);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void merge_small_kernel(SampleLaunch a) {
+  Lds &s = g_small_lds;
+  const uint32_t row = blockIdx.x, tid = threadIdx.x;
+  const uint32_t S = a.chunks;
+  // Every address of the row, computed once and held in vector registers:
+  // the general path's register pressure would otherwise have the compiler
+  // reload (and wait for) kernel arguments between the loads below. A load
+  // with nothing to read targets the row's first chunk summary instead (its
+  // value is ignored), so no load sits in a branch.
+  typedef __attribute__((address_space(1))) const u32x4 GlobalU32x4;
+  typedef __attribute__((address_space(1))) const uint64_t GlobalU64;
+  typedef __attribute__((address_space(1))) const uint32_t GlobalU32;
+  typedef __attribute__((address_space(1))) const float GlobalF32;
+  const bool has_draft = a.draft_tokens && row < a.drafted_rows;
+  const bool has_index = a.uniform_index != nullptr, has_uniform = a.uniforms != nullptr;
+  const BlockHeader *hrow = a.headers + (uint64_t)row * S;
+  uint64_t hbase = (uint64_t)(hrow + (tid < S ? tid : 0u));
+  uint64_t cbase = (uint64_t)(a.cands + (uint64_t)row * S * kBlockCandidates);
+  uint64_t uaddr = has_index     ? (uint64_t)(a.uniform_index + row)
+                   : has_uniform ? (uint64_t)(a.uniforms + a.uniform_offset + row * a.uniform_stride)
+                                 : (uint64_t)hrow;
+  uint64_t ubase = has_uniform ? (uint64_t)a.uniforms : (uint64_t)hrow;
+  uint64_t daddr = has_draft ? (uint64_t)(a.draft_tokens + row) : (uint64_t)hrow;
+  uint64_t qaddr = has_draft ? (uint64_t)(a.cand_ids + (uint64_t)row * 16 + (tid & 15))
+                             : (uint64_t)hrow;
+  uint64_t paddr = has_draft ? (uint64_t)(a.cand_probs + (uint64_t)row * 16 + (tid & 15))
+                             : (uint64_t)hrow;
+  uint64_t pbase = (uint64_t)(a.params + row);
+  asm volatile("" : "+v"(hbase), "+v"(cbase), "+v"(uaddr), "+v"(ubase), "+v"(daddr),
+               "+v"(qaddr), "+v"(paddr), "+s"(pbase));
+  // Every load of the row, before any wait: the uniform (or its index), the
+  // policy, the chunk summaries, the first P slots of every chunk's list,
+  // the draft token and its 16 candidates.
+  uint32_t ubits = *(GlobalU32 *)uaddr;
+  RowPolicyRegs prr = issue_row_policy((const RowParams *)pbase);
+  // BlockHeader: maximum, count, admitted, overflow | best_value, best_id,
+  // floor_key, reserved.
+  const u32x4 h0 = ((GlobalU32x4 *)hbase)[0], h1 = ((GlobalU32x4 *)hbase)[1];
+  constexpr int SPEC = 10;
+  const uint32_t pshift = S <= 20 ? 7u : (S <= 40 ? 6u : 5u), P = 1u << pshift;
+  uint64_t sv[SPEC];
+#pragma unroll
+  for (int k = 0; k < SPEC; ++k) {
+    const uint32_t i = tid + k * kThreads, c = min(i >> pshift, S - 1);
+    sv[k] = ((GlobalU64 *)cbase)[(uint64_t)c * kBlockCandidates + (i & (P - 1))];
+  }
+  const uint32_t draft_raw = *(GlobalU32 *)daddr;
+  const uint32_t cid_raw = *(GlobalU32 *)qaddr;
+  const float cpr_raw = *(GlobalF32 *)paddr;
+  // A uniform through an index: its second load, once the index is in.
+  if (has_index) {
+    uint64_t a2 = ubase + (uint64_t)ubits * sizeof(float);
+    asm volatile("" : "+v"(a2));
+    ubits = *(GlobalU32 *)a2;
+  }
+  const uint32_t draft = has_draft ? draft_raw : kNoToken;
+  const uint32_t cid = has_draft && tid < 16 ? cid_raw : kNoToken;
+  const float cpr = has_draft && tid < 16 ? cpr_raw : 0.0f;
+  const bool hv = tid < S;
+  const float hmax = hv ? u2f(h0.x) : -3.402823466e38f;
+  const float hbest = hv ? u2f(h1.x) : -__builtin_inff();
+  const uint32_t hcount = hv ? h0.y : 0u, hadm = hv ? h0.z : 0u, hovf = hv ? h0.w : 0u,
+                 hfloor = hv ? h1.z : 0u, hbid = hv ? h1.y : kNoToken;
+  const float u = u2f(ubits);
+  for (uint32_t b = tid; b < 1024; b += kThreads) s.merge.bins[b] = 0;
+  const RowParams rp = wait_row_policy(prr);
+
+  if (!(rp.flags & kRowSampled)) {
+    // Greedy: the largest chunk best, the lowest id among equals.
+    if (tid < 64) {
+      float bv = hbest;
+      uint32_t bi = hbid;
+      wave_argmax(bv, bi);
+      if (tid == 0) write_result(a, row, bi, 0.0f, 0);
+    }
+    return;
+  }
+  // The chunk summaries (wave 0): the row maximum, admission, overflow, the
+  // top-k floor (the K-th key is at least every chunk's floor) and the
+  // longest list.
+  if (tid < 64) {
+    const float mx = wave_max_f32(hmax);
+    const uint32_t adm = wave_max_u32(hadm), ovf = wave_max_u32(hovf),
+                   flr = wave_max_u32(hfloor), hcmax = wave_max_u32(hcount);
+    if (tid < S) s.hcnt[tid] = hcount;
+    if (tid == 0) {
+      s.row_max = mx;
+      s.row_admitted = adm;
+      s.row_overflow = ovf;
+      s.row_floor = flr;
+      s.row_maxcount = hcmax;
+    }
+  }
+  if (tid < 16) {
+    s.cids[tid] = draft != kNoToken ? cid : kNoToken;
+    s.cprobs[tid] = draft != kNoToken ? cpr : 0.0f;
+  }
+  __syncthreads();
+  const float maximum = s.row_max;
+  if (s.row_admitted == 0 || maximum == __builtin_inff()) {
+    if (tid == 0) write_result(a, row, kNoToken, 0.0f, 0);
+    return;
+  }
+  uint32_t thr = (rp.flags & kRowMinP)
+                     ? logit_key(__builtin_fminf(maximum + rp.minp_offset, maximum))
+                     : 0u;
+  thr = max(thr, s.row_floor);
+  const uint32_t K = rp.top_k;
+  if (!s.row_overflow && s.row_maxcount <= P && thr > kLowestKey) {
+    uint32_t valid = 0;
+#pragma unroll
+    for (int k = 0; k < SPEC; ++k) {
+      const uint32_t i = tid + k * kThreads, c = i >> pshift;
+      if (c < S && (i & (P - 1)) < s.hcnt[c] && (uint32_t)sv[k] >= thr) valid |= 1u << k;
+    }
+    const int got = spec_select(sv, valid, thr, K, maximum, s);
+    if (got >= 0) {
+      uint32_t n = (uint32_t)got;
+      if (n <= 64u || hist_select(s, n, K, maximum)) {
+        if (tid < 64) wave_finish(a, rp, row, s, n, maximum, u, draft);
+        return;
+      }
+      lds_sort_by_id(s, n);
+      lds_topk(s, n, K);
+      if (rp.flags & kRowTopP) lds_topp(s, n, maximum, rp.inv_t, rp.top_p);
+      lds_draw(a, row, s, n, maximum, rp.inv_t);
+      return;
+    }
+    __syncthreads();
+  }
+  // What the speculative fetch does not cover: the general merge.
+  if (tid == 0) g_small_launch = a;
+  __syncthreads();
+  merge_small_general<DT>(row);
+}
+
 // ---- multi-pass stages ---------------------------------------------------
 
 // A drafted row's dense q over this thread's tokens of a chunk, in the
@@ -2999,6 +3262,15 @@ int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream) {
     hipLaunchKernelGGL(merge_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
   else
     hipLaunchKernelGGL(merge_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream) {
+  const dim3 grid(a.rows), block(kThreads);
+  if (dtype == 0)
+    hipLaunchKernelGGL(merge_small_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(merge_small_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

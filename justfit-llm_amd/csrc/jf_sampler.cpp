@@ -631,7 +631,16 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
                           a->select_done_event);
   }
   if (e != hipSuccess) return hip_fail((hipError_t)e, "select launch");
-  e = jf::launch_merge(L, a->dtype, stream);
+  // The small-K merge takes launches whose sampled rows keep at most 64
+  // tokens and read sparse draft probabilities (or none).
+  bool small = !staged && !a->draft_q;
+  for (uint32_t r = 0; small && r < rows; ++r) {
+    const jf::RowParams &rp = params[r];
+    if ((rp.flags & jf::kRowSampled) && (!(rp.flags & jf::kRowTopK) || rp.top_k > 64u))
+      small = false;
+  }
+  e = small ? jf::launch_merge_small(L, a->dtype, stream)
+            : jf::launch_merge(L, a->dtype, stream);
   if (e != hipSuccess) return hip_fail((hipError_t)e, "merge launch");
   if (staged) {
     for (uint32_t stage = jf::kStageCount1; stage <= jf::kStageLast; ++stage) {
