@@ -2320,42 +2320,114 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(SampleLaunch a) {
 // (an overflowed chunk, a list longer than the slots fetched, values that do
 // not spread over the bins) take merge_kernel's general path.
 
-// Lane exchange at a distance fixed at compile time (after unrolling).
-__device__ __forceinline__ uint64_t xor_lanes_u64(uint64_t v, int j) {
-  switch (j) {
-    case 1: return xor_u64<1>(v);
-    case 2: return xor_u64<2>(v);
-    case 4: return xor_u64<4>(v);
-    case 8: return xor_u64<8>(v);
-    case 16: return xor_u64<16>(v);
-    default: return xor_u64<32>(v);
-  }
-}
-// Bitonic sort of one 64-bit value per lane over the wave: lane 0 ends with
-// the largest (DESC) or the smallest.
-template <bool DESC>
-__device__ __forceinline__ uint64_t wave_sort_u64(uint64_t v) {
+// Bitonic sort of one 32-bit value per lane over the wave, ascending.
+__device__ __forceinline__ uint32_t wave_sort_asc_u32(uint32_t v) {
   const uint32_t lane = lane_id();
 #pragma unroll
   for (int k = 2; k <= 64; k <<= 1) {
 #pragma unroll
     for (int j = k >> 1; j > 0; j >>= 1) {
-      const uint64_t o = xor_lanes_u64(v, j);
-      // The lower lane of a pair takes the larger value in the blocks that
-      // end descending (for DESC, every block of the last merge).
+      uint32_t o;
+      switch (j) {
+        case 1: o = xor_u32<1>(v); break;
+        case 2: o = xor_u32<2>(v); break;
+        case 4: o = xor_u32<4>(v); break;
+        case 8: o = xor_u32<8>(v); break;
+        case 16: o = xor_u32<16>(v); break;
+        default: o = xor_u32<32>(v); break;
+      }
       const bool lower = (lane & j) == 0;
-      const bool block_desc = ((lane & k) == 0) == DESC;
-      const bool take_larger = lower == block_desc;
-      const uint64_t hi = o > v ? o : v, lo = o > v ? v : o;
-      v = take_larger ? hi : lo;
+      const bool block_asc = (lane & k) == 0;
+      const bool take_smaller = lower == block_asc;
+      v = take_smaller ? min(v, o) : max(v, o);
     }
   }
   return v;
 }
 
-// The last steps of a row with at most 64 items left (s.merge.key/id[0, n),
-// any order), by one wave in registers. Sorting the items by (key desc, id
-// asc) gives the top-k cut and the walk of top-p (sampling.metal:585-650);
+// The exact top-K (K <= 64) of a row's candidates held in registers (v[k] =
+// key | id << 32; bit k of `valid` set for an item at or above the floor),
+// written to s.merge.key/id[0, n) in (key desc, id asc) order, n = min(K,
+// items). A 1024-bin histogram of the values over [value(thr), maximum] and
+// its suffix sums give each item its rank up to the items of its own bin,
+// which it compares directly; no sort. Returns n, or -1 when the values do
+// not spread over the bins or the boundary bin holds more than 64 items.
+// The caller zeroed s.merge.bins and s.merge.key[1024, 2048) before a
+// barrier. Every thread calls it. Uses s.merge.id[1024, 2048) and s.hist.
+template <int PER>
+__device__ __forceinline__ int rank_select(const uint64_t (&v)[PER], uint32_t valid,
+                                           uint32_t thr, uint32_t K, float maximum,
+                                           Lds &s) {
+  MergeLds &m = s.merge;
+  uint32_t *excl = m.id + 1024;   // items in the bins above each bin
+  uint32_t *fill = m.key + 1024;  // items placed per bin
+  uint64_t *seg = s.hist;         // items of the kept bins, grouped by bin
+  const uint32_t tid = threadIdx.x;
+  const float lo = key_logit(thr);
+  const float scale = 1023.0f / (maximum - lo);
+  if (!(scale > 0.0f && scale < 3.0e38f)) return -1;
+  auto bin_of = [&](uint32_t key) -> uint32_t {
+    return min(1023u, (uint32_t)((key_logit(key) - lo) * scale));
+  };
+  uint32_t bins[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    bins[k] = bin_of((uint32_t)v[k]);
+    if ((valid >> k) & 1) atomicAdd(&m.bins[bins[k]], 1u);
+  }
+  __syncthreads();
+  // Suffix sums: thread t owns bins 4t .. 4t+3; excl(b) counts the items in
+  // the bins above b.
+  const uint4 c4 = *(const uint4 *)&m.bins[4 * tid];
+  const uint32_t own = c4.x + c4.y + c4.z + c4.w;
+  uint64_t total64;
+  const uint32_t before = (uint32_t)block_excl_scan_u64(own, s, &total64);
+  const uint32_t total = (uint32_t)total64;
+  const uint32_t e3 = total - before - own, e2 = e3 + c4.w, e1 = e2 + c4.z,
+                 e0 = e1 + c4.y;
+  // The boundary bin: where the count from the top reaches K.
+  const uint32_t need = min(K, total);
+  if (tid == 0) s.hit = 0;
+  uint32_t bstar = 0xffffffffu, bcount = 0;
+  if (e3 < need && e3 + c4.w >= need) { bstar = 4 * tid + 3; bcount = c4.w; }
+  else if (e2 < need && e2 + c4.z >= need) { bstar = 4 * tid + 2; bcount = c4.z; }
+  else if (e1 < need && e1 + c4.y >= need) { bstar = 4 * tid + 1; bcount = c4.y; }
+  else if (e0 < need && e0 + c4.x >= need) { bstar = 4 * tid; bcount = c4.x; }
+  *(uint4 *)&excl[4 * tid] = make_uint4(e0, e1, e2, e3);
+  if (bstar != 0xffffffffu) {
+    s.sel_bin = bstar;
+    s.hit = bcount > 64u ? 1u : 0u;
+  }
+  __syncthreads();
+  if (s.hit) return -1;
+  const uint32_t bs = need ? s.sel_bin : 1024u;
+  // Items of the kept bins, grouped by bin in rank order of the bins.
+#pragma unroll
+  for (int k = 0; k < PER; ++k)
+    if (((valid >> k) & 1) && bins[k] >= bs) {
+      const uint32_t pos = excl[bins[k]] + atomicAdd(&fill[bins[k]], 1u);
+      seg[pos] = ((uint64_t)(uint32_t)v[k] << 32) | (uint32_t)~(uint32_t)(v[k] >> 32);
+    }
+  __syncthreads();
+  const uint32_t nsel = need ? excl[bs] + fill[bs] : 0u;
+  if (tid < nsel) {
+    const uint64_t me = seg[tid];
+    const uint32_t b = bin_of((uint32_t)(me >> 32));
+    const uint32_t e = excl[b], cnt = fill[b];
+    uint32_t rank = e;
+    for (uint32_t j = e; j < e + cnt; ++j) rank += seg[j] > me ? 1u : 0u;
+    if (rank < need) {
+      m.key[rank] = (uint32_t)(me >> 32);
+      m.id[rank] = ~(uint32_t)me;
+    }
+  }
+  __syncthreads();
+  return (int)need;
+}
+
+// The last steps of a row with at most 64 items left, s.merge.key/id[0, n)
+// in (key desc, id asc) order (rank_select), by one wave in registers. Rank
+// order gives the top-k cut and the walk of top-p (sampling.metal:585-650);
 // sorting the kept items by id gives the draw's order and the kept outputs
 // (sampling.metal:700-829). The results equal wave_merge's.
 __device__ __forceinline__ void wave_finish(const SampleLaunch &a, const RowParams &rp,
@@ -2363,9 +2435,8 @@ __device__ __forceinline__ void wave_finish(const SampleLaunch &a, const RowPara
                                             float maximum, float u, uint32_t draft) {
   const MergeLds &m = s.merge;
   const uint32_t lane = lane_id();
-  uint64_t c = lane < n ? ((uint64_t)m.key[lane] << 32) | (uint32_t)~m.id[lane] : 0ull;
-  c = wave_sort_u64<true>(c);  // lane r holds the item of rank r
-  const uint32_t key = (uint32_t)(c >> 32), id = ~(uint32_t)c;
+  const uint32_t key = lane < n ? m.key[lane] : 0u;
+  const uint32_t id = lane < n ? m.id[lane] : kNoToken;
   const uint32_t n2 = min(rp.top_k, n);
   const bool in2 = lane < n2;
   const float w = in2 ? weight_of(key_logit(key), maximum, rp.inv_t) : 0.0f;
@@ -2393,10 +2464,11 @@ __device__ __forceinline__ void wave_finish(const SampleLaunch &a, const RowPara
   }
   const uint64_t fm = ballot(drafted && kept && id == draft);
   const float fw = __shfl(w, fm ? (int)__builtin_ctzll(fm) : 0, kWave);
-  // Id order of the kept items, each carrying the lane of its rank.
-  uint64_t e = kept ? ((uint64_t)id << 32) | lane : ~0ull;
-  e = wave_sort_u64<false>(e);
-  const uint32_t src = (uint32_t)e & 63u, iid = (uint32_t)(e >> 32);
+  // Id order of the kept items, each carrying the lane of its rank (ids are
+  // below 2^19, so id and lane share 32 bits).
+  uint32_t e = kept ? (id << 6) | lane : 0xffffffffu;
+  e = wave_sort_asc_u32(e);
+  const uint32_t src = e & 63u, iid = e >> 6;
   const uint64_t dq = shfl_u64(d, (int)src);
   const float wi = __shfl(w, (int)src, kWave);
   if (a.out_kept_ids && kept && lane < a.kept_cap) {
@@ -2498,7 +2570,10 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(SampleLaunch a) {
   const uint32_t hcount = hv ? h0.y : 0u, hadm = hv ? h0.z : 0u, hovf = hv ? h0.w : 0u,
                  hfloor = hv ? h1.z : 0u, hbid = hv ? h1.y : kNoToken;
   const float u = u2f(ubits);
-  for (uint32_t b = tid; b < 1024; b += kThreads) s.merge.bins[b] = 0;
+  for (uint32_t b = tid; b < 1024; b += kThreads) {
+    s.merge.bins[b] = 0;
+    s.merge.key[1024 + b] = 0;
+  }
   const RowParams rp = wait_row_policy(prr);
 
   if (!(rp.flags & kRowSampled)) {
@@ -2549,17 +2624,9 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(SampleLaunch a) {
       const uint32_t i = tid + k * kThreads, c = i >> pshift;
       if (c < S && (i & (P - 1)) < s.hcnt[c] && (uint32_t)sv[k] >= thr) valid |= 1u << k;
     }
-    const int got = spec_select(sv, valid, thr, K, maximum, s);
+    const int got = rank_select(sv, valid, thr, K, maximum, s);
     if (got >= 0) {
-      uint32_t n = (uint32_t)got;
-      if (n <= 64u || hist_select(s, n, K, maximum)) {
-        if (tid < 64) wave_finish(a, rp, row, s, n, maximum, u, draft);
-        return;
-      }
-      lds_sort_by_id(s, n);
-      lds_topk(s, n, K);
-      if (rp.flags & kRowTopP) lds_topp(s, n, maximum, rp.inv_t, rp.top_p);
-      lds_draw(a, row, s, n, maximum, rp.inv_t);
+      if (tid < 64) wave_finish(a, rp, row, s, (uint32_t)got, maximum, u, draft);
       return;
     }
     __syncthreads();
