@@ -27,6 +27,8 @@ FLAGS = [
     "-fno-fast-math",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Leading scalar kernel arguments arrive in SGPRs at wave launch.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I" + os.path.join(REPO, "include"),
     "-I" + CSRC,
 ]

@@ -248,9 +248,11 @@ struct AcceptTreeLaunch {
 // With both events set, they record the selection kernel's own start and end.
 int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
                   void *start_event = nullptr, void *stop_event = nullptr);
+// `uniform`: when every row of the launch has this policy and penalty table
+// row == its own row, or NULL.
 int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
-                       void *stream, void *start_event = nullptr,
-                       void *stop_event = nullptr);
+                       const RowParams *uniform, void *stream,
+                       void *start_event = nullptr, void *stop_event = nullptr);
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);

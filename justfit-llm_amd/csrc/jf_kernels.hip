@@ -1990,7 +1990,13 @@ __device__ __forceinline__ void fast_load(const void *logits, uint64_t stride,
       // places them (no wait here); the registers past the vocabulary are
       // dropped by the caller.
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) tail[e] = rowp[min(vfull + e, V - 1)];
+      for (int e = 0; e < VEC; ++e) {
+        // A vector load (the uniform index would otherwise make it a scalar
+        // load, which the next barrier waits for).
+        uint32_t idx = min(vfull + e, V - 1);
+        asm volatile("" : "+v"(idx));
+        tail[e] = rowp[idx];
+      }
     }
   }
 #pragma unroll
@@ -2031,8 +2037,21 @@ __device__ __forceinline__ uint32_t past_end_bits(uint32_t V, uint32_t base) {
   return bits;
 }
 
+// The arguments a block needs before its first load lead the signature (13
+// dwords, no padding; the hardware has 14 to preload): they arrive in scalar
+// registers at wave launch, so a wave that starts while the memory system is
+// already full of other waves' loads does not wait for its own arguments
+// behind them. `packed`: bits 0-7 the uniform flags, 8-15 the chunks per
+// row, bit 16 set for 512 penalty slots per chunk (else 256), bits 17-30 the
+// first row over 256, bit 31 set when the launch is uniform: every row has
+// those flags, reads penalty table row == its own row and the policy values
+// that follow; otherwise each row reads its flags and penalty row from
+// f.row_info and its policy from f.a.params.
 template <int DT>
-__global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
+__global__ __launch_bounds__(kThreads) void select_fast_kernel(
+    const void *logits, const uint32_t *pen_slots, uint32_t stride, uint32_t V,
+    uint32_t packed, uint32_t u_top_k, float u_minp_offset, float u_repetition,
+    float u_repetition_inverse, float u_presence, float u_frequency, FastLaunch f) {
   constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
                 LOADS = Geo<DT>::LOADS;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
@@ -2040,26 +2059,12 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
   static_assert(TPL == 32, "one drop bit per register");
   const SampleLaunch &a = f.a;
   __shared__ FastLds s;
-  // Every kernel argument the loads need, read in one round trip before the
-  // first branch (the compiler would otherwise fetch some inside branches,
-  // one dependent round trip each, before the first logit load).
-  const uint32_t chunk = blockIdx.x, lrow = blockIdx.y;
-  const uint32_t info = f.row_info[lrow];
-  const uint32_t S = a.chunks, V = a.vocabulary, row = f.row_base + lrow;
-  const uint32_t slot_count = f.slot_count;
-  const uint32_t *pen_slots = f.pen_slots;
-  const void *logits = a.logits;
-  const uint64_t stride = a.stride;
-  const uint32_t *masks = a.masks;
-  const uint64_t mask_stride = a.mask_stride;
-  const RowParams *params = a.params;
-  const uint32_t stop0 = a.stop0, stop1 = a.stop1;
-  BlockHeader *headers = a.headers;
-  uint64_t *cands = a.cands;
-  asm volatile("" ::"s"(info), "s"(S), "s"(V), "s"(row), "s"(slot_count),
-               "s"(pen_slots), "s"(logits), "s"(stride), "s"(masks),
-               "s"(mask_stride), "s"(params), "s"(stop0), "s"(stop1),
-               "s"(headers), "s"(cands));
+  const uint32_t S = (packed >> 8) & 0xffu;
+  const uint32_t slot_count = (packed & 0x10000u) ? 512u : 256u;
+  const uint32_t row_base = ((packed >> 17) & 0x3fffu) << 8;
+  const uint32_t chunk = blockIdx.x, lrow = blockIdx.y, row = row_base + lrow;
+  const bool uni = (packed >> 31) != 0;
+  const uint32_t info = uni ? ((packed & 0xffu) | (row << 8)) : f.row_info[lrow];
   const uint32_t flags = info & 0xffu, prow = info >> 8;
   const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const uint32_t base = chunk * CHUNK;
@@ -2084,9 +2089,10 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
   std::conditional_t<DT == 0, float, uint32_t> tail[VEC];
   uint32_t tail_j;
   fast_load<DT>(logits, stride, V, row, base, full, xs, tail, tail_j);
-  const uint32_t *mrow = masks + (uint64_t)row * mask_stride;
   uint32_t mw[LOADS];
+  const uint32_t *mrow = nullptr;
   if (constrained) {
+    mrow = a.masks + (uint64_t)row * a.mask_stride;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const uint32_t t0 = lane_base + j * SLAB;
@@ -2094,11 +2100,24 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
     }
   }
   if (penalized) __syncthreads();  // drop bitmaps cleared
-  // The row's policy by one scalar load issued after that barrier (a barrier
-  // waits for every outstanding scalar load); its wait sits at the first use.
-  // The compiler itself would read it with vector loads, since it cannot
-  // rule out that this kernel writes the records.
-  RowPolicyRegs prr = issue_row_policy(params + row);
+  // A non-uniform row's policy by one scalar load issued after that barrier
+  // (a barrier waits for every outstanding scalar load); its wait sits at the
+  // first use. The compiler itself would read it with vector loads, since it
+  // cannot rule out that this kernel writes the records.
+  RowPolicyRegs prr{};
+  if (!uni) prr = issue_row_policy(a.params + row);
+  auto row_policy = [&]() -> RowParams {
+    if (!uni) return wait_row_policy(prr);
+    RowParams r{};
+    r.flags = flags;
+    r.top_k = u_top_k;
+    r.minp_offset = u_minp_offset;
+    r.repetition = u_repetition;
+    r.repetition_inverse = u_repetition_inverse;
+    r.presence = u_presence;
+    r.frequency = u_frequency;
+    return r;
+  };
 
   // 2. Penalized tokens: recorded in the drop bitmaps, re-read by their
   // slot's thread, penalized there (sampling.metal:928-963) and admitted
@@ -2129,7 +2148,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
     }
     __syncthreads();  // bitmaps complete
     drop = s.bm[tid];
-    rp = wait_row_policy(prr);
+    rp = row_policy();
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
       if (slot[k]) {
@@ -2139,7 +2158,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
         float v = penalize(x, count, rp.repetition, rp.repetition_inverse,
                            rp.presence, rp.frequency);
         if (constrained && !((mword[k] >> (t & 31)) & 1u)) v = kNotAdmitted;
-        if ((flags & kRowExcludeStop) && (t == stop0 || t == stop1)) v = kNotAdmitted;
+        if ((flags & kRowExcludeStop) && (t == a.stop0 || t == a.stop1)) v = kNotAdmitted;
         side.tok[k] = t;
         side.val[k] = v;
       }
@@ -2158,7 +2177,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
   if (flags & kRowExcludeStop) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const uint32_t st = k ? stop1 : stop0;
+      const uint32_t st = k ? a.stop1 : a.stop0;
       if (st >= base && st < base + CHUNK) {
         stop_here = true;
         const uint32_t o = st - base;
@@ -2185,7 +2204,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
     }
   }
 
-  if (!penalized) rp = wait_row_policy(prr);
+  if (!penalized) rp = row_policy();
 
   // 3. The lane's largest admitted value (fmax skips NaN operands, so the NaN
   // it starts from survives only when the lane admits nothing).
@@ -2194,7 +2213,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
   for (int i = 0; i < TPL; ++i) mx = __builtin_fmaxf(mx, xs[i]);
 #pragma unroll
   for (int k = 0; k < SPT; ++k) mx = __builtin_fmaxf(mx, side.val[k]);
-  BlockHeader *hdr = headers + (uint64_t)row * S + chunk;
+  BlockHeader *hdr = a.headers + (uint64_t)row * S + chunk;
 
   if (!(flags & kRowSampled)) {
     // Greedy (sampling.metal:1427-1464): the block maximum, then the lowest
@@ -2279,7 +2298,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(FastLaunch f) {
     over |= n > kWaveCandidates;
     off[k + 1] = off[k] + min(n, kWaveCandidates);
   }
-  uint64_t *dst = cands + ((uint64_t)row * S + chunk) * kBlockCandidates;
+  uint64_t *dst = a.cands + ((uint64_t)row * S + chunk) * kBlockCandidates;
   if (!over)
     for (uint32_t i = tid; i < off[kWaves]; i += kThreads) {
       const uint32_t k = (i >= off[1]) + (i >= off[2]) + (i >= off[3]);
@@ -3312,14 +3331,25 @@ int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
 }
 
 int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
-                       void *stream, void *start_event, void *stop_event) {
+                       const RowParams *uniform, void *stream, void *start_event,
+                       void *stop_event) {
   const dim3 grid(f.a.chunks, rows), block(kThreads);
   const hipStream_t st = (hipStream_t)stream;
   const hipEvent_t e0 = (hipEvent_t)start_event, e1 = (hipEvent_t)stop_event;
+  const RowParams u = uniform ? *uniform : RowParams{};
+  const uint32_t packed = (uniform ? 0x80000000u | (u.flags & 0xffu) : 0u) |
+                          (f.a.chunks << 8) | (f.slot_count == 512u ? 0x10000u : 0u) |
+                          ((f.row_base >> 8) << 17);
+  auto go = [&](auto kernel) {
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, st, e0, e1, 0, f.a.logits, f.pen_slots,
+                          (uint32_t)f.a.stride, f.a.vocabulary, packed, u.top_k,
+                          u.minp_offset, u.repetition, u.repetition_inverse, u.presence,
+                          u.frequency, f);
+  };
   if (dtype == 0)
-    hipExtLaunchKernelGGL(select_fast_kernel<0>, grid, block, 0, st, e0, e1, 0, f);
+    go(select_fast_kernel<0>);
   else
-    hipExtLaunchKernelGGL(select_fast_kernel<1>, grid, block, 0, st, e0, e1, 0, f);
+    go(select_fast_kernel<1>);
   return (int)hipGetLastError();
 }
 

@@ -613,6 +613,18 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
       F.pen_slots = a->penalties->slots;
       F.slot_count = a->penalties->slot_count;
     }
+    // A uniform launch: every row has the same policy, and penalized rows
+    // read their own table row; the kernel then takes the policy from its
+    // preloaded arguments instead of a memory read per block.
+    bool uniform = true;
+    for (uint32_t r = 0; uniform && r < rows; ++r) {
+      const jf::RowParams &p0 = params[0], &p = params[r];
+      uniform = p.flags == p0.flags && p.top_k == p0.top_k &&
+                p.minp_offset == p0.minp_offset && p.repetition == p0.repetition &&
+                p.repetition_inverse == p0.repetition_inverse &&
+                p.presence == p0.presence && p.frequency == p0.frequency &&
+                (!(p.flags & jf::kRowPenalized) || p.penalty_row == r);
+    }
     for (uint32_t r0 = 0; r0 < rows && e == hipSuccess; r0 += jf::kKernargRows) {
       const uint32_t n = std::min<uint32_t>(rows - r0, jf::kKernargRows);
       F.row_base = r0;
@@ -622,7 +634,7 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
         F.row_info[r] = (rp.flags & 0xffu) | (prow << 8);
       }
       const bool first = r0 == 0, last = r0 + n == rows;
-      e = jf::launch_select_fast(F, n, a->dtype, stream,
+      e = jf::launch_select_fast(F, n, a->dtype, uniform ? &params[0] : nullptr, stream,
                                  first ? a->select_start_event : nullptr,
                                  last ? a->select_done_event : nullptr);
     }
