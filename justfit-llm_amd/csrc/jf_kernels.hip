@@ -1888,8 +1888,8 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
 // every penalty chunk within its fixed slots, no extra verify tokens), with a
 // load phase that requests everything before it waits on anything:
 //   1. the chunk's penalty slots (their address needs only the kernel
-//      arguments), then the logits with nontemporal 16-byte loads, then a
-//      constrained row's mask words;
+//      arguments), then the logits with 16-byte loads, then a constrained
+//      row's mask words;
 //   2. each slot's thread re-reads its token's logit (and mask word): the
 //      block's own request for that line is already in flight, so the read
 //      merges with it in L2 instead of waiting behind the whole stream. The
@@ -1974,11 +1974,13 @@ __device__ __forceinline__ void fast_load(const void *logits, uint64_t stride,
   const uint32_t vfull = V - V % VEC;  // tokens covered by whole vectors
   // One load sequence for both (a branch here makes the compiler wait
   // between the partial chunk's loads): the address is selected, not the code.
+  // Plain loads: the lines stay in L2 for the penalty threads' re-reads
+  // (streaming loads would send many of those back to HBM).
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
     const uint32_t t0 = lane_base + j * SLAB;
     const uint32_t tl = full || t0 + VEC <= vfull ? t0 : vfull - VEC;
-    v[j] = __builtin_nontemporal_load((const u32x4 *)(rowp + tl));
+    v[j] = *(const u32x4 *)(rowp + tl);
   }
   tail_j = 0xffu;
   if (!full) {
@@ -2524,11 +2526,17 @@ __device__ __noinline__ void merge_small_general(uint32_t row) {
   merge_sampled<DT>(a, rp, row, g_small_lds);
 }
 
+// The arguments the first loads need lead the signature (14 dwords, no
+// padding): the hardware preloads them into scalar registers at wave launch.
+// They repeat fields of `a` (drafted_rows is 0 when there are no drafts).
 template <int DT>
-__global__ __launch_bounds__(kThreads) void merge_small_kernel(SampleLaunch a) {
+__global__ __launch_bounds__(kThreads) void merge_small_kernel(
+    const BlockHeader *headers, const uint64_t *cands, const RowParams *params,
+    const float *uniforms, const uint32_t *uniform_index, uint32_t S,
+    uint32_t uniform_offset, uint32_t uniform_stride, uint32_t drafted_rows,
+    SampleLaunch a) {
   Lds &s = g_small_lds;
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
-  const uint32_t S = a.chunks;
   // Every address of the row, computed once and held in vector registers:
   // the general path's register pressure would otherwise have the compiler
   // reload (and wait for) kernel arguments between the loads below. A load
@@ -2538,21 +2546,22 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(SampleLaunch a) {
   typedef __attribute__((address_space(1))) const uint64_t GlobalU64;
   typedef __attribute__((address_space(1))) const uint32_t GlobalU32;
   typedef __attribute__((address_space(1))) const float GlobalF32;
-  const bool has_draft = a.draft_tokens && row < a.drafted_rows;
-  const bool has_index = a.uniform_index != nullptr, has_uniform = a.uniforms != nullptr;
-  const BlockHeader *hrow = a.headers + (uint64_t)row * S;
+  const bool has_draft = row < drafted_rows;
+  const bool has_index = uniform_index != nullptr, has_uniform = uniforms != nullptr;
+  const BlockHeader *hrow = headers + (uint64_t)row * S;
   uint64_t hbase = (uint64_t)(hrow + (tid < S ? tid : 0u));
-  uint64_t cbase = (uint64_t)(a.cands + (uint64_t)row * S * kBlockCandidates);
-  uint64_t uaddr = has_index     ? (uint64_t)(a.uniform_index + row)
-                   : has_uniform ? (uint64_t)(a.uniforms + a.uniform_offset + row * a.uniform_stride)
+  uint64_t cbase = (uint64_t)(cands + (uint64_t)row * S * kBlockCandidates);
+  uint64_t uaddr = has_index     ? (uint64_t)(uniform_index + row)
+                   : has_uniform ? (uint64_t)(uniforms + uniform_offset + (uint64_t)row * uniform_stride)
                                  : (uint64_t)hrow;
-  uint64_t ubase = has_uniform ? (uint64_t)a.uniforms : (uint64_t)hrow;
-  uint64_t daddr = has_draft ? (uint64_t)(a.draft_tokens + row) : (uint64_t)hrow;
-  uint64_t qaddr = has_draft ? (uint64_t)(a.cand_ids + (uint64_t)row * 16 + (tid & 15))
-                             : (uint64_t)hrow;
-  uint64_t paddr = has_draft ? (uint64_t)(a.cand_probs + (uint64_t)row * 16 + (tid & 15))
-                             : (uint64_t)hrow;
-  uint64_t pbase = (uint64_t)(a.params + row);
+  uint64_t ubase = has_uniform ? (uint64_t)uniforms : (uint64_t)hrow;
+  uint64_t daddr = (uint64_t)hrow, qaddr = (uint64_t)hrow, paddr = (uint64_t)hrow;
+  if (has_draft) {
+    daddr = (uint64_t)(a.draft_tokens + row);
+    qaddr = (uint64_t)(a.cand_ids + (uint64_t)row * 16 + (tid & 15));
+    paddr = (uint64_t)(a.cand_probs + (uint64_t)row * 16 + (tid & 15));
+  }
+  uint64_t pbase = (uint64_t)(params + row);
   asm volatile("" : "+v"(hbase), "+v"(cbase), "+v"(uaddr), "+v"(ubase), "+v"(daddr),
                "+v"(qaddr), "+v"(paddr), "+s"(pbase));
   // Every load of the row, before any wait: the uniform (or its index), the
@@ -3364,10 +3373,17 @@ int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream) {
 
 int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream) {
   const dim3 grid(a.rows), block(kThreads);
+  const hipStream_t st = (hipStream_t)stream;
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, a.headers, (const uint64_t *)a.cands,
+                       a.params, a.uniforms, a.uniform_index, a.chunks,
+                       (uint32_t)a.uniform_offset, (uint32_t)a.uniform_stride,
+                       a.draft_tokens ? a.drafted_rows : 0u, a);
+  };
   if (dtype == 0)
-    hipLaunchKernelGGL(merge_small_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
+    go(merge_small_kernel<0>);
   else
-    hipLaunchKernelGGL(merge_small_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+    go(merge_small_kernel<1>);
   return (int)hipGetLastError();
 }
 

@@ -597,7 +597,7 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   // The fast selection kernel takes the launch when every row qualifies:
   // aligned rows, no extra verify tokens, and penalty rows whose chunks fit
   // their fixed slots (and vocabularies of at least one 16-byte vector).
-  bool fast = aligned && V >= 8;
+  bool fast = aligned && V >= 8 && L.stride <= 0xffffffffull;
   for (uint32_t r = 0; fast && r < rows; ++r) {
     const jf::RowParams &rp = params[r];
     if (rp.extra_count) fast = false;
@@ -645,7 +645,8 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   if (e != hipSuccess) return hip_fail((hipError_t)e, "select launch");
   // The small-K merge takes launches whose sampled rows keep at most 64
   // tokens and read sparse draft probabilities (or none).
-  bool small = !staged && !a->draft_q;
+  bool small = !staged && !a->draft_q && a->uniform_offset <= 0xffffffffull &&
+               a->uniform_stride <= 0xffffffffull;
   for (uint32_t r = 0; small && r < rows; ++r) {
     const jf::RowParams &rp = params[r];
     if ((rp.flags & jf::kRowSampled) && (!(rp.flags & jf::kRowTopK) || rp.top_k > 64u))
