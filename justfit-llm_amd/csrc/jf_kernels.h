@@ -148,6 +148,8 @@ struct FastLaunch {
   const uint32_t *pen_slots;  // [table rows][chunks][slot_count]
   uint32_t slot_count;        // 256 or 512
   uint32_t row_base;          // sampler row of blockIdx.y == 0
+  uint32_t fuse_greedy;       // every row greedy: the last block of a row
+                              // finishes it (no merge launch)
   uint32_t row_info[kKernargRows];  // RowFlags | penalty row << 8
 };
 

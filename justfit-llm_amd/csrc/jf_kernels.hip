@@ -2237,9 +2237,43 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     const uint32_t wid = wave_min_u32(id);
     if (lane == 0) s.wu[w] = wid;
     __syncthreads();
+    const float bv = M == M ? M : -__builtin_inff();
+    const uint32_t bi = min(min(s.wu[0], s.wu[1]), min(s.wu[2], s.wu[3]));
+    if (!f.fuse_greedy) {
+      if (tid == 0) {
+        hdr->best_value = bv;
+        hdr->best_id = bi;
+      }
+      return;
+    }
+    // Every row greedy: the row's last block to arrive takes the largest
+    // chunk best, the lowest id among equals (the reference's last-arriving
+    // group, split_reduce.h:14-45). Summaries go out with device-coherent
+    // stores that complete before the arrival; the counter returns to zero.
     if (tid == 0) {
-      hdr->best_value = M == M ? M : -__builtin_inff();
-      hdr->best_id = min(min(s.wu[0], s.wu[1]), min(s.wu[2], s.wu[3]));
+      st_dev(&hdr->best_value, bv);
+      st_dev(&hdr->best_id, bi);
+      wait_memory();
+      const uint32_t prev = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      s.wcount[0] = prev == S - 1 ? 1u : 0u;
+      if (prev == S - 1) st_dev(a.counters + row, 0u);
+    }
+    __syncthreads();
+    if (s.wcount[0] && w == 0) {
+      float v = -__builtin_inff();
+      uint32_t i = kNoToken;
+      for (uint32_t c = lane; c < S; c += 64) {
+        const BlockHeader *h = a.headers + (uint64_t)row * S + c;
+        const float hv = ld_dev(&h->best_value);
+        const uint32_t hi = ld_dev(&h->best_id);
+        if (hv > v || (hv == v && hi < i)) {
+          v = hv;
+          i = hi;
+        }
+      }
+      wave_argmax(v, i);
+      if (lane == 0) write_result(a, row, i, 0.0f, 0);
     }
     return;
   }

@@ -606,9 +606,12 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
       fast = false;
   }
   int e = hipSuccess;
+  // A launch of greedy rows only is finished inside the fast selection.
+  const bool fused = fast && !any_sampled;
   if (fast) {
     jf::FastLaunch F{};
     F.a = L;
+    F.fuse_greedy = fused ? 1u : 0u;
     if (a->penalties) {
       F.pen_slots = a->penalties->slots;
       F.slot_count = a->penalties->slot_count;
@@ -652,9 +655,11 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
     if ((rp.flags & jf::kRowSampled) && (!(rp.flags & jf::kRowTopK) || rp.top_k > 64u))
       small = false;
   }
-  e = small ? jf::launch_merge_small(L, a->dtype, stream)
-            : jf::launch_merge(L, a->dtype, stream);
-  if (e != hipSuccess) return hip_fail((hipError_t)e, "merge launch");
+  if (!fused) {
+    e = small ? jf::launch_merge_small(L, a->dtype, stream)
+              : jf::launch_merge(L, a->dtype, stream);
+    if (e != hipSuccess) return hip_fail((hipError_t)e, "merge launch");
+  }
   if (staged) {
     for (uint32_t stage = jf::kStageCount1; stage <= jf::kStageLast; ++stage) {
       if (stage == jf::kStageCount1 && !need_count1) continue;
