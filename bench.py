@@ -12,6 +12,7 @@ serve a repeated step. Prints one JSON line.
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -260,14 +261,19 @@ def cpu_baseline(w, seconds):
 
 
 def read_traffic(cfg):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+    """HBM bytes per launch and the kernel they were counted on, from the
+    committed rocprofv3 --pmc summary (its first line names the kernel)."""
     path = os.path.join(REPO, "profiles", f"select_c{cfg}_traffic.txt")
     if not os.path.exists(path):
-        return None
+        return None, None
+    traffic, kernel = None, None
     for line in open(path):
+        m = re.match(r"# HBM traffic per launch of (\S+):", line)
+        if m:
+            kernel = m.group(1)
         if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":")[1])
-    return None
+            traffic = float(line.split(":")[1])
+    return traffic, kernel
 
 
 def copy_calibration():
@@ -347,7 +353,7 @@ def main():
     sel_mean, sel_p50 = time_select(g, args.warmup + K, K)
     achieved = w["select_bytes"] / (sel_mean * 1e-6) / 1e9
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
-    traffic = read_traffic(args.config)
+    traffic, kernel = read_traffic(args.config)
     line = {
         "metric": "sampling steps/sec at B=64,V=151936; achieved HBM GB/s vs peak; p50 us/step",
         "value": 1000.0 / ms_per_step,
@@ -370,7 +376,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
                      "traffic": traffic,
-                     "kernel": "jf::select_kernel<%d>" % (1 if "bf16" in w["dtype"] else 0),
+                     "kernel": kernel or "jf selection kernel",
                      "kernel_mean_us": sel_mean, "kernel_p50_us": sel_p50,
                      "algorithmic_bytes": w["select_bytes"],
                      "step_achieved": step_gbs,
