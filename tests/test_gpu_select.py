@@ -188,6 +188,65 @@ def test_small_topk_with_many_ties_at_the_kth_key():
     assert_same(g, r)
 
 
+@pytest.mark.parametrize("bf16,drafted", [(False, False), (True, False), (False, True)])
+def test_small_topk_edge_rows(bf16, drafted):
+    """Launches whose sampled rows all keep at most 64 tokens (the small-K
+    merge): constant rows and rows tied everywhere (overflowing chunks, the
+    general path), -inf and NaN rows, penalties, a greedy row, sparse drafts,
+    and a partial last chunk, in fp32 and bf16."""
+    rng = np.random.default_rng(41 + bf16 + 2 * drafted)
+    V = 3 * 8192 + 100
+    rows = 10
+    x = rand_logits(rng, rows, V)
+    x[0] = 1.0
+    x[1] = -np.inf
+    x[1, [5, 9000, V - 1]] = [0.5, 1.5, -2.0]
+    x[4] = np.round(x[4], 1)
+    x[5, ::2] = np.nan
+    x[6] = np.where(np.arange(V) % 3 == 0, 2.0, -1.0)
+    x[9] = np.nan
+    hist = [rng.integers(0, V, 300).astype(np.uint32) for _ in range(rows)]
+    pols = [J.policy(temperature=1.0, top_k=64), J.policy(temperature=0.9, top_k=50),
+            J.policy(temperature=0.8, top_k=40, top_p=0.9, presence=0.3, frequency=0.2),
+            J.policy(repetition=1.4), J.policy(temperature=1.1, top_k=64, min_p=0.05),
+            J.policy(temperature=1.0, top_k=16), J.policy(temperature=1.0, top_k=33, presence=0.5),
+            J.policy(temperature=0.7, top_k=1), J.policy(temperature=1.0, top_k=20, top_p=0.6),
+            J.policy(temperature=1.0, top_k=8)]
+    u = rng.random(rows).astype(np.float32)
+    kw = dict(histories=hist, generated=[200] * rows, mark_prompt=[True] * rows, uniforms=u,
+              kept_capacity=64)
+    if drafted:
+        draft = rng.integers(0, V, rows).astype(np.uint32)
+        draft[6] = 3 * 7  # a tied token
+        cand = rng.integers(0, V, (rows, 16)).astype(np.uint32)
+        cand[:, 0] = draft
+        kw.update(draft_tokens=draft, drafted_rows=rows - 1, cand_ids=cand,
+                  cand_probs=rng.dirichlet(np.ones(16), rows).astype(np.float32))
+    if bf16:
+        kw["logits_bf16"] = WL.to_bf16_bits(x)
+    else:
+        kw["logits"] = x
+    g, r = both(V, pols, **kw)
+    assert_same(g, r)
+    assert g["tokens"][9] == NO
+
+
+def test_small_topk_over_row_groups():
+    """More rows than one selection launch carries (256 rows per launch):
+    the row groups' summaries meet in one merge."""
+    rng = np.random.default_rng(43)
+    V = 9000
+    rows = 300
+    x = rand_logits(rng, rows, V, decimals=1)
+    hist = [rng.integers(0, V, 50).astype(np.uint32) for _ in range(rows)]
+    pols = [J.policy(temperature=0.9, top_k=10, top_p=0.8, presence=0.2) if i % 7 else
+            J.policy(repetition=1.2) for i in range(rows)]
+    u = rng.random(rows).astype(np.float32)
+    g, r = both(V, pols, logits=x, histories=hist, generated=[20] * rows,
+                mark_prompt=[True] * rows, uniforms=u, kept_capacity=16)
+    assert_same(g, r)
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 def test_overflowing_chunks_reselected(bf16):
     """Chunks with more than 1024 candidates (flat or tied values) are
