@@ -266,6 +266,64 @@ typedef struct jf_accept_tree_args {
 int jf_accept_tree(jf_sampler *sampler, const jf_accept_tree_args *args,
                    void *stream);
 
+/* ---- draft selector ---------------------------------------------------- */
+
+/* The DFlash draft's proposal policy: ops::DraftSelector
+ * (source/runtime/ops/DraftSelector.hpp:40-68, DraftSelector.cpp:43-154),
+ * kernels draft_select_top16_sharded / draft_select_edges /
+ * draft_select_dflash (sampling.metal:995-1359). Lane geometry as in
+ * ExecutionGeometry.h: 8 query rows, 7 proposal positions, 16 candidates per
+ * position, selector rank 256. */
+#define JF_DRAFT_QUERY_ROWS 8u
+#define JF_DRAFT_POSITIONS 7u
+#define JF_DRAFT_SELECTOR_RANK 256u
+
+typedef struct jf_draft_selector jf_draft_selector;
+
+/* DraftSelector::DraftSelector(vocabulary) (DraftSelector.cpp:43-46), plus
+ * the scratch DraftSelector::workspace sizes (DraftSelector.cpp:48-57),
+ * owned here for up to max_lanes lanes per call. Creates on the current HIP
+ * device; synchronous. */
+int jf_draft_selector_create(uint32_t vocabulary, uint32_t max_lanes,
+                             jf_draft_selector **out);
+int jf_draft_selector_destroy(jf_draft_selector *selector);
+
+/* DraftSelector::add (DraftSelector.cpp:59-154) over `lanes` lanes. Lane l
+ * reads its query rows logits + (l*8 + r) * logits_stride (fp32; rows 1..7
+ * are proposal positions 0..6) and selector_hidden + (l*8 + r) * 256 (bf16
+ * bits), the bf16 codebooks [vocabulary][256] (16-byte aligned), anchors[l]
+ * and policies[l] (host; temperature 0 walks greedily, otherwise the lane
+ * draws with uniforms + l*40 + JF_UNIFORM_PROPOSALS + position). Writes, per
+ * proposal row s = l*7 + position: candidates + s*16 and unary + s*16 (the
+ * row's top 16 in (logit desc, id asc) order and their logits; slots past
+ * the row's non-NaN tokens hold JF_NO_TOKEN and -inf), proposed_tokens[s],
+ * and for a sampling lane proposal_probs + s*16 (the walk's candidate
+ * probabilities). Each edge score is the fp32 sum over the rank, in
+ * ascending order, of (predecessor codebook x hidden) x successor codebook;
+ * ids are clamped into the codebooks as the reference does. Optional
+ * select_start_event/select_done_event (hipEvent_t, with no counterpart in
+ * the reference) bracket the top-16 kernel. */
+typedef struct jf_draft_select_args {
+  uint32_t lanes;
+  const float *logits;                   /* device */
+  uint64_t logits_stride;                /* elements, >= vocabulary */
+  const uint16_t *selector_hidden;       /* device */
+  const uint16_t *predecessor_codebook;  /* device */
+  const uint16_t *successor_codebook;    /* device */
+  const uint32_t *anchors;               /* host, lanes entries */
+  const jf_policy *policies;             /* host, lanes entries */
+  const float *uniforms;                 /* device; needed when a lane samples */
+  uint32_t *candidates;                  /* device */
+  float *unary;                          /* device */
+  uint32_t *proposed_tokens;             /* device */
+  float *proposal_probs;                 /* device; needed when a lane samples */
+  void *select_start_event;
+  void *select_done_event;
+} jf_draft_select_args;
+
+int jf_draft_select(jf_draft_selector *selector,
+                    const jf_draft_select_args *args, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

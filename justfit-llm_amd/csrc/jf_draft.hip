@@ -1,0 +1,388 @@
+// The draft selector on gfx950: the DFlash draft's proposal policy
+// (draft_select_top16_sharded, draft_select_edges, draft_select_dflash in
+// sampling.metal:995-1359, dispatched by DraftSelector.cpp:100-154).
+//
+// A lane has 8 query rows of fp32 draft logits; rows 1..7 are its proposal
+// positions. Two launches:
+//   draft_top16_kernel  one block per (8192-token chunk, proposal row): the
+//                       chunk's exact top 16 in (value desc, id asc) order;
+//                       the row's last block to arrive merges the chunks into
+//                       the row's candidates and unary scores.
+//   draft_edges_kernel  one block per (position, lane): the 16 x 16 table of
+//                       edge scores from the previous position's candidates
+//                       (the anchor at position 0) to this position's; the
+//                       lane's last block walks the 7 positions, greedily or
+//                       drawing at the lane's temperature.
+// Edge scores are fp32 sums over the selector rank in ascending dimension
+// order (each product of bf16 operands is exact in fp32); the reference sums
+// the same terms in another order.
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+
+#include "jf_device.h"
+#include "jf_kernels.h"
+
+namespace jf {
+
+namespace {
+
+constexpr uint32_t kDraftChunk = 8192;   // fp32 tokens per block
+constexpr int kDraftLoads = 8;           // 16-byte loads per thread
+constexpr int kDraftTokens = 32;         // tokens per thread
+constexpr uint32_t kDraftK = 16;
+constexpr uint32_t kRank = 256;
+constexpr uint32_t kWaveCap = 256;       // staged candidates per wave
+constexpr uint32_t kPad = kRank + 1;     // LDS row pitch of the edge operands
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16f(uint32_t b) { return u2f(b << 16); }
+__device__ __forceinline__ float readlane_f32(float v, int l) {
+  return u2f(readlane_u32(f2u(v), l));
+}
+
+// (key << 32 | ~id): larger means earlier in (value desc, id asc); ids are
+// unique within a row, so the order is total. 0 is the empty slot
+// (-inf, kNoToken), after every real entry.
+__device__ __forceinline__ uint64_t draft_comp(float x, uint32_t id) {
+  return ((uint64_t)logit_key(x) << 32) | (uint32_t)~id;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  auto step = [&](uint64_t o) { v = o > v ? o : v; };
+  step(xor_u64<1>(v));
+  step(xor_u64<2>(v));
+  step(xor_u64<4>(v));
+  step(xor_u64<8>(v));
+  step(xor_u64<16>(v));
+  step(xor_u64<32>(v));
+  return v;
+}
+
+struct __align__(16) DraftTopLds {
+  uint64_t comp[kWaves * kWaveCap];   // staged candidates, then the row merge
+  uint32_t vbits[kWaves * kWaveCap];  // their values' bits
+  uint64_t top[kDraftK];
+  uint32_t topv[kDraftK];
+  uint64_t wbest[kWaves];
+  uint32_t wcount[kWaves];
+  uint32_t wbound[kWaves];
+  uint32_t last;
+};
+
+}  // namespace
+
+// One chunk of one proposal row. Each thread holds 32 tokens; each wave's
+// 4th largest lane maximum bounds the block (at least 16 tokens are at or
+// above the smallest of the four), so only the tokens at or above it are
+// staged and ranked. A chunk whose staged tokens overflow (ties) takes its
+// top 16 by 16 rounds of block maxima instead. The row's last block merges
+// the chunks' top 16 by rank counting.
+template <bool ALIGNED>
+__global__ __launch_bounds__(kThreads) void draft_top16_kernel(DraftLaunch d) {
+  __shared__ DraftTopLds s;
+  const uint32_t chunk = blockIdx.x, row = blockIdx.y;
+  const uint32_t lane_index = row / kDraftPositions, p = row % kDraftPositions;
+  const uint32_t V = d.vocabulary, S = d.chunks;
+  const float *rowp = d.logits + ((uint64_t)lane_index * kDraftQueryRows + p + 1) * d.stride;
+  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const uint32_t base = chunk * kDraftChunk, lane_base = base + tid * 4;
+  auto token_of = [&](int i) -> uint32_t { return lane_base + (i >> 2) * 1024 + (i & 3); };
+
+  float x[kDraftTokens];
+  if (ALIGNED && base + kDraftChunk <= V) {
+#pragma unroll
+    for (int j = 0; j < kDraftLoads; ++j) {
+      const f32x4 v = *(const f32x4 *)(rowp + lane_base + j * 1024);
+      x[j * 4 + 0] = v.x;
+      x[j * 4 + 1] = v.y;
+      x[j * 4 + 2] = v.z;
+      x[j * 4 + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kDraftTokens; ++i) {
+      const uint32_t t = token_of(i);
+      x[i] = t < V ? rowp[t] : __builtin_nanf("");
+    }
+  }
+  if (tid < kDraftK) {
+    s.top[tid] = 0;
+    s.topv[tid] = f2u(-__builtin_inff());
+  }
+  // The lane's largest key among its non-NaN tokens (0: none), then each
+  // wave's 4th largest by 32 ballots.
+  uint32_t mkey = 0;
+#pragma unroll
+  for (int i = 0; i < kDraftTokens; ++i)
+    if (x[i] == x[i]) mkey = max(mkey, logit_key(x[i]));
+  uint32_t wb = 0;
+#pragma unroll
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t trial = wb | (1u << b);
+    if (__popcll(ballot(mkey >= trial)) >= 4) wb = trial;
+  }
+  if (lane == 0) s.wbound[w] = wb;
+  __syncthreads();
+  const uint32_t bound = min(min(s.wbound[0], s.wbound[1]), min(s.wbound[2], s.wbound[3]));
+
+  // Stage the tokens at or above the bound, per wave.
+  uint32_t run = 0;
+  uint64_t *stage = s.comp + w * kWaveCap;
+  uint32_t *vstage = s.vbits + w * kWaveCap;
+#pragma unroll
+  for (int i = 0; i < kDraftTokens; ++i) {
+    const bool hit = x[i] == x[i] && logit_key(x[i]) >= bound;
+    const uint64_t m = ballot(hit);
+    if (m) {
+      const uint32_t slot = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, run));
+      if (hit && slot < kWaveCap) {
+        stage[slot] = draft_comp(x[i], token_of(i));
+        vstage[slot] = f2u(x[i]);
+      }
+      run += (uint32_t)__popcll(m);
+    }
+  }
+  if (lane == 0) s.wcount[w] = run;
+  __syncthreads();
+  uint32_t n[kWaves], over = 0;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) {
+    n[k] = s.wcount[k];
+    over |= n[k] > kWaveCap;
+  }
+  if (!over) {
+    // Rank by counting: an entry's rank is the number of entries above it.
+    // Each wave ranks its own staged entries.
+    for (uint32_t e = lane; e < n[w]; e += 64) {
+      const uint64_t me = stage[e];
+      uint32_t rank = 0;
+      for (uint32_t k = 0; k < kWaves; ++k)
+        for (uint32_t e2 = 0; e2 < n[k]; ++e2) rank += s.comp[k * kWaveCap + e2] > me ? 1u : 0u;
+      if (rank < kDraftK) {
+        s.top[rank] = me;
+        s.topv[rank] = vstage[e];
+      }
+    }
+  } else {
+    // Ties: 16 rounds of the block's largest remaining entry.
+    uint32_t removed = 0;
+    for (uint32_t r = 0; r < kDraftK; ++r) {
+      uint64_t best = 0;
+#pragma unroll
+      for (int i = 0; i < kDraftTokens; ++i) {
+        const uint64_t c = x[i] == x[i] && !((removed >> i) & 1u) ? draft_comp(x[i], token_of(i)) : 0ull;
+        best = c > best ? c : best;
+      }
+      const uint64_t wbest = wave_max_u64(best);
+      __syncthreads();  // the previous round's readers are done
+      if (lane == 0) s.wbest[w] = wbest;
+      __syncthreads();
+      uint64_t top = s.wbest[0];
+#pragma unroll
+      for (int k = 1; k < kWaves; ++k) top = s.wbest[k] > top ? s.wbest[k] : top;
+      if (top == 0) break;  // uniform: nothing left
+      if (best == top) {
+#pragma unroll
+        for (int i = 0; i < kDraftTokens; ++i)
+          if (x[i] == x[i] && !((removed >> i) & 1u) && draft_comp(x[i], token_of(i)) == top) {
+            removed |= 1u << i;
+            s.top[r] = top;
+            s.topv[r] = f2u(x[i]);
+          }
+      }
+    }
+  }
+  __syncthreads();
+  // The chunk's top 16, then one arrival per block; the row's last block
+  // merges.
+  const uint64_t pi = ((uint64_t)row * S + chunk) * kDraftK;
+  if (tid < kDraftK) {
+    st_dev(d.part_comp + pi + tid, s.top[tid]);
+    st_dev(d.part_vbits + pi + tid, s.topv[tid]);
+  }
+  wait_memory();
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(d.counters + row, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    s.last = prev == S - 1 ? 1u : 0u;
+    if (prev == S - 1) st_dev(d.counters + row, 0u);
+  }
+  __syncthreads();
+  if (!s.last) return;
+
+  const uint32_t total = S * kDraftK;  // <= 1024
+  const uint64_t p0 = (uint64_t)row * S * kDraftK;
+  for (uint32_t e = tid; e < total; e += kThreads) {
+    s.comp[e] = ld_dev(d.part_comp + p0 + e);
+    s.vbits[e] = ld_dev(d.part_vbits + p0 + e);
+  }
+  if (tid < kDraftK) {
+    s.top[tid] = 0;
+    s.topv[tid] = f2u(-__builtin_inff());
+  }
+  __syncthreads();
+  for (uint32_t e = tid; e < total; e += kThreads) {
+    const uint64_t me = s.comp[e];
+    if (!me) continue;
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < total; ++j) rank += s.comp[j] > me ? 1u : 0u;
+    if (rank < kDraftK) {
+      s.top[rank] = me;
+      s.topv[rank] = s.vbits[e];
+    }
+  }
+  __syncthreads();
+  if (tid < kDraftK) {
+    const uint64_t c = s.top[tid];
+    d.candidates[(uint64_t)row * kDraftK + tid] = c ? ~(uint32_t)c : kNoToken;
+    d.unary[(uint64_t)row * kDraftK + tid] = u2f(s.topv[tid]);
+  }
+}
+
+struct __align__(16) DraftEdgeLds {
+  float ctx[kDraftK][kPad];   // predecessor codebook row x hidden
+  float succ[kDraftK][kPad];  // successor codebook rows
+  float hid[kRank];
+  uint32_t pred[kDraftK];
+  uint32_t cand[kDraftK];
+  uint32_t last;
+};
+
+// One proposal position of one lane: the edge scores from each predecessor
+// (the anchor at position 0, else the previous position's candidates) to each
+// candidate, sum over the rank in ascending order; ids are clamped into the
+// codebooks (sampling.metal:1259-1262). The lane's last block walks.
+__global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
+  __shared__ DraftEdgeLds s;
+  __shared__ float tbl[kDraftPositions][kDraftK * kDraftK];
+  __shared__ float un[kDraftPositions][kDraftK];
+  __shared__ uint32_t cands[kDraftPositions][kDraftK];
+  const uint32_t p = blockIdx.x, lane_index = blockIdx.y;
+  const uint32_t row = lane_index * kDraftPositions + p, tid = threadIdx.x;
+  const uint32_t V = d.vocabulary;
+  const DraftLaneParams lp = d.lane_params[lane_index];
+  if (tid < kDraftK) {
+    const uint32_t c = d.candidates[(uint64_t)row * kDraftK + tid];
+    const uint32_t pr = p ? d.candidates[(uint64_t)(row - 1) * kDraftK + tid] : lp.anchor;
+    s.cand[tid] = min(c, V - 1u);
+    s.pred[tid] = min(pr, V - 1u);
+  }
+  const uint16_t *h = d.hidden + ((uint64_t)lane_index * kDraftQueryRows + p + 1) * kRank;
+  s.hid[tid] = bf16f(h[tid]);
+  __syncthreads();
+  // 16 rows x 32 sixteen-byte pieces of each codebook, two pieces a thread.
+  const uint32_t preds = p ? kDraftK : 1u;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const uint32_t k = tid + r * kThreads, i = k >> 5, piece = k & 31;
+    const uint4 sv = *(const uint4 *)(d.succ_codebook + (uint64_t)s.cand[i] * kRank + piece * 8);
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s.succ[i][piece * 8 + 2 * e] = bf16f(sw[e] & 0xffffu);
+      s.succ[i][piece * 8 + 2 * e + 1] = bf16f(sw[e] >> 16);
+    }
+    if (i < preds) {
+      const uint4 pv = *(const uint4 *)(d.pred_codebook + (uint64_t)s.pred[i] * kRank + piece * 8);
+      const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t dm = piece * 8 + 2 * e;
+        s.ctx[i][dm] = bf16f(pw[e] & 0xffffu) * s.hid[dm];
+        s.ctx[i][dm + 1] = bf16f(pw[e] >> 16) * s.hid[dm + 1];
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t i = tid >> 4, j = tid & 15;
+  float *table = d.tables + (uint64_t)lane_index * kDraftPositions * kDraftK * kDraftK;
+  if (i < preds) {
+    float acc = 0.0f;
+    for (uint32_t dm = 0; dm < kRank; ++dm) acc = acc + s.ctx[i][dm] * s.succ[j][dm];
+    st_dev(table + (p * kDraftK + i) * kDraftK + j, acc);
+  }
+  wait_memory();
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t *counter = d.counters + d.lanes * kDraftPositions + lane_index;
+    const uint32_t prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    s.last = prev == kDraftPositions - 1 ? 1u : 0u;
+    if (prev == kDraftPositions - 1) st_dev(counter, 0u);
+  }
+  __syncthreads();
+  if (!s.last) return;
+
+  // The walk (sampling.metal:1316-1359): every table, unary score and
+  // candidate of the lane into LDS, then wave 0 with lane c holding
+  // candidate c; the sums and the running maximum go in candidate order.
+  const uint64_t r0 = (uint64_t)lane_index * kDraftPositions * kDraftK;
+  for (uint32_t e = tid; e < kDraftPositions * kDraftK * kDraftK; e += kThreads) {
+    const uint32_t pp = e / (kDraftK * kDraftK), q = e % (kDraftK * kDraftK);
+    // Position 0 has only the anchor's row.
+    tbl[pp][q] = pp || q < kDraftK ? ld_dev(table + e) : 0.0f;
+  }
+  if (tid < kDraftPositions * kDraftK) {
+    un[tid / kDraftK][tid % kDraftK] = d.unary[r0 + tid];
+    cands[tid / kDraftK][tid % kDraftK] = d.candidates[r0 + tid];
+  }
+  __syncthreads();
+  if (tid >= 64) return;
+  const uint32_t c = tid & 15;
+  const bool sampled = lp.sampled != 0;
+  const float *u = d.uniforms + (uint64_t)lane_index * kSamplingUniforms + kUniformProposals;
+  uint32_t pred_index = 0;
+  for (uint32_t pp = 0; pp < kDraftPositions; ++pp) {
+    const float score = un[pp][c] + tbl[pp][pred_index * kDraftK + c];
+    uint32_t selected = 0;
+    if (sampled) {
+      float maximum = readlane_f32(score, 0);
+      for (int k = 1; k < (int)kDraftK; ++k) maximum = __builtin_fmaxf(maximum, readlane_f32(score, k));
+      const float prob = exp_weight((score - maximum) / lp.temperature);
+      float sum = 0.0f;
+      for (int k = 0; k < (int)kDraftK; ++k) sum = sum + readlane_f32(prob, k);
+      const float q = prob / sum;
+      if (tid < kDraftK) d.q_probs[(r0 + pp * kDraftK) + c] = q;
+      const float uu = u[pp];
+      float cumulative = 0.0f;
+      selected = kDraftK - 1;
+      for (int k = 0; k < (int)kDraftK; ++k) {
+        cumulative = cumulative + readlane_f32(q, k);
+        if (selected == kDraftK - 1 && cumulative > uu) selected = (uint32_t)k;
+      }
+    } else {
+      float best = readlane_f32(score, 0);
+      for (int k = 1; k < (int)kDraftK; ++k) {
+        const float v = readlane_f32(score, k);
+        if (v > best) {
+          best = v;
+          selected = (uint32_t)k;
+        }
+      }
+    }
+    pred_index = selected;
+    if (tid == 0)
+      d.tokens[(uint64_t)lane_index * kDraftPositions + pp] = cands[pp][selected];
+  }
+}
+
+int launch_draft_select(const DraftLaunch &d, bool aligned, void *stream,
+                        void *start_event, void *stop_event) {
+  const hipStream_t st = (hipStream_t)stream;
+  const dim3 g1(d.chunks, d.lanes * kDraftPositions), block(kThreads);
+  if (aligned)
+    hipExtLaunchKernelGGL(draft_top16_kernel<true>, g1, block, 0, st, (hipEvent_t)start_event,
+                          (hipEvent_t)stop_event, 0, d);
+  else
+    hipExtLaunchKernelGGL(draft_top16_kernel<false>, g1, block, 0, st, (hipEvent_t)start_event,
+                          (hipEvent_t)stop_event, 0, d);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(draft_edges_kernel, dim3(kDraftPositions, d.lanes), block, 0, st, d);
+  return (int)hipGetLastError();
+}
+
+}  // namespace jf

@@ -246,6 +246,41 @@ struct AcceptTreeLaunch {
   uint32_t stop1;
 };
 
+// The draft selector (jf_draft.hip): lane geometry of the reference's DFlash
+// draft (ExecutionGeometry.h: 8 query rows, 7 proposal positions, 16
+// candidates, selector rank 256) and the uniform slots of a lane
+// (metal/abi/Sampling.h:19-29).
+constexpr uint32_t kDraftQueryRows = 8;
+constexpr uint32_t kDraftPositions = 7;
+constexpr uint32_t kSamplingUniforms = 40;
+constexpr uint32_t kUniformProposals = 1;
+struct DraftLaneParams {
+  uint32_t anchor;
+  float temperature;
+  uint32_t sampled;
+  uint32_t reserved;
+};
+struct DraftLaunch {
+  const float *logits;        // [lanes * 8][stride]
+  uint64_t stride;
+  uint32_t vocabulary;
+  uint32_t chunks;            // 8192-token chunks per row
+  uint32_t lanes;
+  const uint16_t *hidden;     // bf16 [lanes * 8][256]
+  const uint16_t *pred_codebook;  // bf16 [vocabulary][256]
+  const uint16_t *succ_codebook;  // bf16 [vocabulary][256]
+  const DraftLaneParams *lane_params;
+  const float *uniforms;      // [lanes][40]
+  uint32_t *candidates;       // [lanes * 7][16]
+  float *unary;               // [lanes * 7][16]
+  uint32_t *tokens;           // [lanes * 7]
+  float *q_probs;             // [lanes * 7][16], sampled lanes
+  uint64_t *part_comp;        // [lanes * 7][chunks][16]
+  uint32_t *part_vbits;       // [lanes * 7][chunks][16]
+  float *tables;              // [lanes][7][16][16]
+  uint32_t *counters;         // [lanes * 8], zero between launches
+};
+
 // Launchers (jf_kernels.hip); they return the hipError_t of the launch.
 // With both events set, they record the selection kernel's own start and end.
 int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
@@ -260,5 +295,8 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream);
 int launch_accept_tree(const AcceptTreeLaunch &a, void *stream);
+// jf_draft.hip; the events, when set, bracket the top-16 kernel.
+int launch_draft_select(const DraftLaunch &d, bool aligned, void *stream,
+                        void *start_event = nullptr, void *stop_event = nullptr);
 
 }  // namespace jf

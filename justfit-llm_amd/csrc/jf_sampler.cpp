@@ -784,4 +784,135 @@ int jf_accept_tree(jf_sampler *s, const jf_accept_tree_args *a, void *stream) {
   return JF_OK;
 }
 
+// ---- draft selector ----------------------------------------------------------
+
+}  // extern "C"
+
+struct jf_draft_selector {
+  uint32_t vocabulary = 0;
+  uint32_t max_lanes = 0;
+  uint32_t chunks = 0;
+  int device = 0;
+  jf::DraftLaneParams *lane_params = nullptr;  // [max_lanes]
+  uint64_t *part_comp = nullptr;               // [max_lanes * 7][chunks][16]
+  uint32_t *part_vbits = nullptr;
+  float *tables = nullptr;                     // [max_lanes][7][16][16]
+  uint32_t *counters = nullptr;                // [max_lanes * 8]
+  StagingRing staging;
+};
+
+extern "C" {
+
+int jf_draft_selector_destroy(jf_draft_selector *d) {
+  if (!d) return JF_OK;
+  d->staging.release();
+  (void)hipFree(d->lane_params);
+  (void)hipFree(d->part_comp);
+  (void)hipFree(d->part_vbits);
+  (void)hipFree(d->tables);
+  (void)hipFree(d->counters);
+  delete d;
+  return JF_OK;
+}
+
+int jf_draft_selector_create(uint32_t vocabulary, uint32_t max_lanes,
+                             jf_draft_selector **out) {
+  if (!out) return fail(JF_ERR_INVALID_ARGUMENT, "output pointer is null");
+  *out = nullptr;
+  // DraftSelector.cpp:43-46 and DraftSelector::workspace (48-57).
+  if (!vocabulary) return fail(JF_ERR_INVALID_ARGUMENT, "invalid draft selector vocabulary");
+  if (!max_lanes)
+    return fail(JF_ERR_INVALID_ARGUMENT, "invalid draft selector workspace position count");
+  const uint32_t chunks = (vocabulary + 8191u) / 8192u;
+  if (chunks > 64) return fail(JF_ERR_INVALID_ARGUMENT, "vocabulary exceeds 524288 tokens");
+  jf_draft_selector *d = new (std::nothrow) jf_draft_selector;
+  if (!d) return fail(JF_ERR_NO_MEMORY, "draft selector allocation failed");
+  d->vocabulary = vocabulary;
+  d->max_lanes = max_lanes;
+  d->chunks = chunks;
+  int rc = JF_OK;
+  const hipError_t ge = hipGetDevice(&d->device);
+  if (ge != hipSuccess) rc = hip_fail(ge, "hipGetDevice");
+  const uint64_t rows = (uint64_t)max_lanes * jf::kDraftPositions;
+  if (rc == JF_OK) rc = device_alloc(&d->lane_params, max_lanes, "draft lane parameters");
+  if (rc == JF_OK) rc = device_alloc(&d->part_comp, rows * chunks * JF_DRAFT_CANDIDATES, "draft partials");
+  if (rc == JF_OK) rc = device_alloc(&d->part_vbits, rows * chunks * JF_DRAFT_CANDIDATES, "draft partial values");
+  if (rc == JF_OK)
+    rc = device_alloc(&d->tables, rows * JF_DRAFT_CANDIDATES * JF_DRAFT_CANDIDATES, "draft edge tables");
+  if (rc == JF_OK) rc = device_alloc(&d->counters, (uint64_t)max_lanes * jf::kDraftQueryRows, "draft counters");
+  if (rc == JF_OK) {
+    const hipError_t e1 = hipMemset(d->counters, 0, (uint64_t)max_lanes * jf::kDraftQueryRows * sizeof(uint32_t));
+    const hipError_t e2 = hipDeviceSynchronize();
+    if (e1 != hipSuccess) rc = hip_fail(e1, "counter init");
+    else if (e2 != hipSuccess) rc = hip_fail(e2, "init sync");
+  }
+  if (rc != JF_OK) {
+    jf_draft_selector_destroy(d);
+    return rc;
+  }
+  *out = d;
+  return JF_OK;
+}
+
+int jf_draft_select(jf_draft_selector *d, const jf_draft_select_args *a, void *stream) {
+  if (!d || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null selector or arguments");
+  int rc = check_device(d->device);
+  if (rc != JF_OK) return rc;
+  // DraftSelector::add's checks (DraftSelector.cpp:64-110), before any launch.
+  if (!a->lanes || a->lanes > d->max_lanes || !a->anchors || !a->policies)
+    return fail(JF_ERR_INVALID_ARGUMENT, "invalid draft selector batch");
+  if (!a->logits || a->logits_stride < d->vocabulary)
+    return fail(JF_ERR_INVALID_ARGUMENT, "draft logits buffer too small");
+  if (!a->selector_hidden) return fail(JF_ERR_INVALID_ARGUMENT, "draft selector hidden buffer too small");
+  if (!a->predecessor_codebook || !a->successor_codebook ||
+      (uintptr_t)a->predecessor_codebook % 16 || (uintptr_t)a->successor_codebook % 16)
+    return fail(JF_ERR_INVALID_ARGUMENT, "draft codebooks must be 16-byte aligned device buffers");
+  if (!a->candidates || !a->unary || !a->proposed_tokens)
+    return fail(JF_ERR_INVALID_ARGUMENT, "draft candidate buffer too small");
+  if ((a->select_start_event == nullptr) != (a->select_done_event == nullptr))
+    return fail(JF_ERR_INVALID_ARGUMENT, "select events come in pairs");
+  std::vector<jf::DraftLaneParams> lanes(a->lanes);
+  bool any_sampled = false;
+  for (uint32_t l = 0; l < a->lanes; ++l) {
+    const float t = a->policies[l].temperature;
+    if (!(t == 0.0f || (std::isfinite(t) && t >= FLT_MIN)))
+      return fail(JF_ERR_INVALID_ARGUMENT,
+                  "sampling requires temperature 0 or at least FLT_MIN, top_p in (0,1] and "
+                  "min_p in [0,1]");
+    lanes[l].anchor = a->anchors[l];
+    lanes[l].temperature = t;
+    lanes[l].sampled = t > 0.0f ? 1u : 0u;
+    any_sampled |= t > 0.0f;
+  }
+  if (any_sampled && (!a->uniforms || !a->proposal_probs))
+    return fail(JF_ERR_INVALID_ARGUMENT, "proposal uniform buffer too small");
+  rc = d->staging.upload(d->lane_params, lanes.data(), lanes.size() * sizeof(jf::DraftLaneParams),
+                         (hipStream_t)stream);
+  if (rc != JF_OK) return rc;
+  jf::DraftLaunch L{};
+  L.logits = a->logits;
+  L.stride = a->logits_stride;
+  L.vocabulary = d->vocabulary;
+  L.chunks = d->chunks;
+  L.lanes = a->lanes;
+  L.hidden = a->selector_hidden;
+  L.pred_codebook = a->predecessor_codebook;
+  L.succ_codebook = a->successor_codebook;
+  L.lane_params = d->lane_params;
+  L.uniforms = a->uniforms;
+  L.candidates = a->candidates;
+  L.unary = a->unary;
+  L.tokens = a->proposed_tokens;
+  L.q_probs = a->proposal_probs;
+  L.part_comp = d->part_comp;
+  L.part_vbits = d->part_vbits;
+  L.tables = d->tables;
+  L.counters = d->counters;
+  const bool aligned = (uintptr_t)a->logits % 16 == 0 && a->logits_stride % 4 == 0;
+  const int e = jf::launch_draft_select(L, aligned, stream, a->select_start_event,
+                                        a->select_done_event);
+  if (e != hipSuccess) return hip_fail((hipError_t)e, "draft selector launch");
+  return JF_OK;
+}
+
 }  // extern "C"

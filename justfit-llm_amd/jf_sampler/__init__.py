@@ -35,6 +35,7 @@ EXPORTS = [
     "jf_penalty_table_rebuild", "jf_penalty_table_count",
     "jf_next_uniform", "jf_stage_sampling_cycle", "jf_sample",
     "jf_accept_chain", "jf_accept_tree",
+    "jf_draft_selector_create", "jf_draft_selector_destroy", "jf_draft_select",
 ]
 
 c_u32 = ctypes.c_uint32
@@ -100,6 +101,17 @@ class JfAcceptTreeArgs(ctypes.Structure):
     ]
 
 
+class JfDraftSelectArgs(ctypes.Structure):
+    _fields_ = [
+        ("lanes", c_u32), ("logits", c_vp), ("logits_stride", c_u64),
+        ("selector_hidden", c_vp), ("predecessor_codebook", c_vp),
+        ("successor_codebook", c_vp), ("anchors", c_vp), ("policies", c_vp),
+        ("uniforms", c_vp), ("candidates", c_vp), ("unary", c_vp),
+        ("proposed_tokens", c_vp), ("proposal_probs", c_vp),
+        ("select_start_event", c_vp), ("select_done_event", c_vp),
+    ]
+
+
 class JfError(RuntimeError):
     def __init__(self, code, message):
         super().__init__(f"jf error {code}: {message}")
@@ -145,6 +157,9 @@ def lib():
                                       c_vp]
         L.jf_accept_tree.argtypes = [c_vp, ctypes.POINTER(JfAcceptTreeArgs),
                                      c_vp]
+        L.jf_draft_selector_create.argtypes = [c_u32, c_u32, ctypes.POINTER(c_vp)]
+        L.jf_draft_selector_destroy.argtypes = [c_vp]
+        L.jf_draft_select.argtypes = [c_vp, ctypes.POINTER(JfDraftSelectArgs), c_vp]
         _lib = L
     return _lib
 
@@ -380,6 +395,58 @@ class Sampler:
     def close(self):
         if self.handle:
             lib().jf_sampler_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DraftSelector:
+    """jf_draft_selector: the DFlash draft's proposal policy for up to
+    max_lanes lanes (ops::DraftSelector)."""
+
+    def __init__(self, vocabulary, max_lanes):
+        h = c_vp()
+        check(lib().jf_draft_selector_create(vocabulary, max_lanes, ctypes.byref(h)))
+        self.handle = h
+        self.vocabulary = vocabulary
+        self.max_lanes = max_lanes
+
+    def args(self, *, logits, hidden, pred_codebook, succ_codebook, anchors, policies,
+             candidates, unary, tokens, q=None, uniforms=None, stride=None):
+        """A jf_draft_select_args over torch device tensors; `anchors` and
+        `policies` are host sequences (kept alive on the returned object)."""
+        import numpy as np
+        lanes = len(anchors)
+        a = JfDraftSelectArgs()
+        a.lanes = lanes
+        a.logits = _ptr(logits)
+        a.logits_stride = stride if stride is not None else logits.shape[-1]
+        a.selector_hidden = _ptr(hidden)
+        a.predecessor_codebook = _ptr(pred_codebook)
+        a.successor_codebook = _ptr(succ_codebook)
+        anc = np.ascontiguousarray(anchors, dtype=np.uint32)
+        pol = (JfPolicy * lanes)(*policies)
+        a.anchors = anc.ctypes.data_as(c_vp)
+        a.policies = ctypes.cast(pol, c_vp)
+        a.uniforms = _ptr(uniforms)
+        a.candidates = _ptr(candidates)
+        a.unary = _ptr(unary)
+        a.proposed_tokens = _ptr(tokens)
+        a.proposal_probs = _ptr(q)
+        a._keep = (anc, pol)
+        return a
+
+    def launch(self, a, stream=None):
+        check(lib().jf_draft_select(self.handle, ctypes.byref(a),
+                                    stream if stream is not None else _stream()))
+
+    def close(self):
+        if self.handle:
+            lib().jf_draft_selector_destroy(self.handle)
             self.handle = None
 
     def __del__(self):

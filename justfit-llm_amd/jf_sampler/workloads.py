@@ -185,3 +185,24 @@ def config5(V=V_LARGE, B=256, H=8192):
                 policy=dict(temperature=0.8, top_k=1000, top_p=0.95, min_p=0.05,
                             repetition=1.1, presence=0.5, frequency=0.3),
                 mark_prompt=True)
+
+
+def config_draft(V=V_QWEN, lanes=4, seed=6):
+    """The draft selector's step (DraftSelector.cpp:100-154) at the
+    reference's widest batch (4 lanes): 8 fp32 query rows per lane of
+    N(0, 2^2) draft logits (rows 1..7 are the proposal positions) with a few
+    +6 peaks, bf16 selector hidden rows N(0, 1) and bf16 codebooks
+    N(0, 0.2^2) of rank 256; lanes alternate greedy and sampled (T 0.8)."""
+    rng = np.random.default_rng(seed)
+    logits = rng.normal(0.0, 2.0, (lanes * 8, V)).astype(np.float32)
+    peaks = rng.integers(0, V, (lanes * 8, 8))
+    for r in range(lanes * 8):
+        logits[r, peaks[r]] += 6.0
+    hidden = to_bf16_bits(rng.normal(0.0, 1.0, (lanes * 8, 256)).astype(np.float32))
+    pred = to_bf16_bits(rng.normal(0.0, 0.2, (V, 256)).astype(np.float32))
+    succ = to_bf16_bits(rng.normal(0.0, 0.2, (V, 256)).astype(np.float32))
+    anchors = rng.integers(0, V, lanes).astype(np.uint32)
+    temperatures = [0.0 if l % 2 == 0 else 0.8 for l in range(lanes)]
+    uniforms = rng.random((lanes, 40)).astype(np.float32)
+    return dict(V=V, lanes=lanes, logits=logits, hidden=hidden, pred=pred, succ=succ,
+                anchors=anchors, temperatures=temperatures, uniforms=uniforms)

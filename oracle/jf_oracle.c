@@ -607,3 +607,114 @@ void jfo_accept_tree(const jfo_tree_params *p, const float *target_draft_prob,
   for (uint32_t i = 0; i < JFO_TREE_MAX_DEPTH; ++i)
     path_rows[i] = i < length ? path[i] : path[length - 1];
 }
+
+/* ---- draft selector ---------------------------------------------------- */
+
+/* (value desc, id asc): sampling.metal:995-997. NaN never beats anything. */
+static int draft_beats(float v, uint32_t id, float w, uint32_t wid) {
+  return v > w || (v == w && id < wid);
+}
+
+/* Pinned by tests/test_oracle.py against a numpy lexsort over random rows,
+ * rows with ties, -inf and NaN, and rows with fewer than 16 non-NaN tokens. */
+void jfo_draft_top16(const float *row, uint32_t vocabulary, uint32_t *ids,
+                     float *values) {
+  for (uint32_t i = 0; i < JFO_DRAFT_CANDIDATES; ++i) {
+    values[i] = -INFINITY;
+    ids[i] = JFO_NO_TOKEN;
+  }
+  for (uint32_t t = 0; t < vocabulary; ++t) {
+    const float v = row[t];
+    const uint32_t last = JFO_DRAFT_CANDIDATES - 1;
+    if (!draft_beats(v, t, values[last], ids[last]))
+      continue;
+    uint32_t slot = last;
+    while (slot > 0 && draft_beats(v, t, values[slot - 1], ids[slot - 1])) {
+      values[slot] = values[slot - 1];
+      ids[slot] = ids[slot - 1];
+      --slot;
+    }
+    values[slot] = v;
+    ids[slot] = t;
+  }
+}
+
+static float bf16f(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+/* Pinned by tests/test_oracle.py against float64 dot products (and by the
+ * roles: swapping the codebooks or dropping the hidden factor fails it). */
+float jfo_draft_edge(const uint16_t *pred_row, const uint16_t *hidden,
+                     const uint16_t *succ_row) {
+  float acc = 0.0f;
+  for (uint32_t d = 0; d < JFO_DRAFT_RANK; ++d) {
+    const float context = bf16f(pred_row[d]) * bf16f(hidden[d]);
+    acc = acc + context * bf16f(succ_row[d]);
+  }
+  return acc;
+}
+
+/* draft_select_top16_sharded + draft_select_edges + draft_select_dflash for
+ * one lane. The walk is pinned by tests/test_oracle.py: greedy against a
+ * numpy argmax chain, sampled q against a float64 softmax. */
+void jfo_draft_select_lane(const jfo_draft_lane *lane, const float *logits8,
+                           uint64_t stride, const uint16_t *hidden8,
+                           const uint16_t *pred_codebook,
+                           const uint16_t *succ_codebook,
+                           const float *uniforms40, uint32_t *candidates,
+                           float *unary, uint32_t *tokens, float *q) {
+  const uint32_t V = lane->vocabulary, K = JFO_DRAFT_CANDIDATES;
+  for (uint32_t p = 0; p < JFO_DRAFT_POSITIONS; ++p)
+    jfo_draft_top16(logits8 + (uint64_t)(p + 1) * stride, V, candidates + p * K,
+                    unary + p * K);
+  /* Edge tables: position p scores predecessor i (the anchor at p = 0, row
+   * p - 1's candidate i after) against candidate j (sampling.metal:1233-1288;
+   * ids are clamped into the codebooks as there). */
+  float table[JFO_DRAFT_POSITIONS][JFO_DRAFT_CANDIDATES][JFO_DRAFT_CANDIDATES];
+  for (uint32_t p = 0; p < JFO_DRAFT_POSITIONS; ++p) {
+    const uint16_t *h = hidden8 + (uint64_t)(p + 1) * JFO_DRAFT_RANK;
+    const uint32_t preds = p ? K : 1;
+    for (uint32_t i = 0; i < preds; ++i) {
+      uint32_t pred = p ? candidates[(p - 1) * K + i] : lane->anchor;
+      pred = pred < V - 1 ? pred : V - 1;
+      for (uint32_t j = 0; j < K; ++j) {
+        uint32_t c = candidates[p * K + j];
+        c = c < V - 1 ? c : V - 1;
+        table[p][i][j] = jfo_draft_edge(pred_codebook + (uint64_t)pred * JFO_DRAFT_RANK, h,
+                                        succ_codebook + (uint64_t)c * JFO_DRAFT_RANK);
+      }
+    }
+  }
+  /* The walk (sampling.metal:1316-1359). */
+  uint32_t pred_index = 0;
+  for (uint32_t p = 0; p < JFO_DRAFT_POSITIONS; ++p) {
+    float scores[JFO_DRAFT_CANDIDATES];
+    for (uint32_t i = 0; i < K; ++i)
+      scores[i] = unary[p * K + i] + table[p][pred_index][i];
+    uint32_t selected = 0;
+    if (lane->sampled) {
+      float maximum = scores[0];
+      for (uint32_t i = 1; i < K; ++i)
+        maximum = fmaxf(maximum, scores[i]);
+      float prob[JFO_DRAFT_CANDIDATES], sum = 0.0f;
+      for (uint32_t i = 0; i < K; ++i) {
+        prob[i] = jfo_expf((scores[i] - maximum) / lane->temperature);
+        sum = sum + prob[i];
+      }
+      float cumulative = 0.0f;
+      selected = K - 1;
+      for (uint32_t i = 0; i < K; ++i) {
+        const float pi = prob[i] / sum;
+        q[p * K + i] = pi;
+        cumulative = cumulative + pi;
+        if (selected == K - 1 && cumulative > uniforms40[1 + p])
+          selected = i;
+      }
+    } else {
+      for (uint32_t i = 1; i < K; ++i)
+        if (scores[i] > scores[selected])
+          selected = i;
+    }
+    pred_index = selected;
+    tokens[p] = candidates[p * K + selected];
+  }
+}

@@ -143,6 +143,46 @@ void jfo_accept_tree(const jfo_tree_params *p, const float *target_draft_prob,
                      uint32_t *retained, uint32_t *accepted,
                      uint32_t *path_rows);
 
+/* Draft selector (the DFlash draft's proposal policy: sampling.metal:995-1359,
+ * DraftSelector.cpp:100-154). A lane has 8 query rows; rows 1..7 are its
+ * proposal positions. */
+#define JFO_DRAFT_POSITIONS 7u
+#define JFO_DRAFT_QUERY_ROWS 8u
+#define JFO_DRAFT_RANK 256u
+
+/* The exact top 16 of one fp32 row in (value desc, id asc) order among its
+ * non-NaN tokens (-0 and +0 tie, and tie by id); slots past the row's
+ * non-NaN count hold (-inf, JFO_NO_TOKEN) (sampling.metal:995-1013,
+ * 1040-1165, 1170-1203). */
+void jfo_draft_top16(const float *row, uint32_t vocabulary, uint32_t *ids,
+                     float *values);
+
+/* One edge score: the sum over d = 0..255, in that order, of
+ * (pred[d] * hidden[d]) * succ[d], bf16 operands widened exactly, fp32
+ * products (exact) and fp32 accumulation without contraction
+ * (sampling.metal:1249-1288 scores the same sum in another order). */
+float jfo_draft_edge(const uint16_t *pred_row, const uint16_t *hidden,
+                     const uint16_t *succ_row);
+
+typedef struct {
+  uint32_t vocabulary;
+  uint32_t anchor;
+  float temperature;  /* a sampled lane's */
+  int sampled;
+} jfo_draft_lane;
+
+/* One lane end to end: candidates and unary scores of its 7 positions, the
+ * edge tables, then the walk (sampling.metal:1296-1359). logits8/hidden8 are
+ * the lane's 8 query rows (row stride `stride` floats / 256 bf16); uniforms40
+ * is the lane's 40 uniforms (position p draws slot 1 + p). q (7 x 16) is
+ * written for a sampled lane only. */
+void jfo_draft_select_lane(const jfo_draft_lane *lane, const float *logits8,
+                           uint64_t stride, const uint16_t *hidden8,
+                           const uint16_t *pred_codebook,
+                           const uint16_t *succ_codebook,
+                           const float *uniforms40, uint32_t *candidates,
+                           float *unary, uint32_t *tokens, float *q);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,6 +47,11 @@ class TreeParams(ctypes.Structure):
                 ("chain_q", c_f32 * 8)]
 
 
+class DraftLane(ctypes.Structure):
+    _fields_ = [("vocabulary", c_u32), ("anchor", c_u32), ("temperature", c_f32),
+                ("sampled", ctypes.c_int)]
+
+
 def build():
     subprocess.run(["make", "-s", "-C", HERE], check=True)
     return LIB_PATH
@@ -96,6 +101,13 @@ def lib():
         L.jfo_accept_tree.argtypes = [ctypes.POINTER(TreeParams), c_vp, c_vp,
                                       c_vp, c_vp, c_vp, c_vp]
         L.jfo_accept_tree.restype = None
+        L.jfo_draft_top16.argtypes = [c_vp, c_u32, c_vp, c_vp]
+        L.jfo_draft_top16.restype = None
+        L.jfo_draft_edge.argtypes = [c_vp, c_vp, c_vp]
+        L.jfo_draft_edge.restype = c_f32
+        L.jfo_draft_select_lane.argtypes = [ctypes.POINTER(DraftLane), c_vp, c_u64, c_vp,
+                                            c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]
+        L.jfo_draft_select_lane.restype = None
         _lib = L
     return _lib
 
@@ -241,3 +253,45 @@ def accept_tree(parent, token, chain_rows, chain_q, remaining, sampled,
     lib().jfo_accept_tree(ctypes.byref(p), _p(tp), _p(u), _p(tt),
                           ctypes.byref(ret), ctypes.byref(acc), _p(path))
     return tt, ret.value, acc.value, path
+
+
+def draft_top16(row):
+    """Exact top 16 of one fp32 row: (ids, values) in (value desc, id asc)."""
+    r = np.ascontiguousarray(row, dtype=np.float32)
+    ids = np.zeros(16, np.uint32)
+    vals = np.zeros(16, np.float32)
+    lib().jfo_draft_top16(_p(r), len(r), _p(ids), _p(vals))
+    return ids, vals
+
+
+def draft_edge(pred_row, hidden, succ_row):
+    """One edge score over bf16 bit patterns (uint16 arrays of 256)."""
+    a = [np.ascontiguousarray(x, dtype=np.uint16) for x in (pred_row, hidden, succ_row)]
+    return lib().jfo_draft_edge(_p(a[0]), _p(a[1]), _p(a[2]))
+
+
+def draft_select(logits, hidden, pred_codebook, succ_codebook, anchors, temperatures,
+                 sampled, uniforms40):
+    """Every lane of a draft selection: logits [lanes*8][V] fp32, hidden
+    [lanes*8][256] bf16 bits, codebooks [V][256] bf16 bits, uniforms40
+    [lanes][40]. Returns candidates, unary, tokens, q (q zero for greedy
+    lanes)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    hidden = np.ascontiguousarray(hidden, dtype=np.uint16)
+    pc = np.ascontiguousarray(pred_codebook, dtype=np.uint16)
+    sc = np.ascontiguousarray(succ_codebook, dtype=np.uint16)
+    u = np.ascontiguousarray(uniforms40, dtype=np.float32)
+    lanes = len(anchors)
+    V = logits.shape[1]
+    cand = np.zeros((lanes, 7, 16), np.uint32)
+    unary = np.zeros((lanes, 7, 16), np.float32)
+    tokens = np.zeros((lanes, 7), np.uint32)
+    q = np.zeros((lanes, 7, 16), np.float32)
+    for l in range(lanes):
+        lane = DraftLane(V, int(anchors[l]), float(temperatures[l]), 1 if sampled[l] else 0)
+        lg = np.ascontiguousarray(logits[l * 8:(l + 1) * 8])
+        hd = np.ascontiguousarray(hidden[l * 8:(l + 1) * 8])
+        c, un, t, qq = cand[l], unary[l], tokens[l], q[l]
+        lib().jfo_draft_select_lane(ctypes.byref(lane), _p(lg), V, _p(hd), _p(pc), _p(sc),
+                                    _p(np.ascontiguousarray(u[l])), _p(c), _p(un), _p(t), _p(qq))
+    return cand, unary, tokens, q
