@@ -31,6 +31,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--path", default="sample", choices=["sample", "draft"],
+                    help="sample: jf_sample on --config (the headline); draft: "
+                         "jf_draft_select at 4 lanes, V=151936")
     ap.add_argument("--mode", default="auto",
                     help="C3/C4: greedy or sampled (auto: sampled)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -263,7 +266,8 @@ def cpu_baseline(w, seconds):
 def read_traffic(cfg):
     """HBM bytes per launch and the kernel they were counted on, from the
     committed rocprofv3 --pmc summary (its first line names the kernel)."""
-    path = os.path.join(REPO, "profiles", f"select_c{cfg}_traffic.txt")
+    name = "draft_top16" if cfg == "draft" else f"select_c{cfg}"
+    path = os.path.join(REPO, "profiles", f"{name}_traffic.txt")
     if not os.path.exists(path):
         return None, None
     traffic, kernel = None, None
@@ -308,6 +312,97 @@ def read_ceiling():
                       "frac_of_8TBps": n / (mean.value * 1e-6) / 1e9 / PEAK_HBM_GBS}))
 
 
+def bench_draft(args):
+    """The draft selector (jf_draft_select) at the reference's widest batch:
+    4 lanes x 7 proposal positions over V=151936 fp32 draft logits, inputs
+    resident and rotated over >= 512 MB. The dominant kernel is the top-16
+    pass over the proposal rows (draft_top16_kernel)."""
+    import torch
+    import jf_sampler as J
+    from jf_sampler import workloads as WL
+    c = WL.config_draft()
+    lanes, V = c["lanes"], c["V"]
+    print(f"# draft selector {lanes} lanes V={V}: building inputs", file=sys.stderr, flush=True)
+    dev = torch.device("cuda", 0)
+    base = torch.from_numpy(c["logits"])
+    copies = [base.to(dev) for _ in range(max(2, -(-ROTATE_BYTES // (base.numel() * 4))))]
+    t16 = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+    hidden, pred, succ = t16(c["hidden"]), t16(c["pred"]), t16(c["succ"])
+    u = torch.from_numpy(c["uniforms"]).to(dev)
+    cand = torch.zeros((lanes * 7, 16), dtype=torch.int32, device=dev)
+    unary = torch.zeros((lanes * 7, 16), dtype=torch.float32, device=dev)
+    tokens = torch.zeros(lanes * 7, dtype=torch.int32, device=dev)
+    q = torch.zeros((lanes * 7, 16), dtype=torch.float32, device=dev)
+    sel = J.DraftSelector(V, lanes)
+    pols = [J.policy(temperature=t) for t in c["temperatures"]]
+    argv = [sel.args(logits=x, hidden=hidden, pred_codebook=pred, succ_codebook=succ,
+                     anchors=c["anchors"], policies=pols, candidates=cand, unary=unary,
+                     tokens=tokens, q=q, uniforms=u) for x in copies]
+    for i in range(args.warmup):
+        sel.launch(argv[i % len(argv)])
+    torch.cuda.synchronize()
+    K = args.steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    wall0 = time.perf_counter()
+    ev[0].record()
+    for i in range(K):
+        sel.launch(argv[(args.warmup + i) % len(argv)])
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    per = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(K)]) * 1000.0
+    ms_per_step = ev[0].elapsed_time(ev[K]) / K
+    # The top-16 kernel alone, between events its launch records.
+    hev = HipEvents(2 * K)
+    for i in range(K):
+        a = argv[(args.warmup + i) % len(argv)]
+        a.select_start_event, a.select_done_event = hev.ev[2 * i].value, hev.ev[2 * i + 1].value
+        sel.launch(a)
+        a.select_start_event = a.select_done_event = None
+    torch.cuda.synchronize()
+    kus = np.array([hev.ms(2 * i, 2 * i + 1) for i in range(K)]) * 1000.0
+    hev.destroy()
+    top_bytes = lanes * 7 * V * 4
+    achieved = top_bytes / (kus.mean() * 1e-6) / 1e9
+    traffic, kernel = read_traffic("draft")
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle as O
+        sampled = [t > 0 for t in c["temperatures"]]
+        steps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds:
+            O.draft_select(c["logits"], c["hidden"], c["pred"], c["succ"], c["anchors"],
+                           c["temperatures"], sampled, c["uniforms"])
+            steps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=steps / el, unit="selections/s", cores=1, kind="port",
+                   sample=f"{steps} full selections ({lanes} lanes x 7 positions) of the same "
+                          f"seeded inputs in {el:.1f} s, oracle/jf_oracle.c -O2, one thread")
+    line = {
+        "metric": "draft selections/sec at 4 lanes x 7 positions, V=151936; achieved HBM GB/s "
+                  "vs peak; p50 us/selection",
+        "value": 1000.0 / ms_per_step, "unit": "selections/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "p50_us": float(np.percentile(per, 50)), "p90_us": float(np.percentile(per, 90)),
+        "wall_s": wall, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": f"synthetic (workloads.config_draft), {len(copies)} rotated "
+                                f"logits copies >= 512 MB",
+        "config": {"workload": f"draft selector {lanes} lanes x 7 positions V={V} fp32, "
+                               "bf16 codebooks rank 256, lanes alternate greedy / T0.8",
+                   "rows": lanes * 7, "vocabulary": V, "algorithmic_bytes_per_step": top_bytes},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                     "kernel": kernel or "jf::draft_top16_kernel<true>",
+                     "kernel_mean_us": float(kus.mean()),
+                     "kernel_p50_us": float(np.percentile(kus, 50)),
+                     "algorithmic_bytes": top_bytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    sel.close()
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -325,6 +420,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.path == "draft":
+        bench_draft(args)
+        return
     w = build_workload(args.config, args.mode)
     print(f"# {w['name']}: building inputs", file=sys.stderr, flush=True)
     g = GpuStep(w)

@@ -274,4 +274,29 @@ __device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, uint32_t k) {
   return answer;
 }
 
+// Bitonic sort of one 32-bit value per lane over the wave, ascending.
+__device__ __forceinline__ uint32_t wave_sort_asc_u32(uint32_t v) {
+  const uint32_t lane = lane_id();
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      uint32_t o;
+      switch (j) {
+        case 1: o = xor_u32<1>(v); break;
+        case 2: o = xor_u32<2>(v); break;
+        case 4: o = xor_u32<4>(v); break;
+        case 8: o = xor_u32<8>(v); break;
+        case 16: o = xor_u32<16>(v); break;
+        default: o = xor_u32<32>(v); break;
+      }
+      const bool lower = (lane & j) == 0;
+      const bool block_asc = (lane & k) == 0;
+      const bool take_smaller = lower == block_asc;
+      v = take_smaller ? min(v, o) : max(v, o);
+    }
+  }
+  return v;
+}
+
 }  // namespace jf

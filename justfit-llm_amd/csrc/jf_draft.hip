@@ -30,6 +30,7 @@ constexpr uint32_t kDraftChunk = 8192;   // fp32 tokens per block
 constexpr int kDraftLoads = 8;           // 16-byte loads per thread
 constexpr int kDraftTokens = 32;         // tokens per thread
 constexpr uint32_t kDraftK = 16;
+constexpr uint32_t kDraftMaxChunks = 64;    // vocabulary <= 524288
 constexpr uint32_t kRank = 256;
 constexpr uint32_t kWaveCap = 256;       // staged candidates per wave
 constexpr uint32_t kPad = kRank + 1;     // LDS row pitch of the edge operands
@@ -60,24 +61,24 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 }
 
 struct __align__(16) DraftTopLds {
-  uint64_t comp[kWaves * kWaveCap];   // staged candidates, then the row merge
-  uint32_t vbits[kWaves * kWaveCap];  // their values' bits
+  uint32_t wtop[kWaves * kDraftK];   // each wave's 16 largest lane maxima
+  uint64_t comp[kThreads];           // the chunk's entries at or above the bound
+  uint32_t vbits[kThreads];
   uint64_t top[kDraftK];
   uint32_t topv[kDraftK];
   uint64_t wbest[kWaves];
   uint32_t wcount[kWaves];
-  uint32_t wbound[kWaves];
-  uint32_t last;
 };
 
 }  // namespace
 
-// One chunk of one proposal row. Each thread holds 32 tokens; each wave's
-// 4th largest lane maximum bounds the block (at least 16 tokens are at or
-// above the smallest of the four), so only the tokens at or above it are
-// staged and ranked. A chunk whose staged tokens overflow (ties) takes its
-// top 16 by 16 rounds of block maxima instead. The row's last block merges
-// the chunks' top 16 by rank counting.
+// One chunk of one proposal row: its top 16 in rank order (empty slots 0,
+// value -inf) into the row's partials. Each thread holds 32 tokens. The 16th
+// largest lane maximum of the block bounds the chunk's top 16 (16 lanes hold
+// a token at least that large); each wave sorts its lane maxima, and every
+// wave sorts the 64 wave leaders to find it. The tokens at or above the bound
+// are compacted by a prefix sum and ranked by counting. A chunk with more
+// than 256 of them (ties) takes its top 16 by 16 rounds of block maxima.
 template <bool ALIGNED>
 __global__ __launch_bounds__(kThreads) void draft_top16_kernel(DraftLaunch d) {
   __shared__ DraftTopLds s;
@@ -110,59 +111,54 @@ __global__ __launch_bounds__(kThreads) void draft_top16_kernel(DraftLaunch d) {
     s.top[tid] = 0;
     s.topv[tid] = f2u(-__builtin_inff());
   }
-  // The lane's largest key among its non-NaN tokens (0: none), then each
-  // wave's 4th largest by 32 ballots.
+  // The lane's largest key among its non-NaN tokens (0: none).
   uint32_t mkey = 0;
 #pragma unroll
   for (int i = 0; i < kDraftTokens; ++i)
     if (x[i] == x[i]) mkey = max(mkey, logit_key(x[i]));
-  uint32_t wb = 0;
-#pragma unroll
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t trial = wb | (1u << b);
-    if (__popcll(ballot(mkey >= trial)) >= 4) wb = trial;
-  }
-  if (lane == 0) s.wbound[w] = wb;
+  const uint32_t sorted = wave_sort_asc_u32(mkey);
+  if (lane >= 64 - kDraftK) s.wtop[w * kDraftK + lane - (64 - kDraftK)] = sorted;
   __syncthreads();
-  const uint32_t bound = min(min(s.wbound[0], s.wbound[1]), min(s.wbound[2], s.wbound[3]));
+  const uint32_t bound = readlane_u32(wave_sort_asc_u32(s.wtop[lane]), 64 - kDraftK);
 
-  // Stage the tokens at or above the bound, per wave.
-  uint32_t run = 0;
-  uint64_t *stage = s.comp + w * kWaveCap;
-  uint32_t *vstage = s.vbits + w * kWaveCap;
+  // Compact the tokens at or above the bound: per-thread counts, a block
+  // prefix sum, then each thread writes its own.
+  uint32_t hits = 0;
 #pragma unroll
-  for (int i = 0; i < kDraftTokens; ++i) {
-    const bool hit = x[i] == x[i] && logit_key(x[i]) >= bound;
-    const uint64_t m = ballot(hit);
-    if (m) {
-      const uint32_t slot = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, run));
-      if (hit && slot < kWaveCap) {
-        stage[slot] = draft_comp(x[i], token_of(i));
-        vstage[slot] = f2u(x[i]);
-      }
-      run += (uint32_t)__popcll(m);
-    }
-  }
-  if (lane == 0) s.wcount[w] = run;
+  for (int i = 0; i < kDraftTokens; ++i)
+    hits |= (x[i] == x[i] && logit_key(x[i]) >= bound ? 1u : 0u) << i;
+  const uint32_t cnt = (uint32_t)__popc(hits);
+  const uint32_t incl = wave_incl_scan_u32(cnt);
+  if (lane == 63) s.wcount[w] = incl;
   __syncthreads();
-  uint32_t n[kWaves], over = 0;
+  uint32_t before = 0, n = 0;
 #pragma unroll
   for (int k = 0; k < kWaves; ++k) {
-    n[k] = s.wcount[k];
-    over |= n[k] > kWaveCap;
+    before += (uint32_t)k < w ? s.wcount[k] : 0u;
+    n += s.wcount[k];
   }
-  if (!over) {
-    // Rank by counting: an entry's rank is the number of entries above it.
-    // Each wave ranks its own staged entries.
-    for (uint32_t e = lane; e < n[w]; e += 64) {
-      const uint64_t me = stage[e];
+  if (n <= kThreads) {
+    uint32_t pos = before + incl - cnt;
+#pragma unroll
+    for (int i = 0; i < kDraftTokens; ++i)
+      if ((hits >> i) & 1u) {
+        s.comp[pos] = draft_comp(x[i], token_of(i));
+        s.vbits[pos] = f2u(x[i]);
+        ++pos;
+      }
+    __syncthreads();
+    // Rank by counting, eight reads in flight per step.
+    if (tid < n) {
+      const uint64_t me = s.comp[tid];
       uint32_t rank = 0;
-      for (uint32_t k = 0; k < kWaves; ++k)
-        for (uint32_t e2 = 0; e2 < n[k]; ++e2) rank += s.comp[k * kWaveCap + e2] > me ? 1u : 0u;
+      for (uint32_t e = 0; e < n; e += 8) {
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u)
+          rank += e + u < n && s.comp[min(e + u, (uint32_t)kThreads - 1u)] > me ? 1u : 0u;
+      }
       if (rank < kDraftK) {
         s.top[rank] = me;
-        s.topv[rank] = vstage[e];
+        s.topv[rank] = s.vbits[tid];
       }
     }
   } else {
@@ -195,50 +191,35 @@ __global__ __launch_bounds__(kThreads) void draft_top16_kernel(DraftLaunch d) {
     }
   }
   __syncthreads();
-  // The chunk's top 16, then one arrival per block; the row's last block
-  // merges.
   const uint64_t pi = ((uint64_t)row * S + chunk) * kDraftK;
   if (tid < kDraftK) {
-    st_dev(d.part_comp + pi + tid, s.top[tid]);
-    st_dev(d.part_vbits + pi + tid, s.topv[tid]);
+    d.part_comp[pi + tid] = s.top[tid];
+    d.part_vbits[pi + tid] = s.topv[tid];
   }
-  wait_memory();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(d.counters + row, 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    s.last = prev == S - 1 ? 1u : 0u;
-    if (prev == S - 1) st_dev(d.counters + row, 0u);
-  }
-  __syncthreads();
-  if (!s.last) return;
+}
 
-  const uint32_t total = S * kDraftK;  // <= 1024
-  const uint64_t p0 = (uint64_t)row * S * kDraftK;
-  for (uint32_t e = tid; e < total; e += kThreads) {
-    s.comp[e] = ld_dev(d.part_comp + p0 + e);
-    s.vbits[e] = ld_dev(d.part_vbits + p0 + e);
-  }
-  if (tid < kDraftK) {
-    s.top[tid] = 0;
-    s.topv[tid] = f2u(-__builtin_inff());
-  }
-  __syncthreads();
-  for (uint32_t e = tid; e < total; e += kThreads) {
-    const uint64_t me = s.comp[e];
-    if (!me) continue;
-    uint32_t rank = 0;
-    for (uint32_t j = 0; j < total; ++j) rank += s.comp[j] > me ? 1u : 0u;
-    if (rank < kDraftK) {
-      s.top[rank] = me;
-      s.topv[rank] = s.vbits[e];
+// The top 16 of one proposal row from its chunks' lists (each in rank
+// order), by one wave: lane c holds chunk c's head (S <= 64) and 16 rounds
+// pop the largest head. A head past its list's entries is 0 and never wins
+// a real entry; once every head is 0 the remaining slots stay empty.
+// `comp`/`vbits` are the row's partials in LDS.
+__device__ __forceinline__ void draft_merge_row(const uint64_t *comp, const uint32_t *vbits,
+                                                uint32_t S, uint32_t *ids, float *values) {
+  const uint32_t lane = lane_id();
+  uint32_t head = 0;
+  uint64_t hc = lane < S ? comp[lane * kDraftK] : 0ull;
+  for (uint32_t r = 0; r < kDraftK; ++r) {
+    const uint64_t best = wave_max_u64(hc);
+    if (best != 0 && hc == best) {
+      ids[r] = ~(uint32_t)best;
+      values[r] = u2f(vbits[lane * kDraftK + head]);
+      ++head;
+      hc = head < kDraftK ? comp[lane * kDraftK + head] : 0ull;
     }
-  }
-  __syncthreads();
-  if (tid < kDraftK) {
-    const uint64_t c = s.top[tid];
-    d.candidates[(uint64_t)row * kDraftK + tid] = c ? ~(uint32_t)c : kNoToken;
-    d.unary[(uint64_t)row * kDraftK + tid] = u2f(s.topv[tid]);
+    if (best == 0 && lane == 0) {
+      ids[r] = kNoToken;
+      values[r] = -__builtin_inff();
+    }
   }
 }
 
@@ -246,15 +227,21 @@ struct __align__(16) DraftEdgeLds {
   float ctx[kDraftK][kPad];   // predecessor codebook row x hidden
   float succ[kDraftK][kPad];  // successor codebook rows
   float hid[kRank];
+  uint64_t pcomp[2][kDraftMaxChunks * kDraftK];  // partials of this row, previous row
+  uint32_t pvbits[2][kDraftMaxChunks * kDraftK];
+  uint32_t ids[2][kDraftK];                 // the merged candidates of both rows
+  float vals[2][kDraftK];
   uint32_t pred[kDraftK];
   uint32_t cand[kDraftK];
   uint32_t last;
 };
 
-// One proposal position of one lane: the edge scores from each predecessor
-// (the anchor at position 0, else the previous position's candidates) to each
-// candidate, sum over the rank in ascending order; ids are clamped into the
-// codebooks (sampling.metal:1259-1262). The lane's last block walks.
+// One proposal position of one lane: this row's top 16 from its chunk
+// partials (the row's candidates and unary scores), the previous row's for
+// its predecessors (the anchor at position 0), then the edge scores from
+// each predecessor to each candidate, summed over the rank in ascending
+// order; ids are clamped into the codebooks (sampling.metal:1259-1262). The
+// lane's last block walks.
 __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   __shared__ DraftEdgeLds s;
   __shared__ float tbl[kDraftPositions][kDraftK * kDraftK];
@@ -262,16 +249,28 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   __shared__ uint32_t cands[kDraftPositions][kDraftK];
   const uint32_t p = blockIdx.x, lane_index = blockIdx.y;
   const uint32_t row = lane_index * kDraftPositions + p, tid = threadIdx.x;
-  const uint32_t V = d.vocabulary;
+  const uint32_t V = d.vocabulary, S = d.chunks;
   const DraftLaneParams lp = d.lane_params[lane_index];
-  if (tid < kDraftK) {
-    const uint32_t c = d.candidates[(uint64_t)row * kDraftK + tid];
-    const uint32_t pr = p ? d.candidates[(uint64_t)(row - 1) * kDraftK + tid] : lp.anchor;
-    s.cand[tid] = min(c, V - 1u);
-    s.pred[tid] = min(pr, V - 1u);
+  const uint32_t total = S * kDraftK, rows_here = p ? 2u : 1u;
+  for (uint32_t e = tid; e < rows_here * total; e += kThreads) {
+    const uint32_t which = e >= total, k = e - which * total;
+    const uint64_t at = (uint64_t)(row - which) * total + k;
+    s.pcomp[which][k] = d.part_comp[at];
+    s.pvbits[which][k] = d.part_vbits[at];
   }
   const uint16_t *h = d.hidden + ((uint64_t)lane_index * kDraftQueryRows + p + 1) * kRank;
   s.hid[tid] = bf16f(h[tid]);
+  __syncthreads();
+  const uint32_t wave = tid >> 6;
+  if (wave < rows_here) draft_merge_row(s.pcomp[wave], s.pvbits[wave], S, s.ids[wave], s.vals[wave]);
+  __syncthreads();
+  if (tid < kDraftK) {
+    // This row's outputs; the walk reads them back device-coherently.
+    st_dev(d.candidates + (uint64_t)row * kDraftK + tid, s.ids[0][tid]);
+    st_dev(d.unary + (uint64_t)row * kDraftK + tid, s.vals[0][tid]);
+    s.cand[tid] = min(s.ids[0][tid], V - 1u);
+    s.pred[tid] = min(p ? s.ids[1][tid] : lp.anchor, V - 1u);
+  }
   __syncthreads();
   // 16 rows x 32 sixteen-byte pieces of each codebook, two pieces a thread.
   const uint32_t preds = p ? kDraftK : 1u;
@@ -301,6 +300,7 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   float *table = d.tables + (uint64_t)lane_index * kDraftPositions * kDraftK * kDraftK;
   if (i < preds) {
     float acc = 0.0f;
+#pragma unroll 16
     for (uint32_t dm = 0; dm < kRank; ++dm) acc = acc + s.ctx[i][dm] * s.succ[j][dm];
     st_dev(table + (p * kDraftK + i) * kDraftK + j, acc);
   }
@@ -326,8 +326,8 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
     tbl[pp][q] = pp || q < kDraftK ? ld_dev(table + e) : 0.0f;
   }
   if (tid < kDraftPositions * kDraftK) {
-    un[tid / kDraftK][tid % kDraftK] = d.unary[r0 + tid];
-    cands[tid / kDraftK][tid % kDraftK] = d.candidates[r0 + tid];
+    un[tid / kDraftK][tid % kDraftK] = ld_dev(d.unary + r0 + tid);
+    cands[tid / kDraftK][tid % kDraftK] = ld_dev(d.candidates + r0 + tid);
   }
   __syncthreads();
   if (tid >= 64) return;

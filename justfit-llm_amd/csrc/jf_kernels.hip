@@ -2375,31 +2375,6 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(SampleLaunch a) {
 // (an overflowed chunk, a list longer than the slots fetched, values that do
 // not spread over the bins) take merge_kernel's general path.
 
-// Bitonic sort of one 32-bit value per lane over the wave, ascending.
-__device__ __forceinline__ uint32_t wave_sort_asc_u32(uint32_t v) {
-  const uint32_t lane = lane_id();
-#pragma unroll
-  for (int k = 2; k <= 64; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      uint32_t o;
-      switch (j) {
-        case 1: o = xor_u32<1>(v); break;
-        case 2: o = xor_u32<2>(v); break;
-        case 4: o = xor_u32<4>(v); break;
-        case 8: o = xor_u32<8>(v); break;
-        case 16: o = xor_u32<16>(v); break;
-        default: o = xor_u32<32>(v); break;
-      }
-      const bool lower = (lane & j) == 0;
-      const bool block_asc = (lane & k) == 0;
-      const bool take_smaller = lower == block_asc;
-      v = take_smaller ? min(v, o) : max(v, o);
-    }
-  }
-  return v;
-}
-
 // The exact top-K (K <= 64) of a row's candidates held in registers (v[k] =
 // key | id << 32; bit k of `valid` set for an item at or above the floor),
 // written to s.merge.key/id[0, n) in (key desc, id asc) order, n = min(K,

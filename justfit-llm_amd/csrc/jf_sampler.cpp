@@ -798,6 +798,7 @@ struct jf_draft_selector {
   uint32_t *part_vbits = nullptr;
   float *tables = nullptr;                     // [max_lanes][7][16][16]
   uint32_t *counters = nullptr;                // [max_lanes * 8]
+  std::vector<jf::DraftLaneParams> last_lanes;  // what lane_params holds
   StagingRing staging;
 };
 
@@ -886,9 +887,16 @@ int jf_draft_select(jf_draft_selector *d, const jf_draft_select_args *a, void *s
   }
   if (any_sampled && (!a->uniforms || !a->proposal_probs))
     return fail(JF_ERR_INVALID_ARGUMENT, "proposal uniform buffer too small");
-  rc = d->staging.upload(d->lane_params, lanes.data(), lanes.size() * sizeof(jf::DraftLaneParams),
-                         (hipStream_t)stream);
-  if (rc != JF_OK) return rc;
+  // Uploaded only when they change (stream order keeps earlier launches on
+  // the values they were enqueued with).
+  const size_t lane_bytes = lanes.size() * sizeof(jf::DraftLaneParams);
+  if (d->last_lanes.size() != lanes.size() ||
+      std::memcmp(d->last_lanes.data(), lanes.data(), lane_bytes) != 0) {
+    d->last_lanes.clear();
+    rc = d->staging.upload(d->lane_params, lanes.data(), lane_bytes, (hipStream_t)stream);
+    if (rc != JF_OK) return rc;
+    d->last_lanes = lanes;
+  }
   jf::DraftLaunch L{};
   L.logits = a->logits;
   L.stride = a->logits_stride;
