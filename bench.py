@@ -31,9 +31,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
-    ap.add_argument("--path", default="sample", choices=["sample", "draft"],
+    ap.add_argument("--path", default="sample", choices=["sample", "draft", "gather"],
                     help="sample: jf_sample on --config (the headline); draft: "
-                         "jf_draft_select at 4 lanes, V=151936")
+                         "jf_draft_select at 4 lanes, V=151936; gather: jf_tree_gather "
+                         "of one KV-like tensor family after C4's tree acceptance")
     ap.add_argument("--mode", default="auto",
                     help="C3/C4: greedy or sampled (auto: sampled)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -266,7 +267,7 @@ def cpu_baseline(w, seconds):
 def read_traffic(cfg):
     """HBM bytes per launch and the kernel they were counted on, from the
     committed rocprofv3 --pmc summary (its first line names the kernel)."""
-    name = "draft_top16" if cfg == "draft" else f"select_c{cfg}"
+    name = {"draft": "draft_top16", "gather": "tree_gather"}.get(cfg, f"select_c{cfg}")
     path = os.path.join(REPO, "profiles", f"{name}_traffic.txt")
     if not os.path.exists(path):
         return None, None
@@ -403,6 +404,88 @@ def bench_draft(args):
     sel.close()
 
 
+def bench_gather(args):
+    """The tree gather (jf_tree_gather) of one KV-like tensor family: 16
+    lanes (C4's requests) x 16 verify rows, 36 layers x 1024 bf16 columns
+    per row (8 KV heads x 128), each lane's accepted path (ascending, depth
+    <= 8) moved to its first rows. Algorithmic bytes: each moved element read
+    and written once."""
+    import torch
+    import jf_sampler as J
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    from gather_cases import gather_case
+    rng = np.random.default_rng(7)
+    data, path, retained, p = gather_case(rng, lanes=16, layers=36, rows=16, columns=1024,
+                                          inner=1024, pad=0)
+    moved = sum(1 for b in range(p["lanes"]) for i in range(min(int(retained[b]), 8))
+                if int(path[b, i]) != i)
+    alg = moved * p["layers"] * p["columns"] * 2 * 2
+    print(f"# tree gather {p}: {moved} moved rows", file=sys.stderr, flush=True)
+    dev = torch.device("cuda", 0)
+    base = torch.from_numpy(data.view(np.int16))
+    copies = [base.to(dev) for _ in range(max(2, -(-ROTATE_BYTES // data.nbytes)))]
+    pr = torch.from_numpy(path.view(np.int32)).to(dev)
+    rt = torch.from_numpy(retained.view(np.int32)).to(dev)
+    argv = [J.tree_gather_args(c, pr, rt, **p) for c in copies]
+    for i in range(args.warmup):
+        J.tree_gather(argv[i % len(argv)])
+    torch.cuda.synchronize()
+    K = args.steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
+    wall0 = time.perf_counter()
+    ev[0].record()
+    for i in range(K):
+        J.tree_gather(argv[(args.warmup + i) % len(argv)])
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    per = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(K)]) * 1000.0
+    ms_per_step = ev[0].elapsed_time(ev[K]) / K
+    hev = HipEvents(2 * K)
+    for i in range(K):
+        a = argv[(args.warmup + i) % len(argv)]
+        a.start_event, a.done_event = hev.ev[2 * i].value, hev.ev[2 * i + 1].value
+        J.tree_gather(a)
+        a.start_event = a.done_event = None
+    torch.cuda.synchronize()
+    kus = np.array([hev.ms(2 * i, 2 * i + 1) for i in range(K)]) * 1000.0
+    hev.destroy()
+    achieved = alg / (kus.mean() * 1e-6) / 1e9
+    traffic, kernel = read_traffic("gather")
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle as O
+        steps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds:
+            O.tree_gather(data, path, retained, **p)
+            steps += 1
+        el = time.perf_counter() - t0
+        cpu = dict(value=steps / el, unit="gathers/s", cores=1, kind="port",
+                   sample=f"{steps} whole gathers of the same inputs in {el:.1f} s (each "
+                          f"includes a {data.nbytes >> 20} MiB copy of the tensor), "
+                          f"oracle/jf_oracle.c -O2, one thread")
+    line = {
+        "metric": "tree gathers/sec of one KV-like family (16 lanes x 16 rows, 36 layers x "
+                  "1024 bf16); achieved HBM GB/s vs peak; p50 us/gather",
+        "value": 1000.0 / ms_per_step, "unit": "gathers/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "p50_us": float(np.percentile(per, 50)), "p90_us": float(np.percentile(per, 90)),
+        "wall_s": wall, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u16", "data": f"synthetic (tests/gather_cases.py, seed 7), {len(copies)} rotated "
+                                f"copies >= 512 MB",
+        "config": {"workload": "tree gather 16 lanes x 16 rows x 36 layers x 1024 columns bf16",
+                   "moved_rows": moved, "algorithmic_bytes_per_step": alg},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                     "kernel": kernel or "jf::tree_gather_kernel<true>",
+                     "kernel_mean_us": float(kus.mean()),
+                     "kernel_p50_us": float(np.percentile(kus, 50)), "algorithmic_bytes": alg},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -422,6 +505,9 @@ def main():
         sys.exit(1)
     if args.path == "draft":
         bench_draft(args)
+        return
+    if args.path == "gather":
+        bench_gather(args)
         return
     w = build_workload(args.config, args.mode)
     print(f"# {w['name']}: building inputs", file=sys.stderr, flush=True)

@@ -324,6 +324,41 @@ typedef struct jf_draft_select_args {
 int jf_draft_select(jf_draft_selector *selector,
                     const jf_draft_select_args *args, void *stream);
 
+/* ---- tree gather -------------------------------------------------------- */
+
+/* verify_tree_gather (tree.metal:86-107), which Runtime::encodeTreeGathers
+ * (Runtime.cpp:1311-1341) dispatches once per tensor family: in place, each
+ * lane's accepted path rows move to rows 0 .. retained - 1. The layout fields
+ * are JustFitTreeGatherParams (metal/abi/TreeVerify.h:54-69), in 16-bit
+ * units: element (row, column) of lane b and layer y sits at
+ *   y*layer_stride + b*lane_stride + row*row_stride
+ *   + (column / inner)*outer_stride + (column % inner)*inner_stride.
+ * path_rows + b*8 and retained[b] are jf_accept_tree's outputs (device).
+ * With no counterpart in the reference, for the extent check and device
+ * safety: data_units (elements in data) and rows (rows per lane of the
+ * tensor, 1..16; a path row at or past it is skipped). Optional
+ * start_event/done_event (hipEvent_t) bracket the kernel. */
+typedef struct jf_tree_gather_args {
+  uint16_t *data;
+  uint64_t data_units;
+  const uint32_t *path_rows;
+  const uint32_t *retained;
+  uint32_t columns;
+  uint32_t inner;
+  uint32_t inner_stride;
+  uint32_t outer_stride;
+  uint32_t row_stride;
+  uint32_t lane_stride;
+  uint32_t layer_stride;
+  uint32_t layers;
+  uint32_t lanes;
+  uint32_t rows;
+  void *start_event;
+  void *done_event;
+} jf_tree_gather_args;
+
+int jf_tree_gather(const jf_tree_gather_args *args, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

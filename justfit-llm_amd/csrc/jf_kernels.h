@@ -281,6 +281,18 @@ struct DraftLaunch {
   uint32_t *counters;         // [lanes * 8], zero between launches
 };
 
+// The tree gather (jf_gather.hip): JustFitTreeGatherParams (TreeVerify.h:54-69)
+// in 16-bit units, plus the rows per lane of the tensor.
+constexpr uint32_t kGatherDepth = 8;  // path entries per lane
+struct GatherLaunch {
+  uint16_t *data;
+  const uint32_t *path_rows;  // [lanes][8]
+  const uint32_t *retained;   // [lanes]
+  uint32_t columns, inner, inner_stride, outer_stride;
+  uint64_t row_stride, lane_stride, layer_stride;
+  uint32_t layers, lanes, rows;
+};
+
 // Launchers (jf_kernels.hip); they return the hipError_t of the launch.
 // With both events set, they record the selection kernel's own start and end.
 int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
@@ -298,5 +310,8 @@ int launch_accept_tree(const AcceptTreeLaunch &a, void *stream);
 // jf_draft.hip; the events, when set, bracket the top-16 kernel.
 int launch_draft_select(const DraftLaunch &d, bool aligned, void *stream,
                         void *start_event = nullptr, void *stop_event = nullptr);
+// jf_gather.hip; vec8: 8 columns per thread with 16-byte accesses.
+int launch_tree_gather(const GatherLaunch &g, bool vec8, void *stream,
+                       void *start_event = nullptr, void *stop_event = nullptr);
 
 }  // namespace jf

@@ -923,4 +923,46 @@ int jf_draft_select(jf_draft_selector *d, const jf_draft_select_args *a, void *s
   return JF_OK;
 }
 
+// ---- tree gather -------------------------------------------------------------
+
+int jf_tree_gather(const jf_tree_gather_args *a, void *stream) {
+  if (!a) return fail(JF_ERR_INVALID_ARGUMENT, "null tree gather arguments");
+  if (!a->data || !a->path_rows || !a->retained)
+    return fail(JF_ERR_INVALID_ARGUMENT, "tree gather buffers are null");
+  if (!a->columns || !a->inner || !a->layers || !a->lanes || !a->rows ||
+      a->rows > JF_TREE_MAXIMUM_ROWS)
+    return fail(JF_ERR_INVALID_ARGUMENT, "invalid tree gather geometry");
+  if ((a->start_event == nullptr) != (a->done_event == nullptr))
+    return fail(JF_ERR_INVALID_ARGUMENT, "gather events come in pairs");
+  // The largest unit any thread touches.
+  const uint64_t last_column = a->columns - 1u;
+  const uint64_t in_group = std::min<uint64_t>(a->inner - 1u, last_column);
+  const uint64_t top = (uint64_t)(a->layers - 1u) * a->layer_stride +
+                       (uint64_t)(a->lanes - 1u) * a->lane_stride +
+                       (uint64_t)(a->rows - 1u) * a->row_stride +
+                       (last_column / a->inner) * a->outer_stride + in_group * a->inner_stride;
+  if (top >= a->data_units) return fail(JF_ERR_INVALID_ARGUMENT, "tree gather data buffer too small");
+  jf::GatherLaunch g{};
+  g.data = a->data;
+  g.path_rows = a->path_rows;
+  g.retained = a->retained;
+  g.columns = a->columns;
+  g.inner = a->inner;
+  g.inner_stride = a->inner_stride;
+  g.outer_stride = a->outer_stride;
+  g.row_stride = a->row_stride;
+  g.lane_stride = a->lane_stride;
+  g.layer_stride = a->layer_stride;
+  g.layers = a->layers;
+  g.lanes = a->lanes;
+  g.rows = a->rows;
+  // 8 columns a thread when a row's columns are contiguous 16-byte runs.
+  const bool vec8 = (uintptr_t)a->data % 16 == 0 && a->inner_stride == 1 && a->inner % 8 == 0 &&
+                    a->columns % 8 == 0 && a->outer_stride % 8 == 0 && a->row_stride % 8 == 0 &&
+                    a->row_stride >= 8 && a->lane_stride % 8 == 0 && a->layer_stride % 8 == 0;
+  const int e = jf::launch_tree_gather(g, vec8, stream, a->start_event, a->done_event);
+  if (e != hipSuccess) return hip_fail((hipError_t)e, "tree gather launch");
+  return JF_OK;
+}
+
 }  // extern "C"

@@ -36,6 +36,7 @@ EXPORTS = [
     "jf_next_uniform", "jf_stage_sampling_cycle", "jf_sample",
     "jf_accept_chain", "jf_accept_tree",
     "jf_draft_selector_create", "jf_draft_selector_destroy", "jf_draft_select",
+    "jf_tree_gather",
 ]
 
 c_u32 = ctypes.c_uint32
@@ -112,6 +113,13 @@ class JfDraftSelectArgs(ctypes.Structure):
     ]
 
 
+class JfTreeGatherArgs(ctypes.Structure):
+    _fields_ = [("data", c_vp), ("data_units", c_u64), ("path_rows", c_vp), ("retained", c_vp)] + [
+        (n, c_u32) for n in ("columns", "inner", "inner_stride", "outer_stride", "row_stride",
+                             "lane_stride", "layer_stride", "layers", "lanes", "rows")] + [
+        ("start_event", c_vp), ("done_event", c_vp)]
+
+
 class JfError(RuntimeError):
     def __init__(self, code, message):
         super().__init__(f"jf error {code}: {message}")
@@ -160,6 +168,7 @@ def lib():
         L.jf_draft_selector_create.argtypes = [c_u32, c_u32, ctypes.POINTER(c_vp)]
         L.jf_draft_selector_destroy.argtypes = [c_vp]
         L.jf_draft_select.argtypes = [c_vp, ctypes.POINTER(JfDraftSelectArgs), c_vp]
+        L.jf_tree_gather.argtypes = [ctypes.POINTER(JfTreeGatherArgs), c_vp]
         _lib = L
     return _lib
 
@@ -454,6 +463,24 @@ class DraftSelector:
             self.close()
         except Exception:
             pass
+
+
+def tree_gather_args(data, path_rows, retained, **layout):
+    """A jf_tree_gather_args over torch device tensors (data: 16-bit
+    elements); layout: columns, inner, inner_stride, outer_stride,
+    row_stride, lane_stride, layer_stride, layers, lanes, rows."""
+    a = JfTreeGatherArgs()
+    a.data = _ptr(data)
+    a.data_units = data.numel()
+    a.path_rows = _ptr(path_rows)
+    a.retained = _ptr(retained)
+    for k, v in layout.items():
+        setattr(a, k, v)
+    return a
+
+
+def tree_gather(a, stream=None):
+    check(lib().jf_tree_gather(ctypes.byref(a), stream if stream is not None else _stream()))
 
 
 def tree_lane(parent, token, chain_rows=0, chain_q=None):

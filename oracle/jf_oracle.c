@@ -718,3 +718,26 @@ void jfo_draft_select_lane(const jfo_draft_lane *lane, const float *logits8,
     tokens[p] = candidates[p * K + selected];
   }
 }
+
+/* ---- tree gather --------------------------------------------------------- */
+
+/* verify_tree_gather (tree.metal:86-107), one column at a time. Pinned by
+ * tests/test_oracle.py against the closed form row i := original row
+ * path[i] (i < retained), other rows unchanged. */
+void jfo_tree_gather(uint16_t *data, const uint32_t *path_rows,
+                     const uint32_t *retained, const jfo_gather_params *p) {
+  for (uint32_t b = 0; b < p->lanes; ++b) {
+    uint32_t rows = retained[b] < JFO_TREE_MAX_DEPTH ? retained[b] : JFO_TREE_MAX_DEPTH;
+    for (uint32_t y = 0; y < p->layers; ++y)
+      for (uint32_t c = 0; c < p->columns; ++c) {
+        const uint64_t base = (uint64_t)y * p->layer_stride + (uint64_t)b * p->lane_stride +
+                              (uint64_t)(c / p->inner) * p->outer_stride +
+                              (uint64_t)(c % p->inner) * p->inner_stride;
+        for (uint32_t i = 0; i < rows; ++i) {
+          const uint32_t src = path_rows[b * JFO_TREE_MAX_DEPTH + i];
+          if (src != i && src < p->rows)
+            data[base + (uint64_t)i * p->row_stride] = data[base + (uint64_t)src * p->row_stride];
+        }
+      }
+  }
+}

@@ -183,6 +183,20 @@ void jfo_draft_select_lane(const jfo_draft_lane *lane, const float *logits8,
                            const float *uniforms40, uint32_t *candidates,
                            float *unary, uint32_t *tokens, float *q);
 
+/* Tree gather (verify_tree_gather, tree.metal:86-107; params TreeVerify.h:54-69):
+ * for each lane b < lanes, layer y < layers and column c < columns, element
+ * (row, c) sits at base + row * row_stride with base = y * layer_stride +
+ * b * lane_stride + (c / inner) * outer_stride + (c % inner) * inner_stride
+ * (16-bit units); rows i < retained[b] take row path_rows[b * 8 + i], copied
+ * in increasing i, in place. Sources at or past `rows` (rows per lane) are
+ * skipped. */
+typedef struct {
+  uint32_t columns, inner, inner_stride, outer_stride, row_stride, lane_stride,
+      layer_stride, layers, lanes, rows;
+} jfo_gather_params;
+void jfo_tree_gather(uint16_t *data, const uint32_t *path_rows,
+                     const uint32_t *retained, const jfo_gather_params *p);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,12 @@ class DraftLane(ctypes.Structure):
                 ("sampled", ctypes.c_int)]
 
 
+class GatherParams(ctypes.Structure):
+    _fields_ = [(n, c_u32) for n in ("columns", "inner", "inner_stride", "outer_stride",
+                                     "row_stride", "lane_stride", "layer_stride", "layers",
+                                     "lanes", "rows")]
+
+
 def build():
     subprocess.run(["make", "-s", "-C", HERE], check=True)
     return LIB_PATH
@@ -108,6 +114,8 @@ def lib():
         L.jfo_draft_select_lane.argtypes = [ctypes.POINTER(DraftLane), c_vp, c_u64, c_vp,
                                             c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]
         L.jfo_draft_select_lane.restype = None
+        L.jfo_tree_gather.argtypes = [c_vp, c_vp, c_vp, ctypes.POINTER(GatherParams)]
+        L.jfo_tree_gather.restype = None
         _lib = L
     return _lib
 
@@ -295,3 +303,13 @@ def draft_select(logits, hidden, pred_codebook, succ_codebook, anchors, temperat
         lib().jfo_draft_select_lane(ctypes.byref(lane), _p(lg), V, _p(hd), _p(pc), _p(sc),
                                     _p(np.ascontiguousarray(u[l])), _p(c), _p(un), _p(t), _p(qq))
     return cand, unary, tokens, q
+
+
+def tree_gather(data, path_rows, retained, **params):
+    """verify_tree_gather in place on a copy of `data` (uint16); returns it."""
+    out = np.ascontiguousarray(data, dtype=np.uint16).copy()
+    pr = np.ascontiguousarray(path_rows, dtype=np.uint32)
+    rt = np.ascontiguousarray(retained, dtype=np.uint32)
+    p = GatherParams(**params)
+    lib().jfo_tree_gather(_p(out), _p(pr), _p(rt), ctypes.byref(p))
+    return out

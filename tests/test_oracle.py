@@ -527,3 +527,16 @@ def test_draft_walk_greedy_and_sampled():
                 sel = int(hit[0]) if len(hit) else 15
             assert tokens[l, p] == cand[l, p, sel]
             pred = sel
+
+
+# ---- tree gather (tree.metal:86-107) ---------------------------------------
+
+from gather_cases import gather_case, gather_closed_form
+
+@pytest.mark.parametrize("shape", [dict(), dict(columns=48, inner=8, inner_stride=2, outer_stride=20),
+                                   dict(columns=30, inner=5, inner_stride=1, outer_stride=7)])
+def test_tree_gather_closed_form(shape):
+    rng = np.random.default_rng(len(shape))
+    data, path, retained, p = gather_case(rng, **shape)
+    got = O.tree_gather(data, path, retained, **p)
+    assert np.array_equal(got, gather_closed_form(data, path, retained, p))
