@@ -319,10 +319,48 @@ typedef struct jf_draft_select_args {
   float *proposal_probs;                 /* device; needed when a lane samples */
   void *select_start_event;
   void *select_done_event;
+  /* Optional (device, [lanes][7][16][16], or NULL): the edge tables, entry
+   * (p, i, j) the score from predecessor i to candidate j at position p, for
+   * jf_build_draft_tree. Position 0 has only predecessor 0 (the anchor); its
+   * other rows are left unwritten. */
+  float *edge_tables;
 } jf_draft_select_args;
 
 int jf_draft_select(jf_draft_selector *selector,
                     const jf_draft_select_args *args, void *stream);
+
+/* ---- draft tree builder ------------------------------------------------- */
+
+/* One lane's draft tree in its verify rows: JustFitTreeLane
+ * (metal/abi/TreeVerify.h:14-32). Rows are in DFS preorder: row 0 is the
+ * anchor (depth 0) and every row's parent row is smaller than the row. A copy
+ * is one root-to-leaf path; path[c][d] is its row at depth d. Every row
+ * belongs to the first copy, in DFS order, whose path holds it. */
+typedef struct jf_draft_tree {
+  uint32_t rows;
+  uint32_t copies;
+  uint32_t parent[JF_TREE_MAXIMUM_ROWS];
+  uint32_t depth[JF_TREE_MAXIMUM_ROWS];
+  uint32_t copy[JF_TREE_MAXIMUM_ROWS];
+  uint32_t token[JF_TREE_MAXIMUM_ROWS];
+  uint32_t path_length[JF_TREE_MAXIMUM_ROWS];
+  uint32_t path[JF_TREE_MAXIMUM_ROWS][JF_TREE_MAXIMUM_DEPTH];
+} jf_draft_tree;
+
+/* buildDraftTree (source/runtime/model/Runtime.cpp:58-174), host only and
+ * synchronous: one lane's tree of at most `rows` (1..16) rows from the draft
+ * selector's candidates [7][16] and unary scores [7][16] (jf_draft_select's
+ * outputs) and its edge tables [7][16][16] (entry (p, i, j): predecessor i to
+ * candidate j at position p; position 0 reads predecessor 0, the anchor).
+ * Nodes are taken best first by path log-probability (double), children of a
+ * node scored by a log-softmax over its 16 candidates. chain_picks (7
+ * candidate indices, or NULL) forces a sampled lane's chain as the leftmost
+ * path. expected / chain_expected (optional) receive the sum of the tree's
+ * node probabilities and that of the selector's own greedy chain. */
+int jf_build_draft_tree(const uint32_t *candidates, const float *unary,
+                        const float *edges, uint32_t anchor, uint32_t rows,
+                        const uint32_t *chain_picks, jf_draft_tree *out,
+                        double *expected, double *chain_expected);
 
 /* ---- tree gather -------------------------------------------------------- */
 

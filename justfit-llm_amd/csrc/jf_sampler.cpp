@@ -111,6 +111,11 @@ uint32_t effective_top_k(const jf_policy &p, uint32_t vocabulary) {
 
 }  // namespace
 
+namespace jf {
+// For the library's other host sources (jf_tree.cpp).
+int set_error(int code, const char *message) { return fail(code, message); }
+}  // namespace jf
+
 struct jf_penalty_table {
   uint32_t vocabulary = 0;
   uint32_t rows = 0;
@@ -914,7 +919,7 @@ int jf_draft_select(jf_draft_selector *d, const jf_draft_select_args *a, void *s
   L.q_probs = a->proposal_probs;
   L.part_comp = d->part_comp;
   L.part_vbits = d->part_vbits;
-  L.tables = d->tables;
+  L.tables = a->edge_tables ? a->edge_tables : d->tables;
   L.counters = d->counters;
   const bool aligned = (uintptr_t)a->logits % 16 == 0 && a->logits_stride % 4 == 0;
   const int e = jf::launch_draft_select(L, aligned, stream, a->select_start_event,

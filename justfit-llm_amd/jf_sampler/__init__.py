@@ -36,7 +36,7 @@ EXPORTS = [
     "jf_next_uniform", "jf_stage_sampling_cycle", "jf_sample",
     "jf_accept_chain", "jf_accept_tree",
     "jf_draft_selector_create", "jf_draft_selector_destroy", "jf_draft_select",
-    "jf_tree_gather",
+    "jf_tree_gather", "jf_build_draft_tree",
 ]
 
 c_u32 = ctypes.c_uint32
@@ -110,6 +110,7 @@ class JfDraftSelectArgs(ctypes.Structure):
         ("uniforms", c_vp), ("candidates", c_vp), ("unary", c_vp),
         ("proposed_tokens", c_vp), ("proposal_probs", c_vp),
         ("select_start_event", c_vp), ("select_done_event", c_vp),
+        ("edge_tables", c_vp),
     ]
 
 
@@ -118,6 +119,12 @@ class JfTreeGatherArgs(ctypes.Structure):
         (n, c_u32) for n in ("columns", "inner", "inner_stride", "outer_stride", "row_stride",
                              "lane_stride", "layer_stride", "layers", "lanes", "rows")] + [
         ("start_event", c_vp), ("done_event", c_vp)]
+
+
+class JfDraftTree(ctypes.Structure):
+    _fields_ = [("rows", c_u32), ("copies", c_u32), ("parent", c_u32 * 16), ("depth", c_u32 * 16),
+                ("copy", c_u32 * 16), ("token", c_u32 * 16), ("path_length", c_u32 * 16),
+                ("path", (c_u32 * 8) * 16)]
 
 
 class JfError(RuntimeError):
@@ -169,6 +176,9 @@ def lib():
         L.jf_draft_selector_destroy.argtypes = [c_vp]
         L.jf_draft_select.argtypes = [c_vp, ctypes.POINTER(JfDraftSelectArgs), c_vp]
         L.jf_tree_gather.argtypes = [ctypes.POINTER(JfTreeGatherArgs), c_vp]
+        L.jf_build_draft_tree.argtypes = [c_vp, c_vp, c_vp, c_u32, c_u32, c_vp,
+                                          ctypes.POINTER(JfDraftTree), ctypes.POINTER(ctypes.c_double),
+                                          ctypes.POINTER(ctypes.c_double)]
         _lib = L
     return _lib
 
@@ -425,7 +435,7 @@ class DraftSelector:
         self.max_lanes = max_lanes
 
     def args(self, *, logits, hidden, pred_codebook, succ_codebook, anchors, policies,
-             candidates, unary, tokens, q=None, uniforms=None, stride=None):
+             candidates, unary, tokens, q=None, uniforms=None, stride=None, edge_tables=None):
         """A jf_draft_select_args over torch device tensors; `anchors` and
         `policies` are host sequences (kept alive on the returned object)."""
         import numpy as np
@@ -446,6 +456,7 @@ class DraftSelector:
         a.unary = _ptr(unary)
         a.proposed_tokens = _ptr(tokens)
         a.proposal_probs = _ptr(q)
+        a.edge_tables = _ptr(edge_tables)
         a._keep = (anc, pol)
         return a
 
@@ -481,6 +492,25 @@ def tree_gather_args(data, path_rows, retained, **layout):
 
 def tree_gather(a, stream=None):
     check(lib().jf_tree_gather(ctypes.byref(a), stream if stream is not None else _stream()))
+
+
+def build_draft_tree(candidates, unary, edges, anchor, rows, chain_picks=None):
+    """jf_build_draft_tree on host arrays; returns the tree as a dict plus
+    expected / chain_expected."""
+    import numpy as np
+    c = np.ascontiguousarray(candidates, dtype=np.uint32)
+    u = np.ascontiguousarray(unary, dtype=np.float32)
+    e = np.ascontiguousarray(edges, dtype=np.float32)
+    cp = None if chain_picks is None else np.ascontiguousarray(chain_picks, dtype=np.uint32)
+    t = JfDraftTree()
+    ex, cx = ctypes.c_double(), ctypes.c_double()
+    check(lib().jf_build_draft_tree(c.ctypes.data_as(c_vp), u.ctypes.data_as(c_vp),
+                                    e.ctypes.data_as(c_vp), anchor, rows,
+                                    None if cp is None else cp.ctypes.data_as(c_vp),
+                                    ctypes.byref(t), ctypes.byref(ex), ctypes.byref(cx)))
+    return dict(rows=t.rows, copies=t.copies, parent=list(t.parent), depth=list(t.depth),
+                copy=list(t.copy), token=list(t.token), path_length=list(t.path_length),
+                path=[list(r) for r in t.path], expected=ex.value, chain_expected=cx.value)
 
 
 def tree_lane(parent, token, chain_rows=0, chain_q=None):

@@ -313,3 +313,110 @@ def tree_gather(data, path_rows, retained, **params):
     p = GatherParams(**params)
     lib().jfo_tree_gather(_p(out), _p(pr), _p(rt), ctypes.byref(p))
     return out
+
+
+# ---- draft tree builder (Runtime.cpp:58-174), pure Python ------------------
+#
+# The frontier is Python's heapq ordered by (-logp, pick, insertion order).
+# The reference's std::priority_queue breaks exact (logp, pick) ties by its
+# heap layout instead; the tests use inputs without such ties.
+
+def build_draft_tree(candidates, unary, edges, anchor, rows, chain_picks=None):
+    """Returns dict(rows, copies, parent, depth, copy, token, path_length,
+    path, expected, chain_expected) for one lane; candidates/unary [7][16],
+    edges [7][16][16] (float32 arrays)."""
+    import heapq
+    import math
+    C, P = 16, 7
+    un = np.asarray(unary, np.float32).reshape(P, C)
+    ed = np.asarray(edges, np.float32).reshape(P, C, C)
+    cand = np.asarray(candidates, np.uint32).reshape(P, C)
+
+    def score(p, k, j):
+        return float(un[p, j]) + float(ed[p, k, j])
+
+    def norm(p, k):
+        top = max(score(p, k, j) for j in range(C))
+        total = 0.0
+        for j in range(C):
+            total += math.exp(score(p, k, j) - top)
+        return top + math.log(total)
+
+    heap, seq = [], [0]
+
+    def expand(parent, p, k, base, skip=None):
+        n = norm(p, k)
+        for j in range(C):
+            if j != skip:
+                heapq.heappush(heap, (-(base + score(p, k, j) - n), j, seq[0], p, parent))
+                seq[0] += 1
+
+    nodes = [dict(token=int(anchor), depth=0, pick=0, logp=0.0, chain=chain_picks is not None,
+                  children=[])]
+    if chain_picks is not None:
+        parent, k, logp = 0, 0, 0.0
+        for p in range(P):
+            if len(nodes) >= rows:
+                break
+            pick = int(chain_picks[p])
+            base = logp
+            logp += score(p, k, pick) - norm(p, k)
+            expand(parent, p, k, base, pick)
+            nodes.append(dict(token=int(cand[p, pick]), depth=p + 1, pick=pick, logp=logp,
+                              chain=True, children=[]))
+            nodes[parent]["children"].append(len(nodes) - 1)
+            parent, k = len(nodes) - 1, pick
+    else:
+        expand(0, 0, 0, 0.0)
+    while len(nodes) < rows and heap:
+        neg, pick, _, p, parent = heapq.heappop(heap)
+        nodes.append(dict(token=int(cand[p, pick]), depth=p + 1, pick=pick, logp=-neg,
+                          chain=False, children=[]))
+        nodes[parent]["children"].append(len(nodes) - 1)
+        if p + 1 < P:
+            expand(len(nodes) - 1, p + 1, pick, -neg)
+    out = dict(rows=len(nodes), copies=0, parent=[0] * 16, depth=[0] * 16, copy=[0] * 16,
+               token=[0] * 16, path_length=[0] * 16, path=[[0] * 8 for _ in range(16)])
+    assigned = [False] * 16
+    stack, nxt = [], [0]
+
+    def visit(node, parent_row):
+        row = nxt[0]
+        nxt[0] += 1
+        out["parent"][row] = parent_row
+        out["depth"][row] = nodes[node]["depth"]
+        out["token"][row] = nodes[node]["token"]
+        stack.append(row)
+        kids = sorted(nodes[node]["children"],
+                      key=lambda c: (not nodes[c]["chain"], -nodes[c]["logp"], nodes[c]["pick"]))
+        if not kids:
+            c = out["copies"]
+            out["copies"] += 1
+            out["path_length"][c] = len(stack)
+            for i, r in enumerate(stack):
+                out["path"][c][i] = r
+            for r in stack:
+                if not assigned[r]:
+                    assigned[r] = True
+                    out["copy"][r] = c
+        for kid in kids:
+            visit(kid, row)
+        stack.pop()
+
+    visit(0, 0)
+    out["expected"] = sum(math.exp(n["logp"]) for n in nodes[1:])
+    total, logp, k = 0.0, 0.0, 0
+    for p in range(P):
+        top, best = -math.inf, 0
+        for j in range(C):
+            s = score(p, k, j)
+            if s > top:
+                top, best = s, j
+        ssum = 0.0
+        for j in range(C):
+            ssum += math.exp(score(p, k, j) - top)
+        logp -= math.log(ssum)
+        total += math.exp(logp)
+        k = best
+    out["chain_expected"] = total
+    return out
