@@ -362,6 +362,54 @@ int jf_build_draft_tree(const uint32_t *candidates, const float *unary,
                         const uint32_t *chain_picks, jf_draft_tree *out,
                         double *expected, double *chain_expected);
 
+/* ---- mask wire format --------------------------------------------------- */
+
+/* The frames between the engine's grammar and the runtime
+ * (source/runtime/engine/Protocol.hpp:22-25, 34-50, 185-203, 263-278): a
+ * 16-byte header ("SPLH", u16 protocol version 9, u16 frame type, u64
+ * payload bytes), then the payload; every integer little-endian. */
+#define JF_FRAME_MASK_RESPONSE 0x0003u
+#define JF_FRAME_MASK_REQUEST 0x0103u
+#define JF_FRAME_MASK_TREE_REQUEST 0x0109u
+
+/* encodeMaskRequest (Protocol.cpp:616-632) with validateMaskRequest
+ * (Protocol.cpp:469-500) at the default ProtocolLimits: payload u64
+ * request_id, u64 mask_request_id, u32 words_per_mask, u32 count, count u32
+ * simulation tokens, and for a tree (parents != NULL, MaskTreeRequest) count
+ * u32 parents (parents[0] == 0, parents[r] < r). `written` receives the frame
+ * bytes. */
+int jf_mask_request_encode(uint64_t request_id, uint64_t mask_request_id,
+                           uint32_t words_per_mask, const uint32_t *tokens,
+                           uint32_t count, const uint32_t *parents,
+                           uint8_t *out, uint64_t capacity, uint64_t *written);
+
+/* decodeMaskResponse (Protocol.cpp:793-820) with validateMaskResponse
+ * (402-414) of one whole MaskResponse frame: payload u64 request_id, u64
+ * mask_request_id, u32 count, count u32 mask words (into words, capacity
+ * words). */
+int jf_mask_response_decode(const uint8_t *frame, uint64_t bytes,
+                            uint64_t *request_id, uint64_t *mask_request_id,
+                            uint32_t *words, uint32_t capacity, uint32_t *count);
+
+/* Runtime::provideMask's checks (Runtime.cpp:3466-3481) on `rows` mask rows
+ * of mask_words words: every row admits a token, and for a verify mask
+ * (pending_token != JF_NO_TOKEN) row 0 admits the pending anchor. The rows
+ * are then the `masks` of jf_sample (mask_stride = mask_words). */
+int jf_mask_rows_check(const uint32_t *words, uint32_t rows,
+                       uint32_t mask_words, uint32_t pending_token);
+
+/* The row rules of the engine's masks (rust/frontend/src/grammar.rs:222-270),
+ * in place on count + 1 rows of mask_words words. Chain: rows 0..valid hold
+ * the masks after 0..valid accepted simulation tokens; rows past valid
+ * repeat row valid. Tree: row 0 is the state before the anchor and row r + 1
+ * the state after token row r's path; a token row whose own token is
+ * refused[r], or whose parent row is itself refused, takes the mask of its
+ * parent's row (row 0 for the anchor). */
+int jf_mask_chain_fill(uint32_t *words, uint32_t count, uint32_t valid,
+                       uint32_t mask_words);
+int jf_mask_tree_fill(uint32_t *words, uint32_t count, const uint32_t *parents,
+                      const uint8_t *refused, uint32_t mask_words);
+
 /* ---- tree gather -------------------------------------------------------- */
 
 /* verify_tree_gather (tree.metal:86-107), which Runtime::encodeTreeGathers

@@ -36,7 +36,8 @@ EXPORTS = [
     "jf_next_uniform", "jf_stage_sampling_cycle", "jf_sample",
     "jf_accept_chain", "jf_accept_tree",
     "jf_draft_selector_create", "jf_draft_selector_destroy", "jf_draft_select",
-    "jf_tree_gather", "jf_build_draft_tree",
+    "jf_tree_gather", "jf_build_draft_tree", "jf_mask_request_encode",
+    "jf_mask_response_decode", "jf_mask_rows_check", "jf_mask_chain_fill", "jf_mask_tree_fill",
 ]
 
 c_u32 = ctypes.c_uint32
@@ -179,6 +180,14 @@ def lib():
         L.jf_build_draft_tree.argtypes = [c_vp, c_vp, c_vp, c_u32, c_u32, c_vp,
                                           ctypes.POINTER(JfDraftTree), ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_double)]
+        L.jf_mask_request_encode.argtypes = [c_u64, c_u64, c_u32, c_vp, c_u32, c_vp, c_vp, c_u64,
+                                             ctypes.POINTER(c_u64)]
+        L.jf_mask_response_decode.argtypes = [c_vp, c_u64, ctypes.POINTER(c_u64),
+                                              ctypes.POINTER(c_u64), c_vp, c_u32,
+                                              ctypes.POINTER(c_u32)]
+        L.jf_mask_rows_check.argtypes = [c_vp, c_u32, c_u32, c_u32]
+        L.jf_mask_chain_fill.argtypes = [c_vp, c_u32, c_u32, c_u32]
+        L.jf_mask_tree_fill.argtypes = [c_vp, c_u32, c_vp, c_vp, c_u32]
         _lib = L
     return _lib
 
@@ -511,6 +520,55 @@ def build_draft_tree(candidates, unary, edges, anchor, rows, chain_picks=None):
     return dict(rows=t.rows, copies=t.copies, parent=list(t.parent), depth=list(t.depth),
                 copy=list(t.copy), token=list(t.token), path_length=list(t.path_length),
                 path=[list(r) for r in t.path], expected=ex.value, chain_expected=cx.value)
+
+
+def mask_request_encode(request_id, mask_id, words_per_mask, tokens, parents=None):
+    """One MaskRequest (or, with parents, MaskTreeRequest) frame as bytes."""
+    import numpy as np
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    p = None if parents is None else np.ascontiguousarray(parents, dtype=np.uint32)
+    out = np.zeros(16 + 24 + 8 * len(t), np.uint8)
+    n = c_u64()
+    check(lib().jf_mask_request_encode(request_id, mask_id, words_per_mask,
+                                       t.ctypes.data_as(c_vp), len(t),
+                                       None if p is None else p.ctypes.data_as(c_vp),
+                                       out.ctypes.data_as(c_vp), out.size, ctypes.byref(n)))
+    return out[:n.value].tobytes()
+
+
+def mask_response_decode(frame, capacity=1 << 20):
+    """(request_id, mask_request_id, words) of one MaskResponse frame."""
+    import numpy as np
+    f = np.frombuffer(frame, dtype=np.uint8)
+    words = np.zeros(capacity, np.uint32)
+    rid, mid, n = c_u64(), c_u64(), c_u32()
+    check(lib().jf_mask_response_decode(f.ctypes.data_as(c_vp), f.size, ctypes.byref(rid),
+                                        ctypes.byref(mid), words.ctypes.data_as(c_vp), capacity,
+                                        ctypes.byref(n)))
+    return rid.value, mid.value, words[:n.value].copy()
+
+
+def mask_rows_check(words, rows, mask_words, pending_token=JF_NO_TOKEN):
+    import numpy as np
+    w = np.ascontiguousarray(words, dtype=np.uint32)
+    check(lib().jf_mask_rows_check(w.ctypes.data_as(c_vp), rows, mask_words, pending_token))
+
+
+def mask_chain_fill(words, count, valid, mask_words):
+    import numpy as np
+    w = np.ascontiguousarray(words, dtype=np.uint32).copy()
+    check(lib().jf_mask_chain_fill(w.ctypes.data_as(c_vp), count, valid, mask_words))
+    return w
+
+
+def mask_tree_fill(words, parents, refused, mask_words):
+    import numpy as np
+    w = np.ascontiguousarray(words, dtype=np.uint32).copy()
+    p = np.ascontiguousarray(parents, dtype=np.uint32)
+    r = np.ascontiguousarray(refused, dtype=np.uint8)
+    check(lib().jf_mask_tree_fill(w.ctypes.data_as(c_vp), len(p), p.ctypes.data_as(c_vp),
+                                  r.ctypes.data_as(c_vp), mask_words))
+    return w
 
 
 def tree_lane(parent, token, chain_rows=0, chain_q=None):
