@@ -41,6 +41,7 @@ __device__ __forceinline__ float bf16f(uint32_t b) { return u2f(b << 16); }
 __device__ __forceinline__ float readlane_f32(float v, int l) {
   return u2f(readlane_u32(f2u(v), l));
 }
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // (key << 32 | ~id): larger means earlier in (value desc, id asc); ids are
 // unique within a row, so the order is total. 0 is the empty slot
@@ -233,6 +234,7 @@ struct __align__(16) DraftEdgeLds {
   float vals[2][kDraftK];
   uint32_t pred[kDraftK];
   uint32_t cand[kDraftK];
+  float walk[2 * kDraftK];  // the walk's weights, then quotients, in candidate order
   uint32_t last;
 };
 
@@ -252,11 +254,28 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   const uint32_t V = d.vocabulary, S = d.chunks;
   const DraftLaneParams lp = d.lane_params[lane_index];
   const uint32_t total = S * kDraftK, rows_here = p ? 2u : 1u;
-  for (uint32_t e = tid; e < rows_here * total; e += kThreads) {
+  // Every partial load issued before any lands in LDS (a load-then-store
+  // loop would wait for each round trip in turn).
+  constexpr uint32_t kPartLoads = 2 * kDraftMaxChunks * kDraftK / kThreads;
+  uint64_t pc[kPartLoads];
+  uint32_t pv[kPartLoads];
+#pragma unroll
+  for (uint32_t r = 0; r < kPartLoads; ++r) {
+    const uint32_t e = tid + r * kThreads;
     const uint32_t which = e >= total, k = e - which * total;
     const uint64_t at = (uint64_t)(row - which) * total + k;
-    s.pcomp[which][k] = d.part_comp[at];
-    s.pvbits[which][k] = d.part_vbits[at];
+    const bool in = e < rows_here * total;
+    pc[r] = in ? d.part_comp[at] : 0ull;
+    pv[r] = in ? d.part_vbits[at] : 0u;
+  }
+#pragma unroll
+  for (uint32_t r = 0; r < kPartLoads; ++r) {
+    const uint32_t e = tid + r * kThreads;
+    const uint32_t which = e >= total, k = e - which * total;
+    if (e < rows_here * total) {
+      s.pcomp[which][k] = pc[r];
+      s.pvbits[which][k] = pv[r];
+    }
   }
   const uint16_t *h = d.hidden + ((uint64_t)lane_index * kDraftQueryRows + p + 1) * kRank;
   s.hid[tid] = bf16f(h[tid]);
@@ -319,19 +338,31 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   // The walk (sampling.metal:1316-1359): every table, unary score and
   // candidate of the lane into LDS, then wave 0 with lane c holding
   // candidate c; the sums and the running maximum go in candidate order.
+  // Every load issued before any lands in LDS. Entry tid of position pp
+  // (256 per position); position 0 has only the anchor's row.
   const uint64_t r0 = (uint64_t)lane_index * kDraftPositions * kDraftK;
-  for (uint32_t e = tid; e < kDraftPositions * kDraftK * kDraftK; e += kThreads) {
-    const uint32_t pp = e / (kDraftK * kDraftK), q = e % (kDraftK * kDraftK);
-    // Position 0 has only the anchor's row.
-    tbl[pp][q] = pp || q < kDraftK ? ld_dev(table + e) : 0.0f;
-  }
-  if (tid < kDraftPositions * kDraftK) {
-    un[tid / kDraftK][tid % kDraftK] = ld_dev(d.unary + r0 + tid);
-    cands[tid / kDraftK][tid % kDraftK] = ld_dev(d.candidates + r0 + tid);
+  static_assert(kDraftK * kDraftK == kThreads, "one table entry per thread and position");
+  float tv[kDraftPositions];
+#pragma unroll
+  for (uint32_t pp = 0; pp < kDraftPositions; ++pp)
+    tv[pp] = pp || tid < kDraftK ? ld_dev(table + pp * kThreads + tid) : 0.0f;
+  const bool mine = tid < kDraftPositions * kDraftK;
+  const float uv = mine ? ld_dev(d.unary + r0 + tid) : 0.0f;
+  const uint32_t cv = mine ? ld_dev(d.candidates + r0 + tid) : 0u;
+#pragma unroll
+  for (uint32_t pp = 0; pp < kDraftPositions; ++pp) tbl[pp][tid] = tv[pp];
+  if (mine) {
+    un[tid / kDraftK][tid % kDraftK] = uv;
+    cands[tid / kDraftK][tid % kDraftK] = cv;
   }
   __syncthreads();
   if (tid >= 64) return;
-  const uint32_t c = tid & 15;
+  // Lane c holds candidate c (lanes 16..63 repeat them). The maximum is a
+  // wave reduction (fmax is order-free, so it equals the running maximum);
+  // the weights and quotients are computed per lane; the sum and the
+  // cumulative test, whose rounding depends on the order, run in candidate
+  // order on lane 0 over LDS copies.
+  const uint32_t c = tid & 15, lane = tid;
   const bool sampled = lp.sampled != 0;
   const float *u = d.uniforms + (uint64_t)lane_index * kSamplingUniforms + kUniformProposals;
   uint32_t pred_index = 0;
@@ -339,32 +370,42 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
     const float score = un[pp][c] + tbl[pp][pred_index * kDraftK + c];
     uint32_t selected = 0;
     if (sampled) {
-      float maximum = readlane_f32(score, 0);
-      for (int k = 1; k < (int)kDraftK; ++k) maximum = __builtin_fmaxf(maximum, readlane_f32(score, k));
+      const float maximum = wave_max_f32(score);
       const float prob = exp_weight((score - maximum) / lp.temperature);
+      if (lane < kDraftK) s.walk[c] = prob;
+      wave_lds_sync();
       float sum = 0.0f;
-      for (int k = 0; k < (int)kDraftK; ++k) sum = sum + readlane_f32(prob, k);
+      if (lane == 0)
+        for (uint32_t k = 0; k < kDraftK; ++k) sum = sum + s.walk[k];
+      sum = readlane_f32(sum, 0);
       const float q = prob / sum;
-      if (tid < kDraftK) d.q_probs[(r0 + pp * kDraftK) + c] = q;
-      const float uu = u[pp];
-      float cumulative = 0.0f;
-      selected = kDraftK - 1;
-      for (int k = 0; k < (int)kDraftK; ++k) {
-        cumulative = cumulative + readlane_f32(q, k);
-        if (selected == kDraftK - 1 && cumulative > uu) selected = (uint32_t)k;
+      if (lane < kDraftK) {
+        d.q_probs[(r0 + pp * kDraftK) + c] = q;
+        s.walk[kDraftK + c] = q;
       }
-    } else {
-      float best = readlane_f32(score, 0);
-      for (int k = 1; k < (int)kDraftK; ++k) {
-        const float v = readlane_f32(score, k);
-        if (v > best) {
-          best = v;
-          selected = (uint32_t)k;
+      wave_lds_sync();
+      const float uu = u[pp];
+      uint32_t sel = kDraftK - 1;
+      if (lane == 0) {
+        float cumulative = 0.0f;
+        for (uint32_t k = 0; k < kDraftK; ++k) {
+          cumulative = cumulative + s.walk[kDraftK + k];
+          if (sel == kDraftK - 1 && cumulative > uu) sel = k;
         }
+      }
+      selected = readlane_u32(sel, 0);
+    } else {
+      // The first strict maximum in candidate order: candidate 0 when its
+      // score is NaN (nothing compares above it), else the first candidate
+      // holding the largest non-NaN score.
+      const float s0 = readlane_f32(score, 0);
+      if (s0 == s0) {
+        const float best = wave_max_f32(score);
+        selected = (uint32_t)__builtin_ctzll(ballot(lane < kDraftK && score == best));
       }
     }
     pred_index = selected;
-    if (tid == 0)
+    if (lane == 0)
       d.tokens[(uint64_t)lane_index * kDraftPositions + pp] = cands[pp][selected];
   }
 }
