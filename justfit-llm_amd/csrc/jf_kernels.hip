@@ -1475,6 +1475,7 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
     if (tid < S) {
       s.hoff[tid + 1] = incl;
       s.hcnt[tid] = hc;
+      s.hmax[tid] = hm;
     }
     if (tid == 0) {
       s.u64a = omask;
@@ -1518,6 +1519,16 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
       if (tid < S) s.hoff[tid + 1] = incl;
     }
     for (uint32_t b = tid; b < 1024; b += kThreads) s.merge.bins[b] = 0;
+    __syncthreads();
+  }
+  // A chunk whose maximum is below the threshold holds no item at or above
+  // it: the offsets skip its list (every use below wants only such items).
+  if (thr > kLowestKey) {
+    if (tid < 64) {
+      const bool use = tid < S && logit_key(s.hmax[tid]) >= thr;
+      const uint32_t incl = wave_incl_scan_u32(use ? s.hcnt[tid] : 0u);
+      if (tid < S) s.hoff[tid + 1] = incl;
+    }
     __syncthreads();
   }
   const uint32_t n_all = s.hoff[S];
