@@ -37,9 +37,11 @@ __device__ __forceinline__ float key_logit(uint32_t key) {
 // r = x - n ln2 with the two-constant Cody-Waite split of ln2,
 // e^r = 1 + r + r^2 P(r) with Cephes' degree-5 P, times 2^n. Zero below
 // -86, so every nonzero result is a normal float.
-__device__ __forceinline__ float exp_weight(float x) {
-  if (!(x >= -86.0f)) return 0.0f;
-  if (x > 88.0f) return __builtin_inff();
+// Branch-free: the polynomial runs on the argument clamped to [-87, 88]
+// (equal to it inside the range), and the two range ends are selected
+// afterwards, so a wave runs no exec-mask branches per token.
+__device__ __forceinline__ float exp_weight(float x_in) {
+  const float x = __builtin_fminf(__builtin_fmaxf(x_in, -87.0f), 88.0f);
   const float n = __builtin_rintf(x * 1.44269504088896341f);
   float r = __builtin_fmaf(n, -0.693359375f, x);
   r = __builtin_fmaf(n, 2.12194440e-4f, r);
@@ -52,7 +54,9 @@ __device__ __forceinline__ float exp_weight(float x) {
   const float r2 = r * r;
   const float y = __builtin_fmaf(p, r2, r) + 1.0f;
   const int ni = (int)n;
-  return y * u2f((uint32_t)(ni + 127) << 23);
+  const float e = y * u2f((uint32_t)(ni + 127) << 23);
+  const float hi = x_in > 88.0f ? __builtin_inff() : e;
+  return x_in >= -86.0f ? hi : 0.0f;  // NaN and below -86: zero
 }
 
 // A token's softmax weight relative to the row maximum (sampling.metal:38-40,

@@ -102,6 +102,7 @@ struct SampleLaunch {
   uint32_t stop1;
   uint32_t stage;
   uint32_t aligned;       // rows start on 16-byte boundaries: vector loads
+  uint32_t all_sampled;   // every row of the launch is sampled
   const uint2 *pen_entries;
   const uint32_t *pen_offsets;
   uint32_t pen_max_entries;
@@ -150,6 +151,9 @@ struct FastLaunch {
   uint32_t row_base;          // sampler row of blockIdx.y == 0
   uint32_t fuse_greedy;       // every row greedy: the last block of a row
                               // finishes it (no merge launch)
+  uint32_t mass_only;         // sampled rows keep every admitted token:
+                              // write chunk maxima only (mass_draw_kernel
+                              // follows)
   uint32_t row_info[kKernargRows];  // RowFlags | penalty row << 8
 };
 
@@ -304,6 +308,7 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
                        void *start_event = nullptr, void *stop_event = nullptr);
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream);
+int launch_mass_draw(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream);
 int launch_accept_tree(const AcceptTreeLaunch &a, void *stream);

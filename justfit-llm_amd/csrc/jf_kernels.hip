@@ -107,6 +107,22 @@ struct __align__(16) SelectLds {
   uint32_t wu2[kWaves];
 };
 
+// The mass-and-draw kernel's LDS: the chunk's penalty lookup, the
+// reductions and the walk's offsets (no merge buffers, so more blocks stay
+// resident during the mass pass).
+struct __align__(16) DrawLds {
+  PrepLds prep;
+  uint64_t wj[kWaves][8];
+  uint64_t wl[kWaves];
+  uint32_t cids[16];
+  float cprobs[16];
+  uint32_t last;
+  uint32_t hit;
+  uint32_t sel_bin;
+  uint64_t sel_excl;
+  uint64_t u64a;
+};
+
 // ---- block helpers (every thread of the block calls them) ---------------
 
 template <class L>
@@ -614,8 +630,9 @@ __device__ __forceinline__ uint32_t row_draft(const SampleLaunch &a,
 // The draft's probability of `token` for a drafted row: its dense q, or
 // the first sparse candidate that lists it (sampling.metal:703-708); the
 // merge stages the row's 16 candidates in s.cids/s.cprobs.
+template <class L>
 __device__ __forceinline__ float draft_q(const SampleLaunch &a, uint32_t row,
-                                         uint32_t token, const Lds &s) {
+                                         uint32_t token, const L &s) {
   if (a.dense_q) return a.dense_q[(uint64_t)row * a.q_stride + token];
   for (int j = 0; j < 16; ++j)
     if (s.cids[j] == token) return s.cprobs[j];
@@ -1703,8 +1720,9 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
 // Every thread's device-coherent stores complete, then one arrival; true in
 // every thread of the block that arrives last, which returns the counter to
 // zero for the next launch.
+template <class L>
 __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t S,
-                                            Lds &s) {
+                                            L &s) {
   wait_memory();
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -2312,6 +2330,15 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   const uint32_t badm = s.wu[0] | s.wu[1] | s.wu[2] | s.wu[3];
   const uint32_t tk =
       bound ? min(min(s.wu2[0], s.wu2[1]), min(s.wu2[2], s.wu2[3])) : 0u;
+  if (f.mass_only) {
+    // The launch's sampled rows keep every admitted token: the chunk's
+    // maximum and admission are all the mass-and-draw launch reads.
+    if (tid == 0) {
+      hdr->maximum = bmax;
+      hdr->admitted = badm;
+    }
+    return;
+  }
   uint32_t thr = tk;
   if (flags & kRowMinP)
     thr = max(thr, logit_key(__builtin_fminf(bmax + rp.minp_offset, bmax)));
@@ -2725,12 +2752,12 @@ __device__ __forceinline__ void load_dense_q(const SampleLaunch &a, uint32_t row
 // admitted tokens at or above `thr_key` and at or before the kept boundary
 // (bkey, bid). Every thread of the block calls it; every thread gets the
 // token.
-template <int DT>
+template <int DT, class L>
 __device__ __forceinline__ uint32_t walk_chunk(const SampleLaunch &a, const RowParams &rp,
                                                uint32_t row, uint32_t c, float M,
                                                uint32_t thr_key, uint32_t bkey, uint32_t bid,
                                                bool residual, uint64_t mass3,
-                                               uint64_t within, Lds &s) {
+                                               uint64_t within, L &s) {
   constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
                 LOADS = Geo<DT>::LOADS;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
@@ -3244,6 +3271,154 @@ __global__ __launch_bounds__(kThreads) void walk_kernel(SampleLaunch a) {
   }
 }
 
+// Rows that keep every admitted token (no min-p, top-k or top-p cut) and
+// carry no draft: the draw's two passes in one launch, after a select pass
+// that wrote only the chunk maxima. One block per (row, chunk) sums its
+// chunk's fixed-point weights against the row maximum; the row's last block
+// to arrive picks the chunk whose running mass passes u * mass and walks it
+// in id order (sampling.metal:694-829 over the whole row; the same members,
+// weights and walk as the Mass3 and Walk stages, so the token is the same).
+// Greedy rows take the argmax of the chunk bests in their chunk-0 block.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
+  constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS;
+  __shared__ DrawLds s;
+  const uint32_t S = a.chunks;
+  const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  // Every row of the launch sampled (no greedy row whose chunk need not be
+  // read): the chunk's requests go out before the row's policy arrives.
+  const bool all_sampled = a.all_sampled != 0;
+  const RowParams rp = a.params[row];
+  // Requested up front: the chunk summaries (every wave, one lane per
+  // chunk; the select launch ended before this one began) and the row's
+  // uniform, which only the last block uses.
+  const BlockHeader *hb = a.headers + (uint64_t)row * S;
+  float hm = -3.402823466e38f, hv = -__builtin_inff();
+  uint32_t ha = 0, hi = kNoToken;
+  if (lane < S) {
+    hm = hb[lane].maximum;
+    ha = hb[lane].admitted;
+  }
+  if (!all_sampled && !(rp.flags & kRowSampled)) {
+    // Greedy (sampling.metal:1478-1512): the largest chunk best, the lowest
+    // id among equals.
+    if (chunk == 0 && tid < 64) {
+      if (lane < S) {
+        hv = hb[lane].best_value;
+        hi = hb[lane].best_id;
+      }
+      wave_argmax(hv, hi);
+      if (tid == 0) write_result(a, row, hi, 0.0f, 0);
+    }
+    return;
+  }
+  const float u = row_uniform(a, row);
+  float xs[TPL];
+  load_chunk<DT>(a, rp, row, chunk, s, xs);
+  const float M = wave_max_f32(hm);
+  const uint32_t admitted = wave_sum_u32(ha);
+  if (admitted == 0 || M == __builtin_inff()) {
+    // Nothing to draw from: the sentinel, as the merge writes it.
+    if (chunk == 0 && tid == 0) write_result(a, row, kNoToken, 0.0f, 0);
+    return;
+  }
+  // Each wave's sum per load (its 64 x VEC consecutive tokens), in id
+  // order j * kWaves + w at v[1..], and the chunk's mass at v[0]. A NaN
+  // (not admitted) token weighs zero.
+  const float inv_t = rp.inv_t;
+  const uint32_t w = tid >> 6;
+  StagePartial *parts = a.partials + (uint64_t)row * S;
+  uint64_t total = 0;
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    uint64_t sj = 0;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) sj += quantize(weight_of(xs[j * VEC + e], M, inv_t));
+    sj = wave_sum_u64(sj);
+    if (lane == 0) st_dev(&parts[chunk].v[1 + j * kWaves + w], sj);
+    total += sj;
+  }
+  if (lane == 0) s.wl[w] = total;
+  __syncthreads();
+  if (tid == 0) st_dev(&parts[chunk].v[0], s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3]);
+  if (!arrive_last(a.counters + row, S, s)) return;
+
+  // The last block: the chunk masses in id order, the target u * mass, the
+  // chunk whose running mass passes it, the wave slice inside that chunk,
+  // then the token inside that slice.
+  if (tid < 64) {
+    const bool in = tid < S;
+    const uint64_t v = in ? ld_dev(&parts[tid].v[0]) : 0ull;
+    const uint64_t incl = wave_incl_scan_u64(v);
+    const uint64_t mass = readlane_u64(incl, 63);
+    uint64_t within = 0;
+    uint32_t c = 0, g = 0;
+    if (mass != 0) {
+      uint64_t target = floor_mul(mass, u);
+      if (target >= mass) target = mass - 1;
+      // incl at the last lane is mass > target: some lane passes it.
+      c = (uint32_t)__builtin_ctzll(ballot(in && incl > target));
+      within = target - readlane_u64(incl - v, c);
+      constexpr uint32_t G = LOADS * kWaves;
+      const bool gin = tid < G;
+      const uint64_t vg = gin ? ld_dev(&parts[c].v[1 + tid]) : 0ull;
+      const uint64_t ginc = wave_incl_scan_u64(vg);
+      // The slices of chunk c sum to its mass, which passes `within`.
+      g = (uint32_t)__builtin_ctzll(ballot(gin && ginc > within));
+      within -= readlane_u64(ginc - vg, g);
+    }
+    if (tid == 0) {
+      s.u64a = mass;
+      s.sel_excl = within;
+      s.sel_bin = c | (g << 8);
+    }
+  }
+  __syncthreads();
+  const uint64_t mass = s.u64a, within = s.sel_excl;
+  const uint32_t c = s.sel_bin & 0xffu, g = s.sel_bin >> 8;
+  __syncthreads();
+  if (mass == 0) {
+    if (tid == 0) write_result(a, row, kNoToken, 0.0f, 0);
+    return;
+  }
+  // Chunk c again (block-wide: a penalized row stages its table entries),
+  // then only slice g's wave weighs its VEC tokens per lane.
+  load_chunk<DT>(a, rp, row, c, s, xs);
+  const uint32_t jg = g / kWaves;
+  if (w == g % kWaves) {
+    float xv[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) xv[e] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        if ((uint32_t)j == jg) xv[e] = xs[j * VEC + e];
+    uint64_t q[VEC], lsum = 0;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      q[e] = quantize(weight_of(xv[e], M, inv_t));
+      lsum += q[e];
+    }
+    const uint64_t incl = wave_incl_scan_u64(lsum);
+    // The slice sums to more than `within`: some lane passes it.
+    const uint32_t hl = (uint32_t)__builtin_ctzll(ballot(incl > within));
+    if (lane == hl) {
+      // The lane's first token whose running sum passes `within`.
+      uint64_t run = incl - lsum;
+      uint32_t e_hit = VEC;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        if (e_hit == VEC && q[e] && run + q[e] > within) e_hit = (uint32_t)e;
+        run += q[e];
+      }
+      const uint32_t token = c * Geo<DT>::CHUNK + jg * Geo<DT>::SLAB + tid * VEC + e_hit;
+      write_result(a, row, token, 0.0f, 0);
+    }
+  }
+}
+
 // ---- acceptance --------------------------------------------------------
 
 // finish_acceptance (sampling.metal:1381-1392).
@@ -3388,6 +3563,15 @@ int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream) {
     hipLaunchKernelGGL(merge_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
   else
     hipLaunchKernelGGL(merge_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_mass_draw(const SampleLaunch &a, uint32_t dtype, void *stream) {
+  const dim3 grid(a.rows * a.chunks), block(kThreads);
+  if (dtype == 0)
+    hipLaunchKernelGGL(mass_draw_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(mass_draw_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

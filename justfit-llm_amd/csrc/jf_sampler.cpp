@@ -613,10 +613,18 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   int e = hipSuccess;
   // A launch of greedy rows only is finished inside the fast selection.
   const bool fused = fast && !any_sampled;
+  // Sampled rows that keep every admitted token (no min-p, top-k or top-p
+  // cut) and carry no draft need only the row maximum and the chunk masses:
+  // the selection writes chunk maxima, then one mass-and-draw launch finishes
+  // every row (no merge, no stages).
+  bool unfiltered = fast && any_sampled && !kept && L.drafted_rows == 0;
+  for (uint32_t r = 0; unfiltered && r < rows; ++r)
+    if (params[r].flags & (jf::kRowMinP | jf::kRowTopK | jf::kRowTopP)) unfiltered = false;
   if (fast) {
     jf::FastLaunch F{};
     F.a = L;
     F.fuse_greedy = fused ? 1u : 0u;
+    F.mass_only = unfiltered ? 1u : 0u;
     if (a->penalties) {
       F.pen_slots = a->penalties->slots;
       F.slot_count = a->penalties->slot_count;
@@ -659,6 +667,14 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
     const jf::RowParams &rp = params[r];
     if ((rp.flags & jf::kRowSampled) && (!(rp.flags & jf::kRowTopK) || rp.top_k > 64u))
       small = false;
+  }
+  if (unfiltered) {
+    L.all_sampled = 1u;
+    for (uint32_t r = 0; r < rows; ++r)
+      if (!(params[r].flags & jf::kRowSampled)) L.all_sampled = 0u;
+    e = jf::launch_mass_draw(L, a->dtype, stream);
+    if (e != hipSuccess) return hip_fail((hipError_t)e, "mass-and-draw launch");
+    return JF_OK;
   }
   if (!fused) {
     e = small ? jf::launch_merge_small(L, a->dtype, stream)

@@ -295,6 +295,69 @@ def test_multipass_stages(kind):
     assert_same(g, r)
 
 
+@pytest.mark.parametrize("bf16,greedy", [(False, True), (True, True), (False, False)])
+def test_unfiltered_mass_draw(bf16, greedy):
+    """Launches whose sampled rows keep every admitted token and carry no
+    draft, without kept outputs: chunk maxima, then the mass-and-draw launch
+    (greedy rows ride along). Penalties, masks, stop exclusion, a partial
+    last chunk, the sentinel rows and uniforms at both ends."""
+    rng = np.random.default_rng(61 + bf16)
+    V = 8 * 8192 + 4465
+    rows = 12
+    x = rand_logits(rng, rows, V, scale=1.5)
+    allowed = rng.random((rows, V)) < 0.3
+    x[1] = np.nan                             # nothing admitted: sentinel
+    x[2] = -np.inf                            # no mass: sentinel
+    x[3, 123] = np.inf                        # +inf maximum: sentinel
+    x[4, ::3] = np.nan                        # NaN tokens are never drawn
+    allowed[5] = False
+    allowed[5, [7, 8, 40000]] = True          # the stop tokens and one other
+    x[6] = -80.0
+    x[6, V - 1] = 3.0                         # the partial chunk's last token
+    x[6, 5] = 2.9
+    x[10] = np.round(x[10], 0)                # ties everywhere
+    masks = WL.mask_words(allowed)
+    hist = [rng.integers(0, V, 500).astype(np.uint32) for _ in range(rows)]
+    hist[11] = np.concatenate([hist[11], np.full(900, 4321, np.uint32)])
+    pols = [J.policy(temperature=1.0, constrained=True), J.policy(temperature=1.0),
+            J.policy(temperature=0.8), J.policy(temperature=1.0),
+            J.policy(temperature=0.7, presence=0.4, frequency=0.2),
+            J.policy(temperature=1.0, constrained=True, exclude_stop=True),
+            J.policy(temperature=0.25), J.policy(constrained=True, repetition=1.2),
+            J.policy(), J.policy(temperature=2.0, repetition=1.3),
+            J.policy(temperature=1.0), J.policy(temperature=1.5, presence=1.0, frequency=0.5)]
+    if not greedy:  # every row sampled: the chunk loads go out first
+        pols[7] = J.policy(temperature=1.0, constrained=True, repetition=1.2)
+        pols[8] = J.policy(temperature=3.0)
+    u = rng.random(rows).astype(np.float32)
+    u[0] = 0.0
+    u[9] = np.float32(1.0) - np.float32(2.0 ** -24)
+    kw = dict(masks=masks, histories=hist, generated=[300] * rows,
+              mark_prompt=[True] * rows, uniforms=u, stop=(7, 8))
+    if bf16:
+        kw["logits_bf16"] = WL.to_bf16_bits(x)
+    else:
+        kw["logits"] = x
+    g, r = both(V, pols, **kw)
+    assert_same(g, r)
+    assert all(g["tokens"][k] == NO for k in (1, 2, 3))
+    assert g["tokens"][5] == 40000
+    assert g["tokens"][8] != NO and g["tokens"][0] != NO
+
+
+def test_c3_sampled_without_kept_outputs():
+    """C3 sampled as the engine calls it (no kept outputs): the two-pass
+    mass-and-draw path at full size."""
+    c = WL.config3()
+    B = c["logits_bf16"].shape[0]
+    p = J.policy(temperature=1.0, constrained=True)
+    g, r = both(c["V"], [p] * B, logits_bf16=c["logits_bf16"], masks=c["masks"],
+                uniforms=c["uniforms"])
+    assert_same(g, r)
+    for row in range(B):
+        assert c["allowed"][row, g["tokens"][row]]
+
+
 def test_dense_residual_multipass():
     rng = np.random.default_rng(15)
     V = 40000
