@@ -69,6 +69,35 @@ __device__ __forceinline__ uint64_t quantize(float w) {
   return (uint64_t)(w * 0x1p44f);
 }
 
+// quantize(weight_of(value, maximum, inv_t)) for value <= maximum or NaN
+// (every member of a row: the maximum is the row's largest admitted value),
+// without the float scaling and the float-to-u64 conversion. exp_weight's
+// result is y * 2^n exactly (y in [0.70, 1.42], n in [-124, 0], a normal
+// float), so floor(y * 2^(n + 44)) is the integer Y = y * 2^30 (exact: y
+// has 24 mantissa bits and exponent -1 or 0) shifted by n + 14, here
+// (Y << 32) >> (18 - n); a shift of 63 gives zero, below -86 or for NaN.
+// Checked equal to quantize(exp_weight(x)) for every float x in [-90, 0]
+// and NaN.
+__device__ __forceinline__ uint64_t quantized_weight(float value, float maximum,
+                                                     float inv_t) {
+  const float x_in = (value - maximum) * inv_t;
+  const float x = __builtin_fminf(__builtin_fmaxf(x_in, -87.0f), 88.0f);
+  const float n = __builtin_rintf(x * 1.44269504088896341f);
+  float r = __builtin_fmaf(n, -0.693359375f, x);
+  r = __builtin_fmaf(n, 2.12194440e-4f, r);
+  float p = 1.9875691500e-4f;
+  p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+  p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+  p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+  p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+  p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+  const float r2 = r * r;
+  const float y = __builtin_fmaf(p, r2, r) + 1.0f;
+  const uint32_t Y = (uint32_t)(y * 0x1p30f);
+  const int k = x_in >= -86.0f ? min(18 - (int)n, 63) : 63;
+  return ((uint64_t)Y << 32) >> k;
+}
+
 // floor(a * f) exactly for f in [0, 1]; NaN and f <= 0 give 0, f >= 1 gives a.
 __device__ __forceinline__ uint64_t floor_mul(uint64_t a, float f) {
   if (!(f > 0.0f)) return 0;

@@ -309,6 +309,7 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_mass_draw(const SampleLaunch &a, uint32_t dtype, void *stream);
+int launch_residual_draw(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream);
 int launch_accept_tree(const AcceptTreeLaunch &a, void *stream);

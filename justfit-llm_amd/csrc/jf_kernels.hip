@@ -638,8 +638,9 @@ __device__ __forceinline__ float draft_q(const SampleLaunch &a, uint32_t row,
     if (s.cids[j] == token) return s.cprobs[j];
   return 0.0f;
 }
+template <class L>
 __device__ __forceinline__ void stage_candidates(const SampleLaunch &a,
-                                                 uint32_t row, Lds &s) {
+                                                 uint32_t row, L &s) {
   if (threadIdx.x < 16) {
     const bool sparse = !a.dense_q && row_draft(a, row) != kNoToken;
     s.cids[threadIdx.x] = sparse ? a.cand_ids[(uint64_t)row * 16 + threadIdx.x] : kNoToken;
@@ -3271,28 +3272,80 @@ __global__ __launch_bounds__(kThreads) void walk_kernel(SampleLaunch a) {
   }
 }
 
-// Rows that keep every admitted token (no min-p, top-k or top-p cut) and
-// carry no draft: the draw's two passes in one launch, after a select pass
-// that wrote only the chunk maxima. One block per (row, chunk) sums its
-// chunk's fixed-point weights against the row maximum; the row's last block
-// to arrive picks the chunk whose running mass passes u * mass and walks it
-// in id order (sampling.metal:694-829 over the whole row; the same members,
-// weights and walk as the Mass3 and Walk stages, so the token is the same).
+// Inside one wave's slice of a chunk (64 lanes x VEC consecutive tokens,
+// lane-major): q[e] are the lane's weights in id order and the slice's
+// weights sum past `within`. Returns the lane whose running sum first passes
+// it, and in that lane the index of the first token that does (the walk of
+// sampling.metal:790-829 restricted to the slice).
+template <int VEC>
+__device__ __forceinline__ uint32_t slice_hit(const uint64_t (&q)[VEC], uint64_t within,
+                                              uint32_t &e_hit) {
+  uint64_t lsum = 0;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) lsum += q[e];
+  const uint64_t incl = wave_incl_scan_u64(lsum);
+  const uint32_t hl = (uint32_t)__builtin_ctzll(ballot(incl > within));
+  uint64_t run = incl - lsum;
+  e_hit = VEC;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    if (e_hit == (uint32_t)VEC && q[e] && run + q[e] > within) e_hit = (uint32_t)e;
+    run += q[e];
+  }
+  return hl;
+}
+
+// The slice g of chunk c that holds `within` (slice sums at v[off + g]),
+// and `within` made relative to it; wave-wide, every lane gets both.
+__device__ __forceinline__ uint32_t pick_slice(const StagePartial *parts, uint32_t c,
+                                               uint32_t off, uint32_t G, uint64_t &within) {
+  const uint32_t l = lane_id();
+  const bool gin = l < G;
+  const uint64_t vg = gin ? ld_dev(&parts[c].v[off + l]) : 0ull;
+  const uint64_t ginc = wave_incl_scan_u64(vg);
+  // The slices of chunk c sum to its mass, which passes `within`.
+  const uint32_t g = (uint32_t)__builtin_ctzll(ballot(gin && ginc > within));
+  within -= readlane_u64(ginc - vg, g);
+  return g;
+}
+
+// Rows that keep every admitted token (no min-p, top-k or top-p cut): the
+// draw's passes after a select pass that wrote only the chunk maxima.
+// Partial slots per (row, chunk): v[0] the chunk's mass and v[1 + g] its
+// slices' masses (slice g = load g / kWaves of wave g % kWaves, 64 x VEC
+// consecutive tokens, so g runs in id order); v[kDraftSlot] the draft
+// token's weight; v[kResidualSlot] and v[kResidualSlot + 1 + g] the same
+// sums over residual weights.
+constexpr uint32_t kDraftSlot = 40;
+constexpr uint32_t kResidualSlot = 63;
+
+// One block per (row, chunk) sums its chunk's fixed-point weights against
+// the row maximum; the row's last block to arrive picks the chunk and slice
+// whose running mass passes u * mass and walks the slice in id order
+// (sampling.metal:694-829 over the whole row; the same members, weights and
+// walk as the Mass3 and Walk stages, so the token is the same). A drafted
+// row instead leaves its mass and draft weight in its state for
+// residual_draw_kernel (the Mass3 stage's hand-over to the Draw stage).
 // Greedy rows take the argmax of the chunk bests in their chunk-0 block.
 template <int DT>
 __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
-  constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS;
+  constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
+                SLAB = Geo<DT>::SLAB;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves;
   __shared__ DrawLds s;
   const uint32_t S = a.chunks;
   const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
-  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // The launch carries drafted rows: every row's state says whether the
+  // residual launch has work for it.
+  const bool drafts = a.draft_tokens && a.drafted_rows;
   // Every row of the launch sampled (no greedy row whose chunk need not be
   // read): the chunk's requests go out before the row's policy arrives.
   const bool all_sampled = a.all_sampled != 0;
   const RowParams rp = a.params[row];
   // Requested up front: the chunk summaries (every wave, one lane per
-  // chunk; the select launch ended before this one began) and the row's
-  // uniform, which only the last block uses.
+  // chunk; the select launch ended before this one began), the draft token
+  // and the row's uniform, which only the last block uses.
   const BlockHeader *hb = a.headers + (uint64_t)row * S;
   float hm = -3.402823466e38f, hv = -__builtin_inff();
   uint32_t ha = 0, hi = kNoToken;
@@ -3300,6 +3353,7 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
     hm = hb[lane].maximum;
     ha = hb[lane].admitted;
   }
+  const uint32_t draft = row_draft(a, row);
   if (!all_sampled && !(rp.flags & kRowSampled)) {
     // Greedy (sampling.metal:1478-1512): the largest chunk best, the lowest
     // id among equals.
@@ -3309,7 +3363,10 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
         hi = hb[lane].best_id;
       }
       wave_argmax(hv, hi);
-      if (tid == 0) write_result(a, row, hi, 0.0f, 0);
+      if (tid == 0) {
+        write_result(a, row, hi, 0.0f, 0);
+        if (drafts) a.states[row].stage = kStageDone;
+      }
     }
     return;
   }
@@ -3320,24 +3377,37 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
   const uint32_t admitted = wave_sum_u32(ha);
   if (admitted == 0 || M == __builtin_inff()) {
     // Nothing to draw from: the sentinel, as the merge writes it.
-    if (chunk == 0 && tid == 0) write_result(a, row, kNoToken, 0.0f, 0);
+    if (chunk == 0 && tid == 0) {
+      write_result(a, row, kNoToken, 0.0f, 0);
+      if (drafts) a.states[row].stage = kStageDone;
+    }
     return;
   }
-  // Each wave's sum per load (its 64 x VEC consecutive tokens), in id
-  // order j * kWaves + w at v[1..], and the chunk's mass at v[0]. A NaN
-  // (not admitted) token weighs zero.
+  // Each wave's mass per load, then the chunk's. A NaN (not admitted) token
+  // weighs zero.
   const float inv_t = rp.inv_t;
-  const uint32_t w = tid >> 6;
   StagePartial *parts = a.partials + (uint64_t)row * S;
   uint64_t total = 0;
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
     uint64_t sj = 0;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) sj += quantize(weight_of(xs[j * VEC + e], M, inv_t));
+    for (int e = 0; e < VEC; ++e) sj += quantized_weight(xs[j * VEC + e], M, inv_t);
     sj = wave_sum_u64(sj);
     if (lane == 0) st_dev(&parts[chunk].v[1 + j * kWaves + w], sj);
     total += sj;
+  }
+  // The draft token's weight, from the thread that holds it (zero when the
+  // row does not admit it).
+  if (draft < a.vocabulary && draft / CHUNK == chunk) {
+    const uint32_t o = draft - chunk * CHUNK;
+    if (tid == (o % SLAB) / VEC) {
+      const uint32_t i = (o / SLAB) * VEC + o % VEC;
+      float xd = 0.0f;
+#pragma unroll
+      for (int k = 0; k < TPL; ++k) xd = (uint32_t)k == i ? xs[k] : xd;
+      st_dev(&parts[chunk].v[kDraftSlot], (uint64_t)f2u(weight_of(xd, M, inv_t)));
+    }
   }
   if (lane == 0) s.wl[w] = total;
   __syncthreads();
@@ -3345,8 +3415,7 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
   if (!arrive_last(a.counters + row, S, s)) return;
 
   // The last block: the chunk masses in id order, the target u * mass, the
-  // chunk whose running mass passes it, the wave slice inside that chunk,
-  // then the token inside that slice.
+  // chunk whose running mass passes it, the slice inside that chunk.
   if (tid < 64) {
     const bool in = tid < S;
     const uint64_t v = in ? ld_dev(&parts[tid].v[0]) : 0ull;
@@ -3354,67 +3423,155 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
     const uint64_t mass = readlane_u64(incl, 63);
     uint64_t within = 0;
     uint32_t c = 0, g = 0;
-    if (mass != 0) {
+    if (draft != kNoToken) {
+      // Drafted: the residual launch draws (the Mass3 stage's hand-over).
+      // Field by field: the fields residual_draw_kernel reads.
+      if (tid == 0) {
+        RowState *ns = a.states + row;
+        if (mass == 0) {
+          write_result(a, row, kNoToken, 0.0f, 0);
+          ns->stage = kStageDone;
+        } else {
+          ns->maximum = M;
+          ns->mass3 = mass;
+          ns->drafted = 1;
+          ns->draft_w = draft < a.vocabulary
+                            ? u2f((uint32_t)ld_dev(&parts[draft / CHUNK].v[kDraftSlot]))
+                            : 0.0f;
+          ns->stage = kStageDraw;
+        }
+      }
+    } else if (mass != 0) {
       uint64_t target = floor_mul(mass, u);
       if (target >= mass) target = mass - 1;
       // incl at the last lane is mass > target: some lane passes it.
       c = (uint32_t)__builtin_ctzll(ballot(in && incl > target));
       within = target - readlane_u64(incl - v, c);
-      constexpr uint32_t G = LOADS * kWaves;
-      const bool gin = tid < G;
-      const uint64_t vg = gin ? ld_dev(&parts[c].v[1 + tid]) : 0ull;
-      const uint64_t ginc = wave_incl_scan_u64(vg);
-      // The slices of chunk c sum to its mass, which passes `within`.
-      g = (uint32_t)__builtin_ctzll(ballot(gin && ginc > within));
-      within -= readlane_u64(ginc - vg, g);
+      g = pick_slice(parts, c, 1, G, within);
     }
     if (tid == 0) {
-      s.u64a = mass;
+      s.u64a = draft != kNoToken ? 0ull : mass;
       s.sel_excl = within;
       s.sel_bin = c | (g << 8);
+      if (draft == kNoToken) {
+        if (mass == 0) write_result(a, row, kNoToken, 0.0f, 0);
+        if (drafts) a.states[row].stage = kStageDone;
+      }
     }
   }
   __syncthreads();
   const uint64_t mass = s.u64a, within = s.sel_excl;
   const uint32_t c = s.sel_bin & 0xffu, g = s.sel_bin >> 8;
-  __syncthreads();
-  if (mass == 0) {
-    if (tid == 0) write_result(a, row, kNoToken, 0.0f, 0);
-    return;
-  }
+  if (mass == 0) return;
   // Chunk c again (block-wide: a penalized row stages its table entries),
   // then only slice g's wave weighs its VEC tokens per lane.
   load_chunk<DT>(a, rp, row, c, s, xs);
   const uint32_t jg = g / kWaves;
   if (w == g % kWaves) {
-    float xv[VEC];
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) xv[e] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e)
-        if ((uint32_t)j == jg) xv[e] = xs[j * VEC + e];
-    uint64_t q[VEC], lsum = 0;
+    uint64_t q[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      q[e] = quantize(weight_of(xv[e], M, inv_t));
-      lsum += q[e];
-    }
-    const uint64_t incl = wave_incl_scan_u64(lsum);
-    // The slice sums to more than `within`: some lane passes it.
-    const uint32_t hl = (uint32_t)__builtin_ctzll(ballot(incl > within));
-    if (lane == hl) {
-      // The lane's first token whose running sum passes `within`.
-      uint64_t run = incl - lsum;
-      uint32_t e_hit = VEC;
+      float x = 0.0f;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        if (e_hit == VEC && q[e] && run + q[e] > within) e_hit = (uint32_t)e;
-        run += q[e];
-      }
-      const uint32_t token = c * Geo<DT>::CHUNK + jg * Geo<DT>::SLAB + tid * VEC + e_hit;
-      write_result(a, row, token, 0.0f, 0);
+      for (int j = 0; j < LOADS; ++j) x = (uint32_t)j == jg ? xs[j * VEC + e] : x;
+      q[e] = quantized_weight(x, M, inv_t);
+    }
+    uint32_t e_hit;
+    if (lane == slice_hit<VEC>(q, within, e_hit))
+      write_result(a, row, c * CHUNK + jg * SLAB + tid * VEC + e_hit, 0.0f, 0);
+  }
+}
+
+// Drafted rows that keep every admitted token: the residual draw over the
+// row (sampling.metal:694-829 with candidate weights max(w - q * mass, 0),
+// the Draw and Walk stages' arithmetic). One block per (row, chunk) sums its
+// residual weights per slice; the row's last block draws from the residual
+// weights, or from the plain weights when the residual has no mass, and
+// writes p(draft) = w(draft) / mass (sampling.metal:828-829).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a) {
+  constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
+                SLAB = Geo<DT>::SLAB;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves;
+  __shared__ DrawLds s;
+  const uint32_t S = a.chunks;
+  const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const RowState st = a.states[row];
+  if (st.stage != kStageDraw) return;
+  const RowParams rp = a.params[row];
+  float qv[TPL];
+  if (a.dense_q) load_dense_q<DT>(a, row, chunk, qv);
+  float xs[TPL];
+  load_chunk<DT>(a, rp, row, chunk, s, xs);
+  stage_candidates(a, row, s);
+  const float u = row_uniform(a, row);
+  const float M = st.maximum, inv_t = rp.inv_t;
+  const uint64_t mass3 = st.mass3;
+  const uint32_t lane_base = chunk * CHUNK + tid * VEC;
+  StagePartial *parts = a.partials + (uint64_t)row * S;
+  uint64_t total = 0;
+#pragma unroll
+  for (int j = 0; j < LOADS; ++j) {
+    uint64_t sj = 0;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const int i = j * VEC + e;
+      const float q = a.dense_q ? qv[i] : draft_q(a, row, lane_base + j * SLAB + e, s);
+      sj += residual_of(quantized_weight(xs[i], M, inv_t), mass3, q);
+    }
+    sj = wave_sum_u64(sj);
+    if (lane == 0) st_dev(&parts[chunk].v[kResidualSlot + 1 + j * kWaves + w], sj);
+    total += sj;
+  }
+  if (lane == 0) s.wl[w] = total;
+  __syncthreads();
+  if (tid == 0)
+    st_dev(&parts[chunk].v[kResidualSlot], s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3]);
+  if (!arrive_last(a.counters + row, S, s)) return;
+
+  // The last block: residual weights when they have mass, else the plain
+  // weights (whose sums the mass launch left at v[0] and v[1 + g]).
+  if (tid < 64) {
+    const bool in = tid < S;
+    const uint64_t rv = in ? ld_dev(&parts[tid].v[kResidualSlot]) : 0ull;
+    const uint64_t pv = in ? ld_dev(&parts[tid].v[0]) : 0ull;
+    const bool residual = wave_sum_u64(rv) != 0;
+    const uint64_t v = residual ? rv : pv;
+    const uint64_t incl = wave_incl_scan_u64(v);
+    const uint64_t tot = readlane_u64(incl, 63);
+    uint64_t target = floor_mul(tot, u);
+    if (target >= tot) target = tot - 1;
+    const uint32_t c = (uint32_t)__builtin_ctzll(ballot(in && incl > target));
+    uint64_t within = target - readlane_u64(incl - v, c);
+    const uint32_t g = pick_slice(parts, c, residual ? kResidualSlot + 1 : 1u, G, within);
+    if (tid == 0) {
+      s.sel_excl = within;
+      s.sel_bin = c | (g << 8) | (residual ? 1u << 16 : 0u);
+      a.states[row].stage = kStageDone;
+    }
+  }
+  __syncthreads();
+  const uint64_t within = s.sel_excl;
+  const uint32_t c = s.sel_bin & 0xffu, g = (s.sel_bin >> 8) & 0xffu;
+  const bool residual = (s.sel_bin >> 16) != 0;
+  load_chunk<DT>(a, rp, row, c, s, xs);
+  const uint32_t jg = g / kWaves;
+  if (w == g % kWaves) {
+    const uint32_t tbase = c * CHUNK + jg * SLAB + tid * VEC;
+    uint64_t q[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float x = 0.0f;
+#pragma unroll
+      for (int j = 0; j < LOADS; ++j) x = (uint32_t)j == jg ? xs[j * VEC + e] : x;
+      const uint64_t wq = quantized_weight(x, M, inv_t);
+      q[e] = residual ? residual_of(wq, mass3, draft_q(a, row, tbase + e, s)) : wq;
+    }
+    uint32_t e_hit;
+    if (lane == slice_hit<VEC>(q, within, e_hit)) {
+      const double scale = (double)mass3 * 0x1p-44;
+      write_result(a, row, tbase + e_hit, (float)((double)st.draft_w / scale), 0);
     }
   }
 }
@@ -3572,6 +3729,15 @@ int launch_mass_draw(const SampleLaunch &a, uint32_t dtype, void *stream) {
     hipLaunchKernelGGL(mass_draw_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
   else
     hipLaunchKernelGGL(mass_draw_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int launch_residual_draw(const SampleLaunch &a, uint32_t dtype, void *stream) {
+  const dim3 grid(a.rows * a.chunks), block(kThreads);
+  if (dtype == 0)
+    hipLaunchKernelGGL(residual_draw_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(residual_draw_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

@@ -617,7 +617,7 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   // cut) and carry no draft need only the row maximum and the chunk masses:
   // the selection writes chunk maxima, then one mass-and-draw launch finishes
   // every row (no merge, no stages).
-  bool unfiltered = fast && any_sampled && !kept && L.drafted_rows == 0;
+  bool unfiltered = fast && any_sampled && !kept;
   for (uint32_t r = 0; unfiltered && r < rows; ++r)
     if (params[r].flags & (jf::kRowMinP | jf::kRowTopK | jf::kRowTopP)) unfiltered = false;
   if (fast) {
@@ -674,6 +674,10 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
       if (!(params[r].flags & jf::kRowSampled)) L.all_sampled = 0u;
     e = jf::launch_mass_draw(L, a->dtype, stream);
     if (e != hipSuccess) return hip_fail((hipError_t)e, "mass-and-draw launch");
+    if (L.drafted_rows) {
+      e = jf::launch_residual_draw(L, a->dtype, stream);
+      if (e != hipSuccess) return hip_fail((hipError_t)e, "residual draw launch");
+    }
     return JF_OK;
   }
   if (!fused) {

@@ -295,8 +295,10 @@ def test_multipass_stages(kind):
     assert_same(g, r)
 
 
-@pytest.mark.parametrize("bf16,greedy", [(False, True), (True, True), (False, False)])
-def test_unfiltered_mass_draw(bf16, greedy):
+@pytest.mark.parametrize("bf16,greedy,draft", [(False, True, None), (True, True, None),
+                                               (False, False, None), (False, True, "dense"),
+                                               (True, False, "dense"), (False, True, "sparse")])
+def test_unfiltered_mass_draw(bf16, greedy, draft):
     """Launches whose sampled rows keep every admitted token and carry no
     draft, without kept outputs: chunk maxima, then the mass-and-draw launch
     (greedy rows ride along). Penalties, masks, stop exclusion, a partial
@@ -334,6 +336,24 @@ def test_unfiltered_mass_draw(bf16, greedy):
     u[9] = np.float32(1.0) - np.float32(2.0 ** -24)
     kw = dict(masks=masks, histories=hist, generated=[300] * rows,
               mark_prompt=[True] * rows, uniforms=u, stop=(7, 8))
+    if draft is not None:
+        # Drafted rows draw the residual max(p - q, 0): drafts at the row's
+        # best token (mass left only if q is small there), at a token the
+        # mask refuses, and at random tokens; two rows carry no draft.
+        d = rng.integers(0, V, rows).astype(np.uint32)
+        d[0] = int(np.nanargmax(np.where(allowed[0], x[0], -np.inf)))
+        d[5] = 9                              # refused by row 5's mask
+        d[[4, 9]] = NO
+        kw.update(draft_tokens=d, drafted_rows=rows)
+        if draft == "dense":
+            q = rng.dirichlet(np.ones(V) * 0.2, rows).astype(np.float32)
+            q[2] = 0.0
+            q[10, d[10]] = 1.0                # residual without mass at its draft
+            kw["dense_q"] = q
+        else:
+            cand = rng.integers(0, V, (rows, 16)).astype(np.uint32)
+            cand[:, 0] = d
+            kw.update(cand_ids=cand, cand_probs=rng.dirichlet(np.ones(16), rows).astype(np.float32))
     if bf16:
         kw["logits_bf16"] = WL.to_bf16_bits(x)
     else:
@@ -341,7 +361,7 @@ def test_unfiltered_mass_draw(bf16, greedy):
     g, r = both(V, pols, **kw)
     assert_same(g, r)
     assert all(g["tokens"][k] == NO for k in (1, 2, 3))
-    assert g["tokens"][5] == 40000
+    assert g["tokens"][5] == 40000            # the one token row 5 admits
     assert g["tokens"][8] != NO and g["tokens"][0] != NO
 
 
