@@ -651,7 +651,7 @@ __device__ __forceinline__ void stage_candidates(const SampleLaunch &a,
 
 __device__ __forceinline__ uint64_t residual_of(uint64_t wq, uint64_t mass,
                                                 float q) {
-  const uint64_t qm = floor_mul(mass, q);
+  const uint64_t qm = floor_mul_63(mass, q);
   return wq > qm ? wq - qm : 0;
 }
 
