@@ -121,6 +121,8 @@ struct __align__(16) DrawLds {
   uint32_t sel_bin;
   uint64_t sel_excl;
   uint64_t u64a;
+  uint32_t slice;          // the last block's slice and its remainder
+  uint64_t slice_within;
 };
 
 // ---- block helpers (every thread of the block calls them) ---------------
@@ -3295,13 +3297,12 @@ __device__ __forceinline__ uint32_t slice_hit(const uint64_t (&q)[VEC], uint64_t
   return hl;
 }
 
-// The slice g of chunk c that holds `within` (slice sums at v[off + g]),
-// and `within` made relative to it; wave-wide, every lane gets both.
-__device__ __forceinline__ uint32_t pick_slice(const StagePartial *parts, uint32_t c,
-                                               uint32_t off, uint32_t G, uint64_t &within) {
+// The slice g that holds `within`, given lane l's slice sum vg (lanes at or
+// past G hold 0), and `within` made relative to it; wave-wide, every lane
+// gets both.
+__device__ __forceinline__ uint32_t pick_slice(uint64_t vg, uint32_t G, uint64_t &within) {
   const uint32_t l = lane_id();
   const bool gin = l < G;
-  const uint64_t vg = gin ? ld_dev(&parts[c].v[off + l]) : 0ull;
   const uint64_t ginc = wave_incl_scan_u64(vg);
   // The slices of chunk c sum to its mass, which passes `within`.
   const uint32_t g = (uint32_t)__builtin_ctzll(ballot(gin && ginc > within));
@@ -3422,7 +3423,7 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
     const uint64_t incl = wave_incl_scan_u64(v);
     const uint64_t mass = readlane_u64(incl, 63);
     uint64_t within = 0;
-    uint32_t c = 0, g = 0;
+    uint32_t c = 0;
     if (draft != kNoToken) {
       // Drafted: the residual launch draws (the Mass3 stage's hand-over).
       // Field by field: the fields residual_draw_kernel reads.
@@ -3447,12 +3448,11 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
       // incl at the last lane is mass > target: some lane passes it.
       c = (uint32_t)__builtin_ctzll(ballot(in && incl > target));
       within = target - readlane_u64(incl - v, c);
-      g = pick_slice(parts, c, 1, G, within);
     }
     if (tid == 0) {
       s.u64a = draft != kNoToken ? 0ull : mass;
       s.sel_excl = within;
-      s.sel_bin = c | (g << 8);
+      s.sel_bin = c;
       if (draft == kNoToken) {
         if (mass == 0) write_result(a, row, kNoToken, 0.0f, 0);
         if (drafts) a.states[row].stage = kStageDone;
@@ -3460,12 +3460,26 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
     }
   }
   __syncthreads();
-  const uint64_t mass = s.u64a, within = s.sel_excl;
-  const uint32_t c = s.sel_bin & 0xffu, g = s.sel_bin >> 8;
+  const uint64_t mass = s.u64a;
+  const uint32_t c = s.sel_bin;
   if (mass == 0) return;
   // Chunk c again (block-wide: a penalized row stages its table entries),
-  // then only slice g's wave weighs its VEC tokens per lane.
+  // requested together with its slice sums; then the slice, and only that
+  // slice's wave weighs its VEC tokens per lane.
+  uint64_t vg = 0;
+  if (w == 0 && lane < G) vg = ld_dev(&parts[c].v[1 + lane]);
   load_chunk<DT>(a, rp, row, c, s, xs);
+  if (w == 0) {
+    uint64_t wi = s.sel_excl;
+    const uint32_t gg = pick_slice(vg, G, wi);
+    if (lane == 0) {
+      s.slice = gg;
+      s.slice_within = wi;
+    }
+  }
+  __syncthreads();
+  const uint32_t g = s.slice;
+  const uint64_t within = s.slice_within;
   const uint32_t jg = g / kWaves;
   if (w == g % kWaves) {
     uint64_t q[VEC];
@@ -3543,19 +3557,33 @@ __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a)
     uint64_t target = floor_mul(tot, u);
     if (target >= tot) target = tot - 1;
     const uint32_t c = (uint32_t)__builtin_ctzll(ballot(in && incl > target));
-    uint64_t within = target - readlane_u64(incl - v, c);
-    const uint32_t g = pick_slice(parts, c, residual ? kResidualSlot + 1 : 1u, G, within);
+    // Wave-wide: lane c's running sum is read from every lane's registers.
+    const uint64_t before = readlane_u64(incl - v, c);
     if (tid == 0) {
-      s.sel_excl = within;
-      s.sel_bin = c | (g << 8) | (residual ? 1u << 16 : 0u);
+      s.sel_excl = target - before;
+      s.sel_bin = c | (residual ? 1u << 16 : 0u);
       a.states[row].stage = kStageDone;
     }
   }
   __syncthreads();
-  const uint64_t within = s.sel_excl;
-  const uint32_t c = s.sel_bin & 0xffu, g = (s.sel_bin >> 8) & 0xffu;
+  const uint32_t c = s.sel_bin & 0xffu;
   const bool residual = (s.sel_bin >> 16) != 0;
+  // Chunk c again, requested together with its slice sums.
+  uint64_t vg = 0;
+  if (w == 0 && lane < G)
+    vg = ld_dev(&parts[c].v[(residual ? kResidualSlot + 1 : 1u) + lane]);
   load_chunk<DT>(a, rp, row, c, s, xs);
+  if (w == 0) {
+    uint64_t wi = s.sel_excl;
+    const uint32_t gg = pick_slice(vg, G, wi);
+    if (lane == 0) {
+      s.slice = gg;
+      s.slice_within = wi;
+    }
+  }
+  __syncthreads();
+  const uint32_t g = s.slice;
+  const uint64_t within = s.slice_within;
   const uint32_t jg = g / kWaves;
   if (w == g % kWaves) {
     const uint32_t tbase = c * CHUNK + jg * SLAB + tid * VEC;
