@@ -103,6 +103,8 @@ struct SampleLaunch {
   uint32_t stage;
   uint32_t aligned;       // rows start on 16-byte boundaries: vector loads
   uint32_t all_sampled;   // every row of the launch is sampled
+  uint32_t uncut_rows;    // mixed launch: merges skip sampled rows with no
+                          // cut, mass_draw_kernel draws only those
   const uint2 *pen_entries;
   const uint32_t *pen_offsets;
   uint32_t pen_max_entries;

@@ -632,6 +632,13 @@ __device__ __forceinline__ uint32_t row_draft(const SampleLaunch &a,
 // The draft's probability of `token` for a drafted row: its dense q, or
 // the first sparse candidate that lists it (sampling.metal:703-708); the
 // merge stages the row's 16 candidates in s.cids/s.cprobs.
+// A sampled row with no min-p, top-k or top-p cut: it keeps every admitted
+// token. In a launch that mixes such rows with cut ones (a.uncut_rows), the
+// merges finish only the cut rows and mass_draw_kernel the uncut ones.
+__device__ __forceinline__ bool uncut_row(const RowParams &rp) {
+  return (rp.flags & kRowSampled) && !(rp.flags & (kRowMinP | kRowTopK | kRowTopP));
+}
+
 template <class L>
 __device__ __forceinline__ float draft_q(const SampleLaunch &a, uint32_t row,
                                          uint32_t token, const L &s) {
@@ -1744,6 +1751,11 @@ __device__ __forceinline__ void merge_row(const SampleLaunch &a,
                                           const RowParams &rp, uint32_t row,
                                           Lds &s) {
   const uint32_t S = a.chunks, tid = threadIdx.x;
+  if (a.uncut_rows && uncut_row(rp)) {
+    // mass_draw_kernel draws it; no stage may pick it up.
+    if (tid == 0) a.states[row].stage = kStageDone;
+    return;
+  }
   if (!(rp.flags & kRowSampled)) {
     if (tid < 64) {
       float bv = -__builtin_inff();
@@ -2653,6 +2665,11 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     s.merge.key[1024 + b] = 0;
   }
   const RowParams rp = wait_row_policy(prr);
+  if (a.uncut_rows && uncut_row(rp)) {
+    // mass_draw_kernel draws it.
+    if (tid == 0) a.states[row].stage = kStageDone;
+    return;
+  }
 
   if (!(rp.flags & kRowSampled)) {
     // Greedy: the largest chunk best, the lowest id among equals.
@@ -3344,6 +3361,8 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
   // read): the chunk's requests go out before the row's policy arrives.
   const bool all_sampled = a.all_sampled != 0;
   const RowParams rp = a.params[row];
+  // A mixed launch: the merge finished every other row.
+  if (a.uncut_rows && !uncut_row(rp)) return;
   // Requested up front: the chunk summaries (every wave, one lane per
   // chunk; the select launch ended before this one began), the draft token
   // and the row's uniform, which only the last block uses.

@@ -617,9 +617,34 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   // cut) and carry no draft need only the row maximum and the chunk masses:
   // the selection writes chunk maxima, then one mass-and-draw launch finishes
   // every row (no merge, no stages).
-  bool unfiltered = fast && any_sampled && !kept;
-  for (uint32_t r = 0; unfiltered && r < rows; ++r)
-    if (params[r].flags & (jf::kRowMinP | jf::kRowTopK | jf::kRowTopP)) unfiltered = false;
+  constexpr uint32_t kCuts = jf::kRowMinP | jf::kRowTopK | jf::kRowTopP;
+  bool any_uncut = false, any_cut = false;
+  for (uint32_t r = 0; r < rows; ++r)
+    if (params[r].flags & jf::kRowSampled) {
+      if (params[r].flags & kCuts)
+        any_cut = true;
+      else
+        any_uncut = true;
+    }
+  const bool unfiltered = fast && any_sampled && !kept && !any_cut;
+  // A launch that mixes both kinds: the merge (and the stages) finish the
+  // cut rows and skip the uncut ones, which the mass-and-draw launch then
+  // finishes; the uncut rows no longer decide the merge or the stages.
+  const bool mixed = fast && any_uncut && any_cut && !kept;
+  if (mixed) {
+    staged = need_count1 = need_topk = need_topp = false;
+    for (uint32_t r = 0; r < rows; ++r) {
+      const jf::RowParams &rp = params[r];
+      if ((rp.flags & jf::kRowSampled) && (rp.flags & kCuts) &&
+          rp.top_k > (uint32_t)jf::kBlockCandidates) {
+        staged = true;
+        need_count1 |= (rp.flags & (jf::kRowMinP | jf::kRowTopK)) != 0;
+        need_topk |= (rp.flags & jf::kRowTopK) != 0;
+        need_topp |= (rp.flags & jf::kRowTopP) != 0;
+      }
+    }
+    L.uncut_rows = 1u;
+  }
   if (fast) {
     jf::FastLaunch F{};
     F.a = L;
@@ -665,6 +690,7 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
                a->uniform_stride <= 0xffffffffull;
   for (uint32_t r = 0; small && r < rows; ++r) {
     const jf::RowParams &rp = params[r];
+    if (mixed && !(rp.flags & kCuts)) continue;  // the mass-and-draw launch's
     if ((rp.flags & jf::kRowSampled) && (!(rp.flags & jf::kRowTopK) || rp.top_k > 64u))
       small = false;
   }
@@ -695,6 +721,14 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
       L.stage = stage;
       e = jf::launch_stage(L, a->dtype, stream);
       if (e != hipSuccess) return hip_fail((hipError_t)e, "stage launch");
+    }
+  }
+  if (mixed) {
+    e = jf::launch_mass_draw(L, a->dtype, stream);
+    if (e != hipSuccess) return hip_fail((hipError_t)e, "mass-and-draw launch");
+    if (L.drafted_rows) {
+      e = jf::launch_residual_draw(L, a->dtype, stream);
+      if (e != hipSuccess) return hip_fail((hipError_t)e, "residual draw launch");
     }
   }
   return JF_OK;

@@ -365,6 +365,42 @@ def test_unfiltered_mass_draw(bf16, greedy, draft):
     assert g["tokens"][8] != NO and g["tokens"][0] != NO
 
 
+@pytest.mark.parametrize("kind", ["small", "general", "staged", "drafted"])
+def test_mixed_cut_and_uncut_rows(kind):
+    """Launches mixing rows with a cut and rows that keep every admitted
+    token: the merge (small, general, or with stages for a large k) finishes
+    the cut rows and greedy rows, the mass-and-draw launch the uncut ones."""
+    rng = np.random.default_rng(71 + len(kind))
+    V = 5 * 8192 + 1234
+    rows = 10
+    x = rand_logits(rng, rows, V, scale=2.0)
+    x[3, ::5] = np.nan
+    allowed = rng.random((rows, V)) < 0.4
+    masks = WL.mask_words(allowed)
+    cut = {"small": J.policy(temperature=0.8, top_k=50, top_p=0.9),
+           "general": J.policy(temperature=0.8, top_k=300, top_p=0.9),
+           "staged": J.policy(temperature=1.1, top_k=3000, min_p=0.01),
+           "drafted": J.policy(temperature=0.9, top_k=40)}[kind]
+    pols = [cut, J.policy(temperature=1.0), J.policy(), J.policy(temperature=0.6, presence=0.3),
+            cut, J.policy(temperature=1.0, constrained=True), J.policy(temperature=0.7, top_k=20),
+            J.policy(temperature=1.3, repetition=1.2), J.policy(constrained=True),
+            J.policy(temperature=1.0)]
+    hist = [rng.integers(0, V, 400).astype(np.uint32) for _ in range(rows)]
+    u = rng.random(rows).astype(np.float32)
+    kw = dict(masks=masks, histories=hist, generated=[200] * rows,
+              mark_prompt=[True] * rows, uniforms=u, logits=x)
+    if kind == "drafted":
+        d = rng.integers(0, V, rows).astype(np.uint32)
+        d[[2, 8]] = NO
+        cand = rng.integers(0, V, (rows, 16)).astype(np.uint32)
+        cand[:, 0] = d
+        kw.update(draft_tokens=d, drafted_rows=rows, cand_ids=cand,
+                  cand_probs=rng.dirichlet(np.ones(16), rows).astype(np.float32))
+    g, r = both(V, pols, **kw)
+    assert_same(g, r)
+    assert np.all(g["tokens"] != NO)
+
+
 def test_c3_sampled_without_kept_outputs():
     """C3 sampled as the engine calls it (no kept outputs): the two-pass
     mass-and-draw path at full size."""
