@@ -2596,7 +2596,7 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     const BlockHeader *headers, const uint64_t *cands, const RowParams *params,
     const float *uniforms, const uint32_t *uniform_index, uint32_t S,
     uint32_t uniform_offset, uint32_t uniform_stride, uint32_t drafted_rows,
-    SampleLaunch a) {
+    uint32_t uncut_rows, SampleLaunch a) {
   Lds &s = g_small_lds;
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
   // Every address of the row, computed once and held in vector registers:
@@ -2665,7 +2665,7 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     s.merge.key[1024 + b] = 0;
   }
   const RowParams rp = wait_row_policy(prr);
-  if (a.uncut_rows && uncut_row(rp)) {
+  if (uncut_rows && uncut_row(rp)) {
     // mass_draw_kernel draws it.
     if (tid == 0) a.states[row].stage = kStageDone;
     return;
@@ -3795,7 +3795,7 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream) {
     hipLaunchKernelGGL(kernel, grid, block, 0, st, a.headers, (const uint64_t *)a.cands,
                        a.params, a.uniforms, a.uniform_index, a.chunks,
                        (uint32_t)a.uniform_offset, (uint32_t)a.uniform_stride,
-                       a.draft_tokens ? a.drafted_rows : 0u, a);
+                       a.draft_tokens ? a.drafted_rows : 0u, a.uncut_rows, a);
   };
   if (dtype == 0)
     go(merge_small_kernel<0>);
