@@ -496,8 +496,9 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: every box has one "
-                          "MI355X; rows shard across GPUs with no exchange (see "
-                          "DESIGN.md), so run --gpus 1"}))
+                          "MI355X, and rows would shard across GPUs with no "
+                          "exchange (each GPU samples its own rows), so run "
+                          "--gpus 1"}))
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
