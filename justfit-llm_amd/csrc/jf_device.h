@@ -274,6 +274,44 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { JF_BUTTERFLY(uint
 __device__ __forceinline__ float wave_max_f32(float v) { JF_BUTTERFLY(float, xor_f32, max_f32) }
 #undef JF_BUTTERFLY
 
+// Several wave totals at once: v[j] are the lane's N (4 or 8) values, and
+// lane l gets the wave's total of v[j] for j = l / (64 / N). Each exchange
+// step halves what a lane carries: a lane whose bit is clear keeps the
+// lower half of its values and sends the upper half to its partner, which
+// does the opposite. The lanes that share a j then add up their partials.
+// About a third of the instructions of N separate butterflies.
+template <int N>
+__device__ __forceinline__ uint64_t wave_sums_u64(const uint64_t (&v)[N]) {
+  static_assert(N == 4 || N == 8, "four or eight values per lane");
+  const uint32_t l = lane_id();
+  const bool h5 = (l >> 5) & 1u, h4 = (l >> 4) & 1u;
+  constexpr int H = N / 2;
+  uint64_t a[H];
+#pragma unroll
+  for (int k = 0; k < H; ++k) {
+    const uint64_t keep = h5 ? v[H + k] : v[k], send = h5 ? v[k] : v[H + k];
+    a[k] = keep + xor_u64<32>(send);
+  }
+  uint64_t c;
+  if constexpr (N == 8) {
+    const bool h3 = (l >> 3) & 1u;
+    uint64_t b[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint64_t keep = h4 ? a[2 + k] : a[k], send = h4 ? a[k] : a[2 + k];
+      b[k] = keep + xor_u64<16>(send);
+    }
+    c = (h3 ? b[1] : b[0]) + xor_u64<8>(h3 ? b[0] : b[1]);
+  } else {
+    c = (h4 ? a[1] : a[0]) + xor_u64<16>(h4 ? a[0] : a[1]);
+    c += xor_u64<8>(c);
+  }
+  c += xor_u64<4>(c);
+  c += xor_u64<2>(c);
+  c += xor_u64<1>(c);
+  return c;
+}
+
 // Inclusive prefix sums over lanes: row-wise by DPP shifts, then the
 // totals of the rows before (lanes 15, 31, 47) added.
 __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {

@@ -3407,16 +3407,21 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
   // weighs zero.
   const float inv_t = rp.inv_t;
   StagePartial *parts = a.partials + (uint64_t)row * S;
-  uint64_t total = 0;
+  uint64_t lv[LOADS];
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
-    uint64_t sj = 0;
+    lv[j] = 0;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) sj += quantized_weight(xs[j * VEC + e], M, inv_t);
-    sj = wave_sum_u64(sj);
-    if (lane == 0) st_dev(&parts[chunk].v[1 + j * kWaves + w], sj);
-    total += sj;
+    for (int e = 0; e < VEC; ++e) lv[j] += quantized_weight(xs[j * VEC + e], M, inv_t);
   }
+  // Lane l holds the wave's sum of load l / (64 / LOADS); the wave's total
+  // adds one lane of each load.
+  constexpr uint32_t GL = 64 / LOADS;
+  const uint64_t sl = wave_sums_u64<LOADS>(lv);
+  if (lane % GL == 0) st_dev(&parts[chunk].v[1 + (lane / GL) * kWaves + w], sl);
+  uint64_t total = sl;
+#pragma unroll
+  for (uint32_t m = GL; m < 64; m *= 2) total += shfl_xor_u64(total, (int)m);
   // The draft token's weight, from the thread that holds it (zero when the
   // row does not admit it).
   if (draft < a.vocabulary && draft / CHUNK == chunk) {
@@ -3543,20 +3548,24 @@ __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a)
   const uint64_t mass3 = st.mass3;
   const uint32_t lane_base = chunk * CHUNK + tid * VEC;
   StagePartial *parts = a.partials + (uint64_t)row * S;
-  uint64_t total = 0;
+  uint64_t lv[LOADS];
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
-    uint64_t sj = 0;
+    lv[j] = 0;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const int i = j * VEC + e;
       const float q = a.dense_q ? qv[i] : draft_q(a, row, lane_base + j * SLAB + e, s);
-      sj += residual_of(quantized_weight(xs[i], M, inv_t), mass3, q);
+      lv[j] += residual_of(quantized_weight(xs[i], M, inv_t), mass3, q);
     }
-    sj = wave_sum_u64(sj);
-    if (lane == 0) st_dev(&parts[chunk].v[kResidualSlot + 1 + j * kWaves + w], sj);
-    total += sj;
   }
+  constexpr uint32_t GL = 64 / LOADS;
+  const uint64_t sl = wave_sums_u64<LOADS>(lv);
+  if (lane % GL == 0)
+    st_dev(&parts[chunk].v[kResidualSlot + 1 + (lane / GL) * kWaves + w], sl);
+  uint64_t total = sl;
+#pragma unroll
+  for (uint32_t m = GL; m < 64; m *= 2) total += shfl_xor_u64(total, (int)m);
   if (lane == 0) s.wl[w] = total;
   __syncthreads();
   if (tid == 0)
