@@ -4,8 +4,10 @@ Bar: bit-exact tokens, kept sets, kept probabilities and draft probabilities
 (the oracle restates the same fp32 weight and exact integer sums); greedy ids
 bit-exact. Full-size configs C1-C3 and C5 are compared row by row; edge cases
 cover ties, empty/NaN/inf rows, masks, stop exclusion, vocabularies that do
-not fill a chunk, and the multi-pass stages (top-k disabled with top-p or
-min-p, large k)."""
+not fill a chunk, the multi-pass stages (top-k disabled with top-p or
+min-p, large k), the two-pass draw of rows with no cut (with plain, dense
+and sparse drafts, and mixed with cut rows in one launch), and chi-square
+tests of 10^6 draws through the merge and through the two-pass draw."""
 import numpy as np
 import pytest
 
@@ -473,4 +475,42 @@ def test_chi_square_of_one_million_draws():
     keep = expected >= 5
     chi2 = ((counts[keep] - expected[keep]) ** 2 / expected[keep]).sum()
     pval = stats.chi2.sf(chi2, keep.sum() - 1)
+    assert pval > 1e-4, (chi2, pval)
+
+
+def test_chi_square_two_pass_draw():
+    """1e6 draws from rows with no cut (the two-pass draw: chunk masses, then
+    slice and token walks) against the float64 softmax of 200 tokens spread
+    over two chunks and their wave slices; every other token is -inf."""
+    import torch
+    from scipy import stats
+    V = 2 * 8192
+    rows = 4096
+    calls = 245
+    rng = np.random.default_rng(17)
+    ids = np.sort(rng.choice(V, 200, replace=False))
+    ids[:3] = [0, 8191, 8192]                # chunk and slice edges
+    ids = np.unique(ids)
+    base = np.full(V, -np.inf, np.float32)
+    base[ids] = rng.uniform(-1.0, 1.0, len(ids)).astype(np.float32)
+    pol = J.policy(temperature=1.0)
+    dev = torch.device("cuda", 0)
+    lg = torch.from_numpy(np.tile(base, (rows, 1))).to(dev)
+    out = torch.zeros(rows, dtype=torch.int32, device=dev)
+    s = J.Sampler(V, rows)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(17)
+    counts = torch.zeros(V, dtype=torch.int64, device=dev)
+    for _ in range(calls):
+        u = torch.rand(rows, device=dev, generator=gen)
+        s.sample(lg, [pol] * rows, out, uniforms=u)
+        counts += torch.bincount(out.long(), minlength=V)[:V]
+    counts = counts.cpu().numpy()
+    n = rows * calls
+    assert counts.sum() == n
+    assert counts[np.setdiff1d(np.arange(V), ids)].sum() == 0   # only weighted tokens
+    w = np.exp(base[ids].astype(np.float64))
+    expected = w / w.sum() * n
+    chi2 = ((counts[ids] - expected) ** 2 / expected).sum()
+    pval = stats.chi2.sf(chi2, len(ids) - 1)
     assert pval > 1e-4, (chi2, pval)
