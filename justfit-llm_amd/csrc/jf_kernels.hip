@@ -3622,7 +3622,10 @@ __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a)
 #pragma unroll
       for (int j = 0; j < LOADS; ++j) x = (uint32_t)j == jg ? xs[j * VEC + e] : x;
       const uint64_t wq = quantized_weight(x, M, inv_t);
-      q[e] = residual ? residual_of(wq, mass3, draft_q(a, row, tbase + e, s)) : wq;
+      // Past the vocabulary (a partial last chunk) the weight is zero and
+      // no q is read: a dense q row ends at the vocabulary.
+      const float qe = tbase + e < a.vocabulary ? draft_q(a, row, tbase + e, s) : 0.0f;
+      q[e] = residual ? residual_of(wq, mass3, qe) : wq;
     }
     uint32_t e_hit;
     if (lane == slice_hit<VEC>(q, within, e_hit)) {
