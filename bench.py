@@ -40,10 +40,6 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="bound of the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--read-ceiling", action="store_true",
-                    help="time a plain device reduction over C2's logit bytes, "
-                         "one launch at a time after a small kernel as in the "
-                         "sampler's step: what one read of this size reaches")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 64 MiB device copy (20 times): the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / "
@@ -292,27 +288,6 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes_read": n, "bytes_written": n, "launches": 20}))
 
 
-def read_ceiling():
-    """A plain streaming read of C2's logit bytes (libjf_read_probe.so), each
-    launch timed alone by HIP events after a small kernel."""
-    import ctypes
-    import torch
-    probe = ctypes.CDLL(os.path.join(REPO, "justfit-llm_amd", "jf_sampler",
-                                     "libjf_read_probe.so"))
-    n = 38895616
-    copies = [torch.ones(n // 4, dtype=torch.float32, device="cuda") for _ in range(14)]
-    scratch = torch.zeros(4, dtype=torch.float32, device="cuda")
-    ptrs = (ctypes.c_void_p * len(copies))(*[c.data_ptr() for c in copies])
-    mean, p50 = ctypes.c_float(), ctypes.c_float()
-    rc = probe.jf_probe_read_ceiling(ptrs, len(copies), ctypes.c_uint64(n), 200,
-                                     ctypes.c_void_p(scratch.data_ptr()),
-                                     ctypes.byref(mean), ctypes.byref(p50))
-    assert rc == 0, rc
-    print(json.dumps({"read_ceiling_bytes": n, "mean_us": mean.value, "p50_us": p50.value,
-                      "GBps": n / (mean.value * 1e-6) / 1e9,
-                      "frac_of_8TBps": n / (mean.value * 1e-6) / 1e9 / PEAK_HBM_GBS}))
-
-
 def bench_draft(args):
     """The draft selector (jf_draft_select) at the reference's widest batch:
     4 lanes x 7 proposal positions over V=151936 fp32 draft logits, inputs
@@ -490,9 +465,6 @@ def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration()
-        return
-    if args.read_ceiling:
-        read_ceiling()
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: every box has one "

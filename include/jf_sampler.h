@@ -40,12 +40,12 @@ extern "C" {
 #define JF_UNIFORM_CORRECTION 15u
 #define JF_UNIFORM_TREE_DRAWS 24u
 #define JF_SAMPLING_UNIFORMS 40u
-/* Draft candidates per proposal position (ExecutionGeometry.h:288). */
+/* Draft candidates per proposal position (ExecutionGeometry.h:47). */
 #define JF_DRAFT_CANDIDATES 16u
 /* Penalty word layout (metal/abi/Sampling.h:111-112). */
 #define JF_PENALTY_PROMPT_BIT 0x80000000u
 #define JF_PENALTY_COUNT_MASK 0x7fffffffu
-/* Tree geometry (metal/abi/TreeVerify.h:175-176). */
+/* Tree geometry (metal/abi/TreeVerify.h:19-20). */
 #define JF_TREE_MAXIMUM_ROWS 16u
 #define JF_TREE_MAXIMUM_DEPTH 8u
 
@@ -82,8 +82,8 @@ int jf_policy_validate(const jf_policy *policy);
 
 /* ops::Sampling::Sampling(vocabulary) (Sampling.cpp:82-86), plus the device
  * scratch the reference sizes with Sampling::workspace(rows)
- * (Sampling.cpp:37-48), owned here for up to max_rows rows per call. Creates
- * on the current HIP device; synchronous. */
+ * (Sampling.cpp:37-48), owned here for up to max_rows rows per call
+ * (1 .. 4194304). Creates on the current HIP device; synchronous. */
 int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
                       jf_sampler **out);
 int jf_sampler_destroy(jf_sampler *sampler);
@@ -231,8 +231,8 @@ int jf_accept_chain(jf_sampler *sampler, const jf_accept_chain_args *args,
                     void *stream);
 
 /* One lane's draft tree: the fields of JustFitTreeLane that acceptance reads
- * (TreeVerify.h:178-187) and the sampled chain of JustFitTreeAcceptParams
- * (TreeVerify.h:196-208). Rows in DFS preorder, parent[r] < r, row 0 the
+ * (TreeVerify.h:22-31) and the sampled chain of JustFitTreeAcceptParams
+ * (TreeVerify.h:40-52). Rows in DFS preorder, parent[r] < r, row 0 the
  * anchor; rows 0 .. chain_rows-1 are the draft's sampled chain and chain_q[r]
  * is the draft probability of row r+1's token. */
 typedef struct jf_tree_lane {
@@ -269,7 +269,7 @@ int jf_accept_tree(jf_sampler *sampler, const jf_accept_tree_args *args,
 /* ---- draft selector ---------------------------------------------------- */
 
 /* The DFlash draft's proposal policy: ops::DraftSelector
- * (source/runtime/ops/DraftSelector.hpp:40-68, DraftSelector.cpp:43-154),
+ * (source/runtime/ops/DraftSelector.hpp:41-60, DraftSelector.cpp:22-92),
  * kernels draft_select_top16_sharded / draft_select_edges /
  * draft_select_dflash (sampling.metal:995-1359). Lane geometry as in
  * ExecutionGeometry.h: 8 query rows, 7 proposal positions, 16 candidates per
@@ -280,15 +280,15 @@ int jf_accept_tree(jf_sampler *sampler, const jf_accept_tree_args *args,
 
 typedef struct jf_draft_selector jf_draft_selector;
 
-/* DraftSelector::DraftSelector(vocabulary) (DraftSelector.cpp:43-46), plus
- * the scratch DraftSelector::workspace sizes (DraftSelector.cpp:48-57),
+/* DraftSelector::DraftSelector(vocabulary) (DraftSelector.cpp:22-25), plus
+ * the scratch DraftSelector::workspace sizes (DraftSelector.cpp:27-36),
  * owned here for up to max_lanes lanes per call. Creates on the current HIP
  * device; synchronous. */
 int jf_draft_selector_create(uint32_t vocabulary, uint32_t max_lanes,
                              jf_draft_selector **out);
 int jf_draft_selector_destroy(jf_draft_selector *selector);
 
-/* DraftSelector::add (DraftSelector.cpp:59-154) over `lanes` lanes. Lane l
+/* DraftSelector::add (DraftSelector.cpp:38-92) over `lanes` lanes. Lane l
  * reads its query rows logits + (l*8 + r) * logits_stride (fp32; rows 1..7
  * are proposal positions 0..6) and selector_hidden + (l*8 + r) * 256 (bf16
  * bits), the bf16 codebooks [vocabulary][256] (16-byte aligned), anchors[l]

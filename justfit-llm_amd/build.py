@@ -1,18 +1,24 @@
 """Builds libjf_sampler.so (the C-ABI library) in-tree for gfx950.
 
+Each source compiles to its own object in parallel (justfit-llm_amd/_build/),
+then one link makes the shared library.
+
 Usage: python justfit-llm_amd/build.py   (also called by __graft_entry__.build)
 """
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
+OBJ = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "jf_sampler", "libjf_sampler.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["jf_kernels.hip", "jf_draft.hip", "jf_gather.hip", "jf_sampler.cpp", "jf_tree.cpp", "jf_mask_wire.cpp", "sampling.cpp"]
+SOURCES = ["jf_kernels.hip", "jf_draft.hip", "jf_gather.hip", "jf_sampler.cpp",
+           "jf_tree.cpp", "jf_mask_wire.cpp", "sampling.cpp"]
 
 # -ffp-contract=off: every fp32 expression rounds as written, so the CPU
 # restatement reproduces the weights bit for bit. Packed fp32 instructions are
@@ -22,7 +28,6 @@ FLAGS = [
     "-O3",
     "-std=c++20",
     "-fPIC",
-    "-shared",
     "-ffp-contract=off",
     "-fno-fast-math",
     "-Wall",
@@ -32,31 +37,34 @@ FLAGS = [
     "-I" + os.path.join(REPO, "include"),
     "-I" + CSRC,
 ]
+NOISE = "'-packed-fp32-ops' is not a recognized feature"
 
 
-def build(verbose: bool = True) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = OUT + ".tmp"
-    cmd = [HIPCC] + FLAGS + ["-o", tmp] + srcs
+def _run(cmd, what, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "'-packed-fp32-ops' is not a recognized feature"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    err = "\n".join(l for l in res.stderr.splitlines() if NOISE not in l)
     if res.returncode != 0:
         sys.stderr.write(err + "\n")
-        raise RuntimeError("hipcc failed building libjf_sampler.so")
+        raise RuntimeError(f"hipcc failed: {what}")
     if err.strip() and verbose:
         sys.stderr.write(err + "\n")
+
+
+def build(verbose: bool = True) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    objs = [os.path.join(OBJ, s + ".o") for s in SOURCES]
+    jobs = [([HIPCC] + FLAGS + ["-c", "-o", o, os.path.join(CSRC, s)], s, verbose)
+            for s, o in zip(SOURCES, objs)]
+    workers = min(len(jobs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)))
+    with ThreadPoolExecutor(max_workers=max(1, workers)) as pool:
+        for f in [pool.submit(_run, *j) for j in jobs]:
+            f.result()
+    tmp = OUT + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs,
+         "link libjf_sampler.so", verbose)
     os.replace(tmp, OUT)
-    # The read-ceiling probe of bench.py (measurement support, its own library).
-    probe = os.path.join(HERE, "jf_sampler", "libjf_read_probe.so")
-    cmd = [HIPCC] + FLAGS + ["-o", probe + ".tmp", os.path.join(CSRC, "read_probe.hip")]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        sys.stderr.write(res.stderr + "\n")
-        raise RuntimeError("hipcc failed building libjf_read_probe.so")
-    os.replace(probe + ".tmp", probe)
     return OUT
 
 

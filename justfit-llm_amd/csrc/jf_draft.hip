@@ -1,6 +1,6 @@
 // The draft selector on gfx950: the DFlash draft's proposal policy
 // (draft_select_top16_sharded, draft_select_edges, draft_select_dflash in
-// sampling.metal:995-1359, dispatched by DraftSelector.cpp:100-154).
+// sampling.metal:995-1359, dispatched by DraftSelector.cpp:38-92).
 //
 // A lane has 8 query rows of fp32 draft logits; rows 1..7 are its proposal
 // positions. Two launches:

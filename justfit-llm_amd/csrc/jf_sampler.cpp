@@ -101,6 +101,8 @@ int device_alloc(T **p, size_t count, const char *what) {
   return JF_OK;
 }
 
+constexpr uint32_t kMaxRows = 1u << 22;
+
 bool penalties_active(const jf_policy &p) {
   return p.repetition != 1.0f || p.presence != 0.0f || p.frequency != 0.0f;
 }
@@ -199,6 +201,10 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
   *out = nullptr;
   if (!vocabulary) return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling geometry");
   if (!max_rows) return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling workspace row count");
+  // The fast selection launch packs its first row, in units of 256 rows,
+  // into 14 bits of one kernel argument.
+  if (max_rows > kMaxRows)
+    return fail(JF_ERR_INVALID_ARGUMENT, "sampling workspace row count exceeds 4194304");
   const uint32_t max_chunks = (vocabulary + jf::kChunkF32 - 1) / jf::kChunkF32;
   if (max_chunks > 64)
     return fail(JF_ERR_INVALID_ARGUMENT, "vocabulary exceeds 524288 tokens");
@@ -879,7 +885,7 @@ int jf_draft_selector_create(uint32_t vocabulary, uint32_t max_lanes,
                              jf_draft_selector **out) {
   if (!out) return fail(JF_ERR_INVALID_ARGUMENT, "output pointer is null");
   *out = nullptr;
-  // DraftSelector.cpp:43-46 and DraftSelector::workspace (48-57).
+  // DraftSelector.cpp:22-25 and DraftSelector::workspace (27-36).
   if (!vocabulary) return fail(JF_ERR_INVALID_ARGUMENT, "invalid draft selector vocabulary");
   if (!max_lanes)
     return fail(JF_ERR_INVALID_ARGUMENT, "invalid draft selector workspace position count");
@@ -918,7 +924,7 @@ int jf_draft_select(jf_draft_selector *d, const jf_draft_select_args *a, void *s
   if (!d || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null selector or arguments");
   int rc = check_device(d->device);
   if (rc != JF_OK) return rc;
-  // DraftSelector::add's checks (DraftSelector.cpp:64-110), before any launch.
+  // DraftSelector::add's checks (DraftSelector.cpp:43-76), before any launch.
   if (!a->lanes || a->lanes > d->max_lanes || !a->anchors || !a->policies)
     return fail(JF_ERR_INVALID_ARGUMENT, "invalid draft selector batch");
   if (!a->logits || a->logits_stride < d->vocabulary)

@@ -188,7 +188,7 @@ def config5(V=V_LARGE, B=256, H=8192):
 
 
 def config_draft(V=V_QWEN, lanes=4, seed=6):
-    """The draft selector's step (DraftSelector.cpp:100-154) at the
+    """The draft selector's step (DraftSelector.cpp:38-92) at the
     reference's widest batch (4 lanes): 8 fp32 query rows per lane of
     N(0, 2^2) draft logits (rows 1..7 are the proposal positions) with a few
     +6 peaks, bf16 selector hidden rows N(0, 1) and bf16 codebooks

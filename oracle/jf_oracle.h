@@ -144,7 +144,7 @@ void jfo_accept_tree(const jfo_tree_params *p, const float *target_draft_prob,
                      uint32_t *path_rows);
 
 /* Draft selector (the DFlash draft's proposal policy: sampling.metal:995-1359,
- * DraftSelector.cpp:100-154). A lane has 8 query rows; rows 1..7 are its
+ * DraftSelector.cpp:38-92). A lane has 8 query rows; rows 1..7 are its
  * proposal positions. */
 #define JFO_DRAFT_POSITIONS 7u
 #define JFO_DRAFT_QUERY_ROWS 8u

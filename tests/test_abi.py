@@ -87,6 +87,16 @@ def test_policy_validation_matches_reference_rules():
         assert O.lib().jfo_policy_valid(ctypes.byref(O.policy_from(p))) != 0
 
 
+def test_sampler_row_count_is_bounded():
+    """Rows are rejected before any device call: none and more than 2^22 (the
+    fast launch packs its first row in 14 bits of 256-row units)."""
+    for rows, msg in ((0, "row count"), ((1 << 22) + 1, "exceeds 4194304")):
+        h = ctypes.c_void_p()
+        rc = J.lib().jf_sampler_create(1000, rows, ctypes.byref(h))
+        assert rc == J.JF_ERR_INVALID_ARGUMENT and not h.value
+        assert msg in J.lib().jf_last_error().decode()
+
+
 def test_product_has_no_oracle_or_fallback():
     """The product never loads the oracle and has no CPU compute path."""
     pkg = os.path.join(REPO, "justfit-llm_amd")
