@@ -201,6 +201,20 @@ typedef struct jf_sample_args {
 
 int jf_sample(jf_sampler *sampler, const jf_sample_args *args, void *stream);
 
+/* jf_sample without a sampler object and without any allocation. It has no
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The scratch that jf_sampler_create would
+ * allocate is instead one file-scope device array of 21,049,600 bytes, held
+ * by every GPU the library runs on until the process ends. Limits: 1..64
+ * rows and a vocabulary of 1..262,144 tokens; larger calls return
+ * JF_ERR_INVALID_ARGUMENT. The caller still passes inputs and outputs (and
+ * any penalty table, created beforehand). Same arguments, results and errors
+ * as jf_sample otherwise. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (on different streams) race; calls in one
+ * stream's order do not. */
+int jf_sample_static(uint32_t vocabulary, const jf_sample_args *args, void *stream);
+
 /* ---- acceptance ------------------------------------------------------- */
 
 /* Sampling::addAcceptance (Sampling.cpp:278-328) -> decode_accept_dflash

@@ -17,7 +17,7 @@ OBJ = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "jf_sampler", "libjf_sampler.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["jf_kernels.hip", "jf_draft.hip", "jf_gather.hip", "jf_sampler.cpp",
+SOURCES = ["jf_kernels.hip", "jf_draft.hip", "jf_gather.hip", "jf_noalloc.hip", "jf_sampler.cpp",
            "jf_tree.cpp", "jf_mask_wire.cpp", "sampling.cpp"]
 
 # -ffp-contract=off: every fp32 expression rounds as written, so the CPU

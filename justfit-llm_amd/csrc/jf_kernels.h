@@ -5,6 +5,8 @@
 
 #include <stdint.h>
 
+struct jf_sample_args;
+
 namespace jf {
 
 // Per-row target policy as the kernels read it (the reference's
@@ -298,6 +300,33 @@ struct GatherLaunch {
   uint64_t row_stride, lane_stride, layer_stride;
   uint32_t layers, lanes, rows;
 };
+
+// The device scratch of one selection: where its kernels exchange row
+// parameters, chunk summaries, candidate lists, arrival counters (zero
+// between calls), row states and stage partials. Room for max_rows rows of
+// at most max_chunks 8192-token chunks.
+struct SampleScratch {
+  RowParams *params;        // [max_rows]
+  BlockHeader *headers;     // [max_rows * max_chunks]
+  uint64_t *cands;          // [max_rows * max_chunks * kBlockCandidates]
+  uint32_t *counters;       // [max_rows]
+  RowState *states;         // [max_rows]
+  StagePartial *partials;   // [max_rows * max_chunks]
+  uint32_t max_rows;
+  uint32_t max_chunks;
+};
+
+// How a selection's host-built row parameters reach scratch.params before
+// its kernels run (stream-ordered on `stream`); returns a JF_* status.
+typedef int (*ParamUpload)(void *ctx, const RowParams *params, uint32_t rows,
+                           RowParams *device, void *stream);
+
+// The body of jf_sample over a given scratch (jf_sampler.cpp): validates the
+// call, builds each row's parameters into `params` (host, args->rows
+// entries), hands them to `upload`, then enqueues the kernels on `stream`.
+int sample_core(uint32_t vocabulary, const SampleScratch &scratch,
+                const jf_sample_args *args, RowParams *params, ParamUpload upload,
+                void *upload_ctx, void *stream);
 
 // Launchers (jf_kernels.hip); they return the hipError_t of the launch.
 // With both events set, they record the selection kernel's own start and end.

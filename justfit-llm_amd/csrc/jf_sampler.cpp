@@ -458,13 +458,19 @@ void jf_stage_sampling_cycle(uint64_t seed, uint64_t *counter,
 
 // ---- selection ---------------------------------------------------------
 
-int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
-  if (!s || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler or arguments");
-  int rc = check_device(s->device);
-  if (rc != JF_OK) return rc;
-  const uint32_t V = s->vocabulary, rows = a->rows;
-  if (!rows || rows > s->max_rows)
+}  // extern "C"
+
+namespace jf {
+
+int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
+                RowParams *params, ParamUpload upload, void *upload_ctx,
+                void *stream) {
+  int rc = JF_OK;
+  const uint32_t rows = a->rows;
+  if (!rows || rows > sc.max_rows)
     return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling batch width");
+  if ((V + kChunkF32 - 1) / kChunkF32 > sc.max_chunks)
+    return fail(JF_ERR_INVALID_ARGUMENT, "vocabulary exceeds the sampling scratch");
   if (a->dtype != JF_DTYPE_F32 && a->dtype != JF_DTYPE_BF16)
     return fail(JF_ERR_INVALID_ARGUMENT, "unsupported logits dtype");
   if (!a->logits || !a->policies || !a->out_tokens)
@@ -482,7 +488,6 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
     return fail(JF_ERR_INVALID_ARGUMENT,
                 "kept outputs need ids, probabilities, counts and a capacity");
   const uint32_t W = (V + 31) / 32;
-  std::vector<jf::RowParams> params(rows);
   bool any_constrained = false, any_sampled = false, staged = false;
   bool need_count1 = false, need_topk = false, need_topp = false;
   for (uint32_t r = 0; r < rows; ++r) {
@@ -544,24 +549,15 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
       (!a->draft_cand_ids || !a->draft_cand_probs))
     return fail(JF_ERR_INVALID_ARGUMENT, "drafted rows need draft probabilities");
 
-  const hipStream_t st = (hipStream_t)stream;
-  const bool same = s->params_valid && s->last_params.size() == params.size() &&
-                    std::memcmp(s->last_params.data(), params.data(),
-                                params.size() * sizeof(jf::RowParams)) == 0;
-  if (!same) {
-    rc = s->staging.upload(s->params, params.data(),
-                           params.size() * sizeof(jf::RowParams), st);
-    if (rc != JF_OK) return rc;
-    s->last_params = params;
-    s->params_valid = true;
-  }
+  rc = upload(upload_ctx, params, rows, sc.params, stream);
+  if (rc != JF_OK) return rc;
 
   jf::SampleLaunch L{};
   L.logits = a->logits;
   L.stride = rows > 1 ? a->logits_stride : V;
   L.masks = a->masks;
   L.mask_stride = a->mask_stride;
-  L.params = s->params;
+  L.params = sc.params;
   L.vocabulary = V;
   L.chunks = (V + (a->dtype == JF_DTYPE_F32 ? jf::kChunkF32 : jf::kChunkBF16) - 1) /
              (a->dtype == JF_DTYPE_F32 ? jf::kChunkF32 : jf::kChunkBF16);
@@ -587,11 +583,11 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   L.cand_probs = a->draft_cand_probs;
   L.dense_q = a->draft_q;
   L.q_stride = a->draft_q_stride;
-  L.headers = s->headers;
-  L.cands = s->cands;
-  L.counters = s->counters;
-  L.states = s->states;
-  L.partials = s->partials;
+  L.headers = sc.headers;
+  L.cands = sc.cands;
+  L.counters = sc.counters;
+  L.states = sc.states;
+  L.partials = sc.partials;
   L.out_tokens = a->out_tokens;
   L.out_draft = a->out_draft_probs;
   L.out_kept_counts = a->out_kept_counts;
@@ -738,6 +734,43 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
     }
   }
   return JF_OK;
+}
+
+}  // namespace jf
+
+namespace {
+
+// The sampler's row parameters, uploaded through its staging ring only when
+// they differ from the last upload (stream order keeps earlier launches on
+// the values they were enqueued with).
+int sampler_upload(void *ctx, const jf::RowParams *params, uint32_t rows,
+                   jf::RowParams *device, void *stream) {
+  jf_sampler *s = (jf_sampler *)ctx;
+  const size_t bytes = (size_t)rows * sizeof(jf::RowParams);
+  if (s->params_valid && s->last_params.size() == rows &&
+      std::memcmp(s->last_params.data(), params, bytes) == 0)
+    return JF_OK;
+  const int rc = s->staging.upload(device, params, bytes, (hipStream_t)stream);
+  if (rc != JF_OK) return rc;
+  s->last_params.assign(params, params + rows);
+  s->params_valid = true;
+  return JF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
+  if (!s || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler or arguments");
+  int rc = check_device(s->device);
+  if (rc != JF_OK) return rc;
+  if (!a->rows || a->rows > s->max_rows)
+    return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling batch width");
+  const jf::SampleScratch sc{s->params, s->headers,  s->cands,    s->counters,
+                             s->states, s->partials, s->max_rows, s->max_chunks};
+  std::vector<jf::RowParams> params(a->rows);
+  return jf::sample_core(s->vocabulary, sc, a, params.data(), sampler_upload, s, stream);
 }
 
 // ---- acceptance -----------------------------------------------------------

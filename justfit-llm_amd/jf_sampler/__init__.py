@@ -33,7 +33,7 @@ EXPORTS = [
     "jf_penalty_words_rebuild", "jf_penalty_words_count",
     "jf_penalty_table_create", "jf_penalty_table_destroy",
     "jf_penalty_table_rebuild", "jf_penalty_table_count",
-    "jf_next_uniform", "jf_stage_sampling_cycle", "jf_sample",
+    "jf_next_uniform", "jf_stage_sampling_cycle", "jf_sample", "jf_sample_static",
     "jf_accept_chain", "jf_accept_tree",
     "jf_draft_selector_create", "jf_draft_selector_destroy", "jf_draft_select",
     "jf_tree_gather", "jf_build_draft_tree", "jf_mask_request_encode",
@@ -146,6 +146,13 @@ def lib():
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build it with "
                 "python justfit-llm_amd/build.py (no fallback exists)")
+        # One HIP runtime per process: torch's, which owns the device memory
+        # and streams handed to the library. Loaded first, its
+        # libamdhip64.so.7 is the one the library's dependency resolves to
+        # (loaded after the library, torch would bring a second runtime), and
+        # it is initialized before the library registers its code objects.
+        import torch
+        torch.cuda.is_available()
         L = ctypes.CDLL(LIB_PATH)
         L.jf_last_error.restype = ctypes.c_char_p
         L.jf_policy_validate.argtypes = [ctypes.POINTER(JfPolicy)]
@@ -169,6 +176,7 @@ def lib():
             c_u64, ctypes.POINTER(c_u64), c_u32, ctypes.c_int, c_vp]
         L.jf_stage_sampling_cycle.restype = None
         L.jf_sample.argtypes = [c_vp, ctypes.POINTER(JfSampleArgs), c_vp]
+        L.jf_sample_static.argtypes = [c_u32, ctypes.POINTER(JfSampleArgs), c_vp]
         L.jf_accept_chain.argtypes = [c_vp, ctypes.POINTER(JfAcceptChainArgs),
                                       c_vp]
         L.jf_accept_tree.argtypes = [c_vp, ctypes.POINTER(JfAcceptTreeArgs),
@@ -195,6 +203,14 @@ def lib():
 def check(rc):
     if rc != JF_OK:
         raise JfError(rc, lib().jf_last_error().decode())
+
+
+def sample_static(vocabulary, a, stream=None):
+    """jf_sample_static: one selection with the library's static device
+    scratch (no sampler object, no allocation); `a` as Sampler.sample_args
+    builds it."""
+    check(lib().jf_sample_static(vocabulary, ctypes.byref(a),
+                                 _stream() if stream is None else stream))
 
 
 def policy(top_k=0, temperature=0.0, top_p=1.0, min_p=0.0, repetition=1.0,

@@ -23,7 +23,7 @@ def header_functions():
 def test_library_exports_every_declared_symbol():
     declared = header_functions()
     assert sorted(J.EXPORTS) == declared
-    lib = ctypes.CDLL(J.LIB_PATH)
+    lib = J.lib()  # loads torch's HIP runtime first: one runtime per process
     for name in declared:
         assert hasattr(lib, name), name
 
