@@ -19,6 +19,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["jf_kernels.hip", "jf_draft.hip", "jf_gather.hip", "jf_noalloc.hip", "jf_sampler.cpp",
            "jf_tree.cpp", "jf_mask_wire.cpp", "sampling.cpp"]
+# jf_kernels.hip compiles as four objects (its JF_PART sections), in parallel.
+PARTS = {"jf_kernels.hip": 4}
 
 # -ffp-contract=off: every fp32 expression rounds as written, so the CPU
 # restatement reproduces the weights bit for bit. Packed fp32 instructions are
@@ -54,9 +56,17 @@ def _run(cmd, what, verbose):
 
 def build(verbose: bool = True) -> str:
     os.makedirs(OBJ, exist_ok=True)
-    objs = [os.path.join(OBJ, s + ".o") for s in SOURCES]
-    jobs = [([HIPCC] + FLAGS + ["-c", "-o", o, os.path.join(CSRC, s)], s, verbose)
-            for s, o in zip(SOURCES, objs)]
+    units = []  # (source, extra flags, object)
+    for src in SOURCES:
+        n = PARTS.get(src, 0)
+        if n:
+            units += [(src, [f"-DJF_PART={p}"], os.path.join(OBJ, f"{src}.{p}.o"))
+                      for p in range(1, n + 1)]
+        else:
+            units.append((src, [], os.path.join(OBJ, src + ".o")))
+    objs = [o for _, _, o in units]
+    jobs = [([HIPCC] + FLAGS + extra + ["-c", "-o", o, os.path.join(CSRC, src)],
+             f"{src} {' '.join(extra)}", verbose) for src, extra, o in units]
     workers = min(len(jobs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)))
     with ThreadPoolExecutor(max_workers=max(1, workers)) as pool:
         for f in [pool.submit(_run, *j) for j in jobs]:

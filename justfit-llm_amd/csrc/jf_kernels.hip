@@ -20,6 +20,13 @@
 #include "jf_device.h"
 #include "jf_kernels.h"
 
+// The kernels compile in four parts (JF_PART 1..4, one object each) so the
+// build runs in parallel; JF_PART 0 (the default) compiles all of them.
+#ifndef JF_PART
+#define JF_PART 0
+#endif
+#define JF_IN(p) (JF_PART == 0 || JF_PART == (p))
+
 namespace jf {
 
 template <int DT>
@@ -1782,6 +1789,7 @@ __device__ __forceinline__ void merge_row(const SampleLaunch &a,
 
 // ---- the single-pass selection kernel -------------------------------------
 
+#if JF_IN(1)
 template <int DT>
 __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
   constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
@@ -1925,6 +1933,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
     }
   }
 }
+#endif
 
 // ---- the fast selection kernel ---------------------------------------------
 //
@@ -2093,6 +2102,7 @@ __device__ __forceinline__ uint32_t past_end_bits(uint32_t V, uint32_t base) {
 // those flags, reads penalty table row == its own row and the policy values
 // that follow; otherwise each row reads its flags and penalty row from
 // f.row_info and its policy from f.a.params.
+#if JF_IN(1)
 template <int DT>
 __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     const void *logits, const uint32_t *pen_slots, uint32_t stride, uint32_t V,
@@ -2403,10 +2413,12 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     hdr->floor_key = tk;
   }
 }
+#endif
 
 // One block per row merges the row's chunk summaries (the reduction the
 // reference's last-arriving group does, split_reduce.h:14-45; here the
 // kernel boundary orders the partials before their reader).
+#if JF_IN(2)
 template <int DT>
 __global__ __launch_bounds__(kThreads) void merge_kernel(SampleLaunch a) {
   __shared__ Lds s;
@@ -2414,6 +2426,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(SampleLaunch a) {
   const RowParams rp = a.params[row];
   merge_row<DT>(a, rp, row, s);
 }
+#endif
 
 // ---- the small-K merge -----------------------------------------------------
 //
@@ -2460,9 +2473,11 @@ __device__ __forceinline__ int rank_select(const uint64_t (&v)[PER], uint32_t va
   }
   __syncthreads();
   // Suffix sums: thread t owns bins 4t .. 4t+3; excl(b) counts the items in
-  // the bins above b.
+  // the bins above b. (The scan's barriers order the flag's reset before the
+  // boundary thread sets it.)
   const uint4 c4 = *(const uint4 *)&m.bins[4 * tid];
   const uint32_t own = c4.x + c4.y + c4.z + c4.w;
+  if (tid == 0) s.hit = 0;
   uint64_t total64;
   const uint32_t before = (uint32_t)block_excl_scan_u64(own, s, &total64);
   const uint32_t total = (uint32_t)total64;
@@ -2470,7 +2485,6 @@ __device__ __forceinline__ int rank_select(const uint64_t (&v)[PER], uint32_t va
                  e0 = e1 + c4.y;
   // The boundary bin: where the count from the top reaches K.
   const uint32_t need = min(K, total);
-  if (tid == 0) s.hit = 0;
   uint32_t bstar = 0xffffffffu, bcount = 0;
   if (e3 < need && e3 + c4.w >= need) { bstar = 4 * tid + 3; bcount = c4.w; }
   else if (e2 < need && e2 + c4.z >= need) { bstar = 4 * tid + 2; bcount = c4.z; }
@@ -2579,6 +2593,7 @@ __device__ __forceinline__ void wave_finish(const SampleLaunch &a, const RowPara
 // function cannot reach the kernel's arguments (its kernel-argument segment
 // pointer is null), so the kernel copies the launch record into LDS first;
 // the function works in the kernel's LDS record.
+#if JF_IN(2)
 __shared__ Lds g_small_lds;
 __shared__ SampleLaunch g_small_launch;
 template <int DT>
@@ -2587,10 +2602,12 @@ __device__ __noinline__ void merge_small_general(uint32_t row) {
   const RowParams rp = a.params[row];
   merge_sampled<DT>(a, rp, row, g_small_lds);
 }
+#endif
 
 // The arguments the first loads need lead the signature (14 dwords, no
 // padding): the hardware preloads them into scalar registers at wave launch.
 // They repeat fields of `a` (drafted_rows is 0 when there are no drafts).
+#if JF_IN(2)
 template <int DT>
 __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     const BlockHeader *headers, const uint64_t *cands, const RowParams *params,
@@ -2731,6 +2748,7 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
   __syncthreads();
   merge_small_general<DT>(row);
 }
+#endif
 
 // ---- multi-pass stages ---------------------------------------------------
 
@@ -2849,6 +2867,7 @@ __device__ __forceinline__ uint32_t walk_chunk(const SampleLaunch &a, const RowP
 
 // The stage kernel is compiled once per class of stages, so each launch
 // carries only its stage's code and registers.
+#if JF_IN(3)
 template <int DT, int CLS>
 __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
   constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
@@ -3270,8 +3289,10 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
       break;
   }
 }
+#endif
 
 // The draw inside the chunk the row's last stage chose: one block per row.
+#if JF_IN(3)
 template <int DT>
 __global__ __launch_bounds__(kThreads) void walk_kernel(SampleLaunch a) {
   __shared__ Lds s;
@@ -3290,6 +3311,7 @@ __global__ __launch_bounds__(kThreads) void walk_kernel(SampleLaunch a) {
     a.states[row].stage = a.out_kept_ids ? kStageKeptCount : kStageDone;
   }
 }
+#endif
 
 // Inside one wave's slice of a chunk (64 lanes x VEC consecutive tokens,
 // lane-major): q[e] are the lane's weights in id order and the slice's
@@ -3345,6 +3367,7 @@ constexpr uint32_t kResidualSlot = 63;
 // row instead leaves its mass and draft weight in its state for
 // residual_draw_kernel (the Mass3 stage's hand-over to the Draw stage).
 // Greedy rows take the argmax of the chunk bests in their chunk-0 block.
+#if JF_IN(4)
 template <int DT>
 __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
   constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
@@ -3519,6 +3542,7 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
       write_result(a, row, c * CHUNK + jg * SLAB + tid * VEC + e_hit, 0.0f, 0);
   }
 }
+#endif
 
 // Drafted rows that keep every admitted token: the residual draw over the
 // row (sampling.metal:694-829 with candidate weights max(w - q * mass, 0),
@@ -3526,6 +3550,7 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
 // residual weights per slice; the row's last block draws from the residual
 // weights, or from the plain weights when the residual has no mass, and
 // writes p(draft) = w(draft) / mass (sampling.metal:828-829).
+#if JF_IN(4)
 template <int DT>
 __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a) {
   constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
@@ -3634,6 +3659,7 @@ __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a)
     }
   }
 }
+#endif
 
 // ---- acceptance --------------------------------------------------------
 
@@ -3654,6 +3680,7 @@ __device__ __forceinline__ void finish(const uint32_t *tokens, uint32_t accepted
 
 // decode_accept_dflash (sampling.metal:1399-1423, 1514-1558), one thread per
 // lane.
+#if JF_IN(4)
 __global__ void accept_chain_kernel(AcceptChainLaunch a) {
   const uint32_t lane = blockIdx.x * blockDim.x + threadIdx.x;
   if (lane >= a.lanes) return;
@@ -3687,8 +3714,10 @@ __global__ void accept_chain_kernel(AcceptChainLaunch a) {
   finish(tokens, accepted, lp.remaining, a.stop0, a.stop1, a.retained + lane,
          a.accepted + lane);
 }
+#endif
 
 // verify_tree_accept (tree.metal:20-84), one thread per lane.
+#if JF_IN(4)
 __global__ void accept_tree_kernel(AcceptTreeLaunch a) {
   const uint32_t lane = blockIdx.x * blockDim.x + threadIdx.x;
   if (lane >= a.lanes) return;
@@ -3729,9 +3758,11 @@ __global__ void accept_tree_kernel(AcceptTreeLaunch a) {
   for (uint32_t i = 0; i < 8; ++i)
     a.path_rows[(uint64_t)lane * 8 + i] = i < length ? path[i] : path[length - 1];
 }
+#endif
 
 // ---- launchers -------------------------------------------------------
 
+#if JF_IN(1)
 int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
                   void *start_event, void *stop_event) {
   const dim3 grid(a.rows * a.chunks), block(kThreads);
@@ -3749,7 +3780,9 @@ int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
   }
   return (int)hipGetLastError();
 }
+#endif
 
+#if JF_IN(1)
 int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
                        const RowParams *uniform, void *stream, void *start_event,
                        void *stop_event) {
@@ -3772,7 +3805,9 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
     go(select_fast_kernel<1>);
   return (int)hipGetLastError();
 }
+#endif
 
+#if JF_IN(2)
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream) {
   const dim3 grid(a.rows), block(kThreads);
   if (dtype == 0)
@@ -3781,7 +3816,9 @@ int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream) {
     hipLaunchKernelGGL(merge_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
+#endif
 
+#if JF_IN(4)
 int launch_mass_draw(const SampleLaunch &a, uint32_t dtype, void *stream) {
   const dim3 grid(a.rows * a.chunks), block(kThreads);
   if (dtype == 0)
@@ -3790,7 +3827,9 @@ int launch_mass_draw(const SampleLaunch &a, uint32_t dtype, void *stream) {
     hipLaunchKernelGGL(mass_draw_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
+#endif
 
+#if JF_IN(4)
 int launch_residual_draw(const SampleLaunch &a, uint32_t dtype, void *stream) {
   const dim3 grid(a.rows * a.chunks), block(kThreads);
   if (dtype == 0)
@@ -3799,7 +3838,9 @@ int launch_residual_draw(const SampleLaunch &a, uint32_t dtype, void *stream) {
     hipLaunchKernelGGL(residual_draw_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
+#endif
 
+#if JF_IN(2)
 int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream) {
   const dim3 grid(a.rows), block(kThreads);
   const hipStream_t st = (hipStream_t)stream;
@@ -3815,7 +3856,9 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream) {
     go(merge_small_kernel<1>);
   return (int)hipGetLastError();
 }
+#endif
 
+#if JF_IN(3)
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream) {
   const dim3 grid(a.rows * a.chunks), block(kThreads);
   const hipStream_t st = (hipStream_t)stream;
@@ -3849,17 +3892,22 @@ int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream) {
 #undef JF_STAGE_CASE
   return (int)hipGetLastError();
 }
+#endif
 
+#if JF_IN(4)
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream) {
   const dim3 grid((a.lanes + 63) / 64), block(64);
   hipLaunchKernelGGL(accept_chain_kernel, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
+#endif
 
+#if JF_IN(4)
 int launch_accept_tree(const AcceptTreeLaunch &a, void *stream) {
   const dim3 grid((a.lanes + 63) / 64), block(64);
   hipLaunchKernelGGL(accept_tree_kernel, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
+#endif
 
 }  // namespace jf
