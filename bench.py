@@ -155,6 +155,7 @@ class GpuStep:
             extra["draft_tokens"] = torch.from_numpy(draft.view(np.int32)).to(dev)
             self.q = [torch.from_numpy(c["q"]).to(dev) for _ in range(len(self.copies))]
             extra["out_draft_probs"] = torch.zeros(rows, dtype=torch.float32, device=dev)
+        self.draft_probs = extra.get("out_draft_probs")
         self.out = torch.zeros(rows, dtype=torch.int32, device=dev)
         for i in range(len(self.copies)):
             kw = dict(extra)

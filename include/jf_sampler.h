@@ -197,6 +197,22 @@ typedef struct jf_sample_args {
    * Both NULL records nothing. */
   void *select_start_event;
   void *select_done_event;
+  /* Optional per-row addressing (host arrays of `rows` entries, or NULL for
+   * the linear forms above), so that one call covers every lane of a verify
+   * batch as the reference's one dispatch set does (Sampling.cpp:149-172;
+   * row addressing sampling.metal:52-70, 912-913):
+   *   mask_rows[r]          row r's mask is masks + mask_rows[r] * mask_stride
+   *   draft_token_index[r]  row r's draft token is draft_tokens[index], or
+   *                         JF_NO_TOKEN for an undrafted row (replaces
+   *                         drafted_rows)
+   *   draft_cand_index[r]   its draft distribution: draft_cand_ids/probs +
+   *                         index * JF_DRAFT_CANDIDATES, or dense row index
+   *   extra_offsets[r]      its extra tokens start at extra_tokens + offset
+   *                         (replaces r * extra_stride) */
+  const uint32_t *mask_rows;
+  const uint32_t *draft_token_index;
+  const uint32_t *draft_cand_index;
+  const uint64_t *extra_offsets;
 } jf_sample_args;
 
 int jf_sample(jf_sampler *sampler, const jf_sample_args *args, void *stream);

@@ -24,7 +24,13 @@ struct RowParams {
   float frequency;
   uint32_t penalty_row;
   uint32_t extra_count;
-  uint32_t reserved[5];
+  uint32_t extra_offset;      // the row's extra tokens: SampleLaunch::extra + this
+  uint32_t draft_index;       // its draft token: draft_tokens[draft_index]
+                              // (kNoToken: not drafted)
+  uint32_t cand_index;        // its draft distribution: sparse candidates
+                              // cand_ids/probs + 16 * this, dense q row this
+  uint32_t mask_row;          // its constraint mask: masks + this * mask_stride
+  uint32_t reserved;
 };
 static_assert(sizeof(RowParams) == 64, "row params are 64 bytes");
 
@@ -107,6 +113,8 @@ struct SampleLaunch {
   uint32_t all_sampled;   // every row of the launch is sampled
   uint32_t uncut_rows;    // mixed launch: merges skip sampled rows with no
                           // cut, mass_draw_kernel draws only those
+  uint32_t row_indexed;   // drafts are addressed through RowParams'
+                          // draft_index/cand_index, not the row number
   const uint2 *pen_entries;
   const uint32_t *pen_offsets;
   uint32_t pen_max_entries;

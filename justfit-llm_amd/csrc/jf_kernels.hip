@@ -349,7 +349,7 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
   const bool constrained = (rp.flags & kRowConstrained) != 0;
   uint32_t mwords[LOADS];
   if (constrained) {
-    const uint32_t *mrow = a.masks + (uint64_t)row * a.mask_stride;
+    const uint32_t *mrow = a.masks + (uint64_t)rp.mask_row * a.mask_stride;
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const uint32_t t0 = lane_base + j * SLAB;
@@ -384,7 +384,7 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
         p.xbits[i] = 0;
       }
     }
-    if (tid < nx) p.extras[tid] = a.extra[(uint64_t)row * a.extra_stride + tid];
+    if (tid < nx) p.extras[tid] = a.extra[(uint64_t)rp.extra_offset + tid];
     const uint32_t prow = rp.penalty_row;
     const uint32_t *offs = a.pen_offsets + (uint64_t)prow * (a.pen_buckets + 1);
     const uint32_t b0 = base / kPenaltyBucket;
@@ -459,7 +459,7 @@ __device__ __forceinline__ void load_chunk(const SampleLaunch &a,
       // The first round's tokens stay with their entries' threads (value
       // and admission computed there); the lanes holding them drop them.
       static_assert(EPT == kSideEntries, "one side entry per prefetched entry");
-      const uint32_t *mrow = a.masks + (uint64_t)row * a.mask_stride;
+      const uint32_t *mrow = a.masks + (uint64_t)rp.mask_row * a.mask_stride;
 #pragma unroll
       for (int k = 0; k < EPT; ++k) {
         const uint32_t e = tid + k * kThreads;
@@ -630,10 +630,9 @@ __device__ __forceinline__ float row_uniform(const SampleLaunch &a,
 }
 
 // The draft token a row's draw corrects, or kNoToken.
-__device__ __forceinline__ uint32_t row_draft(const SampleLaunch &a,
-                                              uint32_t row) {
-  return (a.draft_tokens && row < a.drafted_rows) ? a.draft_tokens[row]
-                                                   : kNoToken;
+__device__ __forceinline__ uint32_t row_draft(const SampleLaunch &a, const RowParams &rp) {
+  return (a.draft_tokens && rp.draft_index != kNoToken) ? a.draft_tokens[rp.draft_index]
+                                                        : kNoToken;
 }
 
 // The draft's probability of `token` for a drafted row: its dense q, or
@@ -647,20 +646,21 @@ __device__ __forceinline__ bool uncut_row(const RowParams &rp) {
 }
 
 template <class L>
-__device__ __forceinline__ float draft_q(const SampleLaunch &a, uint32_t row,
+__device__ __forceinline__ float draft_q(const SampleLaunch &a, const RowParams &rp,
                                          uint32_t token, const L &s) {
-  if (a.dense_q) return a.dense_q[(uint64_t)row * a.q_stride + token];
+  if (a.dense_q) return a.dense_q[(uint64_t)rp.cand_index * a.q_stride + token];
   for (int j = 0; j < 16; ++j)
     if (s.cids[j] == token) return s.cprobs[j];
   return 0.0f;
 }
 template <class L>
 __device__ __forceinline__ void stage_candidates(const SampleLaunch &a,
-                                                 uint32_t row, L &s) {
+                                                 const RowParams &rp, L &s) {
   if (threadIdx.x < 16) {
-    const bool sparse = !a.dense_q && row_draft(a, row) != kNoToken;
-    s.cids[threadIdx.x] = sparse ? a.cand_ids[(uint64_t)row * 16 + threadIdx.x] : kNoToken;
-    s.cprobs[threadIdx.x] = sparse ? a.cand_probs[(uint64_t)row * 16 + threadIdx.x] : 0.0f;
+    const bool sparse = !a.dense_q && row_draft(a, rp) != kNoToken;
+    const uint64_t c = (uint64_t)rp.cand_index * 16 + threadIdx.x;
+    s.cids[threadIdx.x] = sparse ? a.cand_ids[c] : kNoToken;
+    s.cprobs[threadIdx.x] = sparse ? a.cand_probs[c] : 0.0f;
   }
   __syncthreads();
 }
@@ -777,8 +777,9 @@ __device__ __forceinline__ void lds_topp(Lds &s, uint32_t n, float maximum, floa
 
 // The draw over the flagged items in id order (sampling.metal:694-829) and
 // the row's outputs.
-__device__ __forceinline__ void lds_draw(const SampleLaunch &a, uint32_t row, Lds &s,
-                         uint32_t n, float maximum, float inv_t) {
+__device__ __forceinline__ void lds_draw(const SampleLaunch &a, const RowParams &rp,
+                                         uint32_t row, Lds &s, uint32_t n, float maximum,
+                                         float inv_t) {
   MergeLds &m = s.merge;
   const ItemRange r = my_items(n);
   uint64_t mloc = 0;
@@ -810,7 +811,7 @@ __device__ __forceinline__ void lds_draw(const SampleLaunch &a, uint32_t row, Ld
     if (threadIdx.x == 0) write_result(a, row, kNoToken, 0.0f, (uint32_t)kept_total);
     return;
   }
-  const uint32_t draft = row_draft(a, row);
+  const uint32_t draft = row_draft(a, rp);
   const bool drafted = draft != kNoToken;
   uint64_t dloc = 0;
   uint32_t any = 0;
@@ -819,7 +820,7 @@ __device__ __forceinline__ void lds_draw(const SampleLaunch &a, uint32_t row, Ld
       if (m.fl[i]) {
         const uint64_t wq =
             quantize(weight_of(key_logit(m.key[i]), maximum, inv_t));
-        const uint64_t d = residual_of(wq, mass3, draft_q(a, row, m.id[i], s));
+        const uint64_t d = residual_of(wq, mass3, draft_q(a, rp, m.id[i], s));
         dloc += d;
         any |= d > 0;
       }
@@ -841,7 +842,7 @@ __device__ __forceinline__ void lds_draw(const SampleLaunch &a, uint32_t row, Ld
       if (!m.fl[i]) continue;
       const uint64_t wq =
           quantize(weight_of(key_logit(m.key[i]), maximum, inv_t));
-      run += residual ? residual_of(wq, mass3, draft_q(a, row, m.id[i], s)) : wq;
+      run += residual ? residual_of(wq, mass3, draft_q(a, rp, m.id[i], s)) : wq;
       if (run > target) {
         s.hit = m.id[i];
         break;
@@ -917,11 +918,11 @@ __device__ __forceinline__ void small_merge(const SampleLaunch &a,
     if (t == 0) write_result(a, row, kNoToken, 0.0f, n3);
     return;
   }
-  const uint32_t draft = row_draft(a, row);
+  const uint32_t draft = row_draft(a, rp);
   const bool drafted = draft != kNoToken;
   uint64_t d = kept ? wq : 0;
   if (drafted) {
-    const uint64_t r = kept ? residual_of(wq, mass3, draft_q(a, row, id, s)) : 0;
+    const uint64_t r = kept ? residual_of(wq, mass3, draft_q(a, rp, id, s)) : 0;
     if (block_max_u32(r > 0 ? 1u : 0u, s)) d = r;
   }
   // The draw weights in id order, their running sum, the first past u.
@@ -1028,7 +1029,7 @@ __device__ __forceinline__ void wave_merge(const SampleLaunch &a,
   const bool drafted = draft != kNoToken;
   uint64_t d = kept ? wq : 0;
   if (drafted) {
-    const uint64_t r = kept ? residual_of(wq, mass3, draft_q(a, row, id, s)) : 0;
+    const uint64_t r = kept ? residual_of(wq, mass3, draft_q(a, rp, id, s)) : 0;
     if (ballot(r > 0)) d = r;
   }
   const uint64_t fm = ballot(drafted && kept && id == draft);
@@ -1454,7 +1455,7 @@ __device__ __forceinline__ void begin_stages(const SampleLaunch &a, const RowPar
     st.thr_key = 0;
     st.stage = (rp.flags & kRowTopP) ? kStageMass2 : kStageMass3;
   }
-  st.drafted = row_draft(a, row) != kNoToken ? 1u : 0u;
+  st.drafted = row_draft(a, rp) != kNoToken ? 1u : 0u;
   a.states[row] = st;
 }
 
@@ -1468,7 +1469,7 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
   // sparse candidates. The select kernel's writes are visible here because
   // it ended before this launch began.
   const float u = row_uniform(a, row);
-  const uint32_t draft = row_draft(a, row);
+  const uint32_t draft = row_draft(a, rp);
   // Rows with a small top-k also fetch the first P slots of every chunk's
   // candidate list now, before the counts are known (S * P <= SPEC items).
   constexpr int SPEC = 10;
@@ -1487,8 +1488,8 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
   for (uint32_t b = tid; b < 1024; b += kThreads) s.merge.bins[b] = 0;
   if (tid < 16) {
     const bool sparse = !a.dense_q && draft != kNoToken;
-    s.cids[tid] = sparse ? a.cand_ids[(uint64_t)row * 16 + tid] : kNoToken;
-    s.cprobs[tid] = sparse ? a.cand_probs[(uint64_t)row * 16 + tid] : 0.0f;
+    s.cids[tid] = sparse ? a.cand_ids[(uint64_t)rp.cand_index * 16 + tid] : kNoToken;
+    s.cprobs[tid] = sparse ? a.cand_probs[(uint64_t)rp.cand_index * 16 + tid] : 0.0f;
   }
   if (tid < 64) {
     float hm = -3.402823466e38f;
@@ -1592,7 +1593,7 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
         lds_sort_by_id(s, n);
         lds_topk(s, n, K);
         if (rp.flags & kRowTopP) lds_topp(s, n, maximum, rp.inv_t, rp.top_p);
-        lds_draw(a, row, s, n, maximum, rp.inv_t);
+        lds_draw(a, rp, row, s, n, maximum, rp.inv_t);
         return;
       }
       if (tid < 64) wave_merge(a, rp, row, s, n, maximum, u, draft);
@@ -1731,7 +1732,7 @@ __device__ __forceinline__ void merge_sampled(const SampleLaunch &a, const RowPa
   lds_sort_by_id(s, n);
   if (K < n) lds_topk(s, n, K);
   if (rp.flags & kRowTopP) lds_topp(s, n, maximum, rp.inv_t, rp.top_p);
-  lds_draw(a, row, s, n, maximum, rp.inv_t);
+  lds_draw(a, rp, row, s, n, maximum, rp.inv_t);
 }
 
 // Every thread's device-coherent stores complete, then one arrival; true in
@@ -2668,9 +2669,9 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     asm volatile("" : "+v"(a2));
     ubits = *(GlobalU32 *)a2;
   }
-  const uint32_t draft = has_draft ? draft_raw : kNoToken;
-  const uint32_t cid = has_draft && tid < 16 ? cid_raw : kNoToken;
-  const float cpr = has_draft && tid < 16 ? cpr_raw : 0.0f;
+  uint32_t draft = has_draft ? draft_raw : kNoToken;
+  uint32_t cid = has_draft && tid < 16 ? cid_raw : kNoToken;
+  float cpr = has_draft && tid < 16 ? cpr_raw : 0.0f;
   const bool hv = tid < S;
   const float hmax = hv ? u2f(h0.x) : -3.402823466e38f;
   const float hbest = hv ? u2f(h1.x) : -__builtin_inff();
@@ -2682,6 +2683,15 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     s.merge.key[1024 + b] = 0;
   }
   const RowParams rp = wait_row_policy(prr);
+  if (a.row_indexed) {
+    // Drafts addressed through the row's record (a batch of verify lanes):
+    // their loads wait for the policy (the launch passed drafted_rows 0).
+    draft = row_draft(a, rp);
+    if (draft != kNoToken && tid < 16) {
+      cid = a.cand_ids[(uint64_t)rp.cand_index * 16 + tid];
+      cpr = a.cand_probs[(uint64_t)rp.cand_index * 16 + tid];
+    }
+  }
   if (uncut_rows && uncut_row(rp)) {
     // mass_draw_kernel draws it.
     if (tid == 0) a.states[row].stage = kStageDone;
@@ -2755,13 +2765,13 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
 // A drafted row's dense q over this thread's tokens of a chunk, in the
 // order of the chunk's logits; 16-byte loads when the rows are aligned.
 template <int DT>
-__device__ __forceinline__ void load_dense_q(const SampleLaunch &a, uint32_t row,
+__device__ __forceinline__ void load_dense_q(const SampleLaunch &a, const RowParams &rp,
                                              uint32_t chunk,
                                              float (&qv)[Geo<DT>::TPL]) {
   constexpr int VEC = Geo<DT>::VEC, SLAB = Geo<DT>::SLAB, LOADS = Geo<DT>::LOADS;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
   const uint32_t lane_base = chunk * CHUNK + threadIdx.x * VEC;
-  const float *q = a.dense_q + (uint64_t)row * a.q_stride;
+  const float *q = a.dense_q + (uint64_t)rp.cand_index * a.q_stride;
   if (a.q_aligned && chunk * CHUNK + CHUNK <= a.vocabulary) {
 #pragma unroll
     for (int j = 0; j < LOADS; ++j)
@@ -2802,7 +2812,7 @@ __device__ __forceinline__ uint32_t walk_chunk(const SampleLaunch &a, const RowP
   // A dense draft row is requested ahead of the chunk's logits.
   const bool dq = residual && a.dense_q;
   float qv[TPL];
-  if (dq) load_dense_q<DT>(a, row, c, qv);
+  if (dq) load_dense_q<DT>(a, rp, c, qv);
   float xs[TPL];
   load_chunk<DT>(a, rp, row, c, s, xs);
   const uint32_t lane_base = c * CHUNK + threadIdx.x * VEC;
@@ -2815,7 +2825,7 @@ __device__ __forceinline__ uint32_t walk_chunk(const SampleLaunch &a, const RowP
     const uint32_t k = logit_key(v);
     if (k < thr_key || !at_or_before(k, t, bkey, bid)) return 0;
     const uint64_t wq = quantize(weight_of(v, M, inv_t));
-    return residual ? residual_of(wq, mass3, dq ? q : draft_q(a, row, t, s)) : wq;
+    return residual ? residual_of(wq, mass3, dq ? q : draft_q(a, rp, t, s)) : wq;
   };
   uint64_t lsum[LOADS], offs[LOADS];
 #pragma unroll
@@ -2889,10 +2899,10 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
   // The draw stage's dense q is requested ahead of the chunk's logits.
   float qv[CLS == kClsDraw ? TPL : 1];
   if constexpr (CLS == kClsDraw)
-    if (a.dense_q) load_dense_q<DT>(a, row, chunk, qv);
+    if (a.dense_q) load_dense_q<DT>(a, rp, chunk, qv);
   float xs[TPL];
   load_chunk<DT>(a, rp, row, chunk, s, xs);
-  stage_candidates(a, row, s);
+  stage_candidates(a, rp, s);
   const uint32_t lane_base = chunk * CHUNK + tid * VEC;
   const float M = st.maximum, inv_t = rp.inv_t;
   // Members: admitted (non-NaN), at or above the min-p floor, at or before
@@ -2907,7 +2917,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
     if (k >= st.thr_key && at_or_before(k, t, st.bkey, st.bid)) mem |= 1ull << i;
   }
   StagePartial *part = a.partials + (uint64_t)row * S + chunk;
-  const uint32_t draft = row_draft(a, row);
+  const uint32_t draft = row_draft(a, rp);
 
   auto wq_of = [&](int i) -> uint64_t {
     return quantize(weight_of(xs[i], M, inv_t));
@@ -3026,7 +3036,7 @@ __global__ __launch_bounds__(kThreads) void stage_kernel(SampleLaunch a) {
           const uint64_t wq = wq_of(i);
           wsum += wq;
           if (st.drafted) {
-            const float q = a.dense_q ? qv[i] : draft_q(a, row, tok_of(i), s);
+            const float q = a.dense_q ? qv[i] : draft_q(a, rp, tok_of(i), s);
             const uint64_t d = residual_of(wq, st.mass3, q);
             dsum += d;
             any |= d > 0;
@@ -3300,7 +3310,7 @@ __global__ __launch_bounds__(kThreads) void walk_kernel(SampleLaunch a) {
   const RowParams rp = a.params[row];
   const RowState st = a.states[row];
   if (st.stage != kStageWalk) return;
-  stage_candidates(a, row, s);
+  stage_candidates(a, rp, s);
   const uint32_t hit = walk_chunk<DT>(a, rp, row, st.chunk, st.maximum, st.thr_key,
                                       st.bkey, st.bid, st.residual != 0, st.mass3,
                                       st.within, s);
@@ -3396,7 +3406,7 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
     hm = hb[lane].maximum;
     ha = hb[lane].admitted;
   }
-  const uint32_t draft = row_draft(a, row);
+  const uint32_t draft = row_draft(a, rp);
   if (!all_sampled && !(rp.flags & kRowSampled)) {
     // Greedy (sampling.metal:1478-1512): the largest chunk best, the lowest
     // id among equals.
@@ -3564,10 +3574,10 @@ __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a)
   if (st.stage != kStageDraw) return;
   const RowParams rp = a.params[row];
   float qv[TPL];
-  if (a.dense_q) load_dense_q<DT>(a, row, chunk, qv);
+  if (a.dense_q) load_dense_q<DT>(a, rp, chunk, qv);
   float xs[TPL];
   load_chunk<DT>(a, rp, row, chunk, s, xs);
-  stage_candidates(a, row, s);
+  stage_candidates(a, rp, s);
   const float u = row_uniform(a, row);
   const float M = st.maximum, inv_t = rp.inv_t;
   const uint64_t mass3 = st.mass3;
@@ -3580,7 +3590,7 @@ __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       const int i = j * VEC + e;
-      const float q = a.dense_q ? qv[i] : draft_q(a, row, lane_base + j * SLAB + e, s);
+      const float q = a.dense_q ? qv[i] : draft_q(a, rp, lane_base + j * SLAB + e, s);
       lv[j] += residual_of(quantized_weight(xs[i], M, inv_t), mass3, q);
     }
   }
@@ -3649,7 +3659,7 @@ __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a)
       const uint64_t wq = quantized_weight(x, M, inv_t);
       // Past the vocabulary (a partial last chunk) the weight is zero and
       // no q is read: a dense q row ends at the vocabulary.
-      const float qe = tbase + e < a.vocabulary ? draft_q(a, row, tbase + e, s) : 0.0f;
+      const float qe = tbase + e < a.vocabulary ? draft_q(a, rp, tbase + e, s) : 0.0f;
       q[e] = residual ? residual_of(wq, mass3, qe) : wq;
     }
     uint32_t e_hit;
@@ -3848,7 +3858,7 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream) {
     hipLaunchKernelGGL(kernel, grid, block, 0, st, a.headers, (const uint64_t *)a.cands,
                        a.params, a.uniforms, a.uniform_index, a.chunks,
                        (uint32_t)a.uniform_offset, (uint32_t)a.uniform_stride,
-                       a.draft_tokens ? a.drafted_rows : 0u, a.uncut_rows, a);
+                       a.draft_tokens && !a.row_indexed ? a.drafted_rows : 0u, a.uncut_rows, a);
   };
   if (dtype == 0)
     go(merge_small_kernel<0>);

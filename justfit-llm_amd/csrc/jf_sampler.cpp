@@ -488,7 +488,8 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
     return fail(JF_ERR_INVALID_ARGUMENT,
                 "kept outputs need ids, probabilities, counts and a capacity");
   const uint32_t W = (V + 31) / 32;
-  bool any_constrained = false, any_sampled = false, staged = false;
+  bool any_constrained = false, any_sampled = false, staged = false, any_drafted = false;
+  const bool row_indexed = a->draft_token_index || a->draft_cand_index;
   bool need_count1 = false, need_topk = false, need_topp = false;
   for (uint32_t r = 0; r < rows; ++r) {
     const jf_policy &p = a->policies[r];
@@ -521,6 +522,17 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
     }
     if (p.flags & JF_POLICY_EXCLUDE_STOP) rp.flags |= jf::kRowExcludeStop;
     rp.penalty_row = JF_NO_TOKEN;
+    rp.mask_row = a->mask_rows ? a->mask_rows[r] : r;
+    rp.draft_index = a->draft_token_index ? a->draft_token_index[r]
+                     : (a->draft_tokens && r < a->drafted_rows) ? r
+                                                                : JF_NO_TOKEN;
+    rp.cand_index = a->draft_cand_index ? a->draft_cand_index[r] : r;
+    const uint64_t extra_offset =
+        a->extra_offsets ? a->extra_offsets[r] : (uint64_t)r * a->extra_stride;
+    if (extra_offset > 0xffffffffull)
+      return fail(JF_ERR_INVALID_ARGUMENT, "extra token offset exceeds 32 bits");
+    rp.extra_offset = (uint32_t)extra_offset;
+    if (rp.draft_index != JF_NO_TOKEN) any_drafted = true;
     const uint32_t extra = a->extra_counts ? a->extra_counts[r] : 0u;
     if (extra > (uint32_t)jf::kMaxExtra)
       return fail(JF_ERR_INVALID_ARGUMENT, "more than 16 extra penalty tokens in a row");
@@ -545,8 +557,9 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
     return fail(JF_ERR_INVALID_ARGUMENT, "constraint mask buffer is missing or short");
   if (any_sampled && !a->uniforms)
     return fail(JF_ERR_INVALID_ARGUMENT, "sampling uniforms are null");
-  if (a->draft_tokens && a->drafted_rows && !a->draft_q &&
-      (!a->draft_cand_ids || !a->draft_cand_probs))
+  if (any_drafted && !a->draft_tokens)
+    return fail(JF_ERR_INVALID_ARGUMENT, "drafted rows need draft tokens");
+  if (any_drafted && !a->draft_q && (!a->draft_cand_ids || !a->draft_cand_probs))
     return fail(JF_ERR_INVALID_ARGUMENT, "drafted rows need draft probabilities");
 
   rc = upload(upload_ctx, params, rows, sc.params, stream);
@@ -578,7 +591,10 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   L.uniform_offset = a->uniform_offset;
   L.uniform_stride = a->uniform_stride;
   L.draft_tokens = a->draft_tokens;
-  L.drafted_rows = a->draft_tokens ? a->drafted_rows : 0u;
+  // drafted_rows: nonzero when any row is drafted; the merges' early loads
+  // use it as the linear prefix unless the rows are indexed.
+  L.drafted_rows = !any_drafted ? 0u : row_indexed ? rows : a->drafted_rows;
+  L.row_indexed = row_indexed ? 1u : 0u;
   L.cand_ids = a->draft_cand_ids;
   L.cand_probs = a->draft_cand_probs;
   L.dense_q = a->draft_q;
@@ -604,7 +620,8 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   // The fast selection kernel takes the launch when every row qualifies:
   // aligned rows, no extra verify tokens, and penalty rows whose chunks fit
   // their fixed slots (and vocabularies of at least one 16-byte vector).
-  bool fast = aligned && V >= 8 && L.stride <= 0xffffffffull;
+  bool fast = aligned && V >= 8 && L.stride <= 0xffffffffull &&
+              !(a->mask_rows && any_constrained);
   for (uint32_t r = 0; fast && r < rows; ++r) {
     const jf::RowParams &rp = params[r];
     if (rp.extra_count) fast = false;

@@ -60,9 +60,33 @@ Sampling::Sampling(uint32_t vocabulary, uint32_t maximumLanes)
   if (!vocabulary) throw std::invalid_argument("invalid sampling geometry");
   if (!maximumLanes) throw std::invalid_argument("invalid sampling batch width");
   check(jf_sampler_create(vocabulary, maximumLanes * 16, &sampler_));
+  // Row r of lane l draws slot l * 40 + 24 + r (tree) or l * 40 + 15
+  // (the correction), Sampling.h:19-29.
+  const size_t per = (size_t)maximumLanes * 16;
+  std::vector<uint32_t> index(4 * per);
+  for (uint32_t t = 0; t < 4; ++t) {
+    const bool tree = t & 1u;
+    const uint32_t rows = (t & 2u) ? 16u : 8u;
+    for (uint32_t l = 0; l < maximumLanes; ++l)
+      for (uint32_t r = 0; r < rows; ++r)
+        index[t * per + l * rows + r] =
+            l * JF_SAMPLING_UNIFORMS + (tree ? JF_UNIFORM_TREE_DRAWS + r : JF_UNIFORM_CORRECTION);
+  }
+  hipError_t e = hipMalloc((void **)&uniformIndex_, index.size() * sizeof(uint32_t));
+  if (e == hipSuccess)
+    e = hipMemcpy(uniformIndex_, index.data(), index.size() * sizeof(uint32_t),
+                  hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(uniformIndex_);
+    jf_sampler_destroy(sampler_);
+    throw std::runtime_error(std::string("uniform index table: ") + hipGetErrorString(e));
+  }
 }
 
-Sampling::~Sampling() { jf_sampler_destroy(sampler_); }
+Sampling::~Sampling() {
+  (void)hipFree(uniformIndex_);
+  jf_sampler_destroy(sampler_);
+}
 
 void Sampling::rebuildPenaltyWords(std::span<uint32_t> words,
                                    std::span<const uint32_t> history,
@@ -171,43 +195,59 @@ void Sampling::addVerify(hipStream_t stream,
                    (l * (rows - 1) + drafted) * (uint64_t)JF_DRAFT_CANDIDATES * sizeof(float),
                    "draft probability");
     }
-    const jf_policy p = toPolicy(policy);
-    std::vector<jf_policy> ps(rows, p);
+  }
+  // One selection over every row of every lane (the reference's one
+  // dispatch set): row g = l * rows + r reads logits row g, mask row
+  // l * (rows + 1) + 1 + r, input rows 1..r of its lane as extra penalty
+  // tokens, draft token input row r + 1 with candidates l * (rows - 1) + r
+  // below the drafted rows, and its lane's correction or tree uniform.
+  const uint32_t total = (uint32_t)lanes * rows;
+  std::vector<jf_policy> ps(total);
+  std::vector<uint32_t> penaltyRows(total), extra(total), maskRows(total),
+      draftIndex(total), candIndex(total);
+  std::vector<uint64_t> extraOffsets(total);
+  for (uint32_t l = 0; l < lanes; ++l) {
+    const jf_policy p = toPolicy(policies[l]);
     const uint32_t penaltyRow =
         l < penalties.rows.size() ? penalties.rows[l] : JF_NO_TOKEN;
-    std::vector<uint32_t> penaltyRows(rows, penaltyRow);
-    std::vector<uint32_t> extra(rows);
-    for (uint32_t r = 0; r < rows; ++r) extra[r] = r;  // input rows 1..r
-    const uint32_t *inputs = (const uint32_t *)buffers.inputTokens.data + (uint64_t)l * rows;
-    jf_sample_args a{};
-    a.rows = rows;
-    a.dtype = JF_DTYPE_F32;
-    a.logits = (const float *)buffers.logits.data + (uint64_t)l * rows * vocabulary_;
-    a.logits_stride = vocabulary_;
-    a.masks = (const uint32_t *)buffers.constraintMasks.data +
-              ((uint64_t)l * (rows + 1) + 1) * maskWords_;
-    a.mask_stride = maskWords_;
-    a.policies = ps.data();
-    a.stop_token_0 = stopToken0;
-    a.stop_token_1 = stopToken1;
-    a.penalties = penalties.words;
-    a.penalty_rows = penaltyRows.data();
-    a.extra_tokens = inputs + 1;
-    a.extra_counts = extra.data();
-    a.extra_stride = 0;
-    a.uniforms = (const float *)buffers.uniforms.data + (uint64_t)l * JF_SAMPLING_UNIFORMS;
-    a.uniform_offset = tree ? JF_UNIFORM_TREE_DRAWS : JF_UNIFORM_CORRECTION;
-    a.uniform_stride = tree ? 1 : 0;
-    a.draft_tokens = inputs + 1;
-    a.drafted_rows = drafted;
-    a.draft_cand_ids = (const uint32_t *)buffers.draftCandidates.data +
-                       (uint64_t)l * (rows - 1) * JF_DRAFT_CANDIDATES;
-    a.draft_cand_probs = (const float *)buffers.draftProbabilities.data +
-                         (uint64_t)l * (rows - 1) * JF_DRAFT_CANDIDATES;
-    a.out_tokens = (uint32_t *)buffers.outputTokens.data + (uint64_t)l * rows;
-    a.out_draft_probs = (float *)buffers.targetProbabilities.data + (uint64_t)l * rows;
-    check(jf_sample(sampler_, &a, stream));
+    for (uint32_t r = 0; r < rows; ++r) {
+      const uint32_t g = l * rows + r;
+      ps[g] = p;
+      penaltyRows[g] = penaltyRow;
+      extra[g] = r;
+      extraOffsets[g] = (uint64_t)l * rows + 1;
+      maskRows[g] = l * (rows + 1) + 1 + r;
+      draftIndex[g] = r < drafted ? l * rows + r + 1 : JF_NO_TOKEN;
+      candIndex[g] = l * (rows - 1) + r;
+    }
   }
+  const uint32_t table = (tree ? 1u : 0u) | (rows == 16 ? 2u : 0u);
+  jf_sample_args a{};
+  a.rows = total;
+  a.dtype = JF_DTYPE_F32;
+  a.logits = buffers.logits.data;
+  a.logits_stride = vocabulary_;
+  a.masks = (const uint32_t *)buffers.constraintMasks.data;
+  a.mask_stride = maskWords_;
+  a.mask_rows = maskRows.data();
+  a.policies = ps.data();
+  a.stop_token_0 = stopToken0;
+  a.stop_token_1 = stopToken1;
+  a.penalties = penalties.words;
+  a.penalty_rows = penaltyRows.data();
+  a.extra_tokens = (const uint32_t *)buffers.inputTokens.data;
+  a.extra_counts = extra.data();
+  a.extra_offsets = extraOffsets.data();
+  a.uniforms = (const float *)buffers.uniforms.data;
+  a.uniform_index = uniformIndex_ + (size_t)table * maximumLanes_ * 16;
+  a.draft_tokens = (const uint32_t *)buffers.inputTokens.data;
+  a.draft_token_index = draftIndex.data();
+  a.draft_cand_ids = (const uint32_t *)buffers.draftCandidates.data;
+  a.draft_cand_probs = (const float *)buffers.draftProbabilities.data;
+  a.draft_cand_index = candIndex.data();
+  a.out_tokens = (uint32_t *)buffers.outputTokens.data;
+  a.out_draft_probs = (float *)buffers.targetProbabilities.data;
+  check(jf_sample(sampler_, &a, stream));
 }
 
 // Sampling.cpp:278-328

@@ -129,6 +129,9 @@ class Sampling final {
   uint32_t maskWords_ = 0;
   uint32_t maximumLanes_ = 0;
   jf_sampler *sampler_ = nullptr;
+  // Each verify row's uniform slot (device): four tables of maximumLanes * 16
+  // entries, by (tree draws or the correction slot) x (8 or 16 rows).
+  uint32_t *uniformIndex_ = nullptr;
 };
 
 }  // namespace justfit::hip

@@ -68,7 +68,10 @@ class JfSampleArgs(ctypes.Structure):
         ("out_draft_probs", c_vp), ("out_kept_counts", c_vp),
         ("out_kept_ids", c_vp), ("out_kept_probs", c_vp),
         ("kept_capacity", c_u32), ("select_start_event", c_vp),
-        ("select_done_event", c_vp),
+        ("select_done_event", c_vp), ("mask_rows", ctypes.POINTER(c_u32)),
+        ("draft_token_index", ctypes.POINTER(c_u32)),
+        ("draft_cand_index", ctypes.POINTER(c_u32)),
+        ("extra_offsets", ctypes.POINTER(c_u64)),
     ]
 
 
@@ -326,7 +329,8 @@ class Sampler:
                     extra_stride=0, uniforms=None, uniform_index=None,
                     uniform_offset=0, uniform_stride=1, draft_tokens=None,
                     drafted_rows=None, cand_ids=None, cand_probs=None,
-                    dense_q=None, out_draft_probs=None, kept=None):
+                    dense_q=None, out_draft_probs=None, kept=None, mask_rows=None,
+                    draft_token_index=None, draft_cand_index=None, extra_offsets=None):
         """Builds a JfSampleArgs (kept-alive host arrays ride along)."""
         import torch
         rows = logits.shape[0]
@@ -377,6 +381,14 @@ class Sampler:
             a.out_kept_ids = ids.data_ptr()
             a.out_kept_probs = probs.data_ptr()
             a.kept_capacity = ids.shape[1]
+        for name, values, ctype in (("mask_rows", mask_rows, c_u32),
+                                    ("draft_token_index", draft_token_index, c_u32),
+                                    ("draft_cand_index", draft_cand_index, c_u32),
+                                    ("extra_offsets", extra_offsets, c_u64)):
+            if values is not None:
+                arr = (ctype * rows)(*[int(v) for v in values])
+                setattr(a, name, arr)
+                keep.append(arr)
         return a, keep
 
     def sample(self, *args, **kwargs):

@@ -5,6 +5,8 @@
 //                         deterministic inputs (tests/test_cpp_mirror.py
 //                         rebuilds the same inputs and checks the results
 //                         against the CPU oracle)
+//   sampling_mirror verify16  the widest verify step: 4 lanes x 16 rows at
+//                         V = 248,320 (one selection call), then acceptance
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -242,11 +244,128 @@ int gpu_checks() {
   return failures ? 1 : 0;
 }
 
+// The engine's widest verify step: 4 lanes x 16 rows at V = 248,320, two
+// lanes penalized (their verify rows count input rows 1..r on top of the
+// table), sparse drafts; addVerify (correction uniform) and addVerify with
+// tree draws (uniform 24 + r), then addAcceptance of the first. Inputs are
+// restated in tests/test_cpp_mirror.py.
+constexpr uint32_t V16 = 248320;
+float logit16(uint32_t row, uint32_t t) {
+  return (float)(((t * 48271ull + row * 16807ull) % 10007ull) / 1000.0 - 5.0);
+}
+
+int gpu_verify16() {
+  VerifyShapeScope shape(16);
+  const uint32_t rows = activeVerifyRows();
+  const uint32_t lanes = 4;
+  Sampling sampling(V16, lanes);
+  hipStream_t stream;
+  hip(hipStreamCreate(&stream));
+  std::vector<float> logits((size_t)lanes * rows * V16);
+  for (uint32_t r = 0; r < lanes * rows; ++r)
+    for (uint32_t t = 0; t < V16; ++t) logits[(size_t)r * V16 + t] = logit16(r, t);
+  std::vector<float> uniforms(lanes * JF_SAMPLING_UNIFORMS);
+  for (uint32_t l = 0; l < lanes; ++l)
+    for (uint32_t s = 0; s < JF_SAMPLING_UNIFORMS; ++s)
+      uniforms[l * JF_SAMPLING_UNIFORMS + s] = uniform(l, s);
+  std::vector<uint32_t> inputs((size_t)lanes * rows);
+  for (uint32_t i = 0; i < lanes * rows; ++i) inputs[i] = (i * 7717u + 3u) % V16;
+  std::vector<uint32_t> cands((size_t)lanes * (rows - 1) * 16);
+  std::vector<float> cprobs(cands.size());
+  for (uint32_t l = 0; l < lanes; ++l)
+    for (uint32_t r = 0; r + 1 < rows; ++r)
+      for (uint32_t j = 0; j < 16; ++j) {
+        const size_t k = ((size_t)l * (rows - 1) + r) * 16 + j;
+        cands[k] = j ? (r * 5303u + j * 9721u + l) % V16 : inputs[l * rows + r + 1];
+        cprobs[k] = j ? 0.01f : 0.6f;
+      }
+  jf_penalty_table *table = nullptr;
+  if (jf_penalty_table_create(V16, lanes, 4096, &table) != JF_OK)
+    throw std::runtime_error(jf_last_error());
+  // Table row 1 for lane 0, row 3 for lane 2 (lanes 1 and 3 unpenalized).
+  for (uint32_t t = 1; t < 4; t += 2) {
+    std::vector<uint32_t> history(1500);
+    for (uint32_t i = 0; i < history.size(); ++i) history[i] = (i * 131071u + t * 977u) % V16;
+    for (uint32_t i = 0; i < 40; ++i) history[1000 + i] = inputs[(t == 1 ? 0 : 2) * rows + 1 + (i % 5)];
+    if (jf_penalty_table_rebuild(table, t, history.data(), history.size(), 700, 0, 0, 1,
+                                 stream) != JF_OK)
+      throw std::runtime_error(jf_last_error());
+  }
+  const std::vector<uint32_t> stateLanes{1, JF_NO_TOKEN, 3, JF_NO_TOKEN};
+  SamplingBuffers b;
+  b.logits = upload(logits);
+  b.uniforms = upload(uniforms);
+  b.inputTokens = upload(inputs);
+  b.draftCandidates = upload(cands);
+  b.draftProbabilities = upload(cprobs);
+  b.outputTokens = upload(std::vector<uint32_t>((size_t)lanes * rows, 0));
+  b.targetProbabilities = upload(std::vector<float>((size_t)lanes * rows, 0.0f));
+  SamplingPolicy penalized;
+  penalized.temperature = 0.9f;
+  penalized.topK = 40;
+  penalized.topP = 0.92f;
+  penalized.penalties.repetition = 1.15f;
+  penalized.penalties.presence = 0.4f;
+  penalized.penalties.frequency = 0.25f;
+  SamplingPolicy plain;
+  plain.temperature = 0.7f;
+  plain.topK = 20;
+  SamplingPolicy greedy;
+  const std::vector<SamplingPolicy> policies{penalized, plain, penalized, greedy};
+  sampling.addVerify(stream, policies, b, JF_NO_TOKEN, JF_NO_TOKEN,
+                     PenaltyTable{table, stateLanes});
+  hip(hipStreamSynchronize(stream));
+  const std::vector<uint32_t> verifyTokens = download<uint32_t>(b.outputTokens);
+  const std::vector<float> verifyProbs = download<float>(b.targetProbabilities);
+  AcceptanceBuffers ab;
+  std::vector<uint32_t> proposed((size_t)lanes * (rows - 1));
+  for (uint32_t l = 0; l < lanes; ++l)
+    for (uint32_t r = 0; r + 1 < rows; ++r) proposed[l * (rows - 1) + r] = inputs[l * rows + r + 1];
+  ab.proposedTokens = upload(proposed);
+  ab.candidates = b.draftCandidates;
+  ab.proposalProbabilities = b.draftProbabilities;
+  ab.targetProbabilities = b.targetProbabilities;
+  ab.uniforms = b.uniforms;
+  ab.outputTokens = b.outputTokens;
+  ab.retainedCounts = upload(std::vector<uint32_t>(lanes, 0));
+  ab.acceptedCounts = upload(std::vector<uint32_t>(lanes, 0));
+  const std::vector<uint32_t> maximumRetained{16, 9, 12, 16};
+  sampling.addAcceptance(stream, ab, maximumRetained, policies, JF_NO_TOKEN, JF_NO_TOKEN);
+  hip(hipStreamSynchronize(stream));
+  const std::vector<uint32_t> accepted = download<uint32_t>(ab.outputTokens);
+  const std::vector<uint32_t> retained = download<uint32_t>(ab.retainedCounts);
+  const std::vector<uint32_t> acceptedCounts = download<uint32_t>(ab.acceptedCounts);
+  // The tree form: row r draws its own uniform 24 + r; the first 7 rows
+  // carry drafts.
+  sampling.addVerify(stream, policies, b, JF_NO_TOKEN, JF_NO_TOKEN,
+                     PenaltyTable{table, stateLanes}, true);
+  hip(hipStreamSynchronize(stream));
+  const std::vector<uint32_t> treeTokens = download<uint32_t>(b.outputTokens);
+  const std::vector<float> treeProbs = download<float>(b.targetProbabilities);
+  std::printf("{\n");
+  print_u32("verify_tokens", verifyTokens);
+  print_f32("verify_probs_bits", verifyProbs);
+  print_u32("accepted_tokens", accepted);
+  print_u32("retained", retained);
+  print_u32("accepted", acceptedCounts);
+  print_u32("tree_tokens", treeTokens);
+  print_f32("tree_probs_bits", treeProbs);
+  std::printf("\"gpu_failures\": %d\n}\n", failures);
+  jf_penalty_table_destroy(table);
+  for (DeviceBuffer *d : {&b.logits, &b.uniforms, &b.inputTokens, &b.draftCandidates,
+                          &b.draftProbabilities, &b.outputTokens, &b.targetProbabilities,
+                          &ab.proposedTokens, &ab.retainedCounts, &ab.acceptedCounts})
+    hip(hipFree(d->data));
+  hip(hipStreamDestroy(stream));
+  return failures ? 1 : 0;
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
   const std::string mode = argc > 1 ? argv[1] : "cpu";
   try {
+    if (mode == "verify16") return gpu_verify16();
     return mode == "gpu" ? gpu_checks() : cpu_checks();
   } catch (const std::exception &e) {
     std::fprintf(stderr, "error: %s\n", e.what());

@@ -99,3 +99,90 @@ def test_mirror_selection_and_acceptance_on_gpu():
             uniforms40=uniforms(l))
         np.testing.assert_array_equal(np.array(got["accepted_tokens"][l * ROWS:(l + 1) * ROWS], np.uint32), tt)
         assert got["retained"][l] == ret and got["accepted"][l] == acc, (l, ret, acc)
+
+
+# ---- the widest verify step (sampling_mirror verify16) ------------------------
+
+V16, ROWS16, LANES16 = 248320, 16, 4
+
+
+def logits16():
+    r = np.arange(LANES16 * ROWS16, dtype=np.uint64)[:, None]
+    t = np.arange(V16, dtype=np.uint64)[None, :]
+    return (((t * 48271 + r * 16807) % 10007) / 1000.0 - 5.0).astype(np.float32)
+
+
+def inputs16():
+    i = np.arange(LANES16 * ROWS16, dtype=np.uint64)
+    return ((i * 7717 + 3) % V16).astype(np.uint32)
+
+
+def candidates16():
+    inp = inputs16()
+    c = np.zeros((LANES16, ROWS16 - 1, 16), np.uint32)
+    p = np.full((LANES16, ROWS16 - 1, 16), 0.01, np.float32)
+    for l in range(LANES16):
+        for r in range(ROWS16 - 1):
+            for j in range(16):
+                c[l, r, j] = inp[l * ROWS16 + r + 1] if j == 0 else (r * 5303 + j * 9721 + l) % V16
+            p[l, r, 0] = 0.6
+    return c, p
+
+
+def history16(t):
+    inp = inputs16()
+    h = ((np.arange(1500, dtype=np.uint64) * 131071 + t * 977) % V16).astype(np.uint32)
+    lane = 0 if t == 1 else 2
+    for i in range(40):
+        h[1000 + i] = inp[lane * ROWS16 + 1 + (i % 5)]
+    return h
+
+
+@pytest.mark.gpu
+def test_mirror_verify_4_lanes_16_rows_one_call():
+    """addVerify over 4 lanes x 16 rows at V = 248,320 in one selection call
+    (per-row mask, draft, candidate and extra-token addressing), with two
+    penalized lanes counting their verify inputs, sparse drafts, the
+    correction uniform and the tree uniforms; then addAcceptance. Bit-exact
+    against the oracle row by row (Sampling.cpp:149-172, 278-328)."""
+    got = run("verify16")
+    assert got["gpu_failures"] == 0
+    x = logits16()
+    inp = inputs16()
+    cand, cprob = candidates16()
+    words = {0: O.rebuild_penalty_words(V16, history16(1), 700, None, True)[1],
+             2: O.rebuild_penalty_words(V16, history16(3), 700, None, True)[1]}
+    pols = [O.policy(temperature=0.9, top_k=40, top_p=0.92, repetition=1.15, presence=0.4,
+                     frequency=0.25),
+            O.policy(temperature=0.7, top_k=20), None, O.policy()]
+    pols[2] = pols[0]
+    for tree, key in ((False, "verify"), (True, "tree")):
+        drafted_rows = 7 if tree else ROWS16 - 1
+        vt = np.zeros(LANES16 * ROWS16, np.uint32)
+        vp = np.zeros(LANES16 * ROWS16, np.float32)
+        for l in range(LANES16):
+            u = uniforms(l)
+            for r in range(ROWS16):
+                g = l * ROWS16 + r
+                drafted = r < drafted_rows
+                t, dp = O.select_row(
+                    V16, pols[l], logits=x[g], words=words.get(l),
+                    extra=inp[l * ROWS16 + 1:l * ROWS16 + 1 + r] if l in words else None,
+                    uniform=float(u[24 + r] if tree else u[15]),
+                    draft_token=int(inp[g + 1]) if drafted else NO,
+                    cand_ids=cand[l, r] if drafted else None,
+                    cand_probs=cprob[l, r] if drafted else None)[:2]
+                vt[g], vp[g] = t, dp
+        np.testing.assert_array_equal(np.array(got[f"{key}_tokens"], np.uint32), vt, err_msg=key)
+        np.testing.assert_array_equal(np.array(got[f"{key}_probs_bits"], np.uint32),
+                                      vp.view(np.uint32), err_msg=key)
+        if tree:
+            continue
+        for l, remaining in enumerate([16, 9, 12, 16]):
+            sl = slice(l * ROWS16, (l + 1) * ROWS16)
+            tt, ret, acc = O.accept_chain(
+                ROWS16 - 1, remaining, pols[l].temperature > 0, inp[l * ROWS16 + 1:(l + 1) * ROWS16],
+                vt[sl], cand_ids=cand[l], cand_probs=cprob[l], target_draft_prob=vp[sl],
+                uniforms40=uniforms(l))
+            np.testing.assert_array_equal(np.array(got["accepted_tokens"][sl], np.uint32), tt)
+            assert got["retained"][l] == ret and got["accepted"][l] == acc, (l, ret, acc)

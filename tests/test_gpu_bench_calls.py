@@ -1,0 +1,69 @@
+"""The calls bench.py times, checked at full size: bench.GpuStep builds the
+same device inputs, penalty tables and argument records as the timed loop,
+and one of its steps is compared with the oracle row by row (bit-exact
+tokens, and the draft probabilities where the step writes them). C2 and C5
+run as benchmarked, without kept outputs or draft probabilities; C1, C3 and
+C4 greedy and sampled as the bench issues them."""
+import numpy as np
+import pytest
+
+import bench
+from harness import NO, run_oracle
+from jf_sampler import workloads as WL
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_for(w):
+    """The oracle's results for the inputs GpuStep puts on the device."""
+    kw = {}
+    if "logits" in w:
+        kw["logits"] = w["logits"]
+    else:
+        kw["logits_bf16"] = w["logits_bf16"]
+    if "histories" in w:
+        kw.update(histories=w["histories"], generated=w["generated"],
+                  mark_prompt=[w["mark_prompt"]] * w["rows"])
+    if "masks" in w:
+        kw["masks"] = w["masks"]
+    u = w.get("uniforms")
+    if u is not None:
+        if u.ndim == 2:  # C4: row k * 16 + r draws slot 24 + r of request k
+            per = w["rows"] // u.shape[0]
+            u = np.array([u[k, 24 + r] for k in range(u.shape[0]) for r in range(per)],
+                         np.float32)
+        kw["uniforms"] = u
+    if w.get("tree") is not None and w.get("sampled"):
+        c = w["tree"]
+        draft = np.full(w["rows"], NO, np.uint32)
+        for k, parent in enumerate(c["trees"]):
+            for r in range(WL.chain_length(parent) - 1):
+                draft[k * 16 + r] = c["tokens"][k][r + 1]
+        kw.update(draft_tokens=draft, dense_q=c["q"])
+    return run_oracle(w["V"], w["policies"], **kw)
+
+
+@pytest.mark.parametrize("cfg,mode", [(2, "auto"), (5, "auto"), (1, "auto"), (3, "greedy"),
+                                      (3, "sampled"), (4, "greedy"), (4, "sampled")])
+def test_benchmarked_step_matches_oracle(cfg, mode):
+    import torch
+    w = bench.build_workload(cfg, mode)
+    print(f"bench call: {w['name']}", flush=True)
+    g = bench.GpuStep(w)
+    for i in (0, len(g.kw) - 1):  # the first and last rotated copy
+        g.out.fill_(-1)
+        g.step(i)
+        torch.cuda.synchronize()
+        got = g.out.cpu().numpy().view(np.uint32).copy()
+        want = _oracle_for(w) if i == 0 else want
+        np.testing.assert_array_equal(got, want["tokens"])
+        assert np.all(got != NO)
+        if g.draft_probs is not None:
+            c = w["tree"]
+            drafted = np.array([r < WL.chain_length(c["trees"][k]) - 1
+                                for k in range(len(c["trees"])) for r in range(16)])
+            assert drafted.any()
+            dp = g.draft_probs.cpu().numpy()
+            np.testing.assert_array_equal(dp[drafted], want["draft_probs"][drafted])
+    del g
+    torch.cuda.empty_cache()
