@@ -37,7 +37,7 @@ def parse():
                          "of one KV-like tensor family after C4's tree acceptance")
     ap.add_argument("--mode", default="auto",
                     help="C3/C4: greedy or sampled (auto: sampled)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="bound of the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -115,7 +115,7 @@ def build_workload(cfg, mode):
 class GpuStep:
     """Device-resident inputs (rotated copies) and one jf_sample per step."""
 
-    def __init__(self, w):
+    def __init__(self, w, count_headroom=0):
         import torch
         import jf_sampler as J
         self.w = w
@@ -161,7 +161,7 @@ class GpuStep:
             kw = dict(extra)
             if "histories" in w:
                 H = max(len(h) for h in w["histories"])
-                t = J.PenaltyTable(V, rows, H + 8)
+                t = J.PenaltyTable(V, rows, H + 8 + count_headroom)
                 for r, h in enumerate(w["histories"]):
                     t.rebuild(r, h, w["generated"][r], None, w["mark_prompt"])
                 self.tables.append(t)
@@ -225,13 +225,86 @@ def time_select(g, first, steps):
     return float(us.mean()), float(np.percentile(us, 50))
 
 
+def time_with_counts(g, steps):
+    """Steps each followed by the engine's commit of one token per row into
+    the penalty table (jf_penalty_table_count_rows: an in-place device update
+    on the same stream, no upload). The tokens are a fixed synthetic
+    sequence; each step's table is the one its input copy reads."""
+    import torch
+    rows = g.w["rows"]
+    rng = np.random.default_rng(99)
+    idx = np.arange(rows, dtype=np.uint32)
+    toks = rng.integers(0, g.w["V"], (steps, rows), dtype=np.uint32)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for i in range(steps):
+        g.step(i)
+        g.tables[i % len(g.tables)].count_rows(idx, toks[i])
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    per = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]) * 1000.0
+    return {"ms_per_step": ev[0].elapsed_time(ev[steps]) / steps,
+            "p50_us": float(np.percentile(per, 50)),
+            "note": "each step followed by jf_penalty_table_count_rows of one token per row"}
+
+
+def time_cpp_loop(g, steps, with_counts):
+    """The same calls issued from C++ (libjf_bench_loop.so): GPU and host
+    microseconds per step without the Python loop, optionally with the
+    per-step penalty count."""
+    import ctypes
+    import jf_sampler as J
+    J.lib()  # the sampler library first: one HIP runtime in the process
+    L = ctypes.CDLL(os.path.join(REPO, "justfit-llm_amd", "jf_sampler", "libjf_bench_loop.so"))
+    vp, u32 = ctypes.c_void_p, ctypes.c_uint32
+    L.jf_bench_sample_loop.argtypes = [vp, vp, u32, u32, vp, vp, vp, u32, vp,
+                                       ctypes.POINTER(ctypes.c_double),
+                                       ctypes.POINTER(ctypes.c_double)]
+    n = len(g.kw)
+    arr = (J.JfSampleArgs * n)(*[a for a, _ in g.kw])
+    rows = g.w["rows"]
+    tables = idx = toks = None
+    if with_counts:
+        tables = (vp * n)(*[t.handle.value for t in g.tables])
+        idx = np.arange(rows, dtype=np.uint32)
+        toks = np.random.default_rng(98).integers(0, g.w["V"], (steps, rows), dtype=np.uint32)
+    gpu, host = ctypes.c_double(), ctypes.c_double()
+    rc = L.jf_bench_sample_loop(g.sampler.handle, ctypes.cast(arr, vp), n, steps, tables,
+                                None if idx is None else idx.ctypes.data_as(vp),
+                                None if toks is None else toks.ctypes.data_as(vp), rows,
+                                J._stream(), ctypes.byref(gpu), ctypes.byref(host))
+    if rc:
+        raise RuntimeError(f"C++ timing loop failed: {rc} {J.lib().jf_last_error().decode()}")
+    return {"us_per_step": gpu.value, "host_us_per_call": host.value}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w, seconds):
-    """The oracle (a C restatement, -O2, pthreads over rows) on a bounded
-    sample of the same workload: whole steps until `seconds` elapse."""
+    """The oracle (a C restatement, pthreads over rows) built here with -O3
+    -march=native, timed step by step: 3 warm-up steps, then the median of
+    up to 20 timed steps (fewer when 20 would pass `seconds`). Its tokens
+    must equal the -O2 checker build's on the same step."""
+    import tempfile
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
+    if w.get("tree") is not None and w.get("sampled"):
+        return None  # the dense-residual draw is not in the batch driver
     V, rows = w["V"], w["rows"]
-    threads = min(16, os.cpu_count() or 1)
+    # The pool's CPU share for one GPU is 16 cores, whatever the affinity shows.
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    native_dir = tempfile.mkdtemp(prefix="jf_oracle_native_")
+    L = O.native_lib(native_dir)
     pols = [O.policy_from(p) for p in w["policies"]]
     words, pen_rows = None, None
     if "histories" in w:
@@ -244,21 +317,34 @@ def cpu_baseline(w, seconds):
     u = w.get("uniforms")
     if u is not None and u.ndim == 2:
         u = None
-    if w.get("tree") is not None and w.get("sampled"):
-        return None  # the dense-residual draw is not in the batch driver
-    steps = 0
+
+    def step(library):
+        return O.select_batch(V, pols, lg, is_bf16=is_bf16, masks=w.get("masks"),
+                              words=words, pen_rows=pen_rows, uniforms=u,
+                              threads=threads, library=library)[0]
+
+    want = step(None)
+    for _ in range(3):
+        got = step(L)
+    if not np.array_equal(got, want):
+        raise RuntimeError("the -O3 -march=native oracle build disagrees with the checker build")
+    times = []
     t0 = time.perf_counter()
-    while True:
-        O.select_batch(V, pols, lg, is_bf16=is_bf16, masks=w.get("masks"), words=words,
-                       pen_rows=pen_rows, uniforms=u, threads=threads)
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
+    while len(times) < 20:
+        t = time.perf_counter()
+        step(L)
+        times.append(time.perf_counter() - t)
+        if time.perf_counter() - t0 >= seconds and len(times) >= 5:
             break
-    return dict(value=steps / el, unit="steps/s", cores=threads, kind="port",
-                sample=f"{steps} full steps ({rows} rows each) of the same seeded "
-                       f"workload in {el:.1f} s, oracle/jf_oracle.c -O2, "
-                       f"{threads} threads over rows")
+    med = float(np.median(times))
+    model = cpu_model()
+    return dict(value=1.0 / med, unit="steps/s", cores=threads, kind="port",
+                cpu_model=model,
+                sample=f"median of {len(times)} timed full steps ({rows} rows each, after "
+                       f"3 warm-ups) of the same seeded workload: {med * 1e3:.1f} ms/step; "
+                       f"oracle/jf_oracle.c built with -O3 -march=native "
+                       f"-ffp-contract=off on this host ({model}), {threads} threads "
+                       f"over rows; tokens equal to the -O2 checker build's")
 
 
 def read_traffic(cfg):
@@ -485,7 +571,7 @@ def main():
         return
     w = build_workload(args.config, args.mode)
     print(f"# {w['name']}: building inputs", file=sys.stderr, flush=True)
-    g = GpuStep(w)
+    g = GpuStep(w, count_headroom=args.steps)
     for i in range(args.warmup):
         g.step(i)
     torch.cuda.synchronize()
@@ -510,6 +596,10 @@ def main():
     # uniforms and outputs are a few hundred bytes).
     sel_mean, sel_p50 = time_select(g, args.warmup + K, K)
     achieved = w["select_bytes"] / (sel_mean * 1e-6) / 1e9
+    counted = time_with_counts(g, K) if g.tables else None
+    cpp = {"loop": time_cpp_loop(g, K, False)}
+    if g.tables:
+        cpp["loop_with_penalty_count"] = time_cpp_loop(g, K, True)
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
     traffic, kernel = read_traffic(args.config)
     line = {
@@ -539,6 +629,8 @@ def main():
                      "algorithmic_bytes": w["select_bytes"],
                      "step_achieved": step_gbs,
                      "step_frac": step_gbs / PEAK_HBM_GBS},
+        "with_penalty_count": counted,
+        "cpp_loop": cpp,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -116,11 +116,21 @@ int jf_penalty_table_rebuild(jf_penalty_table *table, uint32_t row,
                              uint64_t generated_tokens, int has_pending,
                              uint32_t pending_token, int mark_prompt,
                              void *stream);
-/* countPenaltyTokens into table row `row` (host tokens); uploads on
- * `stream`. */
+/* countPenaltyTokens (Sampling.cpp:75-80) of `count` host tokens into table
+ * row `row`, in order; Runtime.cpp:1397-1406 (commitSelected) is the call
+ * site it serves. The table is updated in place on `stream` by a kernel
+ * whose updates travel as kernel arguments: no upload of the row and no wait
+ * on earlier work. All-or-nothing: a token outside the vocabulary, or new
+ * tokens beyond the row's max_entries, fail before the row changes. */
 int jf_penalty_table_count(jf_penalty_table *table, uint32_t row,
                            const uint32_t *selected, uint64_t count,
                            void *stream);
+/* The same for one step's commits of every lane at once: pair i counts
+ * token selected[i] into row rows[i] (rows may repeat; each row's tokens
+ * apply in order). One launch per 32 tokens. */
+int jf_penalty_table_count_rows(jf_penalty_table *table, const uint32_t *rows,
+                                const uint32_t *selected, uint64_t count,
+                                void *stream);
 
 /* ---- uniforms --------------------------------------------------------- */
 

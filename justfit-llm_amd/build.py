@@ -17,7 +17,8 @@ OBJ = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "jf_sampler", "libjf_sampler.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["jf_kernels.hip", "jf_draft.hip", "jf_gather.hip", "jf_noalloc.hip", "jf_sampler.cpp",
+SOURCES = ["jf_kernels.hip", "jf_draft.hip", "jf_gather.hip", "jf_noalloc.hip", "jf_penalty.hip",
+           "jf_sampler.cpp", "jf_host.cpp",
            "jf_tree.cpp", "jf_mask_wire.cpp", "sampling.cpp"]
 # jf_kernels.hip compiles as four objects (its JF_PART sections), in parallel.
 PARTS = {"jf_kernels.hip": 4}
@@ -40,6 +41,9 @@ FLAGS = [
     "-I" + CSRC,
 ]
 NOISE = "'-packed-fp32-ops' is not a recognized feature"
+
+
+BENCH_LOOP = os.path.join(os.path.dirname(OUT), "libjf_bench_loop.so")
 
 
 def _run(cmd, what, verbose):
@@ -75,6 +79,14 @@ def build(verbose: bool = True) -> str:
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs,
          "link libjf_sampler.so", verbose)
     os.replace(tmp, OUT)
+    # bench.py's C++ timing loop, a separate library over libjf_sampler.so.
+    loop_obj = os.path.join(OBJ, "jf_bench_loop.cpp.o")
+    _run([HIPCC] + FLAGS + ["-c", "-o", loop_obj, os.path.join(CSRC, "jf_bench_loop.cpp")],
+         "jf_bench_loop.cpp", verbose)
+    tmp = BENCH_LOOP + ".tmp"
+    _run([HIPCC, "-shared", "-fPIC", "-o", tmp, loop_obj, "-L" + os.path.dirname(OUT),
+          "-ljf_sampler", "-Wl,-rpath,$ORIGIN"], "link libjf_bench_loop.so", verbose)
+    os.replace(tmp, BENCH_LOOP)
     return OUT
 
 

@@ -5,6 +5,8 @@
 
 #include <stdint.h>
 
+#include "jf_host.h"
+
 struct jf_sample_args;
 
 namespace jf {
@@ -89,7 +91,6 @@ struct StagePartial {
 // Geometry of one selection launch.
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kPenaltyBucket = 2048;
 constexpr int kBlockCandidates = 1024;
 constexpr int kMergeCapacity = 2048;
 constexpr int kPenaltyWordsLds = 2048;
@@ -153,9 +154,6 @@ struct SampleLaunch {
 // prompt bit << 18 | count (< 2^18); an empty slot is 0 (every real entry
 // has a count or the prompt bit).
 constexpr int kKernargRows = 256;
-constexpr uint32_t kSlotCountMask = 0x3ffffu;
-constexpr uint32_t kSlotPromptBit = 0x40000u;
-constexpr int kSlotOffsetShift = 19;
 struct FastLaunch {
   SampleLaunch a;
   const uint32_t *pen_slots;  // [table rows][chunks][slot_count]
@@ -358,5 +356,38 @@ int launch_draft_select(const DraftLaunch &d, bool aligned, void *stream,
 // jf_gather.hip; vec8: 8 columns per thread with 16-byte accesses.
 int launch_tree_gather(const GatherLaunch &g, bool vec8, void *stream,
                        void *start_event = nullptr, void *stop_event = nullptr);
+
+// The device penalty table as penalty_count_kernel updates it.
+struct PenaltyTableView {
+  PenaltyEntry *entries;  // [rows][max_entries]
+  uint32_t *offsets;      // [rows][buckets + 1]
+  uint32_t *slots;        // [rows][chunks][slot_count]
+  uint32_t max_entries;
+  uint32_t buckets;
+  uint32_t chunks;
+  uint32_t slot_count;
+};
+
+// Up to kPenaltyOps counted tokens (PenaltyOp, packed), in call order within
+// each row; block g applies ops [group_start[g], group_start[g + 1]) to
+// table row group_row[g].
+constexpr uint32_t kPenaltyOps = 64;
+struct PackedPenaltyOp {
+  uint32_t token;
+  uint32_t word;
+  uint32_t index;       // entry index | insert << 31
+  uint32_t entries;     // the row's entry count before the op
+  uint32_t slot_value;
+  uint32_t slot;        // slot index | the chunk's used slots << 16; 0xffff: no slot
+};
+struct PenaltyOpBatch {
+  PackedPenaltyOp op[kPenaltyOps];
+  uint32_t group_row[kPenaltyOps];
+  uint32_t group_start[kPenaltyOps + 1];
+};
+static_assert(sizeof(PenaltyOpBatch) <= 2560, "penalty updates travel as kernel arguments");
+
+int launch_penalty_count(const PenaltyTableView &t, const PenaltyOpBatch &b, uint32_t groups,
+                         void *stream);
 
 }  // namespace jf

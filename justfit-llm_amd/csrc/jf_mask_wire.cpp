@@ -7,12 +7,11 @@
 // the payload, every integer little-endian. Host code.
 #include "jf_sampler.h"
 
+#include "jf_host.h"
+
 #include <cstring>
 #include <string>
 
-namespace jf {
-int set_error(int code, const char *message);  // jf_sampler.cpp
-}
 
 namespace {
 

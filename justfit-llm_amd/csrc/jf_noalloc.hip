@@ -14,9 +14,6 @@
 
 #include "jf_kernels.h"
 
-namespace jf {
-int set_error(int code, const char *message);  // jf_sampler.cpp
-}
 
 namespace {
 

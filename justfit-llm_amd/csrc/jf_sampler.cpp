@@ -14,16 +14,12 @@
 #include <utility>
 #include <vector>
 
+#include "jf_host.h"
 #include "jf_kernels.h"
 
 namespace {
 
-thread_local std::string g_error;
-
-int fail(int code, std::string message) {
-  g_error = std::move(message);
-  return code;
-}
+int fail(int code, const std::string &message) { return jf::set_error(code, message); }
 
 int hip_fail(hipError_t e, const char *what) {
   return fail(JF_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
@@ -113,11 +109,6 @@ uint32_t effective_top_k(const jf_policy &p, uint32_t vocabulary) {
 
 }  // namespace
 
-namespace jf {
-// For the library's other host sources (jf_tree.cpp).
-int set_error(int code, const char *message) { return fail(code, message); }
-}  // namespace jf
-
 struct jf_penalty_table {
   uint32_t vocabulary = 0;
   uint32_t rows = 0;
@@ -127,13 +118,13 @@ struct jf_penalty_table {
   uint2 *entries = nullptr;    // [rows][max_entries] {token, word}
   uint32_t *offsets = nullptr; // [rows][buckets + 1]
   // The fast kernel's fixed slots: [rows][chunks][slot_count], 8192-token
-  // chunks; fits[row] when every chunk of the row fits its slots and every
-  // count fits the slot's 18 bits (otherwise select_kernel takes the row).
+  // chunks; host.fits(row) when every chunk of the row fits its slots and
+  // every count fits the slot's 18 bits (otherwise select_kernel takes the
+  // row).
   uint32_t chunks = 0;
   uint32_t slot_count = 0;
   uint32_t *slots = nullptr;
-  std::vector<uint8_t> fits;
-  std::vector<std::vector<std::pair<uint32_t, uint32_t>>> host;
+  jf::PenaltyRows host;  // the rows as the device holds them
   StagingRing staging;
 };
 
@@ -157,26 +148,6 @@ struct jf_sampler {
 };
 
 extern "C" {
-
-const char *jf_last_error(void) { return g_error.c_str(); }
-
-int jf_policy_validate(const jf_policy *p) {
-  if (!p) return fail(JF_ERR_INVALID_ARGUMENT, "policy is null");
-  const bool temperature_valid =
-      p->temperature == 0.0f ||
-      (std::isfinite(p->temperature) && p->temperature >= FLT_MIN);
-  if (!temperature_valid || !(p->top_p > 0.0f && p->top_p <= 1.0f) ||
-      !(p->min_p >= 0.0f) || p->min_p > 1.0f)
-    return fail(JF_ERR_INVALID_ARGUMENT,
-                "sampling requires temperature 0 or at least FLT_MIN, top_p "
-                "in (0,1] and min_p in [0,1]");
-  if (!(std::fabs(p->presence) <= 2.0f) || !(std::fabs(p->frequency) <= 2.0f) ||
-      !std::isfinite(p->repetition) || p->repetition <= 0.0f)
-    return fail(JF_ERR_INVALID_ARGUMENT,
-                "sampling requires presence and frequency penalties in [-2,2] "
-                "and a positive repetition penalty");
-  return JF_OK;
-}
 
 // ---- sampler -------------------------------------------------------------
 
@@ -261,39 +232,6 @@ static int check_device(int device) {
 
 // ---- penalties -------------------------------------------------------------
 
-int jf_penalty_words_rebuild(uint32_t *words, uint32_t vocabulary,
-                             const uint32_t *history, uint64_t history_len,
-                             uint64_t generated, int has_pending,
-                             uint32_t pending, int mark_prompt) {
-  if (history_len <= generated)
-    return fail(JF_ERR_LOGIC, "request history holds no prompt");
-  if ((!words && vocabulary) || (!history && history_len))
-    return fail(JF_ERR_INVALID_ARGUMENT, "null buffer");
-  for (uint64_t i = 0; i < history_len; ++i)
-    if (history[i] >= vocabulary)
-      return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
-  if (has_pending && pending >= vocabulary)
-    return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
-  const uint64_t prompt = history_len - generated;
-  std::fill(words, words + vocabulary, 0u);
-  if (mark_prompt)
-    for (uint64_t i = 0; i < prompt; ++i) words[history[i]] |= JF_PENALTY_PROMPT_BIT;
-  for (uint64_t i = prompt; i < history_len; ++i) ++words[history[i]];
-  if (has_pending) ++words[pending];
-  return JF_OK;
-}
-
-int jf_penalty_words_count(uint32_t *words, uint32_t vocabulary,
-                           const uint32_t *selected, uint64_t count) {
-  if ((!selected && count) || (!words && vocabulary))
-    return fail(JF_ERR_INVALID_ARGUMENT, "null buffer");
-  for (uint64_t i = 0; i < count; ++i)
-    if (selected[i] >= vocabulary)
-      return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
-  for (uint64_t i = 0; i < count; ++i) ++words[selected[i]];
-  return JF_OK;
-}
-
 int jf_penalty_table_destroy(jf_penalty_table *t) {
   if (!t) return JF_OK;
   t->staging.release();
@@ -308,7 +246,7 @@ int jf_penalty_table_create(uint32_t vocabulary, uint32_t rows,
                             uint32_t max_entries, jf_penalty_table **out) {
   if (!out) return fail(JF_ERR_INVALID_ARGUMENT, "output pointer is null");
   *out = nullptr;
-  if (!vocabulary || !rows || !max_entries)
+  if (!vocabulary || !rows || !max_entries || max_entries > 0x7fffffffu)
     return fail(JF_ERR_INVALID_ARGUMENT, "invalid penalty table geometry");
   jf_penalty_table *t = new (std::nothrow) jf_penalty_table;
   if (!t) return fail(JF_ERR_NO_MEMORY, "penalty table allocation failed");
@@ -321,8 +259,7 @@ int jf_penalty_table_create(uint32_t vocabulary, uint32_t rows,
   t->slot_count = (uint64_t)max_entries * 3 / 2 <= (uint64_t)t->chunks * jf::kThreads
                       ? (uint32_t)jf::kThreads
                       : 2u * jf::kThreads;
-  t->fits.assign(rows, 1);
-  t->host.resize(rows);
+  t->host.init(vocabulary, rows, max_entries, t->slot_count);
   int rc = JF_OK;
   hipError_t ge = hipGetDevice(&t->device);
   if (ge != hipSuccess) rc = hip_fail(ge, "hipGetDevice");
@@ -345,43 +282,24 @@ int jf_penalty_table_create(uint32_t vocabulary, uint32_t rows,
   return JF_OK;
 }
 
+// The whole row as the host copy holds it: entries, bucket offsets, and
+// the fixed slots when the row fits them.
 static int upload_penalty_row(jf_penalty_table *t, uint32_t row, void *stream) {
-  const auto &h = t->host[row];
-  std::vector<uint8_t> blob(h.size() * sizeof(uint2) +
-                            (t->buckets + 1) * sizeof(uint32_t));
-  uint2 *ent = (uint2 *)blob.data();
-  uint32_t *off = (uint32_t *)(blob.data() + h.size() * sizeof(uint2));
-  uint32_t bucket = 0;
-  for (size_t i = 0; i < h.size(); ++i) {
-    ent[i] = make_uint2(h[i].first, h[i].second);
-    while (bucket <= h[i].first / jf::kPenaltyBucket) off[bucket++] = (uint32_t)i;
-  }
-  while (bucket <= t->buckets) off[bucket++] = (uint32_t)h.size();
+  const uint32_t n = t->host.size(row);
+  std::vector<uint8_t> blob(n * sizeof(uint2) + (t->buckets + 1) * sizeof(uint32_t));
+  uint32_t *off = (uint32_t *)(blob.data() + n * sizeof(uint2));
+  t->host.entries(row, (jf::PenaltyEntry *)blob.data());
+  t->host.offsets(row, off);
   const hipStream_t st = (hipStream_t)stream;
-  int rc = t->staging.upload(t->entries + (size_t)row * t->max_entries, ent,
-                             h.size() * sizeof(uint2), st);
+  int rc = t->staging.upload(t->entries + (size_t)row * t->max_entries, blob.data(),
+                             n * sizeof(uint2), st);
   if (rc != JF_OK) return rc;
   rc = t->staging.upload(t->offsets + (size_t)row * (t->buckets + 1), off,
                          (t->buckets + 1) * sizeof(uint32_t), st);
-  if (rc != JF_OK) return rc;
-  // The fixed slots of each chunk, entries in token order, empty slots 0.
+  if (rc != JF_OK || !t->host.fits(row)) return rc;
   const size_t per_row = (size_t)t->chunks * t->slot_count;
-  std::vector<uint32_t> sl(per_row, 0u);
-  std::vector<uint32_t> used(t->chunks, 0u);
-  bool fits = true;
-  for (const auto &e : h) {
-    const uint32_t c = e.first / jf::kChunkF32, o = e.first % jf::kChunkF32;
-    const uint32_t count = e.second & JF_PENALTY_COUNT_MASK;
-    if (used[c] >= t->slot_count || count > jf::kSlotCountMask) {
-      fits = false;
-      break;
-    }
-    sl[(size_t)c * t->slot_count + used[c]++] =
-        (o << jf::kSlotOffsetShift) |
-        ((e.second & JF_PENALTY_PROMPT_BIT) ? jf::kSlotPromptBit : 0u) | count;
-  }
-  t->fits[row] = fits ? 1 : 0;
-  if (!fits) return JF_OK;
+  std::vector<uint32_t> sl(per_row);
+  t->host.slots(row, sl.data());
   return t->staging.upload(t->slots + (size_t)row * per_row, sl.data(),
                            per_row * sizeof(uint32_t), st);
 }
@@ -399,13 +317,80 @@ int jf_penalty_table_rebuild(jf_penalty_table *t, uint32_t row,
   rc = jf_penalty_words_rebuild(words.data(), t->vocabulary, history, history_len,
                                 generated, has_pending, pending, mark_prompt);
   if (rc != JF_OK) return rc;
-  std::vector<std::pair<uint32_t, uint32_t>> entries;
-  for (uint32_t v = 0; v < t->vocabulary; ++v)
-    if (words[v]) entries.emplace_back(v, words[v]);
-  if (entries.size() > t->max_entries)
-    return fail(JF_ERR_INVALID_ARGUMENT, "penalty history exceeds the table row");
-  t->host[row] = std::move(entries);
+  rc = t->host.rebuild(row, words.data());
+  if (rc != JF_OK) return rc;
   return upload_penalty_row(t, row, stream);
+}
+
+// countPenaltyTokens (Sampling.cpp:75-80) of n (row, token) pairs, applied
+// in order. Everything is checked before any row changes: rows, tokens, and
+// that each row's new distinct tokens fit its max_entries. The host copy
+// then describes each token's update, and penalty_count_kernel applies them
+// on `stream`, up to kPenaltyOps tokens a launch (passed as kernel
+// arguments: no staging copy, no wait on earlier work).
+static int count_pairs(jf_penalty_table *t, const uint32_t *rows, uint32_t one_row,
+                       const uint32_t *selected, uint64_t n, void *stream) {
+  if (!selected && n) return fail(JF_ERR_INVALID_ARGUMENT, "null buffer");
+  int rc = check_device(t->device);
+  if (rc != JF_OK) return rc;
+  std::vector<std::pair<uint32_t, uint32_t>> fresh;  // (row, token) not yet held
+  for (uint64_t i = 0; i < n; ++i) {
+    const uint32_t row = rows ? rows[i] : one_row;
+    if (row >= t->rows)
+      return fail(JF_ERR_INVALID_ARGUMENT, "penalized lane has no penalty table row");
+    if (selected[i] >= t->vocabulary)
+      return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
+    if (!t->host.holds(row, selected[i])) fresh.emplace_back(row, selected[i]);
+  }
+  std::sort(fresh.begin(), fresh.end());
+  fresh.erase(std::unique(fresh.begin(), fresh.end()), fresh.end());
+  for (size_t i = 0; i < fresh.size();) {
+    size_t j = i;
+    while (j < fresh.size() && fresh[j].first == fresh[i].first) ++j;
+    if (t->host.size(fresh[i].first) + (j - i) > t->max_entries)
+      return fail(JF_ERR_INVALID_ARGUMENT, "penalty history exceeds the table row");
+    i = j;
+  }
+  // Updates grouped by row, call order kept inside each row.
+  std::vector<uint64_t> order(n);
+  for (uint64_t i = 0; i < n; ++i) order[i] = i;
+  if (rows)
+    std::stable_sort(order.begin(), order.end(),
+                     [&](uint64_t x, uint64_t y) { return rows[x] < rows[y]; });
+  const jf::PenaltyTableView view{(jf::PenaltyEntry *)t->entries, t->offsets, t->slots,
+                                  t->max_entries, t->buckets, t->chunks, t->slot_count};
+  jf::PenaltyOpBatch b;
+  uint32_t ops = 0, groups = 0;
+  auto flush = [&]() -> int {
+    if (!ops) return JF_OK;
+    b.group_start[groups] = ops;
+    const int e = jf::launch_penalty_count(view, b, groups, stream);
+    ops = groups = 0;
+    return e == hipSuccess ? JF_OK : hip_fail((hipError_t)e, "penalty count launch");
+  };
+  for (uint64_t i = 0; i < n; ++i) {
+    const uint64_t k = order[i];
+    const uint32_t row = rows ? rows[k] : one_row;
+    if (ops == jf::kPenaltyOps) {
+      rc = flush();
+      if (rc != JF_OK) return rc;
+    }
+    if (!ops || b.group_row[groups - 1] != row) {
+      b.group_row[groups] = row;
+      b.group_start[groups++] = ops;
+    }
+    jf::PenaltyOp op;
+    rc = t->host.count(row, selected[k], &op);
+    if (rc != JF_OK) return rc;  // excluded by the checks above
+    jf::PackedPenaltyOp &p = b.op[ops++];
+    p.token = op.token;
+    p.word = op.word;
+    p.index = op.index | (op.insert ? 0x80000000u : 0u);
+    p.entries = op.entries;
+    p.slot_value = op.slot_value;
+    p.slot = op.slot == jf::kNoSlot ? 0xffffu : (op.slot | op.slot_used << 16);
+  }
+  return flush();
 }
 
 int jf_penalty_table_count(jf_penalty_table *t, uint32_t row,
@@ -414,46 +399,14 @@ int jf_penalty_table_count(jf_penalty_table *t, uint32_t row,
   if (!t) return fail(JF_ERR_INVALID_ARGUMENT, "penalty table is null");
   if (row >= t->rows)
     return fail(JF_ERR_INVALID_ARGUMENT, "penalized lane has no penalty table row");
-  if (!selected && count) return fail(JF_ERR_INVALID_ARGUMENT, "null buffer");
-  int rc = check_device(t->device);
-  if (rc != JF_OK) return rc;
-  for (uint64_t i = 0; i < count; ++i)
-    if (selected[i] >= t->vocabulary)
-      return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
-  auto h = t->host[row];
-  for (uint64_t i = 0; i < count; ++i) {
-    auto it = std::lower_bound(h.begin(), h.end(),
-                               std::make_pair(selected[i], 0u));
-    if (it != h.end() && it->first == selected[i])
-      ++it->second;
-    else
-      h.insert(it, std::make_pair(selected[i], 1u));
-  }
-  if (h.size() > t->max_entries)
-    return fail(JF_ERR_INVALID_ARGUMENT, "penalty history exceeds the table row");
-  t->host[row] = std::move(h);
-  return upload_penalty_row(t, row, stream);
+  return count_pairs(t, nullptr, row, selected, count, stream);
 }
 
-// ---- uniforms ---------------------------------------------------------
-
-float jf_next_uniform(uint64_t seed, uint64_t *counter) {
-  uint64_t v = seed + (++*counter) * 0x9e3779b97f4a7c15ULL;
-  v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ULL;
-  v = (v ^ (v >> 27)) * 0x94d049bb133111ebULL;
-  v ^= v >> 31;
-  return float(v >> 40) * 0x1p-24F;
-}
-
-void jf_stage_sampling_cycle(uint64_t seed, uint64_t *counter,
-                             uint32_t verify_rows, int tree_cycle,
-                             float *u) {
-  std::fill(u, u + JF_SAMPLING_UNIFORMS, 0.0f);
-  const uint32_t end = (tree_cycle && verify_rows == 16) ? JF_SAMPLING_UNIFORMS
-                       : verify_rows == 16                ? 24u
-                                                          : 16u;
-  for (uint32_t i = JF_UNIFORM_PROPOSALS; i < end; ++i)
-    u[i] = jf_next_uniform(seed, counter);
+int jf_penalty_table_count_rows(jf_penalty_table *t, const uint32_t *rows,
+                                const uint32_t *selected, uint64_t count, void *stream) {
+  if (!t) return fail(JF_ERR_INVALID_ARGUMENT, "penalty table is null");
+  if (!rows && count) return fail(JF_ERR_INVALID_ARGUMENT, "null buffer");
+  return count_pairs(t, rows, 0, selected, count, stream);
 }
 
 // ---- selection ---------------------------------------------------------
@@ -626,7 +579,7 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
     const jf::RowParams &rp = params[r];
     if (rp.extra_count) fast = false;
     if ((rp.flags & jf::kRowPenalized) &&
-        (!a->penalties->fits[rp.penalty_row] || rp.penalty_row > 0xffffffu))
+        (!a->penalties->host.fits(rp.penalty_row) || rp.penalty_row > 0xffffffu))
       fast = false;
   }
   int e = hipSuccess;

@@ -8,6 +8,8 @@
 // Host code; all arithmetic in double as the reference does.
 #include "jf_sampler.h"
 
+#include "jf_host.h"
+
 #include <algorithm>
 #include <array>
 #include <cmath>
@@ -173,9 +175,6 @@ void layout(const std::vector<TreeNode> &nodes, jf_draft_tree *tree) {
 
 }  // namespace
 
-namespace jf {
-int set_error(int code, const char *message);  // jf_sampler.cpp: jf_last_error's text
-}
 
 extern "C" int jf_build_draft_tree(const uint32_t *candidates, const float *unary,
                                    const float *edges, uint32_t anchor, uint32_t rows,

@@ -32,7 +32,7 @@ EXPORTS = [
     "jf_sampler_destroy", "jf_sampler_workspace_bytes",
     "jf_penalty_words_rebuild", "jf_penalty_words_count",
     "jf_penalty_table_create", "jf_penalty_table_destroy",
-    "jf_penalty_table_rebuild", "jf_penalty_table_count",
+    "jf_penalty_table_rebuild", "jf_penalty_table_count", "jf_penalty_table_count_rows",
     "jf_next_uniform", "jf_stage_sampling_cycle", "jf_sample", "jf_sample_static",
     "jf_accept_chain", "jf_accept_tree",
     "jf_draft_selector_create", "jf_draft_selector_destroy", "jf_draft_select",
@@ -173,6 +173,7 @@ def lib():
             c_vp, c_u32, c_vp, c_u64, c_u64, ctypes.c_int, c_u32,
             ctypes.c_int, c_vp]
         L.jf_penalty_table_count.argtypes = [c_vp, c_u32, c_vp, c_u64, c_vp]
+        L.jf_penalty_table_count_rows.argtypes = [c_vp, c_vp, c_vp, c_u64, c_vp]
         L.jf_next_uniform.argtypes = [c_u64, ctypes.POINTER(c_u64)]
         L.jf_next_uniform.restype = c_f32
         L.jf_stage_sampling_cycle.argtypes = [
@@ -297,6 +298,16 @@ class PenaltyTable:
         check(lib().jf_penalty_table_count(self.handle, row,
                                            s.ctypes.data_as(c_vp), s.size,
                                            _stream()))
+
+    def count_rows(self, rows, selected):
+        """One step's commits of several rows: token selected[i] into row rows[i]."""
+        import numpy as np
+        r = np.ascontiguousarray(rows, dtype=np.uint32)
+        s = np.ascontiguousarray(selected, dtype=np.uint32)
+        if r.size != s.size:
+            raise ValueError("rows and selected differ in length")
+        check(lib().jf_penalty_table_count_rows(self.handle, r.ctypes.data_as(c_vp),
+                                                s.ctypes.data_as(c_vp), s.size, _stream()))
 
     def close(self):
         if self.handle:

@@ -71,53 +71,63 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             build()
-        L = ctypes.CDLL(LIB_PATH)
-        L.jfo_logit_key.argtypes = [c_f32]
-        L.jfo_logit_key.restype = c_u32
-        L.jfo_key_logit.argtypes = [c_u32]
-        L.jfo_key_logit.restype = c_f32
-        L.jfo_expf.argtypes = [c_f32]
-        L.jfo_expf.restype = c_f32
-        L.jfo_floor_mul.argtypes = [c_u64, c_f32]
-        L.jfo_floor_mul.restype = c_u64
-        L.jfo_splitmix64.argtypes = [c_u64, c_u64]
-        L.jfo_splitmix64.restype = c_u64
-        L.jfo_next_uniform.argtypes = [c_u64, ctypes.POINTER(c_u64)]
-        L.jfo_next_uniform.restype = c_f32
-        L.jfo_stage_cycle.argtypes = [c_u64, ctypes.POINTER(c_u64), c_u32,
-                                      ctypes.c_int, c_vp]
-        L.jfo_stage_cycle.restype = None
-        L.jfo_rebuild_penalty_words.argtypes = [
-            c_vp, c_u32, c_vp, c_u64, c_u64, ctypes.c_int, c_u32, ctypes.c_int]
-        L.jfo_count_penalty_tokens.argtypes = [c_vp, c_u32, c_vp, c_u64]
-        L.jfo_penalize_logit.argtypes = [c_f32, c_u32, c_f32, c_f32, c_f32, c_f32]
-        L.jfo_penalize_logit.restype = c_f32
-        L.jfo_repetition_inverse.argtypes = [c_f32]
-        L.jfo_repetition_inverse.restype = c_f32
-        L.jfo_policy_valid.argtypes = [ctypes.POINTER(Policy)]
-        L.jfo_select_row.argtypes = [c_u32, c_u32, c_u32, ctypes.POINTER(Policy),
-                                     ctypes.POINTER(RowInput),
-                                     ctypes.POINTER(RowOutput), c_vp, c_vp, c_u32]
-        L.jfo_select_batch.argtypes = [
-            c_u32, c_u32, c_u32, c_u32, ctypes.POINTER(Policy), c_vp,
-            ctypes.c_int, c_u64, c_vp, c_u64, c_vp, c_vp, c_vp, c_vp, c_vp, c_u32]
-        L.jfo_accept_chain.argtypes = [ctypes.POINTER(ChainParams), c_vp, c_vp,
-                                       c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]
-        L.jfo_accept_chain.restype = None
-        L.jfo_accept_tree.argtypes = [ctypes.POINTER(TreeParams), c_vp, c_vp,
-                                      c_vp, c_vp, c_vp, c_vp]
-        L.jfo_accept_tree.restype = None
-        L.jfo_draft_top16.argtypes = [c_vp, c_u32, c_vp, c_vp]
-        L.jfo_draft_top16.restype = None
-        L.jfo_draft_edge.argtypes = [c_vp, c_vp, c_vp]
-        L.jfo_draft_edge.restype = c_f32
-        L.jfo_draft_select_lane.argtypes = [ctypes.POINTER(DraftLane), c_vp, c_u64, c_vp,
-                                            c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]
-        L.jfo_draft_select_lane.restype = None
-        L.jfo_tree_gather.argtypes = [c_vp, c_vp, c_vp, ctypes.POINTER(GatherParams)]
-        L.jfo_tree_gather.restype = None
-        _lib = L
+        _lib = _bind(ctypes.CDLL(LIB_PATH))
     return _lib
+
+
+def native_lib(directory):
+    """The same source built with -O3 -march=native into `directory` (the CPU
+    baseline's build, made on the machine that runs it)."""
+    subprocess.run(["make", "-s", "-C", HERE, "native", f"NATIVE={directory}"], check=True)
+    return _bind(ctypes.CDLL(os.path.join(directory, "libjf_oracle_native.so")))
+
+
+def _bind(L):
+    L.jfo_logit_key.argtypes = [c_f32]
+    L.jfo_logit_key.restype = c_u32
+    L.jfo_key_logit.argtypes = [c_u32]
+    L.jfo_key_logit.restype = c_f32
+    L.jfo_expf.argtypes = [c_f32]
+    L.jfo_expf.restype = c_f32
+    L.jfo_floor_mul.argtypes = [c_u64, c_f32]
+    L.jfo_floor_mul.restype = c_u64
+    L.jfo_splitmix64.argtypes = [c_u64, c_u64]
+    L.jfo_splitmix64.restype = c_u64
+    L.jfo_next_uniform.argtypes = [c_u64, ctypes.POINTER(c_u64)]
+    L.jfo_next_uniform.restype = c_f32
+    L.jfo_stage_cycle.argtypes = [c_u64, ctypes.POINTER(c_u64), c_u32,
+                                  ctypes.c_int, c_vp]
+    L.jfo_stage_cycle.restype = None
+    L.jfo_rebuild_penalty_words.argtypes = [
+        c_vp, c_u32, c_vp, c_u64, c_u64, ctypes.c_int, c_u32, ctypes.c_int]
+    L.jfo_count_penalty_tokens.argtypes = [c_vp, c_u32, c_vp, c_u64]
+    L.jfo_penalize_logit.argtypes = [c_f32, c_u32, c_f32, c_f32, c_f32, c_f32]
+    L.jfo_penalize_logit.restype = c_f32
+    L.jfo_repetition_inverse.argtypes = [c_f32]
+    L.jfo_repetition_inverse.restype = c_f32
+    L.jfo_policy_valid.argtypes = [ctypes.POINTER(Policy)]
+    L.jfo_select_row.argtypes = [c_u32, c_u32, c_u32, ctypes.POINTER(Policy),
+                                 ctypes.POINTER(RowInput),
+                                 ctypes.POINTER(RowOutput), c_vp, c_vp, c_u32]
+    L.jfo_select_batch.argtypes = [
+        c_u32, c_u32, c_u32, c_u32, ctypes.POINTER(Policy), c_vp,
+        ctypes.c_int, c_u64, c_vp, c_u64, c_vp, c_vp, c_vp, c_vp, c_vp, c_u32]
+    L.jfo_accept_chain.argtypes = [ctypes.POINTER(ChainParams), c_vp, c_vp,
+                                   c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]
+    L.jfo_accept_chain.restype = None
+    L.jfo_accept_tree.argtypes = [ctypes.POINTER(TreeParams), c_vp, c_vp,
+                                  c_vp, c_vp, c_vp, c_vp]
+    L.jfo_accept_tree.restype = None
+    L.jfo_draft_top16.argtypes = [c_vp, c_u32, c_vp, c_vp]
+    L.jfo_draft_top16.restype = None
+    L.jfo_draft_edge.argtypes = [c_vp, c_vp, c_vp]
+    L.jfo_draft_edge.restype = c_f32
+    L.jfo_draft_select_lane.argtypes = [ctypes.POINTER(DraftLane), c_vp, c_u64, c_vp,
+                                        c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]
+    L.jfo_draft_select_lane.restype = None
+    L.jfo_tree_gather.argtypes = [c_vp, c_vp, c_vp, ctypes.POINTER(GatherParams)]
+    L.jfo_tree_gather.restype = None
+    return L
 
 
 def _p(a):
@@ -180,12 +190,12 @@ def select_row(vocabulary, pol, *, logits=None, logits_bf16=None, mask=None,
 
 def select_batch(vocabulary, policies, logits, *, is_bf16=False, masks=None,
                  words=None, pen_rows=None, uniforms=None,
-                 stop=(NO_TOKEN, NO_TOKEN), threads=1):
+                 stop=(NO_TOKEN, NO_TOKEN), threads=1, library=None):
     rows = logits.shape[0]
     pol = (Policy * rows)(*policies)
     out = np.zeros(rows, dtype=np.uint32)
     mx = np.zeros(rows, dtype=np.float32)
-    rc = lib().jfo_select_batch(
+    rc = (library or lib()).jfo_select_batch(
         rows, vocabulary, stop[0], stop[1], pol, _p(logits), 1 if is_bf16 else 0,
         logits.shape[1], _p(masks), 0 if masks is None else masks.shape[1],
         _p(words), _p(pen_rows), _p(uniforms), _p(out), _p(mx), threads)

@@ -1,0 +1,135 @@
+"""Counted tokens applied to the device penalty table in place
+(jf_penalty_table_count / _count_rows, penalty_count_kernel): after a rebuild
+and a sequence of counts (tokens already held, new tokens, one row many
+times, more tokens than one launch carries, a row pushed past its chunk's
+fixed slots), penalized selection through both select kernels (the fast
+one reads the fixed slots, the general one the sorted entries and bucket
+offsets) equals the oracle over the dense words that countPenaltyTokens
+(Sampling.cpp:75-80) would hold."""
+import numpy as np
+import pytest
+
+import jf_sampler as J
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+V = 151936
+
+
+def _logits(rows, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((rows, V)) * 2.0).astype(np.float32)
+
+
+def _select(table, words, lg, policies, uniforms, extra=None):
+    """Selection on the GPU (through `table`) and in the oracle (through the
+    dense `words`); extra tokens route the launch to the general kernel."""
+    import torch
+    dev = torch.device("cuda", 0)
+    rows = lg.shape[0]
+    s = J.Sampler(V, rows)
+    out = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+    kw = {}
+    if extra is not None:
+        ex = np.zeros((rows, 1), np.uint32)
+        ex[:, 0] = extra
+        kw = dict(extra_tokens=torch.from_numpy(ex.view(np.int32)).to(dev),
+                  extra_counts=[1] * rows, extra_stride=1)
+    s.sample(torch.from_numpy(lg).to(dev), policies, out, penalties=table,
+             penalty_rows=list(range(rows)),
+             uniforms=torch.from_numpy(uniforms).to(dev), **kw)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint32).copy()
+    want = np.array([O.select_row(V, O.policy_from(policies[r]), logits=lg[r], words=words[r],
+                                  extra=None if extra is None else [int(extra[r])],
+                                  uniform=float(uniforms[r]))[0] for r in range(rows)], np.uint32)
+    return got, want
+
+
+@pytest.mark.parametrize("general", [False, True])
+def test_counts_update_the_table_in_place(general):
+    rows = 4
+    rng = np.random.default_rng(7)
+    histories = [rng.integers(0, V, 1500, dtype=np.uint32) for _ in range(rows)]
+    generated = [700, 0, 1499, 10]
+    table = J.PenaltyTable(V, rows, 4096)
+    words = np.zeros((rows, V), np.uint32)
+    for r in range(rows):
+        table.rebuild(r, histories[r], generated[r], None, r % 2 == 0)
+        rc, words[r] = O.rebuild_penalty_words(V, histories[r], generated[r], None, r % 2 == 0)
+        assert rc == 0
+    # Tokens already held, new ones, repeats, and one row many times: 150
+    # pairs (five launches of at most 32).
+    pr, pt = [], []
+    for k in range(150):
+        r = int(rng.integers(0, rows)) if k % 5 else 2
+        if k % 3 == 0:
+            t = int(histories[r][rng.integers(0, len(histories[r]))])
+        elif k % 3 == 1:
+            t = int(rng.integers(0, V))
+        else:
+            t = int(rng.integers(8192 * 3, 8192 * 3 + 50))  # one chunk, many repeats
+        pr.append(r)
+        pt.append(t)
+    table.count_rows(pr, pt)
+    table.count(1, pt[:40])  # the single-row entry point, in order
+    for r, t in zip(pr, pt):
+        words[r, t] += 1
+    for t in pt[:40]:
+        words[1, t] += 1
+    pols = [J.policy(repetition=1.3, presence=0.6, frequency=0.4),
+            J.policy(temperature=0.8, top_k=40, presence=1.5, frequency=1.0),
+            J.policy(temperature=1.1, top_p=0.9, repetition=1.8),
+            J.policy(temperature=0.6, min_p=0.05, top_k=200, frequency=2.0, repetition=0.7)]
+    uniforms = rng.random(rows, dtype=np.float32)
+    lg = _logits(rows, 11)
+    # Penalized tokens near the top, so the counts decide the selections.
+    for r in range(rows):
+        lg[r, pt[r::rows]] += 6.0
+    extra = rng.integers(0, V, rows).astype(np.uint32) if general else None
+    got, want = _select(table, words, lg, pols, uniforms, extra)
+    np.testing.assert_array_equal(got, want)
+    table.close()
+
+
+def test_row_pushed_past_its_slots_still_selects_exactly():
+    """Counts that overflow one chunk's fixed slots take the row off the fast
+    kernel; a later rebuild that fits puts it back."""
+    rows = 2
+    rng = np.random.default_rng(3)
+    table = J.PenaltyTable(V, rows, 4096)
+    words = np.zeros((rows, V), np.uint32)
+    hist = [np.arange(0, 200, dtype=np.uint32), rng.integers(0, V, 900, dtype=np.uint32)]
+    for r in range(rows):
+        table.rebuild(r, hist[r], 100, None, True)
+        words[r] = O.rebuild_penalty_words(V, hist[r], 100, None, True)[1]
+    # 400 new tokens in chunk 0 of row 0: more than its 256 slots.
+    new = np.arange(200, 600, dtype=np.uint32)
+    table.count_rows([0] * len(new), new)
+    words[0, new] += 1
+    pols = [J.policy(repetition=1.5, presence=1.0), J.policy(temperature=0.9, top_k=30, frequency=1.2)]
+    lg = _logits(rows, 5)
+    lg[0, :600] += 5.0
+    uniforms = rng.random(rows, dtype=np.float32)
+    got, want = _select(table, words, lg, pols, uniforms)
+    np.testing.assert_array_equal(got, want)
+    for r in range(rows):
+        table.rebuild(r, hist[r], 100, None, True)
+        words[r] = O.rebuild_penalty_words(V, hist[r], 100, None, True)[1]
+    got, want = _select(table, words, lg, pols, uniforms)
+    np.testing.assert_array_equal(got, want)
+    table.close()
+
+
+def test_count_errors_leave_the_row_unchanged():
+    table = J.PenaltyTable(1000, 2, 8)
+    table.rebuild(0, [1, 2, 3], 1, None, True)
+    with pytest.raises(RuntimeError, match="outside the vocabulary"):
+        table.count_rows([0, 0], [5, 1000])
+    with pytest.raises(RuntimeError, match="no penalty table row"):
+        table.count_rows([0, 2], [5, 6])
+    with pytest.raises(RuntimeError, match="exceeds the table row"):
+        table.count(0, [10, 11, 12, 13, 14, 15, 16])  # 3 held + 7 new > 8
+    table.count(0, [10, 11, 12, 13, 14])  # exactly 8
+    table.close()

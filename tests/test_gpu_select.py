@@ -430,6 +430,32 @@ def test_dense_residual_multipass():
     assert_same(g, r)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_dense_residual_in_the_partial_last_chunk(bf16):
+    """The last row's residual draw lands in the partial last chunk (V is not
+    a multiple of 8192): its mass sits at V - 1, where q is small, and the
+    dense q buffer is exactly rows x V floats, so a read of q past the
+    vocabulary would leave the buffer. Tokens and p(draft) bit-exact."""
+    rng = np.random.default_rng(29 + bf16)
+    V = 151936
+    rows = 3
+    x = np.full((rows, V), -12.0, np.float32) + rng.random((rows, V), dtype=np.float32)
+    x[:, V - 1] = 9.0
+    x[:, V - 40:V - 1] += 4.0
+    q = rng.dirichlet(np.ones(V), rows).astype(np.float32)
+    q[:, V - 1] = 1e-4
+    d = np.array([5, V - 2, 77], np.uint32)
+    u = np.array([0.3, 0.999, 0.9999], np.float32)
+    kw = dict(uniforms=u, draft_tokens=d, dense_q=np.ascontiguousarray(q))
+    if bf16:
+        kw["logits_bf16"] = WL.to_bf16_bits(x)
+    else:
+        kw["logits"] = x
+    g, r = both(V, [J.policy(temperature=1.0)] * rows, **kw)
+    assert_same(g, r)
+    assert g["tokens"][rows - 1] >= V - 4480  # inside the partial last chunk
+
+
 def test_determinism_repeat():
     c = WL.config2(B=16)
     pol = [J.policy(**c["policy"])] * 16
