@@ -249,10 +249,11 @@ def time_with_counts(g, steps):
             "note": "each step followed by jf_penalty_table_count_rows of one token per row"}
 
 
-def time_cpp_loop(g, steps, with_counts):
-    """The same calls issued from C++ (libjf_bench_loop.so): GPU and host
-    microseconds per step without the Python loop, optionally with the
-    per-step penalty count."""
+def time_cpp_loop(g, steps, with_counts, batch=0):
+    """The same calls issued from C++ (libjf_bench_loop.so), as a native
+    engine issues them: GPU and host microseconds per step without the
+    Python loop, optionally with the per-step penalty count, and with
+    `batch` the mean step time of each run of that many steps."""
     import ctypes
     import jf_sampler as J
     J.lib()  # the sampler library first: one HIP runtime in the process
@@ -260,7 +261,7 @@ def time_cpp_loop(g, steps, with_counts):
     vp, u32 = ctypes.c_void_p, ctypes.c_uint32
     L.jf_bench_sample_loop.argtypes = [vp, vp, u32, u32, vp, vp, vp, u32, vp,
                                        ctypes.POINTER(ctypes.c_double),
-                                       ctypes.POINTER(ctypes.c_double)]
+                                       ctypes.POINTER(ctypes.c_double), u32, vp]
     n = len(g.kw)
     arr = (J.JfSampleArgs * n)(*[a for a, _ in g.kw])
     rows = g.w["rows"]
@@ -269,14 +270,19 @@ def time_cpp_loop(g, steps, with_counts):
         tables = (vp * n)(*[t.handle.value for t in g.tables])
         idx = np.arange(rows, dtype=np.uint32)
         toks = np.random.default_rng(98).integers(0, g.w["V"], (steps, rows), dtype=np.uint32)
+    batch_us = np.zeros(steps // batch, np.float32) if batch else None
     gpu, host = ctypes.c_double(), ctypes.c_double()
     rc = L.jf_bench_sample_loop(g.sampler.handle, ctypes.cast(arr, vp), n, steps, tables,
                                 None if idx is None else idx.ctypes.data_as(vp),
                                 None if toks is None else toks.ctypes.data_as(vp), rows,
-                                J._stream(), ctypes.byref(gpu), ctypes.byref(host))
+                                J._stream(), ctypes.byref(gpu), ctypes.byref(host), batch,
+                                None if batch_us is None else batch_us.ctypes.data_as(vp))
     if rc:
         raise RuntimeError(f"C++ timing loop failed: {rc} {J.lib().jf_last_error().decode()}")
-    return {"us_per_step": gpu.value, "host_us_per_call": host.value}
+    out = {"us_per_step": gpu.value, "host_us_per_call": host.value}
+    if batch:
+        out["batch_us"] = batch_us
+    return out
 
 
 def cpu_model():
@@ -347,21 +353,52 @@ def cpu_baseline(w, seconds):
                        f"over rows; tokens equal to the -O2 checker build's")
 
 
-def read_traffic(cfg):
-    """HBM bytes per launch and the kernel they were counted on, from the
-    committed rocprofv3 --pmc summary (its first line names the kernel)."""
-    name = {"draft": "draft_top16", "gather": "tree_gather"}.get(cfg, f"select_c{cfg}")
-    path = os.path.join(REPO, "profiles", f"{name}_traffic.txt")
-    if not os.path.exists(path):
-        return None, None
-    traffic, kernel = None, None
+# The committed rocprofv3 summary of each workload (profiles/<name>.txt): one
+# line per kernel with its trace statistics and HBM traffic.
+PROFILE_NAMES = {(1, "auto"): "select_c1", (2, "auto"): "select_merge_c2",
+                 (3, "greedy"): "select_c3_greedy", (3, "sampled"): "select_uncut_c3_sampled",
+                 (4, "greedy"): "select_c4_greedy", (4, "sampled"): "select_uncut_c4_sampled",
+                 (5, "auto"): "select_merge_c5", ("draft", "auto"): "draft_select",
+                 ("gather", "auto"): "tree_gather"}
+
+
+def profile_key(cfg, mode):
+    if cfg in (3, 4):
+        return (cfg, "greedy" if mode == "greedy" else "sampled")
+    return (cfg, "auto")
+
+
+def profile_row(key, kernel):
+    """The fields of `kernel`'s line in the workload's summary, or None."""
+    name = PROFILE_NAMES.get(key)
+    path = os.path.join(REPO, "profiles", f"{name}.txt") if name else None
+    if not kernel or not path or not os.path.exists(path):
+        return None
     for line in open(path):
-        m = re.match(r"# HBM traffic per launch of (\S+):", line)
-        if m:
-            kernel = m.group(1)
-        if line.startswith("traffic_bytes_per_launch:"):
-            traffic = float(line.split(":")[1])
-    return traffic, kernel
+        f = line.split()
+        if f and f[0] == kernel:
+            return f
+    return None
+
+
+def read_traffic(key, kernel):
+    """HBM bytes per launch of `kernel` (FETCH_SIZE and WRITE_SIZE scaled by a
+    copy kernel's readings) from the committed summary, or None."""
+    f = profile_row(key, kernel)
+    try:
+        return float(f[7]) if f and f[7] != "-" else None
+    except (IndexError, ValueError):
+        return None
+
+
+def read_profile_us(key, kernel):
+    """The kernel's rocprofv3 average duration (us) in the committed summary
+    of the same workload, or None."""
+    f = profile_row(key, kernel)
+    try:
+        return float(f[2]) if f else None
+    except (IndexError, ValueError):
+        return None
 
 
 def copy_calibration():
@@ -427,7 +464,8 @@ def bench_draft(args):
     hev.destroy()
     top_bytes = lanes * 7 * V * 4
     achieved = top_bytes / (kus.mean() * 1e-6) / 1e9
-    traffic, kernel = read_traffic("draft")
+    kernel = "jf::draft_top16_kernel<true>"
+    traffic = read_traffic(("draft", "auto"), kernel)
     cpu = None
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(REPO, "oracle"))
@@ -456,7 +494,7 @@ def bench_draft(args):
                    "rows": lanes * 7, "vocabulary": V, "algorithmic_bytes_per_step": top_bytes},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
-                     "kernel": kernel or "jf::draft_top16_kernel<true>",
+                     "kernel": kernel,
                      "kernel_mean_us": float(kus.mean()),
                      "kernel_p50_us": float(np.percentile(kus, 50)),
                      "algorithmic_bytes": top_bytes},
@@ -513,7 +551,8 @@ def bench_gather(args):
     kus = np.array([hev.ms(2 * i, 2 * i + 1) for i in range(K)]) * 1000.0
     hev.destroy()
     achieved = alg / (kus.mean() * 1e-6) / 1e9
-    traffic, kernel = read_traffic("gather")
+    kernel = "jf::tree_gather_kernel<true>"
+    traffic = read_traffic(("gather", "auto"), kernel)
     cpu = None
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(REPO, "oracle"))
@@ -540,7 +579,7 @@ def bench_gather(args):
                    "moved_rows": moved, "algorithmic_bytes_per_step": alg},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
-                     "kernel": kernel or "jf::tree_gather_kernel<true>",
+                     "kernel": kernel,
                      "kernel_mean_us": float(kus.mean()),
                      "kernel_p50_us": float(np.percentile(kus, 50)), "algorithmic_bytes": alg},
         "cpu_baseline": cpu,
@@ -576,32 +615,43 @@ def main():
         g.step(i)
     torch.cuda.synchronize()
     K = args.steps
+    # The timed steps: jf_sample issued back to back from C++ (the engine's
+    # call), HIP events on the launch stream at the ends and after every 25
+    # steps, a device synchronization on both sides. p50/p90 are over the
+    # 25-step runs' mean step times.
+    batch = 25 if K % 25 == 0 else 1
+    wall0 = time.perf_counter()
+    cpp = time_cpp_loop(g, K, False, batch=batch)
+    wall = time.perf_counter() - wall0
+    per = cpp.pop("batch_us").astype(np.float64)
+    ms_per_step = cpp["us_per_step"] / 1000.0
+    p50, p90 = float(np.percentile(per, 50)), float(np.percentile(per, 90))
+    step_gbs = w["alg_bytes"] / (cpp["us_per_step"] * 1e-6) / 1e9
+    # The same steps from a Python loop (ctypes per call), for comparison.
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
     torch.cuda.synchronize()
-    wall0 = time.perf_counter()
     ev[0].record()
     for i in range(K):
         g.step(args.warmup + i)
         ev[i + 1].record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    per = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(K)]) * 1000.0  # us
-    total_ms = ev[0].elapsed_time(ev[K])
-    ms_per_step = total_ms / K
-    p50, p90 = float(np.percentile(per, 50)), float(np.percentile(per, 90))
-    mean_us = float(per.mean())
-    step_gbs = w["alg_bytes"] / (mean_us * 1e-6) / 1e9
+    py_per = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(K)]) * 1000.0
+    python_loop = {"ms_per_step": ev[0].elapsed_time(ev[K]) / K,
+                   "p50_us": float(np.percentile(py_per, 50))}
     # The dominant kernel (the single pass over the logits) timed alone; its
-    # algorithmic bytes are the logits and the history ids (the merge's
-    # uniforms and outputs are a few hundred bytes).
+    # algorithmic bytes are the logits and the history ids or mask words.
     sel_mean, sel_p50 = time_select(g, args.warmup + K, K)
     achieved = w["select_bytes"] / (sel_mean * 1e-6) / 1e9
-    counted = time_with_counts(g, K) if g.tables else None
-    cpp = {"loop": time_cpp_loop(g, K, False)}
+    counted = None
     if g.tables:
-        cpp["loop_with_penalty_count"] = time_cpp_loop(g, K, True)
+        counted = time_cpp_loop(g, K, True)
+        counted["note"] = ("each step followed by jf_penalty_table_count_rows of one "
+                           "token per row, from C++")
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
-    traffic, kernel = read_traffic(args.config)
+    kernel = f"jf::select_fast_kernel<{0 if w['dtype'] == 'f32' else 1}>"
+    key = profile_key(args.config, args.mode)
+    traffic = read_traffic(key, kernel)
+    prof_us = read_profile_us(key, kernel)
     line = {
         "metric": "sampling steps/sec at B=64,V=151936; achieved HBM GB/s vs peak; p50 us/step",
         "value": 1000.0 / ms_per_step,
@@ -621,16 +671,25 @@ def main():
                 f"{len(g.copies)} rotated input copies >= 512 MB",
         "config": {"workload": w["name"], "rows": w["rows"], "vocabulary": w["V"],
                    "algorithmic_bytes_per_step": w["alg_bytes"]},
+        "timing": "jf_sample called back to back from C++ (libjf_bench_loop.so), HIP events "
+                  "on the launch stream at the ends and every 25 steps (p50/p90 over those "
+                  "runs' mean step); host_us_per_call is that loop's own issue time",
+        "host_us_per_call": cpp["host_us_per_call"],
+        "python_loop": python_loop,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
                      "traffic": traffic,
-                     "kernel": kernel or "jf selection kernel",
+                     "kernel": kernel,
+                     "timing": "mean of HIP events the library records around the kernel's "
+                               "launch (hipExtLaunchKernelGGL) on its stream",
                      "kernel_mean_us": sel_mean, "kernel_p50_us": sel_p50,
+                     "rocprof_mean_us": prof_us,
+                     "rocprof_frac": (w["select_bytes"] / (prof_us * 1e-6) / 1e9 / PEAK_HBM_GBS
+                                      if prof_us else None),
                      "algorithmic_bytes": w["select_bytes"],
                      "step_achieved": step_gbs,
                      "step_frac": step_gbs / PEAK_HBM_GBS},
         "with_penalty_count": counted,
-        "cpp_loop": cpp,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

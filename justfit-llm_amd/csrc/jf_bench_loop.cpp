@@ -3,12 +3,14 @@
 // native caller is measured apart from the Python loop's. Each step issues
 // args[i % n] on `stream`, optionally followed by one token per row counted
 // into tables[i % n] (the engine's commit). Returns the GPU time per step
-// (HIP events around the whole loop) and the host time per step (wall
-// clock of the issuing loop alone).
+// (HIP events around the whole loop), the host time per step (wall clock of
+// the issuing loop alone) and, with batch_us set, the mean step time of
+// each run of `batch` steps between events.
 #include <hip/hip_runtime.h>
 
 #include <chrono>
 #include <cstdint>
+#include <vector>
 
 #include "jf_sampler.h"
 
@@ -16,34 +18,45 @@ extern "C" int jf_bench_sample_loop(jf_sampler *sampler, const jf_sample_args *a
                                     uint32_t n, uint32_t steps, jf_penalty_table *const *tables,
                                     const uint32_t *count_rows, const uint32_t *count_tokens,
                                     uint32_t rows, void *stream, double *gpu_us_per_step,
-                                    double *host_us_per_step) {
+                                    double *host_us_per_step, uint32_t batch, float *batch_us) {
   if (!sampler || !args || !n || !steps || !gpu_us_per_step || !host_us_per_step) return -1;
+  if (batch_us && (!batch || steps % batch)) return -1;
   hipStream_t st = (hipStream_t)stream;
-  hipEvent_t start, stop;
-  if (hipEventCreate(&start) != hipSuccess) return -2;
-  if (hipEventCreate(&stop) != hipSuccess) {
-    (void)hipEventDestroy(start);
-    return -2;
-  }
-  int rc = hipStreamSynchronize(st) == hipSuccess ? 0 : -2;
+  // Events at the loop's ends, and after every `batch` steps when batch
+  // times are asked for (an event per step would add its own packets to
+  // every step).
+  const uint32_t nb = batch_us ? steps / batch : 1;
+  const uint32_t ne = nb + 1;
+  std::vector<hipEvent_t> ev(ne, nullptr);
+  int rc = 0;
+  for (uint32_t i = 0; i < ne && !rc; ++i)
+    if (hipEventCreate(&ev[i]) != hipSuccess) rc = -2;
+  if (!rc && hipStreamSynchronize(st) != hipSuccess) rc = -2;
   const auto t0 = std::chrono::steady_clock::now();
-  if (!rc && hipEventRecord(start, st) != hipSuccess) rc = -2;
+  if (!rc && hipEventRecord(ev[0], st) != hipSuccess) rc = -2;
   for (uint32_t i = 0; i < steps && !rc; ++i) {
     rc = jf_sample(sampler, &args[i % n], stream);
     if (!rc && tables)
       rc = jf_penalty_table_count_rows(tables[i % n], count_rows,
                                        count_tokens + (uint64_t)i * rows, rows, stream);
+    const uint32_t per = batch_us ? batch : steps;
+    if (!rc && (i + 1) % per == 0 && hipEventRecord(ev[(i + 1) / per], st) != hipSuccess)
+      rc = -2;
   }
   const auto t1 = std::chrono::steady_clock::now();
-  if (!rc && hipEventRecord(stop, st) != hipSuccess) rc = -2;
-  if (!rc && hipEventSynchronize(stop) != hipSuccess) rc = -2;
+  if (!rc && hipEventSynchronize(ev[ne - 1]) != hipSuccess) rc = -2;
   float ms = 0.0f;
-  if (!rc && hipEventElapsedTime(&ms, start, stop) != hipSuccess) rc = -2;
+  if (!rc && hipEventElapsedTime(&ms, ev[0], ev[ne - 1]) != hipSuccess) rc = -2;
+  for (uint32_t i = 0; batch_us && i < nb && !rc; ++i) {
+    float m = 0.0f;
+    if (hipEventElapsedTime(&m, ev[i], ev[i + 1]) != hipSuccess) rc = -2;
+    batch_us[i] = 1000.0f * m / batch;
+  }
   if (!rc) {
     *gpu_us_per_step = 1000.0 * ms / steps;
     *host_us_per_step = std::chrono::duration<double, std::micro>(t1 - t0).count() / steps;
   }
-  (void)hipEventDestroy(start);
-  (void)hipEventDestroy(stop);
+  for (hipEvent_t e : ev)
+    if (e) (void)hipEventDestroy(e);
   return rc;
 }

@@ -98,6 +98,33 @@ __device__ __forceinline__ uint64_t quantized_weight(float value, float maximum,
   return ((uint64_t)Y << 32) >> k;
 }
 
+// A chunk mass's rescale from the chunk's maximum to the row's:
+// floor(exp((chunk_max - row_max) / T) * 2^32), in [0, 2^32] (exp_weight's
+// result times 2^32 is exact; the conversion truncates).
+__device__ __forceinline__ uint64_t chunk_scale(float chunk_max, float row_max, float inv_t) {
+  return (uint64_t)(exp_weight((chunk_max - row_max) * inv_t) * 0x1p32f);
+}
+// floor(x * r / 2^32) for x < 2^63 and r <= 2^32: bits 32..95 of the product.
+__device__ __forceinline__ uint64_t scale_down(uint64_t x, uint64_t r) {
+  return (__umul64hi(x, r) << 32) | ((x * r) >> 32);
+}
+// The largest P with scale_down(P, r) <= within, for r in [1, 2^32] and a
+// result below 2^63: ceil((within + 1) * 2^32 / r) - 1, by long division of
+// the 96-bit numerator in 32-bit digits (each partial dividend stays below
+// r * 2^32 <= 2^64).
+__device__ __forceinline__ uint64_t unscaled_bound(uint64_t within, uint64_t r) {
+  if (r >= (1ull << 32)) return within;
+  const uint64_t n = within + 1;
+  // The top digit n >> 32 is below r (the quotient fits 64 bits), so the
+  // division starts at the middle digit with it as the remainder.
+  uint64_t cur = n;
+  const uint64_t q1 = cur / r;
+  cur = (cur % r) << 32;
+  const uint64_t q0 = cur / r;
+  const uint64_t q = (q1 << 32) | q0;
+  return (cur % r) ? q : q - 1;
+}
+
 // floor(a * f) exactly for f in [0, 1]; NaN and f <= 0 give 0, f >= 1 gives a.
 __device__ __forceinline__ uint64_t floor_mul(uint64_t a, float f) {
   if (!(f > 0.0f)) return 0;

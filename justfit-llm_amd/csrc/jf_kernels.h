@@ -111,9 +111,8 @@ struct SampleLaunch {
   uint32_t stop1;
   uint32_t stage;
   uint32_t aligned;       // rows start on 16-byte boundaries: vector loads
-  uint32_t all_sampled;   // every row of the launch is sampled
-  uint32_t uncut_rows;    // mixed launch: merges skip sampled rows with no
-                          // cut, mass_draw_kernel draws only those
+  uint32_t finish_greedy; // no merge runs: uncut_kernel finishes the greedy
+                          // rows
   uint32_t row_indexed;   // drafts are addressed through RowParams'
                           // draft_index/cand_index, not the row number
   const uint2 *pen_entries;
@@ -161,9 +160,6 @@ struct FastLaunch {
   uint32_t row_base;          // sampler row of blockIdx.y == 0
   uint32_t fuse_greedy;       // every row greedy: the last block of a row
                               // finishes it (no merge launch)
-  uint32_t mass_only;         // sampled rows keep every admitted token:
-                              // write chunk maxima only (mass_draw_kernel
-                              // follows)
   uint32_t row_info[kKernargRows];  // RowFlags | penalty row << 8
 };
 
@@ -345,8 +341,9 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
                        void *start_event = nullptr, void *stop_event = nullptr);
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream);
-int launch_mass_draw(const SampleLaunch &a, uint32_t dtype, void *stream);
-int launch_residual_draw(const SampleLaunch &a, uint32_t dtype, void *stream);
+// Rows with no cut (grid rows x per_row: per_row = chunks when the launch
+// has drafted uncut rows, else 1).
+int launch_uncut(const SampleLaunch &a, uint32_t dtype, uint32_t per_row, void *stream);
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream);
 int launch_accept_tree(const AcceptTreeLaunch &a, void *stream);

@@ -109,6 +109,7 @@ struct __align__(16) SelectLds {
   uint32_t wcount[kWaves];
   uint64_t wj[kWaves][8];
   uint64_t wl[kWaves];
+  uint64_t slices[kWaves * 8];  // an uncut row's slice masses
   float wf[kWaves];
   uint32_t wu[kWaves];
   uint32_t wu2[kWaves];
@@ -639,8 +640,7 @@ __device__ __forceinline__ uint32_t row_draft(const SampleLaunch &a, const RowPa
 // the first sparse candidate that lists it (sampling.metal:703-708); the
 // merge stages the row's 16 candidates in s.cids/s.cprobs.
 // A sampled row with no min-p, top-k or top-p cut: it keeps every admitted
-// token. In a launch that mixes such rows with cut ones (a.uncut_rows), the
-// merges finish only the cut rows and mass_draw_kernel the uncut ones.
+// token. The merges and stages skip such rows; uncut_kernel draws them.
 __device__ __forceinline__ bool uncut_row(const RowParams &rp) {
   return (rp.flags & kRowSampled) && !(rp.flags & (kRowMinP | kRowTopK | kRowTopP));
 }
@@ -1759,8 +1759,8 @@ __device__ __forceinline__ void merge_row(const SampleLaunch &a,
                                           const RowParams &rp, uint32_t row,
                                           Lds &s) {
   const uint32_t S = a.chunks, tid = threadIdx.x;
-  if (a.uncut_rows && uncut_row(rp)) {
-    // mass_draw_kernel draws it; no stage may pick it up.
+  if (uncut_row(rp)) {
+    // The uncut kernel draws it; no stage may pick it up.
     if (tid == 0) a.states[row].stage = kStageDone;
     return;
   }
@@ -1791,6 +1791,73 @@ __device__ __forceinline__ void merge_row(const SampleLaunch &a,
 // ---- the single-pass selection kernel -------------------------------------
 
 #if JF_IN(1)
+// A row that keeps every admitted token: the chunk's summary for the uncut
+// kernel instead of candidates. Its maximum, whether it admits a token, its
+// admitted (non-NaN) count, and its exact fixed-point mass against its own
+// maximum (every value of the chunk is at most that maximum): per slice in
+// partial slots v[1 + g] (slice g = load g / kWaves of wave g % kWaves, 64 x
+// VEC consecutive tokens) and in total in v[0]. `side` holds the penalized
+// tokens whose own registers are dropped (NaN), so every token counts once;
+// their weights join their slices through LDS. s.slices is zero on entry
+// (cleared before the block's last barrier). Block-uniform.
+template <int DT, class L>
+__device__ __forceinline__ void uncut_summary(const float (&xs)[Geo<DT>::TPL],
+                                              const SideEntries &side, uint32_t base,
+                                              float bmax, uint32_t badm, float inv_t, L &s,
+                                              BlockHeader *hdr, StagePartial *part) {
+  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS, SLAB = Geo<DT>::SLAB;
+  constexpr uint32_t G = LOADS * kWaves;
+  static_assert(LOADS % 4 == 0, "loads in groups of four");
+  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  uint32_t n = 0;
+  // Four loads at a time (fewer live registers than all of them at once).
+#pragma unroll
+  for (int h = 0; h < LOADS / 4; ++h) {
+    uint64_t lv[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      lv[jj] = 0;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float x = xs[(h * 4 + jj) * VEC + e];
+        lv[jj] += quantized_weight(x, bmax, inv_t);
+        n += x == x;
+      }
+    }
+    // Lane l holds the wave's sum of load h * 4 + l / 16.
+    const uint64_t sl = wave_sums_u64<4>(lv);
+    if (lane % 16 == 0)
+      atomicAdd((unsigned long long *)&s.slices[(h * 4 + lane / 16) * kWaves + w],
+                (unsigned long long)sl);
+  }
+#pragma unroll
+  for (int k = 0; k < kSideEntries; ++k) {
+    const float x = side.val[k];
+    n += x == x;
+    if (side.tok[k] != kNoToken) {
+      const uint32_t o = side.tok[k] - base;
+      const uint32_t g = (o / SLAB) * kWaves + (o % SLAB) / VEC / 64;
+      atomicAdd((unsigned long long *)&s.slices[g],
+                (unsigned long long)quantized_weight(x, bmax, inv_t));
+    }
+  }
+  n = wave_sum_u32(n);
+  if (lane == 0) s.wcount[w] = n;
+  __syncthreads();
+  if (w == 0) {
+    const uint64_t v = lane < G ? s.slices[lane] : 0ull;
+    if (lane < G) part->v[1 + lane] = v;
+    const uint64_t total = wave_sum_u64(v);
+    if (lane == 0) {
+      hdr->maximum = bmax;
+      hdr->admitted = badm;
+      hdr->count = s.wcount[0] + s.wcount[1] + s.wcount[2] + s.wcount[3];
+      hdr->overflow = 0;
+      part->v[0] = total;
+    }
+  }
+}
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
   constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
@@ -1870,12 +1937,18 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
       s.wu[w] = wany;
       s.wu2[w] = wth;
     }
+    if (uncut_row(rp) && tid < kWaves * 8) s.slices[tid] = 0;
     __syncthreads();
     const float bmax = __builtin_fmaxf(
         __builtin_fmaxf(__builtin_fmaxf(s.wf[0], s.wf[1]),
                         __builtin_fmaxf(s.wf[2], s.wf[3])),
         -3.402823466e38f);
     const uint32_t badm = s.wu[0] | s.wu[1] | s.wu[2] | s.wu[3];
+    if (uncut_row(rp)) {
+      uncut_summary<DT>(xs, side, chunk * CHUNK, bmax, badm, rp.inv_t, s, hdr,
+                        a.partials + (uint64_t)row * S + chunk);
+      return;
+    }
     const uint32_t tk =
         bound ? min(min(s.wu2[0], s.wu2[1]), min(s.wu2[2], s.wu2[3])) : 0u;
     uint32_t thr = tk;
@@ -1956,6 +2029,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
 struct __align__(16) FastLds {
   uint32_t bm[kThreads];  // bit i of bm[t]: register i of thread t is dropped
   uint64_t stage[kWaves][kWaveCandidates];
+  uint64_t slices[kWaves * 8];  // an uncut row's slice masses
   uint32_t wcount[kWaves];
   float wf[kWaves];
   uint32_t wu[kWaves];
@@ -2161,8 +2235,11 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   // (a barrier waits for every outstanding scalar load); its wait sits at the
   // first use. The compiler itself would read it with vector loads, since it
   // cannot rule out that this kernel writes the records.
+  // A row with no cut reads its temperature from the record too (a
+  // uniform launch's preloaded policy leaves it out).
+  const bool uncut = (flags & kRowSampled) && !(flags & (kRowMinP | kRowTopK | kRowTopP));
   RowPolicyRegs prr{};
-  if (!uni) prr = issue_row_policy(a.params + row);
+  if (!uni || uncut) prr = issue_row_policy(a.params + row);
   auto row_policy = [&]() -> RowParams {
     if (!uni) return wait_row_policy(prr);
     RowParams r{};
@@ -2348,6 +2425,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     s.wu[w] = wany;
     s.wu2[w] = wth;
   }
+  if (uncut && tid < kWaves * 8) s.slices[tid] = 0;
   __syncthreads();
   const float bmax = __builtin_fmaxf(
       __builtin_fmaxf(__builtin_fmaxf(s.wf[0], s.wf[1]),
@@ -2356,13 +2434,11 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   const uint32_t badm = s.wu[0] | s.wu[1] | s.wu[2] | s.wu[3];
   const uint32_t tk =
       bound ? min(min(s.wu2[0], s.wu2[1]), min(s.wu2[2], s.wu2[3])) : 0u;
-  if (f.mass_only) {
-    // The launch's sampled rows keep every admitted token: the chunk's
-    // maximum and admission are all the mass-and-draw launch reads.
-    if (tid == 0) {
-      hdr->maximum = bmax;
-      hdr->admitted = badm;
-    }
+  if (uncut) {
+    // The row keeps every admitted token: the uncut kernel's chunk summary.
+    const float inv_t = uni ? wait_row_policy(prr).inv_t : rp.inv_t;
+    uncut_summary<DT>(xs, side, base, bmax, badm, inv_t, s, hdr,
+                      a.partials + (uint64_t)row * S + chunk);
     return;
   }
   uint32_t thr = tk;
@@ -2614,7 +2690,7 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     const BlockHeader *headers, const uint64_t *cands, const RowParams *params,
     const float *uniforms, const uint32_t *uniform_index, uint32_t S,
     uint32_t uniform_offset, uint32_t uniform_stride, uint32_t drafted_rows,
-    uint32_t uncut_rows, SampleLaunch a) {
+    SampleLaunch a) {
   Lds &s = g_small_lds;
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
   // Every address of the row, computed once and held in vector registers:
@@ -2692,8 +2768,8 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
       cpr = a.cand_probs[(uint64_t)rp.cand_index * 16 + tid];
     }
   }
-  if (uncut_rows && uncut_row(rp)) {
-    // mass_draw_kernel draws it.
+  if (uncut_row(rp)) {
+    // The uncut kernel draws it.
     if (tid == 0) a.states[row].stage = kStageDone;
     return;
   }
@@ -3359,172 +3435,132 @@ __device__ __forceinline__ uint32_t pick_slice(uint64_t vg, uint32_t G, uint64_t
   return g;
 }
 
-// Rows that keep every admitted token (no min-p, top-k or top-p cut): the
-// draw's passes after a select pass that wrote only the chunk maxima.
-// Partial slots per (row, chunk): v[0] the chunk's mass and v[1 + g] its
-// slices' masses (slice g = load g / kWaves of wave g % kWaves, 64 x VEC
-// consecutive tokens, so g runs in id order); v[kDraftSlot] the draft
-// token's weight; v[kResidualSlot] and v[kResidualSlot + 1 + g] the same
-// sums over residual weights.
+// ---- rows that keep every admitted token -----------------------------------
+//
+// A sampled row with no min-p, top-k or top-p cut keeps every admitted token.
+// The select pass left, per chunk, the chunk's maximum m_c, its admitted
+// count and its exact fixed-point mass S_c against m_c (partials v[0]). The
+// row's mass is W = sum of T_c = floor(S_c * R_c / 2^32) with the rescale
+// R_c = floor(exp((m_c - M) / T) * 2^32), so the mass costs one read of the
+// logits. One block per row draws: the chunk whose running T_c passes
+// u * W, that chunk reloaded, and its first token (id order) whose running
+// mass P has floor(P * R_c / 2^32) past the remainder (sampling.metal:694-829
+// on these weights). A drafted row's blocks, one per chunk, sum the residual
+// max(floor(w * R_c / 2^32) - floor(W * q), 0) per slice; the row's last
+// block draws from them, or plainly when no residual mass remains, and
+// writes p(draft). Chunk 0's block writes the row's kept outputs. Greedy
+// rows take the argmax of the chunk bests when no merge runs.
+//
+// Partial slots per (row, chunk): v[0] S_c; v[kDraftSlot] the draft token's
+// float weight against m_c; v[kResidualSlot] the chunk's residual mass and
+// v[kResidualSlot + 1 + g] its slices' (slice g = load g / kWaves of wave
+// g % kWaves, 64 x VEC consecutive tokens, so g runs in id order).
+struct __align__(16) UncutLds {
+  PrepLds prep;
+  uint64_t wj[kWaves][8];
+  uint64_t wl[kWaves];
+  uint32_t cids[16];
+  float cprobs[16];
+  float cmax[kMaxChunks];       // the row's chunk maxima
+  uint64_t cscale[kMaxChunks];  // R_c
+  uint64_t ctot[kMaxChunks];    // T_c
+  uint32_t ccount[kMaxChunks];  // admitted (non-NaN) tokens per chunk
+  uint64_t slices[kWaves * 8];  // one chunk's slice masses
+  float row_max;
+  uint64_t row_mass;
+  uint32_t row_admitted;
+  uint32_t row_kept;
+  float pd;                     // p(draft)
+  uint32_t residual;
+  uint32_t last;
+  uint32_t sel_bin;
+  uint64_t sel_excl;
+  uint32_t slice;
+  uint64_t slice_within;
+};
+
+#if JF_IN(4)
 constexpr uint32_t kDraftSlot = 40;
 constexpr uint32_t kResidualSlot = 63;
 
-// One block per (row, chunk) sums its chunk's fixed-point weights against
-// the row maximum; the row's last block to arrive picks the chunk and slice
-// whose running mass passes u * mass and walks the slice in id order
-// (sampling.metal:694-829 over the whole row; the same members, weights and
-// walk as the Mass3 and Walk stages, so the token is the same). A drafted
-// row instead leaves its mass and draft weight in its state for
-// residual_draw_kernel (the Mass3 stage's hand-over to the Draw stage).
-// Greedy rows take the argmax of the chunk bests in their chunk-0 block.
-#if JF_IN(4)
+// The reported probability of a token of float weight w (against its
+// chunk's maximum) in a chunk of rescale R: w R / (W 2^-12) in double.
+__device__ __forceinline__ float uncut_probability(float w, uint64_t R, uint64_t W) {
+  return W ? (float)(((double)w * (double)R) / ((double)W * 0x1p-12)) : 0.0f;
+}
+
+// The first kept_cap admitted tokens of the row in id order with their
+// probabilities (chunk 0's block; block-uniform).
 template <int DT>
-__global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
+__device__ __forceinline__ void uncut_kept(const SampleLaunch &a, const RowParams &rp, uint32_t row,
+                           UncutLds &s, uint64_t W) {
+  constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
+                SLAB = Geo<DT>::SLAB;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  const uint32_t cap = a.kept_cap, tid = threadIdx.x;
+  uint32_t *ids = a.out_kept_ids + (uint64_t)row * cap;
+  float *probs = a.out_kept_probs + (uint64_t)row * cap;
+  uint32_t written = 0;
+  for (uint32_t c = 0; c < a.chunks && written < cap; ++c) {
+    if (s.ccount[c] == 0) continue;
+    float xs[TPL];
+    load_chunk<DT>(a, rp, row, c, s, xs);
+    const float mc = s.cmax[c];
+    const uint64_t R = s.cscale[c];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      uint32_t n = 0;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) n += xs[j * VEC + e] == xs[j * VEC + e];
+      uint64_t total;
+      uint32_t pos = written + (uint32_t)block_excl_scan_u64(n, s, &total);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float x = xs[j * VEC + e];
+        if (x == x) {
+          if (pos < cap) {
+            ids[pos] = c * CHUNK + j * SLAB + tid * VEC + e;
+            probs[pos] = uncut_probability(weight_of(x, mc, rp.inv_t), R, W);
+          }
+          ++pos;
+        }
+      }
+      written += (uint32_t)total;
+    }
+  }
+}
+
+// The plain draw of an uncut row from its chunk masses (one block; block-
+// uniform): the chunk, its reload together with its slice masses (which the
+// select pass wrote), the slice, the token.
+template <int DT>
+__device__ __forceinline__ void uncut_draw(const SampleLaunch &a, const RowParams &rp,
+                                           uint32_t row, UncutLds &s, uint64_t W, float u) {
   constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
                 SLAB = Geo<DT>::SLAB;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves;
-  __shared__ DrawLds s;
-  const uint32_t S = a.chunks;
-  const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
-  const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  // The launch carries drafted rows: every row's state says whether the
-  // residual launch has work for it.
-  const bool drafts = a.draft_tokens && a.drafted_rows;
-  // Every row of the launch sampled (no greedy row whose chunk need not be
-  // read): the chunk's requests go out before the row's policy arrives.
-  const bool all_sampled = a.all_sampled != 0;
-  const RowParams rp = a.params[row];
-  // A mixed launch: the merge finished every other row.
-  if (a.uncut_rows && !uncut_row(rp)) return;
-  // Requested up front: the chunk summaries (every wave, one lane per
-  // chunk; the select launch ended before this one began), the draft token
-  // and the row's uniform, which only the last block uses.
-  const BlockHeader *hb = a.headers + (uint64_t)row * S;
-  float hm = -3.402823466e38f, hv = -__builtin_inff();
-  uint32_t ha = 0, hi = kNoToken;
-  if (lane < S) {
-    hm = hb[lane].maximum;
-    ha = hb[lane].admitted;
-  }
-  const uint32_t draft = row_draft(a, rp);
-  if (!all_sampled && !(rp.flags & kRowSampled)) {
-    // Greedy (sampling.metal:1478-1512): the largest chunk best, the lowest
-    // id among equals.
-    if (chunk == 0 && tid < 64) {
-      if (lane < S) {
-        hv = hb[lane].best_value;
-        hi = hb[lane].best_id;
-      }
-      wave_argmax(hv, hi);
-      if (tid == 0) {
-        write_result(a, row, hi, 0.0f, 0);
-        if (drafts) a.states[row].stage = kStageDone;
-      }
-    }
-    return;
-  }
-  const float u = row_uniform(a, row);
-  float xs[TPL];
-  load_chunk<DT>(a, rp, row, chunk, s, xs);
-  const float M = wave_max_f32(hm);
-  const uint32_t admitted = wave_sum_u32(ha);
-  if (admitted == 0 || M == __builtin_inff()) {
-    // Nothing to draw from: the sentinel, as the merge writes it.
-    if (chunk == 0 && tid == 0) {
-      write_result(a, row, kNoToken, 0.0f, 0);
-      if (drafts) a.states[row].stage = kStageDone;
-    }
-    return;
-  }
-  // Each wave's mass per load, then the chunk's. A NaN (not admitted) token
-  // weighs zero.
-  const float inv_t = rp.inv_t;
-  StagePartial *parts = a.partials + (uint64_t)row * S;
-  uint64_t lv[LOADS];
-#pragma unroll
-  for (int j = 0; j < LOADS; ++j) {
-    lv[j] = 0;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) lv[j] += quantized_weight(xs[j * VEC + e], M, inv_t);
-  }
-  // Lane l holds the wave's sum of load l / (64 / LOADS); the wave's total
-  // adds one lane of each load.
-  constexpr uint32_t GL = 64 / LOADS;
-  const uint64_t sl = wave_sums_u64<LOADS>(lv);
-  if (lane % GL == 0) st_dev(&parts[chunk].v[1 + (lane / GL) * kWaves + w], sl);
-  uint64_t total = sl;
-#pragma unroll
-  for (uint32_t m = GL; m < 64; m *= 2) total += shfl_xor_u64(total, (int)m);
-  // The draft token's weight, from the thread that holds it (zero when the
-  // row does not admit it).
-  if (draft < a.vocabulary && draft / CHUNK == chunk) {
-    const uint32_t o = draft - chunk * CHUNK;
-    if (tid == (o % SLAB) / VEC) {
-      const uint32_t i = (o / SLAB) * VEC + o % VEC;
-      float xd = 0.0f;
-#pragma unroll
-      for (int k = 0; k < TPL; ++k) xd = (uint32_t)k == i ? xs[k] : xd;
-      st_dev(&parts[chunk].v[kDraftSlot], (uint64_t)f2u(weight_of(xd, M, inv_t)));
-    }
-  }
-  if (lane == 0) s.wl[w] = total;
-  __syncthreads();
-  if (tid == 0) st_dev(&parts[chunk].v[0], s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3]);
-  if (!arrive_last(a.counters + row, S, s)) return;
-
-  // The last block: the chunk masses in id order, the target u * mass, the
-  // chunk whose running mass passes it, the slice inside that chunk.
-  if (tid < 64) {
-    const bool in = tid < S;
-    const uint64_t v = in ? ld_dev(&parts[tid].v[0]) : 0ull;
-    const uint64_t incl = wave_incl_scan_u64(v);
-    const uint64_t mass = readlane_u64(incl, 63);
-    uint64_t within = 0;
-    uint32_t c = 0;
-    if (draft != kNoToken) {
-      // Drafted: the residual launch draws (the Mass3 stage's hand-over).
-      // Field by field: the fields residual_draw_kernel reads.
-      if (tid == 0) {
-        RowState *ns = a.states + row;
-        if (mass == 0) {
-          write_result(a, row, kNoToken, 0.0f, 0);
-          ns->stage = kStageDone;
-        } else {
-          ns->maximum = M;
-          ns->mass3 = mass;
-          ns->drafted = 1;
-          ns->draft_w = draft < a.vocabulary
-                            ? u2f((uint32_t)ld_dev(&parts[draft / CHUNK].v[kDraftSlot]))
-                            : 0.0f;
-          ns->stage = kStageDraw;
-        }
-      }
-    } else if (mass != 0) {
-      uint64_t target = floor_mul(mass, u);
-      if (target >= mass) target = mass - 1;
-      // incl at the last lane is mass > target: some lane passes it.
-      c = (uint32_t)__builtin_ctzll(ballot(in && incl > target));
-      within = target - readlane_u64(incl - v, c);
-    }
-    if (tid == 0) {
-      s.u64a = draft != kNoToken ? 0ull : mass;
-      s.sel_excl = within;
+  const uint32_t S = a.chunks, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (w == 0) {
+    const bool in = lane < S;
+    const uint64_t T = in ? s.ctot[lane] : 0ull;
+    const uint64_t incl = wave_incl_scan_u64(T);
+    uint64_t target = floor_mul(W, u);
+    if (target >= W) target = W - 1;
+    // incl at the last lane is W > target: some lane passes it.
+    const uint32_t c = (uint32_t)__builtin_ctzll(ballot(in && incl > target));
+    const uint64_t within = target - readlane_u64(incl - T, c);
+    if (lane == 0) {
       s.sel_bin = c;
-      if (draft == kNoToken) {
-        if (mass == 0) write_result(a, row, kNoToken, 0.0f, 0);
-        if (drafts) a.states[row].stage = kStageDone;
-      }
+      // The running mass inside chunk c (against m_c) that the token's
+      // prefix must pass: floor(P * R_c / 2^32) > within <=> P > this.
+      s.sel_excl = unscaled_bound(within, s.cscale[c]);
     }
   }
   __syncthreads();
-  const uint64_t mass = s.u64a;
   const uint32_t c = s.sel_bin;
-  if (mass == 0) return;
-  // Chunk c again (block-wide: a penalized row stages its table entries),
-  // requested together with its slice sums; then the slice, and only that
-  // slice's wave weighs its VEC tokens per lane.
   uint64_t vg = 0;
-  if (w == 0 && lane < G) vg = ld_dev(&parts[c].v[1 + lane]);
+  if (w == 0 && lane < G) vg = a.partials[(uint64_t)row * S + c].v[1 + lane];
+  float xs[TPL];
   load_chunk<DT>(a, rp, row, c, s, xs);
   if (w == 0) {
     uint64_t wi = s.sel_excl;
@@ -3535,54 +3571,108 @@ __global__ __launch_bounds__(kThreads) void mass_draw_kernel(SampleLaunch a) {
     }
   }
   __syncthreads();
-  const uint32_t g = s.slice;
-  const uint64_t within = s.slice_within;
-  const uint32_t jg = g / kWaves;
+  const uint32_t g = s.slice, jg = g / kWaves;
   if (w == g % kWaves) {
+    const float mc = s.cmax[c];
     uint64_t q[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       float x = 0.0f;
 #pragma unroll
       for (int j = 0; j < LOADS; ++j) x = (uint32_t)j == jg ? xs[j * VEC + e] : x;
-      q[e] = quantized_weight(x, M, inv_t);
+      q[e] = quantized_weight(x, mc, rp.inv_t);
     }
     uint32_t e_hit;
-    if (lane == slice_hit<VEC>(q, within, e_hit))
-      write_result(a, row, c * CHUNK + jg * SLAB + tid * VEC + e_hit, 0.0f, 0);
+    if (lane == slice_hit<VEC>(q, s.slice_within, e_hit))
+      write_result(a, row, c * CHUNK + jg * SLAB + tid * VEC + e_hit, s.pd, s.row_kept);
   }
 }
-#endif
 
-// Drafted rows that keep every admitted token: the residual draw over the
-// row (sampling.metal:694-829 with candidate weights max(w - q * mass, 0),
-// the Draw and Walk stages' arithmetic). One block per (row, chunk) sums its
-// residual weights per slice; the row's last block draws from the residual
-// weights, or from the plain weights when the residual has no mass, and
-// writes p(draft) = w(draft) / mass (sampling.metal:828-829).
-#if JF_IN(4)
 template <int DT>
-__global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a) {
+__global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_t per_row) {
   constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
                 SLAB = Geo<DT>::SLAB;
-  constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves;
-  __shared__ DrawLds s;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves, GL = 64 / LOADS;
+  __shared__ UncutLds s;
   const uint32_t S = a.chunks;
-  const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
+  const uint32_t row = blockIdx.x / per_row, chunk = blockIdx.x % per_row;
   const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const RowState st = a.states[row];
-  if (st.stage != kStageDraw) return;
   const RowParams rp = a.params[row];
+  const BlockHeader *hb = a.headers + (uint64_t)row * S;
+  StagePartial *parts = a.partials + (uint64_t)row * S;
+  if (!(rp.flags & kRowSampled)) {
+    // Greedy (sampling.metal:1478-1512), when no merge runs: the largest
+    // chunk best, the lowest id among equals.
+    if (a.finish_greedy && chunk == 0 && tid < 64) {
+      float hv = -__builtin_inff();
+      uint32_t hi = kNoToken;
+      if (lane < S) {
+        hv = hb[lane].best_value;
+        hi = hb[lane].best_id;
+      }
+      wave_argmax(hv, hi);
+      if (tid == 0) write_result(a, row, hi, 0.0f, 0);
+    }
+    return;
+  }
+  if (!uncut_row(rp)) return;  // the merge's
+  const uint32_t draft = row_draft(a, rp);
+  const bool drafted = draft != kNoToken;
+  if (!drafted && chunk != 0) return;
+  const float inv_t = rp.inv_t;
+  // Requested before the chunk summaries are waited for.
+  const float u = row_uniform(a, row);
+  // The row's chunk summaries (S <= 64: one per lane of wave 0).
+  if (w == 0) {
+    const bool in = lane < S;
+    const float m = in ? hb[lane].maximum : -3.402823466e38f;
+    const uint32_t adm = in ? hb[lane].admitted : 0u;
+    const uint32_t cnt = in ? hb[lane].count : 0u;
+    const uint64_t mass = in ? parts[lane].v[0] : 0ull;
+    const float M = wave_max_f32(m);
+    const uint64_t R = in ? chunk_scale(m, M, inv_t) : 0ull;
+    const uint64_t T = scale_down(mass, R);
+    const uint64_t W = wave_sum_u64(T);
+    const uint32_t admitted = wave_sum_u32(adm), kept = wave_sum_u32(cnt);
+    if (in) {
+      s.cmax[lane] = m;
+      s.cscale[lane] = R;
+      s.ctot[lane] = T;
+      s.ccount[lane] = cnt;
+    }
+    if (lane == 0) {
+      s.row_max = M;
+      s.row_mass = W;
+      // Nothing admitted, or a +inf maximum: the sentinel with nothing kept.
+      const bool none = admitted == 0 || M == __builtin_inff();
+      s.row_admitted = none ? 0u : 1u;
+      s.row_kept = none ? 0u : kept;
+      s.pd = 0.0f;
+    }
+  }
+  __syncthreads();
+  const uint64_t W = s.row_mass;
+  if (chunk == 0 && a.out_kept_ids && s.row_admitted && a.kept_cap)
+    uncut_kept<DT>(a, rp, row, s, W);
+  if (!s.row_admitted || W == 0) {
+    // The sentinel (a row of -inf keeps every token at probability 0).
+    if (chunk == 0 && tid == 0) write_result(a, row, kNoToken, 0.0f, s.row_kept);
+    return;
+  }
+  if (!drafted) {
+    uncut_draw<DT>(a, rp, row, s, W, u);
+    return;
+  }
+
+  // A drafted row: this chunk's residual masses per slice.
   float qv[TPL];
   if (a.dense_q) load_dense_q<DT>(a, rp, chunk, qv);
   float xs[TPL];
   load_chunk<DT>(a, rp, row, chunk, s, xs);
   stage_candidates(a, rp, s);
-  const float u = row_uniform(a, row);
-  const float M = st.maximum, inv_t = rp.inv_t;
-  const uint64_t mass3 = st.mass3;
+  const float mc = s.cmax[chunk];
+  const uint64_t Rc = s.cscale[chunk];
   const uint32_t lane_base = chunk * CHUNK + tid * VEC;
-  StagePartial *parts = a.partials + (uint64_t)row * S;
   uint64_t lv[LOADS];
 #pragma unroll
   for (int j = 0; j < LOADS; ++j) {
@@ -3591,50 +3681,61 @@ __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a)
     for (int e = 0; e < VEC; ++e) {
       const int i = j * VEC + e;
       const float q = a.dense_q ? qv[i] : draft_q(a, rp, lane_base + j * SLAB + e, s);
-      lv[j] += residual_of(quantized_weight(xs[i], M, inv_t), mass3, q);
+      lv[j] += residual_of(scale_down(quantized_weight(xs[i], mc, inv_t), Rc), W, q);
     }
   }
-  constexpr uint32_t GL = 64 / LOADS;
   const uint64_t sl = wave_sums_u64<LOADS>(lv);
   if (lane % GL == 0)
     st_dev(&parts[chunk].v[kResidualSlot + 1 + (lane / GL) * kWaves + w], sl);
   uint64_t total = sl;
 #pragma unroll
   for (uint32_t m = GL; m < 64; m *= 2) total += shfl_xor_u64(total, (int)m);
+  // The draft token's float weight, from the thread that holds it.
+  if (draft < a.vocabulary && draft / CHUNK == chunk) {
+    const uint32_t o = draft - chunk * CHUNK;
+    if (tid == (o % SLAB) / VEC) {
+      const uint32_t i = (o / SLAB) * VEC + o % VEC;
+      float xd = 0.0f;
+#pragma unroll
+      for (int k = 0; k < TPL; ++k) xd = (uint32_t)k == i ? xs[k] : xd;
+      st_dev(&parts[chunk].v[kDraftSlot], (uint64_t)f2u(weight_of(xd, mc, inv_t)));
+    }
+  }
   if (lane == 0) s.wl[w] = total;
   __syncthreads();
   if (tid == 0)
     st_dev(&parts[chunk].v[kResidualSlot], s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3]);
   if (!arrive_last(a.counters + row, S, s)) return;
 
-  // The last block: residual weights when they have mass, else the plain
-  // weights (whose sums the mass launch left at v[0] and v[1 + g]).
-  if (tid < 64) {
-    const bool in = tid < S;
-    const uint64_t rv = in ? ld_dev(&parts[tid].v[kResidualSlot]) : 0ull;
-    const uint64_t pv = in ? ld_dev(&parts[tid].v[0]) : 0ull;
-    const bool residual = wave_sum_u64(rv) != 0;
-    const uint64_t v = residual ? rv : pv;
-    const uint64_t incl = wave_incl_scan_u64(v);
+  // The row's last block: p(draft), then the residual draw when it has mass.
+  if (w == 0) {
+    const bool in = lane < S;
+    const uint64_t rv = in ? ld_dev(&parts[lane].v[kResidualSlot]) : 0ull;
+    const uint64_t incl = wave_incl_scan_u64(rv);
     const uint64_t tot = readlane_u64(incl, 63);
     uint64_t target = floor_mul(tot, u);
-    if (target >= tot) target = tot - 1;
-    const uint32_t c = (uint32_t)__builtin_ctzll(ballot(in && incl > target));
-    // Wave-wide: lane c's running sum is read from every lane's registers.
-    const uint64_t before = readlane_u64(incl - v, c);
-    if (tid == 0) {
+    if (tot && target >= tot) target = tot - 1;
+    const uint32_t c = tot ? (uint32_t)__builtin_ctzll(ballot(in && incl > target)) : 0u;
+    const uint64_t before = readlane_u64(incl - rv, c);
+    if (lane == 0) {
+      s.residual = tot ? 1u : 0u;
+      s.sel_bin = c;
       s.sel_excl = target - before;
-      s.sel_bin = c | (residual ? 1u << 16 : 0u);
-      a.states[row].stage = kStageDone;
+      if (draft < a.vocabulary) {
+        const uint32_t cd = draft / CHUNK;
+        s.pd = uncut_probability(u2f((uint32_t)ld_dev(&parts[cd].v[kDraftSlot])),
+                                 s.cscale[cd], W);
+      }
     }
   }
   __syncthreads();
-  const uint32_t c = s.sel_bin & 0xffu;
-  const bool residual = (s.sel_bin >> 16) != 0;
-  // Chunk c again, requested together with its slice sums.
+  if (!s.residual) {
+    uncut_draw<DT>(a, rp, row, s, W, u);
+    return;
+  }
+  const uint32_t c = s.sel_bin;
   uint64_t vg = 0;
-  if (w == 0 && lane < G)
-    vg = ld_dev(&parts[c].v[(residual ? kResidualSlot + 1 : 1u) + lane]);
+  if (w == 0 && lane < G) vg = ld_dev(&parts[c].v[kResidualSlot + 1 + lane]);
   load_chunk<DT>(a, rp, row, c, s, xs);
   if (w == 0) {
     uint64_t wi = s.sel_excl;
@@ -3645,10 +3746,10 @@ __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a)
     }
   }
   __syncthreads();
-  const uint32_t g = s.slice;
-  const uint64_t within = s.slice_within;
-  const uint32_t jg = g / kWaves;
+  const uint32_t g = s.slice, jg = g / kWaves;
   if (w == g % kWaves) {
+    const float mcc = s.cmax[c];
+    const uint64_t Rcc = s.cscale[c];
     const uint32_t tbase = c * CHUNK + jg * SLAB + tid * VEC;
     uint64_t q[VEC];
 #pragma unroll
@@ -3656,17 +3757,14 @@ __global__ __launch_bounds__(kThreads) void residual_draw_kernel(SampleLaunch a)
       float x = 0.0f;
 #pragma unroll
       for (int j = 0; j < LOADS; ++j) x = (uint32_t)j == jg ? xs[j * VEC + e] : x;
-      const uint64_t wq = quantized_weight(x, M, inv_t);
-      // Past the vocabulary (a partial last chunk) the weight is zero and
-      // no q is read: a dense q row ends at the vocabulary.
+      // Past the vocabulary (a partial last chunk) the weight is zero and no
+      // q is read: a dense q row ends at the vocabulary.
       const float qe = tbase + e < a.vocabulary ? draft_q(a, rp, tbase + e, s) : 0.0f;
-      q[e] = residual ? residual_of(wq, mass3, qe) : wq;
+      q[e] = residual_of(scale_down(quantized_weight(x, mcc, inv_t), Rcc), W, qe);
     }
     uint32_t e_hit;
-    if (lane == slice_hit<VEC>(q, within, e_hit)) {
-      const double scale = (double)mass3 * 0x1p-44;
-      write_result(a, row, tbase + e_hit, (float)((double)st.draft_w / scale), 0);
-    }
+    if (lane == slice_hit<VEC>(q, s.slice_within, e_hit))
+      write_result(a, row, tbase + e_hit, s.pd, s.row_kept);
   }
 }
 #endif
@@ -3829,23 +3927,12 @@ int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream) {
 #endif
 
 #if JF_IN(4)
-int launch_mass_draw(const SampleLaunch &a, uint32_t dtype, void *stream) {
-  const dim3 grid(a.rows * a.chunks), block(kThreads);
+int launch_uncut(const SampleLaunch &a, uint32_t dtype, uint32_t per_row, void *stream) {
+  const dim3 grid(a.rows * per_row), block(kThreads);
   if (dtype == 0)
-    hipLaunchKernelGGL(mass_draw_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(uncut_kernel<0>, grid, block, 0, (hipStream_t)stream, a, per_row);
   else
-    hipLaunchKernelGGL(mass_draw_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
-  return (int)hipGetLastError();
-}
-#endif
-
-#if JF_IN(4)
-int launch_residual_draw(const SampleLaunch &a, uint32_t dtype, void *stream) {
-  const dim3 grid(a.rows * a.chunks), block(kThreads);
-  if (dtype == 0)
-    hipLaunchKernelGGL(residual_draw_kernel<0>, grid, block, 0, (hipStream_t)stream, a);
-  else
-    hipLaunchKernelGGL(residual_draw_kernel<1>, grid, block, 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(uncut_kernel<1>, grid, block, 0, (hipStream_t)stream, a, per_row);
   return (int)hipGetLastError();
 }
 #endif
@@ -3858,7 +3945,7 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream) {
     hipLaunchKernelGGL(kernel, grid, block, 0, st, a.headers, (const uint64_t *)a.cands,
                        a.params, a.uniforms, a.uniform_index, a.chunks,
                        (uint32_t)a.uniform_offset, (uint32_t)a.uniform_stride,
-                       a.draft_tokens && !a.row_indexed ? a.drafted_rows : 0u, a.uncut_rows, a);
+                       a.draft_tokens && !a.row_indexed ? a.drafted_rows : 0u, a);
   };
   if (dtype == 0)
     go(merge_small_kernel<0>);

@@ -586,42 +586,38 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   // A launch of greedy rows only is finished inside the fast selection.
   const bool fused = fast && !any_sampled;
   // Sampled rows that keep every admitted token (no min-p, top-k or top-p
-  // cut) and carry no draft need only the row maximum and the chunk masses:
-  // the selection writes chunk maxima, then one mass-and-draw launch finishes
-  // every row (no merge, no stages).
+  // cut): the selection writes their chunk masses and uncut_kernel draws
+  // them; the merge and the stages finish the other rows and skip these, so
+  // only the cut rows decide the merge and the stages.
   constexpr uint32_t kCuts = jf::kRowMinP | jf::kRowTopK | jf::kRowTopP;
-  bool any_uncut = false, any_cut = false;
-  for (uint32_t r = 0; r < rows; ++r)
-    if (params[r].flags & jf::kRowSampled) {
-      if (params[r].flags & kCuts)
-        any_cut = true;
-      else
-        any_uncut = true;
-    }
-  const bool unfiltered = fast && any_sampled && !kept && !any_cut;
-  // A launch that mixes both kinds: the merge (and the stages) finish the
-  // cut rows and skip the uncut ones, which the mass-and-draw launch then
-  // finishes; the uncut rows no longer decide the merge or the stages.
-  const bool mixed = fast && any_uncut && any_cut && !kept;
-  if (mixed) {
-    staged = need_count1 = need_topk = need_topp = false;
-    for (uint32_t r = 0; r < rows; ++r) {
-      const jf::RowParams &rp = params[r];
-      if ((rp.flags & jf::kRowSampled) && (rp.flags & kCuts) &&
-          rp.top_k > (uint32_t)jf::kBlockCandidates) {
+  bool any_uncut = false, any_cut = false, any_greedy = false, uncut_drafted = false;
+  staged = need_count1 = need_topk = need_topp = false;
+  for (uint32_t r = 0; r < rows; ++r) {
+    const jf::RowParams &rp = params[r];
+    if (!(rp.flags & jf::kRowSampled)) {
+      any_greedy = true;
+    } else if (!(rp.flags & kCuts)) {
+      any_uncut = true;
+      if (rp.draft_index != JF_NO_TOKEN) uncut_drafted = true;
+    } else {
+      any_cut = true;
+      if (rp.top_k > (uint32_t)jf::kBlockCandidates) {
         staged = true;
         need_count1 |= (rp.flags & (jf::kRowMinP | jf::kRowTopK)) != 0;
         need_topk |= (rp.flags & jf::kRowTopK) != 0;
         need_topp |= (rp.flags & jf::kRowTopP) != 0;
       }
     }
-    L.uncut_rows = 1u;
   }
+  // The merge finishes the cut rows, and the greedy rows unless the launch
+  // is all greedy and fast (fused) or has uncut rows and no cut ones (then
+  // uncut_kernel takes them).
+  const bool need_merge = !fused && (any_cut || (any_greedy && !any_uncut));
+  L.finish_greedy = any_greedy && !need_merge && !fused ? 1u : 0u;
   if (fast) {
     jf::FastLaunch F{};
     F.a = L;
     F.fuse_greedy = fused ? 1u : 0u;
-    F.mass_only = unfiltered ? 1u : 0u;
     if (a->penalties) {
       F.pen_slots = a->penalties->slots;
       F.slot_count = a->penalties->slot_count;
@@ -656,29 +652,17 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
                           a->select_done_event);
   }
   if (e != hipSuccess) return hip_fail((hipError_t)e, "select launch");
-  // The small-K merge takes launches whose sampled rows keep at most 64
-  // tokens and read sparse draft probabilities (or none).
+  // The small-K merge takes launches whose cut rows keep at most 64 tokens
+  // and read sparse draft probabilities (or none).
   bool small = !staged && !a->draft_q && a->uniform_offset <= 0xffffffffull &&
                a->uniform_stride <= 0xffffffffull;
   for (uint32_t r = 0; small && r < rows; ++r) {
     const jf::RowParams &rp = params[r];
-    if (mixed && !(rp.flags & kCuts)) continue;  // the mass-and-draw launch's
-    if ((rp.flags & jf::kRowSampled) && (!(rp.flags & jf::kRowTopK) || rp.top_k > 64u))
+    if ((rp.flags & jf::kRowSampled) && (rp.flags & kCuts) &&
+        (!(rp.flags & jf::kRowTopK) || rp.top_k > 64u))
       small = false;
   }
-  if (unfiltered) {
-    L.all_sampled = 1u;
-    for (uint32_t r = 0; r < rows; ++r)
-      if (!(params[r].flags & jf::kRowSampled)) L.all_sampled = 0u;
-    e = jf::launch_mass_draw(L, a->dtype, stream);
-    if (e != hipSuccess) return hip_fail((hipError_t)e, "mass-and-draw launch");
-    if (L.drafted_rows) {
-      e = jf::launch_residual_draw(L, a->dtype, stream);
-      if (e != hipSuccess) return hip_fail((hipError_t)e, "residual draw launch");
-    }
-    return JF_OK;
-  }
-  if (!fused) {
+  if (need_merge) {
     e = small ? jf::launch_merge_small(L, a->dtype, stream)
               : jf::launch_merge(L, a->dtype, stream);
     if (e != hipSuccess) return hip_fail((hipError_t)e, "merge launch");
@@ -695,13 +679,11 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
       if (e != hipSuccess) return hip_fail((hipError_t)e, "stage launch");
     }
   }
-  if (mixed) {
-    e = jf::launch_mass_draw(L, a->dtype, stream);
-    if (e != hipSuccess) return hip_fail((hipError_t)e, "mass-and-draw launch");
-    if (L.drafted_rows) {
-      e = jf::launch_residual_draw(L, a->dtype, stream);
-      if (e != hipSuccess) return hip_fail((hipError_t)e, "residual draw launch");
-    }
+  if (any_uncut) {
+    // One block per row; a launch with drafted uncut rows takes one per
+    // (row, chunk) for their residual pass.
+    e = jf::launch_uncut(L, a->dtype, uncut_drafted ? L.chunks : 1u, stream);
+    if (e != hipSuccess) return hip_fail((hipError_t)e, "uncut draw launch");
   }
   return JF_OK;
 }

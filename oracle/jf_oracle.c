@@ -268,6 +268,164 @@ static uint64_t quantize(float w) {
   return (uint64_t)(w * 0x1p44f);
 }
 
+/* ---- rows that keep every admitted token ------------------------------ */
+
+/* A sampled row with no min-p, top-k or top-p cut keeps every admitted
+ * token. Its mass is exact per 8192-token chunk c against the chunk's own
+ * maximum m_c,
+ *   S_c = sum over the chunk of quantize(expf((x - m_c) / T)),
+ * and each chunk's mass is rescaled to the row maximum M once:
+ *   R_c = floor(expf((m_c - M) / T) * 2^32),   T_c = floor(S_c * R_c / 2^32),
+ *   W = sum of T_c.
+ * The draw takes u * W, the chunk whose running T_c passes it, and inside
+ * that chunk the first token (id order) whose running S-mass P satisfies
+ * floor(P * R_c / 2^32) > the remainder. A drafted row draws the residual
+ * max(floor(w_q * R_c / 2^32) - floor(W * q), 0) in id order (w_q the
+ * token's quantized weight), or plainly when no residual mass remains
+ * (sampling.metal:694-829 on these weights). A token's reported probability
+ * (kept outputs, p(draft)) is its float weight w times R_c over W * 2^-12,
+ * in double: float(double(w) * double(R_c) / (double(W) * 2^-12)). One pass over the
+ * logits yields every S_c, so the GPU reads the row once. With a single
+ * chunk (V <= 8192) R = 2^32 and this is the row-maximum definition. */
+#define JFO_MASS_CHUNK 8192u
+
+static uint64_t scale_down(uint64_t x, uint64_t r) {
+  return (uint64_t)(((unsigned __int128)x * r) >> 32);
+}
+
+static int uncut_select(uint32_t V, uint32_t stop0, uint32_t stop1,
+                        const jfo_policy *p, float inv_rep, float inv_t,
+                        const jfo_row_input *in, float M, uint32_t n,
+                        jfo_row_output *out, uint32_t *kept_ids,
+                        float *kept_probs, uint32_t kept_capacity) {
+  const uint32_t C = (V + JFO_MASS_CHUNK - 1) / JFO_MASS_CHUNK;
+  float *cmax = (float *)malloc(sizeof(float) * C);
+  uint64_t *cmass = (uint64_t *)calloc(C, sizeof(uint64_t));
+  uint64_t *cscale = (uint64_t *)malloc(sizeof(uint64_t) * C);
+  uint64_t *ctot = (uint64_t *)malloc(sizeof(uint64_t) * C);
+  if (!cmax || !cmass || !cscale || !ctot) {
+    free(cmax); free(cmass); free(cscale); free(ctot);
+    return -3;
+  }
+  for (uint32_t c = 0; c < C; ++c)
+    cmax[c] = -FLT_MAX;
+  for (uint32_t t = 0; t < V; ++t) {
+    if (!admits(p, in, t, stop0, stop1))
+      continue;
+    const float v = penalized(p, inv_rep, in, t);
+    if (v > cmax[t / JFO_MASS_CHUNK])
+      cmax[t / JFO_MASS_CHUNK] = v;
+  }
+  for (uint32_t t = 0; t < V; ++t) {
+    if (!admits(p, in, t, stop0, stop1))
+      continue;
+    const float v = penalized(p, inv_rep, in, t);
+    if (!isnan(v))
+      cmass[t / JFO_MASS_CHUNK] += quantize(jfo_expf((v - cmax[t / JFO_MASS_CHUNK]) * inv_t));
+  }
+  uint64_t W = 0;
+  for (uint32_t c = 0; c < C; ++c) {
+    cscale[c] = (uint64_t)(jfo_expf((cmax[c] - M) * inv_t) * 0x1p32f);
+    ctot[c] = scale_down(cmass[c], cscale[c]);
+    W += ctot[c];
+  }
+  /* The kept set is every admitted non-NaN token, in id order. */
+  out->kept_count = n;
+  #define FLOAT_WEIGHT(t, v) jfo_expf(((v) - cmax[(t) / JFO_MASS_CHUNK]) * inv_t)
+  #define WEIGHT_OF(t, v) quantize(FLOAT_WEIGHT(t, v))
+  #define PROB_OF(t, v)                                                              \
+    (W ? (float)(((double)FLOAT_WEIGHT(t, v) * (double)cscale[(t) / JFO_MASS_CHUNK]) / \
+                 ((double)W * 0x1p-12))                                               \
+       : 0.0f)
+  if (kept_ids) {
+    uint32_t k = 0;
+    for (uint32_t t = 0; t < V && k < kept_capacity; ++t) {
+      if (!admits(p, in, t, stop0, stop1))
+        continue;
+      const float v = penalized(p, inv_rep, in, t);
+      if (isnan(v))
+        continue;
+      kept_ids[k] = t;
+      kept_probs[k] = PROB_OF(t, v);
+      ++k;
+    }
+  }
+  const int drafted = in->draft_token != JFO_NO_TOKEN;
+  if (W != 0) {
+    int drawn = 0;
+    if (drafted) {
+      /* The residual max(weight - floor(W * q), 0) in id order. */
+      uint64_t total = 0;
+      for (uint32_t t = 0; t < V; ++t) {
+        if (!admits(p, in, t, stop0, stop1))
+          continue;
+        const float v = penalized(p, inv_rep, in, t);
+        if (isnan(v))
+          continue;
+        const uint64_t w = scale_down(WEIGHT_OF(t, v), cscale[t / JFO_MASS_CHUNK]);
+        const uint64_t qm = jfo_floor_mul(W, draft_q(in, t));
+        total += w > qm ? w - qm : 0;
+      }
+      if (total) {
+        uint64_t target = jfo_floor_mul(total, in->uniform);
+        if (target >= total)
+          target = total - 1;
+        uint64_t run = 0;
+        for (uint32_t t = 0; t < V && !drawn; ++t) {
+          if (!admits(p, in, t, stop0, stop1))
+            continue;
+          const float v = penalized(p, inv_rep, in, t);
+          if (isnan(v))
+            continue;
+          const uint64_t w = scale_down(WEIGHT_OF(t, v), cscale[t / JFO_MASS_CHUNK]);
+          const uint64_t qm = jfo_floor_mul(W, draft_q(in, t));
+          run += w > qm ? w - qm : 0;
+          if (run > target) {
+            out->token = t;
+            drawn = 1;
+          }
+        }
+      }
+    }
+    if (!drawn) {
+      uint64_t target = jfo_floor_mul(W, in->uniform);
+      if (target >= W)
+        target = W - 1;
+      uint32_t c = 0;
+      uint64_t before = 0;
+      while (before + ctot[c] <= target)
+        before += ctot[c++];
+      const uint64_t within = target - before;
+      uint64_t P = 0;
+      const uint32_t end = (c + 1) * JFO_MASS_CHUNK < V ? (c + 1) * JFO_MASS_CHUNK : V;
+      for (uint32_t t = c * JFO_MASS_CHUNK; t < end; ++t) {
+        if (!admits(p, in, t, stop0, stop1))
+          continue;
+        const float v = penalized(p, inv_rep, in, t);
+        if (isnan(v))
+          continue;
+        P += WEIGHT_OF(t, v);
+        if (scale_down(P, cscale[c]) > within) {
+          out->token = t;
+          break;
+        }
+      }
+    }
+    /* p(draft) (sampling.metal:828-829). */
+    const uint32_t d = in->draft_token;
+    if (drafted && d < V && admits(p, in, d, stop0, stop1)) {
+      const float v = penalized(p, inv_rep, in, d);
+      if (!isnan(v))
+        out->draft_probability = PROB_OF(d, v);
+    }
+  }
+  #undef PROB_OF
+  #undef WEIGHT_OF
+  #undef FLOAT_WEIGHT
+  free(cmax); free(cmass); free(cscale); free(ctot);
+  return 0;
+}
+
 int jfo_select_row(uint32_t V, uint32_t stop0, uint32_t stop1,
                    const jfo_policy *p, const jfo_row_input *in,
                    jfo_row_output *out, uint32_t *kept_ids, float *kept_probs,
@@ -321,8 +479,13 @@ int jfo_select_row(uint32_t V, uint32_t stop0, uint32_t stop1,
     free(list);
     return 0;
   }
-  qsort(list, n, sizeof(keyed), by_order);
   const float inv_t = 1.0f / p->temperature;
+  if (!(p->min_p > 0.0f) && !(p->top_k && p->top_k < V) && !(p->top_p < 1.0f)) {
+    free(list);
+    return uncut_select(V, stop0, stop1, p, inv_rep, inv_t, in, M, n, out, kept_ids,
+                        kept_probs, kept_capacity);
+  }
+  qsort(list, n, sizeof(keyed), by_order);
 
   /* min-p (sampling.metal:593-607): keys at or above that of
    * min(M + T log(min_p), M). */
