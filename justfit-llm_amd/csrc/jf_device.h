@@ -98,6 +98,34 @@ __device__ __forceinline__ uint64_t quantized_weight(float value, float maximum,
   return ((uint64_t)Y << 32) >> k;
 }
 
+// scale_down(quantized_weight(value, maximum, inv_t), r) for r <= 2^32 in
+// one 32 x 32-bit product: the weight is (Y << 32) >> k (Y < 2^31, k in
+// [18, 63]), so for k <= 32 it is Y * 2^(32 - k) and the scaled weight is
+// (Y * r) >> k; for k > 32 the weight is Y >> (k - 32) and the scaled
+// weight that times r, >> 32. Checked equal to the composition over 2e6
+// random (Y, k, r) with the edge values of r.
+__device__ __forceinline__ uint64_t scaled_weight(float value, float maximum, float inv_t,
+                                                  uint64_t r) {
+  const float x_in = (value - maximum) * inv_t;
+  const float x = __builtin_fminf(__builtin_fmaxf(x_in, -87.0f), 88.0f);
+  const float n = __builtin_rintf(x * 1.44269504088896341f);
+  float rr = __builtin_fmaf(n, -0.693359375f, x);
+  rr = __builtin_fmaf(n, 2.12194440e-4f, rr);
+  float p = 1.9875691500e-4f;
+  p = __builtin_fmaf(p, rr, 1.3981999507e-3f);
+  p = __builtin_fmaf(p, rr, 8.3334519073e-3f);
+  p = __builtin_fmaf(p, rr, 4.1665795894e-2f);
+  p = __builtin_fmaf(p, rr, 1.6666665459e-1f);
+  p = __builtin_fmaf(p, rr, 5.0000001201e-1f);
+  const float r2 = rr * rr;
+  const float y = __builtin_fmaf(p, r2, rr) + 1.0f;
+  const uint32_t Y = (uint32_t)(y * 0x1p30f);
+  const int k = x_in >= -86.0f ? min(18 - (int)n, 63) : 63;
+  const uint32_t m = Y >> max(k - 32, 0);
+  const int sh = min(k, 32);
+  return ((uint64_t)m * r) >> sh;  // m * r < 2^63
+}
+
 // A chunk mass's rescale from the chunk's maximum to the row's:
 // floor(exp((chunk_max - row_max) / T) * 2^32), in [0, 2^32] (exp_weight's
 // result times 2^32 is exact; the conversion truncates).

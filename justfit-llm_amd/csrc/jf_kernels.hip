@@ -3673,23 +3673,29 @@ __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_
   const float mc = s.cmax[chunk];
   const uint64_t Rc = s.cscale[chunk];
   const uint32_t lane_base = chunk * CHUNK + tid * VEC;
-  uint64_t lv[LOADS];
+  uint64_t total = 0;
+  // Four loads at a time (fewer live registers than all of them at once).
 #pragma unroll
-  for (int j = 0; j < LOADS; ++j) {
-    lv[j] = 0;
+  for (int h = 0; h < LOADS / 4; ++h) {
+    uint64_t lv[4];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const int i = j * VEC + e;
-      const float q = a.dense_q ? qv[i] : draft_q(a, rp, lane_base + j * SLAB + e, s);
-      lv[j] += residual_of(scale_down(quantized_weight(xs[i], mc, inv_t), Rc), W, q);
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = h * 4 + jj;
+      lv[jj] = 0;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int i = j * VEC + e;
+        const float q = a.dense_q ? qv[i] : draft_q(a, rp, lane_base + j * SLAB + e, s);
+        lv[jj] += residual_of(scaled_weight(xs[i], mc, inv_t, Rc), W, q);
+      }
     }
+    // Lane l holds the wave's sum of load h * 4 + l / 16.
+    const uint64_t sl = wave_sums_u64<4>(lv);
+    if (lane % 16 == 0)
+      st_dev(&parts[chunk].v[kResidualSlot + 1 + (h * 4 + lane / 16) * kWaves + w], sl);
+    uint64_t t = sl + shfl_xor_u64(sl, 16);
+    total += t + shfl_xor_u64(t, 32);
   }
-  const uint64_t sl = wave_sums_u64<LOADS>(lv);
-  if (lane % GL == 0)
-    st_dev(&parts[chunk].v[kResidualSlot + 1 + (lane / GL) * kWaves + w], sl);
-  uint64_t total = sl;
-#pragma unroll
-  for (uint32_t m = GL; m < 64; m *= 2) total += shfl_xor_u64(total, (int)m);
   // The draft token's float weight, from the thread that holds it.
   if (draft < a.vocabulary && draft / CHUNK == chunk) {
     const uint32_t o = draft - chunk * CHUNK;
@@ -3760,7 +3766,7 @@ __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_
       // Past the vocabulary (a partial last chunk) the weight is zero and no
       // q is read: a dense q row ends at the vocabulary.
       const float qe = tbase + e < a.vocabulary ? draft_q(a, rp, tbase + e, s) : 0.0f;
-      q[e] = residual_of(scale_down(quantized_weight(x, mcc, inv_t), Rcc), W, qe);
+      q[e] = residual_of(scaled_weight(x, mcc, inv_t, Rcc), W, qe);
     }
     uint32_t e_hit;
     if (lane == slice_hit<VEC>(q, s.slice_within, e_hit))
