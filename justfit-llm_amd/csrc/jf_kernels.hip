@@ -2681,7 +2681,7 @@ __device__ __noinline__ void merge_small_general(uint32_t row) {
 }
 #endif
 
-// The arguments the first loads need lead the signature (14 dwords, no
+// The arguments the first loads need lead the signature (15 dwords, no
 // padding): the hardware preloads them into scalar registers at wave launch.
 // They repeat fields of `a` (drafted_rows is 0 when there are no drafts).
 #if JF_IN(2)
@@ -2690,7 +2690,7 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     const BlockHeader *headers, const uint64_t *cands, const RowParams *params,
     const float *uniforms, const uint32_t *uniform_index, uint32_t S,
     uint32_t uniform_offset, uint32_t uniform_stride, uint32_t drafted_rows,
-    SampleLaunch a) {
+    uint32_t row_indexed, SampleLaunch a) {
   Lds &s = g_small_lds;
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
   // Every address of the row, computed once and held in vector registers:
@@ -2759,7 +2759,7 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     s.merge.key[1024 + b] = 0;
   }
   const RowParams rp = wait_row_policy(prr);
-  if (a.row_indexed) {
+  if (row_indexed) {
     // Drafts addressed through the row's record (a batch of verify lanes):
     // their loads wait for the policy (the launch passed drafted_rows 0).
     draft = row_draft(a, rp);
@@ -3951,7 +3951,7 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream) {
     hipLaunchKernelGGL(kernel, grid, block, 0, st, a.headers, (const uint64_t *)a.cands,
                        a.params, a.uniforms, a.uniform_index, a.chunks,
                        (uint32_t)a.uniform_offset, (uint32_t)a.uniform_stride,
-                       a.draft_tokens && !a.row_indexed ? a.drafted_rows : 0u, a);
+                       a.draft_tokens && !a.row_indexed ? a.drafted_rows : 0u, a.row_indexed, a);
   };
   if (dtype == 0)
     go(merge_small_kernel<0>);
