@@ -3597,19 +3597,23 @@ __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_
   const uint32_t S = a.chunks;
   const uint32_t row = blockIdx.x / per_row, chunk = blockIdx.x % per_row;
   const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const RowParams rp = a.params[row];
   const BlockHeader *hb = a.headers + (uint64_t)row * S;
   StagePartial *parts = a.partials + (uint64_t)row * S;
+  // Requested together before anything waits: the row's record, its
+  // uniform, and (wave 0) its chunk summaries, one per lane (S <= 64).
+  const RowParams rp = a.params[row];
+  const float u = row_uniform(a, row);
+  const bool in = w == 0 && lane < S;
+  const BlockHeader *hl = hb + (in ? lane : 0u);
+  const float hm = hl->maximum, hbv = hl->best_value;
+  const uint32_t hadm = hl->admitted, hcnt = hl->count, hbi = hl->best_id;
+  const uint64_t hmass = parts[in ? lane : 0u].v[0];
   if (!(rp.flags & kRowSampled)) {
     // Greedy (sampling.metal:1478-1512), when no merge runs: the largest
     // chunk best, the lowest id among equals.
     if (a.finish_greedy && chunk == 0 && tid < 64) {
-      float hv = -__builtin_inff();
-      uint32_t hi = kNoToken;
-      if (lane < S) {
-        hv = hb[lane].best_value;
-        hi = hb[lane].best_id;
-      }
+      float hv = in ? hbv : -__builtin_inff();
+      uint32_t hi = in ? hbi : kNoToken;
       wave_argmax(hv, hi);
       if (tid == 0) write_result(a, row, hi, 0.0f, 0);
     }
@@ -3620,15 +3624,12 @@ __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_
   const bool drafted = draft != kNoToken;
   if (!drafted && chunk != 0) return;
   const float inv_t = rp.inv_t;
-  // Requested before the chunk summaries are waited for.
-  const float u = row_uniform(a, row);
-  // The row's chunk summaries (S <= 64: one per lane of wave 0).
+  // The row's chunk summaries.
   if (w == 0) {
-    const bool in = lane < S;
-    const float m = in ? hb[lane].maximum : -3.402823466e38f;
-    const uint32_t adm = in ? hb[lane].admitted : 0u;
-    const uint32_t cnt = in ? hb[lane].count : 0u;
-    const uint64_t mass = in ? parts[lane].v[0] : 0ull;
+    const float m = in ? hm : -3.402823466e38f;
+    const uint32_t adm = in ? hadm : 0u;
+    const uint32_t cnt = in ? hcnt : 0u;
+    const uint64_t mass = in ? hmass : 0ull;
     const float M = wave_max_f32(m);
     const uint64_t R = in ? chunk_scale(m, M, inv_t) : 0ull;
     const uint64_t T = scale_down(mass, R);
