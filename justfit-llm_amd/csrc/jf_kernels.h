@@ -32,7 +32,8 @@ struct RowParams {
   uint32_t cand_index;        // its draft distribution: sparse candidates
                               // cand_ids/probs + 16 * this, dense q row this
   uint32_t mask_row;          // its constraint mask: masks + this * mask_stride
-  uint32_t reserved;
+  uint32_t fast_row;          // nonzero: a launch split between the two select
+                              // kernels selects this row in the fast one
 };
 static_assert(sizeof(RowParams) == 64, "row params are 64 bytes");
 
@@ -160,7 +161,11 @@ struct FastLaunch {
   uint32_t row_base;          // sampler row of blockIdx.y == 0
   uint32_t fuse_greedy;       // every row greedy: the last block of a row
                               // finishes it (no merge launch)
+  uint32_t mapped;            // blockIdx.y selects row row_of[blockIdx.y]
+                              // (a launch split between the two kernels;
+                              // the kernel takes it as a preloaded argument)
   uint32_t row_info[kKernargRows];  // RowFlags | penalty row << 8
+  uint32_t row_of[kKernargRows];
 };
 
 // Multi-pass stages, in launch order.

@@ -1868,6 +1868,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
   const uint32_t row = blockIdx.x / S, chunk = blockIdx.x % S;
   const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const RowParams rp = a.params[row];
+  if (rp.fast_row) return;  // select_fast_kernel's row in a split launch
   float xs[TPL];
   SideEntries side;
   load_chunk<DT, true>(a, rp, row, chunk, s, xs, &side);
@@ -2182,7 +2183,8 @@ template <int DT>
 __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     const void *logits, const uint32_t *pen_slots, uint32_t stride, uint32_t V,
     uint32_t packed, uint32_t u_top_k, float u_minp_offset, float u_repetition,
-    float u_repetition_inverse, float u_presence, float u_frequency, FastLaunch f) {
+    float u_repetition_inverse, float u_presence, float u_frequency, uint32_t mapped,
+    FastLaunch f) {
   constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
                 LOADS = Geo<DT>::LOADS;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
@@ -2193,7 +2195,8 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   const uint32_t S = (packed >> 8) & 0xffu;
   const uint32_t slot_count = (packed & 0x10000u) ? 512u : 256u;
   const uint32_t row_base = ((packed >> 17) & 0x3fffu) << 8;
-  const uint32_t chunk = blockIdx.x, lrow = blockIdx.y, row = row_base + lrow;
+  const uint32_t chunk = blockIdx.x, lrow = blockIdx.y;
+  const uint32_t row = mapped ? f.row_of[lrow] : row_base + lrow;
   const bool uni = (packed >> 31) != 0;
   const uint32_t info = uni ? ((packed & 0xffu) | (row << 8)) : f.row_info[lrow];
   const uint32_t flags = info & 0xffu, prow = info >> 8;
@@ -3912,7 +3915,7 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
     hipExtLaunchKernelGGL(kernel, grid, block, 0, st, e0, e1, 0, f.a.logits, f.pen_slots,
                           (uint32_t)f.a.stride, f.a.vocabulary, packed, u.top_k,
                           u.minp_offset, u.repetition, u.repetition_inverse, u.presence,
-                          u.frequency, f);
+                          u.frequency, f.mapped, f);
   };
   if (dtype == 0)
     go(select_fast_kernel<0>);

@@ -515,6 +515,27 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   if (any_drafted && !a->draft_q && (!a->draft_cand_ids || !a->draft_cand_probs))
     return fail(JF_ERR_INVALID_ARGUMENT, "drafted rows need draft probabilities");
 
+  // The rows the fast selection kernel takes: in a launch of 16-byte-aligned
+  // rows (and a vocabulary of at least one vector), each row with no extra
+  // verify tokens whose penalty row fits its fixed slots. When only some
+  // rows qualify the launch is split: the fast kernel selects those, and
+  // select_kernel the others (it skips rows marked fast_row).
+  const uint64_t stride_el = rows > 1 ? a->logits_stride : V;
+  const bool launch_fast = aligned && V >= 8 && stride_el <= 0xffffffffull &&
+                           !(a->mask_rows && any_constrained);
+  uint32_t n_fast = 0;
+  for (uint32_t r = 0; r < rows; ++r) {
+    jf::RowParams &rp = params[r];
+    const bool ok = launch_fast && !rp.extra_count &&
+                    !((rp.flags & jf::kRowPenalized) &&
+                      (!a->penalties->host.fits(rp.penalty_row) || rp.penalty_row > 0xffffffu));
+    rp.fast_row = ok ? 1u : 0u;
+    n_fast += ok ? 1u : 0u;
+  }
+  const bool fast = n_fast == rows, split = n_fast && !fast;
+  if (!split)
+    for (uint32_t r = 0; r < rows; ++r) params[r].fast_row = 0;
+
   rc = upload(upload_ctx, params, rows, sc.params, stream);
   if (rc != JF_OK) return rc;
 
@@ -570,18 +591,6 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
 
   if ((a->select_start_event == nullptr) != (a->select_done_event == nullptr))
     return fail(JF_ERR_INVALID_ARGUMENT, "select events come in pairs");
-  // The fast selection kernel takes the launch when every row qualifies:
-  // aligned rows, no extra verify tokens, and penalty rows whose chunks fit
-  // their fixed slots (and vocabularies of at least one 16-byte vector).
-  bool fast = aligned && V >= 8 && L.stride <= 0xffffffffull &&
-              !(a->mask_rows && any_constrained);
-  for (uint32_t r = 0; fast && r < rows; ++r) {
-    const jf::RowParams &rp = params[r];
-    if (rp.extra_count) fast = false;
-    if ((rp.flags & jf::kRowPenalized) &&
-        (!a->penalties->host.fits(rp.penalty_row) || rp.penalty_row > 0xffffffu))
-      fast = false;
-  }
   int e = hipSuccess;
   // A launch of greedy rows only is finished inside the fast selection.
   const bool fused = fast && !any_sampled;
@@ -614,42 +623,55 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   // uncut_kernel takes them).
   const bool need_merge = !fused && (any_cut || (any_greedy && !any_uncut));
   L.finish_greedy = any_greedy && !need_merge && !fused ? 1u : 0u;
-  if (fast) {
+  if (!fast) {
+    e = jf::launch_select(L, a->dtype, stream, a->select_start_event,
+                          split ? nullptr : a->select_done_event);
+  }
+  if (e == hipSuccess && (fast || split)) {
     jf::FastLaunch F{};
     F.a = L;
     F.fuse_greedy = fused ? 1u : 0u;
+    F.mapped = split ? 1u : 0u;
     if (a->penalties) {
       F.pen_slots = a->penalties->slots;
       F.slot_count = a->penalties->slot_count;
     }
+    std::vector<uint32_t> fast_rows;
+    if (split) {
+      fast_rows.reserve(n_fast);
+      for (uint32_t r = 0; r < rows; ++r)
+        if (params[r].fast_row) fast_rows.push_back(r);
+    }
+    auto row_at = [&](uint32_t i) { return split ? fast_rows[i] : i; };
     // A uniform launch: every row has the same policy, and penalized rows
     // read their own table row; the kernel then takes the policy from its
     // preloaded arguments instead of a memory read per block.
     bool uniform = true;
-    for (uint32_t r = 0; uniform && r < rows; ++r) {
-      const jf::RowParams &p0 = params[0], &p = params[r];
+    const jf::RowParams &p0 = params[row_at(0)];
+    for (uint32_t i = 0; uniform && i < n_fast; ++i) {
+      const uint32_t r = row_at(i);
+      const jf::RowParams &p = params[r];
       uniform = p.flags == p0.flags && p.top_k == p0.top_k &&
                 p.minp_offset == p0.minp_offset && p.repetition == p0.repetition &&
                 p.repetition_inverse == p0.repetition_inverse &&
                 p.presence == p0.presence && p.frequency == p0.frequency &&
                 (!(p.flags & jf::kRowPenalized) || p.penalty_row == r);
     }
-    for (uint32_t r0 = 0; r0 < rows && e == hipSuccess; r0 += jf::kKernargRows) {
-      const uint32_t n = std::min<uint32_t>(rows - r0, jf::kKernargRows);
-      F.row_base = r0;
-      for (uint32_t r = 0; r < n; ++r) {
-        const jf::RowParams &rp = params[r0 + r];
+    for (uint32_t i0 = 0; i0 < n_fast && e == hipSuccess; i0 += jf::kKernargRows) {
+      const uint32_t n = std::min<uint32_t>(n_fast - i0, jf::kKernargRows);
+      F.row_base = split ? 0u : i0;
+      for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t r = row_at(i0 + i);
+        const jf::RowParams &rp = params[r];
         const uint32_t prow = (rp.flags & jf::kRowPenalized) ? rp.penalty_row : 0u;
-        F.row_info[r] = (rp.flags & 0xffu) | (prow << 8);
+        F.row_info[i] = (rp.flags & 0xffu) | (prow << 8);
+        F.row_of[i] = r;
       }
-      const bool first = r0 == 0, last = r0 + n == rows;
-      e = jf::launch_select_fast(F, n, a->dtype, uniform ? &params[0] : nullptr, stream,
+      const bool first = i0 == 0 && !split, last = i0 + n == n_fast;
+      e = jf::launch_select_fast(F, n, a->dtype, uniform ? &p0 : nullptr, stream,
                                  first ? a->select_start_event : nullptr,
                                  last ? a->select_done_event : nullptr);
     }
-  } else {
-    e = jf::launch_select(L, a->dtype, stream, a->select_start_event,
-                          a->select_done_event);
   }
   if (e != hipSuccess) return hip_fail((hipError_t)e, "select launch");
   // The small-K merge takes launches whose cut rows keep at most 64 tokens

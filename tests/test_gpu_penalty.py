@@ -133,3 +133,38 @@ def test_count_errors_leave_the_row_unchanged():
         table.count(0, [10, 11, 12, 13, 14, 15, 16])  # 3 held + 7 new > 8
     table.count(0, [10, 11, 12, 13, 14])  # exactly 8
     table.close()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_launch_split_between_fast_and_general_select(bf16):
+    """A history clustered in low token ids (as real text is) overflows its
+    first chunk's fixed slots: that row takes select_kernel while the other
+    rows of the same call stay on the fast kernel. Greedy, cut and uncut
+    rows, penalized and not; tokens bit-exact against the oracle."""
+    from harness import run_gpu, run_oracle
+    from jf_sampler import workloads as WL
+    rng = np.random.default_rng(41 + bf16)
+    rows = 7
+    x = (rng.standard_normal((rows, V)) * 2.0).astype(np.float32)
+    hist = [rng.integers(0, V, 800).astype(np.uint32) for _ in range(rows)]
+    # Rows 2 and 5: Zipf-like ids, about 600 distinct below 8192.
+    for r in (2, 5):
+        hist[r] = np.minimum(rng.zipf(1.2, 3000), 8191).astype(np.uint32)
+        x[r, :200] += 4.0
+    pols = [J.policy(temperature=0.8, top_k=50, top_p=0.9, presence=0.5),
+            J.policy(repetition=1.2),
+            J.policy(temperature=0.7, top_k=40, frequency=0.8, presence=0.3),
+            J.policy(temperature=1.0, presence=0.4),
+            J.policy(temperature=0.9, top_k=50, top_p=0.9, presence=0.5),
+            J.policy(repetition=1.3, presence=0.2),
+            J.policy(temperature=1.0)]
+    u = rng.random(rows).astype(np.float32)
+    kw = dict(histories=hist, generated=[400] * rows, mark_prompt=[True] * rows, uniforms=u)
+    if bf16:
+        kw["logits_bf16"] = WL.to_bf16_bits(x)
+    else:
+        kw["logits"] = x
+    g = run_gpu(V, pols, **kw)
+    r = run_oracle(V, pols, **kw)
+    np.testing.assert_array_equal(g["tokens"], r["tokens"])
+    assert np.all(g["tokens"] != 0xFFFFFFFF)
