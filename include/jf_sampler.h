@@ -231,7 +231,7 @@ int jf_sample(jf_sampler *sampler, const jf_sample_args *args, void *stream);
  * counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). The scratch that jf_sampler_create would
- * allocate is instead one file-scope device array of 21,049,600 bytes, held
+ * allocate is instead one file-scope device array of 21,065,984 bytes, held
  * by every GPU the library runs on until the process ends. Limits: 1..64
  * rows and a vocabulary of 1..262,144 tokens; larger calls return
  * JF_ERR_INVALID_ARGUMENT. The caller still passes inputs and outputs (and

@@ -135,6 +135,8 @@ struct SampleLaunch {
   BlockHeader *headers;
   uint64_t *cands;       // key | id << 32
   uint32_t *counters;
+  uint64_t *bests;       // all-greedy fast launches: each block's packed best
+                         // (zero between calls)
   RowState *states;
   StagePartial *partials;
   uint32_t *out_tokens;
@@ -309,14 +311,15 @@ struct GatherLaunch {
 };
 
 // The device scratch of one selection: where its kernels exchange row
-// parameters, chunk summaries, candidate lists, arrival counters (zero
-// between calls), row states and stage partials. Room for max_rows rows of
+// parameters, chunk summaries, candidate lists, arrival counters and packed
+// greedy bests (both zero between calls), row states and stage partials. Room for max_rows rows of
 // at most max_chunks 8192-token chunks.
 struct SampleScratch {
   RowParams *params;        // [max_rows]
   BlockHeader *headers;     // [max_rows * max_chunks]
   uint64_t *cands;          // [max_rows * max_chunks * kBlockCandidates]
   uint32_t *counters;       // [max_rows]
+  uint64_t *bests;          // [max_rows * max_chunks], zero between calls
   RowState *states;         // [max_rows]
   StagePartial *partials;   // [max_rows * max_chunks]
   uint32_t max_rows;

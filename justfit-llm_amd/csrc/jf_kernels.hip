@@ -45,6 +45,9 @@ struct Geo<1> {  // bf16: 8 tokens per 16-byte load
 constexpr uint32_t kMaxChunkWords = kChunkF32 / 32;
 constexpr uint32_t kLowestKey = 0x007fffffu;  // the key of -infinity
 constexpr uint32_t kMaxChunks = 64;
+// Reads of a packed greedy best before it is taken as written: far beyond
+// the few microseconds a store issued before its block's arrival needs.
+constexpr uint32_t kBestWaitBound = 1u << 20;
 
 // A chunk's penalized values, compact: the table's entries of the chunk
 // (sorted by token) are processed in rounds of kPenaltySlots; an entry's
@@ -2383,12 +2386,21 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     }
     // Every row greedy: the row's last block to arrive takes the largest
     // chunk best, the lowest id among equals (the reference's last-arriving
-    // group, split_reduce.h:14-45). Summaries go out with device-coherent
-    // stores that complete before the arrival; the counter returns to zero.
+    // group, split_reduce.h:14-45). Each block's best is one 64-bit word:
+    // the value's order key in bits 63..32, 0x7FFFF - id in 31..13 (ids
+    // stay below 2^19, so the larger word holds the larger value, then the
+    // lower id), and bit 0 set, so that a written word is never zero (the
+    // word 1: nothing admitted, below every admitted key). The word's store
+    // and the arrival go out together; the last block reads the row's words
+    // and waits, word by word, for any not yet visible. Each such store was
+    // issued before its block's arrival, so every wait ends; the bound only
+    // caps the loop. The last block returns the words and the counter to
+    // zero.
     if (tid == 0) {
-      st_dev(&hdr->best_value, bv);
-      st_dev(&hdr->best_id, bi);
-      wait_memory();
+      const uint64_t mine =
+          bi == kNoToken ? 1ull
+                         : ((uint64_t)logit_key(bv) << 32) | ((uint64_t)(0x7ffffu - bi) << 13) | 1ull;
+      st_dev(a.bests + (uint64_t)row * S + chunk, mine);
       const uint32_t prev = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT);
       s.wcount[0] = prev == S - 1 ? 1u : 0u;
@@ -2396,19 +2408,17 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     }
     __syncthreads();
     if (s.wcount[0] && w == 0) {
-      float v = -__builtin_inff();
-      uint32_t i = kNoToken;
-      for (uint32_t c = lane; c < S; c += 64) {
-        const BlockHeader *h = a.headers + (uint64_t)row * S + c;
-        const float hv = ld_dev(&h->best_value);
-        const uint32_t hi = ld_dev(&h->best_id);
-        if (hv > v || (hv == v && hi < i)) {
-          v = hv;
-          i = hi;
-        }
+      uint64_t best = 0;
+      if (lane < S) {  // S <= kMaxChunks = 64
+        uint64_t *word = a.bests + (uint64_t)row * S + lane;
+        best = ld_dev(word);
+        for (uint32_t n = 0; best == 0 && n < kBestWaitBound; ++n) best = ld_dev(word);
+        st_dev(word, 0ull);
       }
-      wave_argmax(v, i);
-      if (lane == 0) write_result(a, row, i, 0.0f, 0);
+      const uint32_t key = wave_max_u32((uint32_t)(best >> 32));
+      const uint32_t low = wave_max_u32((uint32_t)(best >> 32) == key ? (uint32_t)best : 0u);
+      if (lane == 0)
+        write_result(a, row, key ? 0x7ffffu - (low >> 13) : kNoToken, 0.0f, 0);
     }
     return;
   }

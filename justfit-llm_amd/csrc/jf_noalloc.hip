@@ -29,7 +29,8 @@ constexpr uint64_t kHeadersOff = align256(kParamsOff + kStaticRows * sizeof(jf::
 constexpr uint64_t kCandsOff = align256(kHeadersOff + kBlocks * sizeof(jf::BlockHeader));
 constexpr uint64_t kCountersOff =
     align256(kCandsOff + kBlocks * jf::kBlockCandidates * sizeof(uint64_t));
-constexpr uint64_t kStatesOff = align256(kCountersOff + kStaticRows * sizeof(uint32_t));
+constexpr uint64_t kBestsOff = align256(kCountersOff + kStaticRows * sizeof(uint32_t));
+constexpr uint64_t kStatesOff = align256(kBestsOff + kBlocks * sizeof(uint64_t));
 constexpr uint64_t kPartialsOff = align256(kStatesOff + kStaticRows * sizeof(jf::RowState));
 constexpr uint64_t kScratchBytes = align256(kPartialsOff + kBlocks * sizeof(jf::StagePartial));
 static_assert(kScratchBytes < (24u << 20), "the static scratch stays under 24 MiB");
@@ -123,6 +124,7 @@ extern "C" int jf_sample_static(uint32_t vocabulary, const jf_sample_args *args,
                              (jf::BlockHeader *)(base + kHeadersOff),
                              (uint64_t *)(base + kCandsOff),
                              (uint32_t *)(base + kCountersOff),
+                             (uint64_t *)(base + kBestsOff),
                              (jf::RowState *)(base + kStatesOff),
                              (jf::StagePartial *)(base + kPartialsOff),
                              kStaticRows,

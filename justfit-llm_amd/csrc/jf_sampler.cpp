@@ -137,6 +137,7 @@ struct jf_sampler {
   jf::BlockHeader *headers = nullptr;
   uint64_t *cands = nullptr;
   uint32_t *counters = nullptr;
+  uint64_t *bests = nullptr;
   jf::RowState *states = nullptr;
   jf::StagePartial *partials = nullptr;
   jf::AcceptChainLane *chain_lanes = nullptr;
@@ -158,6 +159,7 @@ int jf_sampler_destroy(jf_sampler *s) {
   (void)hipFree(s->headers);
   (void)hipFree(s->cands);
   (void)hipFree(s->counters);
+  (void)hipFree(s->bests);
   (void)hipFree(s->states);
   (void)hipFree(s->partials);
   (void)hipFree(s->chain_lanes);
@@ -192,6 +194,7 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
   if (rc == JF_OK) rc = device_alloc(&s->headers, blocks, "block headers");
   if (rc == JF_OK) rc = device_alloc(&s->cands, blocks * jf::kBlockCandidates, "candidates");
   if (rc == JF_OK) rc = device_alloc(&s->counters, max_rows, "arrival counters");
+  if (rc == JF_OK) rc = device_alloc(&s->bests, blocks, "greedy bests");
   if (rc == JF_OK) rc = device_alloc(&s->states, max_rows, "row states");
   if (rc == JF_OK) rc = device_alloc(&s->partials, blocks, "stage partials");
   if (rc == JF_OK) rc = device_alloc(&s->chain_lanes, max_rows, "chain lanes");
@@ -199,9 +202,11 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
   if (rc == JF_OK) {
     const hipError_t e1 = hipMemset(s->counters, 0, max_rows * sizeof(uint32_t));
     const hipError_t e2 = hipMemset(s->states, 0, max_rows * sizeof(jf::RowState));
+    const hipError_t e4 = hipMemset(s->bests, 0, blocks * sizeof(uint64_t));
     const hipError_t e3 = hipDeviceSynchronize();
     if (e1 != hipSuccess) rc = hip_fail(e1, "counter init");
     else if (e2 != hipSuccess) rc = hip_fail(e2, "state init");
+    else if (e4 != hipSuccess) rc = hip_fail(e4, "greedy best init");
     else if (e3 != hipSuccess) rc = hip_fail(e3, "init sync");
   }
   if (rc != JF_OK) {
@@ -212,7 +217,7 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
       max_rows * (sizeof(jf::RowParams) + sizeof(uint32_t) + sizeof(jf::RowState) +
                   sizeof(jf::AcceptChainLane) + sizeof(jf::TreeLaneParams)) +
       blocks * (sizeof(jf::BlockHeader) + jf::kBlockCandidates * sizeof(uint64_t) +
-                sizeof(jf::StagePartial));
+                sizeof(uint64_t) + sizeof(jf::StagePartial));
   *out = s;
   return JF_OK;
 }
@@ -576,6 +581,7 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   L.headers = sc.headers;
   L.cands = sc.cands;
   L.counters = sc.counters;
+  L.bests = sc.bests;
   L.states = sc.states;
   L.partials = sc.partials;
   L.out_tokens = a->out_tokens;
@@ -742,7 +748,8 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   if (!a->rows || a->rows > s->max_rows)
     return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling batch width");
   const jf::SampleScratch sc{s->params, s->headers,  s->cands,    s->counters,
-                             s->states, s->partials, s->max_rows, s->max_chunks};
+                             s->bests,  s->states,   s->partials, s->max_rows,
+                             s->max_chunks};
   std::vector<jf::RowParams> params(a->rows);
   return jf::sample_core(s->vocabulary, sc, a, params.data(), sampler_upload, s, stream);
 }
