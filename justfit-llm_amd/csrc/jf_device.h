@@ -165,28 +165,6 @@ __device__ __forceinline__ uint64_t floor_mul(uint64_t a, float f) {
   return sh >= 128 ? 0 : (uint64_t)(p >> sh);
 }
 
-// floor_mul(a, f) for a < 2^63 (every mass here: at most 2^19 tokens of
-// weight <= 2^44) without a 128-bit product: with f = m * 2^-sh (24-bit m,
-// sh >= 24 for f < 1), a * m is ah * m * 2^32 + al * m, and its floor
-// shift is taken from T = (a * m) >> 32 when sh >= 32, else from the two
-// 32 x 24-bit products. Checked equal to floor_mul over 2e8 random (a, f)
-// and the edge values of f.
-__device__ __forceinline__ uint64_t floor_mul_63(uint64_t a, float f) {
-  const uint32_t b = f2u(f);
-  const uint32_t e = b >> 23;
-  const uint32_t m = e ? ((b & 0x7fffffu) | 0x800000u) : (b & 0x7fffffu);
-  const int sh = e ? 150 - (int)e : 149;
-  const uint32_t ah = (uint32_t)(a >> 32), al = (uint32_t)a;
-  const uint64_t L = (uint64_t)al * m;
-  const uint64_t P = (uint64_t)ah * m;
-  const uint64_t T = P + (L >> 32);
-  const uint64_t hi = T >> min(max(sh - 32, 0), 63);
-  const uint64_t lo = (P << ((32 - sh) & 31)) + (L >> (sh & 31));
-  uint64_t r = sh >= 32 ? hi : lo;
-  r = f > 0.0f ? r : 0ull;  // also NaN
-  return f >= 1.0f ? a : r;
-}
-
 // penalize_logit (sampling.metal:928-935): repetition divides a positive
 // logit and multiplies a negative one, presence and frequency lower it by
 // the count, and the result saturates (a NaN becomes -FLT_MAX).

@@ -668,9 +668,20 @@ __device__ __forceinline__ void stage_candidates(const SampleLaunch &a,
   __syncthreads();
 }
 
+// A drafted row's residual weight max(wq - Q, 0) (sampling.metal:700-708,
+// 760-765): Q = floor(q * m) for m the mass rounded to a float and the
+// product rounded to a float (both to nearest even); q NaN or <= 0 takes
+// nothing off. Every weight is at most 2^44, so a product at or above 2^44
+// leaves nothing; below it the product's integer part is two exact 32-bit
+// conversions (its floor over 2^32, and the remainder, which the fused
+// multiply-add leaves exact).
 __device__ __forceinline__ uint64_t residual_of(uint64_t wq, uint64_t mass,
                                                 float q) {
-  const uint64_t qm = floor_mul_63(mass, q);
+  const float x = q > 0.0f ? q * (float)mass : 0.0f;
+  if (!(x < 0x1p44f)) return 0;
+  const float hf = __builtin_floorf(x * 0x1p-32f);
+  const uint64_t qm =
+      ((uint64_t)(uint32_t)hf << 32) | (uint32_t)__builtin_fmaf(hf, -0x1p32f, x);
   return wq > qm ? wq - qm : 0;
 }
 

@@ -10,6 +10,9 @@
  *                                  round trip over sampled bit patterns.
  *   jfo_expf                       <= 2 ulp against double exp over a sweep.
  *   jfo_floor_mul                  against Python's exact integers.
+ *   jfo_residual                   against numpy float32 products and
+ *                                  Python integers, with the NaN, sign,
+ *                                  2^32 and 2^44 edges.
  *   jfo_splitmix64                 published SplitMix64 known answers
  *                                  (Steele, Lea & Flood 2014; seed 0 ->
  *                                  0xe220a8397b1dcdaf).
@@ -81,6 +84,20 @@ float jfo_expf(float x) {
   const float y = fmaf(p, r2, r) + 1.0f;
   const int ni = (int)n;
   return y * u2f((uint32_t)(ni + 127) << 23);
+}
+
+/* A drafted row's residual weight max(w - Q, 0) (sampling.metal:700-708,
+ * 760-765): Q = floor(q * m) for m the mass rounded to a float and the
+ * product rounded to a float (both to nearest even, as the kernels compute
+ * it). q NaN or <= 0 gives Q = 0; Q at or above 2^44 leaves nothing, since
+ * every weight is at most 2^44. */
+uint64_t jfo_residual(uint64_t w, uint64_t mass, float q) {
+  const float m = (float)mass;
+  const float x = q > 0.0f ? q * m : 0.0f;
+  if (!(x < 0x1p44f))
+    return 0;
+  const uint64_t qm = (uint64_t)x;
+  return w > qm ? w - qm : 0;
 }
 
 /* floor(a * f) exactly, for f in [0, 1] (NaN and f <= 0 give 0, f >= 1 gives
@@ -354,7 +371,7 @@ static int uncut_select(uint32_t V, uint32_t stop0, uint32_t stop1,
   if (W != 0) {
     int drawn = 0;
     if (drafted) {
-      /* The residual max(weight - floor(W * q), 0) in id order. */
+      /* The residual weights (jfo_residual) in id order. */
       uint64_t total = 0;
       for (uint32_t t = 0; t < V; ++t) {
         if (!admits(p, in, t, stop0, stop1))
@@ -363,8 +380,7 @@ static int uncut_select(uint32_t V, uint32_t stop0, uint32_t stop1,
         if (isnan(v))
           continue;
         const uint64_t w = scale_down(WEIGHT_OF(t, v), cscale[t / JFO_MASS_CHUNK]);
-        const uint64_t qm = jfo_floor_mul(W, draft_q(in, t));
-        total += w > qm ? w - qm : 0;
+        total += jfo_residual(w, W, draft_q(in, t));
       }
       if (total) {
         uint64_t target = jfo_floor_mul(total, in->uniform);
@@ -378,8 +394,7 @@ static int uncut_select(uint32_t V, uint32_t stop0, uint32_t stop1,
           if (isnan(v))
             continue;
           const uint64_t w = scale_down(WEIGHT_OF(t, v), cscale[t / JFO_MASS_CHUNK]);
-          const uint64_t qm = jfo_floor_mul(W, draft_q(in, t));
-          run += w > qm ? w - qm : 0;
+          run += jfo_residual(w, W, draft_q(in, t));
           if (run > target) {
             out->token = t;
             drawn = 1;
@@ -569,8 +584,7 @@ int jfo_select_row(uint32_t V, uint32_t stop0, uint32_t stop1,
   int residual = 0;
   for (uint32_t i = 0; i < n3; ++i) {
     if (drafted) {
-      const uint64_t qm = jfo_floor_mul(mass3, draft_q(in, kept[i].id));
-      dq[i] = kq[i] > qm ? kq[i] - qm : 0;
+      dq[i] = jfo_residual(kq[i], mass3, draft_q(in, kept[i].id));
       residual |= dq[i] > 0;
     } else {
       dq[i] = kq[i];

@@ -43,6 +43,7 @@ uint32_t jfo_logit_key(float value);
 float jfo_key_logit(uint32_t key);
 float jfo_expf(float x);
 uint64_t jfo_floor_mul(uint64_t a, float f);
+uint64_t jfo_residual(uint64_t w, uint64_t mass, float q);
 uint64_t jfo_splitmix64(uint64_t seed, uint64_t counter);
 float jfo_next_uniform(uint64_t seed, uint64_t *counter);
 void jfo_stage_cycle(uint64_t seed, uint64_t *counter, uint32_t verify_rows,

@@ -91,6 +91,8 @@ def _bind(L):
     L.jfo_expf.restype = c_f32
     L.jfo_floor_mul.argtypes = [c_u64, c_f32]
     L.jfo_floor_mul.restype = c_u64
+    L.jfo_residual.argtypes = [c_u64, c_u64, c_f32]
+    L.jfo_residual.restype = c_u64
     L.jfo_splitmix64.argtypes = [c_u64, c_u64]
     L.jfo_splitmix64.restype = c_u64
     L.jfo_next_uniform.argtypes = [c_u64, ctypes.POINTER(c_u64)]

@@ -87,6 +87,73 @@ def test_floor_mul_is_exact():
     assert O.lib().jfo_floor_mul(12345, float("nan")) == 0
 
 
+def f32_of_int(n):
+    """n rounded to the nearest float32 (ties to even), by integer
+    arithmetic: numpy's int -> float32 passes through float64 and can round
+    twice."""
+    e = n.bit_length() - 24
+    if e <= 0:
+        return np.float32(n)
+    q, r = divmod(n, 1 << e)
+    half = 1 << (e - 1)
+    if r > half or (r == half and q & 1):
+        q += 1
+    return np.float32(float(q << e))
+
+
+def residual_reference(w, mass, q):
+    """max(w - floor(q * m), 0) for m the mass as a float32 and the product
+    rounded to float32; q NaN or <= 0 takes nothing off, a product at or
+    above 2^44 leaves nothing."""
+    q = np.float32(q)
+    if not q > 0:
+        return w
+    x = q * f32_of_int(mass)  # float32 product, ties to even
+    if not x < np.float32(2.0 ** 44):
+        return 0
+    return max(w - math.floor(Fraction(float(x))), 0)
+
+
+def test_residual_weight():
+    """jfo_residual, the drafted rows' residual weight, against float32
+    products and exact integers; the edges: q NaN/negative/zero/infinite,
+    q >= 1, products on both sides of 2^32 (the kernels' two-word split) and
+    of 2^44 (nothing left), and masses whose float rounds up or down."""
+    L = O.lib()
+    rng = np.random.default_rng(7)
+    cases = []
+    for _ in range(4000):
+        mass = int(rng.integers(1 << 44, 1 << 63))
+        w = int(rng.integers(0, (1 << 44) + 1))
+        kind = rng.integers(0, 4)
+        if kind == 0:
+            q = rng.random()
+        elif kind == 1:
+            q = rng.random() * 1e-6
+        elif kind == 2:
+            # products near 2^32 and 2^44
+            target = 2.0 ** (32 if rng.random() < 0.5 else 44)
+            q = target / float(f32_of_int(mass)) * (1 + (rng.random() - 0.5) * 1e-6)
+        else:
+            q = rng.random() * 1e-30
+        cases.append((w, mass, float(np.float32(q))))
+    cases += [(5, 1 << 44, float("nan")), (5, 1 << 44, -0.5), (5, 1 << 44, 0.0),
+              (5, 1 << 44, float("inf")), (1 << 44, 1 << 44, 1.0), (1 << 44, (1 << 45) - 1, 1.0),
+              (1 << 44, (1 << 44) + 1, 1.0), (123, (1 << 63) - 1, 2.0),
+              ((1 << 44) - 1, (1 << 60) + (1 << 36) + 1, 2.0 ** -20)]
+    hits32 = 0
+    for w, mass, q in cases:
+        want = residual_reference(w, mass, q)
+        assert L.jfo_residual(w, mass, q) == want, (w, mass, q)
+        x = np.float32(q) * f32_of_int(mass) if q > 0 else 0
+        hits32 += 2.0 ** 32 <= x < 2.0 ** 44
+    assert hits32 > 100
+    # Closed forms: no draft mass takes nothing off; q = 1 removes the whole
+    # weight (the mass is at least the weight).
+    assert L.jfo_residual(777, 1 << 50, 0.0) == 777
+    assert L.jfo_residual(1 << 44, 1 << 44, 1.0) == 0
+
+
 # ---- uniforms -------------------------------------------------------------
 
 def splitmix_reference(state):
