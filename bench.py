@@ -39,6 +39,11 @@ def parse():
                     help="C3/C4: greedy or sampled (auto: sampled)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="bound of the CPU-baseline sample")
+    ap.add_argument("--history", default="uniform", choices=["uniform", "zipf", "mixed"],
+                    help="C2 only: zipf gives every row a history clustered in low ids "
+                         "(Zipf 1.2), whose first chunk overflows the fast kernel's "
+                         "penalty slots, so the rows take select_kernel; mixed does so "
+                         "for every fourth row (the call is split between the kernels)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 64 MiB device copy (20 times): the "
@@ -47,7 +52,7 @@ def parse():
     return ap.parse_args()
 
 
-def build_workload(cfg, mode):
+def build_workload(cfg, mode, history="uniform"):
     """Host inputs, per-row policies and the algorithmic bytes of one step."""
     import jf_sampler as J
     from jf_sampler import workloads as WL
@@ -62,11 +67,25 @@ def build_workload(cfg, mode):
     elif cfg == 2:
         c = WL.config2()
         B = c["logits"].shape[0]
+        hists, label = c["histories"], "2048 ids"
+        if history != "uniform":
+            # Ids clustered near 0 as real text's are: about 450 distinct ids
+            # below 8192, past the first chunk's 256 fixed slots.
+            rng = np.random.default_rng(22)
+            every = 1 if history == "zipf" else 4
+            hists = [np.minimum(rng.zipf(1.2, len(h)) - 1, c["V"] - 1).astype(np.uint32)
+                     if r % every == 0 else h for r, h in enumerate(hists)]
+            label = ("2048 Zipf(1.2)-clustered ids (select_kernel)" if every == 1 else
+                     "2048 ids, every 4th row Zipf(1.2)-clustered (split launch)")
+            # The events around the selection then span select_kernel (and,
+            # split, the fast kernel after it).
+            w["kernel"] = ("jf::select_kernel<0>" if every == 1 else
+                           "jf::select_kernel<0> then jf::select_fast_kernel<0>")
         w.update(V=c["V"], logits=c["logits"], policies=[J.policy(**c["policy"])] * B,
-                 histories=c["histories"], generated=c["generated"], mark_prompt=False,
+                 histories=hists, generated=c["generated"], mark_prompt=False,
                  uniforms=c["uniforms"],
                  name="C2 sampled B=64 V=151936 fp32 T0.7 top-k 50 top-p 0.9 "
-                      "presence 0.5 frequency 0.3 over 2048 ids",
+                      f"presence 0.5 frequency 0.3 over {label}",
                  dtype="f32")
         hist_bytes = B * 2048 * 4
     elif cfg == 3:
@@ -395,13 +414,16 @@ def cpu_baseline(w, seconds):
 PROFILE_NAMES = {(1, "auto"): "select_c1", (2, "auto"): "select_merge_c2",
                  (3, "greedy"): "select_c3_greedy", (3, "sampled"): "select_uncut_c3_sampled",
                  (4, "greedy"): "select_c4_greedy", (4, "sampled"): "select_uncut_c4_sampled",
-                 (5, "auto"): "select_merge_c5", ("draft", "auto"): "draft_select",
+                 (5, "auto"): "select_merge_c5", (2, "zipf"): "select_merge_c2_zipf",
+                 (2, "mixed"): "select_merge_c2_mixed", ("draft", "auto"): "draft_select",
                  ("gather", "auto"): "tree_gather"}
 
 
-def profile_key(cfg, mode):
+def profile_key(cfg, mode, history="uniform"):
     if cfg in (3, 4):
         return (cfg, "greedy" if mode == "greedy" else "sampled")
+    if cfg == 2 and history != "uniform":
+        return (cfg, history)
     return (cfg, "auto")
 
 
@@ -645,7 +667,10 @@ def main():
     if args.path == "gather":
         bench_gather(args)
         return
-    w = build_workload(args.config, args.mode)
+    if args.history != "uniform" and args.config != 2:
+        print("--history applies to --config 2 only", file=sys.stderr)
+        sys.exit(2)
+    w = build_workload(args.config, args.mode, args.history)
     print(f"# {w['name']}: building inputs", file=sys.stderr, flush=True)
     g = GpuStep(w, count_headroom=args.steps)
     for i in range(args.warmup):
@@ -686,8 +711,8 @@ def main():
         counted["note"] = ("each step followed by jf_penalty_table_count_rows of one "
                            "token per row, from C++")
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
-    kernel = f"jf::select_fast_kernel<{0 if w['dtype'] == 'f32' else 1}>"
-    key = profile_key(args.config, args.mode)
+    kernel = w.get("kernel", f"jf::select_fast_kernel<{0 if w['dtype'] == 'f32' else 1}>")
+    key = profile_key(args.config, args.mode, args.history)
     traffic = read_traffic(key, kernel)
     prof_us = read_profile_us(key, kernel)
     line = {

@@ -32,7 +32,6 @@ constexpr int kDraftTokens = 32;         // tokens per thread
 constexpr uint32_t kDraftK = 16;
 constexpr uint32_t kDraftMaxChunks = 64;    // vocabulary <= 524288
 constexpr uint32_t kRank = 256;
-constexpr uint32_t kWaveCap = 256;       // staged candidates per wave
 constexpr uint32_t kPad = kRank + 1;     // LDS row pitch of the edge operands
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));

@@ -45,9 +45,6 @@ struct Geo<1> {  // bf16: 8 tokens per 16-byte load
 constexpr uint32_t kMaxChunkWords = kChunkF32 / 32;
 constexpr uint32_t kLowestKey = 0x007fffffu;  // the key of -infinity
 constexpr uint32_t kMaxChunks = 64;
-// Reads of a packed greedy best before it is taken as written: far beyond
-// the few microseconds a store issued before its block's arrival needs.
-constexpr uint32_t kBestWaitBound = 1u << 20;
 
 // A chunk's penalized values, compact: the table's entries of the chunk
 // (sorted by token) are processed in rounds of kPenaltySlots; an entry's
@@ -2419,6 +2416,9 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     }
     __syncthreads();
     if (s.wcount[0] && w == 0) {
+      // Reads of a word before it is taken as written: far beyond the few
+      // microseconds a store issued before its block's arrival needs.
+      constexpr uint32_t kBestWaitBound = 1u << 20;
       uint64_t best = 0;
       if (lane < S) {  // S <= kMaxChunks = 64
         uint64_t *word = a.bests + (uint64_t)row * S + lane;
@@ -3616,7 +3616,7 @@ template <int DT>
 __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_t per_row) {
   constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
                 SLAB = Geo<DT>::SLAB;
-  constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves, GL = 64 / LOADS;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves;
   __shared__ UncutLds s;
   const uint32_t S = a.chunks;
   const uint32_t row = blockIdx.x / per_row, chunk = blockIdx.x % per_row;

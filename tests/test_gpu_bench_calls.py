@@ -3,7 +3,9 @@ same device inputs, penalty tables and argument records as the timed loop,
 and one of its steps is compared with the oracle row by row (bit-exact
 tokens, and the draft probabilities where the step writes them). C2 and C5
 run as benchmarked, without kept outputs or draft probabilities; C1, C3 and
-C4 greedy and sampled as the bench issues them."""
+C4 greedy and sampled as the bench issues them; C2 also with histories
+clustered in low ids (every row on select_kernel, and every fourth row, a
+call split between the two select kernels)."""
 import numpy as np
 import pytest
 
@@ -43,11 +45,13 @@ def _oracle_for(w):
     return run_oracle(w["V"], w["policies"], **kw)
 
 
-@pytest.mark.parametrize("cfg,mode", [(2, "auto"), (5, "auto"), (1, "auto"), (3, "greedy"),
-                                      (3, "sampled"), (4, "greedy"), (4, "sampled")])
-def test_benchmarked_step_matches_oracle(cfg, mode):
+@pytest.mark.parametrize("cfg,mode,history", [
+    (2, "auto", "uniform"), (5, "auto", "uniform"), (1, "auto", "uniform"),
+    (3, "greedy", "uniform"), (3, "sampled", "uniform"), (4, "greedy", "uniform"),
+    (4, "sampled", "uniform"), (2, "auto", "zipf"), (2, "auto", "mixed")])
+def test_benchmarked_step_matches_oracle(cfg, mode, history):
     import torch
-    w = bench.build_workload(cfg, mode)
+    w = bench.build_workload(cfg, mode, history)
     print(f"bench call: {w['name']}", flush=True)
     g = bench.GpuStep(w)
     for i in (0, len(g.kw) - 1):  # the first and last rotated copy

@@ -456,6 +456,52 @@ def test_dense_residual_in_the_partial_last_chunk(bf16):
     assert g["tokens"][rows - 1] >= V - 4480  # inside the partial last chunk
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("V", [5000, 3 * 8192 + 17, 151936])
+def test_all_greedy_launch_edges(bf16, V):
+    """Launches whose rows are all greedy finish inside the selection: each
+    chunk's best is packed into one word and the row's last block takes the
+    largest (sampling.metal:1427-1512). Ties of the maximum across chunks
+    (lowest id), -0 against +0, +inf, all-NaN, all -inf (admitted: it wins
+    over nothing), a mask that admits nothing and one that admits only the
+    partial last chunk; then calls on the same sampler with fewer rows,
+    which find the packed words and counters returned to zero."""
+    rng = np.random.default_rng(41 + V)
+    rows = 8
+    x = rng.normal(0, 2.0, (rows, V)).astype(np.float32)
+    x[1, [10, V // 2, V - 1]] = 50.0            # the maximum in three chunks
+    x[2] = np.nan
+    x[3] = -np.inf
+    x[4] = -1.0
+    x[4, [V - 2, 3]] = -0.0
+    x[4, 7] = 0.0
+    x[5, V // 3] = np.inf
+    allowed = np.ones((rows, V), bool)
+    allowed[6] = False                           # nothing admitted
+    allowed[7] = False
+    allowed[7, V - 5:] = True                    # only the last few tokens
+    masks = WL.mask_words(allowed)
+    pols = [J.policy()] * 6 + [J.policy(constrained=True)] * 2
+    kw = dict(masks=masks)
+    if bf16:
+        kw["logits_bf16"] = (x.view(np.uint32) >> 16).astype(np.uint16)
+    else:
+        kw["logits"] = x
+    s = J.Sampler(V, rows)
+    g = run_gpu(V, pols, sampler=s, repeat=3, **kw)
+    r = run_oracle(V, pols, **kw)
+    assert_same(g, r)
+    assert g["tokens"][1] == 10 and g["tokens"][2] == NO and g["tokens"][3] == 0
+    assert g["tokens"][4] == 3 and g["tokens"][5] == V // 3 and g["tokens"][6] == NO
+    assert g["tokens"][7] >= V - 5
+    for n in (3, 1):
+        sub = {k: v[rows - n:] for k, v in kw.items()}
+        g = run_gpu(V, pols[rows - n:], sampler=s, **sub)
+        r = run_oracle(V, pols[rows - n:], **sub)
+        assert_same(g, r)
+    s.close()
+
+
 def test_determinism_repeat():
     c = WL.config2(B=16)
     pol = [J.policy(**c["policy"])] * 16
