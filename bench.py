@@ -41,9 +41,9 @@ def parse():
                     help="bound of the CPU-baseline sample")
     ap.add_argument("--history", default="uniform", choices=["uniform", "zipf", "mixed"],
                     help="C2 only: zipf gives every row a history clustered in low ids "
-                         "(Zipf 1.2), whose first chunk overflows the fast kernel's "
-                         "penalty slots, so the rows take select_kernel; mixed does so "
-                         "for every fourth row (the call is split between the kernels)")
+                         "(Zipf 1.2, about 450 distinct ids in the first chunk, past 256 "
+                         "fixed penalty slots: the table widens to 512 a chunk); mixed "
+                         "does so for every fourth row")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 64 MiB device copy (20 times): the "
@@ -70,17 +70,14 @@ def build_workload(cfg, mode, history="uniform"):
         hists, label = c["histories"], "2048 ids"
         if history != "uniform":
             # Ids clustered near 0 as real text's are: about 450 distinct ids
-            # below 8192, past the first chunk's 256 fixed slots.
+            # below 8192, past the first chunk's 256 fixed slots (the table
+            # widens to 512).
             rng = np.random.default_rng(22)
             every = 1 if history == "zipf" else 4
             hists = [np.minimum(rng.zipf(1.2, len(h)) - 1, c["V"] - 1).astype(np.uint32)
                      if r % every == 0 else h for r, h in enumerate(hists)]
-            label = ("2048 Zipf(1.2)-clustered ids (select_kernel)" if every == 1 else
-                     "2048 ids, every 4th row Zipf(1.2)-clustered (split launch)")
-            # The events around the selection then span select_kernel (and,
-            # split, the fast kernel after it).
-            w["kernel"] = ("jf::select_kernel<0>" if every == 1 else
-                           "jf::select_kernel<0> then jf::select_fast_kernel<0>")
+            label = ("2048 Zipf(1.2)-clustered ids" if every == 1 else
+                     "2048 ids, every 4th row Zipf(1.2)-clustered")
         w.update(V=c["V"], logits=c["logits"], policies=[J.policy(**c["policy"])] * B,
                  histories=hists, generated=c["generated"], mark_prompt=False,
                  uniforms=c["uniforms"],

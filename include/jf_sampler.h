@@ -120,8 +120,11 @@ int jf_penalty_table_rebuild(jf_penalty_table *table, uint32_t row,
  * row `row`, in order; Runtime.cpp:1397-1406 (commitSelected) is the call
  * site it serves. The table is updated in place on `stream` by a kernel
  * whose updates travel as kernel arguments: no upload of the row and no wait
- * on earlier work. All-or-nothing: a token outside the vocabulary, or new
- * tokens beyond the row's max_entries, fail before the row changes. */
+ * on earlier work. (Once in a table's life, when a row first needs more
+ * than 256 of a chunk's fixed slots and 512 suffice, a rebuild or count
+ * widens them to 512 and uploads every row's slots.) All-or-nothing: a
+ * token outside the vocabulary, or new tokens beyond the row's
+ * max_entries, fail before the row changes. */
 int jf_penalty_table_count(jf_penalty_table *table, uint32_t row,
                            const uint32_t *selected, uint64_t count,
                            void *stream);

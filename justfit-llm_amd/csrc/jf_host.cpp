@@ -49,20 +49,26 @@ uint32_t PenaltyRows::slot_value(const PenaltyEntry &e) {
          (e.word & JF_PENALTY_COUNT_MASK);
 }
 
-// Whether every chunk fits its slots with every count inside the slot's
+// Whether every chunk fits n slots with every count inside the slot's
 // count field.
-void PenaltyRows::refit(uint32_t row) {
+bool PenaltyRows::fits_at(uint32_t row, uint32_t n) const {
   const std::vector<uint32_t> &off = offsets_[row];
-  bool fits = true;
-  for (uint32_t c = 0; c < chunks_ && fits; ++c) {
+  for (uint32_t c = 0; c < chunks_; ++c) {
     const uint32_t b0 = c * kBucketsPerChunk;
     const uint32_t b1 = std::min(b0 + kBucketsPerChunk, buckets_);
-    if (off[b1] - off[b0] > slot_count_) fits = false;
+    if (off[b1] - off[b0] > n) return false;
   }
-  for (uint32_t b = 0; b < buckets_ && fits; ++b)
+  for (uint32_t b = 0; b < buckets_; ++b)
     for (const PenaltyEntry &e : bucket_[row][b])
-      if ((e.word & JF_PENALTY_COUNT_MASK) > kSlotCountMask) fits = false;
-  fits_[row] = fits ? 1 : 0;
+      if ((e.word & JF_PENALTY_COUNT_MASK) > kSlotCountMask) return false;
+  return true;
+}
+
+void PenaltyRows::refit(uint32_t row) { fits_[row] = fits_at(row, slot_count_) ? 1 : 0; }
+
+void PenaltyRows::set_slot_count(uint32_t n) {
+  slot_count_ = n;
+  for (uint32_t r = 0; r < rows_; ++r) refit(r);
 }
 
 int PenaltyRows::rebuild(uint32_t row, const uint32_t *words) {

@@ -73,6 +73,11 @@ class PenaltyRows {
   uint32_t size(uint32_t row) const { return offsets_[row][buckets_]; }
   bool holds(uint32_t row, uint32_t token) const;
   bool fits(uint32_t row) const { return fits_[row] != 0; }
+  // Whether the row would fit chunks of n slots.
+  bool fits_at(uint32_t row, uint32_t n) const;
+  // Lays the slots out n to a chunk from now on and decides again which
+  // rows fit.
+  void set_slot_count(uint32_t n);
   // The row as the device holds it: its entries in token order, its bucket
   // offsets (buckets + 1 values: the index of each bucket's first entry),
   // and its fixed slots (chunks x slot_count values, empty slots 0).

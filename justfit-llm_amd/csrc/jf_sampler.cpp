@@ -109,6 +109,9 @@ uint32_t effective_top_k(const jf_policy &p, uint32_t vocabulary) {
 
 }  // namespace
 
+// Fixed penalty slots a chunk at most (two per thread of the fast kernel).
+constexpr uint32_t kMaxSlots = 2 * jf::kThreads;
+
 struct jf_penalty_table {
   uint32_t vocabulary = 0;
   uint32_t rows = 0;
@@ -120,7 +123,9 @@ struct jf_penalty_table {
   // The fast kernel's fixed slots: [rows][chunks][slot_count], 8192-token
   // chunks; host.fits(row) when every chunk of the row fits its slots and
   // every count fits the slot's 18 bits (otherwise select_kernel takes the
-  // row).
+  // row). The array holds room for 512 slots a chunk; a table laid out 256
+  // to a chunk widens to 512 when a row needs more (a history clustered in
+  // one chunk's ids) and 512 suffice.
   uint32_t chunks = 0;
   uint32_t slot_count = 0;
   uint32_t *slots = nullptr;
@@ -270,12 +275,11 @@ int jf_penalty_table_create(uint32_t vocabulary, uint32_t rows,
   if (ge != hipSuccess) rc = hip_fail(ge, "hipGetDevice");
   if (rc == JF_OK) rc = device_alloc(&t->entries, (size_t)rows * max_entries, "penalty entries");
   if (rc == JF_OK) rc = device_alloc(&t->offsets, (size_t)rows * (t->buckets + 1), "penalty offsets");
-  if (rc == JF_OK)
-    rc = device_alloc(&t->slots, (size_t)rows * t->chunks * t->slot_count, "penalty slots");
+  const size_t slot_room = (size_t)rows * t->chunks * kMaxSlots;
+  if (rc == JF_OK) rc = device_alloc(&t->slots, slot_room, "penalty slots");
   if (rc == JF_OK) {
     ge = hipMemset(t->offsets, 0, (size_t)rows * (t->buckets + 1) * sizeof(uint32_t));
-    if (ge == hipSuccess)
-      ge = hipMemset(t->slots, 0, (size_t)rows * t->chunks * t->slot_count * sizeof(uint32_t));
+    if (ge == hipSuccess) ge = hipMemset(t->slots, 0, slot_room * sizeof(uint32_t));
     if (ge == hipSuccess) ge = hipDeviceSynchronize();
     if (ge != hipSuccess) rc = hip_fail(ge, "penalty table init");
   }
@@ -284,6 +288,34 @@ int jf_penalty_table_create(uint32_t vocabulary, uint32_t rows,
     return rc;
   }
   *out = t;
+  return JF_OK;
+}
+
+// The row's fixed slots as the host copy lays them out.
+static int upload_penalty_slots(jf_penalty_table *t, uint32_t row, void *stream) {
+  const size_t per_row = (size_t)t->chunks * t->slot_count;
+  std::vector<uint32_t> sl(per_row);
+  t->host.slots(row, sl.data());
+  return t->staging.upload(t->slots + (size_t)row * per_row, sl.data(),
+                           per_row * sizeof(uint32_t), (hipStream_t)stream);
+}
+
+// Widens a table of 256 slots a chunk to 512 once some row needs more than
+// 256 and fits 512: every row that fits then is laid out again (after the
+// updates already on `stream`).
+static int widen_slots(jf_penalty_table *t, void *stream) {
+  if (t->slot_count >= kMaxSlots) return JF_OK;
+  bool wider = false;
+  for (uint32_t r = 0; r < t->rows && !wider; ++r)
+    wider = !t->host.fits(r) && t->host.size(r) > 0 && t->host.fits_at(r, kMaxSlots);
+  if (!wider) return JF_OK;
+  t->slot_count = kMaxSlots;
+  t->host.set_slot_count(kMaxSlots);
+  for (uint32_t r = 0; r < t->rows; ++r) {
+    if (!t->host.fits(r)) continue;
+    const int rc = upload_penalty_slots(t, r, stream);
+    if (rc != JF_OK) return rc;
+  }
   return JF_OK;
 }
 
@@ -302,11 +334,7 @@ static int upload_penalty_row(jf_penalty_table *t, uint32_t row, void *stream) {
   rc = t->staging.upload(t->offsets + (size_t)row * (t->buckets + 1), off,
                          (t->buckets + 1) * sizeof(uint32_t), st);
   if (rc != JF_OK || !t->host.fits(row)) return rc;
-  const size_t per_row = (size_t)t->chunks * t->slot_count;
-  std::vector<uint32_t> sl(per_row);
-  t->host.slots(row, sl.data());
-  return t->staging.upload(t->slots + (size_t)row * per_row, sl.data(),
-                           per_row * sizeof(uint32_t), st);
+  return upload_penalty_slots(t, row, stream);
 }
 
 int jf_penalty_table_rebuild(jf_penalty_table *t, uint32_t row,
@@ -324,7 +352,8 @@ int jf_penalty_table_rebuild(jf_penalty_table *t, uint32_t row,
   if (rc != JF_OK) return rc;
   rc = t->host.rebuild(row, words.data());
   if (rc != JF_OK) return rc;
-  return upload_penalty_row(t, row, stream);
+  rc = upload_penalty_row(t, row, stream);
+  return rc == JF_OK ? widen_slots(t, stream) : rc;
 }
 
 // countPenaltyTokens (Sampling.cpp:75-80) of n (row, token) pairs, applied
@@ -395,7 +424,8 @@ static int count_pairs(jf_penalty_table *t, const uint32_t *rows, uint32_t one_r
     p.slot_value = op.slot_value;
     p.slot = op.slot == jf::kNoSlot ? 0xffffu : (op.slot | op.slot_used << 16);
   }
-  return flush();
+  rc = flush();
+  return rc == JF_OK ? widen_slots(t, stream) : rc;
 }
 
 int jf_penalty_table_count(jf_penalty_table *t, uint32_t row,

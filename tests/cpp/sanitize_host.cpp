@@ -130,6 +130,34 @@ void check_penalty_rows(std::mt19937 &rng) {
   }
 }
 
+// A table widened from 256 to 512 slots a chunk lays every row out as a
+// table built at 512 does, and fits exactly the rows that fit 512.
+void check_slot_widening(std::mt19937 &rng) {
+  const uint32_t V = 151936, rows = 4, max_entries = 2048;
+  jf::PenaltyRows narrow, wide;
+  narrow.init(V, rows, max_entries, 256);
+  wide.init(V, rows, max_entries, 512);
+  for (uint32_t row = 0; row < rows; ++row) {
+    // Row r holds 150 + 150 r distinct ids in the first chunk: 150, 300,
+    // 450, 600 (the last fits neither layout).
+    std::vector<uint32_t> words(V, 0);
+    for (uint32_t k = 0; k < 150 + 150 * row; ++k) words[k * 13 % 8192] = 1 + rng() % 3;
+    for (int k = 0; k < 200; ++k) words[8192 + rng() % (V - 8192)] += 1;
+    expect(narrow.rebuild(row, words.data()) == JF_OK, "rebuild narrow");
+    expect(wide.rebuild(row, words.data()) == JF_OK, "rebuild wide");
+    expect(narrow.fits(row) == (row == 0), "narrow fit", row);
+    expect(narrow.fits_at(row, 512) == (row < 3), "fit at 512", row);
+  }
+  narrow.set_slot_count(512);
+  for (uint32_t row = 0; row < rows; ++row) {
+    expect(narrow.fits(row) == wide.fits(row), "widened fit", row);
+    std::vector<uint32_t> a((size_t)narrow.chunks() * 512), b(a.size());
+    narrow.slots(row, a.data());
+    wide.slots(row, b.data());
+    expect(a == b, "widened slots", row);
+  }
+}
+
 void check_policies() {
   const float temps[] = {0.0f, 1e-39f, 1.17549435e-38f, 0.7f, INFINITY, NAN, -1.0f};
   const float ps[] = {0.0f, 1e-7f, 0.5f, 1.0f, 1.0000001f, NAN};
@@ -362,6 +390,7 @@ void check_oracle(std::mt19937 &rng) {
 int main() {
   std::mt19937 rng(20260);
   check_penalty_rows(rng);
+  check_slot_widening(rng);
   check_policies();
   check_mask_wire(rng);
   check_tree_builder(rng);

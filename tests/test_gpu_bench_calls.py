@@ -4,8 +4,8 @@ and one of its steps is compared with the oracle row by row (bit-exact
 tokens, and the draft probabilities where the step writes them). C2 and C5
 run as benchmarked, without kept outputs or draft probabilities; C1, C3 and
 C4 greedy and sampled as the bench issues them; C2 also with histories
-clustered in low ids (every row on select_kernel, and every fourth row, a
-call split between the two select kernels)."""
+clustered in low ids (every row, and every fourth row), which widen the
+penalty table's fixed slots from 256 to 512 a chunk."""
 import numpy as np
 import pytest
 

@@ -122,6 +122,48 @@ def test_row_pushed_past_its_slots_still_selects_exactly():
     table.close()
 
 
+def test_slots_widen_for_a_clustered_row():
+    """A table laid out 256 slots to a chunk widens to 512 when a rebuilt row
+    holds more than 256 ids in one chunk and 512 suffice: every fitting row
+    is laid out again. Counts then update the wider layout in place, and a
+    row pushed past 512 leaves the fast kernel. Selections bit-exact
+    against the oracle at each stage."""
+    rows = 3
+    rng = np.random.default_rng(17)
+    table = J.PenaltyTable(V, rows, 2048)  # 2048 * 1.5 <= 19 chunks * 256: 256 slots
+    words = np.zeros((rows, V), np.uint32)
+    hist = [rng.integers(0, V, 900, dtype=np.uint32),
+            np.concatenate([np.arange(0, 300, dtype=np.uint32),
+                            rng.integers(8192, V, 200, dtype=np.uint32)]),
+            rng.integers(0, V, 700, dtype=np.uint32)]
+    for r in (0, 2, 1):  # the clustered row last: the others are laid out again
+        table.rebuild(r, hist[r], 100, None, True)
+        words[r] = O.rebuild_penalty_words(V, hist[r], 100, None, True)[1]
+    pols = [J.policy(repetition=1.4, presence=0.7),
+            J.policy(temperature=0.9, top_k=30, frequency=1.2, presence=0.5),
+            J.policy(temperature=1.0, top_p=0.8, repetition=1.6)]
+    lg = _logits(rows, 23)
+    lg[:, :700] += 4.0
+    uniforms = rng.random(rows, dtype=np.float32)
+    got, want = _select(table, words, lg, pols, uniforms)
+    np.testing.assert_array_equal(got, want)
+    # 150 new ids in row 1's first chunk (450 <= 512) and counts elsewhere.
+    pr = [1] * 150 + [0, 2, 0, 2]
+    pt = list(range(300, 450)) + [5, 6, 7, 8192 * 4 + 1]
+    table.count_rows(pr, pt)
+    for r, t in zip(pr, pt):
+        words[r, t] += 1
+    got, want = _select(table, words, lg, pols, uniforms)
+    np.testing.assert_array_equal(got, want)
+    # 100 more (550 > 512): row 1 takes select_kernel.
+    more = list(range(450, 550))
+    table.count_rows([1] * len(more), more)
+    words[1, more] += 1
+    got, want = _select(table, words, lg, pols, uniforms)
+    np.testing.assert_array_equal(got, want)
+    table.close()
+
+
 def test_count_errors_leave_the_row_unchanged():
     table = J.PenaltyTable(1000, 2, 8)
     table.rebuild(0, [1, 2, 3], 1, None, True)
