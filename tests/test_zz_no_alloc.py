@@ -1,7 +1,9 @@
 """jf_sample_static (the entry point that allocates nothing, its scratch a
 file-scope device array) against jf_sample on the same inputs: two calls in a
 row, the second smaller, each bit-exact in tokens, draft probabilities and
-kept outputs. Also its size limits, which it rejects before any device call."""
+kept outputs; then two all-greedy calls, the second smaller, which finish
+through the array's packed chunk bests. Also its size limits, which it
+rejects before any device call."""
 import ctypes
 
 import numpy as np
@@ -31,6 +33,20 @@ def _case_inputs(which):
         return dict(V=c["V"], logits=c["logits"], policies=[J.policy(**c["policy"])] * B,
                     histories=c["histories"], generated=c["generated"],
                     uniforms=c["uniforms"], kept_capacity=64)
+    if which in ("greedy", "greedy_small"):
+        # Every row greedy: the selection finishes the rows itself through
+        # the scratch's packed chunk bests, which each call leaves zeroed.
+        rng = np.random.default_rng(78 if which == "greedy" else 79)
+        V, rows = (151936, 24) if which == "greedy" else (20000, 3)
+        x = rng.normal(0, 2, (rows, V)).astype(np.float32)
+        x[0, [5, V - 1]] = 30.0  # the maximum in two chunks: the lower id
+        histories = [rng.integers(0, V, 200).astype(np.uint32) if r % 3 == 1 else None
+                     for r in range(rows)]
+        pols = [J.policy(repetition=1.3, presence=0.4) if h is not None else J.policy()
+                for h in histories]
+        return dict(V=V, logits=x, policies=pols, histories=histories,
+                    generated=[100] * rows, uniforms=rng.random(rows).astype(np.float32),
+                    kept_capacity=0)
     rng = np.random.default_rng(77)
     V, rows = 40000, 6
     x = np.round(rng.normal(0, 2, (rows, V)), 1).astype(np.float32)
@@ -96,7 +112,7 @@ def _host(out, dp, kept):
 def test_static_entry_point_matches_jf_sample_on_two_calls():
     import torch
     dev = torch.device("cuda", 0)
-    for which in ("c2", "small"):
+    for which in ("c2", "small", "greedy", "greedy_small"):
         inp = _case_inputs(which)
         print(f"static vs sampler: case {which} V={inp['V']} rows={len(inp['policies'])}",
               flush=True)
