@@ -45,6 +45,9 @@ enum RowFlags : uint32_t {
   kRowMinP = 16u,
   kRowTopP = 32u,
   kRowTopK = 64u,
+  // A drafted row with no cut, penalty, mask or extra tokens: its residual
+  // pass runs in residual_kernel (set by the host).
+  kRowLean = 128u,
 };
 
 // One block's summary of its chunk of a row.
@@ -352,6 +355,13 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream);
 // Rows with no cut (grid rows x per_row: per_row = chunks when the launch
 // has drafted uncut rows, else 1).
 int launch_uncut(const SampleLaunch &a, uint32_t dtype, uint32_t per_row, void *stream);
+// residual_kernel over the rows row_of[0, n) (n <= kKernargRows), before
+// launch_uncut on the same stream.
+struct LeanLaunch {
+  SampleLaunch a;
+  uint32_t row_of[kKernargRows];
+};
+int launch_residual(const LeanLaunch &l, uint32_t n, uint32_t dtype, void *stream);
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream);
 int launch_accept_tree(const AcceptTreeLaunch &a, void *stream);

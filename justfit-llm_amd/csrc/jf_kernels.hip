@@ -3612,6 +3612,161 @@ __device__ __forceinline__ void uncut_draw(const SampleLaunch &a, const RowParam
   }
 }
 
+struct __align__(16) LeanLds {
+  uint32_t cids[16];
+  float cprobs[16];
+  uint64_t wl[kWaves];
+  float mc;      // this chunk's maximum
+  uint64_t rc;   // its rescale R_c
+  uint64_t W;    // the row's mass
+  uint32_t ok;   // the row has mass to draw from
+};
+
+// The residual pass of the rows flagged kRowLean (drafted, no cut, no
+// penalty, mask or extra tokens), one block per (row, chunk): the same
+// partial slots as uncut_kernel's pass (the chunk's residual mass and its
+// slices', the draft token's float weight), from the same arithmetic, but
+// with nothing else in the kernel and half a chunk's logits and q held at
+// a time, so it keeps few registers and many waves per SIMD. uncut_kernel
+// then finishes these rows in one block each (this launch ends first).
+template <int DT, bool DENSE>
+__global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
+  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS, SLAB = Geo<DT>::SLAB;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  constexpr int HL = LOADS / 2, HV = HL * VEC;  // loads and values per half
+  static_assert(HL == 2 || HL == 4, "two or four loads a half");
+  const SampleLaunch &a = l.a;
+  __shared__ LeanLds s;
+  const uint32_t S = a.chunks;
+  const uint32_t row = l.row_of[blockIdx.x / S], chunk = blockIdx.x % S;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const RowParams rp = a.params[row];
+  const uint32_t draft = row_draft(a, rp);
+  if (draft == kNoToken) return;  // drawn plainly by uncut_kernel
+  const float inv_t = rp.inv_t;
+  // The row's maximum, this chunk's rescale and the row's mass from the
+  // chunk summaries, as uncut_kernel computes them (wave 0, S <= 64).
+  const BlockHeader *hb = a.headers + (uint64_t)row * S;
+  StagePartial *parts = a.partials + (uint64_t)row * S;
+  if (w == 0) {
+    const bool in = lane < S;
+    const uint32_t at = in ? lane : 0u;
+    const float hm = hb[at].maximum;
+    const uint32_t hadm = hb[at].admitted;
+    const uint64_t hmass = parts[at].v[0];
+    const float m = in ? hm : -3.402823466e38f;
+    const float M = wave_max_f32(m);
+    const uint64_t R = in ? chunk_scale(m, M, inv_t) : 0ull;
+    const uint64_t W = wave_sum_u64(scale_down(in ? hmass : 0ull, R));
+    const uint32_t admitted = wave_sum_u32(in ? hadm : 0u);
+    if (lane == chunk) {
+      s.mc = m;
+      s.rc = R;
+    }
+    if (lane == 0) {
+      s.W = W;
+      s.ok = admitted != 0 && M != __builtin_inff() && W != 0 ? 1u : 0u;
+    }
+  }
+  stage_candidates(a, rp, s);  // ends with a barrier
+  if (!s.ok) return;  // uncut_kernel writes the sentinel
+  const float mc = s.mc;
+  const uint64_t Rc = s.rc, W = s.W;
+  const uint32_t V = a.vocabulary, base = chunk * CHUNK;
+  const uint32_t lane_base = base + tid * VEC;
+  const bool full = base + CHUNK <= V;
+  const bool vec_x = full && a.aligned, vec_q = full && a.q_aligned;
+  const float *qrow = DENSE ? a.dense_q + (uint64_t)rp.cand_index * a.q_stride : nullptr;
+  const bool stops = (rp.flags & kRowExcludeStop) &&
+                     ((a.stop0 >= base && a.stop0 < base + CHUNK) ||
+                      (a.stop1 >= base && a.stop1 < base + CHUNK));
+  uint64_t total = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float xv[HV], qv[HV];
+#pragma unroll
+    for (int jj = 0; jj < HL; ++jj) {
+      const uint32_t t0 = lane_base + (h * HL + jj) * SLAB;
+      if constexpr (DT == 0) {
+        const float *rowp = (const float *)a.logits + (uint64_t)row * a.stride;
+        if (vec_x) {
+          const f32x4 v = *(const f32x4 *)(rowp + t0);
+          xv[jj * 4 + 0] = v.x;
+          xv[jj * 4 + 1] = v.y;
+          xv[jj * 4 + 2] = v.z;
+          xv[jj * 4 + 3] = v.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e)
+            xv[jj * VEC + e] = t0 + e < V ? rowp[t0 + e] : kNotAdmitted;
+        }
+      } else {
+        const uint16_t *rowp = (const uint16_t *)a.logits + (uint64_t)row * a.stride;
+        if (vec_x) {
+          const u32x4 v = *(const u32x4 *)(rowp + t0);
+          const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            xv[jj * 8 + 2 * k] = u2f(vw[k] << 16);
+            xv[jj * 8 + 2 * k + 1] = u2f(vw[k] & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e)
+            xv[jj * VEC + e] = t0 + e < V ? bf16_to_float(rowp[t0 + e]) : kNotAdmitted;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const uint32_t t = t0 + e;
+        if constexpr (DENSE) {
+          if (vec_q) {
+            if (e % 4 == 0) {
+              const float4 f = *reinterpret_cast<const float4 *>(qrow + t);
+              qv[jj * VEC + e] = f.x;
+              qv[jj * VEC + e + 1] = f.y;
+              qv[jj * VEC + e + 2] = f.z;
+              qv[jj * VEC + e + 3] = f.w;
+            }
+          } else {
+            qv[jj * VEC + e] = t < V ? qrow[t] : 0.0f;
+          }
+        } else {
+          qv[jj * VEC + e] = draft_q(a, rp, t, s);
+        }
+        if (stops && (t == a.stop0 || t == a.stop1)) xv[jj * VEC + e] = kNotAdmitted;
+      }
+    }
+    uint64_t lv[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int jj = 0; jj < HL; ++jj)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        lv[jj] += residual_of(scaled_weight(xv[jj * VEC + e], mc, inv_t, Rc), W,
+                              qv[jj * VEC + e]);
+    // Lane l holds the wave's sum of load h * HL + l / 16 (l / 16 < HL).
+    const uint64_t sl = wave_sums_u64<4>(lv);
+    if (lane % 16 == 0 && lane / 16 < (uint32_t)HL)
+      parts[chunk].v[kResidualSlot + 1 + (h * HL + lane / 16) * kWaves + w] = sl;
+    uint64_t t = sl + shfl_xor_u64(sl, 16);
+    total += t + shfl_xor_u64(t, 32);
+    // The draft token's float weight, from the thread that holds it.
+    if (draft < V && draft / CHUNK == chunk) {
+      const uint32_t o = draft - base, j = o / SLAB;
+      if (j / HL == (uint32_t)h && tid == (o % SLAB) / VEC) {
+        const uint32_t i = (j % HL) * VEC + o % VEC;
+        float xd = 0.0f;
+#pragma unroll
+        for (int k = 0; k < HV; ++k) xd = (uint32_t)k == i ? xv[k] : xd;
+        parts[chunk].v[kDraftSlot] = (uint64_t)f2u(weight_of(xd, mc, inv_t));
+      }
+    }
+  }
+  if (lane == 0) s.wl[w] = total;
+  __syncthreads();
+  if (tid == 0) parts[chunk].v[kResidualSlot] = s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3];
+}
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_t per_row) {
   constexpr int TPL = Geo<DT>::TPL, VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS,
@@ -3689,54 +3844,61 @@ __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_
     return;
   }
 
-  // A drafted row: this chunk's residual masses per slice.
-  float qv[TPL];
-  if (a.dense_q) load_dense_q<DT>(a, rp, chunk, qv);
   float xs[TPL];
-  load_chunk<DT>(a, rp, row, chunk, s, xs);
-  stage_candidates(a, rp, s);
-  const float mc = s.cmax[chunk];
-  const uint64_t Rc = s.cscale[chunk];
-  const uint32_t lane_base = chunk * CHUNK + tid * VEC;
-  uint64_t total = 0;
-  // Four loads at a time (fewer live registers than all of them at once).
+  if (rp.flags & kRowLean) {
+    // residual_kernel summed this row's residual masses (its launch ended
+    // before this one began): chunk 0's block draws.
+    if (chunk != 0) return;
+    stage_candidates(a, rp, s);
+  } else {
+    // A drafted row: this chunk's residual masses per slice.
+    float qv[TPL];
+    if (a.dense_q) load_dense_q<DT>(a, rp, chunk, qv);
+    load_chunk<DT>(a, rp, row, chunk, s, xs);
+    stage_candidates(a, rp, s);
+    const float mc = s.cmax[chunk];
+    const uint64_t Rc = s.cscale[chunk];
+    const uint32_t lane_base = chunk * CHUNK + tid * VEC;
+    uint64_t total = 0;
+    // Four loads at a time (fewer live registers than all of them at once).
 #pragma unroll
-  for (int h = 0; h < LOADS / 4; ++h) {
-    uint64_t lv[4];
+    for (int h = 0; h < LOADS / 4; ++h) {
+      uint64_t lv[4];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int j = h * 4 + jj;
-      lv[jj] = 0;
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = h * 4 + jj;
+        lv[jj] = 0;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const int i = j * VEC + e;
-        const float q = a.dense_q ? qv[i] : draft_q(a, rp, lane_base + j * SLAB + e, s);
-        lv[jj] += residual_of(scaled_weight(xs[i], mc, inv_t, Rc), W, q);
+        for (int e = 0; e < VEC; ++e) {
+          const int i = j * VEC + e;
+          const float q = a.dense_q ? qv[i] : draft_q(a, rp, lane_base + j * SLAB + e, s);
+          lv[jj] += residual_of(scaled_weight(xs[i], mc, inv_t, Rc), W, q);
+        }
+      }
+      // Lane l holds the wave's sum of load h * 4 + l / 16.
+      const uint64_t sl = wave_sums_u64<4>(lv);
+      if (lane % 16 == 0)
+        st_dev(&parts[chunk].v[kResidualSlot + 1 + (h * 4 + lane / 16) * kWaves + w], sl);
+      uint64_t t = sl + shfl_xor_u64(sl, 16);
+      total += t + shfl_xor_u64(t, 32);
+    }
+    // The draft token's float weight, from the thread that holds it.
+    if (draft < a.vocabulary && draft / CHUNK == chunk) {
+      const uint32_t o = draft - chunk * CHUNK;
+      if (tid == (o % SLAB) / VEC) {
+        const uint32_t i = (o / SLAB) * VEC + o % VEC;
+        float xd = 0.0f;
+#pragma unroll
+        for (int k = 0; k < TPL; ++k) xd = (uint32_t)k == i ? xs[k] : xd;
+        st_dev(&parts[chunk].v[kDraftSlot], (uint64_t)f2u(weight_of(xd, mc, inv_t)));
       }
     }
-    // Lane l holds the wave's sum of load h * 4 + l / 16.
-    const uint64_t sl = wave_sums_u64<4>(lv);
-    if (lane % 16 == 0)
-      st_dev(&parts[chunk].v[kResidualSlot + 1 + (h * 4 + lane / 16) * kWaves + w], sl);
-    uint64_t t = sl + shfl_xor_u64(sl, 16);
-    total += t + shfl_xor_u64(t, 32);
+    if (lane == 0) s.wl[w] = total;
+    __syncthreads();
+    if (tid == 0)
+      st_dev(&parts[chunk].v[kResidualSlot], s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3]);
+    if (!arrive_last(a.counters + row, S, s)) return;
   }
-  // The draft token's float weight, from the thread that holds it.
-  if (draft < a.vocabulary && draft / CHUNK == chunk) {
-    const uint32_t o = draft - chunk * CHUNK;
-    if (tid == (o % SLAB) / VEC) {
-      const uint32_t i = (o / SLAB) * VEC + o % VEC;
-      float xd = 0.0f;
-#pragma unroll
-      for (int k = 0; k < TPL; ++k) xd = (uint32_t)k == i ? xs[k] : xd;
-      st_dev(&parts[chunk].v[kDraftSlot], (uint64_t)f2u(weight_of(xd, mc, inv_t)));
-    }
-  }
-  if (lane == 0) s.wl[w] = total;
-  __syncthreads();
-  if (tid == 0)
-    st_dev(&parts[chunk].v[kResidualSlot], s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3]);
-  if (!arrive_last(a.counters + row, S, s)) return;
 
   // The row's last block: p(draft), then the residual draw when it has mass.
   if (w == 0) {
@@ -3958,6 +4120,25 @@ int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream) {
 #endif
 
 #if JF_IN(4)
+int launch_residual(const LeanLaunch &l, uint32_t n, uint32_t dtype, void *stream) {
+  const dim3 grid(n * l.a.chunks), block(kThreads);
+  const hipStream_t st = (hipStream_t)stream;
+  // A sparse draft's 16-candidate lookup per token takes about 30 more
+  // registers than a dense q row: separate instantiations.
+  if (l.a.dense_q) {
+    if (dtype == 0)
+      hipLaunchKernelGGL((residual_kernel<0, true>), grid, block, 0, st, l);
+    else
+      hipLaunchKernelGGL((residual_kernel<1, true>), grid, block, 0, st, l);
+  } else {
+    if (dtype == 0)
+      hipLaunchKernelGGL((residual_kernel<0, false>), grid, block, 0, st, l);
+    else
+      hipLaunchKernelGGL((residual_kernel<1, false>), grid, block, 0, st, l);
+  }
+  return (int)hipGetLastError();
+}
+
 int launch_uncut(const SampleLaunch &a, uint32_t dtype, uint32_t per_row, void *stream) {
   const dim3 grid(a.rows * per_row), block(kThreads);
   if (dtype == 0)

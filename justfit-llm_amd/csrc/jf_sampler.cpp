@@ -570,6 +570,19 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   const bool fast = n_fast == rows, split = n_fast && !fast;
   if (!split)
     for (uint32_t r = 0; r < rows; ++r) params[r].fast_row = 0;
+  // Drafted rows with no cut, penalty, mask or extra tokens: residual_kernel
+  // takes their residual pass (kRowLean; no other kernel reads the flag but
+  // uncut_kernel).
+  uint32_t n_lean = 0;
+  for (uint32_t r = 0; r < rows; ++r) {
+    jf::RowParams &rp = params[r];
+    const bool lean =
+        (rp.flags & jf::kRowSampled) && rp.draft_index != JF_NO_TOKEN && !rp.extra_count &&
+        !(rp.flags & (jf::kRowMinP | jf::kRowTopK | jf::kRowTopP | jf::kRowPenalized |
+                      jf::kRowConstrained));
+    rp.flags = lean ? rp.flags | jf::kRowLean : rp.flags & ~jf::kRowLean;
+    n_lean += lean ? 1u : 0u;
+  }
 
   rc = upload(upload_ctx, params, rows, sc.params, stream);
   if (rc != JF_OK) return rc;
@@ -635,6 +648,8 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   // them; the merge and the stages finish the other rows and skip these, so
   // only the cut rows decide the merge and the stages.
   constexpr uint32_t kCuts = jf::kRowMinP | jf::kRowTopK | jf::kRowTopP;
+  // uncut_drafted: drafted uncut rows whose residual pass stays in
+  // uncut_kernel (not kRowLean).
   bool any_uncut = false, any_cut = false, any_greedy = false, uncut_drafted = false;
   staged = need_count1 = need_topk = need_topp = false;
   for (uint32_t r = 0; r < rows; ++r) {
@@ -643,7 +658,7 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
       any_greedy = true;
     } else if (!(rp.flags & kCuts)) {
       any_uncut = true;
-      if (rp.draft_index != JF_NO_TOKEN) uncut_drafted = true;
+      if (rp.draft_index != JF_NO_TOKEN && !(rp.flags & jf::kRowLean)) uncut_drafted = true;
     } else {
       any_cut = true;
       if (rp.top_k > (uint32_t)jf::kBlockCandidates) {
@@ -687,7 +702,7 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
     for (uint32_t i = 0; uniform && i < n_fast; ++i) {
       const uint32_t r = row_at(i);
       const jf::RowParams &p = params[r];
-      uniform = p.flags == p0.flags && p.top_k == p0.top_k &&
+      uniform = ((p.flags ^ p0.flags) & ~jf::kRowLean) == 0 && p.top_k == p0.top_k &&
                 p.minp_offset == p0.minp_offset && p.repetition == p0.repetition &&
                 p.repetition_inverse == p0.repetition_inverse &&
                 p.presence == p0.presence && p.frequency == p0.frequency &&
@@ -738,8 +753,22 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
     }
   }
   if (any_uncut) {
-    // One block per row; a launch with drafted uncut rows takes one per
-    // (row, chunk) for their residual pass.
+    // residual_kernel over the kRowLean rows, then uncut_kernel: one block
+    // per row, or one per (row, chunk) when other drafted uncut rows need
+    // their residual pass there.
+    if (n_lean) {
+      jf::LeanLaunch R;
+      R.a = L;
+      uint32_t n = 0;
+      for (uint32_t r = 0; r < rows && e == hipSuccess; ++r) {
+        if (params[r].flags & jf::kRowLean) R.row_of[n++] = r;
+        if (n == (uint32_t)jf::kKernargRows || (n && r + 1 == rows)) {
+          e = jf::launch_residual(R, n, a->dtype, stream);
+          n = 0;
+        }
+      }
+      if (e != hipSuccess) return hip_fail((hipError_t)e, "residual launch");
+    }
     e = jf::launch_uncut(L, a->dtype, uncut_drafted ? L.chunks : 1u, stream);
     if (e != hipSuccess) return hip_fail((hipError_t)e, "uncut draw launch");
   }
