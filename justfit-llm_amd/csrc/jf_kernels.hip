@@ -3470,7 +3470,7 @@ __device__ __forceinline__ uint32_t pick_slice(uint64_t vg, uint32_t G, uint64_t
 // u * W, that chunk reloaded, and its first token (id order) whose running
 // mass P has floor(P * R_c / 2^32) past the remainder (sampling.metal:694-829
 // on these weights). A drafted row's blocks, one per chunk, sum the residual
-// max(floor(w * R_c / 2^32) - floor(W * q), 0) per slice; the row's last
+// weights residual_of(floor(w * R_c / 2^32), W, q) per slice; the row's last
 // block draws from them, or plainly when no residual mass remains, and
 // writes p(draft). Chunk 0's block writes the row's kept outputs. Greedy
 // rows take the argmax of the chunk bests when no merge runs.
