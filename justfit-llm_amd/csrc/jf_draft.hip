@@ -5,14 +5,16 @@
 // A lane has 8 query rows of fp32 draft logits; rows 1..7 are its proposal
 // positions. Two launches:
 //   draft_top16_kernel  one block per (8192-token chunk, proposal row): the
-//                       chunk's exact top 16 in (value desc, id asc) order;
-//                       the row's last block to arrive merges the chunks into
-//                       the row's candidates and unary scores.
-//   draft_edges_kernel  one block per (position, lane): the 16 x 16 table of
-//                       edge scores from the previous position's candidates
-//                       (the anchor at position 0) to this position's; the
-//                       lane's last block walks the 7 positions, greedily or
-//                       drawing at the lane's temperature.
+//                       chunk's exact top 16 in (value desc, id asc) order,
+//                       written as the chunk's partial list.
+//   draft_edges_kernel  one block per (position, lane): merges the partial
+//                       lists of its row (and of the previous row) into the
+//                       candidates and unary scores, then the 16 x 16 table
+//                       of edge scores from the previous position's
+//                       candidates (the anchor at position 0) to this
+//                       position's; the lane's last block walks the 7
+//                       positions, greedily or drawing at the lane's
+//                       temperature.
 // Edge scores are fp32 sums over the selector rank in ascending dimension
 // order (each product of bf16 operands is exact in fp32); the reference sums
 // the same terms in another order.
