@@ -3472,8 +3472,10 @@ __device__ __forceinline__ uint32_t pick_slice(uint64_t vg, uint32_t G, uint64_t
 // on these weights). A drafted row's blocks, one per chunk, sum the residual
 // weights residual_of(floor(w * R_c / 2^32), W, q) per slice; the row's last
 // block draws from them, or plainly when no residual mass remains, and
-// writes p(draft). Chunk 0's block writes the row's kept outputs. Greedy
-// rows take the argmax of the chunk bests when no merge runs.
+// writes p(draft). Drafted rows with no penalty, mask or extra tokens
+// (kRowLean) take that pass in residual_kernel, launched before, and their
+// chunk 0 block here draws. Chunk 0's block writes the row's kept outputs.
+// Greedy rows take the argmax of the chunk bests when no merge runs.
 //
 // Partial slots per (row, chunk): v[0] S_c; v[kDraftSlot] the draft token's
 // float weight against m_c; v[kResidualSlot] the chunk's residual mass and
