@@ -2548,7 +2548,8 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(SampleLaunch a) {
 // items). A 1024-bin histogram of the values over [value(thr), maximum] and
 // its suffix sums give each item its rank up to the items of its own bin,
 // which it compares directly; no sort. Returns n, or -1 when the values do
-// not spread over the bins or the boundary bin holds more than 64 items.
+// not spread over the bins, the boundary bin holds more than 64 items, or
+// more than 64 items would be kept (K above 64).
 // The caller zeroed s.merge.bins and s.merge.key[1024, 2048) before a
 // barrier. Every thread calls it. Uses s.merge.id[1024, 2048) and s.hist.
 template <int PER>
@@ -2586,6 +2587,7 @@ __device__ __forceinline__ int rank_select(const uint64_t (&v)[PER], uint32_t va
                  e0 = e1 + c4.y;
   // The boundary bin: where the count from the top reaches K.
   const uint32_t need = min(K, total);
+  if (need > 64u) return -1;  // more than one wave finishes (K above 64)
   uint32_t bstar = 0xffffffffu, bcount = 0;
   if (e3 < need && e3 + c4.w >= need) { bstar = 4 * tid + 3; bcount = c4.w; }
   else if (e2 < need && e2 + c4.z >= need) { bstar = 4 * tid + 2; bcount = c4.z; }

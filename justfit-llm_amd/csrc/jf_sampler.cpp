@@ -726,13 +726,15 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   }
   if (e != hipSuccess) return hip_fail((hipError_t)e, "select launch");
   // The small-K merge takes launches whose cut rows keep at most 64 tokens
-  // and read sparse draft probabilities (or none).
+  // by their top-k, or have a min-p floor (which usually leaves few: rows
+  // whose floor leaves more than 64 take its general path), and read sparse
+  // draft probabilities (or none).
   bool small = !staged && !a->draft_q && a->uniform_offset <= 0xffffffffull &&
                a->uniform_stride <= 0xffffffffull;
   for (uint32_t r = 0; small && r < rows; ++r) {
     const jf::RowParams &rp = params[r];
     if ((rp.flags & jf::kRowSampled) && (rp.flags & kCuts) &&
-        (!(rp.flags & jf::kRowTopK) || rp.top_k > 64u))
+        !((rp.flags & jf::kRowTopK) && rp.top_k <= 64u) && !(rp.flags & jf::kRowMinP))
       small = false;
   }
   if (need_merge) {
