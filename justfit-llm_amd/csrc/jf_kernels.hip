@@ -2855,8 +2855,15 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     }
     __syncthreads();
   }
-  // What the speculative fetch does not cover: the general merge.
-  if (tid == 0) g_small_launch = a;
+  // What the speculative fetch does not cover: the general merge. The
+  // launch record is copied word by word from the argument segment here
+  // (one word a thread), so no field of it stays live from the kernel's
+  // entry (the compiler otherwise kept some in private memory for this).
+  {
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(&a);
+    uint32_t *dst = reinterpret_cast<uint32_t *>(&g_small_launch);
+    for (uint32_t k = tid; k < sizeof(SampleLaunch) / 4; k += kThreads) dst[k] = src[k];
+  }
   __syncthreads();
   merge_small_general<DT>(row);
 }
