@@ -35,19 +35,31 @@ __global__ __launch_bounds__(256) void tree_gather_kernel(GatherLaunch g) {
   // Every source first, then every destination: a source row path[i] > i
   // is overwritten (if at all) only at step path[i] of the in-order copy,
   // after step i read it, so reading all sources up front reads the same
-  // values, with all loads in flight at once.
-  using Unit = std::conditional_t<VEC8, uint4, uint16_t>;
-  Unit v[kGatherDepth];
-  bool move[kGatherDepth];
+  // values, with all loads in flight at once. The path is the block's, so
+  // which rows move is decided in scalar registers; a row that stays loads
+  // the first moving row's source again (a cache hit, no HBM read) so that
+  // every load is unconditional and the values stay in registers.
+  uint32_t src[kGatherDepth], move = 0, first = kGatherDepth;
 #pragma unroll
   for (uint32_t i = 0; i < kGatherDepth; ++i) {
-    const uint32_t src = i < rows ? path[i] : i;
-    move[i] = src != i && src < g.rows;
-    if (move[i]) v[i] = *(const Unit *)(g.data + base + (uint64_t)src * g.row_stride);
+    src[i] = i < rows ? path[i] : i;
+    if (src[i] != i && src[i] < g.rows) {
+      move |= 1u << i;
+      first = min(first, i);
+    }
+  }
+  if (!move) return;
+  typedef uint32_t U32x4 __attribute__((ext_vector_type(4)));
+  using Unit = std::conditional_t<VEC8, U32x4, uint16_t>;
+  Unit v[kGatherDepth];
+#pragma unroll
+  for (uint32_t i = 0; i < kGatherDepth; ++i) {
+    const uint32_t from = (move >> i) & 1u ? src[i] : src[first];
+    v[i] = *(const Unit *)(g.data + base + (uint64_t)from * g.row_stride);
   }
 #pragma unroll
   for (uint32_t i = 0; i < kGatherDepth; ++i)
-    if (move[i]) *(Unit *)(g.data + base + (uint64_t)i * g.row_stride) = v[i];
+    if ((move >> i) & 1u) *(Unit *)(g.data + base + (uint64_t)i * g.row_stride) = v[i];
 }
 
 int launch_tree_gather(const GatherLaunch &g, bool vec8, void *stream, void *start_event,
