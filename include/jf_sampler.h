@@ -118,9 +118,13 @@ int jf_penalty_table_rebuild(jf_penalty_table *table, uint32_t row,
                              void *stream);
 /* countPenaltyTokens (Sampling.cpp:75-80) of `count` host tokens into table
  * row `row`, in order; Runtime.cpp:1397-1406 (commitSelected) is the call
- * site it serves. The table is updated in place on `stream` by a kernel
- * whose updates travel as kernel arguments: no upload of the row and no wait
- * on earlier work. (Once in a table's life, when a row first needs more
+ * site it serves. The table is updated in place on `stream` by one kernel
+ * launch: up to 64 tokens' updates travel as kernel arguments; a call with
+ * more puts them in host-mapped pinned memory that the kernel reads (four
+ * such buffers a table, each reused once the launch that read it has
+ * completed: the only wait on earlier work). Nothing of the row is
+ * uploaded. Calls on one table must be ordered (one stream, or streams
+ * ordered by the caller). (Once in a table's life, when a row first needs more
  * than 256 of a chunk's fixed slots and 512 suffice, a rebuild or count
  * widens them to 512 and uploads every row's slots.) All-or-nothing: a
  * token outside the vocabulary, or new tokens beyond the row's
@@ -130,7 +134,7 @@ int jf_penalty_table_count(jf_penalty_table *table, uint32_t row,
                            void *stream);
 /* The same for one step's commits of every lane at once: pair i counts
  * token selected[i] into row rows[i] (rows may repeat; each row's tokens
- * apply in order). One launch per 32 tokens. */
+ * apply in order). One launch per call. */
 int jf_penalty_table_count_rows(jf_penalty_table *table, const uint32_t *rows,
                                 const uint32_t *selected, uint64_t count,
                                 void *stream);

@@ -100,6 +100,16 @@ bool PenaltyRows::holds(uint32_t row, uint32_t token) const {
   return it != v.end() && it->token == token;
 }
 
+void PenaltyRows::prefetch(uint32_t row, uint32_t token) const {
+  const uint32_t b = token / kPenaltyBucket;
+  const std::vector<PenaltyEntry> &v = bucket_[row][b];
+  const PenaltyEntry *d = v.data();
+  for (size_t k = 0; k < v.size(); k += 8) __builtin_prefetch(d + k);
+  const uint32_t *off = offsets_[row].data();
+  for (uint32_t k = b; k <= buckets_; k += 16) __builtin_prefetch(off + k);
+  __builtin_prefetch(off + (token / kPenaltyChunk) * kBucketsPerChunk);
+}
+
 int PenaltyRows::count(uint32_t row, uint32_t token, PenaltyOp *op) {
   const uint32_t b = token / kPenaltyBucket;
   std::vector<PenaltyEntry> &v = bucket_[row][b];

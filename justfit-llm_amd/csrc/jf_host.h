@@ -72,6 +72,10 @@ class PenaltyRows {
 
   uint32_t size(uint32_t row) const { return offsets_[row][buckets_]; }
   bool holds(uint32_t row, uint32_t token) const;
+  // Starts the loads a count of `token` on row `row` will make (its bucket's
+  // entries and the row's offsets), so that a batch of counts over many
+  // rows overlaps their cache misses.
+  void prefetch(uint32_t row, uint32_t token) const;
   bool fits(uint32_t row) const { return fits_[row] != 0; }
   // Whether the row would fit chunks of n slots.
   bool fits_at(uint32_t row, uint32_t n) const;

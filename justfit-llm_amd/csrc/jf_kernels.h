@@ -404,5 +404,11 @@ static_assert(sizeof(PenaltyOpBatch) <= 2560, "penalty updates travel as kernel 
 
 int launch_penalty_count(const PenaltyTableView &t, const PenaltyOpBatch &b, uint32_t groups,
                          void *stream);
+// The same updates read from host-mapped memory (calls of more than
+// kPenaltyOps tokens, all in one launch): ops[n], group_row[groups],
+// group_start[groups + 1].
+int launch_penalty_count_mapped(const PenaltyTableView &t, const PackedPenaltyOp *ops,
+                                const uint32_t *group_row, const uint32_t *group_start,
+                                uint32_t groups, void *stream);
 
 }  // namespace jf

@@ -57,16 +57,16 @@ __device__ void insert_at(PenaltyEntry *v, uint32_t n, PenaltyEntry entry, uint3
   } while (hi > 0);
 }
 
-__global__ __launch_bounds__(kThreads) void penalty_count_kernel(PenaltyTableView t,
-                                                                 PenaltyOpBatch b) {
+// One row's updates, in call order (block g: ops [start, end) of row `row`).
+__device__ __forceinline__ void apply_ops(const PenaltyTableView &t, uint32_t row,
+                                          const PackedPenaltyOp *ops, uint32_t k0,
+                                          uint32_t k1) {
   const uint32_t tid = threadIdx.x;
-  const uint32_t row = b.group_row[blockIdx.x];
   PenaltyEntry *e = t.entries + (uint64_t)row * t.max_entries;
   uint32_t *off = t.offsets + (uint64_t)row * (t.buckets + 1);
-  const uint32_t k0 = b.group_start[blockIdx.x], k1 = b.group_start[blockIdx.x + 1];
   for (uint32_t k = k0; k < k1; ++k) {
     if (k != k0) __syncthreads();  // this update reads the previous one's writes
-    const PackedPenaltyOp op = b.op[k];
+    const PackedPenaltyOp op = ops[k];
     const uint32_t index = op.index & 0x7fffffffu;
     const bool insert = (op.index >> 31) != 0;
     const uint32_t slot = op.slot & 0xffffu, used = op.slot >> 16;
@@ -87,12 +87,35 @@ __global__ __launch_bounds__(kThreads) void penalty_count_kernel(PenaltyTableVie
   }
 }
 
+__global__ __launch_bounds__(kThreads) void penalty_count_kernel(PenaltyTableView t,
+                                                                 PenaltyOpBatch b) {
+  apply_ops(t, b.group_row[blockIdx.x], b.op, b.group_start[blockIdx.x],
+            b.group_start[blockIdx.x + 1]);
+}
+
+// The batch in host-mapped memory: each block reads its group's bounds, then
+// each op at its turn, over the bus.
+__global__ __launch_bounds__(kThreads) void penalty_count_mapped_kernel(
+    PenaltyTableView t, const PackedPenaltyOp *ops, const uint32_t *group_row,
+    const uint32_t *group_start) {
+  apply_ops(t, group_row[blockIdx.x], ops, group_start[blockIdx.x],
+            group_start[blockIdx.x + 1]);
+}
+
 }  // namespace
 
 int launch_penalty_count(const PenaltyTableView &t, const PenaltyOpBatch &b, uint32_t groups,
                          void *stream) {
   hipLaunchKernelGGL(penalty_count_kernel, dim3(groups), dim3(kThreads), 0,
                      (hipStream_t)stream, t, b);
+  return (int)hipGetLastError();
+}
+
+int launch_penalty_count_mapped(const PenaltyTableView &t, const PackedPenaltyOp *ops,
+                                const uint32_t *group_row, const uint32_t *group_start,
+                                uint32_t groups, void *stream) {
+  hipLaunchKernelGGL(penalty_count_mapped_kernel, dim3(groups), dim3(kThreads), 0,
+                     (hipStream_t)stream, t, ops, group_row, group_start);
   return (int)hipGetLastError();
 }
 

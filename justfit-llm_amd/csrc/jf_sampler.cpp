@@ -89,6 +89,69 @@ class StagingRing {
   int next_ = 0;
 };
 
+// Host-mapped buffers a kernel reads directly (coherent pinned memory, no
+// copy): a slot is refilled only after the event recorded behind the last
+// launch that read it has completed.
+class MappedRing {
+ public:
+  ~MappedRing() { release(); }
+
+  // A slot of at least `bytes` holding a copy of src; *device receives the
+  // address the kernel reads. record() must follow the launch.
+  int stage(const void *src, size_t bytes, const void **device) {
+    Slot &slot = slots_[next_];
+    if (slot.pending) {
+      JF_HIP(hipEventSynchronize(slot.event), "mapped batch wait");
+      slot.pending = false;
+    }
+    if (slot.capacity < bytes) {
+      if (slot.host) JF_HIP(hipHostFree(slot.host), "mapped batch free");
+      slot.host = nullptr;
+      slot.capacity = 0;
+      size_t cap = 4096;
+      while (cap < bytes) cap <<= 1;
+      JF_HIP(hipHostMalloc(&slot.host, cap, hipHostMallocCoherent | hipHostMallocMapped),
+             "mapped batch alloc");
+      slot.capacity = cap;
+      JF_HIP(hipHostGetDevicePointer(&slot.device, slot.host, 0), "mapped batch address");
+    }
+    if (!slot.event)
+      JF_HIP(hipEventCreateWithFlags(&slot.event, hipEventDisableTiming), "mapped batch event");
+    std::memcpy(slot.host, src, bytes);
+    *device = slot.device;
+    return JF_OK;
+  }
+
+  int record(hipStream_t stream) {
+    Slot &slot = slots_[next_];
+    next_ = (next_ + 1) % kSlots;
+    JF_HIP(hipEventRecord(slot.event, stream), "mapped batch record");
+    slot.pending = true;
+    return JF_OK;
+  }
+
+  void release() {
+    for (Slot &slot : slots_) {
+      if (slot.pending && slot.event) (void)hipEventSynchronize(slot.event);
+      if (slot.event) (void)hipEventDestroy(slot.event);
+      if (slot.host) (void)hipHostFree(slot.host);
+      slot = Slot{};
+    }
+  }
+
+ private:
+  static constexpr int kSlots = 4;
+  struct Slot {
+    void *host = nullptr;
+    void *device = nullptr;
+    size_t capacity = 0;
+    hipEvent_t event = nullptr;
+    bool pending = false;
+  };
+  Slot slots_[kSlots];
+  int next_ = 0;
+};
+
 template <class T>
 int device_alloc(T **p, size_t count, const char *what) {
   *p = nullptr;
@@ -131,6 +194,7 @@ struct jf_penalty_table {
   uint32_t *slots = nullptr;
   jf::PenaltyRows host;  // the rows as the device holds them
   StagingRing staging;
+  MappedRing mapped;  // counts of more than kPenaltyOps tokens a call
 };
 
 struct jf_sampler {
@@ -245,6 +309,7 @@ static int check_device(int device) {
 int jf_penalty_table_destroy(jf_penalty_table *t) {
   if (!t) return JF_OK;
   t->staging.release();
+  t->mapped.release();
   (void)hipFree(t->entries);
   (void)hipFree(t->offsets);
   (void)hipFree(t->slots);
@@ -356,34 +421,77 @@ int jf_penalty_table_rebuild(jf_penalty_table *t, uint32_t row,
   return rc == JF_OK ? widen_slots(t, stream) : rc;
 }
 
+// The update of one (row, token) pair as penalty_count_kernel reads it.
+static int count_op(jf_penalty_table *t, uint32_t row, uint32_t token,
+                    jf::PackedPenaltyOp *p) {
+  jf::PenaltyOp op;
+  const int rc = t->host.count(row, token, &op);
+  if (rc != JF_OK) return rc;
+  p->token = op.token;
+  p->word = op.word;
+  p->index = op.index | (op.insert ? 0x80000000u : 0u);
+  p->entries = op.entries;
+  p->slot_value = op.slot_value;
+  p->slot = op.slot == jf::kNoSlot ? 0xffffu : (op.slot | op.slot_used << 16);
+  return JF_OK;
+}
+
+// More tokens than one kernel-argument batch holds: every update in one
+// launch that reads them from host-mapped memory (ops, group rows, group
+// starts), so a step's commits of many lanes cost one kernel.
+static int count_mapped(jf_penalty_table *t, const jf::PenaltyTableView &view,
+                        const uint32_t *rows, uint32_t one_row, const uint32_t *selected,
+                        const std::vector<uint64_t> &order, void *stream) {
+  const uint64_t n = order.size();
+  std::vector<uint32_t> group_row, group_start;
+  std::vector<jf::PackedPenaltyOp> ops(n);
+  for (uint64_t i = 0; i < n; ++i) {
+    const uint64_t k = order[i];
+    const uint32_t row = rows ? rows[k] : one_row;
+    if (group_row.empty() || group_row.back() != row) {
+      group_row.push_back(row);
+      group_start.push_back((uint32_t)i);
+    }
+    const int rc = count_op(t, row, selected[k], &ops[i]);
+    if (rc != JF_OK) return rc;  // excluded by the caller's checks
+  }
+  group_start.push_back((uint32_t)n);
+  const size_t ob = n * sizeof(jf::PackedPenaltyOp), rb = group_row.size() * sizeof(uint32_t),
+               sb = group_start.size() * sizeof(uint32_t);
+  std::vector<uint8_t> blob(ob + rb + sb);
+  std::memcpy(blob.data(), ops.data(), ob);
+  std::memcpy(blob.data() + ob, group_row.data(), rb);
+  std::memcpy(blob.data() + ob + rb, group_start.data(), sb);
+  const void *dev = nullptr;
+  int rc = t->mapped.stage(blob.data(), blob.size(), &dev);
+  if (rc != JF_OK) return rc;
+  const uint8_t *d = (const uint8_t *)dev;
+  const int e = jf::launch_penalty_count_mapped(
+      view, (const jf::PackedPenaltyOp *)d, (const uint32_t *)(d + ob),
+      (const uint32_t *)(d + ob + rb), (uint32_t)group_row.size(), stream);
+  if (e != hipSuccess) return hip_fail((hipError_t)e, "penalty count launch");
+  rc = t->mapped.record((hipStream_t)stream);
+  return rc == JF_OK ? widen_slots(t, stream) : rc;
+}
+
 // countPenaltyTokens (Sampling.cpp:75-80) of n (row, token) pairs, applied
 // in order. Everything is checked before any row changes: rows, tokens, and
 // that each row's new distinct tokens fit its max_entries. The host copy
 // then describes each token's update, and penalty_count_kernel applies them
-// on `stream`, up to kPenaltyOps tokens a launch (passed as kernel
-// arguments: no staging copy, no wait on earlier work).
+// on `stream` in one launch: as kernel arguments (up to kPenaltyOps tokens,
+// no copy and no wait on earlier work) or from host-mapped memory.
 static int count_pairs(jf_penalty_table *t, const uint32_t *rows, uint32_t one_row,
                        const uint32_t *selected, uint64_t n, void *stream) {
   if (!selected && n) return fail(JF_ERR_INVALID_ARGUMENT, "null buffer");
   int rc = check_device(t->device);
   if (rc != JF_OK) return rc;
-  std::vector<std::pair<uint32_t, uint32_t>> fresh;  // (row, token) not yet held
   for (uint64_t i = 0; i < n; ++i) {
     const uint32_t row = rows ? rows[i] : one_row;
     if (row >= t->rows)
       return fail(JF_ERR_INVALID_ARGUMENT, "penalized lane has no penalty table row");
     if (selected[i] >= t->vocabulary)
       return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
-    if (!t->host.holds(row, selected[i])) fresh.emplace_back(row, selected[i]);
-  }
-  std::sort(fresh.begin(), fresh.end());
-  fresh.erase(std::unique(fresh.begin(), fresh.end()), fresh.end());
-  for (size_t i = 0; i < fresh.size();) {
-    size_t j = i;
-    while (j < fresh.size() && fresh[j].first == fresh[i].first) ++j;
-    if (t->host.size(fresh[i].first) + (j - i) > t->max_entries)
-      return fail(JF_ERR_INVALID_ARGUMENT, "penalty history exceeds the table row");
-    i = j;
+    t->host.prefetch(row, selected[i]);
   }
   // Updates grouped by row, call order kept inside each row.
   std::vector<uint64_t> order(n);
@@ -391,6 +499,25 @@ static int count_pairs(jf_penalty_table *t, const uint32_t *rows, uint32_t one_r
   if (rows)
     std::stable_sort(order.begin(), order.end(),
                      [&](uint64_t x, uint64_t y) { return rows[x] < rows[y]; });
+  // Each row's new distinct tokens must fit its max_entries. A row whose
+  // size plus its token count fits cannot overflow; only the others look
+  // their tokens up.
+  std::vector<uint32_t> fresh;
+  for (uint64_t i = 0; i < n;) {
+    const uint32_t row = rows ? rows[order[i]] : one_row;
+    uint64_t j = i;
+    while (j < n && (rows ? rows[order[j]] : one_row) == row) ++j;
+    if (t->host.size(row) + (j - i) > t->max_entries) {
+      fresh.clear();
+      for (uint64_t k = i; k < j; ++k)
+        if (!t->host.holds(row, selected[order[k]])) fresh.push_back(selected[order[k]]);
+      std::sort(fresh.begin(), fresh.end());
+      const size_t distinct = std::unique(fresh.begin(), fresh.end()) - fresh.begin();
+      if (t->host.size(row) + distinct > t->max_entries)
+        return fail(JF_ERR_INVALID_ARGUMENT, "penalty history exceeds the table row");
+    }
+    i = j;
+  }
   const jf::PenaltyTableView view{(jf::PenaltyEntry *)t->entries, t->offsets, t->slots,
                                   t->max_entries, t->buckets, t->chunks, t->slot_count};
   jf::PenaltyOpBatch b;
@@ -402,6 +529,7 @@ static int count_pairs(jf_penalty_table *t, const uint32_t *rows, uint32_t one_r
     ops = groups = 0;
     return e == hipSuccess ? JF_OK : hip_fail((hipError_t)e, "penalty count launch");
   };
+  if (n > jf::kPenaltyOps) return count_mapped(t, view, rows, one_row, selected, order, stream);
   for (uint64_t i = 0; i < n; ++i) {
     const uint64_t k = order[i];
     const uint32_t row = rows ? rows[k] : one_row;
@@ -413,16 +541,8 @@ static int count_pairs(jf_penalty_table *t, const uint32_t *rows, uint32_t one_r
       b.group_row[groups] = row;
       b.group_start[groups++] = ops;
     }
-    jf::PenaltyOp op;
-    rc = t->host.count(row, selected[k], &op);
+    rc = count_op(t, row, selected[k], &b.op[ops++]);
     if (rc != JF_OK) return rc;  // excluded by the checks above
-    jf::PackedPenaltyOp &p = b.op[ops++];
-    p.token = op.token;
-    p.word = op.word;
-    p.index = op.index | (op.insert ? 0x80000000u : 0u);
-    p.entries = op.entries;
-    p.slot_value = op.slot_value;
-    p.slot = op.slot == jf::kNoSlot ? 0xffffu : (op.slot | op.slot_used << 16);
   }
   rc = flush();
   return rc == JF_OK ? widen_slots(t, stream) : rc;

@@ -60,7 +60,7 @@ def test_counts_update_the_table_in_place(general):
         rc, words[r] = O.rebuild_penalty_words(V, histories[r], generated[r], None, r % 2 == 0)
         assert rc == 0
     # Tokens already held, new ones, repeats, and one row many times: 150
-    # pairs (five launches of at most 32).
+    # pairs (one launch reading host-mapped updates).
     pr, pt = [], []
     for k in range(150):
         r = int(rng.integers(0, rows)) if k % 5 else 2
