@@ -164,6 +164,38 @@ def test_slots_widen_for_a_clustered_row():
     table.close()
 
 
+def test_one_row_counted_past_one_argument_batch():
+    """jf_penalty_table_count of 200 tokens on one row (more than one
+    kernel-argument batch of 64: one launch reading host-mapped updates,
+    one block applying them in order), repeated and new ids mixed, then a
+    second such call on the same table while the first's buffer may still
+    be in use; penalized selections bit-exact against the oracle."""
+    rows = 2
+    rng = np.random.default_rng(29)
+    table = J.PenaltyTable(V, rows, 4096)
+    words = np.zeros((rows, V), np.uint32)
+    hist = [rng.integers(0, V, 700, dtype=np.uint32), rng.integers(0, V, 300, dtype=np.uint32)]
+    for r in range(rows):
+        table.rebuild(r, hist[r], 50, None, r == 0)
+        words[r] = O.rebuild_penalty_words(V, hist[r], 50, None, r == 0)[1]
+    for call in range(2):
+        r = call % rows
+        toks = np.concatenate([hist[r][:60], rng.integers(0, V, 100, dtype=np.uint32),
+                               np.full(40, 8192 * 5 + 3, np.uint32)])
+        rng.shuffle(toks)
+        table.count(r, toks)
+        for t in toks:
+            words[r, t] += 1
+    pols = [J.policy(temperature=0.9, top_k=40, presence=0.8, frequency=0.6, repetition=1.3),
+            J.policy(repetition=1.5, presence=0.4)]
+    lg = _logits(rows, 31)
+    lg[:, hist[0][:60]] += 5.0
+    uniforms = rng.random(rows, dtype=np.float32)
+    got, want = _select(table, words, lg, pols, uniforms)
+    np.testing.assert_array_equal(got, want)
+    table.close()
+
+
 def test_count_errors_leave_the_row_unchanged():
     table = J.PenaltyTable(1000, 2, 8)
     table.rebuild(0, [1, 2, 3], 1, None, True)
