@@ -167,9 +167,10 @@ def test_slots_widen_for_a_clustered_row():
 def test_one_row_counted_past_one_argument_batch():
     """jf_penalty_table_count of 200 tokens on one row (more than one
     kernel-argument batch of 64: one launch reading host-mapped updates,
-    one block applying them in order), repeated and new ids mixed, then a
-    second such call on the same table while the first's buffer may still
-    be in use; penalized selections bit-exact against the oracle."""
+    one block applying them in order), repeated and new ids mixed, six such
+    calls back to back on one table (more calls than the table's four
+    mapped buffers, so later calls reuse buffers earlier launches read);
+    penalized selections bit-exact against the oracle."""
     rows = 2
     rng = np.random.default_rng(29)
     table = J.PenaltyTable(V, rows, 4096)
@@ -178,7 +179,7 @@ def test_one_row_counted_past_one_argument_batch():
     for r in range(rows):
         table.rebuild(r, hist[r], 50, None, r == 0)
         words[r] = O.rebuild_penalty_words(V, hist[r], 50, None, r == 0)[1]
-    for call in range(2):
+    for call in range(6):
         r = call % rows
         toks = np.concatenate([hist[r][:60], rng.integers(0, V, 100, dtype=np.uint32),
                                np.full(40, 8192 * 5 + 3, np.uint32)])
