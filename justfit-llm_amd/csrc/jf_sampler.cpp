@@ -96,9 +96,11 @@ class MappedRing {
  public:
   ~MappedRing() { release(); }
 
-  // A slot of at least `bytes` holding a copy of src; *device receives the
-  // address the kernel reads. record() must follow the launch.
-  int stage(const void *src, size_t bytes, const void **device) {
+  // A slot of at least `bytes` for the caller to fill at *host; *device
+  // receives the address the kernel reads. Waits for the slot's last reader
+  // and allocates before returning, so a failure leaves nothing changed.
+  // record() must follow the launch.
+  int acquire(size_t bytes, void **host, const void **device) {
     Slot &slot = slots_[next_];
     if (slot.pending) {
       JF_HIP(hipEventSynchronize(slot.event), "mapped batch wait");
@@ -117,7 +119,7 @@ class MappedRing {
     }
     if (!slot.event)
       JF_HIP(hipEventCreateWithFlags(&slot.event, hipEventDisableTiming), "mapped batch event");
-    std::memcpy(slot.host, src, bytes);
+    *host = slot.host;
     *device = slot.device;
     return JF_OK;
   }
@@ -444,27 +446,31 @@ static int count_mapped(jf_penalty_table *t, const jf::PenaltyTableView &view,
                         const std::vector<uint64_t> &order, void *stream) {
   const uint64_t n = order.size();
   std::vector<uint32_t> group_row, group_start;
-  std::vector<jf::PackedPenaltyOp> ops(n);
   for (uint64_t i = 0; i < n; ++i) {
-    const uint64_t k = order[i];
-    const uint32_t row = rows ? rows[k] : one_row;
+    const uint32_t row = rows ? rows[order[i]] : one_row;
     if (group_row.empty() || group_row.back() != row) {
       group_row.push_back(row);
       group_start.push_back((uint32_t)i);
     }
-    const int rc = count_op(t, row, selected[k], &ops[i]);
-    if (rc != JF_OK) return rc;  // excluded by the caller's checks
   }
   group_start.push_back((uint32_t)n);
   const size_t ob = n * sizeof(jf::PackedPenaltyOp), rb = group_row.size() * sizeof(uint32_t),
                sb = group_start.size() * sizeof(uint32_t);
-  std::vector<uint8_t> blob(ob + rb + sb);
-  std::memcpy(blob.data(), ops.data(), ob);
-  std::memcpy(blob.data() + ob, group_row.data(), rb);
-  std::memcpy(blob.data() + ob + rb, group_start.data(), sb);
+  // The buffer first (its wait or allocation may fail): the host copy
+  // changes only once the updates have somewhere to go.
+  void *host = nullptr;
   const void *dev = nullptr;
-  int rc = t->mapped.stage(blob.data(), blob.size(), &dev);
+  int rc = t->mapped.acquire(ob + rb + sb, &host, &dev);
   if (rc != JF_OK) return rc;
+  uint8_t *h = (uint8_t *)host;
+  jf::PackedPenaltyOp *ops = (jf::PackedPenaltyOp *)h;
+  for (uint64_t i = 0; i < n; ++i) {
+    const uint64_t k = order[i];
+    rc = count_op(t, rows ? rows[k] : one_row, selected[k], &ops[i]);
+    if (rc != JF_OK) return rc;  // excluded by the caller's checks
+  }
+  std::memcpy(h + ob, group_row.data(), rb);
+  std::memcpy(h + ob + rb, group_start.data(), sb);
   const uint8_t *d = (const uint8_t *)dev;
   const int e = jf::launch_penalty_count_mapped(
       view, (const jf::PackedPenaltyOp *)d, (const uint32_t *)(d + ob),
