@@ -113,11 +113,13 @@ __global__ __launch_bounds__(kThreads) void draft_top16_kernel(DraftLaunch d) {
     s.top[tid] = 0;
     s.topv[tid] = f2u(-__builtin_inff());
   }
-  // The lane's largest key among its non-NaN tokens (0: none).
-  uint32_t mkey = 0;
+  // The lane's largest key among its non-NaN tokens (0: none): fmax skips
+  // NaN operands, so the float maximum is NaN only when every token is, and
+  // the key order is the float order (the two zeros share a key).
+  float mx = x[0];
 #pragma unroll
-  for (int i = 0; i < kDraftTokens; ++i)
-    if (x[i] == x[i]) mkey = max(mkey, logit_key(x[i]));
+  for (int i = 1; i < kDraftTokens; ++i) mx = __builtin_fmaxf(mx, x[i]);
+  const uint32_t mkey = mx == mx ? logit_key(mx) : 0u;
   const uint32_t sorted = wave_sort_asc_u32(mkey);
   if (lane >= 64 - kDraftK) s.wtop[w * kDraftK + lane - (64 - kDraftK)] = sorted;
   __syncthreads();
@@ -125,10 +127,12 @@ __global__ __launch_bounds__(kThreads) void draft_top16_kernel(DraftLaunch d) {
 
   // Compact the tokens at or above the bound: per-thread counts, a block
   // prefix sum, then each thread writes its own.
+  // key(x) >= bound as a float compare: the bound is 0 (every non-NaN token)
+  // or the key of a real value (-inf or above), and NaN fails every compare.
+  const float bv = bound ? key_logit(bound) : -__builtin_inff();
   uint32_t hits = 0;
 #pragma unroll
-  for (int i = 0; i < kDraftTokens; ++i)
-    hits |= (x[i] == x[i] && logit_key(x[i]) >= bound ? 1u : 0u) << i;
+  for (int i = 0; i < kDraftTokens; ++i) hits |= (x[i] >= bv ? 1u : 0u) << i;
   const uint32_t cnt = (uint32_t)__popc(hits);
   const uint32_t incl = wave_incl_scan_u32(cnt);
   if (lane == 63) s.wcount[w] = incl;
