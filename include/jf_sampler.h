@@ -124,7 +124,9 @@ int jf_penalty_table_rebuild(jf_penalty_table *table, uint32_t row,
  * such buffers a table, each reused once the launch that read it has
  * completed: the only wait on earlier work). Nothing of the row is
  * uploaded. Calls on one table must be ordered (one stream, or streams
- * ordered by the caller). (Once in a table's life, when a row first needs more
+ * ordered by the caller). Only calls of up to 64 tokens may be captured
+ * into a HIP graph: a longer call's kernel reads its updates at run time
+ * from a buffer that later calls reuse. (Once in a table's life, when a row first needs more
  * than 256 of a chunk's fixed slots and 512 suffice, a rebuild or count
  * widens them to 512 and uploads every row's slots.) All-or-nothing: a
  * token outside the vocabulary, or new tokens beyond the row's
