@@ -164,8 +164,10 @@ struct FastLaunch {
   const uint32_t *pen_slots;  // [table rows][chunks][slot_count]
   uint32_t slot_count;        // 256 or 512
   uint32_t row_base;          // sampler row of blockIdx.y == 0
-  uint32_t fuse_greedy;       // every row greedy: the last block of a row
-                              // finishes it (no merge launch)
+  uint32_t fuse_greedy;       // every row greedy, no merge launch: 1, the
+                              // row's last block to arrive finishes it; 2
+                              // (set at launch when the grid fits the GPU
+                              // at once), the row's last chunk finishes it
   uint32_t mapped;            // blockIdx.y selects row row_of[blockIdx.y]
                               // (a launch split between the two kernels;
                               // the kernel takes it as a preloaded argument)

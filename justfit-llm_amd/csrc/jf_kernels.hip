@@ -2392,22 +2392,51 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
       }
       return;
     }
+    // Each block's best as one 64-bit word: the value's order key in bits
+    // 63..32, 0x7FFFF - id in 31..13 (ids stay below 2^19, so the larger
+    // word holds the larger value, then the lower id), and bit 0 set, so
+    // that a written word is never zero (the word 1: nothing admitted,
+    // below every admitted key).
+    const uint64_t mine =
+        bi == kNoToken ? 1ull
+                       : ((uint64_t)logit_key(bv) << 32) | ((uint64_t)(0x7ffffu - bi) << 13) | 1ull;
+    if (f.fuse_greedy == 2u) {
+      // The row's last chunk finishes it: every other block stores its word
+      // and ends; this one reads the row's words, waiting word by word for
+      // any not yet visible, and returns them to zero. The launch sets this
+      // mode only when every block of the grid can be resident at once, and
+      // the other blocks never wait, so each word it waits for is stored.
+      // The bound only caps the loop.
+      if (chunk + 1 < S) {
+        if (tid == 0) st_dev(a.bests + (uint64_t)row * S + chunk, mine);
+        return;
+      }
+      if (w == 0) {
+        constexpr uint32_t kBestWaitBound = 1u << 20;
+        uint64_t best = 0;
+        if (lane == chunk) {
+          best = mine;
+        } else if (lane < S) {  // S <= kMaxChunks = 64
+          uint64_t *word = a.bests + (uint64_t)row * S + lane;
+          best = ld_dev(word);
+          for (uint32_t n = 0; best == 0 && n < kBestWaitBound; ++n) best = ld_dev(word);
+          st_dev(word, 0ull);
+        }
+        const uint32_t key = wave_max_u32((uint32_t)(best >> 32));
+        const uint32_t low = wave_max_u32((uint32_t)(best >> 32) == key ? (uint32_t)best : 0u);
+        if (lane == 0)
+          write_result(a, row, key ? 0x7ffffu - (low >> 13) : kNoToken, 0.0f, 0);
+      }
+      return;
+    }
     // Every row greedy: the row's last block to arrive takes the largest
     // chunk best, the lowest id among equals (the reference's last-arriving
-    // group, split_reduce.h:14-45). Each block's best is one 64-bit word:
-    // the value's order key in bits 63..32, 0x7FFFF - id in 31..13 (ids
-    // stay below 2^19, so the larger word holds the larger value, then the
-    // lower id), and bit 0 set, so that a written word is never zero (the
-    // word 1: nothing admitted, below every admitted key). The word's store
-    // and the arrival go out together; the last block reads the row's words
-    // and waits, word by word, for any not yet visible. Each such store was
-    // issued before its block's arrival, so every wait ends; the bound only
-    // caps the loop. The last block returns the words and the counter to
-    // zero.
+    // group, split_reduce.h:14-45). The word's store and the arrival go out
+    // together; the last block reads the row's words and waits, word by
+    // word, for any not yet visible. Each such store was issued before its
+    // block's arrival, so every wait ends; the bound only caps the loop.
+    // The last block returns the words and the counter to zero.
     if (tid == 0) {
-      const uint64_t mine =
-          bi == kNoToken ? 1ull
-                         : ((uint64_t)logit_key(bv) << 32) | ((uint64_t)(0x7ffffu - bi) << 13) | 1ull;
       st_dev(a.bests + (uint64_t)row * S + chunk, mine);
       const uint32_t prev = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT);
@@ -4095,9 +4124,41 @@ int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
 #endif
 
 #if JF_IN(1)
+// Blocks of select_fast_kernel<dtype> the current device holds at once
+// (0 when the query fails), cached per device.
+static uint32_t fast_resident_blocks(uint32_t dtype) {
+  constexpr int kDevices = 64;
+  static uint32_t cache[kDevices][2];
+  static bool known[kDevices][2];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevices) return 0;
+  if (!known[dev][dtype]) {
+    int per_cu = 0, cus = 0;
+    const hipError_t e1 =
+        dtype == 0 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, select_fast_kernel<0>,
+                                                                  kThreads, 0)
+                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, select_fast_kernel<1>,
+                                                                  kThreads, 0);
+    const hipError_t e2 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    cache[dev][dtype] = e1 == hipSuccess && e2 == hipSuccess && per_cu > 0 && cus > 0
+                            ? (uint32_t)per_cu * (uint32_t)cus
+                            : 0u;
+    known[dev][dtype] = true;
+  }
+  return cache[dev][dtype];
+}
+
 int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
                        const RowParams *uniform, void *stream, void *start_event,
                        void *stop_event) {
+  if (f.fuse_greedy == 1u && f.a.chunks > 1 &&
+      (uint64_t)f.a.chunks * rows <= fast_resident_blocks(dtype)) {
+    // The whole grid fits the device at once: each row's last chunk can
+    // wait for the row's other blocks instead of counting arrivals.
+    FastLaunch g = f;
+    g.fuse_greedy = 2u;
+    return launch_select_fast(g, rows, dtype, uniform, stream, start_event, stop_event);
+  }
   const dim3 grid(f.a.chunks, rows), block(kThreads);
   const hipStream_t st = (hipStream_t)stream;
   const hipEvent_t e0 = (hipEvent_t)start_event, e1 = (hipEvent_t)stop_event;
