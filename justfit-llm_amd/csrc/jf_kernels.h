@@ -166,8 +166,9 @@ struct FastLaunch {
   uint32_t row_base;          // sampler row of blockIdx.y == 0
   uint32_t fuse_greedy;       // every row greedy, no merge launch: 1, the
                               // row's last block to arrive finishes it; 2
-                              // (set at launch when the grid fits the GPU
-                              // at once), the row's last chunk finishes it
+                              // (set at launch when its rows are fewer than
+                              // the blocks the GPU holds at once), the
+                              // row's last chunk finishes it
   uint32_t mapped;            // blockIdx.y selects row row_of[blockIdx.y]
                               // (a launch split between the two kernels;
                               // the kernel takes it as a preloaded argument)

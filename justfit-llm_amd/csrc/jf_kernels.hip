@@ -2404,9 +2404,9 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
       // The row's last chunk finishes it: every other block stores its word
       // and ends; this one reads the row's words, waiting word by word for
       // any not yet visible, and returns them to zero. The launch sets this
-      // mode only when every block of the grid can be resident at once, and
-      // the other blocks never wait, so each word it waits for is stored.
-      // The bound only caps the loop.
+      // mode only when its rows (one finisher each) are fewer than the
+      // blocks the device holds at once, and the other blocks never wait,
+      // so each word it waits for is stored. The bound only caps the loop.
       if (chunk + 1 < S) {
         if (tid == 0) st_dev(a.bests + (uint64_t)row * S + chunk, mine);
         return;
@@ -4151,10 +4151,11 @@ static uint32_t fast_resident_blocks(uint32_t dtype) {
 int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
                        const RowParams *uniform, void *stream, void *start_event,
                        void *stop_event) {
-  if (f.fuse_greedy == 1u && f.a.chunks > 1 &&
-      (uint64_t)f.a.chunks * rows <= fast_resident_blocks(dtype)) {
-    // The whole grid fits the device at once: each row's last chunk can
-    // wait for the row's other blocks instead of counting arrivals.
+  if (f.fuse_greedy == 1u && f.a.chunks > 1 && rows < fast_resident_blocks(dtype)) {
+    // Each row's last chunk can wait for the row's other blocks instead of
+    // counting arrivals: only those finishers (one a row) ever wait, and
+    // they are fewer than the blocks the device holds at once, so some
+    // slot always remains for the blocks they wait for, which never wait.
     FastLaunch g = f;
     g.fuse_greedy = 2u;
     return launch_select_fast(g, rows, dtype, uniform, stream, start_event, stop_event);
