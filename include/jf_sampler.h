@@ -234,6 +234,14 @@ typedef struct jf_sample_args {
   const uint64_t *extra_offsets;
 } jf_sample_args;
 
+/* Selection of every row of `args` on `stream`, asynchronous. In an
+ * all-greedy call each row's last chunk block waits for the row's other
+ * blocks; one call's waiting blocks (at most 256) are always fewer than the
+ * device's block slots, so the waits end. Greedy calls running at the same
+ * time from several streams on one GPU should together stay below those
+ * slots (1,536 on MI355X): beyond that a waiting block can hold a slot the
+ * rows it waits for need, and after its bounded wait (about a second) its
+ * token would be wrong. One stream per GPU never meets this. */
 int jf_sample(jf_sampler *sampler, const jf_sample_args *args, void *stream);
 
 /* jf_sample without a sampler object and without any allocation. It has no
