@@ -456,12 +456,33 @@ def test_dense_residual_in_the_partial_last_chunk(bf16):
     assert g["tokens"][rows - 1] >= V - 4480  # inside the partial last chunk
 
 
+def test_greedy_rows_across_two_launches():
+    """300 greedy rows: two launches of the fast kernel (256 rows, then 44),
+    each row finished by its last chunk block waiting for the row's other
+    blocks; maxima tied across chunks in some rows (lowest id wins). Three
+    calls on one sampler (the words return to zero between them); tokens
+    equal the oracle's."""
+    from harness import run_gpu, run_oracle
+    V = 151936
+    rows = 300
+    rng = np.random.default_rng(77)
+    x = rng.normal(0, 2.0, (rows, V)).astype(np.float32)
+    for r in range(0, rows, 7):
+        x[r, [r % 8192, V // 2 + r, V - 1 - r]] = 40.0
+    pols = [J.policy(repetition=1.0)] * rows
+    s = J.Sampler(V, rows)
+    g = run_gpu(V, pols, sampler=s, repeat=3, logits=x)
+    o = run_oracle(V, pols, logits=x)
+    np.testing.assert_array_equal(g["tokens"], o["tokens"])
+    assert np.all(g["tokens"][::7] == np.array([r % 8192 for r in range(0, rows, 7)], np.uint32))
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("V", [5000, 3 * 8192 + 17, 151936])
 def test_all_greedy_launch_edges(bf16, V):
     """Launches whose rows are all greedy finish inside the selection: each
-    chunk's best is packed into one word and the row's last block takes the
-    largest (sampling.metal:1427-1512). Ties of the maximum across chunks
+    chunk's best is packed into one word and the row's finishing block (its
+    last chunk's) takes the largest (sampling.metal:1427-1512). Ties of the maximum across chunks
     (lowest id), -0 against +0, +inf, all-NaN, all -inf (admitted: it wins
     over nothing), a mask that admits nothing and one that admits only the
     partial last chunk; then calls on the same sampler with fewer rows,
