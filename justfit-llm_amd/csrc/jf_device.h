@@ -98,14 +98,15 @@ __device__ __forceinline__ uint64_t quantized_weight(float value, float maximum,
   return ((uint64_t)Y << 32) >> k;
 }
 
-// scale_down(quantized_weight(value, maximum, inv_t), r) for r <= 2^32 in
-// one 32 x 32-bit product: the weight is (Y << 32) >> k (Y < 2^31, k in
-// [18, 63]), so for k <= 32 it is Y * 2^(32 - k) and the scaled weight is
-// (Y * r) >> k; for k > 32 the weight is Y >> (k - 32) and the scaled
-// weight that times r, >> 32. Checked equal to the composition over 2e6
-// random (Y, k, r) with the edge values of r.
+// scale_by(quantized_weight(value, maximum, inv_t), scale) in one 32 x 32-bit
+// product, for a packed chunk scale s << 32 | R (R < 2^32, s >= 31, or R = 0
+// with s = 64): the weight is (Y << 32) >> k (Y < 2^31, k in [18, 63]), so for
+// k <= 32 it is Y * 2^(32 - k) and the scaled weight is (Y * R) >> (s + k - 32);
+// for k > 32 the weight is m = Y >> (k - 32) and the scaled weight
+// (m * R) >> s. Both products stay below 2^63, so a shift clamped to 63 gives
+// the zero that any larger shift would.
 __device__ __forceinline__ uint64_t scaled_weight(float value, float maximum, float inv_t,
-                                                  uint64_t r) {
+                                                  uint64_t scale) {
   const float x_in = (value - maximum) * inv_t;
   const float x = __builtin_fminf(__builtin_fmaxf(x_in, -87.0f), 88.0f);
   const float n = __builtin_rintf(x * 1.44269504088896341f);
@@ -122,35 +123,99 @@ __device__ __forceinline__ uint64_t scaled_weight(float value, float maximum, fl
   const uint32_t Y = (uint32_t)(y * 0x1p30f);
   const int k = x_in >= -86.0f ? min(18 - (int)n, 63) : 63;
   const uint32_t m = Y >> max(k - 32, 0);
-  const int sh = min(k, 32);
-  return ((uint64_t)m * r) >> sh;  // m * r < 2^63
+  const int sh = min((int)(scale >> 32) - 32 + min(k, 32), 63);
+  return ((uint64_t)m * (uint32_t)scale) >> sh;
 }
 
-// A chunk mass's rescale from the chunk's maximum to the row's:
-// floor(exp((chunk_max - row_max) / T) * 2^32), in [0, 2^32] (exp_weight's
-// result times 2^32 is exact; the conversion truncates).
+// e^x in double: the Cody-Waite reduction x = n ln2 + r (n = rint(x log2 e),
+// ln2 split into a 28-bit head, so n * head is exact, and the rounded rest),
+// then e^r by its Taylor series to degree 13 in Horner form with fused
+// multiply-adds, times 2^n. Each step is one IEEE double operation, so a host
+// restatement of the same steps gives the same bits. Zero below -708 (where
+// 2^n would leave the normal range) and for NaN.
+__device__ __forceinline__ double exp64(double x) {
+  if (!(x >= -708.0)) return 0.0;
+  if (x > 709.0) return __builtin_inf();
+  const double n = __builtin_rint(x * 0x1.71547652b82fep+0);
+  double r = __builtin_fma(n, -0x1.62e42ffp-1, x);
+  r = __builtin_fma(n, 0x1.718432a1b0e26p-35, r);
+  double p = 0x1.6124613a86d09p-33;  // 1/13!
+  p = __builtin_fma(p, r, 0x1.1eed8eff8d898p-29);
+  p = __builtin_fma(p, r, 0x1.ae64567f544e4p-26);
+  p = __builtin_fma(p, r, 0x1.27e4fb7789f5cp-22);
+  p = __builtin_fma(p, r, 0x1.71de3a556c734p-19);
+  p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-16);
+  p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-13);
+  p = __builtin_fma(p, r, 0x1.6c16c16c16c17p-10);
+  p = __builtin_fma(p, r, 0x1.1111111111111p-7);
+  p = __builtin_fma(p, r, 0x1.5555555555555p-5);
+  p = __builtin_fma(p, r, 0x1.5555555555555p-3);
+  p = __builtin_fma(p, r, 0x1p-1);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  return p * __longlong_as_double((long long)((int64_t)n + 1023) << 52);
+}
+
+// A chunk mass's rescale from the chunk's maximum to the row's,
+// r = exp64((chunk_max - row_max) * inv_t) (difference and product in double),
+// as R * 2^-s with R the significand rounded half up to 32 bits: R in
+// [2^31, 2^32), relative error at most 2^-32 at any offset. Packed s << 32 | R;
+// r = 0 gives R = 0, s = 64.
 __device__ __forceinline__ uint64_t chunk_scale(float chunk_max, float row_max, float inv_t) {
-  return (uint64_t)(exp_weight((chunk_max - row_max) * inv_t) * 0x1p32f);
+  const double r = exp64(((double)chunk_max - (double)row_max) * (double)inv_t);
+  if (!(r > 0.0)) return 64ull << 32;
+  const uint64_t bits = (uint64_t)__double_as_longlong(r);
+  const int e = (int)(bits >> 52) - 1023;  // r normal: e in [-1022, 0]
+  uint64_t R = (((bits & 0xfffffffffffffull) | (1ull << 52)) + (1ull << 20)) >> 21;
+  uint64_t s = (uint64_t)(31 - e);
+  if (R >> 32) {
+    R >>= 1;
+    s -= 1;
+  }
+  return s << 32 | R;
 }
-// floor(x * r / 2^32) for x < 2^63 and r <= 2^32: bits 32..95 of the product.
-__device__ __forceinline__ uint64_t scale_down(uint64_t x, uint64_t r) {
-  return (__umul64hi(x, r) << 32) | ((x * r) >> 32);
+// The packed scale of nothing (R = 0).
+constexpr uint64_t kZeroScale = 64ull << 32;
+// floor(x * R * 2^-s) for x < 2^63 and a packed scale: the 96-bit product
+// shifted right by s (s >= 31; at or past 128 nothing remains).
+__device__ __forceinline__ uint64_t scale_by(uint64_t x, uint64_t scale) {
+  const uint64_t R = scale & 0xffffffffull;
+  const uint32_t s = (uint32_t)(scale >> 32);
+  const uint64_t lo = x * R, hi = __umul64hi(x, R);
+  if (s >= 128) return 0;
+  if (s >= 64) return hi >> (s - 64);
+  return (hi << (64 - s)) | (lo >> s);
 }
-// The largest P with scale_down(P, r) <= within, for r in [1, 2^32] and a
-// result below 2^63: ceil((within + 1) * 2^32 / r) - 1, by long division of
-// the 96-bit numerator in 32-bit digits (each partial dividend stays below
-// r * 2^32 <= 2^64).
-__device__ __forceinline__ uint64_t unscaled_bound(uint64_t within, uint64_t r) {
-  if (r >= (1ull << 32)) return within;
+// The largest P with scale_by(P, scale) <= within, for R > 0 and a within
+// below scale_by(x, scale) for some x < 2^63 (the chunk the draw chose):
+// floor(((within + 1) * 2^s - 1) / R). The numerator N stays below
+// x * R < 2^95, so N is built as two 64-bit words and divided by R in four
+// 32-bit digits (each partial dividend below R * 2^32 < 2^64).
+__device__ __forceinline__ uint64_t unscaled_bound(uint64_t within, uint64_t scale) {
+  const uint64_t R = scale & 0xffffffffull;
+  const uint32_t s = (uint32_t)(scale >> 32);
   const uint64_t n = within + 1;
-  // The top digit n >> 32 is below r (the quotient fits 64 bits), so the
-  // division starts at the middle digit with it as the remainder.
-  uint64_t cur = n;
-  const uint64_t q1 = cur / r;
-  cur = (cur % r) << 32;
-  const uint64_t q0 = cur / r;
-  const uint64_t q = (q1 << 32) | q0;
-  return (cur % r) ? q : q - 1;
+  uint64_t hi, lo;
+  if (s >= 64) {
+    hi = n << (s - 64);
+    lo = 0;
+  } else {
+    hi = n >> (64 - s);  // s >= 31
+    lo = n << s;
+  }
+  // N - 1 (N >= 2^31 > 0).
+  if (lo == 0) --hi;
+  --lo;
+  uint64_t q = 0, rem = 0;
+  const uint32_t digit[4] = {(uint32_t)(hi >> 32), (uint32_t)hi, (uint32_t)(lo >> 32),
+                             (uint32_t)lo};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint64_t cur = (rem << 32) | digit[d];
+    q = (q << 32) | (cur / R);
+    rem = cur % R;
+  }
+  return q;
 }
 
 // floor(a * f) exactly for f in [0, 1]; NaN and f <= 0 give 0, f >= 1 gives a.

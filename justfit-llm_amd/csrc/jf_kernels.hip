@@ -2060,27 +2060,26 @@ __device__ __forceinline__ uint32_t wave_kth_bound16(uint32_t v, uint32_t k) {
   return answer;
 }
 
-// A RowParams record read through the scalar cache: issue_row_policy starts
-// the load and returns at once; wait_row_policy waits for it (its operands
-// make every use of the record depend on the wait).
-typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
-struct RowPolicyRegs {
-  u32x16 v;
-};
-__device__ __forceinline__ RowPolicyRegs issue_row_policy(const RowParams *p) {
+// A RowParams record read through the scalar cache. The records are written
+// only before the launch (by a copy or an earlier kernel), so the record is
+// read through the constant address space: the compiler then emits scalar
+// loads for the uniform address at this point of the program, counts them
+// itself and waits for them before the first use of a field. (A scalar load
+// inside inline asm is invisible to the compiler's wait counting: code the
+// compiler places between such a load and its wait, such as register copies,
+// would read registers the load has not yet written.)
+typedef const __attribute__((address_space(4))) uint32_t *ConstWords;
+__device__ __forceinline__ RowParams load_row_policy(const RowParams *p) {
   const uint64_t addr = (uint64_t)p;
   const uint64_t u =
       ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(addr >> 32)) << 32) |
       (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)addr);
-  RowPolicyRegs r;
-  asm volatile("s_load_dwordx16 %0, %1, 0x0" : "=s"(r.v) : "s"(u) : "memory");
-  return r;
-}
-__device__ __forceinline__ RowParams wait_row_policy(RowPolicyRegs r) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(r.v)::"memory");
+  const ConstWords w = (ConstWords)u;
+  uint32_t v[sizeof(RowParams) / 4];
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(RowParams) / 4); ++i) v[i] = w[i];
   RowParams rp;
-  static_assert(sizeof(RowParams) == sizeof(u32x16), "one record per load");
-  __builtin_memcpy(&rp, &r.v, sizeof(rp));
+  __builtin_memcpy(&rp, v, sizeof(rp));
   return rp;
 }
 
@@ -2245,17 +2244,16 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     }
   }
   if (penalized) __syncthreads();  // drop bitmaps cleared
-  // A non-uniform row's policy by one scalar load issued after that barrier
-  // (a barrier waits for every outstanding scalar load); its wait sits at the
-  // first use. The compiler itself would read it with vector loads, since it
-  // cannot rule out that this kernel writes the records.
+  // A non-uniform row's policy by scalar loads issued after that barrier
+  // (a barrier waits for every outstanding scalar load); their wait sits at
+  // the first use.
   // A row with no cut reads its temperature from the record too (a
   // uniform launch's preloaded policy leaves it out).
   const bool uncut = (flags & kRowSampled) && !(flags & (kRowMinP | kRowTopK | kRowTopP));
-  RowPolicyRegs prr{};
-  if (!uni || uncut) prr = issue_row_policy(a.params + row);
+  RowParams prec{};
+  if (!uni || uncut) prec = load_row_policy(a.params + row);
   auto row_policy = [&]() -> RowParams {
-    if (!uni) return wait_row_policy(prr);
+    if (!uni) return prec;
     RowParams r{};
     r.flags = flags;
     r.top_k = u_top_k;
@@ -2489,7 +2487,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
       bound ? min(min(s.wu2[0], s.wu2[1]), min(s.wu2[2], s.wu2[3])) : 0u;
   if (uncut) {
     // The row keeps every admitted token: the uncut kernel's chunk summary.
-    const float inv_t = uni ? wait_row_policy(prr).inv_t : rp.inv_t;
+    const float inv_t = uni ? prec.inv_t : rp.inv_t;
     uncut_summary<DT>(xs, side, base, bmax, badm, inv_t, s, hdr,
                       a.partials + (uint64_t)row * S + chunk);
     return;
@@ -2779,7 +2777,7 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
   // policy, the chunk summaries, the first P slots of every chunk's list,
   // the draft token and its 16 candidates.
   uint32_t ubits = *(GlobalU32 *)uaddr;
-  RowPolicyRegs prr = issue_row_policy((const RowParams *)pbase);
+  const RowParams prec = load_row_policy((const RowParams *)pbase);
   // BlockHeader: maximum, count, admitted, overflow | best_value, best_id,
   // floor_key, reserved.
   const u32x4 h0 = ((GlobalU32x4 *)hbase)[0], h1 = ((GlobalU32x4 *)hbase)[1];
@@ -2813,7 +2811,7 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     s.merge.bins[b] = 0;
     s.merge.key[1024 + b] = 0;
   }
-  const RowParams rp = wait_row_policy(prr);
+  const RowParams rp = prec;
   if (row_indexed) {
     // Drafts addressed through the row's record (a batch of verify lanes):
     // their loads wait for the policy (the launch passed drafted_rows 0).
@@ -3502,17 +3500,19 @@ __device__ __forceinline__ uint32_t pick_slice(uint64_t vg, uint32_t G, uint64_t
 // A sampled row with no min-p, top-k or top-p cut keeps every admitted token.
 // The select pass left, per chunk, the chunk's maximum m_c, its admitted
 // count and its exact fixed-point mass S_c against m_c (partials v[0]). The
-// row's mass is W = sum of T_c = floor(S_c * R_c / 2^32) with the rescale
-// R_c = floor(exp((m_c - M) / T) * 2^32), so the mass costs one read of the
-// logits. One block per row draws: the chunk whose running T_c passes
-// u * W, that chunk reloaded, and its first token (id order) whose running
-// mass P has floor(P * R_c / 2^32) past the remainder (sampling.metal:694-829
-// on these weights). A drafted row's blocks, one per chunk, sum the residual
-// weights residual_of(floor(w * R_c / 2^32), W, q) per slice; the row's last
-// block draws from them, or plainly when no residual mass remains, and
-// writes p(draft). Drafted rows with no penalty, mask or extra tokens
-// (kRowLean) take that pass in residual_kernel, launched before, and their
-// chunk 0 block here draws. Chunk 0's block writes the row's kept outputs.
+// row's mass is W = sum of T_c = floor(S_c * r_c) with the rescale
+// r_c = exp((m_c - M) / T) carried as R_c * 2^-s_c (chunk_scale: a 32-bit
+// significand and a shift, relative precision 2^-32 at any offset), so the
+// mass costs one read of the logits. One block per row draws: the chunk whose
+// running T_c passes u * W, that chunk reloaded, and its first token (id
+// order) whose running mass P has floor(P * r_c) past the remainder
+// (sampling.metal:694-829 on these weights). A drafted row's blocks, one per
+// chunk, sum the residual weights residual_of(floor(w * r_c), W, q) per slice;
+// the row's last block draws from them, or plainly when no residual mass
+// remains, and writes p(draft). Drafted rows with no penalty, mask or extra
+// tokens (kRowLean) take that pass in residual_kernel, launched before, and
+// their chunk 0 block here draws. Chunk 0's block writes the row's kept
+// outputs, each probability w * r_c / W from the token's float weight.
 // Greedy rows take the argmax of the chunk bests when no merge runs.
 //
 // Partial slots per (row, chunk): v[0] S_c; v[kDraftSlot] the draft token's
@@ -3526,7 +3526,7 @@ struct __align__(16) UncutLds {
   uint32_t cids[16];
   float cprobs[16];
   float cmax[kMaxChunks];       // the row's chunk maxima
-  uint64_t cscale[kMaxChunks];  // R_c
+  uint64_t cscale[kMaxChunks];  // r_c, packed s_c << 32 | R_c
   uint64_t ctot[kMaxChunks];    // T_c
   uint32_t ccount[kMaxChunks];  // admitted (non-NaN) tokens per chunk
   uint64_t slices[kWaves * 8];  // one chunk's slice masses
@@ -3548,9 +3548,14 @@ constexpr uint32_t kDraftSlot = 40;
 constexpr uint32_t kResidualSlot = 63;
 
 // The reported probability of a token of float weight w (against its
-// chunk's maximum) in a chunk of rescale R: w R / (W 2^-12) in double.
-__device__ __forceinline__ float uncut_probability(float w, uint64_t R, uint64_t W) {
-  return W ? (float)(((double)w * (double)R) / ((double)W * 0x1p-12)) : 0.0f;
+// chunk's maximum) in a chunk of packed rescale s << 32 | R: w R 2^-s over the
+// row mass W (units of 2^-44), in double; below FLT_MIN it reports 0, so no
+// denormal conversion is involved.
+__device__ __forceinline__ float uncut_probability(float w, uint64_t scale, uint64_t W) {
+  if (!W) return 0.0f;
+  const double r = __builtin_ldexp((double)(uint32_t)scale, -(int)(scale >> 32));
+  const double p = ((double)w * r) / ((double)W * 0x1p-44);
+  return p >= 0x1p-126 ? (float)p : 0.0f;
 }
 
 // The first kept_cap admitted tokens of the row in id order with their
@@ -3616,7 +3621,7 @@ __device__ __forceinline__ void uncut_draw(const SampleLaunch &a, const RowParam
     if (lane == 0) {
       s.sel_bin = c;
       // The running mass inside chunk c (against m_c) that the token's
-      // prefix must pass: floor(P * R_c / 2^32) > within <=> P > this.
+      // prefix must pass: floor(P * r_c) > within <=> P > this.
       s.sel_excl = unscaled_bound(within, s.cscale[c]);
     }
   }
@@ -3657,7 +3662,7 @@ struct __align__(16) LeanLds {
   float cprobs[16];
   uint64_t wl[kWaves];
   float mc;      // this chunk's maximum
-  uint64_t rc;   // its rescale R_c
+  uint64_t rc;   // its rescale r_c, packed
   uint64_t W;    // the row's mass
   uint32_t ok;   // the row has mass to draw from
 };
@@ -3696,8 +3701,8 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
     const uint64_t hmass = parts[at].v[0];
     const float m = in ? hm : -3.402823466e38f;
     const float M = wave_max_f32(m);
-    const uint64_t R = in ? chunk_scale(m, M, inv_t) : 0ull;
-    const uint64_t W = wave_sum_u64(scale_down(in ? hmass : 0ull, R));
+    const uint64_t R = in ? chunk_scale(m, M, inv_t) : kZeroScale;
+    const uint64_t W = wave_sum_u64(scale_by(in ? hmass : 0ull, R));
     const uint32_t admitted = wave_sum_u32(in ? hadm : 0u);
     if (lane == chunk) {
       s.mc = m;
@@ -3850,8 +3855,8 @@ __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_
     const uint32_t cnt = in ? hcnt : 0u;
     const uint64_t mass = in ? hmass : 0ull;
     const float M = wave_max_f32(m);
-    const uint64_t R = in ? chunk_scale(m, M, inv_t) : 0ull;
-    const uint64_t T = scale_down(mass, R);
+    const uint64_t R = in ? chunk_scale(m, M, inv_t) : kZeroScale;
+    const uint64_t T = scale_by(mass, R);
     const uint64_t W = wave_sum_u64(T);
     const uint32_t admitted = wave_sum_u32(adm), kept = wave_sum_u32(cnt);
     if (in) {

@@ -86,6 +86,84 @@ float jfo_expf(float x) {
   return y * u2f((uint32_t)(ni + 127) << 23);
 }
 
+/* e^x in double, for the per-chunk rescale of rows with no cut: the Cody-Waite
+ * reduction x = n ln2 + r (n = rint(x log2 e), ln2 split into a 28-bit head,
+ * so n * head is exact, and the rounded rest), |r| <= ln2 / 2, then e^r by its
+ * Taylor series to degree 13 (the truncation is below 5e-18 relative) in
+ * Horner form with fused multiply-adds, times 2^n. Every step is one IEEE
+ * double operation, so the device restatement gives the same bits. Zero below
+ * -708 (where 2^n would leave the normal range) and for NaN. */
+double jfo_exp64(double x) {
+  if (!(x >= -708.0))
+    return 0.0;
+  if (x > 709.0)
+    return INFINITY;
+  const double n = rint(x * 0x1.71547652b82fep+0);
+  double r = fma(n, -0x1.62e42ffp-1, x);
+  r = fma(n, 0x1.718432a1b0e26p-35, r);
+  double p = 0x1.6124613a86d09p-33;  /* 1/13! */
+  p = fma(p, r, 0x1.1eed8eff8d898p-29);
+  p = fma(p, r, 0x1.ae64567f544e4p-26);
+  p = fma(p, r, 0x1.27e4fb7789f5cp-22);
+  p = fma(p, r, 0x1.71de3a556c734p-19);
+  p = fma(p, r, 0x1.a01a01a01a01ap-16);
+  p = fma(p, r, 0x1.a01a01a01a01ap-13);
+  p = fma(p, r, 0x1.6c16c16c16c17p-10);
+  p = fma(p, r, 0x1.1111111111111p-7);
+  p = fma(p, r, 0x1.5555555555555p-5);
+  p = fma(p, r, 0x1.5555555555555p-3);
+  p = fma(p, r, 0x1p-1);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  const uint64_t bits = (uint64_t)((int64_t)n + 1023) << 52;
+  double two_n;
+  memcpy(&two_n, &bits, 8);
+  return p * two_n;
+}
+
+/* The rescale of a chunk's mass from its maximum m_c to the row maximum M:
+ * r = exp64((m_c - M) * inv_t) (the difference and product in double) as
+ * R * 2^-s, R its 53-bit significand rounded (half up) to 32 bits, so R is in
+ * [2^31, 2^32) and the relative error of the representation is at most
+ * 2^-32 whatever the offset. r = 0 gives R = 0, s = 64. Returned packed as
+ * s << 32 | R (the kernels keep it in one 64-bit word). */
+uint64_t jfo_chunk_scale(float chunk_max, float row_max, float inv_t) {
+  const double r = jfo_exp64(((double)chunk_max - (double)row_max) * (double)inv_t);
+  if (!(r > 0.0))
+    return 64ull << 32;
+  uint64_t bits;
+  memcpy(&bits, &r, 8);
+  const int e = (int)(bits >> 52) - 1023;  /* r normal: e in [-1022, 0] */
+  uint64_t R = (((bits & 0xfffffffffffffull) | (1ull << 52)) + (1ull << 20)) >> 21;
+  uint64_t s = (uint64_t)(31 - e);
+  if (R >> 32) {
+    R >>= 1;
+    s -= 1;
+  }
+  return s << 32 | R;
+}
+
+/* floor(x * R * 2^-s) exactly, for the packed rescale s << 32 | R. */
+uint64_t jfo_scale_by(uint64_t x, uint64_t scale) {
+  const uint64_t R = scale & 0xffffffffull, s = scale >> 32;
+  if (s >= 128)
+    return 0;
+  return (uint64_t)(((unsigned __int128)x * R) >> s);
+}
+
+/* A token's reported probability on a row with no cut: its float weight w
+ * against its chunk's maximum, times the chunk's rescale, over the row mass
+ * W (units of 2^-44), in double; results below FLT_MIN report 0 (on both
+ * sides of the build, so no denormal conversion is involved). */
+float jfo_uncut_probability(float w, uint64_t scale, uint64_t W) {
+  if (!W)
+    return 0.0f;
+  const uint64_t R = scale & 0xffffffffull, s = scale >> 32;
+  const double r = ldexp((double)R, -(int)s);
+  const double p = ((double)w * r) / ((double)W * 0x1p-44);
+  return p >= (double)FLT_MIN ? (float)p : 0.0f;
+}
+
 /* A drafted row's residual weight max(w - Q, 0) (sampling.metal:700-708,
  * 760-765): Q = floor(q * m) for m the mass rounded to a float and the
  * product rounded to a float (both to nearest even, as the kernels compute
@@ -291,24 +369,23 @@ static uint64_t quantize(float w) {
  * token. Its mass is exact per 8192-token chunk c against the chunk's own
  * maximum m_c,
  *   S_c = sum over the chunk of quantize(expf((x - m_c) / T)),
- * and each chunk's mass is rescaled to the row maximum M once:
- *   R_c = floor(expf((m_c - M) / T) * 2^32),   T_c = floor(S_c * R_c / 2^32),
- *   W = sum of T_c.
+ * and each chunk's mass is rescaled to the row maximum M once, by
+ * r_c = exp((m_c - M) / T) carried as R_c * 2^-s_c (jfo_chunk_scale: a 32-bit
+ * significand, relative precision 2^-32 at any offset):
+ *   T_c = floor(S_c * r_c),   W = sum of T_c.
  * The draw takes u * W, the chunk whose running T_c passes it, and inside
  * that chunk the first token (id order) whose running S-mass P satisfies
- * floor(P * R_c / 2^32) > the remainder. A drafted row draws the residual
- * max(floor(w_q * R_c / 2^32) - floor(W * q), 0) in id order (w_q the
- * token's quantized weight), or plainly when no residual mass remains
+ * floor(P * r_c) > the remainder. A drafted row draws the residual
+ * max(floor(w_q * r_c) - floor(W * q), 0) in id order (w_q the token's
+ * quantized weight), or plainly when no residual mass remains
  * (sampling.metal:694-829 on these weights). A token's reported probability
- * (kept outputs, p(draft)) is its float weight w times R_c over W * 2^-12,
- * in double: float(double(w) * double(R_c) / (double(W) * 2^-12)). One pass over the
- * logits yields every S_c, so the GPU reads the row once. With a single
- * chunk (V <= 8192) R = 2^32 and this is the row-maximum definition. */
+ * (kept outputs, p(draft)) is its float weight times r_c over the mass,
+ * float(w * r_c / (W * 2^-44)) in double (jfo_uncut_probability), which is
+ * exp((x - M) / T) / sum to float precision at any offset down to where float
+ * results underflow. One pass over the logits yields every S_c, so the GPU
+ * reads the row once. With a single chunk (V <= 8192) r = 1 and this is the
+ * row-maximum definition. */
 #define JFO_MASS_CHUNK 8192u
-
-static uint64_t scale_down(uint64_t x, uint64_t r) {
-  return (uint64_t)(((unsigned __int128)x * r) >> 32);
-}
 
 static int uncut_select(uint32_t V, uint32_t stop0, uint32_t stop1,
                         const jfo_policy *p, float inv_rep, float inv_t,
@@ -342,18 +419,16 @@ static int uncut_select(uint32_t V, uint32_t stop0, uint32_t stop1,
   }
   uint64_t W = 0;
   for (uint32_t c = 0; c < C; ++c) {
-    cscale[c] = (uint64_t)(jfo_expf((cmax[c] - M) * inv_t) * 0x1p32f);
-    ctot[c] = scale_down(cmass[c], cscale[c]);
+    cscale[c] = jfo_chunk_scale(cmax[c], M, inv_t);
+    ctot[c] = jfo_scale_by(cmass[c], cscale[c]);
     W += ctot[c];
   }
   /* The kept set is every admitted non-NaN token, in id order. */
   out->kept_count = n;
   #define FLOAT_WEIGHT(t, v) jfo_expf(((v) - cmax[(t) / JFO_MASS_CHUNK]) * inv_t)
   #define WEIGHT_OF(t, v) quantize(FLOAT_WEIGHT(t, v))
-  #define PROB_OF(t, v)                                                              \
-    (W ? (float)(((double)FLOAT_WEIGHT(t, v) * (double)cscale[(t) / JFO_MASS_CHUNK]) / \
-                 ((double)W * 0x1p-12))                                               \
-       : 0.0f)
+  #define PROB_OF(t, v) \
+    jfo_uncut_probability(FLOAT_WEIGHT(t, v), cscale[(t) / JFO_MASS_CHUNK], W)
   if (kept_ids) {
     uint32_t k = 0;
     for (uint32_t t = 0; t < V && k < kept_capacity; ++t) {
@@ -379,7 +454,7 @@ static int uncut_select(uint32_t V, uint32_t stop0, uint32_t stop1,
         const float v = penalized(p, inv_rep, in, t);
         if (isnan(v))
           continue;
-        const uint64_t w = scale_down(WEIGHT_OF(t, v), cscale[t / JFO_MASS_CHUNK]);
+        const uint64_t w = jfo_scale_by(WEIGHT_OF(t, v), cscale[t / JFO_MASS_CHUNK]);
         total += jfo_residual(w, W, draft_q(in, t));
       }
       if (total) {
@@ -393,7 +468,7 @@ static int uncut_select(uint32_t V, uint32_t stop0, uint32_t stop1,
           const float v = penalized(p, inv_rep, in, t);
           if (isnan(v))
             continue;
-          const uint64_t w = scale_down(WEIGHT_OF(t, v), cscale[t / JFO_MASS_CHUNK]);
+          const uint64_t w = jfo_scale_by(WEIGHT_OF(t, v), cscale[t / JFO_MASS_CHUNK]);
           run += jfo_residual(w, W, draft_q(in, t));
           if (run > target) {
             out->token = t;
@@ -420,7 +495,7 @@ static int uncut_select(uint32_t V, uint32_t stop0, uint32_t stop1,
         if (isnan(v))
           continue;
         P += WEIGHT_OF(t, v);
-        if (scale_down(P, cscale[c]) > within) {
+        if (jfo_scale_by(P, cscale[c]) > within) {
           out->token = t;
           break;
         }

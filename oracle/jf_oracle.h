@@ -16,7 +16,10 @@
  *   - every sum that decides a token (top-p mass, nucleus walk, the draw, the
  *     residual) runs on w_q = floor(w * 2^44) in exact 64-bit integers, so the
  *     order of summation cannot change a result;
- *   - sampled rows never keep a NaN logit.
+ *   - sampled rows never keep a NaN logit;
+ *   - rows with no cut sum per 8192-token chunk against the chunk maximum and
+ *     rescale each chunk by jfo_chunk_scale (exp in double by jfo_exp64, a
+ *     32-bit significand and a shift).
  * How each function is pinned (brute force, closed form, known answers,
  * statistics) is recorded next to it in jf_oracle.c; nothing here is "parity
  * unpinned".
@@ -44,6 +47,10 @@ float jfo_key_logit(uint32_t key);
 float jfo_expf(float x);
 uint64_t jfo_floor_mul(uint64_t a, float f);
 uint64_t jfo_residual(uint64_t w, uint64_t mass, float q);
+double jfo_exp64(double x);
+uint64_t jfo_chunk_scale(float chunk_max, float row_max, float inv_t);
+uint64_t jfo_scale_by(uint64_t x, uint64_t scale);
+float jfo_uncut_probability(float w, uint64_t scale, uint64_t W);
 uint64_t jfo_splitmix64(uint64_t seed, uint64_t counter);
 float jfo_next_uniform(uint64_t seed, uint64_t *counter);
 void jfo_stage_cycle(uint64_t seed, uint64_t *counter, uint32_t verify_rows,

@@ -93,6 +93,14 @@ def _bind(L):
     L.jfo_floor_mul.restype = c_u64
     L.jfo_residual.argtypes = [c_u64, c_u64, c_f32]
     L.jfo_residual.restype = c_u64
+    L.jfo_exp64.argtypes = [ctypes.c_double]
+    L.jfo_exp64.restype = ctypes.c_double
+    L.jfo_chunk_scale.argtypes = [c_f32, c_f32, c_f32]
+    L.jfo_chunk_scale.restype = c_u64
+    L.jfo_scale_by.argtypes = [c_u64, c_u64]
+    L.jfo_scale_by.restype = c_u64
+    L.jfo_uncut_probability.argtypes = [c_f32, c_u64, c_u64]
+    L.jfo_uncut_probability.restype = c_f32
     L.jfo_splitmix64.argtypes = [c_u64, c_u64]
     L.jfo_splitmix64.restype = c_u64
     L.jfo_next_uniform.argtypes = [c_u64, ctypes.POINTER(c_u64)]

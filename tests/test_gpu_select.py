@@ -456,6 +456,104 @@ def test_dense_residual_in_the_partial_last_chunk(bf16):
     assert g["tokens"][rows - 1] >= V - 4480  # inside the partial last chunk
 
 
+FAR_OFFSETS = [0, 5, 10, 15, 20, 22, 30, 45, 60, 80]
+
+
+def far_row(rng, T, shift):
+    """One row whose chunk c holds values up to 4 T below
+    3 - FAR_OFFSETS[(c + shift) % 10] T (the row maximum 3 in one chunk), a
+    partial last chunk, and four tokens at 3 - 82 T."""
+    C = len(FAR_OFFSETS)
+    V = C * 8192 + 333
+    x = np.empty(V, np.float32)
+    offs = np.roll(FAR_OFFSETS, shift)
+    for c in range(C + 1):
+        lo, hi = c * 8192, min((c + 1) * 8192, V)
+        d = offs[c] if c < C else 3
+        x[lo:hi] = 3.0 - d * T - 4.0 * T * rng.random(hi - lo)
+        x[lo + int(rng.integers(0, hi - lo))] = 3.0 - d * T
+    x[rng.integers(0, V, 4)] = 3.0 - 82.0 * T
+    return V, x
+
+
+def assert_softmax_close(got, want):
+    """1e-5 relative where the probability is a normal float with margin;
+    below that the reported value is either 0 (flushed under FLT_MIN) or
+    within the same bound."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    ok = (np.abs(got - want) <= 1e-5 * want) | ((want < 1e-36) & (got == 0))
+    assert ok.all(), (got[~ok][:5], want[~ok][:5])
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("draft", [None, "sparse", "dense"])
+def test_far_chunk_offsets_report_softmax_probabilities(bf16, draft):
+    """Rows with no cut whose chunk maxima sit 0 to 80 T below the row maximum
+    (tokens to 84 T): tokens, kept probabilities and p(draft) bit-exact with
+    the oracle, and every reported probability within 1e-5 relative of
+    float64 softmax (sampling.metal:38-40, 647-652, 828-829). Masked rows take
+    the general uncut pass (kept outputs, sparse drafts); unmasked rows with a
+    dense q take the lean residual pass. Drafts sit in chunks whose offsets
+    differ by row."""
+    rng = np.random.default_rng(91 + 2 * bf16 + (draft == "dense"))
+    rows = 6
+    T = [0.7, 1.0, 2.0] * 2
+    xs = []
+    for r in range(rows):
+        V, x = far_row(rng, T[r], r)
+        xs.append(x)
+    x = np.stack(xs)
+    if bf16:
+        lg = WL.to_bf16_bits(x)
+        x = (lg.astype(np.uint32) << 16).view(np.float32)
+    else:
+        lg = x
+    masked = draft != "dense"
+    allowed = np.ones((rows, V), bool)
+    if masked:
+        allowed = rng.random((rows, V)) < 0.002
+        allowed[:, ::4096] = True
+    pols = [J.policy(temperature=T[r], constrained=masked) for r in range(rows)]
+    u = rng.random(rows).astype(np.float32)
+    kw = dict(uniforms=u, kept_capacity=512 if masked else 0)
+    kw["logits_bf16" if bf16 else "logits"] = lg
+    if masked:
+        kw["masks"] = WL.mask_words(allowed)
+    if draft is not None:
+        d = np.empty(rows, np.uint32)
+        for r in range(rows):
+            c = (3 * r + 1) % 10
+            d[r] = c * 8192 + int(rng.choice(np.flatnonzero(allowed[r, c * 8192:(c + 1) * 8192])))
+        kw.update(draft_tokens=d, drafted_rows=rows)
+        if draft == "dense":
+            kw["dense_q"] = rng.dirichlet(np.ones(V) * 0.5, rows).astype(np.float32)
+        else:
+            cand = rng.integers(0, V, (rows, 16)).astype(np.uint32)
+            cand[:, 0] = d
+            kw.update(cand_ids=cand,
+                      cand_probs=rng.dirichlet(np.ones(16), rows).astype(np.float32))
+    g, r = both(V, pols, **kw)
+    assert_same(g, r)
+    for k in range(rows):
+        ref = softmax_rows(x[k:k + 1], allowed[k:k + 1], T[k])[0]
+        if masked:
+            n = int(r["kept_counts"][k])
+            assert n == int(allowed[k].sum()) and n <= 512
+            assert_softmax_close(g["kept_probs"][k, :n], ref[r["kept_ids"][k, :n]])
+        if draft is not None:
+            assert_softmax_close([g["draft_probs"][k]], [ref[int(kw["draft_tokens"][k])]])
+
+
+def softmax_rows(x, allowed, T):
+    out = np.zeros(x.shape)
+    for r in range(x.shape[0]):
+        v = np.where(allowed[r], x[r].astype(np.float64), -np.inf)
+        e = np.exp((v - v.max()) / float(np.float32(T)))
+        out[r] = e / e.sum()
+    return out
+
+
 def test_greedy_rows_across_two_launches():
     """300 greedy rows: two launches of the fast kernel (256 rows, then 44),
     each row finished by its last chunk block waiting for the row's other
