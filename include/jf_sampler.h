@@ -28,7 +28,8 @@ extern "C" {
 #define JF_OK 0
 #define JF_ERR_INVALID_ARGUMENT 1 /* std::invalid_argument in the reference */
 #define JF_ERR_LOGIC 2            /* std::logic_error in the reference */
-#define JF_ERR_DEVICE 3           /* a HIP runtime call failed */
+#define JF_ERR_DEVICE 3           /* a HIP runtime call failed, or a device-side
+                                     bounded wait expired (jf_sampler_status) */
 #define JF_ERR_NO_MEMORY 4
 
 #define JF_NO_TOKEN 0xffffffffu
@@ -89,6 +90,23 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
 int jf_sampler_destroy(jf_sampler *sampler);
 /* Bytes of device scratch the sampler holds (Sampling::workspace role). */
 uint64_t jf_sampler_workspace_bytes(const jf_sampler *sampler);
+
+/* No counterpart in the reference (whose last-arriving group never waits,
+ * split_reduce.h:14-45). In an all-greedy jf_sample call each row's
+ * finishing block waits, word by word, for the row's other blocks' results;
+ * that wait is bounded, and the sampler holds a host-mapped status word that
+ * a finishing block sets if its bound is ever reached. jf_sampler_status
+ * reports that as JF_ERR_DEVICE, once (jf_sample does the same before it
+ * enqueues anything), and enqueues on `stream` the clearing of the words
+ * such a call left. Reading the word needs no device synchronization; it
+ * covers the calls whose kernels have run by then. */
+int jf_sampler_status(jf_sampler *sampler, void *stream);
+/* No counterpart in the reference: the bound of that wait, in reads of one
+ * result word (default 2^20, about a second). It exists so that a test can
+ * drive the expiry path from the host: with 0, the finishing block of every
+ * row of an all-greedy call gives up at once (it reads no other block's
+ * result) and every kernel still exits normally. */
+int jf_sampler_set_wait_bound(jf_sampler *sampler, uint32_t reads);
 
 /* ---- penalties -------------------------------------------------------- */
 
@@ -234,14 +252,24 @@ typedef struct jf_sample_args {
   const uint64_t *extra_offsets;
 } jf_sample_args;
 
-/* Selection of every row of `args` on `stream`, asynchronous. In an
- * all-greedy call each row's last chunk block waits for the row's other
- * blocks; one call's waiting blocks (at most 256) are always fewer than the
- * device's block slots, so the waits end. Greedy calls running at the same
- * time from several streams on one GPU should together stay below those
- * slots (1,536 on MI355X): beyond that a waiting block can hold a slot the
- * rows it waits for need, and after its bounded wait (about a second) its
- * token would be wrong. One stream per GPU never meets this. */
+/* Selection of every row of `args` on `stream`, asynchronous.
+ *
+ * Stream contract: one sampler's scratch (row parameters, chunk summaries,
+ * candidate lists, counters, packed bests) is shared by every call on it, so
+ * calls on one sampler must be ordered: issued on one stream, or on streams
+ * the caller orders (events). Two unordered calls on one sampler race. This
+ * is the reference's own model: one engine thread records every selection
+ * into one command graph (Sampling.hpp:114-199; Runtime.cpp:2290-2295).
+ * Separate samplers are independent.
+ *
+ * In an all-greedy call each row's finishing block (its last chunk, or its
+ * last block to arrive) waits for the row's other blocks' results. Blocks
+ * are dispatched in the order of their index, chunk fastest, so the blocks
+ * a finisher waits for were dispatched before it, and they wait on nothing:
+ * every wait ends. The wait is still bounded; should the bound ever be
+ * reached, the row gets JF_NO_TOKEN and the sampler's status word is set,
+ * which the next jf_sample (or jf_sampler_status) reports as JF_ERR_DEVICE
+ * before enqueuing anything else. */
 int jf_sample(jf_sampler *sampler, const jf_sample_args *args, void *stream);
 
 /* jf_sample without a sampler object and without any allocation. It has no
@@ -255,7 +283,9 @@ int jf_sample(jf_sampler *sampler, const jf_sample_args *args, void *stream);
  * any penalty table, created beforehand). Same arguments, results and errors
  * as jf_sample otherwise. Every call on one GPU shares that GPU's array:
  * calls that overlap on one GPU (on different streams) race; calls in one
- * stream's order do not. */
+ * stream's order do not. It has no status word: should an all-greedy row's
+ * bounded wait ever expire, that row's output is JF_NO_TOKEN (in-band, as
+ * the reference reports numeric failures) and nothing else reports it. */
 int jf_sample_static(uint32_t vocabulary, const jf_sample_args *args, void *stream);
 
 /* ---- acceptance ------------------------------------------------------- */

@@ -139,7 +139,7 @@ struct SampleLaunch {
   uint64_t *cands;       // key | id << 32
   uint32_t *counters;
   uint64_t *bests;       // all-greedy fast launches: each block's packed best
-                         // (zero between calls)
+                         // (zero between calls unless a wait gave up)
   RowState *states;
   StagePartial *partials;
   uint32_t *out_tokens;
@@ -149,6 +149,9 @@ struct SampleLaunch {
   float *out_kept_probs;
   uint32_t kept_cap;
   uint32_t q_aligned;     // dense q rows start on 16-byte boundaries
+  uint32_t epoch;         // the call's tag of its packed greedy bests (1..4095)
+  uint32_t wait_bound;    // reads of a packed best before its wait gives up
+  uint32_t *status;       // set to 1 when a wait gave up (host-mapped), or NULL
 };
 
 // The fast selection launch: the per-row facts every block needs before its
@@ -330,6 +333,9 @@ struct SampleScratch {
   StagePartial *partials;   // [max_rows * max_chunks]
   uint32_t max_rows;
   uint32_t max_chunks;
+  uint32_t *status;         // device address of a host-mapped word, or NULL
+  uint32_t epoch;           // this call's tag (1..4095)
+  uint32_t wait_bound;      // reads of a packed best before its wait gives up
 };
 
 // How a selection's host-built row parameters reach scratch.params before

@@ -17,6 +17,8 @@
 // a result.
 #include <hip/hip_ext.h>
 
+#include <mutex>
+
 #include "jf_device.h"
 #include "jf_kernels.h"
 
@@ -2189,6 +2191,40 @@ __device__ __forceinline__ uint32_t past_end_bits(uint32_t V, uint32_t base) {
 // that follow; otherwise each row reads its flags and penalty row from
 // f.row_info and its policy from f.a.params.
 #if JF_IN(1)
+// The greedy finish of one row by wave 0 of its finishing block: lane c < S
+// reads chunk c's packed best (lane `own` holds `mine`, its own chunk's),
+// re-reading up to a.wait_bound times until the word carries this call's
+// tag, and returns each word it took to zero. The largest word wins.
+// Should a wait reach its bound (a word not written by then: the argument
+// that every wait ends has failed), the row gets JF_NO_TOKEN, the sampler's
+// status word is set for the host to report, and the words are left for
+// the host's clear.
+__device__ __forceinline__ void finish_greedy_row(const SampleLaunch &a, uint32_t row,
+                                                  uint32_t S, uint32_t own, uint64_t mine,
+                                                  uint64_t tag) {
+  const uint32_t lane = lane_id();
+  uint64_t best = 0;
+  bool ok = true;
+  if (lane == own) {
+    best = mine;
+  } else if (lane < S) {  // S <= kMaxChunks = 64
+    uint64_t *word = a.bests + (uint64_t)row * S + lane;
+    for (uint32_t n = 0; (best & 0x1fffu) != tag && n < a.wait_bound; ++n) best = ld_dev(word);
+    ok = (best & 0x1fffu) == tag;
+    if (ok) st_dev(word, 0ull);
+  }
+  if (ballot(!ok) != 0) {
+    if (lane == 0) {
+      write_result(a, row, kNoToken, 0.0f, 0);
+      if (a.status) __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    return;
+  }
+  const uint32_t key = wave_max_u32((uint32_t)(best >> 32));
+  const uint32_t low = wave_max_u32((uint32_t)(best >> 32) == key ? (uint32_t)best : 0u);
+  if (lane == 0) write_result(a, row, key ? 0x7ffffu - (low >> 13) : kNoToken, 0.0f, 0);
+}
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     const void *logits, const uint32_t *pen_slots, uint32_t stride, uint32_t V,
@@ -2392,39 +2428,27 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     }
     // Each block's best as one 64-bit word: the value's order key in bits
     // 63..32, 0x7FFFF - id in 31..13 (ids stay below 2^19, so the larger
-    // word holds the larger value, then the lower id), and bit 0 set, so
-    // that a written word is never zero (the word 1: nothing admitted,
-    // below every admitted key).
+    // word holds the larger value, then the lower id), the call's epoch in
+    // 12..1 and bit 0 set (the tag: nothing admitted is the tag alone,
+    // below every admitted key). A reader takes a word as this call's only
+    // when its tag matches, so neither a cleared word nor a late store of an
+    // earlier call passes for it.
+    const uint64_t tag = ((uint64_t)(a.epoch & 0xfffu) << 1) | 1ull;
     const uint64_t mine =
-        bi == kNoToken ? 1ull
-                       : ((uint64_t)logit_key(bv) << 32) | ((uint64_t)(0x7ffffu - bi) << 13) | 1ull;
+        bi == kNoToken ? tag
+                       : ((uint64_t)logit_key(bv) << 32) | ((uint64_t)(0x7ffffu - bi) << 13) | tag;
     if (f.fuse_greedy == 2u) {
       // The row's last chunk finishes it: every other block stores its word
       // and ends; this one reads the row's words, waiting word by word for
-      // any not yet visible, and returns them to zero. The launch sets this
-      // mode only when its rows (one finisher each) are fewer than the
-      // blocks the device holds at once, and the other blocks never wait,
-      // so each word it waits for is stored. The bound only caps the loop.
+      // any not yet written, and returns them to zero. Its wait ends: blocks
+      // are dispatched in the order of their index (chunk fastest), so the
+      // row's other blocks were dispatched before it, and they wait on
+      // nothing.
       if (chunk + 1 < S) {
         if (tid == 0) st_dev(a.bests + (uint64_t)row * S + chunk, mine);
         return;
       }
-      if (w == 0) {
-        constexpr uint32_t kBestWaitBound = 1u << 20;
-        uint64_t best = 0;
-        if (lane == chunk) {
-          best = mine;
-        } else if (lane < S) {  // S <= kMaxChunks = 64
-          uint64_t *word = a.bests + (uint64_t)row * S + lane;
-          best = ld_dev(word);
-          for (uint32_t n = 0; best == 0 && n < kBestWaitBound; ++n) best = ld_dev(word);
-          st_dev(word, 0ull);
-        }
-        const uint32_t key = wave_max_u32((uint32_t)(best >> 32));
-        const uint32_t low = wave_max_u32((uint32_t)(best >> 32) == key ? (uint32_t)best : 0u);
-        if (lane == 0)
-          write_result(a, row, key ? 0x7ffffu - (low >> 13) : kNoToken, 0.0f, 0);
-      }
+      if (w == 0) finish_greedy_row(a, row, S, chunk, mine, tag);
       return;
     }
     // Every row greedy: the row's last block to arrive takes the largest
@@ -2432,8 +2456,8 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     // group, split_reduce.h:14-45). The word's store and the arrival go out
     // together; the last block reads the row's words and waits, word by
     // word, for any not yet visible. Each such store was issued before its
-    // block's arrival, so every wait ends; the bound only caps the loop.
-    // The last block returns the words and the counter to zero.
+    // block's arrival, so every wait ends. The last block returns the words
+    // and the counter to zero.
     if (tid == 0) {
       st_dev(a.bests + (uint64_t)row * S + chunk, mine);
       const uint32_t prev = __hip_atomic_fetch_add(a.counters + row, 1u, __ATOMIC_RELAXED,
@@ -2442,22 +2466,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
       if (prev == S - 1) st_dev(a.counters + row, 0u);
     }
     __syncthreads();
-    if (s.wcount[0] && w == 0) {
-      // Reads of a word before it is taken as written: far beyond the few
-      // microseconds a store issued before its block's arrival needs.
-      constexpr uint32_t kBestWaitBound = 1u << 20;
-      uint64_t best = 0;
-      if (lane < S) {  // S <= kMaxChunks = 64
-        uint64_t *word = a.bests + (uint64_t)row * S + lane;
-        best = ld_dev(word);
-        for (uint32_t n = 0; best == 0 && n < kBestWaitBound; ++n) best = ld_dev(word);
-        st_dev(word, 0ull);
-      }
-      const uint32_t key = wave_max_u32((uint32_t)(best >> 32));
-      const uint32_t low = wave_max_u32((uint32_t)(best >> 32) == key ? (uint32_t)best : 0u);
-      if (lane == 0)
-        write_result(a, row, key ? 0x7ffffu - (low >> 13) : kNoToken, 0.0f, 0);
-    }
+    if (s.wcount[0] && w == 0) finish_greedy_row(a, row, S, S, 0ull, tag);
     return;
   }
 
@@ -4130,13 +4139,16 @@ int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
 
 #if JF_IN(1)
 // Blocks of select_fast_kernel<dtype> the current device holds at once
-// (0 when the query fails), cached per device.
+// (0 when the query fails), cached per device; the cache is shared by every
+// host thread, so it is read and filled under a lock.
 static uint32_t fast_resident_blocks(uint32_t dtype) {
   constexpr int kDevices = 64;
+  static std::mutex lock;
   static uint32_t cache[kDevices][2];
   static bool known[kDevices][2];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevices) return 0;
+  std::lock_guard<std::mutex> guard(lock);
   if (!known[dev][dtype]) {
     int per_cu = 0, cus = 0;
     const hipError_t e1 =

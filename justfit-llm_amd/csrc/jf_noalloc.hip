@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "jf_kernels.h"
@@ -120,6 +121,9 @@ extern "C" int jf_sample_static(uint32_t vocabulary, const jf_sample_args *args,
   uint8_t *base = nullptr;
   const int rc = scratch_address(&base);
   if (rc != JF_OK) return rc;
+  // Each call's tag of its packed greedy bests (a captured graph replays the
+  // one it was captured with; the words are cleared as they are taken).
+  static std::atomic<uint32_t> epochs{0};
   const jf::SampleScratch sc{(jf::RowParams *)(base + kParamsOff),
                              (jf::BlockHeader *)(base + kHeadersOff),
                              (uint64_t *)(base + kCandsOff),
@@ -128,7 +132,10 @@ extern "C" int jf_sample_static(uint32_t vocabulary, const jf_sample_args *args,
                              (jf::RowState *)(base + kStatesOff),
                              (jf::StagePartial *)(base + kPartialsOff),
                              kStaticRows,
-                             kStaticChunks};
+                             kStaticChunks,
+                             nullptr,
+                             epochs.fetch_add(1, std::memory_order_relaxed) % 4095u + 1u,
+                             1u << 20};
   jf::RowParams params[kStaticRows];
   return jf::sample_core(vocabulary, sc, args, params, static_upload, base, stream);
 }

@@ -195,6 +195,9 @@ struct jf_penalty_table {
   uint32_t slot_count = 0;
   uint32_t *slots = nullptr;
   jf::PenaltyRows host;  // the rows as the device holds them
+  // Rows a failed count may have left different on the device than in the
+  // host copy: refused by jf_sample and by counts until rebuilt.
+  std::vector<uint8_t> stale;
   StagingRing staging;
   MappedRing mapped;  // counts of more than kPenaltyOps tokens a call
 };
@@ -215,8 +218,15 @@ struct jf_sampler {
   jf::TreeLaneParams *tree_lanes = nullptr;
   uint64_t workspace_bytes = 0;
   std::vector<jf::RowParams> last_params;
+  std::vector<jf::RowParams> host_params;  // the call's rows, reused across calls
   bool params_valid = false;
   StagingRing staging;
+  // Set to 1 by a greedy finisher whose bounded wait gave up (coherent
+  // host-mapped memory: the host reads it without a device synchronization).
+  uint32_t *status_host = nullptr;
+  uint32_t *status_device = nullptr;
+  uint32_t epoch = 0;                 // the last call's tag, 1..4095
+  uint32_t wait_bound = 1u << 20;     // reads of a packed best before giving up
 };
 
 extern "C" {
@@ -235,6 +245,7 @@ int jf_sampler_destroy(jf_sampler *s) {
   (void)hipFree(s->partials);
   (void)hipFree(s->chain_lanes);
   (void)hipFree(s->tree_lanes);
+  if (s->status_host) (void)hipHostFree(s->status_host);
   delete s;
   return JF_OK;
 }
@@ -270,6 +281,19 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
   if (rc == JF_OK) rc = device_alloc(&s->partials, blocks, "stage partials");
   if (rc == JF_OK) rc = device_alloc(&s->chain_lanes, max_rows, "chain lanes");
   if (rc == JF_OK) rc = device_alloc(&s->tree_lanes, max_rows, "tree lanes");
+  if (rc == JF_OK) {
+    const hipError_t e =
+        hipHostMalloc((void **)&s->status_host, sizeof(uint32_t),
+                      hipHostMallocCoherent | hipHostMallocMapped);
+    if (e != hipSuccess) {
+      s->status_host = nullptr;
+      rc = hip_fail(e, "status word");
+    } else {
+      *s->status_host = 0;
+      const hipError_t e2 = hipHostGetDevicePointer((void **)&s->status_device, s->status_host, 0);
+      if (e2 != hipSuccess) rc = hip_fail(e2, "status word address");
+    }
+  }
   if (rc == JF_OK) {
     const hipError_t e1 = hipMemset(s->counters, 0, max_rows * sizeof(uint32_t));
     const hipError_t e2 = hipMemset(s->states, 0, max_rows * sizeof(jf::RowState));
@@ -337,6 +361,7 @@ int jf_penalty_table_create(uint32_t vocabulary, uint32_t rows,
                       ? (uint32_t)jf::kThreads
                       : 2u * jf::kThreads;
   t->host.init(vocabulary, rows, max_entries, t->slot_count);
+  t->stale.assign(rows, 0);
   int rc = JF_OK;
   hipError_t ge = hipGetDevice(&t->device);
   if (ge != hipSuccess) rc = hip_fail(ge, "hipGetDevice");
@@ -381,7 +406,11 @@ static int widen_slots(jf_penalty_table *t, void *stream) {
   for (uint32_t r = 0; r < t->rows; ++r) {
     if (!t->host.fits(r)) continue;
     const int rc = upload_penalty_slots(t, r, stream);
-    if (rc != JF_OK) return rc;
+    if (rc != JF_OK) {
+      // This row and the later ones keep the narrower layout on the device.
+      for (uint32_t q = r; q < t->rows; ++q) t->stale[q] = 1;
+      return rc;
+    }
   }
   return JF_OK;
 }
@@ -420,7 +449,12 @@ int jf_penalty_table_rebuild(jf_penalty_table *t, uint32_t row,
   rc = t->host.rebuild(row, words.data());
   if (rc != JF_OK) return rc;
   rc = upload_penalty_row(t, row, stream);
-  return rc == JF_OK ? widen_slots(t, stream) : rc;
+  if (rc != JF_OK) {
+    t->stale[row] = 1;
+    return rc;
+  }
+  t->stale[row] = 0;
+  return widen_slots(t, stream);
 }
 
 // The update of one (row, token) pair as penalty_count_kernel reads it.
@@ -486,6 +520,9 @@ static int count_mapped(jf_penalty_table *t, const jf::PenaltyTableView &view,
 // then describes each token's update, and penalty_count_kernel applies them
 // on `stream` in one launch: as kernel arguments (up to kPenaltyOps tokens,
 // no copy and no wait on earlier work) or from host-mapped memory.
+static int count_pairs_checked(jf_penalty_table *t, const uint32_t *rows, uint32_t one_row,
+                               const uint32_t *selected, uint64_t n, void *stream);
+
 static int count_pairs(jf_penalty_table *t, const uint32_t *rows, uint32_t one_row,
                        const uint32_t *selected, uint64_t n, void *stream) {
   if (!selected && n) return fail(JF_ERR_INVALID_ARGUMENT, "null buffer");
@@ -497,8 +534,24 @@ static int count_pairs(jf_penalty_table *t, const uint32_t *rows, uint32_t one_r
       return fail(JF_ERR_INVALID_ARGUMENT, "penalized lane has no penalty table row");
     if (selected[i] >= t->vocabulary)
       return fail(JF_ERR_INVALID_ARGUMENT, "penalty token is outside the vocabulary");
+    if (t->stale[row])
+      return fail(JF_ERR_LOGIC, "penalty table row is out of date after a failed update; "
+                                "rebuild it");
     t->host.prefetch(row, selected[i]);
   }
+  rc = count_pairs_checked(t, rows, one_row, selected, n, stream);
+  if (rc == JF_ERR_DEVICE) {
+    // A launch or an upload failed after the host copy took some of the
+    // updates: the device rows may differ from it.
+    for (uint64_t i = 0; i < n; ++i) t->stale[rows ? rows[i] : one_row] = 1;
+  }
+  return rc;
+}
+
+// count_pairs after its argument checks.
+static int count_pairs_checked(jf_penalty_table *t, const uint32_t *rows, uint32_t one_row,
+                               const uint32_t *selected, uint64_t n, void *stream) {
+  int rc = JF_OK;
   // Updates grouped by row, call order kept inside each row.
   std::vector<uint64_t> order(n);
   for (uint64_t i = 0; i < n; ++i) order[i] = i;
@@ -657,6 +710,9 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
         return fail(JF_ERR_INVALID_ARGUMENT, "penalized lane has no penalty table row");
       if (a->penalties->vocabulary != V)
         return fail(JF_ERR_INVALID_ARGUMENT, "penalty table vocabulary differs");
+      if (a->penalties->stale[a->penalty_rows[r]])
+        return fail(JF_ERR_LOGIC, "penalty table row is out of date after a failed update; "
+                                  "rebuild it");
       rp.flags |= jf::kRowPenalized;
       rp.penalty_row = a->penalty_rows[r];
       rp.extra_count = extra;
@@ -763,6 +819,9 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
                         (a->draft_q_stride * sizeof(float)) % 16 == 0
                     ? 1u
                     : 0u;
+  L.epoch = sc.epoch;
+  L.wait_bound = sc.wait_bound;
+  L.status = sc.status;
 
   if ((a->select_start_event == nullptr) != (a->select_done_event == nullptr))
     return fail(JF_ERR_INVALID_ARGUMENT, "select events come in pairs");
@@ -928,17 +987,57 @@ int sampler_upload(void *ctx, const jf::RowParams *params, uint32_t rows,
 
 extern "C" {
 
+// A greedy finisher's wait that gave up in an earlier call (the status word
+// set): reported once as JF_ERR_DEVICE, with the packed bests and arrival
+// counters cleared on `stream` behind every earlier launch, so that no word
+// that call left behind reaches a later one.
+static int take_status(jf_sampler *s, void *stream) {
+  if (!__atomic_load_n(s->status_host, __ATOMIC_ACQUIRE)) return JF_OK;
+  __atomic_store_n(s->status_host, 0u, __ATOMIC_RELEASE);
+  const hipStream_t st = (hipStream_t)stream;
+  JF_HIP(hipMemsetAsync(s->bests, 0, (size_t)s->max_rows * s->max_chunks * sizeof(uint64_t), st),
+         "greedy best clear");
+  JF_HIP(hipMemsetAsync(s->counters, 0, (size_t)s->max_rows * sizeof(uint32_t), st),
+         "counter clear");
+  return fail(JF_ERR_DEVICE,
+              "a greedy selection's bounded wait for a chunk result expired in an earlier "
+              "call; that call's rows affected hold JF_NO_TOKEN");
+}
+
 int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   if (!s || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler or arguments");
   int rc = check_device(s->device);
   if (rc != JF_OK) return rc;
+  rc = take_status(s, stream);
+  if (rc != JF_OK) return rc;
   if (!a->rows || a->rows > s->max_rows)
     return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling batch width");
-  const jf::SampleScratch sc{s->params, s->headers,  s->cands,    s->counters,
-                             s->bests,  s->states,   s->partials, s->max_rows,
-                             s->max_chunks};
-  std::vector<jf::RowParams> params(a->rows);
-  return jf::sample_core(s->vocabulary, sc, a, params.data(), sampler_upload, s, stream);
+  s->epoch = s->epoch % 4095u + 1u;
+  const jf::SampleScratch sc{s->params,    s->headers,  s->cands,    s->counters,
+                             s->bests,     s->states,   s->partials, s->max_rows,
+                             s->max_chunks, s->status_device, s->epoch, s->wait_bound};
+  if (s->host_params.size() < a->rows) {
+    try {
+      s->host_params.resize(a->rows);
+    } catch (const std::bad_alloc &) {
+      return fail(JF_ERR_NO_MEMORY, "row parameter allocation failed");
+    }
+  }
+  return jf::sample_core(s->vocabulary, sc, a, s->host_params.data(), sampler_upload, s,
+                         stream);
+}
+
+int jf_sampler_status(jf_sampler *s, void *stream) {
+  if (!s) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler");
+  const int rc = check_device(s->device);
+  if (rc != JF_OK) return rc;
+  return take_status(s, stream);
+}
+
+int jf_sampler_set_wait_bound(jf_sampler *s, uint32_t reads) {
+  if (!s) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler");
+  s->wait_bound = reads;
+  return JF_OK;
 }
 
 // ---- acceptance -----------------------------------------------------------

@@ -29,7 +29,8 @@ JF_UNIFORM_TREE_DRAWS = 24
 # Every symbol include/jf_sampler.h declares.
 EXPORTS = [
     "jf_last_error", "jf_policy_validate", "jf_sampler_create",
-    "jf_sampler_destroy", "jf_sampler_workspace_bytes",
+    "jf_sampler_destroy", "jf_sampler_workspace_bytes", "jf_sampler_status",
+    "jf_sampler_set_wait_bound",
     "jf_penalty_words_rebuild", "jf_penalty_words_count",
     "jf_penalty_table_create", "jf_penalty_table_destroy",
     "jf_penalty_table_rebuild", "jf_penalty_table_count", "jf_penalty_table_count_rows",
@@ -163,6 +164,8 @@ def lib():
         L.jf_sampler_destroy.argtypes = [c_vp]
         L.jf_sampler_workspace_bytes.argtypes = [c_vp]
         L.jf_sampler_workspace_bytes.restype = c_u64
+        L.jf_sampler_status.argtypes = [c_vp, c_vp]
+        L.jf_sampler_set_wait_bound.argtypes = [c_vp, c_u32]
         L.jf_penalty_words_rebuild.argtypes = [
             c_vp, c_u32, c_vp, c_u64, c_u64, ctypes.c_int, c_u32, ctypes.c_int]
         L.jf_penalty_words_count.argtypes = [c_vp, c_u32, c_vp, c_u64]
@@ -333,6 +336,14 @@ class Sampler:
 
     def workspace_bytes(self):
         return lib().jf_sampler_workspace_bytes(self.handle)
+
+    def status(self, stream=None):
+        """jf_sampler_status: raises JfError (JF_ERR_DEVICE) once if a greedy
+        finisher's bounded wait expired in a call that has run."""
+        check(lib().jf_sampler_status(self.handle, _stream() if stream is None else stream))
+
+    def set_wait_bound(self, reads):
+        check(lib().jf_sampler_set_wait_bound(self.handle, reads))
 
     def sample_args(self, logits, policies, out_tokens, *, masks=None,
                     stop_tokens=(JF_NO_TOKEN, JF_NO_TOKEN), penalties=None,

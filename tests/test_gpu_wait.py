@@ -1,0 +1,64 @@
+"""The greedy finisher's bounded wait (no counterpart in the reference, whose
+last-arriving group never waits; split_reduce.h:14-45): its expiry path,
+driven from the host by a wait bound of 0, so that every kernel still exits
+normally. Both finisher forms: the row's last chunk block (V = 151,936, 19
+chunks) and the last block to arrive (V = 8,000, one chunk). Expiry gives
+JF_NO_TOKEN rows and a status the host reports once as JF_ERR_DEVICE (by
+jf_sampler_status, or by the next jf_sample before it enqueues anything);
+the words the expired call left are cleared, and the next calls at the
+default bound are bit-exact with the oracle again."""
+import numpy as np
+import pytest
+
+import jf_sampler as J
+from harness import NO, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def greedy_call(s, x):
+    import torch
+    dev = torch.device("cuda", 0)
+    out = torch.full((x.shape[0],), -1, dtype=torch.int32, device=dev)
+    s.sample(torch.from_numpy(x).to(dev), [J.policy()] * x.shape[0], out)
+    torch.cuda.synchronize()
+    return out.cpu().numpy().view(np.uint32).copy()
+
+
+@pytest.mark.parametrize("V", [151936, 8000])
+def test_expired_wait_reports_and_recovers(V):
+    import torch
+    print(f"case V={V}", flush=True)
+    rng = np.random.default_rng(V)
+    rows = 8
+    x = rng.normal(0, 2.0, (rows, V)).astype(np.float32)
+    want = run_oracle(V, [J.policy()] * rows, logits=x)["tokens"]
+    s = J.Sampler(V, rows)
+    np.testing.assert_array_equal(greedy_call(s, x), want)
+    s.status()  # nothing to report
+
+    # Bound 0: every row's finisher gives up.
+    s.set_wait_bound(0)
+    got = greedy_call(s, x)
+    assert np.all(got == NO), got
+    with pytest.raises(J.JfError) as e:
+        s.status()
+    assert e.value.code == J.JF_ERR_DEVICE and "expired" in e.value.message
+    s.status()  # reported once
+    s.set_wait_bound(1 << 20)
+    np.testing.assert_array_equal(greedy_call(s, x), want)
+
+    # The next jf_sample reports it instead, enqueuing nothing, then recovers.
+    s.set_wait_bound(0)
+    assert np.all(greedy_call(s, x) == NO)
+    s.set_wait_bound(1 << 20)
+    dev = torch.device("cuda", 0)
+    out = torch.full((rows,), 7, dtype=torch.int32, device=dev)
+    with pytest.raises(J.JfError) as e:
+        s.sample(torch.from_numpy(x).to(dev), [J.policy()] * rows, out)
+    assert e.value.code == J.JF_ERR_DEVICE
+    torch.cuda.synchronize()
+    assert np.all(out.cpu().numpy() == 7)  # nothing ran
+    for _ in range(3):
+        np.testing.assert_array_equal(greedy_call(s, x), want)
+    s.status()
