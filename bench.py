@@ -31,10 +31,13 @@ def parse():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
-    ap.add_argument("--path", default="sample", choices=["sample", "draft", "gather"],
+    ap.add_argument("--path", default="sample",
+                    choices=["sample", "draft", "gather", "verify"],
                     help="sample: jf_sample on --config (the headline); draft: "
                          "jf_draft_select at 4 lanes, V=151936; gather: jf_tree_gather "
-                         "of one KV-like tensor family after C4's tree acceptance")
+                         "of one KV-like tensor family after C4's tree acceptance; verify: "
+                         "the engine's penalized chain verify (4 lanes x 16 rows, "
+                         "V=248320, extras and sparse drafts) plus chain acceptance")
     ap.add_argument("--mode", default="auto",
                     help="C3/C4: greedy or sampled (auto: sampled)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
@@ -103,7 +106,8 @@ def build_workload(cfg, mode, history="uniform"):
         pol = J.policy(temperature=1.0) if sampled else J.policy()
         w.update(V=c["V"], logits=c["logits"], policies=[pol] * rows,
                  name=f"C4 tree verify 16x16 nodes V=151936 fp32 "
-                      f"{'rejection sampling (dense q)' if sampled else 'greedy'}",
+                      f"{'rejection sampling (dense q)' if sampled else 'greedy'}"
+                      " + tree acceptance",
                  dtype="f32", tree=c, sampled=sampled)
         hist_bytes = c["q"].nbytes if sampled else 0
         if sampled:
@@ -174,6 +178,35 @@ class GpuStep:
         self.draft_probs = extra.get("out_draft_probs")
         self.extra = extra  # the device tensors the argument records point at
         self.out = torch.zeros(rows, dtype=torch.int32, device=dev)
+        # C4's step ends as the engine's does: tree acceptance over the
+        # selected tokens (tree.metal:20-84; Runtime.cpp:1284-1306), which
+        # rewrites them in place into each request's accepted path.
+        self.accept = None
+        if w.get("tree") is not None:
+            c = w["tree"]
+            from jf_sampler import workloads as WL
+            rq, per = len(c["trees"]), rows // len(c["trees"])
+            sampled = w.get("sampled")
+            trees = []
+            for k in range(rq):
+                if sampled:
+                    n = WL.chain_length(c["trees"][k])
+                    cq = [float(c["q"][k * per + j, c["tokens"][k][j + 1]]) for j in range(n - 1)]
+                    trees.append(J.tree_lane(c["trees"][k], c["tokens"][k], n, cq))
+                else:
+                    trees.append(J.tree_lane(c["trees"][k], c["tokens"][k]))
+            self.acc_out = [torch.zeros(rq, dtype=torch.int32, device=dev) for _ in range(2)]
+            self.acc_path = torch.zeros((rq, 8), dtype=torch.int32, device=dev)
+            kw_acc = dict(trees=trees, rows_per_lane=per, target_tokens=self.out.view(rq, per),
+                          retained=self.acc_out[0], accepted=self.acc_out[1],
+                          path_rows=self.acc_path, maximum_retained=[8] * rq,
+                          policies=[w["policies"][0]] * rq)
+            if sampled:
+                self.acc_u = torch.from_numpy(np.ascontiguousarray(c["uniforms"])).to(dev)
+                kw_acc.update(target_draft_probs=self.draft_probs.view(rq, per),
+                              uniforms=self.acc_u)
+            self.acc_trees = trees
+            self.accept = ("tree",) + self.sampler.accept_tree_args(**kw_acc)
         for i in range(len(self.copies)):
             kw = dict(extra)
             if "histories" in w:
@@ -193,6 +226,77 @@ class GpuStep:
     def step(self, i):
         a, _ = self.kw[i % len(self.kw)]
         self.sampler.launch(a)
+        if self.accept is not None:
+            self.sampler.launch_accept(self.accept)
+
+
+class VerifyStep:
+    """The engine's penalized chain-verify step (Sampling::addVerify then
+    addAcceptance, Sampling.cpp:149-172, 278-328): one jf_sample over every
+    lane's 16 verify rows, addressed per row (draft token, candidate row,
+    extra penalty tokens), then jf_accept_chain over the lanes, which
+    rewrites the selected tokens into each lane's accepted chain. Inputs
+    resident and rotated like GpuStep's."""
+
+    def __init__(self, c):
+        import torch
+        import jf_sampler as J
+        dev = torch.device("cuda", 0)
+        V, lanes, rows = c["V"], c["lanes"], c["rows"]
+        B = lanes * rows
+        pol = J.policy(**c["policy"])
+        self.c = c
+        self.w = dict(V=V, rows=B, policies=[pol] * B, dtype="f32",
+                      name=f"verify {lanes} lanes x {rows} rows V={V} fp32, T0.7 top-k 50 "
+                           "top-p 0.9 repetition 1.1 presence 0.5 frequency 0.3 over 2048 ids "
+                           "+ verify extras, 16 sparse candidates a proposal, then chain "
+                           "acceptance")
+        base = torch.from_numpy(c["logits"])
+        per = base.numel() * base.element_size()
+        self.copies = [base.to(dev) for _ in range(max(2, -(-ROTATE_BYTES // per)))]
+        self.sampler = J.Sampler(V, B)
+        t32 = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev)
+        self.inputs = t32(c["inputs"])
+        self.cand = t32(c["cand_ids"])
+        self.cprob = torch.from_numpy(c["cand_probs"]).to(dev)
+        self.u = torch.from_numpy(np.ascontiguousarray(c["uniforms"].reshape(-1))).to(dev)
+        self.uidx = t32(c["uniform_index"])
+        self.proposed = t32(c["inputs"].reshape(lanes, rows)[:, 1:])
+        self.out = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.draft_probs = torch.zeros(B, dtype=torch.float32, device=dev)
+        self.retained = torch.zeros(lanes, dtype=torch.int32, device=dev)
+        self.accepted = torch.zeros(lanes, dtype=torch.int32, device=dev)
+        H = max(len(h) for h in c["histories"])
+        self.tables, self.kw = [], []
+        for x in self.copies:
+            t = J.PenaltyTable(V, lanes, H + 8)
+            for l, h in enumerate(c["histories"]):
+                t.rebuild(l, h, c["generated"][l], None, c["mark_prompt"])
+            self.tables.append(t)
+            self.kw.append(self.sampler.sample_args(
+                x, self.w["policies"], self.out, penalties=t,
+                penalty_rows=[g // rows for g in range(B)], extra_tokens=self.inputs,
+                extra_counts=list(c["extra_counts"]), uniforms=self.u,
+                uniform_index=self.uidx, draft_tokens=self.inputs, cand_ids=self.cand,
+                cand_probs=self.cprob, out_draft_probs=self.draft_probs,
+                draft_token_index=c["draft_index"], draft_cand_index=c["cand_index"],
+                extra_offsets=c["extra_offsets"]))
+        self.accept = ("chain",) + self.sampler.accept_chain_args(
+            verify_rows=rows, proposed=self.proposed, target_tokens=self.out,
+            retained=self.retained, accepted=self.accepted, maximum_retained=[rows] * lanes,
+            policies=[pol] * lanes, candidates=self.cand, proposal_probs=self.cprob,
+            target_draft_probs=self.draft_probs, uniforms=self.u)
+        torch.cuda.synchronize()
+
+    def step(self, i):
+        a, _ = self.kw[i % len(self.kw)]
+        self.sampler.launch(a)
+        self.sampler.launch_accept(self.accept)
+
+    def close(self):
+        for t in self.tables:
+            t.close()
+        self.sampler.close()
 
 
 class HipEvents:
@@ -266,6 +370,16 @@ def time_with_counts(g, steps):
             "note": "each step followed by jf_penalty_table_count_rows of one token per row"}
 
 
+def accept_ptr(g, kind):
+    """The step's prepared acceptance record of `kind` ("chain" or "tree"),
+    as a pointer for the C++ loop, or None."""
+    import ctypes
+    acc = getattr(g, "accept", None)
+    if acc is None or acc[0] != kind:
+        return None
+    return ctypes.cast(ctypes.pointer(acc[1]), ctypes.c_void_p)
+
+
 def time_cpp_loop(g, steps, with_counts, batch=0):
     """The same calls issued from C++ (libjf_bench_loop.so), as a native
     engine issues them: GPU and host microseconds per step without the
@@ -278,7 +392,7 @@ def time_cpp_loop(g, steps, with_counts, batch=0):
     vp, u32 = ctypes.c_void_p, ctypes.c_uint32
     L.jf_bench_sample_loop.argtypes = [vp, vp, u32, u32, vp, vp, vp, u32, vp,
                                        ctypes.POINTER(ctypes.c_double),
-                                       ctypes.POINTER(ctypes.c_double), u32, vp]
+                                       ctypes.POINTER(ctypes.c_double), u32, vp, vp, vp]
     n = len(g.kw)
     arr = (J.JfSampleArgs * n)(*[a for a, _ in g.kw])
     rows = g.w["rows"]
@@ -293,7 +407,8 @@ def time_cpp_loop(g, steps, with_counts, batch=0):
                                 None if idx is None else idx.ctypes.data_as(vp),
                                 None if toks is None else toks.ctypes.data_as(vp), rows,
                                 J._stream(), ctypes.byref(gpu), ctypes.byref(host), batch,
-                                None if batch_us is None else batch_us.ctypes.data_as(vp))
+                                None if batch_us is None else batch_us.ctypes.data_as(vp),
+                                accept_ptr(g, "chain"), accept_ptr(g, "tree"))
     if rc:
         raise RuntimeError(f"C++ timing loop failed: {rc} {J.lib().jf_last_error().decode()}")
     out = {"us_per_step": gpu.value, "host_us_per_call": host.value}
@@ -302,18 +417,30 @@ def time_cpp_loop(g, steps, with_counts, batch=0):
     return out
 
 
+def pick_batch(steps):
+    """Steps per timed run for the step-time distribution: the largest
+    divisor of `steps` up to 25 that leaves at least four runs, else at least
+    two (1 when none does)."""
+    for runs in (4, 2):
+        for d in range(min(25, steps // runs), 1, -1):
+            if steps % d == 0:
+                return d
+    return 1
+
+
 def time_graph(g, steps):
     """Steps captured in a HIP graph and replayed: jf_sample_static (the
     entry point that allocates nothing; row parameters travel as kernel
-    arguments) over 25 rotated input copies per graph, the graph replayed
-    steps / 25 times between HIP events. None where the static entry point's
-    limits (64 rows, 262,144 tokens) exclude the workload."""
+    arguments) over pick_batch(steps) rotated input copies per graph, the
+    graph replayed until `steps` steps have run, between HIP events. None
+    where the static entry point's limits (64 rows, 262,144 tokens) exclude
+    the workload."""
     import torch
     import jf_sampler as J
     V, rows = g.w["V"], g.w["rows"]
-    if rows > 64 or V > 262144 or steps % 25:
+    if rows > 64 or V > 262144:
         return None
-    per = 25
+    per = pick_batch(steps)
     args = [g.kw[i % len(g.kw)][0] for i in range(per)]
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -335,7 +462,8 @@ def time_graph(g, steps):
     us = e0.elapsed_time(e1) * 1000.0 / steps
     del graph
     return {"us_per_step": us,
-            "note": "jf_sample_static captured 25 steps to a HIP graph, replayed"}
+            "note": f"jf_sample_static captured {per} steps to a HIP graph, replayed "
+                    f"{steps // per} times"}
 
 
 def cpu_model():
@@ -413,7 +541,7 @@ PROFILE_NAMES = {(1, "auto"): "select_c1", (2, "auto"): "select_merge_c2",
                  (4, "greedy"): "select_c4_greedy", (4, "sampled"): "select_uncut_c4_sampled",
                  (5, "auto"): "select_merge_c5", (2, "zipf"): "select_merge_c2_zipf",
                  (2, "mixed"): "select_merge_c2_mixed", ("draft", "auto"): "draft_select",
-                 ("gather", "auto"): "tree_gather"}
+                 ("gather", "auto"): "tree_gather", ("verify", "auto"): "select_verify"}
 
 
 def profile_key(cfg, mode, history="uniform"):
@@ -643,6 +771,123 @@ def bench_gather(args):
     print(json.dumps(line), flush=True)
 
 
+def verify_cpu_baseline(c, seconds):
+    """The oracle (C restatement, one thread) over whole verify steps: every
+    row's selection (jfo_select_row with its extras, draft and candidates)
+    and each lane's chain acceptance, repeated for about `seconds`."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    V, lanes, rows = c["V"], c["lanes"], c["rows"]
+    pol = O.policy(**c["policy"])
+    words = [O.rebuild_penalty_words(V, h, c["generated"][l], None, c["mark_prompt"])[1]
+             for l, h in enumerate(c["histories"])]
+    inp = c["inputs"]
+
+    def step():
+        vt = np.zeros(lanes * rows, np.uint32)
+        vp = np.zeros(lanes * rows, np.float32)
+        for l in range(lanes):
+            for r in range(rows):
+                g = l * rows + r
+                d = int(c["draft_index"][g])
+                ci = int(c["cand_index"][g])
+                vt[g], vp[g] = O.select_row(
+                    V, pol, logits=c["logits"][g], words=words[l],
+                    extra=inp[l * rows + 1:l * rows + 1 + r],
+                    uniform=float(c["uniforms"][l, 15]),
+                    draft_token=int(inp[d]) if d != 0xFFFFFFFF else O.NO_TOKEN,
+                    cand_ids=c["cand_ids"][ci] if d != 0xFFFFFFFF else None,
+                    cand_probs=c["cand_probs"][ci] if d != 0xFFFFFFFF else None)[:2]
+        out = []
+        for l in range(lanes):
+            P = rows - 1
+            out.append(O.accept_chain(P, rows, True, inp[l * rows + 1:(l + 1) * rows],
+                                      vt[l * rows:(l + 1) * rows],
+                                      cand_ids=c["cand_ids"][l * P:(l + 1) * P],
+                                      cand_probs=c["cand_probs"][l * P:(l + 1) * P],
+                                      target_draft_prob=vp[l * rows:(l + 1) * rows],
+                                      uniforms40=c["uniforms"][l]))
+        return vt, vp, out
+
+    n, t0 = 0, time.perf_counter()
+    while True:
+        step()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= 2:
+            break
+    return dict(value=n / el, unit="steps/s", cores=1, kind="port", cpu_model=cpu_model(),
+                sample=f"{n} whole verify steps ({lanes * rows} rows' selections with extras "
+                       f"and sparse drafts, then {lanes} lanes' chain acceptance) of the same "
+                       f"seeded inputs in {el:.1f} s: oracle/jf_oracle.c -O2 through ctypes, "
+                       f"one thread")
+
+
+def bench_verify(args):
+    """The penalized chain-verify shape (VerifyStep): its step timed from
+    C++ as the sample path's is, its dominant kernel (select_kernel: rows
+    with extra verify tokens take the general single pass) timed alone."""
+    import torch
+    from jf_sampler import workloads as WL
+    c = WL.config_verify()
+    g = VerifyStep(c)
+    print(f"# {g.w['name']}: {len(g.copies)} rotated copies", file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        g.step(i)
+    torch.cuda.synchronize()
+    K = args.steps
+    wall0 = time.perf_counter()
+    cpp = time_cpp_loop(g, K, False)
+    wall = time.perf_counter() - wall0
+    ms_per_step = cpp["us_per_step"] / 1000.0
+    batch = pick_batch(K)
+    per = time_cpp_loop(g, K, False, batch=batch)["batch_us"].astype(np.float64)
+    sel_mean, sel_p50 = time_select(g, args.warmup + K, K)
+    B, V = g.w["rows"], g.w["V"]
+    H = len(c["histories"][0])
+    # Algorithmic bytes of the selection kernel: every row's logits, its
+    # lane's history ids (each row applies them), its extra tokens and its
+    # 16 candidates; the step adds uniforms, outputs and the acceptance.
+    sel_bytes = B * V * 4 + B * H * 4 + int(np.sum(c["extra_counts"])) * 4 + B * 16 * 8
+    step_bytes = sel_bytes + B * 4 * 3 + c["lanes"] * (c["rows"] - 1) * (4 + 16 * 8)
+    achieved = sel_bytes / (sel_mean * 1e-6) / 1e9
+    step_gbs = step_bytes / (cpp["us_per_step"] * 1e-6) / 1e9
+    kernel = "jf::select_kernel<0>"
+    key = ("verify", "auto")
+    traffic = read_traffic(key, kernel)
+    prof_us = read_profile_us(key, kernel)
+    cpu = None if args.no_cpu else verify_cpu_baseline(c, args.cpu_seconds)
+    line = {
+        "metric": "verify steps/sec at 4 lanes x 16 rows, V=248320 (select + chain "
+                  "acceptance); achieved HBM GB/s vs peak; p50 us/step",
+        "value": 1000.0 / ms_per_step, "unit": "steps/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "p50_us": float(np.percentile(per, 50)), "p90_us": float(np.percentile(per, 90)),
+        "wall_s": wall, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32",
+        "data": f"synthetic (workloads.config_verify, seed 8), {len(g.copies)} rotated "
+                f"logits copies >= 512 MB",
+        "config": {"workload": g.w["name"], "rows": B, "vocabulary": V,
+                   "algorithmic_bytes_per_step": step_bytes},
+        "timing": f"jf_sample + jf_accept_chain back to back from C++, events at the loop's "
+                  f"two ends; p50/p90 over runs of {batch} steps in a second pass",
+        "host_us_per_call": cpp["host_us_per_call"],
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "kernel": kernel,
+                     "timing": "mean of HIP events the library records around the kernel's "
+                               "launch on its stream",
+                     "kernel_mean_us": sel_mean, "kernel_p50_us": sel_p50,
+                     "rocprof_mean_us": prof_us,
+                     "rocprof_frac": (sel_bytes / (prof_us * 1e-6) / 1e9 / PEAK_HBM_GBS
+                                      if prof_us else None),
+                     "algorithmic_bytes": sel_bytes, "step_achieved": step_gbs,
+                     "step_frac": step_gbs / PEAK_HBM_GBS},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    g.close()
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -664,26 +909,33 @@ def main():
     if args.path == "gather":
         bench_gather(args)
         return
+    if args.path == "verify":
+        bench_verify(args)
+        return
     if args.history != "uniform" and args.config != 2:
         print("--history applies to --config 2 only", file=sys.stderr)
         sys.exit(2)
     w = build_workload(args.config, args.mode, args.history)
     print(f"# {w['name']}: building inputs", file=sys.stderr, flush=True)
-    g = GpuStep(w, count_headroom=args.steps)
+    # Table rows hold room for the counted loop's tokens and its warm-up's.
+    count_warm = max(args.warmup, 32)
+    g = GpuStep(w, count_headroom=args.steps + count_warm)
     for i in range(args.warmup):
         g.step(i)
     torch.cuda.synchronize()
     K = args.steps
     # The timed steps: jf_sample issued back to back from C++ (the engine's
-    # call), HIP events on the launch stream at the ends and after every 25
-    # steps, a device synchronization on both sides. p50/p90 are over the
-    # 25-step runs' mean step times.
-    batch = 25 if K % 25 == 0 else 1
+    # call), HIP events on the launch stream at the loop's two ends only, a
+    # device synchronization on both sides: `value`. Then a second pass of
+    # K steps with an event after every `batch` steps for the distribution
+    # (p50/p90 over those runs' mean step times): an event between steps
+    # adds its own packets to the steps around it.
     wall0 = time.perf_counter()
-    cpp = time_cpp_loop(g, K, False, batch=batch)
+    cpp = time_cpp_loop(g, K, False)
     wall = time.perf_counter() - wall0
-    per = cpp.pop("batch_us").astype(np.float64)
     ms_per_step = cpp["us_per_step"] / 1000.0
+    batch = pick_batch(K)
+    per = time_cpp_loop(g, K, False, batch=batch)["batch_us"].astype(np.float64)
     p50, p90 = float(np.percentile(per, 50)), float(np.percentile(per, 90))
     step_gbs = w["alg_bytes"] / (cpp["us_per_step"] * 1e-6) / 1e9
     # The same steps from a Python loop (ctypes per call), for comparison.
@@ -704,6 +956,11 @@ def main():
     graphed = time_graph(g, K)
     counted = None
     if g.tables:
+        # Warm-up first, untimed: every rotated copy's table takes its first
+        # counts (host copy growth, first touches) here. Each table then
+        # takes at most (warm + K) / tables + 1 <= K + count_warm tokens a
+        # row, the headroom its rows were given.
+        time_cpp_loop(g, max(count_warm, len(g.tables)), True)
         counted = time_cpp_loop(g, K, True)
         counted["note"] = ("each step followed by jf_penalty_table_count_rows of one "
                            "token per row, from C++")
@@ -732,8 +989,9 @@ def main():
         "config": {"workload": w["name"], "rows": w["rows"], "vocabulary": w["V"],
                    "algorithmic_bytes_per_step": w["alg_bytes"]},
         "timing": "jf_sample called back to back from C++ (libjf_bench_loop.so), HIP events "
-                  "on the launch stream at the ends and every 25 steps (p50/p90 over those "
-                  "runs' mean step); host_us_per_call is that loop's own issue time",
+                  "on the launch stream at the loop's two ends (value, ms_per_step); p50/p90 "
+                  f"over the runs of a second pass of {K} steps with an event every {batch} "
+                  "steps; host_us_per_call is the first loop's own issue time",
         "host_us_per_call": cpp["host_us_per_call"],
         "python_loop": python_loop,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,

@@ -232,6 +232,10 @@ struct AcceptChainLane {
   uint32_t sampled;
 };
 
+// Chain acceptance: up to kChainLanesPerLaunch lanes a launch, their
+// records in the kernel arguments (no upload); the pointers start at the
+// launch's first lane.
+constexpr uint32_t kChainLanesPerLaunch = 256;
 struct AcceptChainLaunch {
   uint32_t lanes;
   uint32_t verify_rows;
@@ -243,9 +247,9 @@ struct AcceptChainLaunch {
   uint32_t *target_tokens;
   uint32_t *retained;
   uint32_t *accepted;
-  const AcceptChainLane *lane_params;
   uint32_t stop0;
   uint32_t stop1;
+  AcceptChainLane lane_params[kChainLanesPerLaunch];
 };
 
 struct TreeLaneParams {
@@ -258,10 +262,12 @@ struct TreeLaneParams {
   float chain_q[8];
 };
 
+// Tree acceptance: up to kTreeLanesPerLaunch lanes a launch, their trees in
+// the kernel arguments; the pointers start at the launch's first lane.
+constexpr uint32_t kTreeLanesPerLaunch = 16;
 struct AcceptTreeLaunch {
   uint32_t lanes;
   uint32_t rows_per_lane;
-  const TreeLaneParams *trees;
   const float *target_draft_probs;
   const float *uniforms;
   uint32_t *target_tokens;
@@ -270,6 +276,7 @@ struct AcceptTreeLaunch {
   uint32_t *path_rows;
   uint32_t stop0;
   uint32_t stop1;
+  TreeLaneParams trees[kTreeLanesPerLaunch];
 };
 
 // The draft selector (jf_draft.hip): lane geometry of the reference's DFlash
@@ -360,7 +367,9 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
                        const RowParams *uniform, void *stream,
                        void *start_event = nullptr, void *stop_event = nullptr);
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
-int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream);
+// wide: some cut row of the launch has no min-p floor (longer candidate
+// lists); the merge then fetches more list slots a chunk where that helps.
+int launch_merge_small(const SampleLaunch &a, uint32_t dtype, bool wide, void *stream);
 // Rows with no cut (grid rows x per_row: per_row = chunks when the launch
 // has drafted uncut rows, else 1).
 int launch_uncut(const SampleLaunch &a, uint32_t dtype, uint32_t per_row, void *stream);

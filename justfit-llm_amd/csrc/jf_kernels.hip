@@ -2747,7 +2747,11 @@ __device__ __noinline__ void merge_small_general(uint32_t row) {
 // padding): the hardware preloads them into scalar registers at wave launch.
 // They repeat fields of `a` (drafted_rows is 0 when there are no drafts).
 #if JF_IN(2)
-template <int DT>
+// SPEC: speculatively fetched list slots a thread. 10 gives 128 slots a
+// chunk up to 20 chunks (64 up to 40); 16 gives 128 a chunk up to 32 chunks,
+// for vocabularies past 163,840 tokens whose cut rows have no min-p floor
+// (their lists run past 64 candidates).
+template <int DT, int SPEC>
 __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     const BlockHeader *headers, const uint64_t *cands, const RowParams *params,
     const float *uniforms, const uint32_t *uniform_index, uint32_t S,
@@ -2790,8 +2794,9 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
   // BlockHeader: maximum, count, admitted, overflow | best_value, best_id,
   // floor_key, reserved.
   const u32x4 h0 = ((GlobalU32x4 *)hbase)[0], h1 = ((GlobalU32x4 *)hbase)[1];
-  constexpr int SPEC = 10;
-  const uint32_t pshift = S <= 20 ? 7u : (S <= 40 ? 6u : 5u), P = 1u << pshift;
+  constexpr uint32_t kSlots = SPEC * kThreads;
+  const uint32_t pshift = S * 128u <= kSlots ? 7u : (S * 64u <= kSlots ? 6u : 5u),
+                 P = 1u << pshift;
   uint64_t sv[SPEC];
 #pragma unroll
   for (int k = 0; k < SPEC; ++k) {
@@ -4017,101 +4022,141 @@ __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_
 #endif
 
 // ---- acceptance --------------------------------------------------------
+//
+// One wave per lane. Everything the lane's walk can read goes out in one
+// round of loads (thread t holds row or proposal t); the walk itself then
+// runs on registers: readlane for the current row, a ballot for a child
+// search or for the leading run of accepted proposals. The result is that
+// of the reference's one-thread loops, step for step.
 
-// finish_acceptance (sampling.metal:1381-1392).
-__device__ __forceinline__ void finish(const uint32_t *tokens, uint32_t accepted,
-                                       uint32_t remaining, uint32_t stop0,
-                                       uint32_t stop1, uint32_t *retained,
-                                       uint32_t *accepted_out) {
-  *accepted_out = accepted;
+// finish_acceptance (sampling.metal:1381-1392) on a wave that holds the
+// lane's output token t in thread t: the budget min(accepted + 1,
+// remaining), then cut after the first stop token within it.
+__device__ __forceinline__ uint32_t finish_kept(uint32_t out, uint32_t accepted,
+                                                uint32_t remaining, uint32_t stop0,
+                                                uint32_t stop1) {
+  const uint32_t t = lane_id();
   uint32_t kept = min(accepted + 1, remaining);
-  for (uint32_t i = 0; i < kept; ++i)
-    if (tokens[i] == stop0 || tokens[i] == stop1) {
-      kept = i + 1;
-      break;
-    }
-  *retained = kept;
+  const uint64_t stops = ballot(t < kept && (out == stop0 || out == stop1));
+  if (stops) kept = (uint32_t)__builtin_ctzll(stops) + 1;
+  return kept;
 }
 
-// decode_accept_dflash (sampling.metal:1399-1423, 1514-1558), one thread per
-// lane.
+// decode_accept_dflash (sampling.metal:1399-1423, 1514-1558). Greedy:
+// the leading proposals equal to the target's tokens. Sampled: the leading
+// proposals that pass u q < p (q the draft's probability of the proposal
+// among its 16 candidates, the first that lists it; 0 when none does), each
+// replacing the target's token; a proposal of JF_NO_TOKEN ends the run.
 #if JF_IN(4)
-__global__ void accept_chain_kernel(AcceptChainLaunch a) {
-  const uint32_t lane = blockIdx.x * blockDim.x + threadIdx.x;
-  if (lane >= a.lanes) return;
-  const uint32_t P = a.verify_rows - 1;
+__global__ __launch_bounds__(64) void accept_chain_kernel(AcceptChainLaunch a) {
+  const uint32_t lane = blockIdx.x, t = threadIdx.x;
   const AcceptChainLane lp = a.lane_params[lane];
-  const uint32_t *draft = a.proposed + (uint64_t)lane * P;
-  uint32_t *tokens = a.target_tokens + (uint64_t)lane * a.verify_rows;
-  uint32_t accepted = 0;
+  const uint32_t VR = a.verify_rows, P = VR - 1;
+  uint32_t *tokens = a.target_tokens + (uint64_t)lane * VR;
+  const uint32_t tok = t < VR ? tokens[t] : kNoToken;
+  const uint32_t d = t < P ? a.proposed[(uint64_t)lane * P + t] : kNoToken;
+  bool ok;
   if (lp.sampled) {
-    const uint32_t *ids = a.candidates + (uint64_t)lane * P * 16;
-    const float *probs = a.proposal_probs + (uint64_t)lane * P * 16;
-    const float *p = a.target_draft_probs + (uint64_t)lane * a.verify_rows;
-    const float *u = a.uniforms + (uint64_t)lane * 40;
-    while (accepted < P) {
-      const uint32_t token = draft[accepted];
-      if (token == kNoToken) break;
-      float q = 0.0f;
-      for (int j = 0; j < 16; ++j)
-        if (ids[accepted * 16 + j] == token) {
-          q = probs[accepted * 16 + j];
-          break;
-        }
-      const float uu = u[accepted < 7 ? 8 + accepted : 16 + accepted - 7];
-      if (!(uu * q < p[accepted])) break;
-      tokens[accepted] = token;
-      ++accepted;
+    uint32_t ids[16];
+    float probs[16];
+    float p = 0.0f, u = 0.0f;
+    if (t < P) {
+      const uint64_t c = ((uint64_t)lane * P + t) * 16;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        ids[j] = a.candidates[c + j];
+        probs[j] = a.proposal_probs[c + j];
+      }
+      p = a.target_draft_probs[(uint64_t)lane * VR + t];
+      u = a.uniforms[(uint64_t)lane * 40 + (t < 7 ? 8 + t : 16 + t - 7)];
     }
+    float q = 0.0f;
+    bool seen = false;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bool m = t < P && !seen && ids[j] == d;
+      q = m ? probs[j] : q;
+      seen |= m;
+    }
+    ok = t < P && d != kNoToken && u * q < p;
   } else {
-    while (accepted < P && draft[accepted] == tokens[accepted]) ++accepted;
+    ok = t < P && d == tok;
   }
-  finish(tokens, accepted, lp.remaining, a.stop0, a.stop1, a.retained + lane,
-         a.accepted + lane);
+  // Bit P of ~ballot is set (no thread at or past P is ok): accepted <= P.
+  const uint32_t accepted = (uint32_t)__builtin_ctzll(~ballot(ok));
+  const bool replace = lp.sampled && t < accepted;
+  if (replace) tokens[t] = d;
+  const uint32_t out = replace ? d : tok;
+  const uint32_t kept = finish_kept(out, accepted, lp.remaining, a.stop0, a.stop1);
+  if (t == 0) {
+    a.retained[lane] = kept;
+    a.accepted[lane] = accepted;
+  }
 }
 #endif
 
-// verify_tree_accept (tree.metal:20-84), one thread per lane.
+// verify_tree_accept (tree.metal:20-84). From row 0, while the path is
+// shorter than 8: a sampled lane's chain row (current + 1 < chain_rows)
+// takes its chain child when u[8 + current] q < p; otherwise the lowest row
+// below that is a child of the current row and holds the current row's
+// target token (a sampled lane's chain child excluded) extends the path;
+// none ends it. Each path row emits its child's token, the last row its own
+// target token; the accepted path's rows go to path_rows.
 #if JF_IN(4)
-__global__ void accept_tree_kernel(AcceptTreeLaunch a) {
-  const uint32_t lane = blockIdx.x * blockDim.x + threadIdx.x;
-  if (lane >= a.lanes) return;
+__global__ __launch_bounds__(64) void accept_tree_kernel(AcceptTreeLaunch a) {
+  const uint32_t lane = blockIdx.x, t = threadIdx.x;
   const TreeLaneParams &tr = a.trees[lane];
-  uint32_t *tokens = a.target_tokens + (uint64_t)lane * a.rows_per_lane;
-  const float *p = a.target_draft_probs + (uint64_t)lane * a.rows_per_lane;
-  const float *u = a.uniforms + (uint64_t)lane * 40;
+  const uint32_t R = a.rows_per_lane, rows = tr.rows, chain = tr.chain_rows;
   const bool sampled = tr.sampled != 0;
-  uint32_t path[8];
-  uint32_t length = 1, current = 0;
-  path[0] = 0;
+  uint32_t *tokens = a.target_tokens + (uint64_t)lane * R;
+  const uint32_t tok = t < R ? tokens[t] : kNoToken;
+  float pv = 0.0f, uv = 0.0f;
+  if (sampled) {
+    if (t < R) pv = a.target_draft_probs[(uint64_t)lane * R + t];
+    if (t < 16) uv = a.uniforms[(uint64_t)lane * 40 + 8 + t];
+  }
+  const uint32_t par = t < rows ? tr.parent[t] : kNoToken;
+  const uint32_t dtok = t < rows ? tr.token[t] : kNoToken;
+  uint32_t length = 1, current = 0, path = 0;  // thread i holds path[i]
   while (length < 8) {
-    if (sampled && current + 1 < tr.chain_rows) {
-      if (u[8 + current] * tr.chain_q[current] < p[current]) {
-        path[length++] = current + 1;
-        current = current + 1;
+    if (sampled && current + 1 < chain) {
+      // Rows 0 .. chain - 1 form a chain (checked by the host), so the
+      // chain steps keep current below 7.
+      const float q = tr.chain_q[min(current, 7u)];
+      const float p = __builtin_bit_cast(float, readlane_u32(__builtin_bit_cast(uint32_t, pv),
+                                                             (int)current));
+      const float u = __builtin_bit_cast(float, readlane_u32(__builtin_bit_cast(uint32_t, uv),
+                                                             (int)current));
+      if (u * q < p) {
+        if (t == length) path = current + 1;
+        ++length;
+        ++current;
         continue;
       }
     }
-    const uint32_t wanted = tokens[current];
-    uint32_t found = 0;
-    for (uint32_t r = current + 1; r < tr.rows; ++r)
-      if (tr.parent[r] == current && tr.token[r] == wanted &&
-          !(sampled && r == current + 1 && current + 1 < tr.chain_rows)) {
-        found = r;
-        break;
-      }
-    if (!found) break;
-    path[length++] = found;
-    current = found;
+    const uint32_t wanted = readlane_u32(tok, (int)current);
+    const bool hit = t > current && t < rows && par == current && dtok == wanted &&
+                     !(sampled && t == current + 1 && current + 1 < chain);
+    const uint64_t b = ballot(hit);
+    if (!b) break;
+    current = (uint32_t)__builtin_ctzll(b);
+    if (t == length) path = current;
+    ++length;
   }
-  uint32_t output[8];
-  for (uint32_t i = 0; i < length; ++i)
-    output[i] = i + 1 < length ? tr.token[path[i + 1]] : tokens[path[i]];
-  for (uint32_t i = 0; i < length; ++i) tokens[i] = output[i];
-  finish(tokens, length - 1, tr.remaining, a.stop0, a.stop1, a.retained + lane,
-         a.accepted + lane);
-  for (uint32_t i = 0; i < 8; ++i)
-    a.path_rows[(uint64_t)lane * 8 + i] = i < length ? path[i] : path[length - 1];
+  // Thread i < length: path row i emits its child's token (path[i + 1]) or,
+  // the last, its own target token.
+  const uint32_t next = __shfl_down(path, 1);
+  const uint32_t child_tok = __shfl(dtok, (int)next);
+  const uint32_t own_tok = __shfl(tok, (int)path);
+  const uint32_t out = t + 1 < length ? child_tok : own_tok;
+  if (t < length) tokens[t] = out;
+  const uint32_t kept = finish_kept(out, length - 1, tr.remaining, a.stop0, a.stop1);
+  const uint32_t last = readlane_u32(path, (int)(length - 1));
+  if (t < 8) a.path_rows[(uint64_t)lane * 8 + t] = t < length ? path : last;
+  if (t == 0) {
+    a.retained[lane] = kept;
+    a.accepted[lane] = length - 1;
+  }
 }
 #endif
 
@@ -4240,7 +4285,7 @@ int launch_uncut(const SampleLaunch &a, uint32_t dtype, uint32_t per_row, void *
 #endif
 
 #if JF_IN(2)
-int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream) {
+int launch_merge_small(const SampleLaunch &a, uint32_t dtype, bool wide, void *stream) {
   const dim3 grid(a.rows), block(kThreads);
   const hipStream_t st = (hipStream_t)stream;
   auto go = [&](auto kernel) {
@@ -4249,10 +4294,12 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, void *stream) {
                        (uint32_t)a.uniform_offset, (uint32_t)a.uniform_stride,
                        a.draft_tokens && !a.row_indexed ? a.drafted_rows : 0u, a.row_indexed, a);
   };
+  // The wider fetch only where it adds slots: 21 to 32 chunks.
+  const bool w = wide && a.chunks > 20 && a.chunks <= 32;
   if (dtype == 0)
-    go(merge_small_kernel<0>);
+    w ? go(merge_small_kernel<0, 16>) : go(merge_small_kernel<0, 10>);
   else
-    go(merge_small_kernel<1>);
+    w ? go(merge_small_kernel<1, 16>) : go(merge_small_kernel<1, 10>);
   return (int)hipGetLastError();
 }
 #endif
@@ -4295,7 +4342,7 @@ int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream) {
 
 #if JF_IN(4)
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream) {
-  const dim3 grid((a.lanes + 63) / 64), block(64);
+  const dim3 grid(a.lanes), block(64);
   hipLaunchKernelGGL(accept_chain_kernel, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
@@ -4303,7 +4350,7 @@ int launch_accept_chain(const AcceptChainLaunch &a, void *stream) {
 
 #if JF_IN(4)
 int launch_accept_tree(const AcceptTreeLaunch &a, void *stream) {
-  const dim3 grid((a.lanes + 63) / 64), block(64);
+  const dim3 grid(a.lanes), block(64);
   hipLaunchKernelGGL(accept_tree_kernel, grid, block, 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }

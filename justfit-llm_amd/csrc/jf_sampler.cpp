@@ -214,8 +214,6 @@ struct jf_sampler {
   uint64_t *bests = nullptr;
   jf::RowState *states = nullptr;
   jf::StagePartial *partials = nullptr;
-  jf::AcceptChainLane *chain_lanes = nullptr;
-  jf::TreeLaneParams *tree_lanes = nullptr;
   uint64_t workspace_bytes = 0;
   std::vector<jf::RowParams> last_params;
   std::vector<jf::RowParams> host_params;  // the call's rows, reused across calls
@@ -243,8 +241,6 @@ int jf_sampler_destroy(jf_sampler *s) {
   (void)hipFree(s->bests);
   (void)hipFree(s->states);
   (void)hipFree(s->partials);
-  (void)hipFree(s->chain_lanes);
-  (void)hipFree(s->tree_lanes);
   if (s->status_host) (void)hipHostFree(s->status_host);
   delete s;
   return JF_OK;
@@ -279,8 +275,6 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
   if (rc == JF_OK) rc = device_alloc(&s->bests, blocks, "greedy bests");
   if (rc == JF_OK) rc = device_alloc(&s->states, max_rows, "row states");
   if (rc == JF_OK) rc = device_alloc(&s->partials, blocks, "stage partials");
-  if (rc == JF_OK) rc = device_alloc(&s->chain_lanes, max_rows, "chain lanes");
-  if (rc == JF_OK) rc = device_alloc(&s->tree_lanes, max_rows, "tree lanes");
   if (rc == JF_OK) {
     const hipError_t e =
         hipHostMalloc((void **)&s->status_host, sizeof(uint32_t),
@@ -309,8 +303,7 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
     return rc;
   }
   s->workspace_bytes =
-      max_rows * (sizeof(jf::RowParams) + sizeof(uint32_t) + sizeof(jf::RowState) +
-                  sizeof(jf::AcceptChainLane) + sizeof(jf::TreeLaneParams)) +
+      max_rows * (sizeof(jf::RowParams) + sizeof(uint32_t) + sizeof(jf::RowState)) +
       blocks * (sizeof(jf::BlockHeader) + jf::kBlockCandidates * sizeof(uint64_t) +
                 sizeof(uint64_t) + sizeof(jf::StagePartial));
   *out = s;
@@ -916,14 +909,16 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   // draft probabilities (or none).
   bool small = !staged && !a->draft_q && a->uniform_offset <= 0xffffffffull &&
                a->uniform_stride <= 0xffffffffull;
+  bool wide = false;
   for (uint32_t r = 0; small && r < rows; ++r) {
     const jf::RowParams &rp = params[r];
     if ((rp.flags & jf::kRowSampled) && (rp.flags & kCuts) &&
         !((rp.flags & jf::kRowTopK) && rp.top_k <= 64u) && !(rp.flags & jf::kRowMinP))
       small = false;
+    wide |= (rp.flags & jf::kRowSampled) && (rp.flags & kCuts) && !(rp.flags & jf::kRowMinP);
   }
   if (need_merge) {
-    e = small ? jf::launch_merge_small(L, a->dtype, stream)
+    e = small ? jf::launch_merge_small(L, a->dtype, wide, stream)
               : jf::launch_merge(L, a->dtype, stream);
     if (e != hipSuccess) return hip_fail((hipError_t)e, "merge launch");
   }
@@ -1054,40 +1049,43 @@ int jf_accept_chain(jf_sampler *s, const jf_accept_chain_args *a,
   if (!a->proposed_tokens || !a->target_tokens || !a->retained_counts ||
       !a->accepted_counts)
     return fail(JF_ERR_INVALID_ARGUMENT, "null acceptance buffer");
-  std::vector<jf::AcceptChainLane> lanes(a->lanes);
   bool any_sampled = false;
   for (uint32_t l = 0; l < a->lanes; ++l) {
     const uint32_t m = a->maximum_retained[l];
     if (!m || m > a->verify_rows)
       return fail(JF_ERR_INVALID_ARGUMENT, "invalid DFlash retention limit");
-    lanes[l].remaining = m;
-    lanes[l].sampled = a->policies[l].temperature > 0.0f ? 1u : 0u;
-    any_sampled |= lanes[l].sampled != 0;
+    any_sampled |= a->policies[l].temperature > 0.0f;
   }
   if (any_sampled && (!a->candidates || !a->proposal_probs ||
                       !a->target_draft_probs || !a->uniforms))
     return fail(JF_ERR_INVALID_ARGUMENT, "sampled acceptance needs candidates, "
                                          "probabilities and uniforms");
-  rc = s->staging.upload(s->chain_lanes, lanes.data(),
-                         lanes.size() * sizeof(jf::AcceptChainLane),
-                         (hipStream_t)stream);
-  if (rc != JF_OK) return rc;
-  jf::AcceptChainLaunch L{};
-  L.lanes = a->lanes;
+  // The lanes' records travel in the kernel arguments, kChainLanesPerLaunch
+  // lanes a launch: nothing is uploaded.
+  const uint32_t P = a->verify_rows - 1;
+  jf::AcceptChainLaunch L;
   L.verify_rows = a->verify_rows;
-  L.proposed = a->proposed_tokens;
-  L.candidates = a->candidates;
-  L.proposal_probs = a->proposal_probs;
-  L.target_draft_probs = a->target_draft_probs;
-  L.uniforms = a->uniforms;
-  L.target_tokens = a->target_tokens;
-  L.retained = a->retained_counts;
-  L.accepted = a->accepted_counts;
-  L.lane_params = s->chain_lanes;
   L.stop0 = a->stop_token_0;
   L.stop1 = a->stop_token_1;
-  const int e = jf::launch_accept_chain(L, stream);
-  if (e != hipSuccess) return hip_fail((hipError_t)e, "acceptance launch");
+  for (uint32_t l0 = 0; l0 < a->lanes; l0 += jf::kChainLanesPerLaunch) {
+    const uint32_t n = std::min(a->lanes - l0, jf::kChainLanesPerLaunch);
+    L.lanes = n;
+    L.proposed = a->proposed_tokens + (uint64_t)l0 * P;
+    L.candidates = a->candidates ? a->candidates + (uint64_t)l0 * P * 16 : nullptr;
+    L.proposal_probs = a->proposal_probs ? a->proposal_probs + (uint64_t)l0 * P * 16 : nullptr;
+    L.target_draft_probs =
+        a->target_draft_probs ? a->target_draft_probs + (uint64_t)l0 * a->verify_rows : nullptr;
+    L.uniforms = a->uniforms ? a->uniforms + (uint64_t)l0 * 40 : nullptr;
+    L.target_tokens = a->target_tokens + (uint64_t)l0 * a->verify_rows;
+    L.retained = a->retained_counts + l0;
+    L.accepted = a->accepted_counts + l0;
+    for (uint32_t i = 0; i < n; ++i) {
+      L.lane_params[i].remaining = a->maximum_retained[l0 + i];
+      L.lane_params[i].sampled = a->policies[l0 + i].temperature > 0.0f ? 1u : 0u;
+    }
+    const int e = jf::launch_accept_chain(L, stream);
+    if (e != hipSuccess) return hip_fail((hipError_t)e, "acceptance launch");
+  }
   return JF_OK;
 }
 
@@ -1103,7 +1101,6 @@ int jf_accept_tree(jf_sampler *s, const jf_accept_tree_args *a, void *stream) {
   if (!a->target_tokens || !a->retained_counts || !a->accepted_counts ||
       !a->path_rows)
     return fail(JF_ERR_INVALID_ARGUMENT, "null acceptance buffer");
-  std::vector<jf::TreeLaneParams> lanes(a->lanes);
   bool any_sampled = false;
   for (uint32_t l = 0; l < a->lanes; ++l) {
     const jf_tree_lane &t = a->trees[l];
@@ -1112,40 +1109,50 @@ int jf_accept_tree(jf_sampler *s, const jf_accept_tree_args *a, void *stream) {
     for (uint32_t r = 1; r < t.rows; ++r)
       if (t.parent[r] >= r)
         return fail(JF_ERR_INVALID_ARGUMENT, "draft tree rows are not in DFS preorder");
+    // Rows 0 .. chain_rows - 1 are the draft's sampled chain (each the
+    // previous row's child): the walk reads chain_q at those rows only.
+    for (uint32_t r = 1; r < t.chain_rows; ++r)
+      if (t.parent[r] != r - 1)
+        return fail(JF_ERR_INVALID_ARGUMENT, "draft tree chain rows do not form a chain");
     const uint32_t m = a->maximum_retained[l];
     if (!m || m > JF_TREE_MAXIMUM_DEPTH)
       return fail(JF_ERR_INVALID_ARGUMENT, "invalid tree retention limit");
-    jf::TreeLaneParams &p = lanes[l];
-    p.rows = t.rows;
-    p.chain_rows = t.chain_rows;
-    p.remaining = m;
-    p.sampled = a->policies[l].temperature > 0.0f ? 1u : 0u;
-    any_sampled |= p.sampled != 0;
-    std::memcpy(p.parent, t.parent, sizeof(p.parent));
-    std::memcpy(p.token, t.token, sizeof(p.token));
-    std::memcpy(p.chain_q, t.chain_q, sizeof(p.chain_q));
+    any_sampled |= a->policies[l].temperature > 0.0f;
   }
   if (any_sampled && (!a->target_draft_probs || !a->uniforms))
     return fail(JF_ERR_INVALID_ARGUMENT,
                 "sampled tree acceptance needs probabilities and uniforms");
-  rc = s->staging.upload(s->tree_lanes, lanes.data(),
-                         lanes.size() * sizeof(jf::TreeLaneParams),
-                         (hipStream_t)stream);
-  if (rc != JF_OK) return rc;
-  jf::AcceptTreeLaunch L{};
-  L.lanes = a->lanes;
-  L.rows_per_lane = a->rows_per_lane;
-  L.trees = s->tree_lanes;
-  L.target_draft_probs = a->target_draft_probs;
-  L.uniforms = a->uniforms;
-  L.target_tokens = a->target_tokens;
-  L.retained = a->retained_counts;
-  L.accepted = a->accepted_counts;
-  L.path_rows = a->path_rows;
+  // The lanes' trees travel in the kernel arguments, kTreeLanesPerLaunch
+  // lanes a launch: nothing is uploaded.
+  const uint32_t R = a->rows_per_lane;
+  jf::AcceptTreeLaunch L;
+  L.rows_per_lane = R;
   L.stop0 = a->stop_token_0;
   L.stop1 = a->stop_token_1;
-  const int e = jf::launch_accept_tree(L, stream);
-  if (e != hipSuccess) return hip_fail((hipError_t)e, "tree acceptance launch");
+  for (uint32_t l0 = 0; l0 < a->lanes; l0 += jf::kTreeLanesPerLaunch) {
+    const uint32_t n = std::min(a->lanes - l0, jf::kTreeLanesPerLaunch);
+    L.lanes = n;
+    L.target_draft_probs =
+        a->target_draft_probs ? a->target_draft_probs + (uint64_t)l0 * R : nullptr;
+    L.uniforms = a->uniforms ? a->uniforms + (uint64_t)l0 * 40 : nullptr;
+    L.target_tokens = a->target_tokens + (uint64_t)l0 * R;
+    L.retained = a->retained_counts + l0;
+    L.accepted = a->accepted_counts + l0;
+    L.path_rows = a->path_rows + (uint64_t)l0 * 8;
+    for (uint32_t i = 0; i < n; ++i) {
+      const jf_tree_lane &t = a->trees[l0 + i];
+      jf::TreeLaneParams &p = L.trees[i];
+      p.rows = t.rows;
+      p.chain_rows = t.chain_rows;
+      p.remaining = a->maximum_retained[l0 + i];
+      p.sampled = a->policies[l0 + i].temperature > 0.0f ? 1u : 0u;
+      std::memcpy(p.parent, t.parent, sizeof(p.parent));
+      std::memcpy(p.token, t.token, sizeof(p.token));
+      std::memcpy(p.chain_q, t.chain_q, sizeof(p.chain_q));
+    }
+    const int e = jf::launch_accept_tree(L, stream);
+    if (e != hipSuccess) return hip_fail((hipError_t)e, "tree acceptance launch");
+  }
   return JF_OK;
 }
 

@@ -422,10 +422,11 @@ class Sampler:
         check(lib().jf_sample(self.handle, ctypes.byref(a),
                               _stream() if stream is None else stream))
 
-    def accept_chain(self, *, verify_rows, proposed, target_tokens, retained,
-                     accepted, maximum_retained, policies, candidates=None,
-                     proposal_probs=None, target_draft_probs=None,
-                     uniforms=None, stop_tokens=(JF_NO_TOKEN, JF_NO_TOKEN)):
+    def accept_chain_args(self, *, verify_rows, proposed, target_tokens, retained,
+                          accepted, maximum_retained, policies, candidates=None,
+                          proposal_probs=None, target_draft_probs=None,
+                          uniforms=None, stop_tokens=(JF_NO_TOKEN, JF_NO_TOKEN)):
+        """Builds a JfAcceptChainArgs (kept-alive host arrays ride along)."""
         lanes = len(maximum_retained)
         a = JfAcceptChainArgs()
         a.lanes = lanes
@@ -444,12 +445,22 @@ class Sampler:
         a.maximum_retained = mr
         a.policies = pol
         a.stop_token_0, a.stop_token_1 = stop_tokens
+        return a, [mr, pol]
+
+    def launch_accept(self, acc, stream=None):
+        """Issues a prepared acceptance: ("chain" | "tree", args, keep)."""
+        fn = lib().jf_accept_chain if acc[0] == "chain" else lib().jf_accept_tree
+        check(fn(self.handle, ctypes.byref(acc[1]), _stream() if stream is None else stream))
+
+    def accept_chain(self, **kwargs):
+        a, keep = self.accept_chain_args(**kwargs)
         check(lib().jf_accept_chain(self.handle, ctypes.byref(a), _stream()))
 
-    def accept_tree(self, *, trees, rows_per_lane, target_tokens, retained,
-                    accepted, path_rows, maximum_retained, policies,
-                    target_draft_probs=None, uniforms=None,
-                    stop_tokens=(JF_NO_TOKEN, JF_NO_TOKEN)):
+    def accept_tree_args(self, *, trees, rows_per_lane, target_tokens, retained,
+                         accepted, path_rows, maximum_retained, policies,
+                         target_draft_probs=None, uniforms=None,
+                         stop_tokens=(JF_NO_TOKEN, JF_NO_TOKEN)):
+        """Builds a JfAcceptTreeArgs (kept-alive host arrays ride along)."""
         lanes = len(trees)
         a = JfAcceptTreeArgs()
         a.lanes = lanes
@@ -468,6 +479,10 @@ class Sampler:
         a.maximum_retained = mr
         a.policies = pol
         a.stop_token_0, a.stop_token_1 = stop_tokens
+        return a, [tl, mr, pol]
+
+    def accept_tree(self, **kwargs):
+        a, keep = self.accept_tree_args(**kwargs)
         check(lib().jf_accept_tree(self.handle, ctypes.byref(a), _stream()))
 
     def close(self):

@@ -22,6 +22,19 @@ C4 tree        16 requests x 16-row DFS-preorder trees, branching U{1..3},
 C5 large       B=256, V=248,320 bf16 = 3 N(0,1) + t(3) (seed 5); repetition
                1.1, presence 0.5, frequency 0.3 over 8,192 ids (first 4,096
                prompt); min-p 0.05, top-k 1000, top-p 0.95, T 0.8.
+verify         The engine's penalized chain verify (Sampling::addVerify,
+               Sampling.cpp:149-172; penalize_verify, sampling.metal:978-993)
+               at the reference's widest batch: 4 lanes x 16 verify rows of
+               V=248,320 fp32 ~ N(0, 2.5^2) plus 8.0 at 8 ids per row (seed 8);
+               each lane's 16 input tokens (the anchor, then 15 proposals,
+               each proposal +14.0 in the row that verifies it); row r follows
+               proposal r + 1 (rows 0..14) with 16 sparse candidates (0.6 on
+               the proposal, Dirichlet(0.5) over the rest), counts
+               the lane's proposals 1..r as extra penalty tokens, and draws
+               with the lane's correction uniform (slot 15 of 40); T 0.7,
+               top-k 50, top-p 0.9, repetition 1.1, presence 0.5, frequency
+               0.3 over 2,048-id histories (the first 1,024 prompt); then
+               chain acceptance (verify rows 16, all 16 retainable).
 """
 import numpy as np
 
@@ -206,3 +219,59 @@ def config_draft(V=V_QWEN, lanes=4, seed=6):
     uniforms = rng.random((lanes, 40)).astype(np.float32)
     return dict(V=V, lanes=lanes, logits=logits, hidden=hidden, pred=pred, succ=succ,
                 anchors=anchors, temperatures=temperatures, uniforms=uniforms)
+
+
+def config_verify(V=V_LARGE, lanes=4, rows=16, H=2048):
+    """The penalized chain-verify step (see the module docstring): host
+    arrays in the row-indexed form of jf_sample_args (per-row draft token,
+    candidate row and extra-token offset) and the acceptance inputs."""
+    rng = np.random.default_rng(8)
+    B = lanes * rows
+    logits = rng.normal(0.0, 2.5, (B, V)).astype(np.float32)
+    for g in range(B):
+        logits[g, rng.choice(V, 8, replace=False)] += np.float32(8.0)
+    # inputs[l * rows + i]: the lane's input i (0 the anchor, 1..15 proposals).
+    inputs = rng.integers(0, V, B, dtype=np.int64).astype(np.uint32)
+    for l in range(lanes):
+        for r in range(rows - 1):
+            logits[l * rows + r, inputs[l * rows + r + 1]] += np.float32(14.0)
+    # Per row g = l * rows + r: its draft token inputs[g + 1] (rows 0..14),
+    # its 16 candidates at row l * (rows - 1) + r of the lanes' candidate
+    # array (the layout chain acceptance reads), its extra penalty tokens
+    # inputs[l * rows + 1 ..][:r].
+    P = rows - 1
+    draft_index = np.full(B, NO_TOKEN, np.uint32)
+    cand_index = np.zeros(B, np.uint32)
+    extra_offsets = np.zeros(B, np.uint64)
+    extra_counts = np.zeros(B, np.uint32)
+    for l in range(lanes):
+        for r in range(rows):
+            g = l * rows + r
+            if r < P:
+                draft_index[g] = g + 1
+                cand_index[g] = l * P + r
+            extra_offsets[g] = l * rows + 1
+            extra_counts[g] = r
+    cand = rng.integers(0, V, (lanes * P, 16), dtype=np.int64).astype(np.uint32)
+    for l in range(lanes):
+        cand[l * P:(l + 1) * P, 0] = inputs[l * rows + 1:(l + 1) * rows]
+    # The draft put about 0.6 on its proposal, the rest on the other 15.
+    cprob = np.empty((lanes * P, 16), np.float32)
+    cprob[:, 0] = np.float32(0.6)
+    cprob[:, 1:] = (0.4 * rng.dirichlet(np.ones(15) * 0.5, lanes * P)).astype(np.float32)
+    hist = rng.integers(0, V, (lanes, H), dtype=np.int64).astype(np.uint32)
+    uniforms = np.zeros((lanes, 40), np.float32)
+    for l in range(lanes):
+        for slot in range(1, 40):
+            uniforms[l, slot] = splitmix_uniform(row_seed(8, l), slot - 1)
+    uniform_index = np.array([l * 40 + 15 for l in range(lanes) for _ in range(rows)],
+                             np.uint32)
+    return dict(V=V, lanes=lanes, rows=rows, logits=logits, inputs=inputs,
+                draft_index=draft_index, cand_index=cand_index, cand_ids=cand,
+                cand_probs=cprob,
+                extra_offsets=extra_offsets, extra_counts=extra_counts,
+                histories=list(hist), generated=[H // 2] * lanes, uniforms=uniforms,
+                uniform_index=uniform_index,
+                policy=dict(temperature=0.7, top_k=50, top_p=0.9, repetition=1.1,
+                            presence=0.5, frequency=0.3),
+                mark_prompt=True)

@@ -1,11 +1,15 @@
-"""The calls bench.py times, checked at full size: bench.GpuStep builds the
-same device inputs, penalty tables and argument records as the timed loop,
-and one of its steps is compared with the oracle row by row (bit-exact
-tokens, and the draft probabilities where the step writes them). C2 and C5
-run as benchmarked, without kept outputs or draft probabilities; C1, C3 and
-C4 greedy and sampled as the bench issues them; C2 also with histories
-clustered in low ids (every row, and every fourth row), which widen the
-penalty table's fixed slots from 256 to 512 a chunk."""
+"""The calls bench.py times, checked at full size: bench.GpuStep and
+bench.VerifyStep build the same device inputs, penalty tables and argument
+records as the timed loop, and one of their steps is compared with the
+oracle row by row (bit-exact tokens, and the draft probabilities where the
+step writes them). C2 and C5 run as benchmarked, without kept outputs or
+draft probabilities; C1, C3 and C4 greedy and sampled as the bench issues
+them, C4's selection and then its tree acceptance (retained and accepted
+counts, path rows, the accepted tokens); C2 also with histories clustered
+in low ids (every row, and every fourth row), which widen the penalty
+table's fixed slots from 256 to 512 a chunk; and the penalized chain-verify
+step (4 lanes x 16 rows, V = 248,320: extras, sparse drafts, then chain
+acceptance)."""
 import numpy as np
 import pytest
 
@@ -56,12 +60,14 @@ def test_benchmarked_step_matches_oracle(cfg, mode, history):
     g = bench.GpuStep(w)
     for i in (0, len(g.kw) - 1):  # the first and last rotated copy
         g.out.fill_(-1)
-        g.step(i)
+        g.sampler.launch(g.kw[i][0])  # the step's selection
         torch.cuda.synchronize()
         got = g.out.cpu().numpy().view(np.uint32).copy()
         want = _oracle_for(w) if i == 0 else want
         np.testing.assert_array_equal(got, want["tokens"])
         assert np.all(got != NO)
+        if g.accept is not None:
+            _check_tree_acceptance(g, w, want)
         if g.draft_probs is not None:
             c = w["tree"]
             drafted = np.array([r < WL.chain_length(c["trees"][k]) - 1
@@ -71,3 +77,94 @@ def test_benchmarked_step_matches_oracle(cfg, mode, history):
             np.testing.assert_array_equal(dp[drafted], want["draft_probs"][drafted])
     del g
     torch.cuda.empty_cache()
+
+
+def _check_tree_acceptance(g, w, want):
+    """The rest of C4's step: jf_accept_tree over the selected tokens, against
+    the oracle's walk of each request's tree."""
+    import torch
+    import oracle as O
+    c = w["tree"]
+    rq = len(c["trees"])
+    per = w["rows"] // rq
+    g.sampler.launch_accept(g.accept)
+    torch.cuda.synchronize()
+    tt = g.out.cpu().numpy().view(np.uint32).reshape(rq, per)
+    ret = g.acc_out[0].cpu().numpy()
+    acc = g.acc_out[1].cpu().numpy()
+    path = g.acc_path.cpu().numpy().view(np.uint32)
+    for k in range(rq):
+        tree = g.acc_trees[k]
+        sampled = bool(w.get("sampled"))
+        wt, wr, wa, wp = O.accept_tree(
+            c["trees"][k], c["tokens"][k], tree.chain_rows if sampled else 0,
+            list(tree.chain_q)[:8] if sampled else None, 8, sampled,
+            want["tokens"][k * per:(k + 1) * per],
+            want["draft_probs"][k * per:(k + 1) * per] if sampled else None,
+            c["uniforms"][k] if sampled else None)
+        assert ret[k] == wr and acc[k] == wa, (k, ret[k], wr, acc[k], wa)
+        np.testing.assert_array_equal(path[k], wp)
+        np.testing.assert_array_equal(tt[k, :wr], wt[:wr])
+
+
+def test_benchmarked_verify_step_matches_oracle():
+    import torch
+    import oracle as O
+    c = WL.config_verify()
+    g = bench.VerifyStep(c)
+    V, lanes, rows = c["V"], c["lanes"], c["rows"]
+    print(f"bench call: {g.w['name']}", flush=True)
+    vt, vp, chains = bench_oracle_verify(c)
+    for i in (0, len(g.kw) - 1):
+        g.out.fill_(-1)
+        g.sampler.launch(g.kw[i][0])
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(g.out.cpu().numpy().view(np.uint32), vt)
+        dp = g.draft_probs.cpu().numpy()
+        drafted = c["draft_index"] != NO
+        np.testing.assert_array_equal(dp[drafted], vp[drafted])
+        g.sampler.launch_accept(g.accept)
+        torch.cuda.synchronize()
+        tt = g.out.cpu().numpy().view(np.uint32).reshape(lanes, rows)
+        ret, acc = g.retained.cpu().numpy(), g.accepted.cpu().numpy()
+        for l, (wt, wr, wa) in enumerate(chains):
+            assert ret[l] == wr and acc[l] == wa, (l, ret[l], wr, acc[l], wa)
+            np.testing.assert_array_equal(tt[l, :wr], wt[:wr])
+    assert max(a for _, _, a in chains) >= 1  # some proposals are accepted
+    g.close()
+    del g
+    torch.cuda.empty_cache()
+
+
+def bench_oracle_verify(c):
+    """The oracle's verify step: every row's selection, then each lane's chain
+    acceptance (the same calls as bench.verify_cpu_baseline)."""
+    import oracle as O
+    V, lanes, rows = c["V"], c["lanes"], c["rows"]
+    pol = O.policy(**c["policy"])
+    inp = c["inputs"]
+    vt = np.zeros(lanes * rows, np.uint32)
+    vp = np.zeros(lanes * rows, np.float32)
+    for l in range(lanes):
+        words = O.rebuild_penalty_words(V, c["histories"][l], c["generated"][l], None,
+                                        c["mark_prompt"])[1]
+        for r in range(rows):
+            g = l * rows + r
+            d = int(c["draft_index"][g])
+            ci = int(c["cand_index"][g])
+            vt[g], vp[g] = O.select_row(
+                V, pol, logits=c["logits"][g], words=words,
+                extra=inp[l * rows + 1:l * rows + 1 + r], uniform=float(c["uniforms"][l, 15]),
+                draft_token=int(inp[d]) if d != NO else NO,
+                cand_ids=c["cand_ids"][ci] if d != NO else None,
+                cand_probs=c["cand_probs"][ci] if d != NO else None)[:2]
+    chains = []
+    P = rows - 1
+    for l in range(lanes):
+        chains.append(O.accept_chain(P, rows, True, inp[l * rows + 1:(l + 1) * rows],
+                                     vt[l * rows:(l + 1) * rows],
+                                     cand_ids=c["cand_ids"][l * P:(l + 1) * P],
+                                     cand_probs=c["cand_probs"][l * P:(l + 1) * P],
+                                     target_draft_prob=vp[l * rows:(l + 1) * rows],
+                                     uniforms40=c["uniforms"][l]))
+    return vt, vp, chains
