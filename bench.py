@@ -417,6 +417,22 @@ def time_cpp_loop(g, steps, with_counts, batch=0):
     return out
 
 
+def host_issue_us(g, bursts=20, per=16):
+    """The host's own cost of issuing one step: bursts of `per` steps from
+    C++, each started on an idle stream, timed on the host only. A burst
+    stays far below the depth of the device queue, so no call waits for the
+    GPU (in a long loop the host runs ahead until the queue is full and then
+    issues at the GPU's pace, which the long loop's host time shows).
+    Returns the median over the bursts, in microseconds per step."""
+    import torch
+    vals = []
+    for _ in range(bursts):
+        torch.cuda.synchronize()
+        vals.append(time_cpp_loop(g, per, False)["host_us_per_call"])
+    torch.cuda.synchronize()
+    return float(np.median(vals))
+
+
 def pick_batch(steps):
     """Steps per timed run for the step-time distribution: the largest
     divisor of `steps` up to 25 that leaves at least four runs, else at least
@@ -825,8 +841,9 @@ def verify_cpu_baseline(c, seconds):
 
 def bench_verify(args):
     """The penalized chain-verify shape (VerifyStep): its step timed from
-    C++ as the sample path's is, its dominant kernel (select_kernel: rows
-    with extra verify tokens take the general single pass) timed alone."""
+    C++ as the sample path's is, its dominant kernel (the single pass with
+    the verify rows' extra penalty tokens, select_fast_kernel<0, true>)
+    timed alone."""
     import torch
     from jf_sampler import workloads as WL
     c = WL.config_verify()
@@ -852,7 +869,7 @@ def bench_verify(args):
     step_bytes = sel_bytes + B * 4 * 3 + c["lanes"] * (c["rows"] - 1) * (4 + 16 * 8)
     achieved = sel_bytes / (sel_mean * 1e-6) / 1e9
     step_gbs = step_bytes / (cpp["us_per_step"] * 1e-6) / 1e9
-    kernel = "jf::select_kernel<0>"
+    kernel = "jf::select_fast_kernel<0, true>"
     key = ("verify", "auto")
     traffic = read_traffic(key, kernel)
     prof_us = read_profile_us(key, kernel)
@@ -872,6 +889,7 @@ def bench_verify(args):
         "timing": f"jf_sample + jf_accept_chain back to back from C++, events at the loop's "
                   f"two ends; p50/p90 over runs of {batch} steps in a second pass",
         "host_us_per_call": cpp["host_us_per_call"],
+        "host_issue_us": host_issue_us(g),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "kernel": kernel,
                      "timing": "mean of HIP events the library records around the kernel's "
@@ -965,7 +983,7 @@ def main():
         counted["note"] = ("each step followed by jf_penalty_table_count_rows of one "
                            "token per row, from C++")
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
-    kernel = w.get("kernel", f"jf::select_fast_kernel<{0 if w['dtype'] == 'f32' else 1}>")
+    kernel = w.get("kernel", f"jf::select_fast_kernel<{0 if w['dtype'] == 'f32' else 1}, false>")
     key = profile_key(args.config, args.mode, args.history)
     traffic = read_traffic(key, kernel)
     prof_us = read_profile_us(key, kernel)
@@ -991,8 +1009,11 @@ def main():
         "timing": "jf_sample called back to back from C++ (libjf_bench_loop.so), HIP events "
                   "on the launch stream at the loop's two ends (value, ms_per_step); p50/p90 "
                   f"over the runs of a second pass of {K} steps with an event every {batch} "
-                  "steps; host_us_per_call is the first loop's own issue time",
+                  "steps; host_us_per_call is the first loop's own issue time (paced by the "
+                  "GPU once the device queue is full); host_issue_us is the median host cost "
+                  "of a step in 16-step bursts issued to an idle stream",
         "host_us_per_call": cpp["host_us_per_call"],
+        "host_issue_us": host_issue_us(g),
         "python_loop": python_loop,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,

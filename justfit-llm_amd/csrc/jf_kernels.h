@@ -177,7 +177,12 @@ struct FastLaunch {
                               // the kernel takes it as a preloaded argument)
   uint32_t row_info[kKernargRows];  // RowFlags | penalty row << 8
   uint32_t row_of[kKernargRows];
+  // Launches whose rows carry extra (verify) penalty tokens: the row's
+  // extras are SampleLaunch::extra + (this & kExtraOffsetMask), this >> 27
+  // of them (<= kMaxExtra).
+  uint32_t row_extra[kKernargRows];
 };
+constexpr uint32_t kExtraOffsetMask = (1u << 27) - 1u;
 
 // Multi-pass stages, in launch order.
 enum Stage : uint32_t {
@@ -363,8 +368,9 @@ int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
                   void *start_event = nullptr, void *stop_event = nullptr);
 // `uniform`: when every row of the launch has this policy and penalty table
 // row == its own row, or NULL.
+// extras: some row of the launch has extra penalty tokens (row_extra).
 int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
-                       const RowParams *uniform, void *stream,
+                       const RowParams *uniform, bool extras, void *stream,
                        void *start_event = nullptr, void *stop_event = nullptr);
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
 // wide: some cut row of the launch has no min-p floor (longer candidate

@@ -2042,6 +2042,7 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
 
 struct __align__(16) FastLds {
   uint32_t bm[kThreads];  // bit i of bm[t]: register i of thread t is dropped
+  uint32_t xt[kMaxExtra];  // the row's extra penalty tokens (XTRA launches)
   uint64_t stage[kWaves][kWaveCandidates];
   uint64_t slices[kWaves * 8];  // an uncut row's slice masses
   uint32_t wcount[kWaves];
@@ -2225,7 +2226,9 @@ __device__ __forceinline__ void finish_greedy_row(const SampleLaunch &a, uint32_
   if (lane == 0) write_result(a, row, key ? 0x7ffffu - (low >> 13) : kNoToken, 0.0f, 0);
 }
 
-template <int DT>
+// XTRA: the launch's rows may carry extra (verify) penalty tokens, read as
+// scalars from f.row_extra's place in SampleLaunch::extra.
+template <int DT, bool XTRA>
 __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     const void *logits, const uint32_t *pen_slots, uint32_t stride, uint32_t V,
     uint32_t packed, uint32_t u_top_k, float u_minp_offset, float u_repetition,
@@ -2265,6 +2268,16 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
       if (k * kThreads < (int)slot_count) slot[k] = sp[tid + k * kThreads];
     s.bm[tid] = 0;
   }
+  // A verify row's extra penalty tokens (penalize_verify, sampling.metal:
+  // 978-993: row r counts the draft tokens 1..r): up to 16, lane e of each
+  // wave loading extra e, requested with the slots (before the logits) and
+  // staged in LDS before the first barrier.
+  uint32_t xtok = kNoToken;
+  if constexpr (XTRA) {
+    const uint32_t xr = f.row_extra[lrow];
+    const uint32_t nx = penalized ? xr >> 27 : 0u;
+    if (tid < nx) xtok = a.extra[(xr & kExtraOffsetMask) + tid];
+  }
   float xs[TPL];
   std::conditional_t<DT == 0, float, uint32_t> tail[VEC];
   uint32_t tail_j;
@@ -2279,7 +2292,10 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
       mw[j] = t0 < V ? mrow[t0 >> 5] : 0u;
     }
   }
-  if (penalized) __syncthreads();  // drop bitmaps cleared
+  if constexpr (XTRA) {
+    if (tid < kMaxExtra) s.xt[tid] = xtok;
+  }
+  if (penalized) __syncthreads();  // drop bitmaps cleared (and extras staged)
   // A non-uniform row's policy by scalar loads issued after that barrier
   // (a barrier waits for every outstanding scalar load); their wait sits at
   // the first use.
@@ -2304,7 +2320,8 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   // 2. Penalized tokens: recorded in the drop bitmaps, re-read by their
   // slot's thread, penalized there (sampling.metal:928-963) and admitted
   // (sampling.metal:33-37).
-  uint32_t drop = 0;
+  uint32_t drop = 0, slot_drop = 0;
+  uint32_t xin = 0, xmine = kNoToken, xcnt = 0;  // this chunk's extras (XTRA launches)
   SideEntries side;
 #pragma unroll
   for (int k = 0; k < SPT; ++k) {
@@ -2330,12 +2347,33 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     }
     __syncthreads();  // bitmaps complete
     drop = s.bm[tid];
+    slot_drop = drop;
     rp = row_policy();
+    if constexpr (XTRA) {
+      // Lane e < 16 of every wave: extra e, whether it lies in this chunk and
+      // is the first of its equal ones (bit e of xin, the same in every
+      // wave), and how many of the row's extras equal it (xcnt).
+      const uint32_t le = lane & (kMaxExtra - 1);
+      xmine = s.xt[le];
+      bool first = lane < kMaxExtra && xmine - base < CHUNK && xmine < V;
+      for (uint32_t e2 = 0; e2 < (uint32_t)kMaxExtra; ++e2) {
+        const uint32_t o2 = s.xt[e2];
+        xcnt += o2 == xmine ? 1u : 0u;
+        first = first && !(e2 < le && o2 == xmine);
+      }
+      xin = (uint32_t)ballot(first);
+    }
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
       if (slot[k]) {
         const uint32_t o = slot[k] >> kSlotOffsetShift, t = base + o;
-        const uint32_t count = slot[k] & kSlotCountMask;
+        uint32_t count = slot[k] & kSlotCountMask;
+        if constexpr (XTRA) {
+          for (uint32_t bits = xin; bits; bits &= bits - 1) {
+            const int e = __builtin_ctz(bits);
+            count += readlane_u32(xmine, e) == t ? readlane_u32(xcnt, e) : 0u;
+          }
+        }
         const float x = DT == 0 ? u2f(raw[k]) : bf16_to_float(raw[k]);
         float v = penalize(x, count, rp.repetition, rp.repetition_inverse,
                            rp.presence, rp.frequency);
@@ -2376,6 +2414,24 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
         for (int e = 0; e < VEC; ++e)
           xs[j * VEC + e] = (uint32_t)j == tail_j ? (DT == 0 ? (float)tail[e] : bf16_to_float((uint32_t)tail[e]))
                                                   : xs[j * VEC + e];
+  }
+  if constexpr (XTRA) {
+    // An extra token with no fixed slot in this chunk holds no table entry
+    // (a row on this kernel has every entry in a slot): its penalty is its
+    // extras' count alone (sampling.metal:941-963), applied in place by the
+    // thread that loaded it.
+    for (uint32_t bits = xin; bits; bits &= bits - 1) {
+      const int e = __builtin_ctz(bits);
+      const uint32_t o = readlane_u32(xmine, e) - base, reg = register_of<DT>(o);
+      float xv = 0.0f;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) xv = (uint32_t)i == reg ? xs[i] : xv;
+      const float pv = penalize(xv, readlane_u32(xcnt, e), rp.repetition, rp.repetition_inverse,
+                                rp.presence, rp.frequency);
+      const bool mine = tid == owner_of<DT>(o) && !((slot_drop >> reg) & 1u);
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) xs[i] = mine && (uint32_t)i == reg ? pv : xs[i];
+    }
   }
   if (penalized || constrained || stop_here || !full) {
     // A dropped register becomes NaN: its exponent bits and quiet bit set.
@@ -2854,12 +2910,24 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
   // The chunk summaries (wave 0): the row maximum, admission, overflow, the
   // top-k floor (the K-th key is at least every chunk's floor) and the
   // longest list.
+  // Also each chunk's offset among the candidates of the chunks whose
+  // maximum reaches the row's threshold (hoff; the others hold none at or
+  // above it), for a compact refetch.
   if (tid < 64) {
     const float mx = wave_max_f32(hmax);
     const uint32_t adm = wave_max_u32(hadm), ovf = wave_max_u32(hovf),
                    flr = wave_max_u32(hfloor), hcmax = wave_max_u32(hcount);
-    if (tid < S) s.hcnt[tid] = hcount;
+    const uint32_t wthr =
+        max((prec.flags & kRowMinP) ? logit_key(__builtin_fminf(mx + prec.minp_offset, mx)) : 0u,
+            flr);
+    const bool use = hv && logit_key(hmax) >= wthr;
+    const uint32_t incl = wave_incl_scan_u32(use ? hcount : 0u);
+    if (tid < S) {
+      s.hcnt[tid] = hcount;
+      s.hoff[tid + 1] = incl;
+    }
     if (tid == 0) {
+      s.hoff[0] = 0;
       s.row_max = mx;
       s.row_admitted = adm;
       s.row_overflow = ovf;
@@ -2882,12 +2950,42 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
                      : 0u;
   thr = max(thr, s.row_floor);
   const uint32_t K = rp.top_k;
-  if (!s.row_overflow && s.row_maxcount <= P && thr > kLowestKey) {
+  const uint32_t n_all = s.hoff[S];
+  if (!s.row_overflow && thr > kLowestKey && (s.row_maxcount <= P || n_all <= kSlots)) {
     uint32_t valid = 0;
+    if (s.row_maxcount <= P) {
 #pragma unroll
-    for (int k = 0; k < SPEC; ++k) {
-      const uint32_t i = tid + k * kThreads, c = i >> pshift;
-      if (c < S && (i & (P - 1)) < s.hcnt[c] && (uint32_t)sv[k] >= thr) valid |= 1u << k;
+      for (int k = 0; k < SPEC; ++k) {
+        const uint32_t i = tid + k * kThreads, c = i >> pshift;
+        if (c < S && (i & (P - 1)) < s.hcnt[c] && (uint32_t)sv[k] >= thr) valid |= 1u << k;
+      }
+    } else {
+      // A list longer than its fetched slots, but every candidate at or
+      // above the threshold fits the registers: item i = tid + k * threads
+      // of the chunks that reach the threshold, its chunk the last c with
+      // hoff[c] <= i (binary searches, all items at once), fetched now.
+      uint32_t cc[SPEC];
+#pragma unroll
+      for (int k = 0; k < SPEC; ++k) cc[k] = 0;
+      for (uint32_t step = kMaxChunks / 2; step; step >>= 1) {
+#pragma unroll
+        for (int k = 0; k < SPEC; ++k) {
+          const uint32_t i = tid + k * kThreads;
+          if (cc[k] + step < S && s.hoff[cc[k] + step] <= i) cc[k] += step;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < SPEC; ++k) {
+        const uint32_t i = tid + k * kThreads;
+        sv[k] = i < n_all ? ((GlobalU64 *)cbase)[(uint64_t)cc[k] * kBlockCandidates +
+                                                 (i - s.hoff[cc[k]])]
+                          : 0ull;
+      }
+#pragma unroll
+      for (int k = 0; k < SPEC; ++k) {
+        const uint32_t i = tid + k * kThreads;
+        if (i < n_all && (uint32_t)sv[k] >= thr) valid |= 1u << k;
+      }
     }
     const int got = rank_select(sv, valid, thr, K, maximum, s);
     if (got >= 0) {
@@ -4197,10 +4295,11 @@ static uint32_t fast_resident_blocks(uint32_t dtype) {
   if (!known[dev][dtype]) {
     int per_cu = 0, cus = 0;
     const hipError_t e1 =
-        dtype == 0 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, select_fast_kernel<0>,
-                                                                  kThreads, 0)
-                   : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, select_fast_kernel<1>,
-                                                                  kThreads, 0);
+        dtype == 0
+            ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, select_fast_kernel<0, false>,
+                                                           kThreads, 0)
+            : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, select_fast_kernel<1, false>,
+                                                           kThreads, 0);
     const hipError_t e2 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     cache[dev][dtype] = e1 == hipSuccess && e2 == hipSuccess && per_cu > 0 && cus > 0
                             ? (uint32_t)per_cu * (uint32_t)cus
@@ -4211,7 +4310,7 @@ static uint32_t fast_resident_blocks(uint32_t dtype) {
 }
 
 int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
-                       const RowParams *uniform, void *stream, void *start_event,
+                       const RowParams *uniform, bool extras, void *stream, void *start_event,
                        void *stop_event) {
   if (f.fuse_greedy == 1u && f.a.chunks > 1 && rows < fast_resident_blocks(dtype)) {
     // Each row's last chunk can wait for the row's other blocks instead of
@@ -4220,7 +4319,7 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
     // slot always remains for the blocks they wait for, which never wait.
     FastLaunch g = f;
     g.fuse_greedy = 2u;
-    return launch_select_fast(g, rows, dtype, uniform, stream, start_event, stop_event);
+    return launch_select_fast(g, rows, dtype, uniform, extras, stream, start_event, stop_event);
   }
   const dim3 grid(f.a.chunks, rows), block(kThreads);
   const hipStream_t st = (hipStream_t)stream;
@@ -4236,9 +4335,9 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
                           u.frequency, f.mapped, f);
   };
   if (dtype == 0)
-    go(select_fast_kernel<0>);
+    extras ? go(select_fast_kernel<0, true>) : go(select_fast_kernel<0, false>);
   else
-    go(select_fast_kernel<1>);
+    extras ? go(select_fast_kernel<1, true>) : go(select_fast_kernel<1, false>);
   return (int)hipGetLastError();
 }
 #endif

@@ -726,17 +726,18 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
     return fail(JF_ERR_INVALID_ARGUMENT, "drafted rows need draft probabilities");
 
   // The rows the fast selection kernel takes: in a launch of 16-byte-aligned
-  // rows (and a vocabulary of at least one vector), each row with no extra
-  // verify tokens whose penalty row fits its fixed slots. When only some
-  // rows qualify the launch is split: the fast kernel selects those, and
-  // select_kernel the others (it skips rows marked fast_row).
+  // rows (and a vocabulary of at least one vector), each row whose penalty
+  // row fits its fixed slots and whose extra verify tokens (if any) start
+  // below 2^27 (their offset travels in 27 bits of a kernel argument). When
+  // only some rows qualify the launch is split: the fast kernel selects
+  // those, and select_kernel the others (it skips rows marked fast_row).
   const uint64_t stride_el = rows > 1 ? a->logits_stride : V;
   const bool launch_fast = aligned && V >= 8 && stride_el <= 0xffffffffull &&
                            !(a->mask_rows && any_constrained);
   uint32_t n_fast = 0;
   for (uint32_t r = 0; r < rows; ++r) {
     jf::RowParams &rp = params[r];
-    const bool ok = launch_fast && !rp.extra_count &&
+    const bool ok = launch_fast && (!rp.extra_count || rp.extra_offset <= jf::kExtraOffsetMask) &&
                     !((rp.flags & jf::kRowPenalized) &&
                       (!a->penalties->host.fits(rp.penalty_row) || rp.penalty_row > 0xffffffu));
     rp.fast_row = ok ? 1u : 0u;
@@ -889,15 +890,18 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
     for (uint32_t i0 = 0; i0 < n_fast && e == hipSuccess; i0 += jf::kKernargRows) {
       const uint32_t n = std::min<uint32_t>(n_fast - i0, jf::kKernargRows);
       F.row_base = split ? 0u : i0;
+      bool extras = false;
       for (uint32_t i = 0; i < n; ++i) {
         const uint32_t r = row_at(i0 + i);
         const jf::RowParams &rp = params[r];
         const uint32_t prow = (rp.flags & jf::kRowPenalized) ? rp.penalty_row : 0u;
         F.row_info[i] = (rp.flags & 0xffu) | (prow << 8);
         F.row_of[i] = r;
+        F.row_extra[i] = rp.extra_count ? rp.extra_offset | rp.extra_count << 27 : 0u;
+        extras |= rp.extra_count != 0;
       }
       const bool first = i0 == 0 && !split, last = i0 + n == n_fast;
-      e = jf::launch_select_fast(F, n, a->dtype, uniform ? &p0 : nullptr, stream,
+      e = jf::launch_select_fast(F, n, a->dtype, uniform ? &p0 : nullptr, extras, stream,
                                  first ? a->select_start_event : nullptr,
                                  last ? a->select_done_event : nullptr);
     }

@@ -167,6 +167,91 @@ def test_extra_verify_tokens_and_sparse_draft():
     assert np.any(g["draft_probs"][:rows - 1] > 0)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_extra_tokens_on_the_fast_path(bf16):
+    """Verify rows' extra penalty tokens (penalize_verify, sampling.metal:
+    978-993) taken by the single fast pass: extras equal to history tokens
+    (their fixed slot's count grows), extras with no table entry (penalized
+    in place with their own count), repeated extras, extras in the partial
+    last chunk, refused by the mask, equal to the stop tokens, and 16 extras
+    in one row; greedy, cut and uncut sampled rows, drafted and not. Tokens,
+    kept sets and probabilities bit-exact."""
+    rng = np.random.default_rng(81 + bf16)
+    V = 5 * 8192 + 1234
+    rows = 12
+    x = rand_logits(rng, rows, V, scale=2.0)
+    hist = [rng.integers(0, V, 300).astype(np.uint32) for _ in range(rows)]
+    extra = []
+    for r in range(rows):
+        n = [0, 1, 3, 16, 5, 8, 2, 16, 4, 7, 9, 11][r]
+        e = rng.integers(0, V, n).astype(np.uint32)
+        if n >= 3:
+            e[0] = hist[r][5]                 # a history token: its slot counts it
+            e[1] = e[2] = np.argmax(x[r])     # repeated, at the row's best token
+        if n >= 5:
+            e[3] = V - 3                      # the partial last chunk
+            e[4] = 7                          # a stop token
+        extra.append(e)
+        for t in e:                            # make extras matter: near the top
+            x[r, t] = max(x[r, t], np.float32(5.0) + np.float32(rng.random()))
+    allowed = rng.random((rows, V)) < 0.6
+    allowed[:, 7] = True
+    allowed[5, extra[5][5]] = False            # an extra the mask refuses
+    pols = [J.policy(repetition=1.3, presence=0.5, frequency=0.4),
+            J.policy(temperature=0.8, top_k=40, top_p=0.9, repetition=1.2, presence=0.3),
+            J.policy(temperature=1.0, presence=0.8, frequency=0.5),          # uncut
+            J.policy(temperature=0.7, top_k=20, repetition=1.1, frequency=1.5),
+            J.policy(temperature=0.9, top_k=60, top_p=0.95, presence=2.0, exclude_stop=True),
+            J.policy(temperature=0.8, top_k=30, repetition=1.4, constrained=True),
+            J.policy(repetition=1.5, presence=1.0, constrained=True),
+            J.policy(temperature=1.2, min_p=0.02, top_k=200, presence=0.5, frequency=0.5),
+            J.policy(temperature=0.6, top_k=50, top_p=0.8, repetition=0.9, presence=-0.5),
+            J.policy(temperature=1.0, repetition=1.2, exclude_stop=True),        # uncut
+            J.policy(frequency=2.0, presence=2.0, exclude_stop=True),
+            J.policy(temperature=0.75, top_k=10, repetition=1.25, presence=0.2, frequency=0.1)]
+    u = rng.random(rows).astype(np.float32)
+    d = np.array([int(e[-1]) if len(e) else NO for e in extra], np.uint32)
+    cand = rng.integers(0, V, (rows, 16)).astype(np.uint32)
+    cand[:, 0] = d
+    kw = dict(masks=WL.mask_words(allowed), histories=hist, generated=[150] * rows,
+              mark_prompt=[True] * rows, extra=extra, uniforms=u, stop=(7, 9),
+              draft_tokens=d, drafted_rows=rows, cand_ids=cand,
+              cand_probs=rng.dirichlet(np.ones(16), rows).astype(np.float32),
+              kept_capacity=256)
+    if bf16:
+        kw["logits_bf16"] = WL.to_bf16_bits(x)
+    else:
+        kw["logits"] = x
+    g, r = both(V, pols, **kw)
+    assert_same(g, r)
+
+
+@pytest.mark.parametrize("V", [24 * 8192, 32 * 8192, 248320])
+def test_small_merge_refetches_long_lists(V):
+    """Rows with top-k 50 and no min-p over 24, 32 and 30.3 chunks (a partial
+    last chunk of 2,560 tokens, whose looser bound leaves a long list): some
+    chunk's list passes the 128 slots the small merge fetches up front, and
+    the merge refetches the candidates of the chunks that reach the row's
+    threshold compactly. Drafted rows with sparse candidates and penalized
+    rows among them; bit-exact with the oracle."""
+    rng = np.random.default_rng(V % 1000)
+    rows = 16
+    x = rand_logits(rng, rows, V, scale=2.5)
+    pols = [J.policy(temperature=0.7, top_k=50, top_p=0.9, presence=0.5, frequency=0.3)
+            if r % 2 else J.policy(temperature=0.9, top_k=40) for r in range(rows)]
+    hist = [rng.integers(0, V, 600).astype(np.uint32) for _ in range(rows)]
+    d = rng.integers(0, V, rows).astype(np.uint32)
+    d[::3] = NO
+    cand = rng.integers(0, V, (rows, 16)).astype(np.uint32)
+    cand[:, 0] = d
+    u = rng.random(rows).astype(np.float32)
+    g, r = both(V, pols, logits=x, histories=hist, generated=[300] * rows,
+                mark_prompt=[False] * rows, uniforms=u, draft_tokens=d, drafted_rows=rows,
+                cand_ids=cand, cand_probs=rng.dirichlet(np.ones(16), rows).astype(np.float32),
+                kept_capacity=64)
+    assert_same(g, r)
+
+
 def test_small_topk_with_many_ties_at_the_kth_key():
     """Rows with top-k <= 64 whose boundary holds hundreds of tied tokens
     spread over the chunks (the one-wave merge's exact top-k by radix and id
