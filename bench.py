@@ -575,9 +575,9 @@ def profile_row(key, kernel):
     if not kernel or not path or not os.path.exists(path):
         return None
     for line in open(path):
-        f = line.split()
-        if f and f[0] == kernel:
-            return f
+        # The name may hold spaces (template arguments); the fields follow it.
+        if line.startswith(kernel + " "):
+            return [kernel] + line[len(kernel):].split()
     return None
 
 
