@@ -842,7 +842,7 @@ def verify_cpu_baseline(c, seconds):
 def bench_verify(args):
     """The penalized chain-verify shape (VerifyStep): its step timed from
     C++ as the sample path's is, its dominant kernel (the single pass with
-    the verify rows' extra penalty tokens, select_fast_kernel<0, true>)
+    the verify rows' extra penalty tokens, select_fast_kernel<0, true, FastRows>)
     timed alone."""
     import torch
     from jf_sampler import workloads as WL
@@ -869,7 +869,7 @@ def bench_verify(args):
     step_bytes = sel_bytes + B * 4 * 3 + c["lanes"] * (c["rows"] - 1) * (4 + 16 * 8)
     achieved = sel_bytes / (sel_mean * 1e-6) / 1e9
     step_gbs = step_bytes / (cpp["us_per_step"] * 1e-6) / 1e9
-    kernel = "jf::select_fast_kernel<0, true>"
+    kernel = "jf::select_fast_kernel<0, true, jf::FastRows>"
     key = ("verify", "auto")
     traffic = read_traffic(key, kernel)
     prof_us = read_profile_us(key, kernel)
@@ -983,7 +983,10 @@ def main():
         counted["note"] = ("each step followed by jf_penalty_table_count_rows of one "
                            "token per row, from C++")
     cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
-    kernel = w.get("kernel", f"jf::select_fast_kernel<{0 if w['dtype'] == 'f32' else 1}, false>")
+    # Every benchmarked sample workload is a uniform launch (one policy, each
+    # row its own penalty row): the fast kernel's variant without per-row facts.
+    kernel = w.get("kernel",
+                   f"jf::select_fast_kernel<{0 if w['dtype'] == 'f32' else 1}, false, jf::NoRows>")
     key = profile_key(args.config, args.mode, args.history)
     traffic = read_traffic(key, kernel)
     prof_us = read_profile_us(key, kernel)

@@ -160,7 +160,10 @@ struct SampleLaunch {
 // `slot_count` 32-bit slots, so a block requests them together with its
 // logits and waits on nothing first. Slot = offset in the chunk << 19 |
 // prompt bit << 18 | count (< 2^18); an empty slot is 0 (every real entry
-// has a count or the prompt bit).
+// has a count or the prompt bit). A uniform launch (every row the same
+// policy, each reading its own penalty row, no row map, no extra tokens)
+// carries no per-row facts (FastRows) at all: the kernel-argument segment
+// the runtime copies for every launch then stays small.
 constexpr int kKernargRows = 256;
 struct FastLaunch {
   SampleLaunch a;
@@ -175,6 +178,9 @@ struct FastLaunch {
   uint32_t mapped;            // blockIdx.y selects row row_of[blockIdx.y]
                               // (a launch split between the two kernels;
                               // the kernel takes it as a preloaded argument)
+};
+// The per-row facts of a launch that is not uniform, by blockIdx.y.
+struct FastRows {
   uint32_t row_info[kKernargRows];  // RowFlags | penalty row << 8
   uint32_t row_of[kKernargRows];
   // Launches whose rows carry extra (verify) penalty tokens: the row's
@@ -182,6 +188,8 @@ struct FastLaunch {
   // of them (<= kMaxExtra).
   uint32_t row_extra[kKernargRows];
 };
+// The argument a uniform launch passes in FastRows' place.
+struct NoRows {};
 constexpr uint32_t kExtraOffsetMask = (1u << 27) - 1u;
 
 // Multi-pass stages, in launch order.
@@ -367,9 +375,10 @@ int sample_core(uint32_t vocabulary, const SampleScratch &scratch,
 int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
                   void *start_event = nullptr, void *stop_event = nullptr);
 // `uniform`: when every row of the launch has this policy and penalty table
-// row == its own row, or NULL.
-// extras: some row of the launch has extra penalty tokens (row_extra).
-int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
+// row == its own row, or NULL. `fr`: the launch's per-row facts, or NULL for
+// a uniform launch with no row map and no extra tokens.
+// extras: some row of the launch has extra penalty tokens (fr->row_extra).
+int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, uint32_t dtype,
                        const RowParams *uniform, bool extras, void *stream,
                        void *start_event = nullptr, void *stop_event = nullptr);
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);

@@ -2226,28 +2226,69 @@ __device__ __forceinline__ void finish_greedy_row(const SampleLaunch &a, uint32_
   if (lane == 0) write_result(a, row, key ? 0x7ffffu - (low >> 13) : kNoToken, 0.0f, 0);
 }
 
+// select_fast_kernel's arguments as the kernel-argument segment holds them
+// (each at its natural alignment, in order).
+struct FastKernelArgs {
+  const void *logits;
+  const uint32_t *pen_slots;
+  uint32_t stride, V, packed, u_top_k;
+  float u_minp_offset, u_repetition, u_repetition_inverse, u_presence, u_frequency;
+  uint32_t mapped;
+  FastLaunch f;
+};
+static_assert(offsetof(FastKernelArgs, f) == 56, "the launch record follows 14 dwords");
+
+// The fast selection's launch record, read in place in the kernel-argument
+// segment: each field by a scalar load where it is used. The segment's
+// address passes through an empty asm statement so that the compiler cannot
+// trace the loads to the kernel argument: it would otherwise load the whole
+// record into scalar registers at the kernel's entry and keep it there,
+// which raised the kernel's register use (bf16: 69 to 85 vector registers,
+// one wave less per SIMD). (Taking the argument's address instead would
+// make the compiler copy the record to private memory.)
+__device__ __forceinline__ const SampleLaunch &fast_launch_record() {
+  uint64_t u = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(u));
+  typedef const __attribute__((address_space(4))) FastKernelArgs *KernargPtr;
+  return ((const FastKernelArgs *)(KernargPtr)u)->f.a;
+}
+
+// A launch's per-row fact of row `i`: 0 its sampler row, 1 its flags and
+// penalty row, 2 its extra tokens (0 without per-row facts).
+template <int F, class R>
+__device__ __forceinline__ uint32_t fast_row_fact(const R &fr, uint32_t i) {
+  if constexpr (std::is_same_v<R, NoRows>) {
+    return 0u;
+  } else {
+    return F == 0 ? fr.row_of[i] : F == 1 ? fr.row_info[i] : fr.row_extra[i];
+  }
+}
+
 // XTRA: the launch's rows may carry extra (verify) penalty tokens, read as
-// scalars from f.row_extra's place in SampleLaunch::extra.
-template <int DT, bool XTRA>
+// scalars from fr.row_extra's place in SampleLaunch::extra. R: FastRows, or
+// NoRows for a uniform launch with no row map and no extra tokens.
+template <int DT, bool XTRA, class R>
 __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     const void *logits, const uint32_t *pen_slots, uint32_t stride, uint32_t V,
     uint32_t packed, uint32_t u_top_k, float u_minp_offset, float u_repetition,
     float u_repetition_inverse, float u_presence, float u_frequency, uint32_t mapped,
-    FastLaunch f) {
+    FastLaunch f, R fr) {
   constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
                 LOADS = Geo<DT>::LOADS;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
   constexpr uint32_t VMASK = (1u << VEC) - 1u;
+  constexpr bool kRows = !std::is_same_v<R, NoRows>;
   static_assert(TPL == 32, "one drop bit per register");
-  const SampleLaunch &a = f.a;
+  static_assert(kRows || !XTRA, "extra tokens travel in the per-row facts");
+  const SampleLaunch &a = fast_launch_record();
   __shared__ FastLds s;
   const uint32_t S = (packed >> 8) & 0xffu;
   const uint32_t slot_count = (packed & 0x10000u) ? 512u : 256u;
   const uint32_t row_base = ((packed >> 17) & 0x3fffu) << 8;
   const uint32_t chunk = blockIdx.x, lrow = blockIdx.y;
-  const uint32_t row = mapped ? f.row_of[lrow] : row_base + lrow;
-  const bool uni = (packed >> 31) != 0;
-  const uint32_t info = uni ? ((packed & 0xffu) | (row << 8)) : f.row_info[lrow];
+  const uint32_t row = kRows && mapped ? fast_row_fact<0>(fr, lrow) : row_base + lrow;
+  const bool uni = !kRows || (packed >> 31) != 0;
+  const uint32_t info = uni ? ((packed & 0xffu) | (row << 8)) : fast_row_fact<1>(fr, lrow);
   const uint32_t flags = info & 0xffu, prow = info >> 8;
   const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const uint32_t base = chunk * CHUNK;
@@ -2274,7 +2315,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   // staged in LDS before the first barrier.
   uint32_t xtok = kNoToken;
   if constexpr (XTRA) {
-    const uint32_t xr = f.row_extra[lrow];
+    const uint32_t xr = fast_row_fact<2>(fr, lrow);
     const uint32_t nx = penalized ? xr >> 27 : 0u;
     if (tid < nx) xtok = a.extra[(xr & kExtraOffsetMask) + tid];
   }
@@ -4296,10 +4337,10 @@ static uint32_t fast_resident_blocks(uint32_t dtype) {
     int per_cu = 0, cus = 0;
     const hipError_t e1 =
         dtype == 0
-            ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, select_fast_kernel<0, false>,
-                                                           kThreads, 0)
-            : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, select_fast_kernel<1, false>,
-                                                           kThreads, 0);
+            ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                  &per_cu, select_fast_kernel<0, false, FastRows>, kThreads, 0)
+            : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                  &per_cu, select_fast_kernel<1, false, FastRows>, kThreads, 0);
     const hipError_t e2 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     cache[dev][dtype] = e1 == hipSuccess && e2 == hipSuccess && per_cu > 0 && cus > 0
                             ? (uint32_t)per_cu * (uint32_t)cus
@@ -4309,7 +4350,7 @@ static uint32_t fast_resident_blocks(uint32_t dtype) {
   return cache[dev][dtype];
 }
 
-int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
+int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, uint32_t dtype,
                        const RowParams *uniform, bool extras, void *stream, void *start_event,
                        void *stop_event) {
   if (f.fuse_greedy == 1u && f.a.chunks > 1 && rows < fast_resident_blocks(dtype)) {
@@ -4319,8 +4360,10 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
     // slot always remains for the blocks they wait for, which never wait.
     FastLaunch g = f;
     g.fuse_greedy = 2u;
-    return launch_select_fast(g, rows, dtype, uniform, extras, stream, start_event, stop_event);
+    return launch_select_fast(g, fr, rows, dtype, uniform, extras, stream, start_event,
+                              stop_event);
   }
+  if (!fr && (!uniform || f.mapped || extras)) return (int)hipErrorInvalidValue;
   const dim3 grid(f.a.chunks, rows), block(kThreads);
   const hipStream_t st = (hipStream_t)stream;
   const hipEvent_t e0 = (hipEvent_t)start_event, e1 = (hipEvent_t)stop_event;
@@ -4328,16 +4371,22 @@ int launch_select_fast(const FastLaunch &f, uint32_t rows, uint32_t dtype,
   const uint32_t packed = (uniform ? 0x80000000u | (u.flags & 0xffu) : 0u) |
                           (f.a.chunks << 8) | (f.slot_count == 512u ? 0x10000u : 0u) |
                           ((f.row_base >> 8) << 17);
-  auto go = [&](auto kernel) {
+  auto go = [&](auto kernel, const auto &rows_arg) {
     hipExtLaunchKernelGGL(kernel, grid, block, 0, st, e0, e1, 0, f.a.logits, f.pen_slots,
                           (uint32_t)f.a.stride, f.a.vocabulary, packed, u.top_k,
                           u.minp_offset, u.repetition, u.repetition_inverse, u.presence,
-                          u.frequency, f.mapped, f);
+                          u.frequency, f.mapped, f, rows_arg);
   };
-  if (dtype == 0)
-    extras ? go(select_fast_kernel<0, true>) : go(select_fast_kernel<0, false>);
-  else
-    extras ? go(select_fast_kernel<1, true>) : go(select_fast_kernel<1, false>);
+  if (!fr) {
+    dtype == 0 ? go(select_fast_kernel<0, false, NoRows>, NoRows{})
+               : go(select_fast_kernel<1, false, NoRows>, NoRows{});
+  } else if (dtype == 0) {
+    extras ? go(select_fast_kernel<0, true, FastRows>, *fr)
+           : go(select_fast_kernel<0, false, FastRows>, *fr);
+  } else {
+    extras ? go(select_fast_kernel<1, true, FastRows>, *fr)
+           : go(select_fast_kernel<1, false, FastRows>, *fr);
+  }
   return (int)hipGetLastError();
 }
 #endif

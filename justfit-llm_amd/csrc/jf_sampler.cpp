@@ -859,6 +859,7 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   }
   if (e == hipSuccess && (fast || split)) {
     jf::FastLaunch F{};
+    thread_local jf::FastRows s_rows;  // copied into the launch's arguments
     F.a = L;
     F.fuse_greedy = fused ? 1u : 0u;
     F.mapped = split ? 1u : 0u;
@@ -891,17 +892,23 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
       const uint32_t n = std::min<uint32_t>(n_fast - i0, jf::kKernargRows);
       F.row_base = split ? 0u : i0;
       bool extras = false;
-      for (uint32_t i = 0; i < n; ++i) {
-        const uint32_t r = row_at(i0 + i);
-        const jf::RowParams &rp = params[r];
-        const uint32_t prow = (rp.flags & jf::kRowPenalized) ? rp.penalty_row : 0u;
-        F.row_info[i] = (rp.flags & 0xffu) | (prow << 8);
-        F.row_of[i] = r;
-        F.row_extra[i] = rp.extra_count ? rp.extra_offset | rp.extra_count << 27 : 0u;
-        extras |= rp.extra_count != 0;
+      for (uint32_t i = 0; i < n; ++i) extras |= params[row_at(i0 + i)].extra_count != 0;
+      // Per-row facts only where the kernel reads them (a launch that is not
+      // uniform, mapped or with extra tokens).
+      const bool rows_arg = !uniform || split || extras;
+      if (rows_arg) {
+        for (uint32_t i = 0; i < n; ++i) {
+          const uint32_t r = row_at(i0 + i);
+          const jf::RowParams &rp = params[r];
+          const uint32_t prow = (rp.flags & jf::kRowPenalized) ? rp.penalty_row : 0u;
+          s_rows.row_info[i] = (rp.flags & 0xffu) | (prow << 8);
+          s_rows.row_of[i] = r;
+          s_rows.row_extra[i] = rp.extra_count ? rp.extra_offset | rp.extra_count << 27 : 0u;
+        }
       }
       const bool first = i0 == 0 && !split, last = i0 + n == n_fast;
-      e = jf::launch_select_fast(F, n, a->dtype, uniform ? &p0 : nullptr, extras, stream,
+      e = jf::launch_select_fast(F, rows_arg ? &s_rows : nullptr, n, a->dtype,
+                                 uniform ? &p0 : nullptr, extras, stream,
                                  first ? a->select_start_event : nullptr,
                                  last ? a->select_done_event : nullptr);
     }
