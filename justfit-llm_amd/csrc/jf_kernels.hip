@@ -100,6 +100,7 @@ struct __align__(16) Lds {
   uint32_t row_overflow;
   uint32_t row_floor;
   uint32_t row_maxcount;
+  uint32_t row_long;  // merge_small_kernel: a list is longer than its fetched slots
   uint64_t u64a;
 };
 
@@ -2844,10 +2845,10 @@ __device__ __noinline__ void merge_small_general(uint32_t row) {
 // padding): the hardware preloads them into scalar registers at wave launch.
 // They repeat fields of `a` (drafted_rows is 0 when there are no drafts).
 #if JF_IN(2)
-// SPEC: speculatively fetched list slots a thread. 10 gives 128 slots a
-// chunk up to 20 chunks (64 up to 40); 16 gives 128 a chunk up to 32 chunks,
-// for vocabularies past 163,840 tokens whose cut rows have no min-p floor
-// (their lists run past 64 candidates).
+// SPEC: speculatively fetched list slots a thread. 10 gives floor(2560 / S)
+// slots a chunk (134 at 19 chunks); 20 gives floor(5120 / S) (165 at 31
+// chunks), for vocabularies past 163,840 tokens whose cut rows have no
+// min-p floor (their lists average about 75 candidates and reach 130).
 template <int DT, int SPEC>
 __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     const BlockHeader *headers, const uint64_t *cands, const RowParams *params,
@@ -2892,13 +2893,20 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
   // floor_key, reserved.
   const u32x4 h0 = ((GlobalU32x4 *)hbase)[0], h1 = ((GlobalU32x4 *)hbase)[1];
   constexpr uint32_t kSlots = SPEC * kThreads;
-  const uint32_t pshift = S * 128u <= kSlots ? 7u : (S * 64u <= kSlots ? 6u : 5u),
-                 P = 1u << pshift;
+  // P = floor(kSlots / S) slots a chunk (at most a list's capacity), the
+  // slots left over to the last chunk: slot i of the fetch is item i - c P
+  // of chunk c = min(i / P, S - 1), read within the chunk's list. i / P as
+  // the high word of i * ceil(2^32 / P), exact for i P < 2^32.
+  const uint32_t P = min(kSlots / S, (uint32_t)kBlockCandidates);
+  const uint32_t last_cap = min(kSlots - (S - 1) * P, (uint32_t)kBlockCandidates);
+  const uint32_t pinv = (uint32_t)((0xffffffffull + P) / P);
+  auto chunk_of = [&](uint32_t i) { return min(__umulhi(i, pinv), S - 1); };
   uint64_t sv[SPEC];
 #pragma unroll
   for (int k = 0; k < SPEC; ++k) {
-    const uint32_t i = tid + k * kThreads, c = min(i >> pshift, S - 1);
-    sv[k] = ((GlobalU64 *)cbase)[(uint64_t)c * kBlockCandidates + (i & (P - 1))];
+    const uint32_t i = tid + k * kThreads, c = chunk_of(i);
+    const uint32_t j = min(i - c * P, (uint32_t)kBlockCandidates - 1);
+    sv[k] = ((GlobalU64 *)cbase)[(uint64_t)c * kBlockCandidates + j];
   }
   const uint32_t draft_raw = *(GlobalU32 *)daddr;
   const uint32_t cid_raw = *(GlobalU32 *)qaddr;
@@ -2949,15 +2957,16 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     return;
   }
   // The chunk summaries (wave 0): the row maximum, admission, overflow, the
-  // top-k floor (the K-th key is at least every chunk's floor) and the
-  // longest list.
+  // top-k floor (the K-th key is at least every chunk's floor) and whether
+  // some list is longer than its fetched slots.
   // Also each chunk's offset among the candidates of the chunks whose
   // maximum reaches the row's threshold (hoff; the others hold none at or
   // above it), for a compact refetch.
   if (tid < 64) {
     const float mx = wave_max_f32(hmax);
+    const bool long_list = hv && hcount > (tid + 1 == S ? last_cap : P);
     const uint32_t adm = wave_max_u32(hadm), ovf = wave_max_u32(hovf),
-                   flr = wave_max_u32(hfloor), hcmax = wave_max_u32(hcount);
+                   flr = wave_max_u32(hfloor), longer = ballot(long_list) ? 1u : 0u;
     const uint32_t wthr =
         max((prec.flags & kRowMinP) ? logit_key(__builtin_fminf(mx + prec.minp_offset, mx)) : 0u,
             flr);
@@ -2973,7 +2982,7 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
       s.row_admitted = adm;
       s.row_overflow = ovf;
       s.row_floor = flr;
-      s.row_maxcount = hcmax;
+      s.row_long = longer;
     }
   }
   if (tid < 16) {
@@ -2992,13 +3001,13 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
   thr = max(thr, s.row_floor);
   const uint32_t K = rp.top_k;
   const uint32_t n_all = s.hoff[S];
-  if (!s.row_overflow && thr > kLowestKey && (s.row_maxcount <= P || n_all <= kSlots)) {
+  if (!s.row_overflow && thr > kLowestKey && (!s.row_long || n_all <= kSlots)) {
     uint32_t valid = 0;
-    if (s.row_maxcount <= P) {
+    if (!s.row_long) {
 #pragma unroll
       for (int k = 0; k < SPEC; ++k) {
-        const uint32_t i = tid + k * kThreads, c = i >> pshift;
-        if (c < S && (i & (P - 1)) < s.hcnt[c] && (uint32_t)sv[k] >= thr) valid |= 1u << k;
+        const uint32_t i = tid + k * kThreads, c = chunk_of(i);
+        if (i - c * P < s.hcnt[c] && (uint32_t)sv[k] >= thr) valid |= 1u << k;
       }
     } else {
       // A list longer than its fetched slots, but every candidate at or
@@ -4442,12 +4451,12 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, bool wide, void *s
                        (uint32_t)a.uniform_offset, (uint32_t)a.uniform_stride,
                        a.draft_tokens && !a.row_indexed ? a.drafted_rows : 0u, a.row_indexed, a);
   };
-  // The wider fetch only where it adds slots: 21 to 32 chunks.
-  const bool w = wide && a.chunks > 20 && a.chunks <= 32;
+  // The wider fetch past 20 chunks (fewer than 128 slots a chunk otherwise).
+  const bool w = wide && a.chunks > 20;
   if (dtype == 0)
-    w ? go(merge_small_kernel<0, 16>) : go(merge_small_kernel<0, 10>);
+    w ? go(merge_small_kernel<0, 20>) : go(merge_small_kernel<0, 10>);
   else
-    w ? go(merge_small_kernel<1, 16>) : go(merge_small_kernel<1, 10>);
+    w ? go(merge_small_kernel<1, 20>) : go(merge_small_kernel<1, 10>);
   return (int)hipGetLastError();
 }
 #endif

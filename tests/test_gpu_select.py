@@ -229,14 +229,44 @@ def test_extra_tokens_on_the_fast_path(bf16):
 @pytest.mark.parametrize("V", [24 * 8192, 32 * 8192, 248320])
 def test_small_merge_refetches_long_lists(V):
     """Rows with top-k 50 and no min-p over 24, 32 and 30.3 chunks (a partial
-    last chunk of 2,560 tokens, whose looser bound leaves a long list): some
-    chunk's list passes the 128 slots the small merge fetches up front, and
-    the merge refetches the candidates of the chunks that reach the row's
-    threshold compactly. Drafted rows with sparse candidates and penalized
-    rows among them; bit-exact with the oracle."""
+    last chunk of 2,560 tokens): the small merge's wide fetch (floor(5120 /
+    S) slots a chunk, the rest to the last chunk), and where a list passes
+    its slots, the compact refetch of the candidates of the chunks that
+    reach the row's threshold. Drafted rows with sparse candidates and
+    penalized rows among them; bit-exact with the oracle."""
     rng = np.random.default_rng(V % 1000)
     rows = 16
     x = rand_logits(rng, rows, V, scale=2.5)
+    pols = [J.policy(temperature=0.7, top_k=50, top_p=0.9, presence=0.5, frequency=0.3)
+            if r % 2 else J.policy(temperature=0.9, top_k=40) for r in range(rows)]
+    hist = [rng.integers(0, V, 600).astype(np.uint32) for _ in range(rows)]
+    d = rng.integers(0, V, rows).astype(np.uint32)
+    d[::3] = NO
+    cand = rng.integers(0, V, (rows, 16)).astype(np.uint32)
+    cand[:, 0] = d
+    u = rng.random(rows).astype(np.float32)
+    g, r = both(V, pols, logits=x, histories=hist, generated=[300] * rows,
+                mark_prompt=[False] * rows, uniforms=u, draft_tokens=d, drafted_rows=rows,
+                cand_ids=cand, cand_probs=rng.dirichlet(np.ones(16), rows).astype(np.float32),
+                kept_capacity=64)
+    assert_same(g, r)
+
+
+def test_small_merge_refetches_a_long_inner_list():
+    """A long list in a chunk other than the last (the last chunk's list also
+    gets the fetch's spare slots): chunk 3 of each row holds 320 high,
+    distinct values in the registers of its first 10 threads, so few lane
+    maxima reach them and the chunk's bound admits all 320. The merge then
+    refetches compactly; the rank selection still succeeds (no ties)."""
+    rng = np.random.default_rng(77)
+    V, rows = 248320, 8
+    x = rand_logits(rng, rows, V, scale=1.0)
+    # fp32 token c * 8192 + j * 1024 + t * 4 + e sits in thread t's register
+    # j * 4 + e.
+    toks = np.array([3 * 8192 + j * 1024 + t * 4 + e
+                     for j in range(8) for t in range(10) for e in range(4)])
+    for r in range(rows):
+        x[r, toks] = rng.permutation(np.linspace(3.5, 6.0, toks.size)).astype(np.float32)
     pols = [J.policy(temperature=0.7, top_k=50, top_p=0.9, presence=0.5, frequency=0.3)
             if r % 2 else J.policy(temperature=0.9, top_k=40) for r in range(rows)]
     hist = [rng.integers(0, V, 600).astype(np.uint32) for _ in range(rows)]
