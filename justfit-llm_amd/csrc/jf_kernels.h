@@ -378,8 +378,11 @@ int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
 // row == its own row, or NULL. `fr`: the launch's per-row facts, or NULL for
 // a uniform launch with no row map and no extra tokens.
 // extras: some row of the launch has extra penalty tokens (fr->row_extra).
+// fuse_uncut: every row is sampled with no cut, draft, penalty or extra
+// token and no kept outputs are asked for: each row's last chunk block draws
+// it (no uncut_kernel launch).
 int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, uint32_t dtype,
-                       const RowParams *uniform, bool extras, void *stream,
+                       const RowParams *uniform, bool extras, bool fuse_uncut, void *stream,
                        void *start_event = nullptr, void *stop_event = nullptr);
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
 // wide: some cut row of the launch has no min-p floor (longer candidate

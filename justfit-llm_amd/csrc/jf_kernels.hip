@@ -1805,22 +1805,19 @@ __device__ __forceinline__ void merge_row(const SampleLaunch &a,
 // ---- the single-pass selection kernel -------------------------------------
 
 #if JF_IN(1)
-// A row that keeps every admitted token: the chunk's summary for the uncut
-// kernel instead of candidates. Its maximum, whether it admits a token, its
-// admitted (non-NaN) count, and its exact fixed-point mass against its own
-// maximum (every value of the chunk is at most that maximum): per slice in
-// partial slots v[1 + g] (slice g = load g / kWaves of wave g % kWaves, 64 x
-// VEC consecutive tokens) and in total in v[0]. `side` holds the penalized
-// tokens whose own registers are dropped (NaN), so every token counts once;
-// their weights join their slices through LDS. s.slices is zero on entry
-// (cleared before the block's last barrier). Block-uniform.
+// A row that keeps every admitted token: its chunk's exact fixed-point mass
+// against the chunk's own maximum `bmax` (every value of the chunk is at most
+// that maximum), per slice into s.slices[g] (slice g = load g / kWaves of
+// wave g % kWaves, 64 x VEC consecutive tokens), and its admitted (non-NaN)
+// count per wave into s.wcount. `side` holds the penalized tokens whose own
+// registers are dropped (NaN), so every token counts once; their weights join
+// their slices through LDS. s.slices is zero on entry (cleared before the
+// block's last barrier). Ends with a barrier. Block-uniform.
 template <int DT, class L>
-__device__ __forceinline__ void uncut_summary(const float (&xs)[Geo<DT>::TPL],
-                                              const SideEntries &side, uint32_t base,
-                                              float bmax, uint32_t badm, float inv_t, L &s,
-                                              BlockHeader *hdr, StagePartial *part) {
+__device__ __forceinline__ void uncut_slices(const float (&xs)[Geo<DT>::TPL],
+                                             const SideEntries &side, uint32_t base,
+                                             float bmax, float inv_t, L &s) {
   constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS, SLAB = Geo<DT>::SLAB;
-  constexpr uint32_t G = LOADS * kWaves;
   static_assert(LOADS % 4 == 0, "loads in groups of four");
   const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   uint32_t n = 0;
@@ -1858,6 +1855,19 @@ __device__ __forceinline__ void uncut_summary(const float (&xs)[Geo<DT>::TPL],
   n = wave_sum_u32(n);
   if (lane == 0) s.wcount[w] = n;
   __syncthreads();
+}
+
+// The chunk's summary for the uncut kernel instead of candidates: its
+// maximum, whether it admits a token, its admitted count, and its slice
+// masses (partial slots v[1 + g]) and total (v[0]) from uncut_slices.
+template <int DT, class L>
+__device__ __forceinline__ void uncut_summary(const float (&xs)[Geo<DT>::TPL],
+                                              const SideEntries &side, uint32_t base,
+                                              float bmax, uint32_t badm, float inv_t, L &s,
+                                              BlockHeader *hdr, StagePartial *part) {
+  constexpr uint32_t G = Geo<DT>::LOADS * kWaves;
+  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  uncut_slices<DT>(xs, side, base, bmax, inv_t, s);
   if (w == 0) {
     const uint64_t v = lane < G ? s.slices[lane] : 0ull;
     if (lane < G) part->v[1 + lane] = v;
@@ -2024,6 +2034,42 @@ __global__ __launch_bounds__(kThreads) void select_kernel(SampleLaunch a) {
 }
 #endif
 
+// Inside one wave's slice of a chunk (64 lanes x VEC consecutive tokens,
+// lane-major): q[e] are the lane's weights in id order and the slice's
+// weights sum past `within`. Returns the lane whose running sum first passes
+// it, and in that lane the index of the first token that does (the walk of
+// sampling.metal:790-829 restricted to the slice).
+template <int VEC>
+__device__ __forceinline__ uint32_t slice_hit(const uint64_t (&q)[VEC], uint64_t within,
+                                              uint32_t &e_hit) {
+  uint64_t lsum = 0;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) lsum += q[e];
+  const uint64_t incl = wave_incl_scan_u64(lsum);
+  const uint32_t hl = (uint32_t)__builtin_ctzll(ballot(incl > within));
+  uint64_t run = incl - lsum;
+  e_hit = VEC;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    if (e_hit == (uint32_t)VEC && q[e] && run + q[e] > within) e_hit = (uint32_t)e;
+    run += q[e];
+  }
+  return hl;
+}
+
+// The slice g that holds `within`, given lane l's slice sum vg (lanes at or
+// past G hold 0), and `within` made relative to it; wave-wide, every lane
+// gets both.
+__device__ __forceinline__ uint32_t pick_slice(uint64_t vg, uint32_t G, uint64_t &within) {
+  const uint32_t l = lane_id();
+  const bool gin = l < G;
+  const uint64_t ginc = wave_incl_scan_u64(vg);
+  // The slices of chunk c sum to its mass, which passes `within`.
+  const uint32_t g = (uint32_t)__builtin_ctzll(ballot(gin && ginc > within));
+  within -= readlane_u64(ginc - vg, g);
+  return g;
+}
+
 // ---- the fast selection kernel ---------------------------------------------
 //
 // select_kernel's results for the rows the host admits (16-byte aligned rows,
@@ -2050,6 +2096,16 @@ struct __align__(16) FastLds {
   float wf[kWaves];
   uint32_t wu[kWaves];
   uint32_t wu2[kWaves];
+};
+
+// LDS of the fast kernel's variant that finishes rows with no cut itself:
+// the row's chunk slice masses and summaries, gathered by its last chunk's
+// block.
+struct __align__(16) FusedUncutLds : FastLds {
+  uint64_t fsl[kMaxChunks * 32];  // slice masses, G a chunk, chunk-major
+  float cmax[kMaxChunks];         // chunk maxima
+  uint32_t cinfo[kMaxChunks];     // admitted count << 1 | admits
+  uint32_t fail;                  // some wait gave up
 };
 
 // The largest multiple of 2^16 with at least k (1..64) lanes holding a value
@@ -2254,6 +2310,168 @@ __device__ __forceinline__ const SampleLaunch &fast_launch_record() {
   return ((const FastKernelArgs *)(KernargPtr)u)->f.a;
 }
 
+// Rows with no cut finished in the select launch (every row of the launch
+// sampled with no min-p, top-k or top-p cut, no draft, penalty, extra token
+// or kept output). Each chunk block publishes its chunk's summary and slice
+// masses as self-validating words: the summary in partial slot
+// kFusedSummarySlot (the maximum's order key << 32 | admitted count << 14 |
+// admits << 13 | tag), slice g in kFusedSliceSlot + g (mass, below 2^54, |
+// tag10 << 54); tag = call epoch << 1 | 1 (12 bits of it, 9 for tag10). The
+// row's last chunk's block gathers them, waiting word by word (bounded) for
+// any not yet written, returns each word it took to zero, and draws as
+// uncut_kernel does for a row without a draft: M, the rescales r_c, the
+// chunk masses T_c and W; the chunk and slice that hold floor(u W); that
+// slice's 64 x VEC logits reloaded (masked and stop tokens dropped) and
+// walked. Its waits end: the row's other blocks were dispatched before it
+// (in order of block index, chunk fastest) and wait on nothing. Should one
+// give up, the row gets JF_NO_TOKEN and the status word is set.
+constexpr uint32_t kFusedSummarySlot = 100, kFusedSliceSlot = 101;
+template <int DT>
+__device__ __forceinline__ void finish_uncut_row(const SampleLaunch &a, const float (&xs)[32],
+                                                 const SideEntries &side, uint32_t base,
+                                                 float bmax, uint32_t badm, float inv_t,
+                                                 FusedUncutLds &s, uint32_t row, uint32_t chunk,
+                                                 uint32_t S, uint32_t flags) {
+  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS, SLAB = Geo<DT>::SLAB;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves;
+  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  StagePartial *parts = a.partials + (uint64_t)row * S;
+  const bool finisher = chunk + 1 == S;
+  // The row's uniform, requested before the gather.
+  const float u = finisher ? row_uniform(a, row) : 0.0f;
+  if (tid == 0) s.fail = 0;
+  uncut_slices<DT>(xs, side, base, bmax, inv_t, s);
+  const uint32_t count = s.wcount[0] + s.wcount[1] + s.wcount[2] + s.wcount[3];
+  const uint32_t info = count << 1 | (badm ? 1u : 0u);
+  const uint64_t tag = ((uint64_t)(a.epoch & 0xfffu) << 1) | 1ull;
+  const uint64_t tag10 = ((uint64_t)(a.epoch & 0x1ffu) << 1) | 1ull;
+  constexpr uint64_t kMass54 = (1ull << 54) - 1ull;
+  if (!finisher) {
+    if (w == 0) {
+      if (lane < G) st_dev(&parts[chunk].v[kFusedSliceSlot + lane], s.slices[lane] | tag10 << 54);
+      if (lane == 0)
+        st_dev(&parts[chunk].v[kFusedSummarySlot],
+               (uint64_t)logit_key(bmax) << 32 | (uint64_t)info << 13 | tag);
+    }
+    return;
+  }
+  // The gather: every other chunk's slices (all threads) and summaries
+  // (threads 0 .. S - 2), each word re-read until it carries this call's tag.
+  bool ok = true;
+  for (uint32_t k = tid; k < (S - 1) * G; k += kThreads) {
+    const uint32_t c = k / G, g = k % G;
+    uint64_t *word = &parts[c].v[kFusedSliceSlot + g];
+    uint64_t v = 0;
+    for (uint32_t n = 0; (v >> 54) != tag10 && n < a.wait_bound; ++n) v = ld_dev(word);
+    if ((v >> 54) == tag10) {
+      s.fsl[k] = v & kMass54;
+      st_dev(word, 0ull);
+    } else {
+      ok = false;
+    }
+  }
+  if (tid + 1 < S) {
+    uint64_t *word = &parts[tid].v[kFusedSummarySlot];
+    uint64_t v = 0;
+    for (uint32_t n = 0; (v & 0x1fffu) != tag && n < a.wait_bound; ++n) v = ld_dev(word);
+    if ((v & 0x1fffu) == tag) {
+      s.cmax[tid] = key_logit((uint32_t)(v >> 32));
+      s.cinfo[tid] = (uint32_t)(v >> 13) & 0x7fffu;
+      st_dev(word, 0ull);
+    } else {
+      ok = false;
+    }
+  }
+  if (tid < G) s.fsl[(S - 1) * G + tid] = s.slices[tid];
+  if (tid == 0) {
+    s.cmax[S - 1] = bmax;
+    s.cinfo[S - 1] = info;
+  }
+  if (!ok) s.fail = 1;
+  __syncthreads();
+  if (s.fail) {
+    if (tid == 0) {
+      write_result(a, row, kNoToken, 0.0f, 0);
+      if (a.status) __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    return;
+  }
+  if (w != 0) return;
+  // Wave 0 draws (uncut_kernel's undrafted row): lane c < S holds chunk c.
+  const bool in = lane < S;
+  const float m = in ? s.cmax[lane] : -3.402823466e38f;
+  const uint32_t ci = in ? s.cinfo[lane] : 0u;
+  uint64_t mass = 0;
+  if (in)
+#pragma unroll
+    for (uint32_t g = 0; g < G; ++g) mass += s.fsl[lane * G + g];
+  const float M = wave_max_f32(m);
+  const uint64_t R = in ? chunk_scale(m, M, inv_t) : kZeroScale;
+  const uint64_t T = scale_by(mass, R);
+  const uint64_t incl = wave_incl_scan_u64(T);
+  const uint64_t W = readlane_u64(incl, 63);
+  const uint32_t admitted = wave_sum_u32(ci & 1u), kept = wave_sum_u32(ci >> 1);
+  const bool none = admitted == 0 || M == __builtin_inff();
+  if (none || W == 0) {
+    // The sentinel (a row of -inf keeps every token at probability 0).
+    if (lane == 0) write_result(a, row, kNoToken, 0.0f, none ? 0u : kept);
+    return;
+  }
+  uint64_t target = floor_mul(W, u);
+  if (target >= W) target = W - 1;
+  // incl at the last lane is W > target: some lane passes it.
+  const uint32_t c = (uint32_t)__builtin_ctzll(ballot(in && incl > target));
+  uint64_t within = unscaled_bound(target - readlane_u64(incl - T, c), readlane_u64(R, c));
+  const uint64_t vg = lane < G ? s.fsl[c * G + lane] : 0ull;
+  const uint32_t g = pick_slice(vg, G, within);
+  // Slice g of chunk c: load g / kWaves of wave g % kWaves.
+  const uint32_t jg = g / kWaves, wg = g % kWaves;
+  const uint32_t V = a.vocabulary;
+  const uint32_t t0 = c * CHUNK + jg * SLAB + (wg * 64 + lane) * VEC;
+  float x[VEC];
+  if constexpr (DT == 0) {
+    const float *rowp = (const float *)a.logits + (uint64_t)row * a.stride;
+    if (t0 + VEC <= V) {
+      const f32x4 v = *(const f32x4 *)(rowp + t0);
+      x[0] = v.x;
+      x[1] = v.y;
+      x[2] = v.z;
+      x[3] = v.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] = t0 + e < V ? rowp[t0 + e] : kNotAdmitted;
+    }
+  } else {
+    const uint16_t *rowp = (const uint16_t *)a.logits + (uint64_t)row * a.stride;
+    if (t0 + VEC <= V) {
+      const u32x4 v = *(const u32x4 *)(rowp + t0);
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        x[2 * k] = u2f(vw[k] << 16);
+        x[2 * k + 1] = u2f(vw[k] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] = t0 + e < V ? bf16_to_float(rowp[t0 + e]) : kNotAdmitted;
+    }
+  }
+  // The slice's VEC tokens share one mask word (t0 is a multiple of VEC).
+  const uint32_t mword =
+      (flags & kRowConstrained) && t0 < V ? a.masks[(uint64_t)row * a.mask_stride + (t0 >> 5)] : ~0u;
+  const float mc = __shfl(m, (int)c, kWave);
+  uint64_t q[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    const uint32_t t = t0 + e;
+    const bool drop = !((mword >> (t & 31)) & 1u) ||
+                      ((flags & kRowExcludeStop) && (t == a.stop0 || t == a.stop1));
+    q[e] = quantized_weight(drop ? kNotAdmitted : x[e], mc, inv_t);
+  }
+  uint32_t e_hit;
+  if (lane == slice_hit<VEC>(q, within, e_hit)) write_result(a, row, t0 + e_hit, 0.0f, kept);
+}
+
 // A launch's per-row fact of row `i`: 0 its sampler row, 1 its flags and
 // penalty row, 2 its extra tokens (0 without per-row facts).
 template <int F, class R>
@@ -2268,7 +2486,7 @@ __device__ __forceinline__ uint32_t fast_row_fact(const R &fr, uint32_t i) {
 // XTRA: the launch's rows may carry extra (verify) penalty tokens, read as
 // scalars from fr.row_extra's place in SampleLaunch::extra. R: FastRows, or
 // NoRows for a uniform launch with no row map and no extra tokens.
-template <int DT, bool XTRA, class R>
+template <int DT, bool XTRA, class R, bool FUSE>
 __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     const void *logits, const uint32_t *pen_slots, uint32_t stride, uint32_t V,
     uint32_t packed, uint32_t u_top_k, float u_minp_offset, float u_repetition,
@@ -2282,7 +2500,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   static_assert(TPL == 32, "one drop bit per register");
   static_assert(kRows || !XTRA, "extra tokens travel in the per-row facts");
   const SampleLaunch &a = fast_launch_record();
-  __shared__ FastLds s;
+  __shared__ std::conditional_t<FUSE, FusedUncutLds, FastLds> s;
   const uint32_t S = (packed >> 8) & 0xffu;
   const uint32_t slot_count = (packed & 0x10000u) ? 512u : 256u;
   const uint32_t row_base = ((packed >> 17) & 0x3fffu) << 8;
@@ -2593,10 +2811,14 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   const uint32_t tk =
       bound ? min(min(s.wu2[0], s.wu2[1]), min(s.wu2[2], s.wu2[3])) : 0u;
   if (uncut) {
-    // The row keeps every admitted token: the uncut kernel's chunk summary.
+    // The row keeps every admitted token: the uncut kernel's chunk summary,
+    // or (FUSE) the row finished here.
     const float inv_t = uni ? prec.inv_t : rp.inv_t;
-    uncut_summary<DT>(xs, side, base, bmax, badm, inv_t, s, hdr,
-                      a.partials + (uint64_t)row * S + chunk);
+    if constexpr (FUSE)
+      finish_uncut_row<DT>(a, xs, side, base, bmax, badm, inv_t, s, row, chunk, S, flags);
+    else
+      uncut_summary<DT>(xs, side, base, bmax, badm, inv_t, s, hdr,
+                        a.partials + (uint64_t)row * S + chunk);
     return;
   }
   uint32_t thr = tk;
@@ -3621,42 +3843,6 @@ __global__ __launch_bounds__(kThreads) void walk_kernel(SampleLaunch a) {
 }
 #endif
 
-// Inside one wave's slice of a chunk (64 lanes x VEC consecutive tokens,
-// lane-major): q[e] are the lane's weights in id order and the slice's
-// weights sum past `within`. Returns the lane whose running sum first passes
-// it, and in that lane the index of the first token that does (the walk of
-// sampling.metal:790-829 restricted to the slice).
-template <int VEC>
-__device__ __forceinline__ uint32_t slice_hit(const uint64_t (&q)[VEC], uint64_t within,
-                                              uint32_t &e_hit) {
-  uint64_t lsum = 0;
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) lsum += q[e];
-  const uint64_t incl = wave_incl_scan_u64(lsum);
-  const uint32_t hl = (uint32_t)__builtin_ctzll(ballot(incl > within));
-  uint64_t run = incl - lsum;
-  e_hit = VEC;
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) {
-    if (e_hit == (uint32_t)VEC && q[e] && run + q[e] > within) e_hit = (uint32_t)e;
-    run += q[e];
-  }
-  return hl;
-}
-
-// The slice g that holds `within`, given lane l's slice sum vg (lanes at or
-// past G hold 0), and `within` made relative to it; wave-wide, every lane
-// gets both.
-__device__ __forceinline__ uint32_t pick_slice(uint64_t vg, uint32_t G, uint64_t &within) {
-  const uint32_t l = lane_id();
-  const bool gin = l < G;
-  const uint64_t ginc = wave_incl_scan_u64(vg);
-  // The slices of chunk c sum to its mass, which passes `within`.
-  const uint32_t g = (uint32_t)__builtin_ctzll(ballot(gin && ginc > within));
-  within -= readlane_u64(ginc - vg, g);
-  return g;
-}
-
 // ---- rows that keep every admitted token -----------------------------------
 //
 // A sampled row with no min-p, top-k or top-p cut keeps every admitted token.
@@ -4347,9 +4533,9 @@ static uint32_t fast_resident_blocks(uint32_t dtype) {
     const hipError_t e1 =
         dtype == 0
             ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                  &per_cu, select_fast_kernel<0, false, FastRows>, kThreads, 0)
+                  &per_cu, select_fast_kernel<0, false, FastRows, false>, kThreads, 0)
             : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                  &per_cu, select_fast_kernel<1, false, FastRows>, kThreads, 0);
+                  &per_cu, select_fast_kernel<1, false, FastRows, false>, kThreads, 0);
     const hipError_t e2 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     cache[dev][dtype] = e1 == hipSuccess && e2 == hipSuccess && per_cu > 0 && cus > 0
                             ? (uint32_t)per_cu * (uint32_t)cus
@@ -4360,8 +4546,8 @@ static uint32_t fast_resident_blocks(uint32_t dtype) {
 }
 
 int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, uint32_t dtype,
-                       const RowParams *uniform, bool extras, void *stream, void *start_event,
-                       void *stop_event) {
+                       const RowParams *uniform, bool extras, bool fuse_uncut, void *stream,
+                       void *start_event, void *stop_event) {
   if (f.fuse_greedy == 1u && f.a.chunks > 1 && rows < fast_resident_blocks(dtype)) {
     // Each row's last chunk can wait for the row's other blocks instead of
     // counting arrivals: only those finishers (one a row) ever wait, and
@@ -4369,10 +4555,11 @@ int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, u
     // slot always remains for the blocks they wait for, which never wait.
     FastLaunch g = f;
     g.fuse_greedy = 2u;
-    return launch_select_fast(g, fr, rows, dtype, uniform, extras, stream, start_event,
-                              stop_event);
+    return launch_select_fast(g, fr, rows, dtype, uniform, extras, fuse_uncut, stream,
+                              start_event, stop_event);
   }
   if (!fr && (!uniform || f.mapped || extras)) return (int)hipErrorInvalidValue;
+  if (fuse_uncut && (extras || f.mapped)) return (int)hipErrorInvalidValue;
   const dim3 grid(f.a.chunks, rows), block(kThreads);
   const hipStream_t st = (hipStream_t)stream;
   const hipEvent_t e0 = (hipEvent_t)start_event, e1 = (hipEvent_t)stop_event;
@@ -4386,15 +4573,22 @@ int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, u
                           u.minp_offset, u.repetition, u.repetition_inverse, u.presence,
                           u.frequency, f.mapped, f, rows_arg);
   };
-  if (!fr) {
-    dtype == 0 ? go(select_fast_kernel<0, false, NoRows>, NoRows{})
-               : go(select_fast_kernel<1, false, NoRows>, NoRows{});
+  if (fuse_uncut) {
+    if (!fr)
+      dtype == 0 ? go(select_fast_kernel<0, false, NoRows, true>, NoRows{})
+                 : go(select_fast_kernel<1, false, NoRows, true>, NoRows{});
+    else
+      dtype == 0 ? go(select_fast_kernel<0, false, FastRows, true>, *fr)
+                 : go(select_fast_kernel<1, false, FastRows, true>, *fr);
+  } else if (!fr) {
+    dtype == 0 ? go(select_fast_kernel<0, false, NoRows, false>, NoRows{})
+               : go(select_fast_kernel<1, false, NoRows, false>, NoRows{});
   } else if (dtype == 0) {
-    extras ? go(select_fast_kernel<0, true, FastRows>, *fr)
-           : go(select_fast_kernel<0, false, FastRows>, *fr);
+    extras ? go(select_fast_kernel<0, true, FastRows, false>, *fr)
+           : go(select_fast_kernel<0, false, FastRows, false>, *fr);
   } else {
-    extras ? go(select_fast_kernel<1, true, FastRows>, *fr)
-           : go(select_fast_kernel<1, false, FastRows>, *fr);
+    extras ? go(select_fast_kernel<1, true, FastRows, false>, *fr)
+           : go(select_fast_kernel<1, false, FastRows, false>, *fr);
   }
   return (int)hipGetLastError();
 }

@@ -292,10 +292,13 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
     const hipError_t e1 = hipMemset(s->counters, 0, max_rows * sizeof(uint32_t));
     const hipError_t e2 = hipMemset(s->states, 0, max_rows * sizeof(jf::RowState));
     const hipError_t e4 = hipMemset(s->bests, 0, blocks * sizeof(uint64_t));
+    // The fused draw's self-validating summary words start as zero too.
+    const hipError_t e5 = hipMemset(s->partials, 0, blocks * sizeof(jf::StagePartial));
     const hipError_t e3 = hipDeviceSynchronize();
     if (e1 != hipSuccess) rc = hip_fail(e1, "counter init");
     else if (e2 != hipSuccess) rc = hip_fail(e2, "state init");
     else if (e4 != hipSuccess) rc = hip_fail(e4, "greedy best init");
+    else if (e5 != hipSuccess) rc = hip_fail(e5, "chunk summary init");
     else if (e3 != hipSuccess) rc = hip_fail(e3, "init sync");
   }
   if (rc != JF_OK) {
@@ -848,6 +851,12 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
       }
     }
   }
+  // A fast launch of rows that all keep every admitted token, with no draft,
+  // penalty or extra token and no kept outputs: each row's last chunk block
+  // draws it, so no uncut_kernel launch follows.
+  bool fuse_uncut = fast && any_uncut && !any_cut && !any_greedy && !any_drafted && !kept;
+  for (uint32_t r = 0; fuse_uncut && r < rows; ++r)
+    fuse_uncut = !(params[r].flags & jf::kRowPenalized) && !params[r].extra_count;
   // The merge finishes the cut rows, and the greedy rows unless the launch
   // is all greedy and fast (fused) or has uncut rows and no cut ones (then
   // uncut_kernel takes them).
@@ -908,7 +917,7 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
       }
       const bool first = i0 == 0 && !split, last = i0 + n == n_fast;
       e = jf::launch_select_fast(F, rows_arg ? &s_rows : nullptr, n, a->dtype,
-                                 uniform ? &p0 : nullptr, extras, stream,
+                                 uniform ? &p0 : nullptr, extras, fuse_uncut, stream,
                                  first ? a->select_start_event : nullptr,
                                  last ? a->select_done_event : nullptr);
     }
@@ -945,7 +954,7 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
       if (e != hipSuccess) return hip_fail((hipError_t)e, "stage launch");
     }
   }
-  if (any_uncut) {
+  if (any_uncut && !fuse_uncut) {
     // residual_kernel over the kRowLean rows, then uncut_kernel: one block
     // per row, or one per (row, chunk) when other drafted uncut rows need
     // their residual pass there.
@@ -993,10 +1002,10 @@ int sampler_upload(void *ctx, const jf::RowParams *params, uint32_t rows,
 
 extern "C" {
 
-// A greedy finisher's wait that gave up in an earlier call (the status word
-// set): reported once as JF_ERR_DEVICE, with the packed bests and arrival
-// counters cleared on `stream` behind every earlier launch, so that no word
-// that call left behind reaches a later one.
+// A finisher's wait that gave up in an earlier call (the status word set):
+// reported once as JF_ERR_DEVICE, with the packed bests, arrival counters and
+// chunk summaries cleared on `stream` behind every earlier launch, so that no
+// word that call left behind reaches a later one.
 static int take_status(jf_sampler *s, void *stream) {
   if (!__atomic_load_n(s->status_host, __ATOMIC_ACQUIRE)) return JF_OK;
   __atomic_store_n(s->status_host, 0u, __ATOMIC_RELEASE);
@@ -1005,9 +1014,12 @@ static int take_status(jf_sampler *s, void *stream) {
          "greedy best clear");
   JF_HIP(hipMemsetAsync(s->counters, 0, (size_t)s->max_rows * sizeof(uint32_t), st),
          "counter clear");
+  JF_HIP(hipMemsetAsync(s->partials, 0,
+                        (size_t)s->max_rows * s->max_chunks * sizeof(jf::StagePartial), st),
+         "chunk summary clear");
   return fail(JF_ERR_DEVICE,
-              "a greedy selection's bounded wait for a chunk result expired in an earlier "
-              "call; that call's rows affected hold JF_NO_TOKEN");
+              "a selection's bounded wait for a chunk result expired in an earlier call; "
+              "that call's rows affected hold JF_NO_TOKEN");
 }
 
 int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {

@@ -518,9 +518,78 @@ def test_mixed_cut_and_uncut_rows(kind):
     assert np.all(g["tokens"] != NO)
 
 
+def _uncut_rows(rng, rows, V, uniform):
+    """Rows that keep every admitted token, with masks, stop exclusion and
+    the sentinel cases, for the draw finished in the select launch."""
+    x = rand_logits(rng, rows, V, scale=1.5)
+    allowed = rng.random((rows, V)) < 0.3
+    allowed[:, :40] = True
+    if rows >= 8:
+        allowed[3, 123] = True
+        x[1] = np.nan                         # nothing admitted: sentinel
+        x[2] = -np.inf                        # no mass: sentinel
+        x[3, 123] = np.inf                    # +inf maximum: sentinel
+        x[4, ::3] = np.nan                    # NaN tokens are never drawn
+        allowed[5] = False
+        allowed[5, [7, 8, V - 2]] = True      # the stop tokens and one other
+        x[6] = -60.0
+        x[6, V - 1] = 3.0                     # the last chunk's last token
+        x[6, 5] = 2.5
+        x[7] = np.round(x[7], 0)              # ties everywhere
+    masks = WL.mask_words(allowed)
+    if uniform:
+        pols = [J.policy(temperature=1.0, constrained=True, exclude_stop=True)] * rows
+    else:
+        temps = [1.0, 1.0, 0.8, 1.0, 0.7, 1.0, 0.25, 1.3, 3.0, 0.5]
+        pols = [J.policy(temperature=temps[r % 10], constrained=r % 3 != 1,
+                         exclude_stop=r % 2 == 1) for r in range(rows)]
+    u = rng.random(rows).astype(np.float32)
+    u[0] = 0.0
+    u[rows - 1] = np.float32(1.0) - np.float32(2.0 ** -24)
+    return x, masks, pols, u
+
+
+# Vocabularies whose rows stay 16-byte aligned (the fast kernel's launches).
+@pytest.mark.parametrize("bf16,uniform,V", [(False, True, 5 * 8192 + 1240),
+                                            (True, True, 5 * 8192 + 1240),
+                                            (False, False, 19 * 8192 - 4),
+                                            (True, False, 3000)])
+def test_rows_with_no_cut_drawn_in_the_select_launch(bf16, uniform, V):
+    """Launches whose rows all keep every admitted token, with no draft,
+    penalty or kept output: each row's last chunk block gathers the other
+    chunks' self-validating summaries and draws (no uncut_kernel launch).
+    Uniform and per-row policies, fp32 and bf16, a partial last chunk, one
+    chunk only; bit-exact with the oracle."""
+    rng = np.random.default_rng(V + 2 * bf16 + uniform)
+    rows = 10
+    x, masks, pols, u = _uncut_rows(rng, rows, V, uniform)
+    kw = dict(masks=masks, uniforms=u, stop=(7, 8))
+    kw["logits_bf16" if bf16 else "logits"] = WL.to_bf16_bits(x) if bf16 else x
+    g, r = both(V, pols, **kw)
+    assert_same(g, r)
+    assert all(g["tokens"][k] == NO for k in (1, 2, 3))
+    assert g["tokens"][0] != NO
+
+
+def test_rows_with_no_cut_across_calls_on_one_sampler():
+    """The in-launch draw's summary words are returned to zero by each call's
+    finisher: calls of 10, 3 and 10 rows with new inputs on one sampler,
+    each bit-exact with the oracle."""
+    rng = np.random.default_rng(91)
+    V = 7 * 8192 + 100
+    s = J.Sampler(V, 10)
+    for rows in (10, 3, 10, 10):
+        x, masks, pols, u = _uncut_rows(rng, rows, V, uniform=rows == 3)
+        kw = dict(masks=masks, uniforms=u, stop=(7, 8), logits=x)
+        print(f"call rows={rows}", flush=True)
+        g = run_gpu(V, pols, sampler=s, **kw)
+        r = run_oracle(V, pols, **kw)
+        assert_same(g, r)
+
+
 def test_c3_sampled_without_kept_outputs():
-    """C3 sampled as the engine calls it (no kept outputs): the two-pass
-    mass-and-draw path at full size."""
+    """C3 sampled as the engine calls it (no kept outputs): the draw finished
+    in the select launch, at full size."""
     c = WL.config3()
     B = c["logits_bf16"].shape[0]
     p = J.policy(temperature=1.0, constrained=True)

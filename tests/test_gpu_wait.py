@@ -1,12 +1,13 @@
-"""The greedy finisher's bounded wait (no counterpart in the reference, whose
-last-arriving group never waits; split_reduce.h:14-45): its expiry path,
+"""The finishers' bounded waits (no counterpart in the reference, whose
+last-arriving group never waits; split_reduce.h:14-45): their expiry path,
 driven from the host by a wait bound of 0, so that every kernel still exits
 normally. Both finisher forms: the row's last chunk block (V = 151,936, 19
 chunks) and the last block to arrive (V = 8,000, one chunk). Expiry gives
 JF_NO_TOKEN rows and a status the host reports once as JF_ERR_DEVICE (by
 jf_sampler_status, or by the next jf_sample before it enqueues anything);
 the words the expired call left are cleared, and the next calls at the
-default bound are bit-exact with the oracle again."""
+default bound are bit-exact with the oracle again. The same for the draw of
+rows with no cut finished in the select launch."""
 import numpy as np
 import pytest
 
@@ -61,4 +62,38 @@ def test_expired_wait_reports_and_recovers(V):
     assert np.all(out.cpu().numpy() == 7)  # nothing ran
     for _ in range(3):
         np.testing.assert_array_equal(greedy_call(s, x), want)
+    s.status()
+
+
+def test_expired_wait_of_the_in_launch_draw():
+    """Rows with no cut drawn by each row's last chunk block (its gather of
+    the other chunks' summary words is the same bounded wait): bound 0 gives
+    JF_NO_TOKEN rows and one JF_ERR_DEVICE report; the next calls at the
+    default bound are bit-exact again."""
+    import torch
+    V, rows = 5 * 8192 + 76, 6  # 16-byte aligned rows: the fast kernel's launch
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 1.5, (rows, V)).astype(np.float32)
+    u = rng.random(rows).astype(np.float32)
+    pols = [J.policy(temperature=0.9)] * rows
+    want = run_oracle(V, pols, logits=x, uniforms=u)["tokens"]
+    dev = torch.device("cuda", 0)
+    s = J.Sampler(V, rows)
+    xt, ut = torch.from_numpy(x).to(dev), torch.from_numpy(u).to(dev)
+
+    def call():
+        out = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+        s.sample(xt, pols, out, uniforms=ut)
+        torch.cuda.synchronize()
+        return out.cpu().numpy().view(np.uint32).copy()
+
+    np.testing.assert_array_equal(call(), want)
+    s.set_wait_bound(0)
+    assert np.all(call() == NO)
+    with pytest.raises(J.JfError) as e:
+        s.status()
+    assert e.value.code == J.JF_ERR_DEVICE
+    s.set_wait_bound(1 << 20)
+    for _ in range(3):
+        np.testing.assert_array_equal(call(), want)
     s.status()
