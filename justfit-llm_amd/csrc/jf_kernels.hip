@@ -2831,10 +2831,13 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     const bool hit = x >= tv;
     const uint64_t m = ballot(hit);
     if (m) {
-      const uint32_t slot_i = __builtin_amdgcn_mbcnt_hi(
-          (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, run));
-      if (hit && slot_i < kWaveCandidates)
-        stage[slot_i] = (uint64_t)f2u(x) | ((uint64_t)token << 32);
+      // Hits past the wave's list land on its last entry: the wave's count
+      // then exceeds the list and the chunk is flagged as overflowed, so
+      // its staged list is never copied out.
+      const uint32_t slot_i = min(__builtin_amdgcn_mbcnt_hi(
+                                      (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, run)),
+                                  (uint32_t)kWaveCandidates - 1u);
+      if (hit) stage[slot_i] = (uint64_t)f2u(x) | ((uint64_t)token << 32);
       run += (uint32_t)__popcll(m);
     }
   };

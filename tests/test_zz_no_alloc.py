@@ -2,8 +2,9 @@
 file-scope device array) against jf_sample on the same inputs: two calls in a
 row, the second smaller, each bit-exact in tokens, draft probabilities and
 kept outputs; then two all-greedy calls, the second smaller, which finish
-through the array's packed chunk bests. Also its size limits, which it
-rejects before any device call."""
+through the array's packed chunk bests, and two calls of rows with no cut,
+drawn in the select launch through the array's chunk summary words. Also
+its size limits, which it rejects before any device call."""
 import ctypes
 
 import numpy as np
@@ -47,6 +48,16 @@ def _case_inputs(which):
         return dict(V=V, logits=x, policies=pols, histories=histories,
                     generated=[100] * rows, uniforms=rng.random(rows).astype(np.float32),
                     kept_capacity=0)
+    if which in ("uncut", "uncut_small"):
+        # Every row keeps every admitted token (no cut, draft, penalty or
+        # kept output): each row's last chunk block draws it through the
+        # array's chunk summary words, which each call returns to zero.
+        rng = np.random.default_rng(80 if which == "uncut" else 81)
+        V, rows = (151936, 16) if which == "uncut" else (20000, 3)
+        x = rng.normal(0, 1.5, (rows, V)).astype(np.float32)
+        pols = [J.policy(temperature=0.7 + 0.1 * (r % 5)) for r in range(rows)]
+        return dict(V=V, logits=x, policies=pols, histories=None, generated=[0] * rows,
+                    uniforms=rng.random(rows).astype(np.float32), kept_capacity=0)
     rng = np.random.default_rng(77)
     V, rows = 40000, 6
     x = np.round(rng.normal(0, 2, (rows, V)), 1).astype(np.float32)
@@ -112,7 +123,7 @@ def _host(out, dp, kept):
 def test_static_entry_point_matches_jf_sample_on_two_calls():
     import torch
     dev = torch.device("cuda", 0)
-    for which in ("c2", "small", "greedy", "greedy_small"):
+    for which in ("c2", "small", "greedy", "greedy_small", "uncut", "uncut_small"):
         inp = _case_inputs(which)
         print(f"static vs sampler: case {which} V={inp['V']} rows={len(inp['policies'])}",
               flush=True)
