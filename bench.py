@@ -228,6 +228,11 @@ class GpuStep:
 
     def step(self, i):
         a, _ = self.kw[i % len(self.kw)]
+        if self.accept is not None and self.accept[0] == "tree":
+            # Selection and tree acceptance in one call (one launch when the
+            # lanes are greedy).
+            self.sampler.launch_sample_accept_tree(a, self.accept[1])
+            return
         self.sampler.launch(a)
         if self.accept is not None:
             self.sampler.launch_accept(self.accept)
@@ -395,7 +400,8 @@ def time_cpp_loop(g, steps, with_counts, batch=0):
     vp, u32 = ctypes.c_void_p, ctypes.c_uint32
     L.jf_bench_sample_loop.argtypes = [vp, vp, u32, u32, vp, vp, vp, u32, vp,
                                        ctypes.POINTER(ctypes.c_double),
-                                       ctypes.POINTER(ctypes.c_double), u32, vp, vp, vp]
+                                       ctypes.POINTER(ctypes.c_double), u32, vp, vp, vp,
+                                       ctypes.c_int]
     n = len(g.kw)
     arr = (J.JfSampleArgs * n)(*[a for a, _ in g.kw])
     rows = g.w["rows"]
@@ -411,7 +417,7 @@ def time_cpp_loop(g, steps, with_counts, batch=0):
                                 None if toks is None else toks.ctypes.data_as(vp), rows,
                                 J._stream(), ctypes.byref(gpu), ctypes.byref(host), batch,
                                 None if batch_us is None else batch_us.ctypes.data_as(vp),
-                                accept_ptr(g, "chain"), accept_ptr(g, "tree"))
+                                accept_ptr(g, "chain"), accept_ptr(g, "tree"), 1)
     if rc:
         raise RuntimeError(f"C++ timing loop failed: {rc} {J.lib().jf_last_error().decode()}")
     out = {"us_per_step": gpu.value, "host_us_per_call": host.value}

@@ -353,6 +353,21 @@ typedef struct jf_accept_tree_args {
 int jf_accept_tree(jf_sampler *sampler, const jf_accept_tree_args *args,
                    void *stream);
 
+/* No single counterpart in the reference, whose engine records the
+ * selection (Sampling::addInitial/addVerify) and verify_tree_accept into one
+ * command buffer (Runtime.cpp:1284-1306): jf_sample(sample) then
+ * jf_accept_tree(accept) on `stream`, with the same results, as one launch
+ * when it can: every lane greedy, the lanes' rows the selection's rows in
+ * order (lanes x rows_per_lane == rows, accept->target_tokens ==
+ * sample->out_tokens, at most 16 lanes), and the selection a uniform
+ * all-greedy launch that each row's last chunk block finishes. Then the
+ * finisher of each lane's last row gathers the lane's tokens and walks the
+ * tree. Otherwise the two calls run one after the other. A bounded wait
+ * that gives up leaves the lane's rows JF_NO_TOKEN and is reported as for
+ * jf_sample. */
+int jf_sample_accept_tree(jf_sampler *sampler, const jf_sample_args *sample,
+                          const jf_accept_tree_args *accept, void *stream);
+
 /* ---- draft selector ---------------------------------------------------- */
 
 /* The DFlash draft's proposal policy: ops::DraftSelector

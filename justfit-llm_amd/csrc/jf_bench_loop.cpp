@@ -3,8 +3,9 @@
 // native caller is measured apart from the Python loop's. Each step issues
 // args[i % n] on `stream`, then optionally the step's acceptance over its
 // tokens (chain: jf_accept_chain; tree: jf_accept_tree, the prepared
-// records), then optionally one token per row counted into tables[i % n]
-// (the engine's commit). Returns the GPU time per step (HIP events around
+// records, or with tree_combined jf_sample_accept_tree for both), then
+// optionally one token per row counted into tables[i % n] (the engine's
+// commit). Returns the GPU time per step (HIP events around
 // the whole loop), the host time per step (wall clock of the issuing loop
 // alone) and, with batch_us set, the mean step time of each run of `batch`
 // steps between events.
@@ -22,7 +23,7 @@ extern "C" int jf_bench_sample_loop(jf_sampler *sampler, const jf_sample_args *a
                                     uint32_t rows, void *stream, double *gpu_us_per_step,
                                     double *host_us_per_step, uint32_t batch, float *batch_us,
                                     const jf_accept_chain_args *chain,
-                                    const jf_accept_tree_args *tree) {
+                                    const jf_accept_tree_args *tree, int tree_combined) {
   if (!sampler || !args || !n || !steps || !gpu_us_per_step || !host_us_per_step) return -1;
   if (batch_us && (!batch || steps % batch)) return -1;
   hipStream_t st = (hipStream_t)stream;
@@ -39,9 +40,13 @@ extern "C" int jf_bench_sample_loop(jf_sampler *sampler, const jf_sample_args *a
   const auto t0 = std::chrono::steady_clock::now();
   if (!rc && hipEventRecord(ev[0], st) != hipSuccess) rc = -2;
   for (uint32_t i = 0; i < steps && !rc; ++i) {
-    rc = jf_sample(sampler, &args[i % n], stream);
+    if (tree && tree_combined) {
+      rc = jf_sample_accept_tree(sampler, &args[i % n], tree, stream);
+    } else {
+      rc = jf_sample(sampler, &args[i % n], stream);
+      if (!rc && tree) rc = jf_accept_tree(sampler, tree, stream);
+    }
     if (!rc && chain) rc = jf_accept_chain(sampler, chain, stream);
-    if (!rc && tree) rc = jf_accept_tree(sampler, tree, stream);
     if (!rc && tables)
       rc = jf_penalty_table_count_rows(tables[i % n], count_rows,
                                        count_tokens + (uint64_t)i * rows, rows, stream);

@@ -190,6 +190,11 @@ struct FastRows {
 };
 // The argument a uniform launch passes in FastRows' place.
 struct NoRows {};
+// The fast selection's last argument, naming what its finishing blocks do
+// beyond selecting: nothing more, draw rows with no cut (UncutFinish), or
+// (an AcceptTreeLaunch) run each lane's tree acceptance.
+struct NoFinish {};
+struct UncutFinish {};
 constexpr uint32_t kExtraOffsetMask = (1u << 27) - 1u;
 
 // Multi-pass stages, in launch order.
@@ -366,9 +371,12 @@ typedef int (*ParamUpload)(void *ctx, const RowParams *params, uint32_t rows,
 // The body of jf_sample over a given scratch (jf_sampler.cpp): validates the
 // call, builds each row's parameters into `params` (host, args->rows
 // entries), hands them to `upload`, then enqueues the kernels on `stream`.
+// accept: the lanes' tree acceptance to run in the selection's launch if it
+// can (*accepted tells whether it did), or NULL.
 int sample_core(uint32_t vocabulary, const SampleScratch &scratch,
                 const jf_sample_args *args, RowParams *params, ParamUpload upload,
-                void *upload_ctx, void *stream);
+                void *upload_ctx, void *stream, const AcceptTreeLaunch *accept = nullptr,
+                bool *accepted = nullptr);
 
 // Launchers (jf_kernels.hip); they return the hipError_t of the launch.
 // With both events set, they record the selection kernel's own start and end.
@@ -380,9 +388,14 @@ int launch_select(const SampleLaunch &a, uint32_t dtype, void *stream,
 // extras: some row of the launch has extra penalty tokens (fr->row_extra).
 // fuse_uncut: every row is sampled with no cut, draft, penalty or extra
 // token and no kept outputs are asked for: each row's last chunk block draws
-// it (no uncut_kernel launch).
+// it (no uncut_kernel launch). accept: the lanes' tree acceptance over this
+// launch's rows (greedy lanes, rows = lanes x rows_per_lane), run by the
+// row finishers when the launch is uniform, all greedy and finished by
+// each row's last chunk; *accepted tells whether it was (else the caller
+// launches it).
 int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, uint32_t dtype,
-                       const RowParams *uniform, bool extras, bool fuse_uncut, void *stream,
+                       const RowParams *uniform, bool extras, bool fuse_uncut,
+                       const AcceptTreeLaunch *accept, bool *accepted, void *stream,
                        void *start_event = nullptr, void *stop_event = nullptr);
 int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream);
 // wide: some cut row of the launch has no min-p floor (longer candidate

@@ -2070,6 +2070,92 @@ __device__ __forceinline__ uint32_t pick_slice(uint64_t vg, uint32_t G, uint64_t
   return g;
 }
 
+// finish_acceptance (sampling.metal:1381-1392) on a wave that holds the
+// lane's output token t in thread t: the budget min(accepted + 1,
+// remaining), then cut after the first stop token within it.
+__device__ __forceinline__ uint32_t finish_kept(uint32_t out, uint32_t accepted,
+                                                uint32_t remaining, uint32_t stop0,
+                                                uint32_t stop1) {
+  const uint32_t t = lane_id();
+  uint32_t kept = min(accepted + 1, remaining);
+  const uint64_t stops = ballot(t < kept && (out == stop0 || out == stop1));
+  if (stops) kept = (uint32_t)__builtin_ctzll(stops) + 1;
+  return kept;
+}
+
+// verify_tree_accept (tree.metal:20-84), on a wave whose thread t holds
+// row t's target token `tok` (and, sampled, its p(draft) pv and uniform uv
+// of slot 8 + t). From row 0, while the path is shorter than 8: a sampled
+// lane's chain row (current + 1 < chain_rows) takes its chain child when
+// u[8 + current] q < p; otherwise the lowest row below that is a child of
+// the current row and holds the current row's target token (a sampled
+// lane's chain child excluded) extends the path; none ends it. Returns the
+// path's length; thread i < length holds path[i] in `path`.
+__device__ __forceinline__ uint32_t accept_tree_wave(const TreeLaneParams &tr, uint32_t tok,
+                                                     float pv, float uv, uint32_t &path) {
+  const uint32_t t = lane_id();
+  const uint32_t rows = tr.rows, chain = tr.chain_rows;
+  const bool sampled = tr.sampled != 0;
+  const uint32_t par = t < rows ? tr.parent[t] : kNoToken;
+  const uint32_t dtok = t < rows ? tr.token[t] : kNoToken;
+  uint32_t length = 1, current = 0;
+  path = 0;
+  while (length < 8) {
+    if (sampled && current + 1 < chain) {
+      // Rows 0 .. chain - 1 form a chain (checked by the host), so the
+      // chain steps keep current below 7.
+      const float q = tr.chain_q[min(current, 7u)];
+      const float p = __builtin_bit_cast(float, readlane_u32(__builtin_bit_cast(uint32_t, pv),
+                                                             (int)current));
+      const float u = __builtin_bit_cast(float, readlane_u32(__builtin_bit_cast(uint32_t, uv),
+                                                             (int)current));
+      if (u * q < p) {
+        if (t == length) path = current + 1;
+        ++length;
+        ++current;
+        continue;
+      }
+    }
+    const uint32_t wanted = readlane_u32(tok, (int)current);
+    const bool hit = t > current && t < rows && par == current && dtok == wanted &&
+                     !(sampled && t == current + 1 && current + 1 < chain);
+    const uint64_t b = ballot(hit);
+    if (!b) break;
+    current = (uint32_t)__builtin_ctzll(b);
+    if (t == length) path = current;
+    ++length;
+  }
+  return length;
+}
+
+// Thread i < length: path row i emits its child's token (path[i + 1]) or,
+// the last, its own target token (the value for threads past the path is
+// not used).
+__device__ __forceinline__ uint32_t tree_path_token(const TreeLaneParams &tr, uint32_t tok,
+                                                    uint32_t path, uint32_t length) {
+  const uint32_t t = lane_id();
+  const uint32_t dtok = t < tr.rows ? tr.token[t] : kNoToken;
+  const uint32_t next = __shfl_down(path, 1);
+  const uint32_t child_tok = __shfl(dtok, (int)next);
+  const uint32_t own_tok = __shfl(tok, (int)path);
+  return t + 1 < length ? child_tok : own_tok;
+}
+
+// The lane's retained and accepted counts and its path rows, from the wave
+// whose thread t holds output token `out` and path row `path`.
+__device__ __forceinline__ void finish_tree_lane(const AcceptTreeLaunch &a, uint32_t lane,
+                                                 const TreeLaneParams &tr, uint32_t out,
+                                                 uint32_t path, uint32_t length) {
+  const uint32_t t = lane_id();
+  const uint32_t kept = finish_kept(out, length - 1, tr.remaining, a.stop0, a.stop1);
+  const uint32_t last = readlane_u32(path, (int)(length - 1));
+  if (t < 8) a.path_rows[(uint64_t)lane * 8 + t] = t < length ? path : last;
+  if (t == 0) {
+    a.retained[lane] = kept;
+    a.accepted[lane] = length - 1;
+  }
+}
+
 // ---- the fast selection kernel ---------------------------------------------
 //
 // select_kernel's results for the rows the host admits (16-byte aligned rows,
@@ -2257,9 +2343,12 @@ __device__ __forceinline__ uint32_t past_end_bits(uint32_t V, uint32_t base) {
 // that every wait ends has failed), the row gets JF_NO_TOKEN, the sampler's
 // status word is set for the host to report, and the words are left for
 // the host's clear.
-__device__ __forceinline__ void finish_greedy_row(const SampleLaunch &a, uint32_t row,
+// Returns whether the row finished (its token in `token`, every lane); with
+// `write` false the caller writes the result.
+__device__ __forceinline__ bool finish_greedy_row(const SampleLaunch &a, uint32_t row,
                                                   uint32_t S, uint32_t own, uint64_t mine,
-                                                  uint64_t tag) {
+                                                  uint64_t tag, uint32_t &token,
+                                                  bool write = true) {
   const uint32_t lane = lane_id();
   uint64_t best = 0;
   bool ok = true;
@@ -2271,16 +2360,116 @@ __device__ __forceinline__ void finish_greedy_row(const SampleLaunch &a, uint32_
     ok = (best & 0x1fffu) == tag;
     if (ok) st_dev(word, 0ull);
   }
+  token = kNoToken;
   if (ballot(!ok) != 0) {
     if (lane == 0) {
-      write_result(a, row, kNoToken, 0.0f, 0);
+      if (write) write_result(a, row, kNoToken, 0.0f, 0);
       if (a.status) __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
-    return;
+    return false;
   }
   const uint32_t key = wave_max_u32((uint32_t)(best >> 32));
   const uint32_t low = wave_max_u32((uint32_t)(best >> 32) == key ? (uint32_t)best : 0u);
-  if (lane == 0) write_result(a, row, key ? 0x7ffffu - (low >> 13) : kNoToken, 0.0f, 0);
+  token = key ? 0x7ffffu - (low >> 13) : kNoToken;
+  if (write && lane == 0) write_result(a, row, token, 0.0f, 0);
+  return true;
+}
+
+// All-greedy rows whose lanes' tree acceptance runs in the select launch
+// (the lanes' rows = the launch's rows, R a lane, every lane greedy). Each
+// row's finisher publishes its token as a self-validating word (token << 32
+// | tag) in partial slot kAcceptSlot of the row's chunk 0; the finisher of
+// a lane's last row gathers the lane's tokens (thread t row t, bounded
+// waits, each word returned to zero), writes every row's result (the path's
+// outputs over the first rows, the selected tokens after them) and the
+// lane's counts and path rows. Its waits are for blocks dispatched before
+// it (rows in order, chunk fastest), which wait on nothing but their own
+// rows' earlier blocks. A wait that gives up leaves the lane's rows
+// JF_NO_TOKEN and sets the status word.
+constexpr uint32_t kAcceptSlot = 200;
+// The walk of lane `row / R` by the finisher of its last row, whose own
+// token is `token`; lanes 32 + t of the wave hold row t's published word in
+// `early` (t < R - 1) when the caller gathered them already (have_early),
+// else they are gathered here.
+__device__ __forceinline__ void accept_lane(const SampleLaunch &a, const AcceptTreeLaunch &acc,
+                                            uint32_t row, uint32_t S, uint32_t token, bool ok,
+                                            uint64_t tag, bool have_early, uint64_t early) {
+  const uint32_t t = lane_id();
+  const uint32_t R = acc.rows_per_lane, lane = row / R, first = lane * R;
+  uint32_t tok = token;
+  bool got = ok;
+  if (have_early) {
+    const uint64_t v = shfl_u64(early, (int)(32 + t));
+    if (t + 1 < R) {
+      got = (v & 0x1fffu) == tag;
+      tok = (uint32_t)(v >> 32);
+    }
+  } else if (t + 1 < R) {
+    uint64_t *word = &a.partials[(uint64_t)(first + t) * S].v[kAcceptSlot];
+    uint64_t v = 0;
+    for (uint32_t n = 0; (v & 0x1fffu) != tag && n < a.wait_bound; ++n) v = ld_dev(word);
+    got = (v & 0x1fffu) == tag;
+    if (got) st_dev(word, 0ull);
+    tok = (uint32_t)(v >> 32);
+  }
+  if (ballot(t < R && !got) != 0) {
+    if (t < R) write_result(a, first + t, kNoToken, 0.0f, 0);
+    if (t == 0 && a.status)
+      __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return;
+  }
+  if (t >= R) tok = kNoToken;
+  const TreeLaneParams &tr = acc.trees[lane];
+  uint32_t path;
+  const uint32_t length = accept_tree_wave(tr, tok, 0.0f, 0.0f, path);
+  const uint32_t out = tree_path_token(tr, tok, path, length);
+  if (t < R) write_result(a, first + t, t < length ? out : tok, 0.0f, 0);
+  finish_tree_lane(acc, lane, tr, out, path, length);
+}
+
+// A row's finisher in a launch with the lanes' tree acceptance: a lane's
+// last row gathers its chunk bests (lanes 0 .. S - 1) and, in the same
+// round of reads, the lane's other rows' tokens (lanes 32 .. 32 + R - 2)
+// when the row has at most 32 chunks, then walks the tree; any other row
+// publishes its token.
+__device__ __forceinline__ void finish_row_and_lane(const SampleLaunch &a,
+                                                    const AcceptTreeLaunch &acc, uint32_t row,
+                                                    uint32_t S, uint32_t own, uint64_t mine,
+                                                    uint64_t tag) {
+  const uint32_t t = lane_id();
+  const uint32_t R = acc.rows_per_lane, first = row / R * R;
+  const bool lane_last = row + 1 == first + R;
+  if (!lane_last || S > 32) {
+    uint32_t token;
+    const bool ok = finish_greedy_row(a, row, S, own, mine, tag, token, false);
+    if (!lane_last) {
+      if (ok && t == 0)
+        st_dev(&a.partials[(uint64_t)row * S].v[kAcceptSlot], (uint64_t)token << 32 | tag);
+      return;
+    }
+    accept_lane(a, acc, row, S, token, ok, tag, false, 0ull);
+    return;
+  }
+  uint64_t v = 0;
+  bool ok = true;
+  uint64_t *word = nullptr;
+  if (t == own) v = mine;
+  else if (t < S) word = a.bests + (uint64_t)row * S + t;
+  else if (t >= 32 && t - 32 + 1 < R)
+    word = &a.partials[(uint64_t)(first + t - 32) * S].v[kAcceptSlot];
+  if (word) {
+    for (uint32_t n = 0; (v & 0x1fffu) != tag && n < a.wait_bound; ++n) v = ld_dev(word);
+    ok = (v & 0x1fffu) == tag;
+    if (ok) st_dev(word, 0ull);
+  }
+  const bool row_ok = ballot(t < S && !ok) == 0;
+  const uint32_t hi = t < S ? (uint32_t)(v >> 32) : 0u;
+  const uint32_t key = wave_max_u32(hi);
+  const uint32_t low = wave_max_u32(t < S && hi == key ? (uint32_t)v : 0u);
+  const uint32_t token = key ? 0x7ffffu - (low >> 13) : kNoToken;
+  if (!row_ok && t == 0 && a.status)
+    __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  accept_lane(a, acc, row, S, token, row_ok, tag, true, v);
 }
 
 // select_fast_kernel's arguments as the kernel-argument segment holds them
@@ -2486,17 +2675,19 @@ __device__ __forceinline__ uint32_t fast_row_fact(const R &fr, uint32_t i) {
 // XTRA: the launch's rows may carry extra (verify) penalty tokens, read as
 // scalars from fr.row_extra's place in SampleLaunch::extra. R: FastRows, or
 // NoRows for a uniform launch with no row map and no extra tokens.
-template <int DT, bool XTRA, class R, bool FUSE>
+template <int DT, bool XTRA, class R, class FIN>
 __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     const void *logits, const uint32_t *pen_slots, uint32_t stride, uint32_t V,
     uint32_t packed, uint32_t u_top_k, float u_minp_offset, float u_repetition,
     float u_repetition_inverse, float u_presence, float u_frequency, uint32_t mapped,
-    FastLaunch f, R fr) {
+    FastLaunch f, R fr, FIN fin) {
   constexpr int VEC = Geo<DT>::VEC, TPL = Geo<DT>::TPL, SLAB = Geo<DT>::SLAB,
                 LOADS = Geo<DT>::LOADS;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
   constexpr uint32_t VMASK = (1u << VEC) - 1u;
   constexpr bool kRows = !std::is_same_v<R, NoRows>;
+  constexpr bool FUSE = std::is_same_v<FIN, UncutFinish>;
+  constexpr bool ACCEPT = std::is_same_v<FIN, AcceptTreeLaunch>;
   static_assert(TPL == 32, "one drop bit per register");
   static_assert(kRows || !XTRA, "extra tokens travel in the per-row facts");
   const SampleLaunch &a = fast_launch_record();
@@ -2764,7 +2955,14 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
         if (tid == 0) st_dev(a.bests + (uint64_t)row * S + chunk, mine);
         return;
       }
-      if (w == 0) finish_greedy_row(a, row, S, chunk, mine, tag);
+      if (w == 0) {
+        if constexpr (ACCEPT) {
+          finish_row_and_lane(a, fin, row, S, chunk, mine, tag);
+        } else {
+          uint32_t token;
+          finish_greedy_row(a, row, S, chunk, mine, tag, token);
+        }
+      }
       return;
     }
     // Every row greedy: the row's last block to arrive takes the largest
@@ -2782,7 +2980,10 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
       if (prev == S - 1) st_dev(a.counters + row, 0u);
     }
     __syncthreads();
-    if (s.wcount[0] && w == 0) finish_greedy_row(a, row, S, S, 0ull, tag);
+    if (s.wcount[0] && w == 0) {
+      uint32_t token;
+      finish_greedy_row(a, row, S, S, 0ull, tag, token);
+    }
     return;
   }
 
@@ -4366,19 +4567,6 @@ __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_
 // search or for the leading run of accepted proposals. The result is that
 // of the reference's one-thread loops, step for step.
 
-// finish_acceptance (sampling.metal:1381-1392) on a wave that holds the
-// lane's output token t in thread t: the budget min(accepted + 1,
-// remaining), then cut after the first stop token within it.
-__device__ __forceinline__ uint32_t finish_kept(uint32_t out, uint32_t accepted,
-                                                uint32_t remaining, uint32_t stop0,
-                                                uint32_t stop1) {
-  const uint32_t t = lane_id();
-  uint32_t kept = min(accepted + 1, remaining);
-  const uint64_t stops = ballot(t < kept && (out == stop0 || out == stop1));
-  if (stops) kept = (uint32_t)__builtin_ctzll(stops) + 1;
-  return kept;
-}
-
 // decode_accept_dflash (sampling.metal:1399-1423, 1514-1558). Greedy:
 // the leading proposals equal to the target's tokens. Sampled: the leading
 // proposals that pass u q < p (q the draft's probability of the proposal
@@ -4432,68 +4620,25 @@ __global__ __launch_bounds__(64) void accept_chain_kernel(AcceptChainLaunch a) {
 }
 #endif
 
-// verify_tree_accept (tree.metal:20-84). From row 0, while the path is
-// shorter than 8: a sampled lane's chain row (current + 1 < chain_rows)
-// takes its chain child when u[8 + current] q < p; otherwise the lowest row
-// below that is a child of the current row and holds the current row's
-// target token (a sampled lane's chain child excluded) extends the path;
-// none ends it. Each path row emits its child's token, the last row its own
-// target token; the accepted path's rows go to path_rows.
 #if JF_IN(4)
 __global__ __launch_bounds__(64) void accept_tree_kernel(AcceptTreeLaunch a) {
   const uint32_t lane = blockIdx.x, t = threadIdx.x;
   const TreeLaneParams &tr = a.trees[lane];
-  const uint32_t R = a.rows_per_lane, rows = tr.rows, chain = tr.chain_rows;
-  const bool sampled = tr.sampled != 0;
+  const uint32_t R = a.rows_per_lane;
   uint32_t *tokens = a.target_tokens + (uint64_t)lane * R;
   const uint32_t tok = t < R ? tokens[t] : kNoToken;
   float pv = 0.0f, uv = 0.0f;
-  if (sampled) {
+  if (tr.sampled) {
     if (t < R) pv = a.target_draft_probs[(uint64_t)lane * R + t];
     if (t < 16) uv = a.uniforms[(uint64_t)lane * 40 + 8 + t];
   }
-  const uint32_t par = t < rows ? tr.parent[t] : kNoToken;
-  const uint32_t dtok = t < rows ? tr.token[t] : kNoToken;
-  uint32_t length = 1, current = 0, path = 0;  // thread i holds path[i]
-  while (length < 8) {
-    if (sampled && current + 1 < chain) {
-      // Rows 0 .. chain - 1 form a chain (checked by the host), so the
-      // chain steps keep current below 7.
-      const float q = tr.chain_q[min(current, 7u)];
-      const float p = __builtin_bit_cast(float, readlane_u32(__builtin_bit_cast(uint32_t, pv),
-                                                             (int)current));
-      const float u = __builtin_bit_cast(float, readlane_u32(__builtin_bit_cast(uint32_t, uv),
-                                                             (int)current));
-      if (u * q < p) {
-        if (t == length) path = current + 1;
-        ++length;
-        ++current;
-        continue;
-      }
-    }
-    const uint32_t wanted = readlane_u32(tok, (int)current);
-    const bool hit = t > current && t < rows && par == current && dtok == wanted &&
-                     !(sampled && t == current + 1 && current + 1 < chain);
-    const uint64_t b = ballot(hit);
-    if (!b) break;
-    current = (uint32_t)__builtin_ctzll(b);
-    if (t == length) path = current;
-    ++length;
-  }
-  // Thread i < length: path row i emits its child's token (path[i + 1]) or,
-  // the last, its own target token.
-  const uint32_t next = __shfl_down(path, 1);
-  const uint32_t child_tok = __shfl(dtok, (int)next);
-  const uint32_t own_tok = __shfl(tok, (int)path);
-  const uint32_t out = t + 1 < length ? child_tok : own_tok;
+  uint32_t path;
+  const uint32_t length = accept_tree_wave(tr, tok, pv, uv, path);
+  // Thread i < length: path row i's output; the rows past the path keep
+  // their selected tokens.
+  const uint32_t out = tree_path_token(tr, tok, path, length);
   if (t < length) tokens[t] = out;
-  const uint32_t kept = finish_kept(out, length - 1, tr.remaining, a.stop0, a.stop1);
-  const uint32_t last = readlane_u32(path, (int)(length - 1));
-  if (t < 8) a.path_rows[(uint64_t)lane * 8 + t] = t < length ? path : last;
-  if (t == 0) {
-    a.retained[lane] = kept;
-    a.accepted[lane] = length - 1;
-  }
+  finish_tree_lane(a, lane, tr, out, path, length);
 }
 #endif
 
@@ -4536,9 +4681,9 @@ static uint32_t fast_resident_blocks(uint32_t dtype) {
     const hipError_t e1 =
         dtype == 0
             ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                  &per_cu, select_fast_kernel<0, false, FastRows, false>, kThreads, 0)
+                  &per_cu, select_fast_kernel<0, false, FastRows, NoFinish>, kThreads, 0)
             : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                  &per_cu, select_fast_kernel<1, false, FastRows, false>, kThreads, 0);
+                  &per_cu, select_fast_kernel<1, false, FastRows, NoFinish>, kThreads, 0);
     const hipError_t e2 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     cache[dev][dtype] = e1 == hipSuccess && e2 == hipSuccess && per_cu > 0 && cus > 0
                             ? (uint32_t)per_cu * (uint32_t)cus
@@ -4549,8 +4694,10 @@ static uint32_t fast_resident_blocks(uint32_t dtype) {
 }
 
 int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, uint32_t dtype,
-                       const RowParams *uniform, bool extras, bool fuse_uncut, void *stream,
+                       const RowParams *uniform, bool extras, bool fuse_uncut,
+                       const AcceptTreeLaunch *accept, bool *accepted, void *stream,
                        void *start_event, void *stop_event) {
+  if (accepted) *accepted = false;
   if (f.fuse_greedy == 1u && f.a.chunks > 1 && rows < fast_resident_blocks(dtype)) {
     // Each row's last chunk can wait for the row's other blocks instead of
     // counting arrivals: only those finishers (one a row) ever wait, and
@@ -4558,8 +4705,8 @@ int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, u
     // slot always remains for the blocks they wait for, which never wait.
     FastLaunch g = f;
     g.fuse_greedy = 2u;
-    return launch_select_fast(g, fr, rows, dtype, uniform, extras, fuse_uncut, stream,
-                              start_event, stop_event);
+    return launch_select_fast(g, fr, rows, dtype, uniform, extras, fuse_uncut, accept, accepted,
+                              stream, start_event, stop_event);
   }
   if (!fr && (!uniform || f.mapped || extras)) return (int)hipErrorInvalidValue;
   if (fuse_uncut && (extras || f.mapped)) return (int)hipErrorInvalidValue;
@@ -4570,28 +4717,34 @@ int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, u
   const uint32_t packed = (uniform ? 0x80000000u | (u.flags & 0xffu) : 0u) |
                           (f.a.chunks << 8) | (f.slot_count == 512u ? 0x10000u : 0u) |
                           ((f.row_base >> 8) << 17);
-  auto go = [&](auto kernel, const auto &rows_arg) {
+  auto go = [&](auto kernel, const auto &rows_arg, const auto &fin) {
     hipExtLaunchKernelGGL(kernel, grid, block, 0, st, e0, e1, 0, f.a.logits, f.pen_slots,
                           (uint32_t)f.a.stride, f.a.vocabulary, packed, u.top_k,
                           u.minp_offset, u.repetition, u.repetition_inverse, u.presence,
-                          u.frequency, f.mapped, f, rows_arg);
+                          u.frequency, f.mapped, f, rows_arg, fin);
   };
-  if (fuse_uncut) {
+  // The lanes' tree acceptance rides on the row finishers (each row's last
+  // chunk block) of a uniform all-greedy launch.
+  if (accept && f.fuse_greedy == 2u && !fr && !extras && !f.mapped && f.row_base == 0) {
+    dtype == 0 ? go(select_fast_kernel<0, false, NoRows, AcceptTreeLaunch>, NoRows{}, *accept)
+               : go(select_fast_kernel<1, false, NoRows, AcceptTreeLaunch>, NoRows{}, *accept);
+    if (accepted) *accepted = true;
+  } else if (fuse_uncut) {
     if (!fr)
-      dtype == 0 ? go(select_fast_kernel<0, false, NoRows, true>, NoRows{})
-                 : go(select_fast_kernel<1, false, NoRows, true>, NoRows{});
+      dtype == 0 ? go(select_fast_kernel<0, false, NoRows, UncutFinish>, NoRows{}, UncutFinish{})
+                 : go(select_fast_kernel<1, false, NoRows, UncutFinish>, NoRows{}, UncutFinish{});
     else
-      dtype == 0 ? go(select_fast_kernel<0, false, FastRows, true>, *fr)
-                 : go(select_fast_kernel<1, false, FastRows, true>, *fr);
+      dtype == 0 ? go(select_fast_kernel<0, false, FastRows, UncutFinish>, *fr, UncutFinish{})
+                 : go(select_fast_kernel<1, false, FastRows, UncutFinish>, *fr, UncutFinish{});
   } else if (!fr) {
-    dtype == 0 ? go(select_fast_kernel<0, false, NoRows, false>, NoRows{})
-               : go(select_fast_kernel<1, false, NoRows, false>, NoRows{});
+    dtype == 0 ? go(select_fast_kernel<0, false, NoRows, NoFinish>, NoRows{}, NoFinish{})
+               : go(select_fast_kernel<1, false, NoRows, NoFinish>, NoRows{}, NoFinish{});
   } else if (dtype == 0) {
-    extras ? go(select_fast_kernel<0, true, FastRows, false>, *fr)
-           : go(select_fast_kernel<0, false, FastRows, false>, *fr);
+    extras ? go(select_fast_kernel<0, true, FastRows, NoFinish>, *fr, NoFinish{})
+           : go(select_fast_kernel<0, false, FastRows, NoFinish>, *fr, NoFinish{});
   } else {
-    extras ? go(select_fast_kernel<1, true, FastRows, false>, *fr)
-           : go(select_fast_kernel<1, false, FastRows, false>, *fr);
+    extras ? go(select_fast_kernel<1, true, FastRows, NoFinish>, *fr, NoFinish{})
+           : go(select_fast_kernel<1, false, FastRows, NoFinish>, *fr, NoFinish{});
   }
   return (int)hipGetLastError();
 }

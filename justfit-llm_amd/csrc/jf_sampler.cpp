@@ -627,7 +627,8 @@ namespace jf {
 
 int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
                 RowParams *params, ParamUpload upload, void *upload_ctx,
-                void *stream) {
+                void *stream, const AcceptTreeLaunch *accept, bool *accepted) {
+  if (accepted) *accepted = false;
   int rc = JF_OK;
   const uint32_t rows = a->rows;
   if (!rows || rows > sc.max_rows)
@@ -916,8 +917,11 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
         }
       }
       const bool first = i0 == 0 && !split, last = i0 + n == n_fast;
+      // The lanes' tree acceptance in this launch: all rows greedy, one launch.
+      const bool with_accept = accept && fused && !split && n == rows;
       e = jf::launch_select_fast(F, rows_arg ? &s_rows : nullptr, n, a->dtype,
-                                 uniform ? &p0 : nullptr, extras, fuse_uncut, stream,
+                                 uniform ? &p0 : nullptr, extras, fuse_uncut,
+                                 with_accept ? accept : nullptr, accepted, stream,
                                  first ? a->select_start_event : nullptr,
                                  last ? a->select_done_event : nullptr);
     }
@@ -1022,12 +1026,21 @@ static int take_status(jf_sampler *s, void *stream) {
               "that call's rows affected hold JF_NO_TOKEN");
 }
 
+static int sample_impl(jf_sampler *s, const jf_sample_args *a, void *stream,
+                       const jf::AcceptTreeLaunch *accept, bool *accepted);
+
 int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
   if (!s || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler or arguments");
   int rc = check_device(s->device);
   if (rc != JF_OK) return rc;
   rc = take_status(s, stream);
   if (rc != JF_OK) return rc;
+  return sample_impl(s, a, stream, nullptr, nullptr);
+}
+
+// jf_sample's body after the device and status checks.
+static int sample_impl(jf_sampler *s, const jf_sample_args *a, void *stream,
+                       const jf::AcceptTreeLaunch *accept, bool *accepted) {
   if (!a->rows || a->rows > s->max_rows)
     return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling batch width");
   s->epoch = s->epoch % 4095u + 1u;
@@ -1042,7 +1055,7 @@ int jf_sample(jf_sampler *s, const jf_sample_args *a, void *stream) {
     }
   }
   return jf::sample_core(s->vocabulary, sc, a, s->host_params.data(), sampler_upload, s,
-                         stream);
+                         stream, accept, accepted);
 }
 
 int jf_sampler_status(jf_sampler *s, void *stream) {
@@ -1112,10 +1125,8 @@ int jf_accept_chain(jf_sampler *s, const jf_accept_chain_args *a,
   return JF_OK;
 }
 
-int jf_accept_tree(jf_sampler *s, const jf_accept_tree_args *a, void *stream) {
-  if (!s || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler or arguments");
-  int rc = check_device(s->device);
-  if (rc != JF_OK) return rc;
+// Checks a tree acceptance call (any_sampled: some lane samples).
+static int check_tree_args(jf_sampler *s, const jf_accept_tree_args *a, bool *any_sampled) {
   if (!a->lanes || a->lanes > s->max_rows || !a->trees || !a->maximum_retained ||
       !a->policies)
     return fail(JF_ERR_INVALID_ARGUMENT, "invalid tree acceptance batch");
@@ -1124,7 +1135,7 @@ int jf_accept_tree(jf_sampler *s, const jf_accept_tree_args *a, void *stream) {
   if (!a->target_tokens || !a->retained_counts || !a->accepted_counts ||
       !a->path_rows)
     return fail(JF_ERR_INVALID_ARGUMENT, "null acceptance buffer");
-  bool any_sampled = false;
+  *any_sampled = false;
   for (uint32_t l = 0; l < a->lanes; ++l) {
     const jf_tree_lane &t = a->trees[l];
     if (!t.rows || t.rows > a->rows_per_lane || t.chain_rows > t.rows)
@@ -1140,43 +1151,84 @@ int jf_accept_tree(jf_sampler *s, const jf_accept_tree_args *a, void *stream) {
     const uint32_t m = a->maximum_retained[l];
     if (!m || m > JF_TREE_MAXIMUM_DEPTH)
       return fail(JF_ERR_INVALID_ARGUMENT, "invalid tree retention limit");
-    any_sampled |= a->policies[l].temperature > 0.0f;
+    *any_sampled |= a->policies[l].temperature > 0.0f;
   }
-  if (any_sampled && (!a->target_draft_probs || !a->uniforms))
+  if (*any_sampled && (!a->target_draft_probs || !a->uniforms))
     return fail(JF_ERR_INVALID_ARGUMENT,
                 "sampled tree acceptance needs probabilities and uniforms");
-  // The lanes' trees travel in the kernel arguments, kTreeLanesPerLaunch
-  // lanes a launch: nothing is uploaded.
+  return JF_OK;
+}
+
+// The launch record of lanes l0 .. l0 + n - 1 (n <= kTreeLanesPerLaunch):
+// their trees travel in the kernel arguments, nothing is uploaded.
+static void fill_tree_launch(const jf_accept_tree_args *a, uint32_t l0, uint32_t n,
+                             jf::AcceptTreeLaunch &L) {
   const uint32_t R = a->rows_per_lane;
-  jf::AcceptTreeLaunch L;
   L.rows_per_lane = R;
   L.stop0 = a->stop_token_0;
   L.stop1 = a->stop_token_1;
+  L.lanes = n;
+  L.target_draft_probs =
+      a->target_draft_probs ? a->target_draft_probs + (uint64_t)l0 * R : nullptr;
+  L.uniforms = a->uniforms ? a->uniforms + (uint64_t)l0 * 40 : nullptr;
+  L.target_tokens = a->target_tokens + (uint64_t)l0 * R;
+  L.retained = a->retained_counts + l0;
+  L.accepted = a->accepted_counts + l0;
+  L.path_rows = a->path_rows + (uint64_t)l0 * 8;
+  for (uint32_t i = 0; i < n; ++i) {
+    const jf_tree_lane &t = a->trees[l0 + i];
+    jf::TreeLaneParams &p = L.trees[i];
+    p.rows = t.rows;
+    p.chain_rows = t.chain_rows;
+    p.remaining = a->maximum_retained[l0 + i];
+    p.sampled = a->policies[l0 + i].temperature > 0.0f ? 1u : 0u;
+    std::memcpy(p.parent, t.parent, sizeof(p.parent));
+    std::memcpy(p.token, t.token, sizeof(p.token));
+    std::memcpy(p.chain_q, t.chain_q, sizeof(p.chain_q));
+  }
+}
+
+static int accept_tree_checked(const jf_accept_tree_args *a, void *stream) {
+  jf::AcceptTreeLaunch L;
   for (uint32_t l0 = 0; l0 < a->lanes; l0 += jf::kTreeLanesPerLaunch) {
-    const uint32_t n = std::min(a->lanes - l0, jf::kTreeLanesPerLaunch);
-    L.lanes = n;
-    L.target_draft_probs =
-        a->target_draft_probs ? a->target_draft_probs + (uint64_t)l0 * R : nullptr;
-    L.uniforms = a->uniforms ? a->uniforms + (uint64_t)l0 * 40 : nullptr;
-    L.target_tokens = a->target_tokens + (uint64_t)l0 * R;
-    L.retained = a->retained_counts + l0;
-    L.accepted = a->accepted_counts + l0;
-    L.path_rows = a->path_rows + (uint64_t)l0 * 8;
-    for (uint32_t i = 0; i < n; ++i) {
-      const jf_tree_lane &t = a->trees[l0 + i];
-      jf::TreeLaneParams &p = L.trees[i];
-      p.rows = t.rows;
-      p.chain_rows = t.chain_rows;
-      p.remaining = a->maximum_retained[l0 + i];
-      p.sampled = a->policies[l0 + i].temperature > 0.0f ? 1u : 0u;
-      std::memcpy(p.parent, t.parent, sizeof(p.parent));
-      std::memcpy(p.token, t.token, sizeof(p.token));
-      std::memcpy(p.chain_q, t.chain_q, sizeof(p.chain_q));
-    }
+    fill_tree_launch(a, l0, std::min(a->lanes - l0, jf::kTreeLanesPerLaunch), L);
     const int e = jf::launch_accept_tree(L, stream);
     if (e != hipSuccess) return hip_fail((hipError_t)e, "tree acceptance launch");
   }
   return JF_OK;
+}
+
+int jf_accept_tree(jf_sampler *s, const jf_accept_tree_args *a, void *stream) {
+  if (!s || !a) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler or arguments");
+  int rc = check_device(s->device);
+  if (rc != JF_OK) return rc;
+  bool any_sampled;
+  rc = check_tree_args(s, a, &any_sampled);
+  if (rc != JF_OK) return rc;
+  return accept_tree_checked(a, stream);
+}
+
+int jf_sample_accept_tree(jf_sampler *s, const jf_sample_args *sa,
+                          const jf_accept_tree_args *ta, void *stream) {
+  if (!s || !sa || !ta) return fail(JF_ERR_INVALID_ARGUMENT, "null sampler or arguments");
+  int rc = check_device(s->device);
+  if (rc != JF_OK) return rc;
+  rc = take_status(s, stream);
+  if (rc != JF_OK) return rc;
+  bool any_sampled;
+  rc = check_tree_args(s, ta, &any_sampled);
+  if (rc != JF_OK) return rc;
+  // In the selection's launch when the lanes are greedy, take the
+  // selection's rows in order and fit one launch record.
+  const bool fusable = !any_sampled && ta->lanes <= jf::kTreeLanesPerLaunch &&
+                       (uint64_t)ta->lanes * ta->rows_per_lane == sa->rows &&
+                       ta->target_tokens == sa->out_tokens;
+  jf::AcceptTreeLaunch L;
+  if (fusable) fill_tree_launch(ta, 0, ta->lanes, L);
+  bool accepted = false;
+  rc = sample_impl(s, sa, stream, fusable ? &L : nullptr, &accepted);
+  if (rc != JF_OK) return rc;
+  return accepted ? JF_OK : accept_tree_checked(ta, stream);
 }
 
 // ---- draft selector ----------------------------------------------------------

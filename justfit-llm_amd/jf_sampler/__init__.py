@@ -35,7 +35,7 @@ EXPORTS = [
     "jf_penalty_table_create", "jf_penalty_table_destroy",
     "jf_penalty_table_rebuild", "jf_penalty_table_count", "jf_penalty_table_count_rows",
     "jf_next_uniform", "jf_stage_sampling_cycle", "jf_sample", "jf_sample_static",
-    "jf_accept_chain", "jf_accept_tree",
+    "jf_accept_chain", "jf_accept_tree", "jf_sample_accept_tree",
     "jf_draft_selector_create", "jf_draft_selector_destroy", "jf_draft_select",
     "jf_tree_gather", "jf_build_draft_tree", "jf_mask_request_encode",
     "jf_mask_response_decode", "jf_mask_rows_check", "jf_mask_chain_fill", "jf_mask_tree_fill",
@@ -188,6 +188,8 @@ def lib():
                                       c_vp]
         L.jf_accept_tree.argtypes = [c_vp, ctypes.POINTER(JfAcceptTreeArgs),
                                      c_vp]
+        L.jf_sample_accept_tree.argtypes = [c_vp, ctypes.POINTER(JfSampleArgs),
+                                            ctypes.POINTER(JfAcceptTreeArgs), c_vp]
         L.jf_draft_selector_create.argtypes = [c_u32, c_u32, ctypes.POINTER(c_vp)]
         L.jf_draft_selector_destroy.argtypes = [c_vp]
         L.jf_draft_select.argtypes = [c_vp, ctypes.POINTER(JfDraftSelectArgs), c_vp]
@@ -484,6 +486,12 @@ class Sampler:
     def accept_tree(self, **kwargs):
         a, keep = self.accept_tree_args(**kwargs)
         check(lib().jf_accept_tree(self.handle, ctypes.byref(a), _stream()))
+
+    def launch_sample_accept_tree(self, sample_args, tree_args, stream=None):
+        """jf_sample_accept_tree over prepared JfSampleArgs and JfAcceptTreeArgs."""
+        check(lib().jf_sample_accept_tree(self.handle, ctypes.byref(sample_args),
+                                          ctypes.byref(tree_args),
+                                          _stream() if stream is None else stream))
 
     def close(self):
         if self.handle:

@@ -179,3 +179,123 @@ def test_c4_tree_sampled(plant):
         assert u32(acc)[k] == want_a and u32(ret)[k] == want_r
         np.testing.assert_array_equal(u32(path)[k], want_p)
         np.testing.assert_array_equal(u32(tt)[k, :want_r], want_t[:want_r])
+
+
+def _random_trees(rng, lanes, R, argmax):
+    """Trees of R rows in preorder (each parent an earlier row), their tokens
+    planted with the parent row's argmax 60% of the time (greedy walks go
+    deep), and the lanes' argmax rows."""
+    trees, toks = [], []
+    for q in range(lanes):
+        parent = [NO] + [int(rng.integers(0, r)) for r in range(1, R)]
+        tok = rng.integers(0, 1000, R).astype(np.uint32)
+        for r in range(1, R):
+            if rng.random() < 0.6:
+                tok[r] = argmax[q * R + parent[r]]
+        trees.append(parent)
+        toks.append(tok)
+    return trees, toks
+
+
+@pytest.mark.parametrize("case", ["c4", "c4_planted", "r8_stops", "fallback_17_lanes"])
+def test_sample_accept_tree_one_call(case):
+    """jf_sample_accept_tree against jf_sample then jf_accept_tree on a second
+    sampler: every row's token, each lane's retained and accepted counts and
+    path rows equal. Greedy lanes over the selection's rows take one launch
+    (each lane's last row finisher walks the tree); 17 lanes take the two
+    calls. The full C4 tree step (16 lanes x 16 rows), with and without
+    planted deep paths; 12 lanes x 8 rows with stop tokens on the paths."""
+    import torch
+    rng = np.random.default_rng(len(case))
+    if case.startswith("c4"):
+        c, tokens = c4_inputs(case == "c4_planted")
+        V, R, lanes = c["V"], 16, len(c["trees"])
+        x = c["logits"]
+        trees = [J.tree_lane(c["trees"][q], tokens[q]) for q in range(lanes)]
+        stops = (NO, NO)
+    else:
+        V = 151936
+        R, lanes = 8, (12 if case == "r8_stops" else 17)
+        x = rng.normal(0, 2.0, (lanes * R, V)).astype(np.float32)
+        am = x.argmax(axis=1)
+        par, toks = _random_trees(rng, lanes, R, am)
+        trees = [J.tree_lane(par[q], toks[q]) for q in range(lanes)]
+        stops = (int(am[3]), int(am[R + 1])) if case == "r8_stops" else (NO, NO)
+    rows = lanes * R
+    print(f"case {case}: {lanes} lanes x {R} rows, V={V}", flush=True)
+    pols = [J.policy()] * rows
+    lg = torch.from_numpy(x).cuda()
+    results = []
+    for combined in (True, False):
+        s = J.Sampler(V, rows)
+        out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+        ret = torch.full((lanes,), -1, dtype=torch.int32, device="cuda")
+        acc = torch.full((lanes,), -1, dtype=torch.int32, device="cuda")
+        path = torch.full((lanes, 8), -1, dtype=torch.int32, device="cuda")
+        sa, keep_s = s.sample_args(lg, pols, out)
+        ta, keep_t = s.accept_tree_args(
+            trees=trees, rows_per_lane=R, target_tokens=out.view(lanes, R), retained=ret,
+            accepted=acc, path_rows=path, maximum_retained=[8] * lanes,
+            policies=[J.policy()] * lanes, stop_tokens=stops)
+        for _ in range(2):  # twice: the words each call leaves are zero again
+            if combined:
+                s.launch_sample_accept_tree(sa, ta)
+            else:
+                s.launch(sa)
+                s.launch_accept(("tree", ta, keep_t))
+        torch.cuda.synchronize()
+        results.append([u32(out).copy(), u32(ret).copy(), u32(acc).copy(), u32(path).copy()])
+        s.close()
+    for got, want in zip(*results):
+        np.testing.assert_array_equal(got, want)
+    # and the oracle's walk over the oracle's tokens
+    want_tok = run_oracle(V, pols, logits=x)["tokens"]
+    for q in range(lanes):
+        par = list(trees[q].parent)[:trees[q].rows]
+        tk = list(trees[q].token)[:trees[q].rows]
+        wt, wr, wa, wp = O.accept_tree(par, tk, 0, None, 8, False,
+                                       want_tok[q * R:(q + 1) * R], stop=stops)
+        assert results[0][1][q] == wr and results[0][2][q] == wa, (q, wr, wa)
+        np.testing.assert_array_equal(results[0][3][q], wp)
+        np.testing.assert_array_equal(results[0][0][q * R:q * R + wr], wt[:wr])
+
+
+def test_sample_accept_tree_expired_wait():
+    """The combined call's bounded waits: with a bound of 0 every row's
+    finisher gives up, the lanes' rows hold JF_NO_TOKEN and the status is
+    reported once as JF_ERR_DEVICE; at the default bound the next calls are
+    bit-exact again."""
+    import torch
+    c, tokens = c4_inputs(True)
+    V, R, lanes = c["V"], 16, len(c["trees"])
+    rows = lanes * R
+    pols = [J.policy()] * rows
+    lg = torch.from_numpy(c["logits"]).cuda()
+    trees = [J.tree_lane(c["trees"][q], tokens[q]) for q in range(lanes)]
+    s = J.Sampler(V, rows)
+    out = torch.full((rows,), -1, dtype=torch.int32, device="cuda")
+    ret = torch.zeros(lanes, dtype=torch.int32, device="cuda")
+    acc = torch.zeros(lanes, dtype=torch.int32, device="cuda")
+    path = torch.zeros((lanes, 8), dtype=torch.int32, device="cuda")
+    sa, keep_s = s.sample_args(lg, pols, out)
+    ta, keep_t = s.accept_tree_args(
+        trees=trees, rows_per_lane=R, target_tokens=out.view(lanes, R), retained=ret,
+        accepted=acc, path_rows=path, maximum_retained=[8] * lanes,
+        policies=[J.policy()] * lanes)
+    s.launch_sample_accept_tree(sa, ta)
+    torch.cuda.synchronize()
+    want = [u32(out).copy(), u32(ret).copy(), u32(acc).copy(), u32(path).copy()]
+    s.set_wait_bound(0)
+    s.launch_sample_accept_tree(sa, ta)
+    torch.cuda.synchronize()
+    assert np.all(u32(out) == NO)
+    with pytest.raises(J.JfError) as e:
+        s.status()
+    assert e.value.code == J.JF_ERR_DEVICE
+    s.set_wait_bound(1 << 20)
+    for _ in range(2):
+        s.launch_sample_accept_tree(sa, ta)
+        torch.cuda.synchronize()
+        for g, w in zip([u32(out), u32(ret), u32(acc), u32(path)], want):
+            np.testing.assert_array_equal(g, w)
+    s.status()
