@@ -5,7 +5,8 @@ oracle row by row (bit-exact tokens, and the draft probabilities where the
 step writes them). C2 and C5 run as benchmarked, without kept outputs or
 draft probabilities; C1, C3 and C4 greedy and sampled as the bench issues
 them, C4's selection and then its tree acceptance (retained and accepted
-counts, path rows, the accepted tokens); C2 also with histories clustered
+counts, path rows, the accepted tokens), as two calls and as the step the
+bench times (jf_sample_accept_tree); C2 also with histories clustered
 in low ids (every row, and every fourth row), which widen the penalty
 table's fixed slots from 256 to 512 a chunk; and the penalized chain-verify
 step (4 lanes x 16 rows, V = 248,320: extras, sparse drafts, then chain
@@ -68,6 +69,12 @@ def test_benchmarked_step_matches_oracle(cfg, mode, history):
         assert np.all(got != NO)
         if g.accept is not None:
             _check_tree_acceptance(g, w, want)
+            # The step as benchmarked: jf_sample_accept_tree (one launch for
+            # greedy lanes), the same results.
+            g.out.fill_(-1)
+            g.step(i)
+            torch.cuda.synchronize()
+            _check_tree_acceptance(g, w, want, launch=False)
         if g.draft_probs is not None:
             c = w["tree"]
             drafted = np.array([r < WL.chain_length(c["trees"][k]) - 1
@@ -79,16 +86,18 @@ def test_benchmarked_step_matches_oracle(cfg, mode, history):
     torch.cuda.empty_cache()
 
 
-def _check_tree_acceptance(g, w, want):
-    """The rest of C4's step: jf_accept_tree over the selected tokens, against
-    the oracle's walk of each request's tree."""
+def _check_tree_acceptance(g, w, want, launch=True):
+    """The rest of C4's step: jf_accept_tree over the selected tokens (or,
+    launch False, the results the step left), against the oracle's walk of
+    each request's tree."""
     import torch
     import oracle as O
     c = w["tree"]
     rq = len(c["trees"])
     per = w["rows"] // rq
-    g.sampler.launch_accept(g.accept)
-    torch.cuda.synchronize()
+    if launch:
+        g.sampler.launch_accept(g.accept)
+        torch.cuda.synchronize()
     tt = g.out.cpu().numpy().view(np.uint32).reshape(rq, per)
     ret = g.acc_out[0].cpu().numpy()
     acc = g.acc_out[1].cpu().numpy()
