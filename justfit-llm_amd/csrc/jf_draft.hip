@@ -42,7 +42,6 @@ __device__ __forceinline__ float bf16f(uint32_t b) { return u2f(b << 16); }
 __device__ __forceinline__ float readlane_f32(float v, int l) {
   return u2f(readlane_u32(f2u(v), l));
 }
-__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // (key << 32 | ~id): larger means earlier in (value desc, id asc); ids are
 // unique within a row, so the order is total. 0 is the empty slot
@@ -59,6 +58,39 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   step(xor_u64<8>(v));
   step(xor_u64<16>(v));
   step(xor_u64<32>(v));
+  return v;
+}
+// The largest of a 32-bit value over each 16-lane row, in every lane of the
+// row: DPP quad permutes, then row rotations by 4 and 8.
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false));
+  return v;
+}
+// The largest over the wave (WIDE) or over lanes 0..31 when lanes 32..63
+// hold nothing larger. Across rows by gfx950's lane swaps, VALU work with no
+// LDS crossbar: v_permlane16_swap leaves each lane one value of each row of
+// its row pair (rows 0,1 and 2,3), v_permlane32_swap one of each half.
+template <bool WIDE>
+__device__ __forceinline__ uint32_t lanes_max_u32(uint32_t v) {
+  v = row_max_u32(v);
+  const auto rows = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max((uint32_t)rows[0], (uint32_t)rows[1]);
+  if constexpr (WIDE) {
+    const auto halves = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = max((uint32_t)halves[0], (uint32_t)halves[1]);
+  }
+  return v;
+}
+// The largest value of each 16-lane row, in every lane of the row (DPP
+// only): the wave's largest when every row holds the same 16 values.
+__device__ __forceinline__ float row_max_f32(float v) {
+  v = __builtin_fmaxf(v, xor_f32<1>(v));
+  v = __builtin_fmaxf(v, xor_f32<2>(v));
+  v = __builtin_fmaxf(v, xor_f32<4>(v));
+  v = __builtin_fmaxf(v, xor_f32<8>(v));
   return v;
 }
 
@@ -205,27 +237,54 @@ __global__ __launch_bounds__(kThreads) void draft_top16_kernel(DraftLaunch d) {
 }
 
 // The top 16 of one proposal row from its chunks' lists (each in rank
-// order), by one wave: lane c holds chunk c's head (S <= 64) and 16 rounds
-// pop the largest head. A head past its list's entries is 0 and never wins
-// a real entry; once every head is 0 the remaining slots stay empty.
-// `comp`/`vbits` are the row's partials in LDS.
+// order), by one wave: lane c holds chunk c's head (S <= 64, S <= 32 unless
+// WIDE) and 16 rounds pop the largest head, comparing the value keys first
+// and, where several heads share the largest, the ids. A head past its
+// list's entries is 0 and never wins (a real entry's value key is nonzero);
+// once every head is 0 the remaining slots stay empty. `comp`/`vbits` are
+// the row's partials in LDS.
+template <bool WIDE>
 __device__ __forceinline__ void draft_merge_row(const uint64_t *comp, const uint32_t *vbits,
                                                 uint32_t S, uint32_t *ids, float *values) {
   const uint32_t lane = lane_id();
   uint32_t head = 0;
-  uint64_t hc = lane < S ? comp[lane * kDraftK] : 0ull;
+  // Each list's head and the entry after it. Every round reads the entry
+  // after that, which lands while the round compares heads (past the
+  // list's end it reads the last entry; the win that would take it there
+  // takes 0 instead). Lanes past S hold 0 and never win.
+  const bool live = lane < S;
+  uint64_t hc = live ? comp[lane * kDraftK] : 0ull;
+  uint64_t hn = live ? comp[lane * kDraftK + 1] : 0ull;
+  // Lane r < 16 collects slot r: its id and where its value bits lie.
+  uint32_t my_id = kNoToken, my_at = ~0u;
   for (uint32_t r = 0; r < kDraftK; ++r) {
-    const uint64_t best = wave_max_u64(hc);
-    if (best != 0 && hc == best) {
-      ids[r] = ~(uint32_t)best;
-      values[r] = u2f(vbits[lane * kDraftK + head]);
+    const uint64_t after = comp[lane * kDraftK + min(head + 2, kDraftK - 1)];
+    const uint32_t hi = (uint32_t)(hc >> 32);
+    // top == 0: every list is spent; every lane then ties on (0, 0), lane
+    // 0 takes the round and the slot stays empty.
+    const uint32_t top = __builtin_amdgcn_readfirstlane(lanes_max_u32<WIDE>(hi));
+    uint64_t at = ballot(hi == top);
+    if (__builtin_popcountll(at) > 1) {
+      const uint32_t lo = hi == top ? (uint32_t)hc : 0u;
+      const uint32_t lo_top = __builtin_amdgcn_readfirstlane(lanes_max_u32<WIDE>(lo));
+      at = ballot(hi == top && (uint32_t)hc == lo_top);
+    }
+    const uint32_t winner = (uint32_t)__builtin_ctzll(at);
+    const uint32_t id = ~readlane_u32((uint32_t)hc, (int)winner);
+    const uint32_t entry = winner * kDraftK + readlane_u32(head, (int)winner);
+    if (lane == r && top != 0) {
+      my_id = id;
+      my_at = entry;
+    }
+    if (lane == winner) {
       ++head;
-      hc = head < kDraftK ? comp[lane * kDraftK + head] : 0ull;
+      hc = head < kDraftK ? hn : 0ull;
+      hn = after;
     }
-    if (best == 0 && lane == 0) {
-      ids[r] = kNoToken;
-      values[r] = -__builtin_inff();
-    }
+  }
+  if (lane < kDraftK) {
+    ids[lane] = my_id;
+    values[lane] = my_at != ~0u ? u2f(vbits[my_at]) : -__builtin_inff();
   }
 }
 
@@ -239,7 +298,6 @@ struct __align__(16) DraftEdgeLds {
   float vals[2][kDraftK];
   uint32_t pred[kDraftK];
   uint32_t cand[kDraftK];
-  float walk[2 * kDraftK];  // the walk's weights, then quotients, in candidate order
   uint32_t last;
 };
 
@@ -286,7 +344,12 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   s.hid[tid] = bf16f(h[tid]);
   __syncthreads();
   const uint32_t wave = tid >> 6;
-  if (wave < rows_here) draft_merge_row(s.pcomp[wave], s.pvbits[wave], S, s.ids[wave], s.vals[wave]);
+  if (wave < rows_here) {
+    if (S > 32)
+      draft_merge_row<true>(s.pcomp[wave], s.pvbits[wave], S, s.ids[wave], s.vals[wave]);
+    else
+      draft_merge_row<false>(s.pcomp[wave], s.pvbits[wave], S, s.ids[wave], s.vals[wave]);
+  }
   __syncthreads();
   if (tid < kDraftK) {
     // This row's outputs; the walk reads them back device-coherently.
@@ -363,49 +426,52 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   __syncthreads();
   if (tid >= 64) return;
   // Lane c holds candidate c (lanes 16..63 repeat them). The maximum is a
-  // wave reduction (fmax is order-free, so it equals the running maximum);
+  // reduction over each 16-lane row, which holds every candidate (fmax is
+  // order-free, so it equals the running maximum);
   // the weights and quotients are computed per lane; the sum and the
-  // cumulative test, whose rounding depends on the order, run in candidate
-  // order on lane 0 over LDS copies.
+  // cumulative sums, whose rounding depends on the order, are chains in
+  // candidate order over values read from lanes 0..15.
   const uint32_t c = tid & 15, lane = tid;
   const bool sampled = lp.sampled != 0;
-  const float *u = d.uniforms + (uint64_t)lane_index * kSamplingUniforms + kUniformProposals;
+  // The proposal uniforms, lane pp holding position pp's, read before the
+  // walk: inside it each would wait behind the previous position's stores.
+  const float u_lane =
+      sampled && lane < kDraftPositions
+          ? d.uniforms[(uint64_t)lane_index * kSamplingUniforms + kUniformProposals + lane]
+          : 0.0f;
   uint32_t pred_index = 0;
   for (uint32_t pp = 0; pp < kDraftPositions; ++pp) {
     const float score = un[pp][c] + tbl[pp][pred_index * kDraftK + c];
     uint32_t selected = 0;
     if (sampled) {
-      const float maximum = wave_max_f32(score);
+      const float maximum = row_max_f32(score);  // lane c holds candidate c & 15
       const float prob = exp_weight((score - maximum) / lp.temperature);
-      if (lane < kDraftK) s.walk[c] = prob;
-      wave_lds_sync();
+      // The sum and the cumulative sums in candidate order, as chains over
+      // the 16 weights read across lanes.
       float sum = 0.0f;
-      if (lane == 0)
-        for (uint32_t k = 0; k < kDraftK; ++k) sum = sum + s.walk[k];
-      sum = readlane_f32(sum, 0);
+#pragma unroll
+      for (uint32_t k = 0; k < kDraftK; ++k) sum = sum + readlane_f32(prob, (int)k);
       const float q = prob / sum;
-      if (lane < kDraftK) {
-        d.q_probs[(r0 + pp * kDraftK) + c] = q;
-        s.walk[kDraftK + c] = q;
+      if (lane < kDraftK) d.q_probs[(r0 + pp * kDraftK) + c] = q;
+      // Lane k ends holding the cumulative sum through candidate k.
+      float cumulative = 0.0f, through = 0.0f;
+#pragma unroll
+      for (uint32_t k = 0; k < kDraftK; ++k) {
+        cumulative = cumulative + readlane_f32(q, (int)k);
+        through = lane == k ? cumulative : through;
       }
-      wave_lds_sync();
-      const float uu = u[pp];
-      uint32_t sel = kDraftK - 1;
-      if (lane == 0) {
-        float cumulative = 0.0f;
-        for (uint32_t k = 0; k < kDraftK; ++k) {
-          cumulative = cumulative + s.walk[kDraftK + k];
-          if (sel == kDraftK - 1 && cumulative > uu) sel = k;
-        }
-      }
-      selected = readlane_u32(sel, 0);
+      // The first candidate whose cumulative sum passes the uniform, else
+      // the last.
+      const float uu = readlane_f32(u_lane, (int)pp);
+      const uint64_t passed = ballot(lane < kDraftK && through > uu);
+      selected = passed ? (uint32_t)__builtin_ctzll(passed) : kDraftK - 1;
     } else {
       // The first strict maximum in candidate order: candidate 0 when its
       // score is NaN (nothing compares above it), else the first candidate
       // holding the largest non-NaN score.
       const float s0 = readlane_f32(score, 0);
       if (s0 == s0) {
-        const float best = wave_max_f32(score);
+        const float best = row_max_f32(score);
         selected = (uint32_t)__builtin_ctzll(ballot(lane < kDraftK && score == best));
       }
     }

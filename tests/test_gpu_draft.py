@@ -65,7 +65,9 @@ def test_draft_select_full_vocabulary():
     assert_same(g, r, sampled)
 
 
-@pytest.mark.parametrize("V,stride", [(3000, None), (8192 * 2 + 5, 8192 * 2 + 7), (40000, None)])
+# 8192 * 40 + 3: 41 chunks, past the 32 one half-wave of list heads holds.
+@pytest.mark.parametrize("V,stride", [(3000, None), (8192 * 2 + 5, 8192 * 2 + 7), (40000, None),
+                                      (8192 * 40 + 3, None)])
 def test_draft_select_shapes_ties_and_edge_rows(V, stride):
     c = WL.config_draft(V=V, lanes=3, seed=V)
     x = c["logits"]
