@@ -290,10 +290,14 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t mask) {
       __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
-// Lane exchanges without the LDS crossbar where the lane pattern allows:
-// DPP quad permutes for xor 1 and 2, DPP row shifts for xor 4 and 8 (both
-// partners lie in the same 16-lane row), a swizzle for xor 16 and a
-// permute for xor 32.
+// Lane exchanges without the LDS crossbar: DPP quad permutes for xor 1 and
+// 2, DPP row shifts for xor 4 and 8 (both partners lie in the same 16-lane
+// row), and gfx950's lane swaps for xor 16 and 32. v_permlane16_swap of a
+// value with itself leaves, in every lane, the value of the even row of its
+// row pair (rows 0,1 and 2,3) in the first result and the odd row's in the
+// second; v_permlane32_swap likewise the lower half's and the upper half's.
+// The partner's is the one of the other row (half). Exchanges are made with
+// the whole wave active.
 template <int M>
 __device__ __forceinline__ uint32_t xor_u32(uint32_t v) {
   static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32);
@@ -307,10 +311,11 @@ __device__ __forceinline__ uint32_t xor_u32(uint32_t v) {
     const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x110 + M, 0xF, 0xF, false);
     return (lane_id() & M) ? dn : up;
   } else if constexpr (M == 16) {
-    // Bitmask swizzle within 32 lanes: and 0x1f, or 0, xor 0x10.
-    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F);
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane_id() & 16) ? (uint32_t)p[0] : (uint32_t)p[1];
   } else {
-    return (uint32_t)__shfl_xor((int)v, 32, kWave);
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane_id() & 32) ? (uint32_t)p[0] : (uint32_t)p[1];
   }
 }
 template <int M>

@@ -212,7 +212,7 @@ __device__ __forceinline__ void crossing_bin(Lds &s, uint64_t T) {
     const uint64_t suf = readlane_u64(incl, 63) - (incl - own);
     const uint64_t m = ballot(suf >= T);
     const int L = m ? (int)__popcll(m) - 1 : 0;
-    const uint64_t above = shfl_u64(suf - own, L);
+    const uint64_t above = readlane_u64(suf - own, L);
     if ((int)l == L) {
       // Walk this lane's four bins from the top.
       uint64_t acc = above;
@@ -1047,7 +1047,7 @@ __device__ __forceinline__ void wave_merge(const SampleLaunch &a,
     if (ballot(r > 0)) d = r;
   }
   const uint64_t fm = ballot(drafted && kept && id == draft);
-  const float fw = __shfl(w, fm ? (int)__builtin_ctzll(fm) : 0, kWave);
+  const float fw = u2f(readlane_u32(f2u(w), fm ? (int)__builtin_ctzll(fm) : 0));
   if (kept) {
     D[irank] = d;
     F[irank] = id;
@@ -3223,7 +3223,7 @@ __device__ __forceinline__ void wave_finish(const SampleLaunch &a, const RowPara
     if (ballot(r > 0)) d = r;
   }
   const uint64_t fm = ballot(drafted && kept && id == draft);
-  const float fw = __shfl(w, fm ? (int)__builtin_ctzll(fm) : 0, kWave);
+  const float fw = u2f(readlane_u32(f2u(w), fm ? (int)__builtin_ctzll(fm) : 0));
   // Id order of the kept items, each carrying the lane of its rank (ids are
   // below 2^19, so id and lane share 32 bits).
   uint32_t e = kept ? (id << 6) | lane : 0xffffffffu;
@@ -4345,8 +4345,8 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
     const uint64_t sl = wave_sums_u64<4>(lv);
     if (lane % 16 == 0 && lane / 16 < (uint32_t)HL)
       parts[chunk].v[kResidualSlot + 1 + (h * HL + lane / 16) * kWaves + w] = sl;
-    uint64_t t = sl + shfl_xor_u64(sl, 16);
-    total += t + shfl_xor_u64(t, 32);
+    uint64_t t = sl + xor_u64<16>(sl);
+    total += t + xor_u64<32>(t);
     // The draft token's float weight, from the thread that holds it.
     if (draft < V && draft / CHUNK == chunk) {
       const uint32_t o = draft - base, j = o / SLAB;
@@ -4476,8 +4476,8 @@ __global__ __launch_bounds__(kThreads) void uncut_kernel(SampleLaunch a, uint32_
       const uint64_t sl = wave_sums_u64<4>(lv);
       if (lane % 16 == 0)
         st_dev(&parts[chunk].v[kResidualSlot + 1 + (h * 4 + lane / 16) * kWaves + w], sl);
-      uint64_t t = sl + shfl_xor_u64(sl, 16);
-      total += t + shfl_xor_u64(t, 32);
+      uint64_t t = sl + xor_u64<16>(sl);
+      total += t + xor_u64<32>(t);
     }
     // The draft token's float weight, from the thread that holds it.
     if (draft < a.vocabulary && draft / CHUNK == chunk) {
