@@ -453,6 +453,53 @@ def pick_batch(steps):
     return 1
 
 
+def time_cpp_calls(kind, argv, steps, batch=0, selector=None):
+    """jf_draft_select on `selector` (kind "draft") or jf_tree_gather (kind
+    "gather") over the prepared argument records `argv` (rotated), issued
+    back to back from C++ (libjf_bench_loop.so): GPU and host microseconds
+    per step, and with `batch` the mean step time of each run of that many
+    steps."""
+    import ctypes
+    import jf_sampler as J
+    J.lib()  # the sampler library first: one HIP runtime in the process
+    L = ctypes.CDLL(os.path.join(REPO, "justfit-llm_amd", "jf_sampler", "libjf_bench_loop.so"))
+    vp, u32, dp = ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double)
+    n = len(argv)
+    arr = (type(argv[0]) * n)(*argv)
+    batch_us = np.zeros(steps // batch, np.float32) if batch else None
+    gpu, host = ctypes.c_double(), ctypes.c_double()
+    tail = (J._stream(), ctypes.byref(gpu), ctypes.byref(host), batch,
+            None if batch_us is None else batch_us.ctypes.data_as(vp))
+    if kind == "draft":
+        f = L.jf_bench_draft_loop
+        f.argtypes = [vp, vp, u32, u32, vp, dp, dp, u32, vp]
+        rc = f(selector.handle, ctypes.cast(arr, vp), n, steps, *tail)
+    else:
+        f = L.jf_bench_gather_loop
+        f.argtypes = [vp, u32, u32, vp, dp, dp, u32, vp]
+        rc = f(ctypes.cast(arr, vp), n, steps, *tail)
+    if rc:
+        raise RuntimeError(f"C++ timing loop failed: {rc} {J.lib().jf_last_error().decode()}")
+    out = {"us_per_step": gpu.value, "host_us_per_call": host.value}
+    if batch:
+        out["batch_us"] = batch_us.astype(np.float64)
+    return out
+
+
+def time_python_calls(call, argv, steps):
+    """The same calls from a Python/ctypes loop, between events at the
+    loop's ends: microseconds per step."""
+    import torch
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(steps):
+        call(argv[i % len(argv)])
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / steps
+
+
 def time_graph(g, steps):
     """Steps captured in a HIP graph and replayed: jf_sample_static (the
     entry point that allocates nothing; row parameters travel as kernel
@@ -651,16 +698,12 @@ def bench_draft(args):
         sel.launch(argv[i % len(argv)])
     torch.cuda.synchronize()
     K = args.steps
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
     wall0 = time.perf_counter()
-    ev[0].record()
-    for i in range(K):
-        sel.launch(argv[(args.warmup + i) % len(argv)])
-        ev[i + 1].record()
-    torch.cuda.synchronize()
+    cpp = time_cpp_calls("draft", argv, K, selector=sel)
     wall = time.perf_counter() - wall0
-    per = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(K)]) * 1000.0
-    ms_per_step = ev[0].elapsed_time(ev[K]) / K
+    ms_per_step = cpp["us_per_step"] / 1000.0
+    per = time_cpp_calls("draft", argv, K, batch=pick_batch(K), selector=sel)["batch_us"]
+    py_us = time_python_calls(sel.launch, argv, K)
     # The top-16 kernel alone, between events its launch records.
     hev = HipEvents(2 * K)
     for i in range(K):
@@ -695,7 +738,10 @@ def bench_draft(args):
         "value": 1000.0 / ms_per_step, "unit": "selections/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": ms_per_step,
         "p50_us": float(np.percentile(per, 50)), "p90_us": float(np.percentile(per, 90)),
-        "wall_s": wall, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "wall_s": wall, "host_us_per_call": cpp["host_us_per_call"], "python_loop_us": py_us,
+        "timing": "jf_draft_select called back to back from C++ (libjf_bench_loop.so), HIP "
+                  "events at the loop's ends; p50/p90 over runs of pick_batch(K) steps",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": f"synthetic (workloads.config_draft), {len(copies)} rotated "
                                 f"logits copies >= 512 MB",
         "config": {"workload": f"draft selector {lanes} lanes x 7 positions V={V} fp32, "
@@ -740,16 +786,12 @@ def bench_gather(args):
         J.tree_gather(argv[i % len(argv)])
     torch.cuda.synchronize()
     K = args.steps
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(K + 1)]
     wall0 = time.perf_counter()
-    ev[0].record()
-    for i in range(K):
-        J.tree_gather(argv[(args.warmup + i) % len(argv)])
-        ev[i + 1].record()
-    torch.cuda.synchronize()
+    cpp = time_cpp_calls("gather", argv, K)
     wall = time.perf_counter() - wall0
-    per = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(K)]) * 1000.0
-    ms_per_step = ev[0].elapsed_time(ev[K]) / K
+    ms_per_step = cpp["us_per_step"] / 1000.0
+    per = time_cpp_calls("gather", argv, K, batch=pick_batch(K))["batch_us"]
+    py_us = time_python_calls(J.tree_gather, argv, K)
     hev = HipEvents(2 * K)
     for i in range(K):
         a = argv[(args.warmup + i) % len(argv)]
@@ -781,7 +823,10 @@ def bench_gather(args):
         "value": 1000.0 / ms_per_step, "unit": "gathers/s", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": ms_per_step,
         "p50_us": float(np.percentile(per, 50)), "p90_us": float(np.percentile(per, 90)),
-        "wall_s": wall, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "wall_s": wall, "host_us_per_call": cpp["host_us_per_call"], "python_loop_us": py_us,
+        "timing": "jf_tree_gather called back to back from C++ (libjf_bench_loop.so), HIP "
+                  "events at the loop's ends; p50/p90 over runs of pick_batch(K) steps",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "u16", "data": f"synthetic (tests/gather_cases.py, seed 7), {len(copies)} rotated "
                                 f"copies >= 512 MB",
         "config": {"workload": "tree gather 16 lanes x 16 rows x 36 layers x 1024 columns bf16",

@@ -177,3 +177,58 @@ def bench_oracle_verify(c):
                                      target_draft_prob=vp[l * rows:(l + 1) * rows],
                                      uniforms40=c["uniforms"][l]))
     return vt, vp, chains
+
+
+def test_cpp_loops_issue_the_draft_and_gather_calls():
+    """bench.time_cpp_calls (libjf_bench_loop.so's draft and gather loops)
+    issues the same calls as the Python wrappers: the draft selector's
+    outputs after the loop equal one direct call's, and three in-place tree
+    gathers from the loop leave the tensor as three direct calls do."""
+    import torch
+    import jf_sampler as J
+    from gather_cases import gather_case
+    dev = torch.device("cuda", 0)
+    c = WL.config_draft(V=40000, lanes=3, seed=3)
+    lanes, V = c["lanes"], c["V"]
+    print(f"bench loops: draft V={V} lanes={lanes}, gather", flush=True)
+    t16 = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+    x = torch.from_numpy(c["logits"]).to(dev)
+    hidden, pred, succ = t16(c["hidden"]), t16(c["pred"]), t16(c["succ"])
+    u = torch.from_numpy(c["uniforms"]).to(dev)
+    outs = [torch.zeros((lanes * 7, 16), dtype=torch.int32, device=dev),
+            torch.zeros((lanes * 7, 16), dtype=torch.float32, device=dev),
+            torch.zeros(lanes * 7, dtype=torch.int32, device=dev),
+            torch.zeros((lanes * 7, 16), dtype=torch.float32, device=dev)]
+    sel = J.DraftSelector(V, lanes)
+    pols = [J.policy(temperature=t) for t in c["temperatures"]]
+    a = sel.args(logits=x, hidden=hidden, pred_codebook=pred, succ_codebook=succ,
+                 anchors=c["anchors"], policies=pols, candidates=outs[0], unary=outs[1],
+                 tokens=outs[2], q=outs[3], uniforms=u)
+    # Rows the call leaves unwritten (a greedy lane's probabilities) keep
+    # the fill in both runs.
+    for o in outs:
+        o.fill_(-1)
+    sel.launch(a)
+    torch.cuda.synchronize()
+    want = [o.clone() for o in outs]
+    for o in outs:
+        o.fill_(-1)
+    r = bench.time_cpp_calls("draft", [a], 4, batch=2, selector=sel)
+    assert r["us_per_step"] > 0 and len(r["batch_us"]) == 2
+    for o, w in zip(outs, want):
+        assert torch.equal(o.view(torch.int32), w.view(torch.int32))
+    sel.close()
+
+    rng = np.random.default_rng(5)
+    data, path, retained, p = gather_case(rng, lanes=6, layers=4, rows=16, columns=64,
+                                          inner=64, pad=0)
+    pr = torch.from_numpy(path.view(np.int32)).to(dev)
+    rt = torch.from_numpy(retained.view(np.int32)).to(dev)
+    direct = torch.from_numpy(data.view(np.int16)).to(dev)
+    looped = direct.clone()
+    ad = J.tree_gather_args(direct, pr, rt, **p)
+    for _ in range(3):
+        J.tree_gather(ad)
+    bench.time_cpp_calls("gather", [J.tree_gather_args(looped, pr, rt, **p)], 3)
+    torch.cuda.synchronize()
+    assert torch.equal(direct, looped)
