@@ -60,29 +60,32 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   step(xor_u64<32>(v));
   return v;
 }
-// The largest of a 32-bit value over each 16-lane row, in every lane of the
-// row: DPP quad permutes, then row rotations by 4 and 8.
-__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false));
-  return v;
-}
-// The largest over the wave (WIDE) or over lanes 0..31 when lanes 32..63
-// hold nothing larger. Across rows by gfx950's lane swaps, VALU work with no
-// LDS crossbar: v_permlane16_swap leaves each lane one value of each row of
-// its row pair (rows 0,1 and 2,3), v_permlane32_swap one of each half.
-template <bool WIDE>
-__device__ __forceinline__ uint32_t lanes_max_u32(uint32_t v) {
-  v = row_max_u32(v);
+// A reduction of a 32-bit value over the wave (WIDE) or over lanes 0..31
+// (when lanes 32..63 hold the operation's identity), in every lane: DPP
+// quad permutes and row rotations by 4 and 8 within each 16-lane row, then
+// across rows by gfx950's lane swaps, VALU work with no LDS crossbar:
+// v_permlane16_swap leaves each lane one value of each row of its row pair
+// (rows 0,1 and 2,3), v_permlane32_swap one of each half.
+template <bool WIDE, class Op>
+__device__ __forceinline__ uint32_t lanes_reduce_u32(uint32_t v, Op op) {
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false));
   const auto rows = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  v = max((uint32_t)rows[0], (uint32_t)rows[1]);
+  v = op((uint32_t)rows[0], (uint32_t)rows[1]);
   if constexpr (WIDE) {
     const auto halves = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    v = max((uint32_t)halves[0], (uint32_t)halves[1]);
+    v = op((uint32_t)halves[0], (uint32_t)halves[1]);
   }
   return v;
+}
+template <bool WIDE>
+__device__ __forceinline__ uint32_t lanes_max_u32(uint32_t v) {
+  return lanes_reduce_u32<WIDE>(v, [](uint32_t a, uint32_t b) { return max(a, b); });
+}
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+  return lanes_reduce_u32<true>(v, [](uint32_t a, uint32_t b) { return a | b; });
 }
 // The largest value of each 16-lane row, in every lane of the row (DPP
 // only): the wave's largest when every row holds the same 16 values.
@@ -95,13 +98,14 @@ __device__ __forceinline__ float row_max_f32(float v) {
 }
 
 struct __align__(16) DraftTopLds {
-  uint32_t wtop[kWaves * kDraftK];   // each wave's 16 largest lane maxima
+  uint32_t wtop[kWaves];             // each wave's 4th largest lane maximum
   uint64_t comp[kThreads];           // the chunk's entries at or above the bound
   uint32_t vbits[kThreads];
   uint64_t top[kDraftK];
   uint32_t topv[kDraftK];
   uint64_t wbest[kWaves];
   uint32_t wcount[kWaves];
+  uint32_t taken;                    // slots taken by the waves' entries
 };
 
 }  // namespace
@@ -145,6 +149,9 @@ __global__ __launch_bounds__(kThreads) void draft_top16_kernel(DraftLaunch d) {
     s.top[tid] = 0;
     s.topv[tid] = f2u(-__builtin_inff());
   }
+  // The first 64 slots read 0 (below every entry) until an entry lands.
+  if (tid < 64) s.comp[tid] = 0ull;
+  if (tid == 0) s.taken = 0;
   // The lane's largest key among its non-NaN tokens (0: none): fmax skips
   // NaN operands, so the float maximum is NaN only when every token is, and
   // the key order is the float order (the two zeros share a key).
@@ -152,13 +159,26 @@ __global__ __launch_bounds__(kThreads) void draft_top16_kernel(DraftLaunch d) {
 #pragma unroll
   for (int i = 1; i < kDraftTokens; ++i) mx = __builtin_fmaxf(mx, x[i]);
   const uint32_t mkey = mx == mx ? logit_key(mx) : 0u;
-  const uint32_t sorted = wave_sort_asc_u32(mkey);
-  if (lane >= 64 - kDraftK) s.wtop[w * kDraftK + lane - (64 - kDraftK)] = sorted;
+  // The bound: the smallest of the waves' 4th largest lane maxima. Each
+  // wave has four lanes, each with a token at or above its own, so the
+  // chunk has 16 tokens at or above the bound and its top 16 lie there.
+  uint32_t rest = mkey, t4 = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    t4 = __builtin_amdgcn_readfirstlane(lanes_max_u32<true>(rest));
+    const uint64_t at = ballot(rest == t4);
+    if (lane == (uint32_t)__builtin_ctzll(at)) rest = 0;
+  }
+  if (lane == 0) s.wtop[w] = t4;
   __syncthreads();
-  const uint32_t bound = readlane_u32(wave_sort_asc_u32(s.wtop[lane]), 64 - kDraftK);
+  uint32_t bound = s.wtop[0];
+#pragma unroll
+  for (int k = 1; k < kWaves; ++k) bound = min(bound, s.wtop[k]);
+  bound = __builtin_amdgcn_readfirstlane(bound);
 
-  // Compact the tokens at or above the bound: per-thread counts, a block
-  // prefix sum, then each thread writes its own.
+  // The tokens at or above the bound: at most 64 (the usual case) are
+  // gathered per wave and ranked by wave 0; more are compacted by a block
+  // prefix sum and ranked by counting.
   // key(x) >= bound as a float compare: the bound is 0 (every non-NaN token)
   // or the key of a real value (-inf or above), and NaN fails every compare.
   const float bv = bound ? key_logit(bound) : -__builtin_inff();
@@ -166,17 +186,81 @@ __global__ __launch_bounds__(kThreads) void draft_top16_kernel(DraftLaunch d) {
 #pragma unroll
   for (int i = 0; i < kDraftTokens; ++i) hits |= (x[i] >= bv ? 1u : 0u) << i;
   const uint32_t cnt = (uint32_t)__popc(hits);
-  const uint32_t incl = wave_incl_scan_u32(cnt);
-  if (lane == 63) s.wcount[w] = incl;
-  __syncthreads();
-  uint32_t before = 0, n = 0;
-#pragma unroll
-  for (int k = 0; k < kWaves; ++k) {
-    before += (uint32_t)k < w ? s.wcount[k] : 0u;
-    n += s.wcount[k];
+  // The tokens at or above the bound into the first 64 slots, each wave's
+  // at the slots it takes from a block counter (more than 64 in the block
+  // leave the slots to the block's compaction below). A lane with one
+  // holds it as its maximum (the one token at or above the bound is the
+  // largest) at index ctz(hits); the rare lanes with more are read out one
+  // at a time.
+  const uint32_t wcount = lanes_reduce_u32<true>(cnt, [](uint32_t a, uint32_t b) { return a + b; });
+  uint32_t first = 0;
+  if (lane == 0) {
+    s.wcount[w] = wcount;
+    first = wcount ? atomicAdd(&s.taken, wcount) : 0u;
   }
+  first = __builtin_amdgcn_readfirstlane(first);
+  const uint64_t single = ballot(cnt == 1u);
+  if (cnt == 1u) {
+    const uint32_t slot = first + mbcnt(single);
+    if (slot < 64u) {
+      s.comp[slot] = draft_comp(mx, token_of(__builtin_ctz(hits)));
+      s.vbits[slot] = f2u(mx);
+    }
+  }
+  uint64_t multi = ballot(cnt > 1u);
+  uint32_t slot = first + (uint32_t)__popcll(single);
+  while (multi) {
+    const uint32_t l = (uint32_t)__builtin_ctzll(multi);
+    multi &= multi - 1u;
+    uint32_t h = readlane_u32(hits, (int)l);
+    while (h) {
+      const uint32_t i = (uint32_t)__builtin_ctz(h);
+      h &= h - 1u;
+      const float v = readlane_f32(x[i], (int)l);
+      if (lane == 0 && slot < 64u) {
+        s.comp[slot] = draft_comp(v, base + (w * 64 + l) * 4 + (i >> 2) * 1024 + (i & 3));
+        s.vbits[slot] = f2u(v);
+      }
+      ++slot;
+    }
+  }
+  __syncthreads();
+  const uint32_t n = __builtin_amdgcn_readfirstlane(s.taken);
+  if (n <= 64) {
+    // Wave 0 ranks them: lane j takes slot j and counts the entries above
+    // it (sixteen slots a step, read by all lanes at once; slots past n
+    // read 0), then writes its entry at its rank. Slots past n stay empty.
+    if (w != 0) return;
+    const uint64_t pi = ((uint64_t)row * S + chunk) * kDraftK;
+    const uint64_t me = s.comp[lane];
+    const uint32_t bits = s.vbits[lane];
+    uint32_t rank = 0;
+    for (uint32_t e = 0; e < n; e += 16) {
+      ulonglong2 two[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        two[u] = *reinterpret_cast<const ulonglong2 *>(&s.comp[min(e + 2 * u, 62u)]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        rank += (two[u].x > me ? 1u : 0u) + (two[u].y > me ? 1u : 0u);
+    }
+    if (lane < n && rank < kDraftK) {
+      d.part_comp[pi + rank] = me;
+      d.part_vbits[pi + rank] = bits;
+    }
+    if (lane >= n && lane < kDraftK) {
+      d.part_comp[pi + lane] = 0ull;
+      d.part_vbits[pi + lane] = f2u(-__builtin_inff());
+    }
+    return;
+  }
+  uint32_t before = 0;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) before += (uint32_t)k < w ? s.wcount[k] : 0u;
+  // More than 64: the block's compaction (which rewrites the slots) and
+  // ranking.
   if (n <= kThreads) {
-    uint32_t pos = before + incl - cnt;
+    uint32_t pos = before + wave_incl_scan_u32(cnt) - cnt;
 #pragma unroll
     for (int i = 0; i < kDraftTokens; ++i)
       if ((hits >> i) & 1u) {

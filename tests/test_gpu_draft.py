@@ -78,6 +78,12 @@ def test_draft_select_shapes_ties_and_edge_rows(V, stride):
     x[4, [7, V - 1]] = [2.0, -3.0]        # fewer than 16 finite
     x[5] = np.nan
     x[5, :5] = [0.0, -0.0, 1.0, -0.0, 0.0]  # fewer than 16 non-NaN, signed zeros
+    # About 100 equal largest tokens a chunk: more than 64 at or above the
+    # chunk's bound, so the block's compaction ranks them.
+    pick = np.random.default_rng(V + 1)
+    for c0 in range(0, V, 8192):
+        span = min(8192, V - c0)
+        x[6, c0 + pick.choice(span, min(100, span), replace=False)] = 5.0
     c["anchors"][1] = 0xFFFFFFF0          # clamped into the codebooks
     c["temperatures"] = [0.0, 1.0, 0.3]
     g, r, sampled = run_both(c, stride)
