@@ -34,7 +34,10 @@ constexpr int kDraftTokens = 32;         // tokens per thread
 constexpr uint32_t kDraftK = 16;
 constexpr uint32_t kDraftMaxChunks = 64;    // vocabulary <= 524288
 constexpr uint32_t kRank = 256;
-constexpr uint32_t kPad = kRank + 1;     // LDS row pitch of the edge operands
+// LDS row pitch of the edge operands: 16-byte rows for four-float reads,
+// and 4 mod 32 words, so the 16 successor rows start on distinct banks in
+// pairs (a 2-way conflict at most).
+constexpr uint32_t kPad = kRank + 4;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -372,6 +375,65 @@ __device__ __forceinline__ void draft_merge_row(const uint64_t *comp, const uint
   }
 }
 
+// The top 16 of one proposal row from its chunks' lists, by one wave,
+// through a bound: the first m = min(64 / S, 16) entries of every list, one
+// a lane, are at least 16 entries, so the 16th largest of their value keys,
+// taken to its upper 16 bits (a 16-step bitwise descent), bounds the row's
+// 16th entry from below. Each list's entries at or above it (a prefix: the
+// lists are in rank order) are gathered into `keys`/`at` (64 slots that read
+// 0 past the entries) and ranked by counting. Returns false, having written
+// no output, when the bound is 0 (fewer than 16 non-empty entries among
+// those probed) or more than 64 entries reach it: the caller then merges
+// round by round.
+__device__ __forceinline__ bool draft_merge_bounded(const uint64_t *comp, const uint32_t *vbits,
+                                                    uint32_t S, uint64_t *keys, uint32_t *at,
+                                                    uint32_t *ids, float *values) {
+  const uint32_t lane = lane_id();
+  const uint32_t m = min(64u / S, kDraftK);
+  const uint32_t pc = lane / m, pt = lane - pc * m;
+  const uint32_t probe = pc < S ? (uint32_t)(comp[pc * kDraftK + pt] >> 32) : 0u;
+  uint32_t bound = 0;
+#pragma unroll
+  for (int b = 31; b >= 16; --b) {
+    const uint32_t trial = bound | (1u << b);
+    if ((uint32_t)__popcll(ballot(probe >= trial)) >= kDraftK) bound = trial;
+  }
+  if (bound == 0) return false;
+  uint32_t count = 0;
+  if (lane < S) {
+    const ulonglong2 *list = reinterpret_cast<const ulonglong2 *>(comp + lane * kDraftK);
+#pragma unroll
+    for (int k = 0; k < (int)kDraftK / 2; ++k) {
+      const ulonglong2 two = list[k];
+      count += ((uint32_t)(two.x >> 32) >= bound ? 1u : 0u) +
+               ((uint32_t)(two.y >> 32) >= bound ? 1u : 0u);
+    }
+  }
+  const uint32_t incl = wave_incl_scan_u32(count);
+  const uint32_t n = readlane_u32(incl, 63);
+  if (n > 64) return false;
+  for (uint32_t t = 0, o = incl - count; t < count; ++t, ++o) {
+    keys[o] = comp[lane * kDraftK + t];
+    at[o] = lane * kDraftK + t;
+  }
+  // (The wave's LDS writes land before its reads below: one wave's LDS
+  // operations complete in order.)
+  const uint64_t me = keys[lane];
+  uint32_t rank = 0;
+  for (uint32_t e = 0; e < n; e += 16) {
+    ulonglong2 two[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) two[u] = *reinterpret_cast<const ulonglong2 *>(&keys[e + 2 * u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) rank += (two[u].x > me ? 1u : 0u) + (two[u].y > me ? 1u : 0u);
+  }
+  if (lane < n && rank < kDraftK) {
+    ids[rank] = ~(uint32_t)me;
+    values[rank] = u2f(vbits[at[lane]]);
+  }
+  return true;
+}
+
 struct __align__(16) DraftEdgeLds {
   float ctx[kDraftK][kPad];   // predecessor codebook row x hidden
   float succ[kDraftK][kPad];  // successor codebook rows
@@ -382,6 +444,8 @@ struct __align__(16) DraftEdgeLds {
   float vals[2][kDraftK];
   uint32_t pred[kDraftK];
   uint32_t cand[kDraftK];
+  uint64_t mkeys[2][64];  // the bounded merge's entries (0 past them)
+  uint32_t mat[2][64];
   uint32_t last;
 };
 
@@ -426,9 +490,12 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   }
   const uint16_t *h = d.hidden + ((uint64_t)lane_index * kDraftQueryRows + p + 1) * kRank;
   s.hid[tid] = bf16f(h[tid]);
+  if (tid < 128) s.mkeys[tid >> 6][tid & 63] = 0ull;
   __syncthreads();
   const uint32_t wave = tid >> 6;
-  if (wave < rows_here) {
+  if (wave < rows_here &&
+      !draft_merge_bounded(s.pcomp[wave], s.pvbits[wave], S, s.mkeys[wave], s.mat[wave],
+                           s.ids[wave], s.vals[wave])) {
     if (S > 32)
       draft_merge_row<true>(s.pcomp[wave], s.pvbits[wave], S, s.ids[wave], s.vals[wave]);
     else
@@ -470,9 +537,18 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   const uint32_t i = tid >> 4, j = tid & 15;
   float *table = d.tables + (uint64_t)lane_index * kDraftPositions * kDraftK * kDraftK;
   if (i < preds) {
+    // Four dimensions a read, summed one at a time in ascending order.
+    const f32x4 *cr = reinterpret_cast<const f32x4 *>(s.ctx[i]);
+    const f32x4 *sr = reinterpret_cast<const f32x4 *>(s.succ[j]);
     float acc = 0.0f;
-#pragma unroll 16
-    for (uint32_t dm = 0; dm < kRank; ++dm) acc = acc + s.ctx[i][dm] * s.succ[j][dm];
+#pragma unroll 8
+    for (uint32_t q4 = 0; q4 < kRank / 4; ++q4) {
+      const f32x4 a = cr[q4], b = sr[q4];
+      acc = acc + a.x * b.x;
+      acc = acc + a.y * b.y;
+      acc = acc + a.z * b.z;
+      acc = acc + a.w * b.w;
+    }
     st_dev(table + (p * kDraftK + i) * kDraftK + j, acc);
   }
   wait_memory();
