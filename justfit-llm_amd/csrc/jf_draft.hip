@@ -12,9 +12,10 @@
 //                       candidates and unary scores, then the 16 x 16 table
 //                       of edge scores from the previous position's
 //                       candidates (the anchor at position 0) to this
-//                       position's; the lane's last block walks the 7
-//                       positions, greedily or drawing at the lane's
-//                       temperature.
+//                       position's, and the walk's step at this position
+//                       after each predecessor (greedily or drawing at the
+//                       lane's temperature); the lane's last block chains
+//                       the 7 positions' steps.
 // Edge scores are fp32 sums over the selector rank in ascending dimension
 // order (each product of bf16 operands is exact in fp32); the reference sums
 // the same terms in another order.
@@ -87,17 +88,38 @@ template <bool WIDE>
 __device__ __forceinline__ uint32_t lanes_max_u32(uint32_t v) {
   return lanes_reduce_u32<WIDE>(v, [](uint32_t a, uint32_t b) { return max(a, b); });
 }
-__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
-  return lanes_reduce_u32<true>(v, [](uint32_t a, uint32_t b) { return a | b; });
-}
 // The largest value of each 16-lane row, in every lane of the row (DPP
 // only): the wave's largest when every row holds the same 16 values.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(x), CTRL, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float row_max_f32(float v) {
-  v = __builtin_fmaxf(v, xor_f32<1>(v));
-  v = __builtin_fmaxf(v, xor_f32<2>(v));
-  v = __builtin_fmaxf(v, xor_f32<4>(v));
-  v = __builtin_fmaxf(v, xor_f32<8>(v));
+  v = __builtin_fmaxf(v, dpp_f32<0xB1>(v));   // quad xor 1
+  v = __builtin_fmaxf(v, dpp_f32<0x4E>(v));   // quad xor 2
+  v = __builtin_fmaxf(v, dpp_f32<0x124>(v));  // row rotate by 4
+  v = __builtin_fmaxf(v, dpp_f32<0x128>(v));  // row rotate by 8
   return v;
+}
+
+// Lane k of each 16-lane row, in every lane of the row.
+__device__ __forceinline__ float row_lane_f32(float v, int k) {
+  const float r0 = readlane_f32(v, k), r1 = readlane_f32(v, 16 + k),
+              r2 = readlane_f32(v, 32 + k), r3 = readlane_f32(v, 48 + k);
+  const uint32_t r = lane_id() >> 4;
+  return r == 0 ? r0 : r == 1 ? r1 : r == 2 ? r2 : r3;
+}
+// Lane j of each 16-lane row ends holding ((0 + w_0) + w_1) + ... + w_j: a
+// sum in lane order with that order's rounding, each step taking the sum
+// so far from the lane before by a DPP row shift.
+__device__ __forceinline__ float row_ordered_sums(float w, uint32_t j) {
+  float c = 0.0f + w;
+#pragma unroll
+  for (uint32_t k = 1; k < kDraftK; ++k) {
+    const float before = dpp_f32<0x111>(c);  // row_shr:1
+    c = j == k ? before + w : c;
+  }
+  return c;
 }
 
 struct __align__(16) DraftTopLds {
@@ -453,17 +475,19 @@ struct __align__(16) DraftEdgeLds {
 // partials (the row's candidates and unary scores), the previous row's for
 // its predecessors (the anchor at position 0), then the edge scores from
 // each predecessor to each candidate, summed over the rank in ascending
-// order; ids are clamped into the codebooks (sampling.metal:1259-1262). The
-// lane's last block walks.
+// order; ids are clamped into the codebooks (sampling.metal:1259-1262),
+// and the walk's step after each predecessor. The lane's last block walks.
 __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   __shared__ DraftEdgeLds s;
-  __shared__ float tbl[kDraftPositions][kDraftK * kDraftK];
-  __shared__ float un[kDraftPositions][kDraftK];
-  __shared__ uint32_t cands[kDraftPositions][kDraftK];
+  __shared__ float tbl[kDraftPositions][kDraftK * kDraftK];  // the walk's probabilities
   const uint32_t p = blockIdx.x, lane_index = blockIdx.y;
   const uint32_t row = lane_index * kDraftPositions + p, tid = threadIdx.x;
   const uint32_t V = d.vocabulary, S = d.chunks;
   const DraftLaneParams lp = d.lane_params[lane_index];
+  const bool sampled = lp.sampled != 0;
+  // This position's proposal uniform, requested now for the walk's step.
+  const float uniform =
+      sampled ? d.uniforms[(uint64_t)lane_index * kSamplingUniforms + kUniformProposals + p] : 0.0f;
   const uint32_t total = S * kDraftK, rows_here = p ? 2u : 1u;
   // Every partial load issued before any lands in LDS (a load-then-store
   // loop would wait for each round trip in turn).
@@ -550,6 +574,37 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
       acc = acc + a.w * b.w;
     }
     st_dev(table + (p * kDraftK + i) * kDraftK + j, acc);
+    // The walk's step at this position after each predecessor i
+    // (sampling.metal:1316-1359), row i with lane j holding candidate j:
+    // the score is the candidate's unary plus the edge. The row maximum is
+    // a DPP reduction (fmax is order-free, so it equals the running
+    // maximum); the sum and the cumulative sums, whose rounding depends on
+    // the order, go in candidate order.
+    const float score = s.vals[0][j] + acc;
+    const uint32_t shift = tid & 48;
+    uint32_t pick = 0;
+    if (sampled) {
+      const float maximum = row_max_f32(score);
+      const float prob = exp_weight((score - maximum) / lp.temperature);
+      const float sum = row_lane_f32(row_ordered_sums(prob, j), kDraftK - 1);
+      const float q = prob / sum;
+      st_dev(d.choice_q + ((uint64_t)row * kDraftK + i) * kDraftK + j, q);
+      // The first candidate whose cumulative sum passes the uniform, else
+      // the last.
+      const uint32_t passed =
+          (uint32_t)(ballot(row_ordered_sums(q, j) > uniform) >> shift) & 0xffffu;
+      pick = passed ? (uint32_t)__builtin_ctz(passed) : kDraftK - 1;
+    } else {
+      // The first strict maximum in candidate order: candidate 0 when its
+      // score is NaN (nothing compares above it), else the first candidate
+      // holding the largest non-NaN score.
+      const float s0 = row_lane_f32(score, 0);
+      if (s0 == s0) {
+        const float best = row_max_f32(score);
+        pick = (uint32_t)__builtin_ctz((uint32_t)(ballot(score == best) >> shift) & 0xffffu);
+      }
+    }
+    if (j == 0) st_dev(d.choices + (uint64_t)row * kDraftK + i, pick);
   }
   wait_memory();
   __syncthreads();
@@ -563,81 +618,42 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   __syncthreads();
   if (!s.last) return;
 
-  // The walk (sampling.metal:1316-1359): every table, unary score and
-  // candidate of the lane into LDS, then wave 0 with lane c holding
-  // candidate c; the sums and the running maximum go in candidate order.
-  // Every load issued before any lands in LDS. Entry tid of position pp
-  // (256 per position); position 0 has only the anchor's row.
+  // The walk: the last block of the lane chains the positions' steps. Lane
+  // c holds position pp's candidate c and pick after predecessor c; the
+  // picked row's probabilities come through LDS. Every load issued before
+  // any lands.
   const uint64_t r0 = (uint64_t)lane_index * kDraftPositions * kDraftK;
-  static_assert(kDraftK * kDraftK == kThreads, "one table entry per thread and position");
-  float tv[kDraftPositions];
+  static_assert(kDraftK * kDraftK == kThreads, "one probability per thread and position");
+  float qv[kDraftPositions];
+  if (sampled) {
 #pragma unroll
-  for (uint32_t pp = 0; pp < kDraftPositions; ++pp)
-    tv[pp] = pp || tid < kDraftK ? ld_dev(table + pp * kThreads + tid) : 0.0f;
-  const bool mine = tid < kDraftPositions * kDraftK;
-  const float uv = mine ? ld_dev(d.unary + r0 + tid) : 0.0f;
-  const uint32_t cv = mine ? ld_dev(d.candidates + r0 + tid) : 0u;
-#pragma unroll
-  for (uint32_t pp = 0; pp < kDraftPositions; ++pp) tbl[pp][tid] = tv[pp];
-  if (mine) {
-    un[tid / kDraftK][tid % kDraftK] = uv;
-    cands[tid / kDraftK][tid % kDraftK] = cv;
+    for (uint32_t pp = 0; pp < kDraftPositions; ++pp)
+      qv[pp] = pp || tid < kDraftK ? ld_dev(d.choice_q + (r0 + pp * kDraftK) * kDraftK + tid) : 0.0f;
   }
-  __syncthreads();
-  if (tid >= 64) return;
-  // Lane c holds candidate c (lanes 16..63 repeat them). The maximum is a
-  // reduction over each 16-lane row, which holds every candidate (fmax is
-  // order-free, so it equals the running maximum);
-  // the weights and quotients are computed per lane; the sum and the
-  // cumulative sums, whose rounding depends on the order, are chains in
-  // candidate order over values read from lanes 0..15.
-  const uint32_t c = tid & 15, lane = tid;
-  const bool sampled = lp.sampled != 0;
-  // The proposal uniforms, lane pp holding position pp's, read before the
-  // walk: inside it each would wait behind the previous position's stores.
-  const float u_lane =
-      sampled && lane < kDraftPositions
-          ? d.uniforms[(uint64_t)lane_index * kSamplingUniforms + kUniformProposals + lane]
-          : 0.0f;
-  uint32_t pred_index = 0;
-  for (uint32_t pp = 0; pp < kDraftPositions; ++pp) {
-    const float score = un[pp][c] + tbl[pp][pred_index * kDraftK + c];
-    uint32_t selected = 0;
-    if (sampled) {
-      const float maximum = row_max_f32(score);  // lane c holds candidate c & 15
-      const float prob = exp_weight((score - maximum) / lp.temperature);
-      // The sum and the cumulative sums in candidate order, as chains over
-      // the 16 weights read across lanes.
-      float sum = 0.0f;
+  uint32_t cv[kDraftPositions] = {}, picks[kDraftPositions] = {};
+  if (tid < kDraftK) {
 #pragma unroll
-      for (uint32_t k = 0; k < kDraftK; ++k) sum = sum + readlane_f32(prob, (int)k);
-      const float q = prob / sum;
-      if (lane < kDraftK) d.q_probs[(r0 + pp * kDraftK) + c] = q;
-      // Lane k ends holding the cumulative sum through candidate k.
-      float cumulative = 0.0f, through = 0.0f;
-#pragma unroll
-      for (uint32_t k = 0; k < kDraftK; ++k) {
-        cumulative = cumulative + readlane_f32(q, (int)k);
-        through = lane == k ? cumulative : through;
-      }
-      // The first candidate whose cumulative sum passes the uniform, else
-      // the last.
-      const float uu = readlane_f32(u_lane, (int)pp);
-      const uint64_t passed = ballot(lane < kDraftK && through > uu);
-      selected = passed ? (uint32_t)__builtin_ctzll(passed) : kDraftK - 1;
-    } else {
-      // The first strict maximum in candidate order: candidate 0 when its
-      // score is NaN (nothing compares above it), else the first candidate
-      // holding the largest non-NaN score.
-      const float s0 = readlane_f32(score, 0);
-      if (s0 == s0) {
-        const float best = row_max_f32(score);
-        selected = (uint32_t)__builtin_ctzll(ballot(lane < kDraftK && score == best));
-      }
+    for (uint32_t pp = 0; pp < kDraftPositions; ++pp) {
+      cv[pp] = ld_dev(d.candidates + r0 + pp * kDraftK + tid);
+      picks[pp] = pp || tid == 0 ? ld_dev(d.choices + r0 + pp * kDraftK + tid) : 0u;
     }
-    pred_index = selected;
+  }
+  if (sampled) {
+#pragma unroll
+    for (uint32_t pp = 0; pp < kDraftPositions; ++pp) tbl[pp][tid] = qv[pp];
+    __syncthreads();
+  }
+  if (tid >= 64) return;
+  const uint32_t lane = tid;
+  uint32_t pred_index = 0;
+#pragma unroll
+  for (uint32_t pp = 0; pp < kDraftPositions; ++pp) {
+    const uint32_t selected = readlane_u32(picks[pp], (int)pred_index);
     if (lane == 0)
-      d.tokens[(uint64_t)lane_index * kDraftPositions + pp] = cands[pp][selected];
+      d.tokens[(uint64_t)lane_index * kDraftPositions + pp] = readlane_u32(cv[pp], (int)selected);
+    if (sampled && lane < kDraftK)
+      d.q_probs[(r0 + pp * kDraftK) + lane] = tbl[pp][pred_index * kDraftK + lane];
+    pred_index = selected;
   }
 }
 

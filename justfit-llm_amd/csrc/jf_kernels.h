@@ -329,6 +329,8 @@ struct DraftLaunch {
   uint64_t *part_comp;        // [lanes * 7][chunks][16]
   uint32_t *part_vbits;       // [lanes * 7][chunks][16]
   float *tables;              // [lanes][7][16][16]
+  uint32_t *choices;          // [lanes * 7][16]: the walk's pick after each predecessor
+  float *choice_q;            // [lanes * 7][16][16]: its probabilities, sampled lanes
   uint32_t *counters;         // [lanes * 8], zero between launches
 };
 

@@ -1244,6 +1244,8 @@ struct jf_draft_selector {
   uint64_t *part_comp = nullptr;               // [max_lanes * 7][chunks][16]
   uint32_t *part_vbits = nullptr;
   float *tables = nullptr;                     // [max_lanes][7][16][16]
+  uint32_t *choices = nullptr;                 // [max_lanes * 7][16]
+  float *choice_q = nullptr;                   // [max_lanes * 7][16][16]
   uint32_t *counters = nullptr;                // [max_lanes * 8]
   std::vector<jf::DraftLaneParams> last_lanes;  // what lane_params holds
   StagingRing staging;
@@ -1258,6 +1260,8 @@ int jf_draft_selector_destroy(jf_draft_selector *d) {
   (void)hipFree(d->part_comp);
   (void)hipFree(d->part_vbits);
   (void)hipFree(d->tables);
+  (void)hipFree(d->choices);
+  (void)hipFree(d->choice_q);
   (void)hipFree(d->counters);
   delete d;
   return JF_OK;
@@ -1287,6 +1291,10 @@ int jf_draft_selector_create(uint32_t vocabulary, uint32_t max_lanes,
   if (rc == JF_OK) rc = device_alloc(&d->part_vbits, rows * chunks * JF_DRAFT_CANDIDATES, "draft partial values");
   if (rc == JF_OK)
     rc = device_alloc(&d->tables, rows * JF_DRAFT_CANDIDATES * JF_DRAFT_CANDIDATES, "draft edge tables");
+  if (rc == JF_OK) rc = device_alloc(&d->choices, rows * JF_DRAFT_CANDIDATES, "draft walk choices");
+  if (rc == JF_OK)
+    rc = device_alloc(&d->choice_q, rows * JF_DRAFT_CANDIDATES * JF_DRAFT_CANDIDATES,
+                      "draft walk probabilities");
   if (rc == JF_OK) rc = device_alloc(&d->counters, (uint64_t)max_lanes * jf::kDraftQueryRows, "draft counters");
   if (rc == JF_OK) {
     const hipError_t e1 = hipMemset(d->counters, 0, (uint64_t)max_lanes * jf::kDraftQueryRows * sizeof(uint32_t));
@@ -1362,6 +1370,8 @@ int jf_draft_select(jf_draft_selector *d, const jf_draft_select_args *a, void *s
   L.part_comp = d->part_comp;
   L.part_vbits = d->part_vbits;
   L.tables = a->edge_tables ? a->edge_tables : d->tables;
+  L.choices = d->choices;
+  L.choice_q = d->choice_q;
   L.counters = d->counters;
   const bool aligned = (uintptr_t)a->logits % 16 == 0 && a->logits_stride % 4 == 0;
   const int e = jf::launch_draft_select(L, aligned, stream, a->select_start_event,
