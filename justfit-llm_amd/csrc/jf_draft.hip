@@ -527,9 +527,6 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   }
   __syncthreads();
   if (tid < kDraftK) {
-    // This row's outputs; the walk reads them back device-coherently.
-    st_dev(d.candidates + (uint64_t)row * kDraftK + tid, s.ids[0][tid]);
-    st_dev(d.unary + (uint64_t)row * kDraftK + tid, s.vals[0][tid]);
     s.cand[tid] = min(s.ids[0][tid], V - 1u);
     s.pred[tid] = min(p ? s.ids[1][tid] : lp.anchor, V - 1u);
   }
@@ -556,6 +553,13 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
         s.ctx[i][dm + 1] = bf16f(pw[e] >> 16) * s.hid[dm + 1];
       }
     }
+  }
+  // This row's outputs (the walk reads them back device-coherently), stored
+  // after the codebook reads have landed: a wait for a read also waits for
+  // every store issued before it.
+  if (tid < kDraftK) {
+    st_dev(d.candidates + (uint64_t)row * kDraftK + tid, s.ids[0][tid]);
+    st_dev(d.unary + (uint64_t)row * kDraftK + tid, s.vals[0][tid]);
   }
   __syncthreads();
   const uint32_t i = tid >> 4, j = tid & 15;
