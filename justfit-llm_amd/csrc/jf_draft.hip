@@ -649,15 +649,26 @@ __global__ __launch_bounds__(kThreads) void draft_edges_kernel(DraftLaunch d) {
   }
   if (tid >= 64) return;
   const uint32_t lane = tid;
+  // The chain of picks first (scalar work), then every store.
+  uint32_t from[kDraftPositions], pick[kDraftPositions];
   uint32_t pred_index = 0;
 #pragma unroll
   for (uint32_t pp = 0; pp < kDraftPositions; ++pp) {
-    const uint32_t selected = readlane_u32(picks[pp], (int)pred_index);
-    if (lane == 0)
-      d.tokens[(uint64_t)lane_index * kDraftPositions + pp] = readlane_u32(cv[pp], (int)selected);
-    if (sampled && lane < kDraftK)
-      d.q_probs[(r0 + pp * kDraftK) + lane] = tbl[pp][pred_index * kDraftK + lane];
-    pred_index = selected;
+    from[pp] = pred_index;
+    pick[pp] = readlane_u32(picks[pp], (int)pred_index);
+    pred_index = pick[pp];
+  }
+  if (lane < kDraftPositions) {
+    uint32_t token = 0;
+#pragma unroll
+    for (uint32_t pp = 0; pp < kDraftPositions; ++pp)
+      if (lane == pp) token = readlane_u32(cv[pp], (int)pick[pp]);
+    d.tokens[(uint64_t)lane_index * kDraftPositions + lane] = token;
+  }
+  if (sampled && lane < kDraftK) {
+#pragma unroll
+    for (uint32_t pp = 0; pp < kDraftPositions; ++pp)
+      d.q_probs[(r0 + pp * kDraftK) + lane] = tbl[pp][from[pp] * kDraftK + lane];
   }
 }
 
