@@ -2733,6 +2733,20 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   std::conditional_t<DT == 0, float, uint32_t> tail[VEC];
   uint32_t tail_j;
   fast_load<DT>(logits, stride, V, row, base, full, xs, tail, tail_j);
+  if (w == kWaves - 1) {
+    // The last wave, its loads in flight, reads one word of each 64-byte
+    // line of the launch record into the scalar cache: the fields the
+    // block's end reads (list, header and result addresses, the epoch) are
+    // then there instead of a round trip to memory each.
+    // (The record starts 56 bytes into the argument segment, whose lines
+    // start at multiples of 64.)
+    static_assert(offsetof(FastKernelArgs, f) == 56, "the record's offset in the segment");
+    const uint32_t *rec = reinterpret_cast<const uint32_t *>(&a);
+    uint32_t touched = rec[0];
+#pragma unroll
+    for (uint32_t k = 2; k < sizeof(SampleLaunch) / 4; k += 16) touched ^= rec[k];
+    asm volatile("" ::"s"(touched));
+  }
   uint32_t mw[LOADS];
   const uint32_t *mrow = nullptr;
   if (constrained) {
@@ -3351,6 +3365,16 @@ __global__ __launch_bounds__(kThreads) void merge_small_kernel(
   const float hbest = hv ? u2f(h1.x) : -__builtin_inff();
   const uint32_t hcount = hv ? h0.y : 0u, hadm = hv ? h0.z : 0u, hovf = hv ? h0.w : 0u,
                  hfloor = hv ? h1.z : 0u, hbid = hv ? h1.y : kNoToken;
+  if (tid >= 64) {
+    // Waves 1..3, idle until the summaries' barrier, read the launch
+    // record's output fields into the scalar cache, where wave 0's reads at
+    // the end of the row then find them (a read there from memory would be
+    // a round trip on the row's critical path).
+    const void *o0 = a.out_tokens, *o1 = a.out_draft, *o2 = a.out_kept_counts,
+               *o3 = a.out_kept_ids, *o4 = a.out_kept_probs;
+    const uint32_t o5 = a.kept_cap;
+    asm volatile("" ::"s"(o0), "s"(o1), "s"(o2), "s"(o3), "s"(o4), "s"(o5));
+  }
   const float u = u2f(ubits);
   for (uint32_t b = tid; b < 1024; b += kThreads) {
     s.merge.bins[b] = 0;
