@@ -2474,6 +2474,10 @@ __device__ __forceinline__ void finish_row_and_lane(const SampleLaunch &a,
 
 // select_fast_kernel's arguments as the kernel-argument segment holds them
 // (each at its natural alignment, in order).
+// Grids of at most this many blocks warm the scalar cache with the launch
+// record (select_fast_kernel).
+constexpr uint32_t kWarmGrid = 2048;
+
 struct FastKernelArgs {
   const void *logits;
   const uint32_t *pen_slots;
@@ -2733,11 +2737,13 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   std::conditional_t<DT == 0, float, uint32_t> tail[VEC];
   uint32_t tail_j;
   fast_load<DT>(logits, stride, V, row, base, full, xs, tail, tail_j);
-  if (w == kWaves - 1) {
+  if (w == kWaves - 1 && gridDim.x * gridDim.y <= kWarmGrid) {
     // The last wave, its loads in flight, reads one word of each 64-byte
     // line of the launch record into the scalar cache: the fields the
-    // block's end reads (list, header and result addresses, the epoch) are
-    // then there instead of a round trip to memory each.
+    // block's end reads (list, header, best and result addresses, the
+    // epoch) are then there instead of a round trip to memory each. Only
+    // in grids the chip holds at about once: in a larger one the blocks
+    // that follow on a CU find the lines there already.
     // (The record starts 56 bytes into the argument segment, whose lines
     // start at multiples of 64.)
     static_assert(offsetof(FastKernelArgs, f) == 56, "the record's offset in the segment");
