@@ -3287,9 +3287,13 @@ __device__ __noinline__ void merge_small_general(uint32_t row) {
 }
 #endif
 
-// The arguments the first loads need lead the signature (15 dwords, no
-// padding): the hardware preloads them into scalar registers at wave launch.
-// They repeat fields of `a` (drafted_rows is 0 when there are no drafts).
+// The arguments the first loads need lead the signature (14 dwords, no
+// padding): the hardware preloads them into scalar registers at wave launch
+// (14 of its 16 user registers; the argument segment's address takes two).
+// They repeat fields of `a` (drafted_rows is 0 when there are no drafts);
+// bit 31 of `chunks_bits` says the row's draft is addressed through its
+// record (the chunk count below it), so that no later argument is read
+// from memory at the row's start.
 #if JF_IN(2)
 // SPEC: speculatively fetched list slots a thread. 10 gives floor(2560 / S)
 // slots a chunk (134 at 19 chunks); 20 gives floor(5120 / S) (165 at 31
@@ -3298,11 +3302,12 @@ __device__ __noinline__ void merge_small_general(uint32_t row) {
 template <int DT, int SPEC>
 __global__ __launch_bounds__(kThreads) void merge_small_kernel(
     const BlockHeader *headers, const uint64_t *cands, const RowParams *params,
-    const float *uniforms, const uint32_t *uniform_index, uint32_t S,
-    uint32_t uniform_offset, uint32_t uniform_stride, uint32_t drafted_rows,
-    uint32_t row_indexed, SampleLaunch a) {
+    const float *uniforms, const uint32_t *uniform_index, uint32_t chunks_bits,
+    uint32_t uniform_offset, uint32_t uniform_stride, uint32_t drafted_rows, SampleLaunch a) {
   Lds &s = g_small_lds;
   const uint32_t row = blockIdx.x, tid = threadIdx.x;
+  const uint32_t S = chunks_bits & 0x7fffffffu;
+  const bool row_indexed = (chunks_bits >> 31) != 0;
   // Every address of the row, computed once and held in vector registers:
   // the general path's register pressure would otherwise have the compiler
   // reload (and wait for) kernel arguments between the loads below. A load
@@ -4827,9 +4832,10 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, bool wide, void *s
   const hipStream_t st = (hipStream_t)stream;
   auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, block, 0, st, a.headers, (const uint64_t *)a.cands,
-                       a.params, a.uniforms, a.uniform_index, a.chunks,
+                       a.params, a.uniforms, a.uniform_index,
+                       a.chunks | (a.row_indexed ? 0x80000000u : 0u),
                        (uint32_t)a.uniform_offset, (uint32_t)a.uniform_stride,
-                       a.draft_tokens && !a.row_indexed ? a.drafted_rows : 0u, a.row_indexed, a);
+                       a.draft_tokens && !a.row_indexed ? a.drafted_rows : 0u, a);
   };
   // The wider fetch past 20 chunks (fewer than 128 slots a chunk otherwise).
   const bool w = wide && a.chunks > 20;
