@@ -101,7 +101,7 @@ def build_workload(cfg, mode, history="uniform"):
         hist_bytes = c["masks"].nbytes
         if sampled:
             # Every row keeps every admitted token: the select launch draws it.
-            w["kernel"] = "jf::select_fast_kernel<1, false, jf::NoRows, true>"
+            w["kernel"] = "jf::select_fast_kernel<1, false, jf::NoRows, jf::UncutFinish>"
     elif cfg == 4:
         c = WL.config4()
         rows = c["logits"].shape[0]
@@ -896,7 +896,7 @@ def verify_cpu_baseline(c, seconds):
 def bench_verify(args):
     """The penalized chain-verify shape (VerifyStep): its step timed from
     C++ as the sample path's is, its dominant kernel (the single pass with
-    the verify rows' extra penalty tokens, select_fast_kernel<0, true, FastRows, false>)
+    the verify rows' extra penalty tokens, select_fast_kernel<0, true, FastRows, NoFinish>)
     timed alone."""
     import torch
     from jf_sampler import workloads as WL
@@ -923,7 +923,7 @@ def bench_verify(args):
     step_bytes = sel_bytes + B * 4 * 3 + c["lanes"] * (c["rows"] - 1) * (4 + 16 * 8)
     achieved = sel_bytes / (sel_mean * 1e-6) / 1e9
     step_gbs = step_bytes / (cpp["us_per_step"] * 1e-6) / 1e9
-    kernel = "jf::select_fast_kernel<0, true, jf::FastRows, false>"
+    kernel = "jf::select_fast_kernel<0, true, jf::FastRows, jf::NoFinish>"
     key = ("verify", "auto")
     traffic = read_traffic(key, kernel)
     prof_us = read_profile_us(key, kernel)
@@ -1041,7 +1041,7 @@ def main():
     # row its own penalty row): the fast kernel's variant without per-row facts.
     kernel = w.get("kernel",
                    f"jf::select_fast_kernel<{0 if w['dtype'] == 'f32' else 1}, false, jf::NoRows, "
-                   "false>")
+                   "jf::NoFinish>")
     key = profile_key(args.config, args.mode, args.history)
     traffic = read_traffic(key, kernel)
     prof_us = read_profile_us(key, kernel)
