@@ -176,6 +176,12 @@ class GpuStep:
                 for r in range(n - 1):
                     draft[k * 16 + r] = c["tokens"][k][r + 1]
             extra["draft_tokens"] = torch.from_numpy(draft.view(np.int32)).to(dev)
+            # The engine builds its trees on the host (jf_build_draft_tree),
+            # so it names the drafted rows, each lane's chain
+            # (Runtime.cpp:1284-1306 passes chain_rows per lane), as the
+            # row-indexed call does; the other rows draw plainly.
+            extra["draft_token_index"] = [r if draft[r] != 0xFFFFFFFF else 0xFFFFFFFF
+                                          for r in range(rows)]
             self.q = [torch.from_numpy(c["q"]).to(dev) for _ in range(len(self.copies))]
             extra["out_draft_probs"] = torch.zeros(rows, dtype=torch.float32, device=dev)
         self.draft_probs = extra.get("out_draft_probs")

@@ -92,9 +92,11 @@ int jf_sampler_destroy(jf_sampler *sampler);
 uint64_t jf_sampler_workspace_bytes(const jf_sampler *sampler);
 
 /* No counterpart in the reference (whose last-arriving group never waits,
- * split_reduce.h:14-45). In an all-greedy jf_sample call each row's
- * finishing block waits, word by word, for the row's other blocks' results;
- * that wait is bounded, and the sampler holds a host-mapped status word that
+ * split_reduce.h:14-45). In an all-greedy jf_sample call, and for rows with
+ * no cut drawn in the select launch or in the residual launch of drafted
+ * rows, each row's finishing block waits, word by word, for the row's other
+ * blocks' results; that wait is bounded, and the sampler holds a
+ * host-mapped status word that
  * a finishing block sets if its bound is ever reached. jf_sampler_status
  * reports that as JF_ERR_DEVICE, once (jf_sample does the same before it
  * enqueues anything), and enqueues on `stream` the clearing of the words
@@ -104,8 +106,8 @@ int jf_sampler_status(jf_sampler *sampler, void *stream);
 /* No counterpart in the reference: the bound of that wait, in reads of one
  * result word (default 2^20, about a second). It exists so that a test can
  * drive the expiry path from the host: with 0, the finishing block of every
- * row of an all-greedy call gives up at once (it reads no other block's
- * result) and every kernel still exits normally. */
+ * such row gives up at once (it reads no other block's result) and every
+ * kernel still exits normally. */
 int jf_sampler_set_wait_bound(jf_sampler *sampler, uint32_t reads);
 
 /* ---- penalties -------------------------------------------------------- */
@@ -283,9 +285,11 @@ int jf_sample(jf_sampler *sampler, const jf_sample_args *args, void *stream);
  * any penalty table, created beforehand). Same arguments, results and errors
  * as jf_sample otherwise. Every call on one GPU shares that GPU's array:
  * calls that overlap on one GPU (on different streams) race; calls in one
- * stream's order do not. It has no status word: should an all-greedy row's
- * bounded wait ever expire, that row's output is JF_NO_TOKEN (in-band, as
- * the reference reports numeric failures) and nothing else reports it. */
+ * stream's order do not. It has no status word: should a finisher's
+ * bounded wait ever expire (an all-greedy row's, or a row with no cut drawn
+ * in the select or residual launch), that row's output is JF_NO_TOKEN
+ * (in-band, as the reference reports numeric failures) and nothing else
+ * reports it. */
 int jf_sample_static(uint32_t vocabulary, const jf_sample_args *args, void *stream);
 
 /* ---- acceptance ------------------------------------------------------- */

@@ -406,13 +406,21 @@ int launch_merge_small(const SampleLaunch &a, uint32_t dtype, bool wide, void *s
 // Rows with no cut (grid rows x per_row: per_row = chunks when the launch
 // has drafted uncut rows, else 1).
 int launch_uncut(const SampleLaunch &a, uint32_t dtype, uint32_t per_row, void *stream);
-// residual_kernel over the rows row_of[0, n) (n <= kKernargRows), before
-// launch_uncut on the same stream.
+// residual_kernel over the kRowLean rows row_of[0, n_lean) (grid n_lean x
+// chunks), before launch_uncut on the same stream; or, with draw set, a
+// launch that also draws: each lean row's last chunk block draws that row
+// and a share of the rows row_of[n_lean, n_lean + n_plain) (every other row
+// of the launch: greedy ones, and sampled ones with no cut, draft, penalty
+// or extra token), so no launch_uncut follows (n_lean >= 1, n_lean +
+// n_plain <= kKernargRows).
 struct LeanLaunch {
   SampleLaunch a;
+  uint32_t n_lean;
+  uint32_t n_plain;
+  uint32_t draw;
   uint32_t row_of[kKernargRows];
 };
-int launch_residual(const LeanLaunch &l, uint32_t n, uint32_t dtype, void *stream);
+int launch_residual(const LeanLaunch &l, uint32_t dtype, void *stream);
 int launch_stage(const SampleLaunch &a, uint32_t dtype, void *stream);
 int launch_accept_chain(const AcceptChainLaunch &a, void *stream);
 int launch_accept_tree(const AcceptTreeLaunch &a, void *stream);

@@ -2070,6 +2070,84 @@ __device__ __forceinline__ uint32_t pick_slice(uint64_t vg, uint32_t G, uint64_t
   return g;
 }
 
+// One wave draws inside slice g of chunk c (load g / kWaves of wave
+// g % kWaves: 64 x VEC consecutive tokens): the slice's logits reloaded,
+// stop tokens and (constrained rows) masked ones dropped, and the token
+// whose running weight first passes `within` written with `pd` and `kept`.
+// RESID 0: the plain weights quantized_weight(x, mc) (uncut_draw's walk);
+// 1: the residual weights residual_of(floor(w r_c), W, q) against the
+// draft's dense q row; 2: against its sparse candidates in s.cids/s.cprobs.
+// `q_row`: the draft's row of q (RESID 1) or its candidates' (RESID 2).
+template <int DT, int RESID, class L>
+__device__ __forceinline__ void draw_in_slice(const SampleLaunch &a, uint32_t row, uint32_t flags,
+                                              float inv_t, uint32_t q_row, uint32_t c, uint32_t g,
+                                              uint64_t within, float mc, uint64_t Rc,
+                                              uint64_t W, float pd, uint32_t kept, const L &s) {
+  constexpr int VEC = Geo<DT>::VEC, SLAB = Geo<DT>::SLAB;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  const uint32_t lane = lane_id(), V = a.vocabulary;
+  const uint32_t t0 = c * CHUNK + (g / kWaves) * SLAB + ((g % kWaves) * 64 + lane) * VEC;
+  float x[VEC];
+  if constexpr (DT == 0) {
+    const float *rowp = (const float *)a.logits + (uint64_t)row * a.stride;
+    if (t0 + VEC <= V) {
+      const f32x4 v = *(const f32x4 *)(rowp + t0);
+      x[0] = v.x;
+      x[1] = v.y;
+      x[2] = v.z;
+      x[3] = v.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] = t0 + e < V ? rowp[t0 + e] : kNotAdmitted;
+    }
+  } else {
+    const uint16_t *rowp = (const uint16_t *)a.logits + (uint64_t)row * a.stride;
+    if (t0 + VEC <= V) {
+      const u32x4 v = *(const u32x4 *)(rowp + t0);
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        x[2 * k] = u2f(vw[k] << 16);
+        x[2 * k + 1] = u2f(vw[k] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) x[e] = t0 + e < V ? bf16_to_float(rowp[t0 + e]) : kNotAdmitted;
+    }
+  }
+  float qv[VEC];
+  if constexpr (RESID == 1) {
+    // A dense q row ends at the vocabulary.
+    const float *qrow = a.dense_q + (uint64_t)q_row * a.q_stride;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) qv[e] = t0 + e < V ? qrow[t0 + e] : 0.0f;
+  } else if constexpr (RESID == 2) {
+    // The first candidate that lists the token (sampling.metal:703-708).
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      qv[e] = 0.0f;
+      for (int j = 15; j >= 0; --j) qv[e] = s.cids[j] == t0 + e ? s.cprobs[j] : qv[e];
+    }
+  }
+  // The slice's VEC tokens share one mask word (t0 is a multiple of VEC).
+  const uint32_t mword =
+      (flags & kRowConstrained) && t0 < V ? a.masks[(uint64_t)row * a.mask_stride + (t0 >> 5)] : ~0u;
+  uint64_t q[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    const uint32_t t = t0 + e;
+    const bool drop = !((mword >> (t & 31)) & 1u) ||
+                      ((flags & kRowExcludeStop) && (t == a.stop0 || t == a.stop1));
+    const float xe = drop ? kNotAdmitted : x[e];
+    if constexpr (RESID == 0)
+      q[e] = quantized_weight(xe, mc, inv_t);
+    else
+      q[e] = residual_of(scaled_weight(xe, mc, inv_t, Rc), W, qv[e]);
+  }
+  uint32_t e_hit;
+  if (lane == slice_hit<VEC>(q, within, e_hit)) write_result(a, row, t0 + e_hit, pd, kept);
+}
+
 // finish_acceptance (sampling.metal:1381-1392) on a wave that holds the
 // lane's output token t in thread t: the budget min(accepted + 1,
 // remaining), then cut after the first stop token within it.
@@ -2525,8 +2603,7 @@ __device__ __forceinline__ void finish_uncut_row(const SampleLaunch &a, const fl
                                                  float bmax, uint32_t badm, float inv_t,
                                                  FusedUncutLds &s, uint32_t row, uint32_t chunk,
                                                  uint32_t S, uint32_t flags) {
-  constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS, SLAB = Geo<DT>::SLAB;
-  constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves;
+  constexpr uint32_t G = Geo<DT>::LOADS * kWaves;
   const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   StagePartial *parts = a.partials + (uint64_t)row * S;
   const bool finisher = chunk + 1 == S;
@@ -2617,52 +2694,8 @@ __device__ __forceinline__ void finish_uncut_row(const SampleLaunch &a, const fl
   uint64_t within = unscaled_bound(target - readlane_u64(incl - T, c), readlane_u64(R, c));
   const uint64_t vg = lane < G ? s.fsl[c * G + lane] : 0ull;
   const uint32_t g = pick_slice(vg, G, within);
-  // Slice g of chunk c: load g / kWaves of wave g % kWaves.
-  const uint32_t jg = g / kWaves, wg = g % kWaves;
-  const uint32_t V = a.vocabulary;
-  const uint32_t t0 = c * CHUNK + jg * SLAB + (wg * 64 + lane) * VEC;
-  float x[VEC];
-  if constexpr (DT == 0) {
-    const float *rowp = (const float *)a.logits + (uint64_t)row * a.stride;
-    if (t0 + VEC <= V) {
-      const f32x4 v = *(const f32x4 *)(rowp + t0);
-      x[0] = v.x;
-      x[1] = v.y;
-      x[2] = v.z;
-      x[3] = v.w;
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) x[e] = t0 + e < V ? rowp[t0 + e] : kNotAdmitted;
-    }
-  } else {
-    const uint16_t *rowp = (const uint16_t *)a.logits + (uint64_t)row * a.stride;
-    if (t0 + VEC <= V) {
-      const u32x4 v = *(const u32x4 *)(rowp + t0);
-      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        x[2 * k] = u2f(vw[k] << 16);
-        x[2 * k + 1] = u2f(vw[k] & 0xffff0000u);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) x[e] = t0 + e < V ? bf16_to_float(rowp[t0 + e]) : kNotAdmitted;
-    }
-  }
-  // The slice's VEC tokens share one mask word (t0 is a multiple of VEC).
-  const uint32_t mword =
-      (flags & kRowConstrained) && t0 < V ? a.masks[(uint64_t)row * a.mask_stride + (t0 >> 5)] : ~0u;
-  const float mc = __shfl(m, (int)c, kWave);
-  uint64_t q[VEC];
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) {
-    const uint32_t t = t0 + e;
-    const bool drop = !((mword >> (t & 31)) & 1u) ||
-                      ((flags & kRowExcludeStop) && (t == a.stop0 || t == a.stop1));
-    q[e] = quantized_weight(drop ? kNotAdmitted : x[e], mc, inv_t);
-  }
-  uint32_t e_hit;
-  if (lane == slice_hit<VEC>(q, within, e_hit)) write_result(a, row, t0 + e_hit, 0.0f, kept);
+  draw_in_slice<DT, 0>(a, row, flags, inv_t, 0u, c, g, within, __shfl(m, (int)c, kWave), 0ull,
+                       0ull, 0.0f, kept, s);
 }
 
 // A launch's per-row fact of row `i`: 0 its sampler row, 1 its flags and
@@ -4252,56 +4285,172 @@ struct __align__(16) LeanLds {
   uint64_t rc;   // its rescale r_c, packed
   uint64_t W;    // the row's mass
   uint32_t ok;   // the row has mass to draw from
+  uint32_t kept; // its admitted tokens
+  // (drawing launches) every chunk's maximum, rescale and scaled mass T_c;
+  // the finisher's gather: every chunk's slice residual masses, the draft
+  // token's float weight, and whether a wait gave up
+  float cmax[kMaxChunks];
+  uint64_t cscale[kMaxChunks];
+  uint64_t ctot[kMaxChunks];
+  alignas(16) uint64_t fsl[kMaxChunks * 32];
+  uint32_t dw;
+  uint32_t fail;
 };
+
+// One wave: a row's chunk summaries (lane c < S holds chunk c's maximum m,
+// rescale R against the row maximum M and scaled mass T), and W = sum T,
+// the admitted and kept counts, as uncut_kernel computes them.
+struct RowSums {
+  float m, M;
+  uint64_t R, T, W;
+  uint32_t admitted, kept;
+};
+__device__ __forceinline__ RowSums row_sums(const SampleLaunch &a, uint32_t row, float inv_t) {
+  const uint32_t S = a.chunks, lane = lane_id();
+  const bool in = lane < S;
+  const uint32_t at = in ? lane : 0u;
+  const BlockHeader *h = a.headers + (uint64_t)row * S + at;
+  const float hm = h->maximum;
+  const uint32_t hadm = h->admitted, hcnt = h->count;
+  const uint64_t hmass = a.partials[(uint64_t)row * S + at].v[0];
+  RowSums r;
+  r.m = in ? hm : -3.402823466e38f;
+  r.M = wave_max_f32(r.m);
+  r.R = in ? chunk_scale(r.m, r.M, inv_t) : kZeroScale;
+  r.T = scale_by(in ? hmass : 0ull, r.R);
+  r.W = wave_sum_u64(r.T);
+  r.admitted = wave_sum_u32(in ? hadm : 0u);
+  r.kept = wave_sum_u32(in ? hcnt : 0u);
+  return r;
+}
+
+// One wave: the plain draw of an uncut row (uncut_draw's): the chunk and
+// slice that hold floor(u W) by the chunk masses and the slice masses the
+// selection wrote, then the token inside the slice.
+template <int DT, class L>
+__device__ __forceinline__ void plain_draw_wave(const SampleLaunch &a, uint32_t row,
+                                                uint32_t flags, float inv_t, const RowSums &r,
+                                                float u, float pd, const L &s) {
+  constexpr uint32_t G = Geo<DT>::LOADS * kWaves;
+  const uint32_t S = a.chunks, lane = lane_id();
+  const uint64_t incl = wave_incl_scan_u64(r.T);
+  uint64_t target = floor_mul(r.W, u);
+  if (target >= r.W) target = r.W - 1;
+  // incl at the last lane is W > target: some lane passes it.
+  const uint32_t c = (uint32_t)__builtin_ctzll(ballot(lane < S && incl > target));
+  uint64_t within = unscaled_bound(target - readlane_u64(incl - r.T, c), readlane_u64(r.R, c));
+  const uint64_t vg = lane < G ? a.partials[(uint64_t)row * S + c].v[1 + lane] : 0ull;
+  const uint32_t g = pick_slice(vg, G, within);
+  draw_in_slice<DT, 0>(a, row, flags, inv_t, 0u, c, g, within, u2f(readlane_u32(f2u(r.m), c)),
+                       0ull, 0ull, pd, r.kept, s);
+}
+
+// A drawing launch's block for a row with no residual pass (one wave): a
+// greedy row's argmax of the chunk bests (sampling.metal:1478-1512), or a
+// sampled row's plain draw, or the sentinel.
+template <int DT>
+__device__ __forceinline__ void plain_row_block(const SampleLaunch &a, uint32_t row, LeanLds &s) {
+  const uint32_t S = a.chunks, lane = lane_id();
+  const RowParams rp = a.params[row];
+  if (!(rp.flags & kRowSampled)) {
+    const bool in = lane < S;
+    const BlockHeader *h = a.headers + (uint64_t)row * S + (in ? lane : 0u);
+    float hv = in ? h->best_value : -__builtin_inff();
+    uint32_t hi = in ? h->best_id : kNoToken;
+    wave_argmax(hv, hi);
+    if (lane == 0) write_result(a, row, hi, 0.0f, 0);
+    return;
+  }
+  const float u = row_uniform(a, row);
+  const RowSums r = row_sums(a, row, rp.inv_t);
+  const bool none = r.admitted == 0 || r.M == __builtin_inff();
+  if (none || r.W == 0) {
+    // The sentinel (a row of -inf keeps every token at probability 0).
+    if (lane == 0) write_result(a, row, kNoToken, 0.0f, none ? 0u : r.kept);
+    return;
+  }
+  plain_draw_wave<DT>(a, row, rp.flags, rp.inv_t, r, u, 0.0f, s);
+}
 
 // The residual pass of the rows flagged kRowLean (drafted, no cut, no
 // penalty, mask or extra tokens), one block per (row, chunk): the same
 // partial slots as uncut_kernel's pass (the chunk's residual mass and its
 // slices', the draft token's float weight), from the same arithmetic, but
 // with nothing else in the kernel and half a chunk's logits and q held at
-// a time, so it keeps few registers and many waves per SIMD. uncut_kernel
-// then finishes these rows in one block each (this launch ends first).
+// a time, so it keeps few registers and many waves per SIMD. Without
+// l.draw, uncut_kernel then finishes these rows in one block each (this
+// launch ends first). With it, the launch finishes every row itself: the
+// lean rows' last chunk blocks also draw the rows without a residual pass
+// (plain_row_block), and each lean row's last chunk block (its finisher)
+// draws it as uncut_kernel would. The row's other blocks publish their
+// slice masses (below 2^54) as self-validating words, mass | tag10 << 54,
+// and the draft token's weight as tag12 << 32 | its bits (tag = call
+// epoch << 1 | 1, 10 and 12 bits of it); the finisher gathers them, each
+// word re-read until it carries this
+// call's tag (at most a.wait_bound reads), and returns each to zero. Its
+// waits end: the row's other blocks were dispatched before it (block
+// index order) and wait on nothing. Should one give up, the row gets
+// JF_NO_TOKEN and the status word is set.
 template <int DT, bool DENSE>
 __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
   constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS, SLAB = Geo<DT>::SLAB;
-  constexpr uint32_t CHUNK = Geo<DT>::CHUNK;
+  constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves;
   constexpr int HL = LOADS / 2, HV = HL * VEC;  // loads and values per half
   static_assert(HL == 2 || HL == 4, "two or four loads a half");
   const SampleLaunch &a = l.a;
   __shared__ LeanLds s;
   const uint32_t S = a.chunks;
-  const uint32_t row = l.row_of[blockIdx.x / S], chunk = blockIdx.x % S;
   const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint32_t lean = blockIdx.x / S, chunk = blockIdx.x % S;
+  const uint32_t row = l.row_of[lean];
+  // A drawing launch's last chunk blocks first draw the rows without a
+  // residual pass, lean row j's block rows n_lean + j + k n_lean, one per
+  // wave at a time (little else is live yet): the block's own chunk is the
+  // row's partial one when the vocabulary does not fill the last chunk, so
+  // this mostly takes time it would spend waiting for the row's other
+  // blocks.
+  const bool finisher = l.draw && chunk + 1 == S;
+  if (finisher)
+    for (uint32_t i = lean + w * l.n_lean; i < l.n_plain; i += kWaves * l.n_lean)
+      plain_row_block<DT>(a, l.row_of[l.n_lean + i], s);
   const RowParams rp = a.params[row];
   const uint32_t draft = row_draft(a, rp);
-  if (draft == kNoToken) return;  // drawn plainly by uncut_kernel
+  if (draft == kNoToken) {
+    // Drawn plainly: by uncut_kernel, or here by chunk 0's block.
+    if (l.draw && chunk == 0 && w == 0) plain_row_block<DT>(a, row, s);
+    return;
+  }
+  const uint64_t tag10 = ((uint64_t)(a.epoch & 0x1ffu) << 1) | 1ull;
+  const uint64_t tag12 = ((uint64_t)(a.epoch & 0x7ffu) << 1) | 1ull;
+  if (tid == 0) s.fail = 0;
   const float inv_t = rp.inv_t;
   // The row's maximum, this chunk's rescale and the row's mass from the
-  // chunk summaries, as uncut_kernel computes them (wave 0, S <= 64).
-  const BlockHeader *hb = a.headers + (uint64_t)row * S;
+  // chunk summaries (wave 0, S <= 64).
   StagePartial *parts = a.partials + (uint64_t)row * S;
   if (w == 0) {
-    const bool in = lane < S;
-    const uint32_t at = in ? lane : 0u;
-    const float hm = hb[at].maximum;
-    const uint32_t hadm = hb[at].admitted;
-    const uint64_t hmass = parts[at].v[0];
-    const float m = in ? hm : -3.402823466e38f;
-    const float M = wave_max_f32(m);
-    const uint64_t R = in ? chunk_scale(m, M, inv_t) : kZeroScale;
-    const uint64_t W = wave_sum_u64(scale_by(in ? hmass : 0ull, R));
-    const uint32_t admitted = wave_sum_u32(in ? hadm : 0u);
+    const RowSums r = row_sums(a, row, inv_t);
     if (lane == chunk) {
-      s.mc = m;
-      s.rc = R;
+      s.mc = r.m;
+      s.rc = r.R;
+    }
+    if (lane < S) {
+      s.cmax[lane] = r.m;
+      s.cscale[lane] = r.R;
+      s.ctot[lane] = r.T;
     }
     if (lane == 0) {
-      s.W = W;
-      s.ok = admitted != 0 && M != __builtin_inff() && W != 0 ? 1u : 0u;
+      const bool none = r.admitted == 0 || r.M == __builtin_inff();
+      s.W = r.W;
+      s.ok = !none && r.W != 0 ? 1u : 0u;
+      s.kept = none ? 0u : r.kept;
     }
   }
   stage_candidates(a, rp, s);  // ends with a barrier
-  if (!s.ok) return;  // uncut_kernel writes the sentinel
+  if (!s.ok) {
+    // The sentinel: uncut_kernel's, or here chunk 0's block's.
+    if (l.draw && chunk == 0 && tid == 0) write_result(a, row, kNoToken, 0.0f, s.kept);
+    return;
+  }
   const float mc = s.mc;
   const uint64_t Rc = s.rc, W = s.W;
   const uint32_t V = a.vocabulary, base = chunk * CHUNK;
@@ -4378,8 +4527,13 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
                               qv[jj * VEC + e]);
     // Lane l holds the wave's sum of load h * HL + l / 16 (l / 16 < HL).
     const uint64_t sl = wave_sums_u64<4>(lv);
-    if (lane % 16 == 0 && lane / 16 < (uint32_t)HL)
-      parts[chunk].v[kResidualSlot + 1 + (h * HL + lane / 16) * kWaves + w] = sl;
+    if (lane % 16 == 0 && lane / 16 < (uint32_t)HL) {
+      const uint32_t gi = (h * HL + lane / 16) * kWaves + w;
+      if (finisher)
+        s.fsl[chunk * G + gi] = sl;
+      else
+        st_dev(&parts[chunk].v[kResidualSlot + 1 + gi], l.draw ? sl | tag10 << 54 : sl);
+    }
     uint64_t t = sl + xor_u64<16>(sl);
     total += t + xor_u64<32>(t);
     // The draft token's float weight, from the thread that holds it.
@@ -4390,13 +4544,105 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
         float xd = 0.0f;
 #pragma unroll
         for (int k = 0; k < HV; ++k) xd = (uint32_t)k == i ? xv[k] : xd;
-        parts[chunk].v[kDraftSlot] = (uint64_t)f2u(weight_of(xd, mc, inv_t));
+        const uint32_t wd = f2u(weight_of(xd, mc, inv_t));
+        if (finisher)
+          s.dw = wd;
+        else
+          st_dev(&parts[chunk].v[kDraftSlot], l.draw ? tag12 << 32 | wd : (uint64_t)wd);
       }
     }
   }
-  if (lane == 0) s.wl[w] = total;
+  if (!l.draw) {
+    if (lane == 0) s.wl[w] = total;
+    __syncthreads();
+    if (tid == 0) parts[chunk].v[kResidualSlot] = s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3];
+    return;
+  }
+  if (!finisher) return;
+
+  // The finisher's gather: the other chunks' slice masses (word k is slice
+  // k % G of chunk k / G) and, in the last thread, the draft token's
+  // weight (its word PER). Each round re-reads every word of the thread
+  // not yet seen with this call's tag, all requested before any is checked.
+  constexpr uint64_t kMass54 = (1ull << 54) - 1ull;
+  constexpr int PER = (kMaxChunks * G + kThreads - 1) / kThreads;
+  const uint32_t n_words = chunk * G;
+  const uint32_t cd = draft < V ? draft / CHUNK : chunk;
+  uint32_t pending = 0;  // bit i: word i still to be seen
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    pending |= tid + i * kThreads < n_words ? 1u << i : 0u;
+  if (cd != chunk && tid == kThreads - 1) pending |= 1u << PER;
+  uint64_t vw[PER + 1];
+  for (uint32_t n = 0; pending && n < a.wait_bound; ++n) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const uint32_t k = tid + i * kThreads;
+      if ((pending >> i) & 1u) vw[i] = ld_dev(&parts[k / G].v[kResidualSlot + 1 + k % G]);
+    }
+    if ((pending >> PER) & 1u) vw[PER] = ld_dev(&parts[cd].v[kDraftSlot]);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const uint32_t k = tid + i * kThreads;
+      if (((pending >> i) & 1u) && (vw[i] >> 54) == tag10) {
+        s.fsl[k] = vw[i] & kMass54;
+        st_dev(&parts[k / G].v[kResidualSlot + 1 + k % G], 0ull);
+        pending &= ~(1u << i);
+      }
+    }
+    if (((pending >> PER) & 1u) && (vw[PER] >> 32) == tag12) {
+      s.dw = (uint32_t)vw[PER];
+      st_dev(&parts[cd].v[kDraftSlot], 0ull);
+      pending &= ~(1u << PER);
+    }
+  }
+  const bool ok = pending == 0;
+  if (!ok) s.fail = 1;
   __syncthreads();
-  if (tid == 0) parts[chunk].v[kResidualSlot] = s.wl[0] + s.wl[1] + s.wl[2] + s.wl[3];
+  if (w != 0) return;
+  if (s.fail) {
+    if (lane == 0) {
+      write_result(a, row, kNoToken, 0.0f, 0);
+      if (a.status) __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    return;
+  }
+
+  // Wave 0: p(draft), then the residual draw, or the plain one when no
+  // residual mass remains (uncut_kernel's last block). Lane c < S sums
+  // chunk c's slices.
+  const float u = row_uniform(a, row);
+  const bool in = lane < S;
+  uint64_t rv = 0;
+  if (in) {
+    const ulonglong2 *f = reinterpret_cast<const ulonglong2 *>(&s.fsl[lane * G]);
+#pragma unroll
+    for (uint32_t g2 = 0; g2 < G / 2; ++g2) {
+      const ulonglong2 p2 = f[g2];
+      rv += p2.x + p2.y;
+    }
+  }
+  const float pd = draft < V ? uncut_probability(u2f(s.dw), s.cscale[cd], W) : 0.0f;
+  const uint64_t incl = wave_incl_scan_u64(rv);
+  const uint64_t tot = readlane_u64(incl, 63);
+  if (!tot) {
+    RowSums r;
+    r.m = in ? s.cmax[lane] : -3.402823466e38f;
+    r.R = in ? s.cscale[lane] : kZeroScale;
+    r.T = in ? s.ctot[lane] : 0ull;
+    r.W = W;
+    r.kept = s.kept;
+    plain_draw_wave<DT>(a, row, rp.flags, inv_t, r, u, pd, s);
+    return;
+  }
+  uint64_t target = floor_mul(tot, u);
+  if (target >= tot) target = tot - 1;
+  const uint32_t c = (uint32_t)__builtin_ctzll(ballot(in && incl > target));
+  uint64_t within = target - readlane_u64(incl - rv, c);
+  const uint64_t vg = lane < G ? s.fsl[c * G + lane] : 0ull;
+  const uint32_t g = pick_slice(vg, G, within);
+  draw_in_slice<DT, DENSE ? 1 : 2>(a, row, rp.flags, inv_t, rp.cand_index, c, g, within,
+                                   s.cmax[c], s.cscale[c], W, pd, s.kept, s);
 }
 
 template <int DT>
@@ -4797,8 +5043,8 @@ int launch_merge(const SampleLaunch &a, uint32_t dtype, void *stream) {
 #endif
 
 #if JF_IN(4)
-int launch_residual(const LeanLaunch &l, uint32_t n, uint32_t dtype, void *stream) {
-  const dim3 grid(n * l.a.chunks), block(kThreads);
+int launch_residual(const LeanLaunch &l, uint32_t dtype, void *stream) {
+  const dim3 grid(l.n_lean * l.a.chunks), block(kThreads);
   const hipStream_t st = (hipStream_t)stream;
   // A sparse draft's 16-candidate lookup per token takes about 30 more
   // registers than a dense q row: separate instantiations.

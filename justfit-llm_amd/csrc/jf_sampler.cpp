@@ -961,22 +961,67 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   if (any_uncut && !fuse_uncut) {
     // residual_kernel over the kRowLean rows, then uncut_kernel: one block
     // per row, or one per (row, chunk) when other drafted uncut rows need
-    // their residual pass there.
+    // their residual pass there. A launch with lean rows and no cut row,
+    // kept token list, other drafted uncut row, or sampled row whose draw
+    // would reread penalized or extra values is finished by residual_kernel
+    // itself (draw): each lean row by its last chunk block, every other row
+    // by one of those blocks too; no uncut_kernel launch follows.
+    bool draw = n_lean && !any_cut && !a->out_kept_ids && !uncut_drafted;
+    for (uint32_t r = 0; draw && r < rows; ++r) {
+      const jf::RowParams &rp = params[r];
+      draw = !(rp.flags & jf::kRowSampled) || (rp.flags & jf::kRowLean) ||
+             (!(rp.flags & jf::kRowPenalized) && !rp.extra_count);
+    }
     if (n_lean) {
+      thread_local std::vector<uint32_t> lean, plain;
+      lean.clear();
+      plain.clear();
+      for (uint32_t r = 0; r < rows; ++r) {
+        if (params[r].flags & jf::kRowLean)
+          lean.push_back(r);
+        else if (draw)
+          plain.push_back(r);
+      }
+      // Launches of at most kKernargRows rows (a share of each list, at
+      // least one lean row in each: the lean rows' blocks draw the others).
+      const uint32_t nl = (uint32_t)lean.size(), np = (uint32_t)plain.size();
+      const auto share = [](uint32_t total, uint32_t i, uint32_t n) {
+        return (uint32_t)((uint64_t)i * total / n);
+      };
+      const auto fits = [&](uint32_t n) {
+        for (uint32_t i = 0; i < n; ++i)
+          if (share(nl, i + 1, n) - share(nl, i, n) + share(np, i + 1, n) - share(np, i, n) >
+              (uint32_t)jf::kKernargRows)
+            return false;
+        return true;
+      };
+      uint32_t n = (nl + np + jf::kKernargRows - 1) / jf::kKernargRows;
+      while (!fits(n)) ++n;
+      if (draw && n > nl) {
+        draw = false;
+        plain.clear();
+      }
+      const uint32_t launches = draw ? n : (nl + jf::kKernargRows - 1) / jf::kKernargRows;
       jf::LeanLaunch R;
       R.a = L;
-      uint32_t n = 0;
-      for (uint32_t r = 0; r < rows && e == hipSuccess; ++r) {
-        if (params[r].flags & jf::kRowLean) R.row_of[n++] = r;
-        if (n == (uint32_t)jf::kKernargRows || (n && r + 1 == rows)) {
-          e = jf::launch_residual(R, n, a->dtype, stream);
-          n = 0;
-        }
+      R.draw = draw ? 1u : 0u;
+      for (uint32_t i = 0; i < launches && e == hipSuccess; ++i) {
+        const uint32_t l0 = share(nl, i, launches), l1 = share(nl, i + 1, launches);
+        const uint32_t p0 = draw ? share(np, i, launches) : 0u,
+                       p1 = draw ? share(np, i + 1, launches) : 0u;
+        // The lean rows lead row_of, the others follow.
+        std::memcpy(R.row_of, lean.data() + l0, (l1 - l0) * sizeof(uint32_t));
+        std::memcpy(R.row_of + (l1 - l0), plain.data() + p0, (p1 - p0) * sizeof(uint32_t));
+        R.n_lean = l1 - l0;
+        R.n_plain = p1 - p0;
+        e = jf::launch_residual(R, a->dtype, stream);
       }
       if (e != hipSuccess) return hip_fail((hipError_t)e, "residual launch");
     }
-    e = jf::launch_uncut(L, a->dtype, uncut_drafted ? L.chunks : 1u, stream);
-    if (e != hipSuccess) return hip_fail((hipError_t)e, "uncut draw launch");
+    if (!draw) {
+      e = jf::launch_uncut(L, a->dtype, uncut_drafted ? L.chunks : 1u, stream);
+      if (e != hipSuccess) return hip_fail((hipError_t)e, "uncut draw launch");
+    }
   }
   return JF_OK;
 }

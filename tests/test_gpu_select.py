@@ -640,6 +640,79 @@ def test_dense_residual_in_the_partial_last_chunk(bf16):
     assert g["tokens"][rows - 1] >= V - 4480  # inside the partial last chunk
 
 
+@pytest.mark.parametrize("bf16,sparse", [(False, False), (True, False), (False, True)])
+def test_residual_launch_draws_every_row(bf16, sparse):
+    """A launch of drafted rows with no cut, penalty or mask (the residual
+    pass) beside greedy rows and undrafted rows with no cut, without kept
+    lists: the residual launch draws every row (each drafted row in its last
+    chunk block to arrive, the others in blocks of their own), with no
+    further launch. Rows 0-7 are drafted: a draft in the partial last chunk,
+    a q that leaves no residual mass (the plain draw, with p(draft)), a zero
+    q row (the residual is p itself), a row of NaN (the sentinel), a drafted
+    row whose draft is JF_NO_TOKEN, a draft that is an excluded stop token;
+    their q dense, or 16 sparse candidates. Rows 8-13 are not drafted: a
+    penalized and a plain greedy row, a masked row, a row of -inf (the
+    sentinel) and uniforms at both ends. Bit-exact with the oracle."""
+    rng = np.random.default_rng(131 + bf16 + 2 * sparse)
+    V = 6 * 8192 + 777
+    rows, drafted = 14, 8
+    x = rand_logits(rng, rows, V, scale=2.0)
+    x[4] = np.nan                              # nothing admitted
+    x[7, ::7] = np.nan
+    x[12] = -np.inf                            # no mass
+    allowed = rng.random((rows, V)) < 0.3
+    q = rng.dirichlet(np.ones(V) * 0.3, rows).astype(np.float32)
+    q[2] = 1.0                                 # q covers p everywhere: no residual
+    q[3] = 0.0                                 # the residual is p
+    d = rng.integers(0, V, rows).astype(np.uint32)
+    d[1] = V - 3                               # in the partial last chunk
+    d[5] = NO
+    pols = [J.policy(temperature=T) for T in (1.0, 0.7, 1.0, 1.5, 1.0, 0.9)]
+    pols += [J.policy(temperature=1.0, exclude_stop=True), J.policy(temperature=2.0)]
+    pols += [J.policy(repetition=1.3), J.policy(),
+             J.policy(temperature=0.8, constrained=True), J.policy(temperature=1.2),
+             J.policy(temperature=1.0), J.policy(temperature=0.5)]
+    hist = [rng.integers(0, V, 300).astype(np.uint32) for _ in range(rows)]
+    u = rng.random(rows).astype(np.float32)
+    u[0] = 0.0
+    u[13] = np.float32(1.0) - np.float32(2.0 ** -24)
+    kw = dict(masks=WL.mask_words(allowed), histories=hist, generated=[100] * rows,
+              mark_prompt=[True] * rows, uniforms=u, stop=(int(d[6]), 17),
+              draft_tokens=d, drafted_rows=drafted)
+    if sparse:
+        cand = rng.integers(0, V, (rows, 16)).astype(np.uint32)
+        cand[:, 0] = d
+        cand[1, 3] = V - 1
+        kw.update(cand_ids=cand, cand_probs=rng.dirichlet(np.ones(16), rows).astype(np.float32))
+    else:
+        kw["dense_q"] = q
+    kw["logits_bf16" if bf16 else "logits"] = WL.to_bf16_bits(x) if bf16 else x
+    g, r = both(V, pols, **kw)
+    assert_same(g, r)
+    assert g["tokens"][4] == NO and g["tokens"][12] == NO
+    assert g["tokens"][6] != d[6]              # the stop token is excluded
+    assert g["draft_probs"][2] > 0.0
+
+
+def test_residual_launches_over_many_rows():
+    """More rows than one residual launch holds (256): drafted rows with no
+    cut (some with JF_NO_TOKEN drafts) interleaved with greedy rows, then
+    undrafted rows, two vocabulary chunks a row; every launch draws its own
+    rows."""
+    rng = np.random.default_rng(137)
+    V = 2 * 8192 + 100
+    rows = 300
+    x = rand_logits(rng, rows, V, scale=1.5)
+    q = rng.dirichlet(np.ones(V) * 0.5, rows).astype(np.float32)
+    d = rng.integers(0, V, rows).astype(np.uint32)
+    d[::11] = NO
+    pols = [J.policy() if k % 5 == 4 else J.policy(temperature=0.6 + 0.1 * (k % 7))
+            for k in range(rows)]
+    u = rng.random(rows).astype(np.float32)
+    g, r = both(V, pols, logits=x, uniforms=u, draft_tokens=d, drafted_rows=200, dense_q=q)
+    assert_same(g, r)
+
+
 FAR_OFFSETS = [0, 5, 10, 15, 20, 22, 30, 45, 60, 80]
 
 

@@ -97,3 +97,52 @@ def test_expired_wait_of_the_in_launch_draw():
     for _ in range(3):
         np.testing.assert_array_equal(call(), want)
     s.status()
+
+
+def test_expired_wait_of_the_residual_draw():
+    """Drafted rows with no cut drawn by the residual launch's finisher (each
+    row's last chunk block gathers the other chunks' slice words, the same
+    bounded wait), beside undrafted rows drawn in blocks of their own: bound
+    0 gives the drafted rows JF_NO_TOKEN, the others their tokens, and one
+    JF_ERR_DEVICE report; the next calls at the default bound are bit-exact
+    again."""
+    import torch
+    V, rows, drafted = 5 * 8192 + 76, 6, 4
+    rng = np.random.default_rng(7)
+    x = rng.normal(0, 1.5, (rows, V)).astype(np.float32)
+    u = rng.random(rows).astype(np.float32)
+    q = rng.dirichlet(np.ones(V) * 0.5, rows).astype(np.float32)
+    d = rng.integers(0, V, rows).astype(np.uint32)
+    pols = [J.policy(temperature=0.9)] * rows
+    ref = run_oracle(V, pols, logits=x, uniforms=u, draft_tokens=d, drafted_rows=drafted,
+                     dense_q=q)
+    dev = torch.device("cuda", 0)
+    s = J.Sampler(V, rows)
+    xt, ut = torch.from_numpy(x).to(dev), torch.from_numpy(u).to(dev)
+    dt = torch.from_numpy(d.view(np.int32)).to(dev)
+    qt = torch.from_numpy(q).to(dev)
+
+    def call():
+        out = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+        dp = torch.full((rows,), -1.0, dtype=torch.float32, device=dev)
+        s.sample(xt, pols, out, uniforms=ut, draft_tokens=dt, drafted_rows=drafted,
+                 dense_q=qt, out_draft_probs=dp)
+        torch.cuda.synchronize()
+        return out.cpu().numpy().view(np.uint32).copy(), dp.cpu().numpy()
+
+    def same(got):
+        np.testing.assert_array_equal(got[0], ref["tokens"])
+        np.testing.assert_array_equal(got[1], ref["draft_probs"])
+
+    same(call())
+    s.set_wait_bound(0)
+    tokens, _ = call()
+    assert np.all(tokens[:drafted] == NO), tokens
+    np.testing.assert_array_equal(tokens[drafted:], ref["tokens"][drafted:])
+    with pytest.raises(J.JfError) as e:
+        s.status()
+    assert e.value.code == J.JF_ERR_DEVICE
+    s.set_wait_bound(1 << 20)
+    for _ in range(3):
+        same(call())
+    s.status()
