@@ -4305,14 +4305,9 @@ struct RowSums {
   uint64_t R, T, W;
   uint32_t admitted, kept;
 };
-__device__ __forceinline__ RowSums row_sums(const SampleLaunch &a, uint32_t row, float inv_t) {
-  const uint32_t S = a.chunks, lane = lane_id();
-  const bool in = lane < S;
-  const uint32_t at = in ? lane : 0u;
-  const BlockHeader *h = a.headers + (uint64_t)row * S + at;
-  const float hm = h->maximum;
-  const uint32_t hadm = h->admitted, hcnt = h->count;
-  const uint64_t hmass = a.partials[(uint64_t)row * S + at].v[0];
+__device__ __forceinline__ RowSums row_sums_of(uint32_t S, float hm, uint32_t hadm,
+                                               uint32_t hcnt, uint64_t hmass, float inv_t) {
+  const bool in = lane_id() < S;
   RowSums r;
   r.m = in ? hm : -3.402823466e38f;
   r.M = wave_max_f32(r.m);
@@ -4322,6 +4317,12 @@ __device__ __forceinline__ RowSums row_sums(const SampleLaunch &a, uint32_t row,
   r.admitted = wave_sum_u32(in ? hadm : 0u);
   r.kept = wave_sum_u32(in ? hcnt : 0u);
   return r;
+}
+__device__ __forceinline__ RowSums row_sums(const SampleLaunch &a, uint32_t row, float inv_t) {
+  const uint32_t S = a.chunks, at = lane_id() < S ? lane_id() : 0u;
+  const BlockHeader *h = a.headers + (uint64_t)row * S + at;
+  return row_sums_of(S, h->maximum, h->admitted, h->count,
+                     a.partials[(uint64_t)row * S + at].v[0], inv_t);
 }
 
 // One wave: the plain draw of an uncut row (uncut_draw's): the chunk and
@@ -4351,18 +4352,24 @@ __device__ __forceinline__ void plain_draw_wave(const SampleLaunch &a, uint32_t 
 template <int DT>
 __device__ __forceinline__ void plain_row_block(const SampleLaunch &a, uint32_t row, LeanLds &s) {
   const uint32_t S = a.chunks, lane = lane_id();
+  // Every load the row needs first, none waiting on another: the record,
+  // the uniform, the chunk summaries (lane c < S).
+  const bool in = lane < S;
+  const uint32_t at = in ? lane : 0u;
   const RowParams rp = a.params[row];
+  const float u = row_uniform(a, row);
+  const BlockHeader *h = a.headers + (uint64_t)row * S + at;
+  const float hm = h->maximum, hbv = h->best_value;
+  const uint32_t hadm = h->admitted, hcnt = h->count, hbi = h->best_id;
+  const uint64_t hmass = a.partials[(uint64_t)row * S + at].v[0];
   if (!(rp.flags & kRowSampled)) {
-    const bool in = lane < S;
-    const BlockHeader *h = a.headers + (uint64_t)row * S + (in ? lane : 0u);
-    float hv = in ? h->best_value : -__builtin_inff();
-    uint32_t hi = in ? h->best_id : kNoToken;
+    float hv = in ? hbv : -__builtin_inff();
+    uint32_t hi = in ? hbi : kNoToken;
     wave_argmax(hv, hi);
     if (lane == 0) write_result(a, row, hi, 0.0f, 0);
     return;
   }
-  const float u = row_uniform(a, row);
-  const RowSums r = row_sums(a, row, rp.inv_t);
+  const RowSums r = row_sums_of(S, hm, hadm, hcnt, hmass, rp.inv_t);
   const bool none = r.admitted == 0 || r.M == __builtin_inff();
   if (none || r.W == 0) {
     // The sentinel (a row of -inf keeps every token at probability 0).
