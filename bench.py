@@ -115,6 +115,9 @@ def build_workload(cfg, mode, history="uniform"):
         hist_bytes = c["q"].nbytes if sampled else 0
         if sampled:
             w["uniforms"] = c["uniforms"]
+            # The select pass also stores the drafted rows' weights for
+            # their residual pass.
+            w["kernel"] = "jf::select_fast_kernel<0, false, jf::NoRows, jf::StoreWeights>"
     else:
         c = WL.config5()
         B = c["logits_bf16"].shape[0]
@@ -130,7 +133,9 @@ def build_workload(cfg, mode, history="uniform"):
     w["rows"] = rows
     w["alg_bytes"] = lg.nbytes + hist_bytes + rows * 4 * 2  # + uniforms + outputs
     # The select kernel reads the logits and the history ids or mask words;
-    # C4's dense draft q is read only by the multi-pass draw.
+    # C4's dense draft q is read only by the residual pass (C4 sampled's
+    # select also writes the drafted rows' weights for that pass: traffic
+    # beyond these bytes).
     w["select_bytes"] = lg.nbytes + (0 if cfg == 4 else hist_bytes)
     return w
 

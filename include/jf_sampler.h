@@ -88,7 +88,11 @@ int jf_policy_validate(const jf_policy *policy);
 int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
                       jf_sampler **out);
 int jf_sampler_destroy(jf_sampler *sampler);
-/* Bytes of device scratch the sampler holds (Sampling::workspace role). */
+/* Bytes of device scratch the sampler holds (Sampling::workspace role):
+ * what jf_sampler_create allocates, plus the weights a call with drafted
+ * fp32 rows and no cut had the select pass store for their residual pass
+ * (4 bytes a token of those rows' chunks, allocated by the first such call
+ * and grown with the rows, until jf_sampler_destroy). */
 uint64_t jf_sampler_workspace_bytes(const jf_sampler *sampler);
 
 /* No counterpart in the reference (whose last-arriving group never waits,

@@ -77,9 +77,12 @@ __device__ __forceinline__ uint64_t quantize(float w) {
 // has 24 mantissa bits and exponent -1 or 0) shifted by n + 14, here
 // (Y << 32) >> (18 - n); a shift of 63 gives zero, below -86 or for NaN.
 // Checked equal to quantize(exp_weight(x)) for every float x in [-90, 0]
-// and NaN.
-__device__ __forceinline__ uint64_t quantized_weight(float value, float maximum,
-                                                     float inv_t) {
+// and NaN. weight_yk returns Y and that shift k = min(18 - n, 63).
+struct WeightYK {
+  uint32_t Y;
+  int k;
+};
+__device__ __forceinline__ WeightYK weight_yk(float value, float maximum, float inv_t) {
   const float x_in = (value - maximum) * inv_t;
   const float x = __builtin_fminf(__builtin_fmaxf(x_in, -87.0f), 88.0f);
   const float n = __builtin_rintf(x * 1.44269504088896341f);
@@ -93,38 +96,47 @@ __device__ __forceinline__ uint64_t quantized_weight(float value, float maximum,
   p = __builtin_fmaf(p, r, 5.0000001201e-1f);
   const float r2 = r * r;
   const float y = __builtin_fmaf(p, r2, r) + 1.0f;
-  const uint32_t Y = (uint32_t)(y * 0x1p30f);
-  const int k = x_in >= -86.0f ? min(18 - (int)n, 63) : 63;
-  return ((uint64_t)Y << 32) >> k;
+  WeightYK w;
+  w.Y = (uint32_t)(y * 0x1p30f);
+  w.k = x_in >= -86.0f ? min(18 - (int)n, 63) : 63;
+  return w;
+}
+__device__ __forceinline__ uint64_t quantized_weight(float value, float maximum,
+                                                     float inv_t) {
+  const WeightYK w = weight_yk(value, maximum, inv_t);
+  return ((uint64_t)w.Y << 32) >> w.k;
 }
 
-// scale_by(quantized_weight(value, maximum, inv_t), scale) in one 32 x 32-bit
-// product, for a packed chunk scale s << 32 | R (R < 2^32, s >= 31, or R = 0
-// with s = 64): the weight is (Y << 32) >> k (Y < 2^31, k in [18, 63]), so for
-// k <= 32 it is Y * 2^(32 - k) and the scaled weight is (Y * R) >> (s + k - 32);
-// for k > 32 the weight is m = Y >> (k - 32) and the scaled weight
-// (m * R) >> s. Both products stay below 2^63, so a shift clamped to 63 gives
-// the zero that any larger shift would.
-__device__ __forceinline__ uint64_t scaled_weight(float value, float maximum, float inv_t,
-                                                  uint64_t scale) {
-  const float x_in = (value - maximum) * inv_t;
-  const float x = __builtin_fminf(__builtin_fmaxf(x_in, -87.0f), 88.0f);
-  const float n = __builtin_rintf(x * 1.44269504088896341f);
-  float rr = __builtin_fmaf(n, -0.693359375f, x);
-  rr = __builtin_fmaf(n, 2.12194440e-4f, rr);
-  float p = 1.9875691500e-4f;
-  p = __builtin_fmaf(p, rr, 1.3981999507e-3f);
-  p = __builtin_fmaf(p, rr, 8.3334519073e-3f);
-  p = __builtin_fmaf(p, rr, 4.1665795894e-2f);
-  p = __builtin_fmaf(p, rr, 1.6666665459e-1f);
-  p = __builtin_fmaf(p, rr, 5.0000001201e-1f);
-  const float r2 = rr * rr;
-  const float y = __builtin_fmaf(p, r2, rr) + 1.0f;
-  const uint32_t Y = (uint32_t)(y * 0x1p30f);
-  const int k = x_in >= -86.0f ? min(18 - (int)n, 63) : 63;
+// scale_by of the weight (Y << 32) >> k by a packed chunk scale s << 32 | R
+// (R < 2^32, s >= 31, or R = 0 with s = 64) in one 32 x 32-bit product: the
+// weight is Y (< 2^31) with k in [18, 63], so for k <= 32 it is
+// Y * 2^(32 - k) and the scaled weight is (Y * R) >> (s + k - 32); for k > 32
+// it is m = Y >> (k - 32) and the scaled weight (m * R) >> s. Both products
+// stay below 2^63, so a shift clamped to 63 gives the zero that any larger
+// shift would.
+__device__ __forceinline__ uint64_t scale_yk(uint32_t Y, int k, uint64_t scale) {
   const uint32_t m = Y >> max(k - 32, 0);
   const int sh = min((int)(scale >> 32) - 32 + min(k, 32), 63);
   return ((uint64_t)m * (uint32_t)scale) >> sh;
+}
+// scale_by(quantized_weight(value, maximum, inv_t), scale).
+__device__ __forceinline__ uint64_t scaled_weight(float value, float maximum, float inv_t,
+                                                  uint64_t scale) {
+  const WeightYK w = weight_yk(value, maximum, inv_t);
+  return scale_yk(w.Y, w.k, scale);
+}
+
+// A weight's Y and k in one word: Y's low 6 bits are zero (Y = y * 2^30
+// with y's 24-bit mantissa at exponent -1 or 0), so Y >> 6 takes 25 bits,
+// and k (at most 63) the 6 above them.
+__device__ __forceinline__ uint32_t pack_yk(const WeightYK &w) {
+  return (w.Y >> 6) | ((uint32_t)w.k << 25);
+}
+__device__ __forceinline__ WeightYK unpack_yk(uint32_t p) {
+  WeightYK w;
+  w.Y = (p & 0x1ffffffu) << 6;
+  w.k = (int)(p >> 25);
+  return w;
 }
 
 // e^x in double: the Cody-Waite reduction x = n ln2 + r (n = rint(x log2 e),

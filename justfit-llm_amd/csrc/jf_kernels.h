@@ -152,6 +152,12 @@ struct SampleLaunch {
   uint32_t epoch;         // the call's tag of its packed greedy bests (1..4095)
   uint32_t wait_bound;    // reads of a packed best before its wait gives up
   uint32_t *status;       // set to 1 when a wait gave up (host-mapped), or NULL
+  // Drafted rows with no cut (kRowLean) in an all-fast fp32 launch: the
+  // select pass also stores each token's weight there as pack_yk (row r at
+  // r * lean_stride, chunk-major like the logits), and residual_kernel
+  // reads it instead of the logits; NULL otherwise.
+  uint32_t *lean_weights;
+  uint64_t lean_stride;
 };
 
 // The fast selection launch: the per-row facts every block needs before its
@@ -178,6 +184,8 @@ struct FastLaunch {
   uint32_t mapped;            // blockIdx.y selects row row_of[blockIdx.y]
                               // (a launch split between the two kernels;
                               // the kernel takes it as a preloaded argument)
+  uint32_t lean_bits[kKernargRows / 32];  // bit y: row blockIdx.y stores its
+                                          // weights (a.lean_weights)
 };
 // The per-row facts of a launch that is not uniform, by blockIdx.y.
 struct FastRows {
@@ -192,9 +200,12 @@ struct FastRows {
 struct NoRows {};
 // The fast selection's last argument, naming what its finishing blocks do
 // beyond selecting: nothing more, draw rows with no cut (UncutFinish), or
-// (an AcceptTreeLaunch) run each lane's tree acceptance.
+// (an AcceptTreeLaunch) run each lane's tree acceptance; StoreWeights is
+// NoFinish that also stores the drafted rows' weights (a.lean_weights), a
+// separate instantiation since the stores take registers.
 struct NoFinish {};
 struct UncutFinish {};
+struct StoreWeights {};
 constexpr uint32_t kExtraOffsetMask = (1u << 27) - 1u;
 
 // Multi-pass stages, in launch order.
@@ -363,6 +374,10 @@ struct SampleScratch {
   uint32_t *status;         // device address of a host-mapped word, or NULL
   uint32_t epoch;           // this call's tag (1..4095)
   uint32_t wait_bound;      // reads of a packed best before its wait gives up
+  // Room for `rows` drafted rows' stored weights (rows x max_chunks x 8192
+  // words), from the owner (called with the upload context), or NULL when
+  // the owner keeps none: the residual pass then reads the logits.
+  uint32_t *(*lean_weights)(void *ctx, uint32_t rows);
 };
 
 // How a selection's host-built row parameters reach scratch.params before

@@ -1812,11 +1812,15 @@ __device__ __forceinline__ void merge_row(const SampleLaunch &a,
 // count per wave into s.wcount. `side` holds the penalized tokens whose own
 // registers are dropped (NaN), so every token counts once; their weights join
 // their slices through LDS. s.slices is zero on entry (cleared before the
-// block's last barrier). Ends with a barrier. Block-uniform.
+// block's last barrier). Ends with a barrier. Block-uniform. With `wout`
+// (fp32 rows, no penalized token: a drafted row's residual pass reads them),
+// every token's weight is also stored there as pack_yk, at its offset in
+// the chunk.
 template <int DT, class L>
 __device__ __forceinline__ void uncut_slices(const float (&xs)[Geo<DT>::TPL],
                                              const SideEntries &side, uint32_t base,
-                                             float bmax, float inv_t, L &s) {
+                                             float bmax, float inv_t, L &s,
+                                             uint32_t *wout = nullptr) {
   constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS, SLAB = Geo<DT>::SLAB;
   static_assert(LOADS % 4 == 0, "loads in groups of four");
   const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -1828,11 +1832,24 @@ __device__ __forceinline__ void uncut_slices(const float (&xs)[Geo<DT>::TPL],
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       lv[jj] = 0;
+      uint32_t pk[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const float x = xs[(h * 4 + jj) * VEC + e];
-        lv[jj] += quantized_weight(x, bmax, inv_t);
+        const WeightYK wy = weight_yk(x, bmax, inv_t);
+        lv[jj] += ((uint64_t)wy.Y << 32) >> wy.k;
+        pk[e] = pack_yk(wy);
         n += x == x;
+      }
+      if constexpr (VEC == 4) {
+        if (wout) {
+          u32x4 v;
+          v.x = pk[0];
+          v.y = pk[1];
+          v.z = pk[2];
+          v.w = pk[3];
+          *(u32x4 *)(wout + (h * 4 + jj) * SLAB + tid * VEC) = v;
+        }
       }
     }
     // Lane l holds the wave's sum of load h * 4 + l / 16.
@@ -1864,10 +1881,11 @@ template <int DT, class L>
 __device__ __forceinline__ void uncut_summary(const float (&xs)[Geo<DT>::TPL],
                                               const SideEntries &side, uint32_t base,
                                               float bmax, uint32_t badm, float inv_t, L &s,
-                                              BlockHeader *hdr, StagePartial *part) {
+                                              BlockHeader *hdr, StagePartial *part,
+                                              uint32_t *wout = nullptr) {
   constexpr uint32_t G = Geo<DT>::LOADS * kWaves;
   const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  uncut_slices<DT>(xs, side, base, bmax, inv_t, s);
+  uncut_slices<DT>(xs, side, base, bmax, inv_t, s, wout);
   if (w == 0) {
     const uint64_t v = lane < G ? s.slices[lane] : 0ull;
     if (lane < G) part->v[1 + lane] = v;
@@ -2580,6 +2598,14 @@ __device__ __forceinline__ const SampleLaunch &fast_launch_record() {
   typedef const __attribute__((address_space(4))) FastKernelArgs *KernargPtr;
   return ((const FastKernelArgs *)(KernargPtr)u)->f.a;
 }
+// Whether the launch's row y stores its weights (FastLaunch::lean_bits, read
+// in place like the record).
+__device__ __forceinline__ bool fast_lean_row(uint32_t y) {
+  uint64_t u = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(u));
+  typedef const __attribute__((address_space(4))) FastKernelArgs *KernargPtr;
+  return (((const FastKernelArgs *)(KernargPtr)u)->f.lean_bits[y >> 5] >> (y & 31)) & 1u;
+}
 
 // Rows with no cut finished in the select launch (every row of the launch
 // sampled with no min-p, top-k or top-p cut, no draft, penalty, extra token
@@ -2724,6 +2750,7 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
   constexpr uint32_t VMASK = (1u << VEC) - 1u;
   constexpr bool kRows = !std::is_same_v<R, NoRows>;
   constexpr bool FUSE = std::is_same_v<FIN, UncutFinish>;
+  constexpr bool STORE = std::is_same_v<FIN, StoreWeights>;
   constexpr bool ACCEPT = std::is_same_v<FIN, AcceptTreeLaunch>;
   static_assert(TPL == 32, "one drop bit per register");
   static_assert(kRows || !XTRA, "extra tokens travel in the per-row facts");
@@ -3068,11 +3095,16 @@ __global__ __launch_bounds__(kThreads) void select_fast_kernel(
     // The row keeps every admitted token: the uncut kernel's chunk summary,
     // or (FUSE) the row finished here.
     const float inv_t = uni ? prec.inv_t : rp.inv_t;
-    if constexpr (FUSE)
+    if constexpr (FUSE) {
       finish_uncut_row<DT>(a, xs, side, base, bmax, badm, inv_t, s, row, chunk, S, flags);
-    else
+    } else {
+      // A drafted row's weights for its residual pass (fp32, no penalty).
+      uint32_t *wout = nullptr;
+      if (STORE && fast_lean_row(lrow))
+        wout = a.lean_weights + (uint64_t)row * a.lean_stride + (uint64_t)chunk * CHUNK;
       uncut_summary<DT>(xs, side, base, bmax, badm, inv_t, s, hdr,
-                        a.partials + (uint64_t)row * S + chunk);
+                        a.partials + (uint64_t)row * S + chunk, wout);
+    }
     return;
   }
   uint32_t thr = tk;
@@ -4398,8 +4430,9 @@ __device__ __forceinline__ void plain_row_block(const SampleLaunch &a, uint32_t 
 // waits end: the row's other blocks were dispatched before it (block
 // index order) and wait on nothing. Should one give up, the row gets
 // JF_NO_TOKEN and the status word is set.
-template <int DT, bool DENSE>
+template <int DT, bool DENSE, bool PACKED>
 __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
+  static_assert(!PACKED || DT == 0, "packed weights come from fp32 select passes");
   constexpr int VEC = Geo<DT>::VEC, LOADS = Geo<DT>::LOADS, SLAB = Geo<DT>::SLAB;
   constexpr uint32_t CHUNK = Geo<DT>::CHUNK, G = LOADS * kWaves;
   constexpr int HL = LOADS / 2, HV = HL * VEC;  // loads and values per half
@@ -4469,13 +4502,28 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
                      ((a.stop0 >= base && a.stop0 < base + CHUNK) ||
                       (a.stop1 >= base && a.stop1 < base + CHUNK));
   uint64_t total = 0;
+  // PACKED: the select pass stored each token's weight (pack_yk), read in
+  // place of the logit; the draft token's float weight still comes from
+  // its logit, requested here.
+  const uint32_t *wrow = PACKED ? a.lean_weights + (uint64_t)row * a.lean_stride : nullptr;
+  float xdraft = 0.0f;
+  if (PACKED && draft < V && draft / CHUNK == chunk && tid == ((draft - base) % SLAB) / VEC)
+    xdraft = ((const float *)a.logits)[(uint64_t)row * a.stride + draft];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     float xv[HV], qv[HV];
+    uint32_t pv[HV];
 #pragma unroll
     for (int jj = 0; jj < HL; ++jj) {
       const uint32_t t0 = lane_base + (h * HL + jj) * SLAB;
-      if constexpr (DT == 0) {
+      if constexpr (PACKED) {
+        // The weights cover whole chunks (past the vocabulary: zero weights).
+        const u32x4 v = *(const u32x4 *)(wrow + t0);
+        pv[jj * 4 + 0] = v.x;
+        pv[jj * 4 + 1] = v.y;
+        pv[jj * 4 + 2] = v.z;
+        pv[jj * 4 + 3] = v.w;
+      } else if constexpr (DT == 0) {
         const float *rowp = (const float *)a.logits + (uint64_t)row * a.stride;
         if (vec_x) {
           const f32x4 v = *(const f32x4 *)(rowp + t0);
@@ -4522,16 +4570,28 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
         } else {
           qv[jj * VEC + e] = draft_q(a, rp, t, s);
         }
-        if (stops && (t == a.stop0 || t == a.stop1)) xv[jj * VEC + e] = kNotAdmitted;
+        if (stops && (t == a.stop0 || t == a.stop1)) {
+          if constexpr (PACKED)
+            pv[jj * VEC + e] = 63u << 25;
+          else
+            xv[jj * VEC + e] = kNotAdmitted;
+        }
       }
     }
     uint64_t lv[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int jj = 0; jj < HL; ++jj)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e)
-        lv[jj] += residual_of(scaled_weight(xv[jj * VEC + e], mc, inv_t, Rc), W,
-                              qv[jj * VEC + e]);
+      for (int e = 0; e < VEC; ++e) {
+        uint64_t wq;
+        if constexpr (PACKED) {
+          const WeightYK wy = unpack_yk(pv[jj * VEC + e]);
+          wq = scale_yk(wy.Y, wy.k, Rc);
+        } else {
+          wq = scaled_weight(xv[jj * VEC + e], mc, inv_t, Rc);
+        }
+        lv[jj] += residual_of(wq, W, qv[jj * VEC + e]);
+      }
     // Lane l holds the wave's sum of load h * HL + l / 16 (l / 16 < HL).
     const uint64_t sl = wave_sums_u64<4>(lv);
     if (lane % 16 == 0 && lane / 16 < (uint32_t)HL) {
@@ -4547,10 +4607,14 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
     if (draft < V && draft / CHUNK == chunk) {
       const uint32_t o = draft - base, j = o / SLAB;
       if (j / HL == (uint32_t)h && tid == (o % SLAB) / VEC) {
-        const uint32_t i = (j % HL) * VEC + o % VEC;
         float xd = 0.0f;
+        if constexpr (PACKED) {
+          xd = stops && (draft == a.stop0 || draft == a.stop1) ? kNotAdmitted : xdraft;
+        } else {
+          const uint32_t i = (j % HL) * VEC + o % VEC;
 #pragma unroll
-        for (int k = 0; k < HV; ++k) xd = (uint32_t)k == i ? xv[k] : xd;
+          for (int k = 0; k < HV; ++k) xd = (uint32_t)k == i ? xv[k] : xd;
+        }
         const uint32_t wd = f2u(weight_of(xd, mc, inv_t));
         if (finisher)
           s.dw = wd;
@@ -5024,6 +5088,11 @@ int launch_select_fast(const FastLaunch &f, const FastRows *fr, uint32_t rows, u
     else
       dtype == 0 ? go(select_fast_kernel<0, false, FastRows, UncutFinish>, *fr, UncutFinish{})
                  : go(select_fast_kernel<1, false, FastRows, UncutFinish>, *fr, UncutFinish{});
+  } else if (f.a.lean_weights) {
+    // Stored weights: fp32 rows with no extra token only.
+    if (dtype != 0 || extras) return (int)hipErrorInvalidValue;
+    !fr ? go(select_fast_kernel<0, false, NoRows, StoreWeights>, NoRows{}, StoreWeights{})
+        : go(select_fast_kernel<0, false, FastRows, StoreWeights>, *fr, StoreWeights{});
   } else if (!fr) {
     dtype == 0 ? go(select_fast_kernel<0, false, NoRows, NoFinish>, NoRows{}, NoFinish{})
                : go(select_fast_kernel<1, false, NoRows, NoFinish>, NoRows{}, NoFinish{});
@@ -5054,17 +5123,24 @@ int launch_residual(const LeanLaunch &l, uint32_t dtype, void *stream) {
   const dim3 grid(l.n_lean * l.a.chunks), block(kThreads);
   const hipStream_t st = (hipStream_t)stream;
   // A sparse draft's 16-candidate lookup per token takes about 30 more
-  // registers than a dense q row: separate instantiations.
+  // registers than a dense q row: separate instantiations. With the select
+  // pass's stored weights (fp32 rows), the weights are read in place of the
+  // logits.
+  const bool packed = l.a.lean_weights != nullptr;
   if (l.a.dense_q) {
-    if (dtype == 0)
-      hipLaunchKernelGGL((residual_kernel<0, true>), grid, block, 0, st, l);
+    if (dtype == 0 && packed)
+      hipLaunchKernelGGL((residual_kernel<0, true, true>), grid, block, 0, st, l);
+    else if (dtype == 0)
+      hipLaunchKernelGGL((residual_kernel<0, true, false>), grid, block, 0, st, l);
     else
-      hipLaunchKernelGGL((residual_kernel<1, true>), grid, block, 0, st, l);
+      hipLaunchKernelGGL((residual_kernel<1, true, false>), grid, block, 0, st, l);
   } else {
-    if (dtype == 0)
-      hipLaunchKernelGGL((residual_kernel<0, false>), grid, block, 0, st, l);
+    if (dtype == 0 && packed)
+      hipLaunchKernelGGL((residual_kernel<0, false, true>), grid, block, 0, st, l);
+    else if (dtype == 0)
+      hipLaunchKernelGGL((residual_kernel<0, false, false>), grid, block, 0, st, l);
     else
-      hipLaunchKernelGGL((residual_kernel<1, false>), grid, block, 0, st, l);
+      hipLaunchKernelGGL((residual_kernel<1, false, false>), grid, block, 0, st, l);
   }
   return (int)hipGetLastError();
 }

@@ -135,7 +135,8 @@ extern "C" int jf_sample_static(uint32_t vocabulary, const jf_sample_args *args,
                              kStaticChunks,
                              nullptr,
                              epochs.fetch_add(1, std::memory_order_relaxed) % 4095u + 1u,
-                             1u << 20};
+                             1u << 20,
+                             nullptr};
   jf::RowParams params[kStaticRows];
   return jf::sample_core(vocabulary, sc, args, params, static_upload, base, stream);
 }

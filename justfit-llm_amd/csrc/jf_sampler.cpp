@@ -225,6 +225,10 @@ struct jf_sampler {
   uint32_t *status_device = nullptr;
   uint32_t epoch = 0;                 // the last call's tag, 1..4095
   uint32_t wait_bound = 1u << 20;     // reads of a packed best before giving up
+  // Drafted rows' weights stored by the select pass for their residual pass
+  // (lean_rows rows x max_chunks x 8192 words), allocated on first need.
+  uint32_t *lean_weights = nullptr;
+  uint32_t lean_rows = 0;
 };
 
 extern "C" {
@@ -241,6 +245,7 @@ int jf_sampler_destroy(jf_sampler *s) {
   (void)hipFree(s->bests);
   (void)hipFree(s->states);
   (void)hipFree(s->partials);
+  (void)hipFree(s->lean_weights);
   if (s->status_host) (void)hipHostFree(s->status_host);
   delete s;
   return JF_OK;
@@ -314,7 +319,9 @@ int jf_sampler_create(uint32_t vocabulary, uint32_t max_rows,
 }
 
 uint64_t jf_sampler_workspace_bytes(const jf_sampler *s) {
-  return s ? s->workspace_bytes : 0;
+  return s ? s->workspace_bytes +
+                 (uint64_t)s->lean_rows * s->max_chunks * jf::kChunkF32 * sizeof(uint32_t)
+           : 0;
 }
 
 static int check_device(int device) {
@@ -820,6 +827,15 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
   L.epoch = sc.epoch;
   L.wait_bound = sc.wait_bound;
   L.status = sc.status;
+  // Drafted rows with no cut in an all-fast fp32 launch with no extra
+  // tokens: the select pass stores their weights and the residual pass
+  // reads them.
+  bool any_extra = false;
+  for (uint32_t r = 0; r < rows; ++r) any_extra |= params[r].extra_count != 0;
+  if (n_lean && fast && !any_extra && a->dtype == JF_DTYPE_F32 && sc.lean_weights) {
+    L.lean_weights = sc.lean_weights(upload_ctx, rows);
+    L.lean_stride = (uint64_t)L.chunks * jf::kChunkF32;
+  }
 
   if ((a->select_start_event == nullptr) != (a->select_done_event == nullptr))
     return fail(JF_ERR_INVALID_ARGUMENT, "select events come in pairs");
@@ -902,7 +918,12 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
       const uint32_t n = std::min<uint32_t>(n_fast - i0, jf::kKernargRows);
       F.row_base = split ? 0u : i0;
       bool extras = false;
-      for (uint32_t i = 0; i < n; ++i) extras |= params[row_at(i0 + i)].extra_count != 0;
+      std::memset(F.lean_bits, 0, sizeof(F.lean_bits));
+      for (uint32_t i = 0; i < n; ++i) {
+        const jf::RowParams &rp = params[row_at(i0 + i)];
+        extras |= rp.extra_count != 0;
+        if (rp.flags & jf::kRowLean) F.lean_bits[i >> 5] |= 1u << (i & 31);
+      }
       // Per-row facts only where the kernel reads them (a launch that is not
       // uniform, mapped or with extra tokens).
       const bool rows_arg = !uniform || split || extras;
@@ -1030,6 +1051,27 @@ int sample_core(uint32_t V, const SampleScratch &sc, const jf_sample_args *a,
 
 namespace {
 
+// Room for `rows` drafted rows' stored weights, grown on first need (the
+// free of a smaller buffer waits for the kernels that use it); NULL when the
+// allocation fails, and the residual pass then reads the logits.
+uint32_t *sampler_lean_weights(void *ctx, uint32_t rows) {
+  jf_sampler *s = (jf_sampler *)ctx;
+  if (rows > s->lean_rows) {
+    (void)hipFree(s->lean_weights);
+    s->lean_weights = nullptr;
+    s->lean_rows = 0;
+    void *p = nullptr;
+    if (hipMalloc(&p, (size_t)rows * s->max_chunks * jf::kChunkF32 * sizeof(uint32_t)) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    s->lean_weights = (uint32_t *)p;
+    s->lean_rows = rows;
+  }
+  return s->lean_weights;
+}
+
 // The sampler's row parameters, uploaded through its staging ring only when
 // they differ from the last upload (stream order keeps earlier launches on
 // the values they were enqueued with).
@@ -1089,9 +1131,11 @@ static int sample_impl(jf_sampler *s, const jf_sample_args *a, void *stream,
   if (!a->rows || a->rows > s->max_rows)
     return fail(JF_ERR_INVALID_ARGUMENT, "invalid sampling batch width");
   s->epoch = s->epoch % 4095u + 1u;
-  const jf::SampleScratch sc{s->params,    s->headers,  s->cands,    s->counters,
-                             s->bests,     s->states,   s->partials, s->max_rows,
-                             s->max_chunks, s->status_device, s->epoch, s->wait_bound};
+  const jf::SampleScratch sc{s->params,    s->headers,      s->cands,
+                             s->counters,  s->bests,        s->states,
+                             s->partials,  s->max_rows,     s->max_chunks,
+                             s->status_device, s->epoch,    s->wait_bound,
+                             sampler_lean_weights};
   if (s->host_params.size() < a->rows) {
     try {
       s->host_params.resize(a->rows);
