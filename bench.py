@@ -39,7 +39,10 @@ def parse():
                          "the engine's penalized chain verify (4 lanes x 16 rows, "
                          "V=248320, extras and sparse drafts) plus chain acceptance")
     ap.add_argument("--mode", default="auto",
-                    help="C3/C4: greedy or sampled (auto: sampled)")
+                    help="C3/C4: greedy or sampled (auto: sampled); C2: general runs "
+                         "C2's batch through the general kernels (rows one float past "
+                         "16-byte alignment, top-k 3000: select_kernel, merge_kernel "
+                         "and the multi-pass stages)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="bound of the CPU-baseline sample")
     ap.add_argument("--history", default="uniform", choices=["uniform", "zipf", "mixed"],
@@ -81,12 +84,21 @@ def build_workload(cfg, mode, history="uniform"):
                      if r % every == 0 else h for r, h in enumerate(hists)]
             label = ("2048 Zipf(1.2)-clustered ids" if every == 1 else
                      "2048 ids, every 4th row Zipf(1.2)-clustered")
-        w.update(V=c["V"], logits=c["logits"], policies=[J.policy(**c["policy"])] * B,
+        pol = dict(c["policy"])
+        name = ("C2 sampled B=64 V=151936 fp32 T0.7 top-k 50 top-p 0.9 "
+                f"presence 0.5 frequency 0.3 over {label}")
+        if mode == "general":
+            # The kernels a call takes when the fast pass and the small merge
+            # cannot: rows whose logits start one float past a 16-byte
+            # boundary (an engine's views into a padded buffer) and a top-k
+            # past the merge's lists.
+            pol["top_k"] = 3000
+            w["unaligned"] = True
+            w["kernel"] = "jf::select_kernel<0>"
+            name = name.replace("top-k 50", "top-k 3000") + ", rows 4 bytes past alignment"
+        w.update(V=c["V"], logits=c["logits"], policies=[J.policy(**pol)] * B,
                  histories=hists, generated=c["generated"], mark_prompt=False,
-                 uniforms=c["uniforms"],
-                 name="C2 sampled B=64 V=151936 fp32 T0.7 top-k 50 top-p 0.9 "
-                      f"presence 0.5 frequency 0.3 over {label}",
-                 dtype="f32")
+                 uniforms=c["uniforms"], name=name, dtype="f32")
         hist_bytes = B * 2048 * 4
     elif cfg == 3:
         c = WL.config3()
@@ -156,7 +168,15 @@ class GpuStep:
             base = torch.from_numpy(w["logits_bf16"].view(np.int16)).view(torch.bfloat16)
         per = base.numel() * base.element_size()
         copies = max(2, -(-ROTATE_BYTES // per))
-        self.copies = [base.to(dev) for _ in range(copies)]
+        if w.get("unaligned"):
+            # Each row one element past its buffer row's start.
+            def shifted():
+                t = torch.empty((base.shape[0], base.shape[1] + 1), dtype=base.dtype, device=dev)
+                t[:, 1:] = base.to(dev)
+                return t[:, 1:]
+            self.copies = [shifted() for _ in range(copies)]
+        else:
+            self.copies = [base.to(dev) for _ in range(copies)]
         self.sampler = J.Sampler(V, rows)
         self.kw = []
         self.tables = []
@@ -624,7 +644,8 @@ PROFILE_NAMES = {(1, "auto"): "select_c1", (2, "auto"): "select_merge_c2",
                  (4, "greedy"): "select_c4_greedy", (4, "sampled"): "select_uncut_c4_sampled",
                  (5, "auto"): "select_merge_c5", (2, "zipf"): "select_merge_c2_zipf",
                  (2, "mixed"): "select_merge_c2_mixed", ("draft", "auto"): "draft_select",
-                 ("gather", "auto"): "tree_gather", ("verify", "auto"): "select_verify"}
+                 ("gather", "auto"): "tree_gather", ("verify", "auto"): "select_verify",
+                 (2, "general"): "select_general_c2"}
 
 
 def profile_key(cfg, mode, history="uniform"):
@@ -632,6 +653,8 @@ def profile_key(cfg, mode, history="uniform"):
         return (cfg, "greedy" if mode == "greedy" else "sampled")
     if cfg == 2 and history != "uniform":
         return (cfg, history)
+    if cfg == 2 and mode == "general":
+        return (cfg, "general")
     return (cfg, "auto")
 
 
