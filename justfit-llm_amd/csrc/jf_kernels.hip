@@ -4443,21 +4443,24 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const uint32_t lean = blockIdx.x / S, chunk = blockIdx.x % S;
   const uint32_t row = l.row_of[lean];
-  // A drawing launch's last chunk blocks first draw the rows without a
-  // residual pass, lean row j's block rows n_lean + j + k n_lean, one per
-  // wave at a time (little else is live yet): the block's own chunk is the
-  // row's partial one when the vocabulary does not fill the last chunk, so
-  // this mostly takes time it would spend waiting for the row's other
+  // A drawing launch's last chunk blocks also draw the rows without a
+  // residual pass: waves 1-3 of lean row j's block take rows
+  // n_lean + j + k n_lean, one per wave at a time, while wave 0 reads the
+  // row's summaries, before the block's own chunk. That chunk is the row's
+  // partial one when the vocabulary does not fill the last chunk, so this
+  // mostly takes time the block would spend waiting for the row's other
   // blocks.
   const bool finisher = l.draw && chunk + 1 == S;
-  if (finisher)
-    for (uint32_t i = lean + w * l.n_lean; i < l.n_plain; i += kWaves * l.n_lean)
+  const auto draw_plain_share = [&]() {
+    for (uint32_t i = lean + (w - 1) * l.n_lean; i < l.n_plain; i += (kWaves - 1) * l.n_lean)
       plain_row_block<DT>(a, l.row_of[l.n_lean + i], s);
+  };
   const RowParams rp = a.params[row];
   const uint32_t draft = row_draft(a, rp);
   if (draft == kNoToken) {
     // Drawn plainly: by uncut_kernel, or here by chunk 0's block.
     if (l.draw && chunk == 0 && w == 0) plain_row_block<DT>(a, row, s);
+    if (finisher && w != 0) draw_plain_share();
     return;
   }
   const uint64_t tag10 = ((uint64_t)(a.epoch & 0x1ffu) << 1) | 1ull;
@@ -4484,6 +4487,8 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(LeanLaunch l) {
       s.ok = !none && r.W != 0 ? 1u : 0u;
       s.kept = none ? 0u : r.kept;
     }
+  } else if (finisher) {
+    draw_plain_share();
   }
   stage_candidates(a, rp, s);  // ends with a barrier
   if (!s.ok) {
