@@ -1,6 +1,6 @@
 """Benchmark of the MI355X logits->token step (one GPU).
 
-Default: configuration C2 of BASELINE.json (the headline): one sampled step
+Default: configuration C2 (the headline benchmark): one sampled step
 over B=64 rows of V=151,936 fp32 logits with presence/frequency penalties over
 2,048-token histories, T 0.7, top-k 50, top-p 0.9, one uniform per row. A
 "step" is one jf_sample call over one batch; inputs are resident in HBM and
