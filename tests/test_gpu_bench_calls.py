@@ -8,7 +8,9 @@ them, C4's selection and then its tree acceptance (retained and accepted
 counts, path rows, the accepted tokens), as two calls and as the step the
 bench times (jf_sample_accept_tree); C2 also with histories clustered
 in low ids (every row, and every fourth row), which widen the penalty
-table's fixed slots from 256 to 512 a chunk; and the penalized chain-verify
+table's fixed slots from 256 to 512 a chunk, and through the general
+kernels (rows one float past 16-byte alignment, top-k 3000: select_kernel,
+merge_kernel, the multi-pass stages); and the penalized chain-verify
 step (4 lanes x 16 rows, V = 248,320: extras, sparse drafts, then chain
 acceptance)."""
 import numpy as np
@@ -53,7 +55,8 @@ def _oracle_for(w):
 @pytest.mark.parametrize("cfg,mode,history", [
     (2, "auto", "uniform"), (5, "auto", "uniform"), (1, "auto", "uniform"),
     (3, "greedy", "uniform"), (3, "sampled", "uniform"), (4, "greedy", "uniform"),
-    (4, "sampled", "uniform"), (2, "auto", "zipf"), (2, "auto", "mixed")])
+    (4, "sampled", "uniform"), (2, "auto", "zipf"), (2, "auto", "mixed"),
+    (2, "general", "uniform")])
 def test_benchmarked_step_matches_oracle(cfg, mode, history):
     import torch
     w = bench.build_workload(cfg, mode, history)
